@@ -1,0 +1,58 @@
+// common.hpp -- internal helpers shared by the backend's translation units:
+// status reporting, the launch guard, stream casts and the scratch buffer.
+#ifndef EHIP_COMMON_HPP
+#define EHIP_COMMON_HPP
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "ehip.h"
+
+namespace ehip {
+
+// Records a printf-style message for ehip_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Initialises on first use and checks the runtime switch. Every kernel entry
+// point starts with it.
+int ready();
+
+// Launch bookkeeping. before_launch() implements the fault-injection hook
+// (ENGINE_HIP_FAIL_LAUNCH=n refuses the n-th launch, counted from 1, without
+// touching the GPU); after_launch() reads the launch status, counts the
+// launch, and with ENGINE_HIP_SYNC=1 waits for the stream so that a fault is
+// reported by the launch that caused it.
+int before_launch(const char* name);
+int after_launch(const char* name, hipStream_t stream);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Grow-only device scratch owned by the library (never shrinks; replaced by a
+// larger block when asked for more). Work is ordered on one stream, so a
+// buffer released while queued kernels still use it is reused only by later
+// work on that stream. Returns nullptr (with the error recorded) on failure.
+void* scratch(size_t bytes);
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace ehip
+
+// Launches `kernel` through the guard; returns from the calling entry point on
+// any failure.
+#define EHIP_LAUNCH(name, kernel, grid, block, shmem, stream, ...)                  \
+    do {                                                                            \
+        if (int rc_ = ::ehip::before_launch(name)) return rc_;                      \
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);        \
+        if (int rc_ = ::ehip::after_launch(name, stream)) return rc_;               \
+    } while (0)
+
+#define EHIP_READY()                                   \
+    do {                                               \
+        if (int rc_ = ::ehip::ready()) return rc_;     \
+    } while (0)
+
+#endif  // EHIP_COMMON_HPP

@@ -1,0 +1,421 @@
+// elementwise.hip -- the HBM-bound element-wise kernels: binary ops with
+// suffix broadcast, scalar affine, ReLU and its derivative, gradient
+// accumulation, the fused add backward, fill/scale, and the SGD and Adam
+// updates.
+//
+// Every kernel streams 128-bit vectors: a thread issues all U of its loads
+// before any store (so U * inputs loads are in flight per thread), and the
+// vectors of one unrolled step are 256 threads apart, so each wavefront
+// touches 1 KiB contiguous per load instruction. Built with
+// -ffp-contract=off and correctly rounded division and square root, so the
+// arithmetic rounds exactly as the reference's CPU loops do
+// (src/tensor_ops.cpp, src/tensor.cpp:193-202, src/optim.cpp:71-84, 147-160).
+
+#include "common.hpp"
+
+namespace ehip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;  // float4 vectors per thread per input
+
+__device__ __forceinline__ float4 ld4(const float* p, int64_t v) {
+    return reinterpret_cast<const float4*>(p)[v];
+}
+__device__ __forceinline__ void st4(float* p, int64_t v, float4 x) {
+    reinterpret_cast<float4*>(p)[v] = x;
+}
+
+// Applies f component-wise to up to three float4 operands.
+template <class F>
+__device__ __forceinline__ float4 map4(F f, float4 a, float4 b, float4 c) {
+    return make_float4(f(a.x, b.x, c.x), f(a.y, b.y, c.y), f(a.z, b.z, c.z), f(a.w, b.w, c.w));
+}
+
+// Generic streaming skeleton. Op supplies:
+//   static constexpr int kIn;                  inputs loaded per vector
+//   load(v, float4* r)  / store(v, const float4* r)   for vector v (4 elements)
+//   scalar(i)                                   for the tail element i
+template <class Op>
+__global__ __launch_bounds__(kThreads) void stream_vec(Op op, int64_t n) {
+    const int64_t nv = n >> 2;
+    const int64_t base = int64_t(blockIdx.x) * (kThreads * kUnroll) + threadIdx.x;
+    float4 r[kUnroll][Op::kIn];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t v = base + int64_t(u) * kThreads;
+        if (v < nv) op.load(v, r[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t v = base + int64_t(u) * kThreads;
+        if (v < nv) op.store(v, r[u]);
+    }
+    if (blockIdx.x == gridDim.x - 1)
+        for (int64_t i = (nv << 2) + threadIdx.x; i < n; i += kThreads) op.scalar(i);
+}
+
+// Unaligned operands: one element per thread, grid-stride.
+template <class Op>
+__global__ __launch_bounds__(kThreads) void stream_scalar(Op op, int64_t n) {
+    const int64_t step = int64_t(gridDim.x) * kThreads;
+    for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += step) op.scalar(i);
+}
+
+template <class Op>
+int launch_stream(const char* name, const Op& op, int64_t n, bool vec_ok, hipStream_t s) {
+    if (n < 0) return fail(EHIP_EINVAL, "%s: negative size", name);
+    if (n == 0) return EHIP_OK;
+    if (vec_ok) {
+        const int64_t nv = n >> 2;
+        int64_t grid = ceil_div(nv, int64_t(kThreads) * kUnroll);
+        if (grid == 0) grid = 1;
+        if (grid > 0x7fffffff) return fail(EHIP_EINVAL, "%s: %lld elements is too many", name,
+                                           static_cast<long long>(n));
+        EHIP_LAUNCH(name, stream_vec<Op>, dim3(unsigned(grid)), dim3(kThreads), 0, s, op, n);
+    } else {
+        int64_t grid = ceil_div(n, kThreads);
+        if (grid > 65536) grid = 65536;
+        EHIP_LAUNCH(name, stream_scalar<Op>, dim3(unsigned(grid)), dim3(kThreads), 0, s, op, n);
+    }
+    return EHIP_OK;
+}
+
+// ------------------------------------------------------------------ ops
+
+__device__ __forceinline__ float apply_binary(int op, float a, float b) {
+    switch (op) {
+        case EHIP_ADD: return a + b;
+        case EHIP_SUB: return a - b;
+        case EHIP_MUL: return a * b;
+        default: return a / b;
+    }
+}
+
+template <int OP>
+struct Binary {
+    static constexpr int kIn = 2;
+    const float* a;
+    const float* b;
+    float* out;
+    int64_t inner;
+    __device__ void load(int64_t v, float4* r) const {
+        r[0] = ld4(a, v);
+        r[1] = ld4(b, (v << 2) % inner >> 2);
+    }
+    __device__ void store(int64_t v, const float4* r) const {
+        st4(out, v, map4([](float x, float y, float) { return apply_binary(OP, x, y); }, r[0],
+                         r[1], r[1]));
+    }
+    __device__ void scalar(int64_t i) const { out[i] = apply_binary(OP, a[i], b[i % inner]); }
+};
+
+// The scalar node: `t * k` is (k, 0) and `t + k` is (1, k); each rounds once,
+// as on the CPU (src/tensor_ops.cpp:280-285, 307-312).
+struct Scalar {
+    static constexpr int kIn = 1;
+    const float* x;
+    float* out;
+    float mul, add;
+    __device__ float f(float v) const {
+        if (mul == 1.0f) return v + add;
+        if (add == 0.0f) return v * mul;
+        return v * mul + add;
+    }
+    __device__ void load(int64_t v, float4* r) const { r[0] = ld4(x, v); }
+    __device__ void store(int64_t v, const float4* r) const {
+        st4(out, v, make_float4(f(r[0].x), f(r[0].y), f(r[0].z), f(r[0].w)));
+    }
+    __device__ void scalar(int64_t i) const { out[i] = f(x[i]); }
+};
+
+struct Relu {
+    static constexpr int kIn = 1;
+    const float* x;
+    float* y;
+    static __device__ float f(float v, float, float) { return (0.0f < v) ? v : 0.0f; }
+    __device__ void load(int64_t v, float4* r) const { r[0] = ld4(x, v); }
+    __device__ void store(int64_t v, const float4* r) const { st4(y, v, map4(f, r[0], r[0], r[0])); }
+    __device__ void scalar(int64_t i) const { y[i] = f(x[i], 0, 0); }
+};
+
+struct ReluBackward {
+    static constexpr int kIn = 2;
+    const float* x;
+    const float* g;
+    float* dx;
+    static __device__ float f(float v, float gv, float) { return (v > 0.0f) ? gv : 0.0f; }
+    __device__ void load(int64_t v, float4* r) const {
+        r[0] = ld4(x, v);
+        r[1] = ld4(g, v);
+    }
+    __device__ void store(int64_t v, const float4* r) const {
+        st4(dx, v, map4(f, r[0], r[1], r[1]));
+    }
+    __device__ void scalar(int64_t i) const { dx[i] = f(x[i], g[i], 0); }
+};
+
+template <bool INIT>
+struct Accumulate {
+    static constexpr int kIn = INIT ? 1 : 2;
+    float* grad;
+    const float* g;
+    __device__ void load(int64_t v, float4* r) const {
+        r[0] = ld4(g, v);
+        if (!INIT) r[kIn - 1] = ld4(grad, v);
+    }
+    // The first write is 0 + g, not a copy: the reference adds into a zeroed
+    // buffer (src/tensor.cpp:177-202), which turns -0 into +0.
+    __device__ void store(int64_t v, const float4* r) const {
+        if (INIT)
+            st4(grad, v, map4([](float a, float, float) { return 0.0f + a; }, r[0], r[0], r[0]));
+        else
+            st4(grad, v, map4([](float a, float b, float) { return b + a; }, r[0], r[kIn - 1],
+                              r[0]));
+    }
+    __device__ void scalar(int64_t i) const { grad[i] = INIT ? 0.0f + g[i] : grad[i] + g[i]; }
+};
+
+// The add node's backward: g goes to both operands in one pass.
+template <bool ACC_A, bool ACC_B>
+struct AddBackward {
+    static constexpr int kIn = 1 + int(ACC_A) + int(ACC_B);
+    const float* g;
+    float* da;
+    float* db;
+    __device__ void load(int64_t v, float4* r) const {
+        r[0] = ld4(g, v);
+        if (ACC_A) r[1] = ld4(da, v);
+        if (ACC_B) r[kIn - 1] = ld4(db, v);
+    }
+    __device__ void store(int64_t v, const float4* r) const {
+        const auto add = [](float a, float b, float) { return a + b; };
+        const float4 first = map4(add, make_float4(0.0f, 0.0f, 0.0f, 0.0f), r[0], r[0]);
+        st4(da, v, ACC_A ? map4(add, r[1], r[0], r[0]) : first);
+        st4(db, v, ACC_B ? map4(add, r[kIn - 1], r[0], r[0]) : first);
+    }
+    __device__ void scalar(int64_t i) const {
+        const float gv = g[i];
+        da[i] = ACC_A ? da[i] + gv : 0.0f + gv;
+        db[i] = ACC_B ? db[i] + gv : 0.0f + gv;
+    }
+};
+
+struct Fill {
+    static constexpr int kIn = 1;
+    float* x;
+    float value;
+    __device__ void load(int64_t, float4*) const {}
+    __device__ void store(int64_t v, const float4*) const {
+        st4(x, v, make_float4(value, value, value, value));
+    }
+    __device__ void scalar(int64_t i) const { x[i] = value; }
+};
+
+struct Scale {
+    static constexpr int kIn = 1;
+    float* x;
+    float factor;
+    __device__ void load(int64_t v, float4* r) const { r[0] = ld4(x, v); }
+    __device__ void store(int64_t v, const float4* r) const {
+        st4(x, v, make_float4(r[0].x * factor, r[0].y * factor, r[0].z * factor,
+                              r[0].w * factor));
+    }
+    __device__ void scalar(int64_t i) const { x[i] = x[i] * factor; }
+};
+
+// src/optim.cpp:71-84, term for term.
+template <bool MOMENTUM>
+struct Sgd {
+    static constexpr int kIn = MOMENTUM ? 3 : 2;
+    float* p;
+    const float* g;
+    float* vel;
+    float lr, momentum, wd;
+    __device__ void one(float& pv, float gv, float& vv) const {
+        float grad = gv;
+        if (wd != 0.0f) grad += wd * pv;
+        if (MOMENTUM) {
+            vv = momentum * vv + grad;
+            grad = vv;
+        }
+        pv -= lr * grad;
+    }
+    __device__ void load(int64_t v, float4* r) const {
+        r[0] = ld4(p, v);
+        r[1] = ld4(g, v);
+        if (MOMENTUM) r[kIn - 1] = ld4(vel, v);
+    }
+    __device__ void store(int64_t v, const float4* r) const {
+        float4 pv = r[0], vv = r[kIn - 1];
+        one(pv.x, r[1].x, vv.x);
+        one(pv.y, r[1].y, vv.y);
+        one(pv.z, r[1].z, vv.z);
+        one(pv.w, r[1].w, vv.w);
+        st4(p, v, pv);
+        if (MOMENTUM) st4(vel, v, vv);
+    }
+    __device__ void scalar(int64_t i) const {
+        float pv = p[i], vv = MOMENTUM ? vel[i] : 0.0f;
+        one(pv, g[i], vv);
+        p[i] = pv;
+        if (MOMENTUM) vel[i] = vv;
+    }
+};
+
+// src/optim.cpp:147-160, term for term and in the same association order.
+struct Adam {
+    static constexpr int kIn = 4;
+    float* p;
+    const float* g;
+    float* m;
+    float* v;
+    float lr, b1, b2, eps, wd, c1, c2;
+    __device__ void one(float& pv, float gv, float& mv, float& vv) const {
+        float grad = gv;
+        if (wd != 0.0f) grad += wd * pv;
+        mv = b1 * mv + (1.0f - b1) * grad;
+        vv = b2 * vv + (1.0f - b2) * grad * grad;
+        const float m_hat = mv / c1;
+        const float v_hat = vv / c2;
+        pv -= lr * m_hat / (sqrtf(v_hat) + eps);
+    }
+    __device__ void load(int64_t i, float4* r) const {
+        r[0] = ld4(p, i);
+        r[1] = ld4(g, i);
+        r[2] = ld4(m, i);
+        r[3] = ld4(v, i);
+    }
+    __device__ void store(int64_t i, const float4* r) const {
+        float4 pv = r[0], mv = r[2], vv = r[3];
+        one(pv.x, r[1].x, mv.x, vv.x);
+        one(pv.y, r[1].y, mv.y, vv.y);
+        one(pv.z, r[1].z, mv.z, vv.z);
+        one(pv.w, r[1].w, mv.w, vv.w);
+        st4(p, i, pv);
+        st4(m, i, mv);
+        st4(v, i, vv);
+    }
+    __device__ void scalar(int64_t i) const {
+        float pv = p[i], mv = m[i], vv = v[i];
+        one(pv, g[i], mv, vv);
+        p[i] = pv;
+        m[i] = mv;
+        v[i] = vv;
+    }
+};
+
+template <int OP>
+int binary_op(const float* a, const float* b, float* out, int64_t inner, int64_t repeat,
+              hipStream_t s) {
+    const bool vec = aligned16(a) && aligned16(b) && aligned16(out) && inner % 4 == 0;
+    return launch_stream("binary", Binary<OP>{a, b, out, inner}, inner * repeat, vec, s);
+}
+
+}  // namespace
+}  // namespace ehip
+
+using namespace ehip;
+
+extern "C" {
+
+int ehip_binary_f32(int op, const float* a, const float* b, float* out, int64_t inner,
+                    int64_t repeat, void* stream) {
+    EHIP_READY();
+    if (inner <= 0 || repeat < 0) return fail(EHIP_EINVAL, "binary: bad shape");
+    if (!a || !b || !out) return fail(EHIP_EINVAL, "binary: null pointer");
+    hipStream_t s = as_stream(stream);
+    switch (op) {
+        case EHIP_ADD: return binary_op<EHIP_ADD>(a, b, out, inner, repeat, s);
+        case EHIP_SUB: return binary_op<EHIP_SUB>(a, b, out, inner, repeat, s);
+        case EHIP_MUL: return binary_op<EHIP_MUL>(a, b, out, inner, repeat, s);
+        case EHIP_DIV: return binary_op<EHIP_DIV>(a, b, out, inner, repeat, s);
+        default: return fail(EHIP_EINVAL, "binary: unknown op %d", op);
+    }
+}
+
+int ehip_scalar_f32(const float* x, float* out, int64_t n, float mul, float add, void* stream) {
+    EHIP_READY();
+    if (!x || !out) return fail(EHIP_EINVAL, "scalar: null pointer");
+    return launch_stream("scalar", Scalar{x, out, mul, add}, n, aligned16(x) && aligned16(out),
+                         as_stream(stream));
+}
+
+int ehip_relu_f32(const float* x, float* y, int64_t n, void* stream) {
+    EHIP_READY();
+    if (!x || !y) return fail(EHIP_EINVAL, "relu: null pointer");
+    return launch_stream("relu", Relu{x, y}, n, aligned16(x) && aligned16(y), as_stream(stream));
+}
+
+int ehip_relu_backward_f32(const float* x, const float* g, float* dx, int64_t n, void* stream) {
+    EHIP_READY();
+    if (!x || !g || !dx) return fail(EHIP_EINVAL, "relu_backward: null pointer");
+    return launch_stream("relu_backward", ReluBackward{x, g, dx}, n,
+                         aligned16(x) && aligned16(g) && aligned16(dx), as_stream(stream));
+}
+
+int ehip_accumulate_grad_f32(float* grad, const float* g, int64_t n, int initialize,
+                             void* stream) {
+    EHIP_READY();
+    if (!grad || !g) return fail(EHIP_EINVAL, "accumulate_grad: null pointer");
+    const bool vec = aligned16(grad) && aligned16(g);
+    if (initialize)
+        return launch_stream("accumulate_grad", Accumulate<true>{grad, g}, n, vec,
+                             as_stream(stream));
+    return launch_stream("accumulate_grad", Accumulate<false>{grad, g}, n, vec, as_stream(stream));
+}
+
+int ehip_add_backward_f32(const float* g, float* da, float* db, int64_t n, int accumulate_a,
+                          int accumulate_b, void* stream) {
+    EHIP_READY();
+    if (!g || !da || !db) return fail(EHIP_EINVAL, "add_backward: null pointer");
+    if (da == db) return fail(EHIP_EINVAL, "add_backward: da and db alias");
+    const bool vec = aligned16(g) && aligned16(da) && aligned16(db);
+    hipStream_t s = as_stream(stream);
+    if (accumulate_a && accumulate_b)
+        return launch_stream("add_backward", AddBackward<true, true>{g, da, db}, n, vec, s);
+    if (accumulate_a)
+        return launch_stream("add_backward", AddBackward<true, false>{g, da, db}, n, vec, s);
+    if (accumulate_b)
+        return launch_stream("add_backward", AddBackward<false, true>{g, da, db}, n, vec, s);
+    return launch_stream("add_backward", AddBackward<false, false>{g, da, db}, n, vec, s);
+}
+
+int ehip_fill_f32(float* x, int64_t n, float value, void* stream) {
+    EHIP_READY();
+    if (!x && n > 0) return fail(EHIP_EINVAL, "fill: null pointer");
+    return launch_stream("fill", Fill{x, value}, n, aligned16(x), as_stream(stream));
+}
+
+int ehip_scale_f32(float* x, int64_t n, float factor, void* stream) {
+    EHIP_READY();
+    if (!x && n > 0) return fail(EHIP_EINVAL, "scale: null pointer");
+    return launch_stream("scale", Scale{x, factor}, n, aligned16(x), as_stream(stream));
+}
+
+int ehip_sgd_f32(float* p, const float* g, float* velocity, int64_t n, float lr, float momentum,
+                 float weight_decay, void* stream) {
+    EHIP_READY();
+    if (!p || !g) return fail(EHIP_EINVAL, "sgd: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (momentum != 0.0f) {
+        if (!velocity) return fail(EHIP_EINVAL, "sgd: momentum needs a velocity buffer");
+        return launch_stream("sgd", Sgd<true>{p, g, velocity, lr, momentum, weight_decay}, n,
+                             aligned16(p) && aligned16(g) && aligned16(velocity), s);
+    }
+    return launch_stream("sgd", Sgd<false>{p, g, nullptr, lr, momentum, weight_decay}, n,
+                         aligned16(p) && aligned16(g), s);
+}
+
+int ehip_adam_f32(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1,
+                  float beta2, float eps, float weight_decay, float bias_c1, float bias_c2,
+                  void* stream) {
+    EHIP_READY();
+    if (!p || !g || !m || !v) return fail(EHIP_EINVAL, "adam: null pointer");
+    const bool vec = aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v);
+    return launch_stream("adam",
+                         Adam{p, g, m, v, lr, beta1, beta2, eps, weight_decay, bias_c1, bias_c2},
+                         n, vec, as_stream(stream));
+}
+
+}  // extern "C"

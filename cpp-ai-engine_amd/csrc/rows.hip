@@ -1,0 +1,713 @@
+// rows.hip -- kernels that work row by row over the last axis: softmax and its
+// derivative, LayerNorm forward and backward, and the fused softmax
+// cross-entropy (forward, backward from saved probabilities, and the one-pass
+// backward straight from the logits).
+//
+// A row is handled by a "group" of T threads that keeps the whole row in
+// registers, V values per thread: T = 64 (one wavefront, four rows per
+// 256-thread block) for rows up to 2048 values, T = 256 or 1024 (one block
+// per row, 128-bit loads) above that. The row is read from HBM once and
+// written once. Reductions go through wavefront shuffles and, across the
+// wavefronts of a block, LDS in wavefront order: a fixed order per shape, so
+// results are deterministic. Rows longer than the register path holds use a
+// looped fallback that streams the row three times.
+
+#include "common.hpp"
+
+#include <cmath>
+
+namespace ehip {
+namespace {
+
+// ------------------------------------------------------------ reductions
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Reduction over the T threads of a group. T == 64 stays in the wavefront;
+// larger T combines the wavefront results through `sh` in wavefront order.
+// Every thread of the block must call it (it may hold barriers).
+template <int T, bool MAX>
+__device__ __forceinline__ float group_reduce(float v, float* sh) {
+    v = MAX ? wave_max(v) : wave_sum(v);
+    if (T == 64) return v;
+    constexpr int W = T / 64;
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    __syncthreads();  // sh may still be read by the previous reduction
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    float r = sh[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) r = MAX ? fmaxf(r, sh[w]) : r + sh[w];
+    return r;
+}
+
+// ------------------------------------------------------------ row fragments
+
+// V values of one row held by thread `tid` of a T-thread group. VEC4 loads
+// 128 bits at a time: value t sits at column 4 * (tid + T * (t / 4)) + t % 4;
+// otherwise at column tid + T * t.
+template <int T, int V, bool VEC4>
+struct Frag {
+    float v[V];
+    __device__ static int64_t col(int tid, int t) {
+        return VEC4 ? 4 * (int64_t(tid) + int64_t(T) * (t / 4)) + (t % 4)
+                    : int64_t(tid) + int64_t(T) * t;
+    }
+    __device__ void load(const float* row, int64_t cols, int tid, float fill) {
+        if (VEC4) {
+#pragma unroll
+            for (int q = 0; q < V / 4; ++q) {
+                const int64_t c4 = int64_t(tid) + int64_t(T) * q;
+                if (4 * c4 < cols) {
+                    const float4 x = reinterpret_cast<const float4*>(row)[c4];
+                    v[4 * q] = x.x;
+                    v[4 * q + 1] = x.y;
+                    v[4 * q + 2] = x.z;
+                    v[4 * q + 3] = x.w;
+                } else {
+                    v[4 * q] = v[4 * q + 1] = v[4 * q + 2] = v[4 * q + 3] = fill;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < V; ++t) {
+                const int64_t c = col(tid, t);
+                v[t] = c < cols ? row[c] : fill;
+            }
+        }
+    }
+    __device__ void store(float* row, int64_t cols, int tid) const {
+        if (VEC4) {
+#pragma unroll
+            for (int q = 0; q < V / 4; ++q) {
+                const int64_t c4 = int64_t(tid) + int64_t(T) * q;
+                if (4 * c4 < cols)
+                    reinterpret_cast<float4*>(row)[c4] =
+                        make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < V; ++t) {
+                const int64_t c = col(tid, t);
+                if (c < cols) row[c] = v[t];
+            }
+        }
+    }
+};
+
+// Group geometry inside a block of max(T, 256) threads.
+template <int T>
+struct Group {
+    static constexpr int kBlock = T < 256 ? 256 : T;
+    static constexpr int kPerBlock = kBlock / T;
+    __device__ static int tid() { return threadIdx.x % T; }
+    __device__ static int64_t first_row() { return int64_t(blockIdx.x) * kPerBlock + threadIdx.x / T; }
+    __device__ static int64_t row_step() { return int64_t(gridDim.x) * kPerBlock; }
+};
+
+// Softmax of the fragment in place; returns the row max and the sum of
+// exponentials through m and s. Columns past the end hold -inf and give 0.
+template <int T, int V, bool VEC4>
+__device__ __forceinline__ void frag_softmax(Frag<T, V, VEC4>& f, float* sh, float& m, float& s) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < V; ++t) mx = fmaxf(mx, f.v[t]);
+    mx = group_reduce<T, true>(mx, sh);
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < V; ++t) {
+        f.v[t] = expf(f.v[t] - mx);
+        sum += f.v[t];
+    }
+    sum = group_reduce<T, false>(sum, sh);
+#pragma unroll
+    for (int t = 0; t < V; ++t) f.v[t] = f.v[t] / sum;
+    m = mx;
+    s = sum;
+}
+
+// ------------------------------------------------------------ softmax
+
+template <int T, int V, bool VEC4>
+__global__ __launch_bounds__(Group<T>::kBlock) void softmax_rows(const float* __restrict__ x,
+                                                                 float* __restrict__ y,
+                                                                 int64_t rows, int64_t cols) {
+    __shared__ float sh[Group<T>::kBlock / 64];
+    for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
+        Frag<T, V, VEC4> f;
+        f.load(x + r * cols, cols, Group<T>::tid(), -INFINITY);
+        float m, s;
+        frag_softmax<T, V, VEC4>(f, sh, m, s);
+        f.store(y + r * cols, cols, Group<T>::tid());
+    }
+}
+
+template <int T, int V, bool VEC4>
+__global__ __launch_bounds__(Group<T>::kBlock) void softmax_rows_backward(
+    const float* __restrict__ y, const float* __restrict__ g, float* __restrict__ dx, int64_t rows,
+    int64_t cols) {
+    __shared__ float sh[Group<T>::kBlock / 64];
+    for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
+        Frag<T, V, VEC4> fy, fg;
+        fy.load(y + r * cols, cols, Group<T>::tid(), 0.0f);
+        fg.load(g + r * cols, cols, Group<T>::tid(), 0.0f);
+        float dot = 0.0f;
+#pragma unroll
+        for (int t = 0; t < V; ++t) dot += fg.v[t] * fy.v[t];
+        dot = group_reduce<T, false>(dot, sh);
+#pragma unroll
+        for (int t = 0; t < V; ++t) fg.v[t] = fy.v[t] * (fg.v[t] - dot);
+        fg.store(dx + r * cols, cols, Group<T>::tid());
+    }
+}
+
+// Looped fallback for rows beyond the register path: one block per row,
+// three passes over global memory.
+constexpr int kLoopThreads = 1024;
+
+__device__ float block_reduce_loop(float v, float* sh, bool is_max) {
+    v = is_max ? wave_max(v) : wave_sum(v);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    __syncthreads();
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    float r = sh[0];
+    for (int w = 1; w < kLoopThreads / 64; ++w) r = is_max ? fmaxf(r, sh[w]) : r + sh[w];
+    return r;
+}
+
+__global__ __launch_bounds__(kLoopThreads) void softmax_rows_loop(const float* __restrict__ x,
+                                                                  float* __restrict__ y,
+                                                                  int64_t rows, int64_t cols) {
+    __shared__ float sh[kLoopThreads / 64];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* xr = x + r * cols;
+        float* yr = y + r * cols;
+        float mx = -INFINITY;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) mx = fmaxf(mx, xr[c]);
+        mx = block_reduce_loop(mx, sh, true);
+        float sum = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) sum += expf(xr[c] - mx);
+        sum = block_reduce_loop(sum, sh, false);
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) yr[c] = expf(xr[c] - mx) / sum;
+    }
+}
+
+__global__ __launch_bounds__(kLoopThreads) void softmax_rows_backward_loop(
+    const float* __restrict__ y, const float* __restrict__ g, float* __restrict__ dx, int64_t rows,
+    int64_t cols) {
+    __shared__ float sh[kLoopThreads / 64];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* yr = y + r * cols;
+        const float* gr = g + r * cols;
+        float dot = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) dot += gr[c] * yr[c];
+        dot = block_reduce_loop(dot, sh, false);
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads)
+            dx[r * cols + c] = yr[c] * (gr[c] - dot);
+    }
+}
+
+// ------------------------------------------------------------ cross-entropy
+
+// probs = softmax(logits); row_loss[r] = -((x[t] - max) - log(sum)), the
+// expression of src/nn.cpp:371-373. An out-of-range target gives NaN.
+template <int T, int V, bool VEC4>
+__global__ __launch_bounds__(Group<T>::kBlock) void xent_rows(const float* __restrict__ logits,
+                                                              const int32_t* __restrict__ targets,
+                                                              float* __restrict__ probs,
+                                                              float* __restrict__ row_loss,
+                                                              int64_t rows, int64_t cols) {
+    __shared__ float sh[Group<T>::kBlock / 64];
+    for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
+        Frag<T, V, VEC4> f;
+        f.load(logits + r * cols, cols, Group<T>::tid(), -INFINITY);
+        float m, s;
+        frag_softmax<T, V, VEC4>(f, sh, m, s);
+        f.store(probs + r * cols, cols, Group<T>::tid());
+        if (Group<T>::tid() == 0) {
+            const int64_t t = targets[r];
+            row_loss[r] = (t >= 0 && t < cols) ? -((logits[r * cols + t] - m) - logf(s)) : NAN;
+        }
+    }
+}
+
+// dx = (softmax - onehot) * (grad / rows), from the logits in one pass. The
+// softmax is the same code as xent_rows, so the result equals the two-kernel
+// path bit for bit.
+template <int T, int V, bool VEC4>
+__global__ __launch_bounds__(Group<T>::kBlock) void xent_rows_backward_fused(
+    const float* __restrict__ logits, const int32_t* __restrict__ targets, float* __restrict__ dx,
+    int64_t rows, int64_t cols, const float* __restrict__ grad) {
+    __shared__ float sh[Group<T>::kBlock / 64];
+    const float scale = grad[0] / static_cast<float>(rows);
+    for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
+        Frag<T, V, VEC4> f;
+        f.load(logits + r * cols, cols, Group<T>::tid(), -INFINITY);
+        float m, s;
+        frag_softmax<T, V, VEC4>(f, sh, m, s);
+        const int64_t t = targets[r];
+#pragma unroll
+        for (int q = 0; q < V; ++q) {
+            float p = f.v[q];
+            if (Frag<T, V, VEC4>::col(Group<T>::tid(), q) == t) p -= 1.0f;
+            f.v[q] = p * scale;
+        }
+        f.store(dx + r * cols, cols, Group<T>::tid());
+    }
+}
+
+__global__ __launch_bounds__(kLoopThreads) void xent_rows_loop(const float* __restrict__ logits,
+                                                               const int32_t* __restrict__ targets,
+                                                               float* __restrict__ probs,
+                                                               float* __restrict__ row_loss,
+                                                               int64_t rows, int64_t cols) {
+    __shared__ float sh[kLoopThreads / 64];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* xr = logits + r * cols;
+        float mx = -INFINITY;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) mx = fmaxf(mx, xr[c]);
+        mx = block_reduce_loop(mx, sh, true);
+        float sum = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) sum += expf(xr[c] - mx);
+        sum = block_reduce_loop(sum, sh, false);
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads)
+            probs[r * cols + c] = expf(xr[c] - mx) / sum;
+        if (threadIdx.x == 0) {
+            const int64_t t = targets[r];
+            row_loss[r] = (t >= 0 && t < cols) ? -((xr[t] - mx) - logf(sum)) : NAN;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kLoopThreads) void xent_rows_backward_loop(
+    const float* __restrict__ logits, const int32_t* __restrict__ targets, float* __restrict__ dx,
+    int64_t rows, int64_t cols, const float* __restrict__ grad) {
+    __shared__ float sh[kLoopThreads / 64];
+    const float scale = grad[0] / static_cast<float>(rows);
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* xr = logits + r * cols;
+        float mx = -INFINITY;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) mx = fmaxf(mx, xr[c]);
+        mx = block_reduce_loop(mx, sh, true);
+        float sum = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) sum += expf(xr[c] - mx);
+        sum = block_reduce_loop(sum, sh, false);
+        const int64_t t = targets[r];
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) {
+            float p = expf(xr[c] - mx) / sum;
+            if (c == t) p -= 1.0f;
+            dx[r * cols + c] = p * scale;
+        }
+    }
+}
+
+// src/nn.cpp:386-405: (p - onehot) * (grad / N), element by element.
+__global__ __launch_bounds__(256) void xent_backward_from_probs(
+    const float* __restrict__ probs, const int32_t* __restrict__ targets, float* __restrict__ dx,
+    int64_t rows, int64_t cols, const float* __restrict__ grad) {
+    const float scale = grad[0] / static_cast<float>(rows);
+    const int64_t n = rows * cols;
+    const int64_t step = int64_t(gridDim.x) * 256;
+    for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < n; e += step) {
+        const int64_t r = e / cols, c = e % cols;
+        float p = probs[e];
+        if (c == targets[r]) p -= 1.0f;
+        dx[e] = p * scale;
+    }
+}
+
+// mean over rows of row_loss, summed in double over a fixed tree.
+__global__ __launch_bounds__(1024) void mean_rows(const float* __restrict__ row_loss, int64_t rows,
+                                                  float* __restrict__ loss) {
+    __shared__ double sh[1024];
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < rows; i += 1024) acc += row_loss[i];
+    sh[threadIdx.x] = acc;
+    __syncthreads();
+    for (int s = 512; s > 0; s >>= 1) {
+        if (int(threadIdx.x) < s) sh[threadIdx.x] += sh[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) loss[0] = static_cast<float>(sh[0]) / static_cast<float>(rows);
+}
+
+// ------------------------------------------------------------ LayerNorm
+
+// src/transformer.cpp:53-73: mean = (sum x) * (1/D); var = (sum (x-mean)^2) * (1/D);
+// inv = 1 / sqrt(var + eps); xhat = (x - mean) * inv; out = gamma * xhat + beta.
+template <int T, int V>
+__global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float* __restrict__ out, float* __restrict__ xhat, float* __restrict__ inv_std, int64_t rows,
+    int64_t cols, float eps) {
+    __shared__ float sh[Group<T>::kBlock / 64];
+    const float inv_d = 1.0f / static_cast<float>(cols);
+    const int tid = Group<T>::tid();
+    for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
+        Frag<T, V, false> f;
+        f.load(x + r * cols, cols, tid, 0.0f);
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < V; ++t) s += f.v[t];
+        const float mean = group_reduce<T, false>(s, sh) * inv_d;
+        float q = 0.0f;
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+            const float d = Frag<T, V, false>::col(tid, t) < cols ? f.v[t] - mean : 0.0f;
+            q += d * d;
+        }
+        const float var = group_reduce<T, false>(q, sh) * inv_d;
+        const float inv = 1.0f / sqrtf(var + eps);
+        if (tid == 0) inv_std[r] = inv;
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+            const int64_t c = Frag<T, V, false>::col(tid, t);
+            if (c < cols) {
+                const float h = (f.v[t] - mean) * inv;
+                xhat[r * cols + c] = h;
+                out[r * cols + c] = gamma[c] * h + beta[c];
+            }
+        }
+    }
+}
+
+// dx per row (src/transformer.cpp:147-171); dgamma/dbeta partial sums per
+// group over the rows it visits, ascending, into partial[group][2][cols].
+template <int T, int V>
+__global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows_backward(
+    const float* __restrict__ dy, const float* __restrict__ xhat, const float* __restrict__ gamma,
+    const float* __restrict__ inv_std, float* __restrict__ dx, float* __restrict__ partial,
+    int64_t rows, int64_t cols) {
+    __shared__ float sh[Group<T>::kBlock / 64];
+    const float inv_d = 1.0f / static_cast<float>(cols);
+    const int tid = Group<T>::tid();
+    float dg[V], db[V], gm[V];
+#pragma unroll
+    for (int t = 0; t < V; ++t) {
+        dg[t] = 0.0f;
+        db[t] = 0.0f;
+        const int64_t c = Frag<T, V, false>::col(tid, t);
+        gm[t] = c < cols ? gamma[c] : 0.0f;
+    }
+    for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
+        Frag<T, V, false> fd, fh;
+        fd.load(dy + r * cols, cols, tid, 0.0f);
+        fh.load(xhat + r * cols, cols, tid, 0.0f);
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+            const float dxh = fd.v[t] * gm[t];
+            s1 += dxh;
+            s2 += dxh * fh.v[t];
+        }
+        s1 = group_reduce<T, false>(s1, sh);
+        s2 = group_reduce<T, false>(s2, sh);
+        const float inv = inv_std[r];
+        Frag<T, V, false> fo;
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+            const float dxh = fd.v[t] * gm[t];
+            fo.v[t] = inv * (dxh - inv_d * s1 - fh.v[t] * inv_d * s2);
+            dg[t] = dg[t] + fd.v[t] * fh.v[t];
+            db[t] = db[t] + fd.v[t];
+        }
+        fo.store(dx + r * cols, cols, tid);
+    }
+    const int64_t group = Group<T>::first_row();  // group index == its first row
+    float* pg = partial + group * 2 * cols;
+#pragma unroll
+    for (int t = 0; t < V; ++t) {
+        const int64_t c = Frag<T, V, false>::col(tid, t);
+        if (c < cols) {
+            pg[c] = dg[t];
+            pg[cols + c] = db[t];
+        }
+    }
+}
+
+// dgamma[c] = sum over groups of partial[g][0][c], groups ascending; dbeta likewise.
+__global__ __launch_bounds__(256) void layernorm_reduce_partials(const float* __restrict__ partial,
+                                                                 float* __restrict__ dgamma,
+                                                                 float* __restrict__ dbeta,
+                                                                 int64_t groups, int64_t cols) {
+    const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= 2 * cols) return;
+    const int64_t which = e / cols, c = e % cols;
+    float acc = 0.0f;
+    for (int64_t g = 0; g < groups; ++g) acc += partial[(g * 2 + which) * cols + c];
+    (which == 0 ? dgamma : dbeta)[c] = acc;
+}
+
+// ------------------------------------------------------------ dispatch
+
+unsigned row_grid(int64_t rows, int per_block) {
+    int64_t g = ceil_div(rows, per_block);
+    if (g > (int64_t(1) << 20)) g = int64_t(1) << 20;
+    return unsigned(g < 1 ? 1 : g);
+}
+
+// Calls f.template operator()<T, V, VEC4>() for the register path that holds
+// `cols`, or returns false when the row needs the looped fallback.
+template <class F>
+bool dispatch_row(int64_t cols, bool vec_ok, F&& f) {
+    if (cols <= 64) return f.template run<64, 1, false>();
+    if (cols <= 128) return f.template run<64, 2, false>();
+    if (cols <= 256) return f.template run<64, 4, false>();
+    if (cols <= 512) return f.template run<64, 8, false>();
+    if (cols <= 1024) return f.template run<64, 16, false>();
+    if (cols <= 2048) return f.template run<64, 32, false>();
+    if (!vec_ok) return false;
+    if (cols <= 4096) return f.template run<256, 16, true>();
+    if (cols <= 8192) return f.template run<256, 32, true>();
+    if (cols <= 16384) return f.template run<1024, 16, true>();
+    if (cols <= 32768) return f.template run<1024, 32, true>();
+    return false;
+}
+
+struct SoftmaxLaunch {
+    const float* x;
+    float* y;
+    int64_t rows, cols;
+    hipStream_t s;
+    int* rc;
+    template <int T, int V, bool VEC4>
+    bool run() {
+        constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
+        *rc = [&] {
+            EHIP_LAUNCH("softmax", (softmax_rows<T, V, VEC4>), dim3(row_grid(rows, G)), dim3(B), 0,
+                        s, x, y, rows, cols);
+            return int(EHIP_OK);
+        }();
+        return true;
+    }
+};
+
+struct SoftmaxBackwardLaunch {
+    const float* y;
+    const float* g;
+    float* dx;
+    int64_t rows, cols;
+    hipStream_t s;
+    int* rc;
+    template <int T, int V, bool VEC4>
+    bool run() {
+        constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
+        *rc = [&] {
+            EHIP_LAUNCH("softmax_backward", (softmax_rows_backward<T, V, VEC4>),
+                        dim3(row_grid(rows, G)), dim3(B), 0, s, y, g, dx, rows, cols);
+            return int(EHIP_OK);
+        }();
+        return true;
+    }
+};
+
+struct XentLaunch {
+    const float* logits;
+    const int32_t* targets;
+    float* probs;
+    float* row_loss;
+    int64_t rows, cols;
+    hipStream_t s;
+    int* rc;
+    template <int T, int V, bool VEC4>
+    bool run() {
+        constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
+        *rc = [&] {
+            EHIP_LAUNCH("cross_entropy", (xent_rows<T, V, VEC4>), dim3(row_grid(rows, G)), dim3(B),
+                        0, s, logits, targets, probs, row_loss, rows, cols);
+            return int(EHIP_OK);
+        }();
+        return true;
+    }
+};
+
+struct XentBackwardLaunch {
+    const float* logits;
+    const int32_t* targets;
+    float* dx;
+    int64_t rows, cols;
+    const float* grad;
+    hipStream_t s;
+    int* rc;
+    template <int T, int V, bool VEC4>
+    bool run() {
+        constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
+        *rc = [&] {
+            EHIP_LAUNCH("softmax_xent_backward", (xent_rows_backward_fused<T, V, VEC4>),
+                        dim3(row_grid(rows, G)), dim3(B), 0, s, logits, targets, dx, rows, cols,
+                        grad);
+            return int(EHIP_OK);
+        }();
+        return true;
+    }
+};
+
+bool rows_vec_ok(int64_t cols, std::initializer_list<const void*> ptrs) {
+    if (cols % 4 != 0) return false;
+    for (const void* p : ptrs)
+        if (!aligned16(p)) return false;
+    return true;
+}
+
+unsigned loop_grid(int64_t rows) { return unsigned(rows < 65536 ? rows : 65536); }
+
+}  // namespace
+}  // namespace ehip
+
+using namespace ehip;
+
+extern "C" {
+
+int ehip_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream) {
+    EHIP_READY();
+    if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "softmax: bad shape");
+    if (!x || !y) return fail(EHIP_EINVAL, "softmax: null pointer");
+    if (rows == 0) return EHIP_OK;
+    hipStream_t s = as_stream(stream);
+    int rc = EHIP_OK;
+    if (dispatch_row(cols, rows_vec_ok(cols, {x, y}), SoftmaxLaunch{x, y, rows, cols, s, &rc}))
+        return rc;
+    EHIP_LAUNCH("softmax", softmax_rows_loop, dim3(loop_grid(rows)), dim3(kLoopThreads), 0, s, x, y,
+                rows, cols);
+    return EHIP_OK;
+}
+
+int ehip_softmax_backward_f32(const float* y, const float* g, float* dx, int64_t rows,
+                              int64_t cols, void* stream) {
+    EHIP_READY();
+    if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "softmax_backward: bad shape");
+    if (!y || !g || !dx) return fail(EHIP_EINVAL, "softmax_backward: null pointer");
+    if (rows == 0) return EHIP_OK;
+    hipStream_t s = as_stream(stream);
+    int rc = EHIP_OK;
+    if (dispatch_row(cols, rows_vec_ok(cols, {y, g, dx}),
+                     SoftmaxBackwardLaunch{y, g, dx, rows, cols, s, &rc}))
+        return rc;
+    EHIP_LAUNCH("softmax_backward", softmax_rows_backward_loop, dim3(loop_grid(rows)),
+                dim3(kLoopThreads), 0, s, y, g, dx, rows, cols);
+    return EHIP_OK;
+}
+
+int ehip_cross_entropy_f32(const float* logits, const int32_t* targets, float* probs, float* loss,
+                           int64_t rows, int64_t cols, void* stream) {
+    EHIP_READY();
+    if (rows <= 0 || cols <= 0) return fail(EHIP_EINVAL, "cross_entropy: bad shape");
+    if (!logits || !targets || !probs || !loss)
+        return fail(EHIP_EINVAL, "cross_entropy: null pointer");
+    hipStream_t s = as_stream(stream);
+    float* row_loss = static_cast<float*>(scratch(size_t(rows) * sizeof(float)));
+    if (row_loss == nullptr) return EHIP_ENOMEM;
+    int rc = EHIP_OK;
+    if (!dispatch_row(cols, rows_vec_ok(cols, {logits, probs}),
+                      XentLaunch{logits, targets, probs, row_loss, rows, cols, s, &rc})) {
+        EHIP_LAUNCH("cross_entropy", xent_rows_loop, dim3(loop_grid(rows)), dim3(kLoopThreads), 0,
+                    s, logits, targets, probs, row_loss, rows, cols);
+    }
+    if (rc != EHIP_OK) return rc;
+    EHIP_LAUNCH("cross_entropy_mean", mean_rows, dim3(1), dim3(1024), 0, s, row_loss, rows, loss);
+    return EHIP_OK;
+}
+
+int ehip_cross_entropy_backward_f32(const float* probs, const int32_t* targets, float* dx,
+                                    int64_t rows, int64_t cols, const float* grad, void* stream) {
+    EHIP_READY();
+    if (rows <= 0 || cols <= 0) return fail(EHIP_EINVAL, "cross_entropy_backward: bad shape");
+    if (!probs || !targets || !dx || !grad)
+        return fail(EHIP_EINVAL, "cross_entropy_backward: null pointer");
+    int64_t grid = ceil_div(rows * cols, 256);
+    if (grid > 131072) grid = 131072;
+    EHIP_LAUNCH("cross_entropy_backward", xent_backward_from_probs, dim3(unsigned(grid)), dim3(256),
+                0, as_stream(stream), probs, targets, dx, rows, cols, grad);
+    return EHIP_OK;
+}
+
+int ehip_softmax_xent_backward_f32(const float* logits, const int32_t* targets, float* dx,
+                                   int64_t rows, int64_t cols, const float* grad, void* stream) {
+    EHIP_READY();
+    if (rows <= 0 || cols <= 0) return fail(EHIP_EINVAL, "softmax_xent_backward: bad shape");
+    if (!logits || !targets || !dx || !grad)
+        return fail(EHIP_EINVAL, "softmax_xent_backward: null pointer");
+    hipStream_t s = as_stream(stream);
+    int rc = EHIP_OK;
+    if (dispatch_row(cols, rows_vec_ok(cols, {logits, dx}),
+                     XentBackwardLaunch{logits, targets, dx, rows, cols, grad, s, &rc}))
+        return rc;
+    EHIP_LAUNCH("softmax_xent_backward", xent_rows_backward_loop, dim3(loop_grid(rows)),
+                dim3(kLoopThreads), 0, s, logits, targets, dx, rows, cols, grad);
+    return EHIP_OK;
+}
+
+int ehip_layernorm_f32(const float* x, const float* gamma, const float* beta, float* out,
+                       float* xhat, float* inv_std, int64_t rows, int64_t cols, float eps,
+                       void* stream) {
+    EHIP_READY();
+    if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "layernorm: bad shape");
+    if (cols > 8192) return fail(EHIP_EINVAL, "layernorm: width %lld > 8192", (long long)cols);
+    if (!x || !gamma || !beta || !out || !xhat || !inv_std)
+        return fail(EHIP_EINVAL, "layernorm: null pointer");
+    if (rows == 0) return EHIP_OK;
+    hipStream_t s = as_stream(stream);
+#define EHIP_LN(T, V)                                                                        \
+    EHIP_LAUNCH("layernorm", (layernorm_rows<T, V>),                                         \
+                dim3(row_grid(rows, Group<T>::kPerBlock)), dim3(Group<T>::kBlock), 0, s, x, \
+                gamma, beta, out, xhat, inv_std, rows, cols, eps)
+    if (cols <= 64) EHIP_LN(64, 1);
+    else if (cols <= 128) EHIP_LN(64, 2);
+    else if (cols <= 256) EHIP_LN(64, 4);
+    else if (cols <= 512) EHIP_LN(64, 8);
+    else if (cols <= 1024) EHIP_LN(64, 16);
+    else if (cols <= 2048) EHIP_LN(64, 32);
+    else if (cols <= 4096) EHIP_LN(256, 16);
+    else EHIP_LN(256, 32);
+#undef EHIP_LN
+    return EHIP_OK;
+}
+
+int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float* gamma,
+                                const float* inv_std, float* dx, float* dgamma, float* dbeta,
+                                int64_t rows, int64_t cols, void* stream) {
+    EHIP_READY();
+    if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "layernorm_backward: bad shape");
+    if (cols > 8192)
+        return fail(EHIP_EINVAL, "layernorm_backward: width %lld > 8192", (long long)cols);
+    if (!dy || !xhat || !gamma || !inv_std || !dx || !dgamma || !dbeta)
+        return fail(EHIP_EINVAL, "layernorm_backward: null pointer");
+    hipStream_t s = as_stream(stream);
+    // A fixed number of row groups per shape: about 16 rows each, at most 512.
+    const int per_block = cols <= 2048 ? 4 : 1;
+    int64_t groups = ceil_div(rows, 16);
+    if (groups > 512) groups = 512;
+    if (groups < 1) groups = 1;
+    groups = ceil_div(groups, per_block) * per_block;
+    const unsigned grid = unsigned(groups / per_block);
+    float* partial = static_cast<float*>(scratch(size_t(groups) * 2 * size_t(cols) * sizeof(float)));
+    if (partial == nullptr) return EHIP_ENOMEM;
+#define EHIP_LNB(T, V)                                                                          \
+    EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward<T, V>), dim3(grid),              \
+                dim3(Group<T>::kBlock), 0, s, dy, xhat, gamma, inv_std, dx, partial, rows, cols)
+    if (cols <= 64) EHIP_LNB(64, 1);
+    else if (cols <= 128) EHIP_LNB(64, 2);
+    else if (cols <= 256) EHIP_LNB(64, 4);
+    else if (cols <= 512) EHIP_LNB(64, 8);
+    else if (cols <= 1024) EHIP_LNB(64, 16);
+    else if (cols <= 2048) EHIP_LNB(64, 32);
+    else if (cols <= 4096) EHIP_LNB(256, 16);
+    else EHIP_LNB(256, 32);
+#undef EHIP_LNB
+    EHIP_LAUNCH("layernorm_backward_reduce", layernorm_reduce_partials,
+                dim3(unsigned(ceil_div(2 * cols, 256))), dim3(256), 0, s, partial, dgamma, dbeta,
+                groups, cols);
+    return EHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,355 @@
+// runtime.hip -- device context, status reporting, counters, the pooled HBM
+// arena and host/device copies.
+//
+// Replaces the reference's runtime (src/cuda/runtime.cu:65-152 context and
+// peaks, 216-225 counters, 352-418 allocation and copies) and the host buffer
+// pool of src/storage.cpp:44-128. One device (device 0), one engine stream.
+
+#include "common.hpp"
+
+#include <atomic>
+#include <chrono>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace ehip {
+namespace {
+
+thread_local std::string g_error;
+
+struct Context {
+    bool ok = false;
+    int status = EHIP_ENODEV;
+    std::string why;
+    hipDeviceProp_t prop{};
+};
+
+std::once_flag g_init_once;
+Context g_ctx;
+std::atomic<int> g_enabled{1};
+std::atomic<uint64_t> g_launched{0};
+std::atomic<uint64_t> g_failed{0};
+std::atomic<uint64_t> g_launch_serial{0};
+int64_t g_fail_launch_at = 0;  // ENGINE_HIP_FAIL_LAUNCH
+bool g_sync_each = false;      // ENGINE_HIP_SYNC
+
+std::mutex g_stats_mu;
+ehip_transfer_stats_t g_stats{};
+
+void init_once() {
+    const char* on = std::getenv("ENGINE_HIP");
+    if (on != nullptr && std::strcmp(on, "0") == 0) g_enabled = 0;
+    const char* fl = std::getenv("ENGINE_HIP_FAIL_LAUNCH");
+    if (fl != nullptr) g_fail_launch_at = std::atoll(fl);
+    const char* sy = std::getenv("ENGINE_HIP_SYNC");
+    g_sync_each = sy != nullptr && std::strcmp(sy, "1") == 0;
+
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) {
+        g_ctx.why = std::string("no HIP device: ") +
+                    (e != hipSuccess ? hipGetErrorString(e) : "device count is 0");
+        return;
+    }
+    e = hipSetDevice(0);
+    if (e == hipSuccess) e = hipGetDeviceProperties(&g_ctx.prop, 0);
+    if (e != hipSuccess) {
+        g_ctx.why = std::string("device 0: ") + hipGetErrorString(e);
+        return;
+    }
+    if (std::strncmp(g_ctx.prop.gcnArchName, "gfx950", 6) != 0) {
+        g_ctx.why = std::string("device 0 is ") + g_ctx.prop.gcnArchName +
+                    ", this library is built for gfx950 only";
+        return;
+    }
+    g_ctx.ok = true;
+    g_ctx.status = EHIP_OK;
+}
+
+}  // namespace
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int ready() {
+    std::call_once(g_init_once, init_once);
+    if (!g_ctx.ok) return fail(g_ctx.status, "%s", g_ctx.why.c_str());
+    if (!g_enabled.load(std::memory_order_relaxed))
+        return fail(EHIP_EDISABLED, "the HIP backend is switched off");
+    return EHIP_OK;
+}
+
+int before_launch(const char* name) {
+    const uint64_t serial = ++g_launch_serial;
+    if (g_fail_launch_at > 0 && serial == static_cast<uint64_t>(g_fail_launch_at)) {
+        ++g_failed;
+        return fail(EHIP_ELAUNCH, "%s: launch %llu refused by ENGINE_HIP_FAIL_LAUNCH", name,
+                    static_cast<unsigned long long>(serial));
+    }
+    return EHIP_OK;
+}
+
+int after_launch(const char* name, hipStream_t stream) {
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && g_sync_each) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) {
+        ++g_failed;
+        return fail(EHIP_ELAUNCH, "%s: %s", name, hipGetErrorString(e));
+    }
+    ++g_launched;
+    return EHIP_OK;
+}
+
+// ------------------------------------------------------------------ arena
+
+namespace {
+
+struct Arena {
+    std::mutex mu;
+    std::unordered_map<size_t, std::vector<void*>> cache;  // class size -> free blocks
+    std::unordered_map<void*, size_t> live;                // block -> class size
+    ehip_arena_stats_t stats{};
+};
+
+Arena& arena() {
+    static Arena* a = new Arena();  // never destroyed: blocks outlive static teardown
+    return *a;
+}
+
+// 256-byte granules up to 4 KiB, then four classes per power of two.
+size_t size_class(size_t bytes) {
+    size_t n = bytes < 256 ? 256 : (bytes + 255) & ~size_t(255);
+    if (n <= 4096) return n;
+    int e = 63 - __builtin_clzll(n);
+    size_t step = (size_t(1) << e) / 4;
+    return (n + step - 1) / step * step;
+}
+
+// Frees every cached block. Caller holds the lock.
+void release_cache(Arena& a) {
+    (void)hipDeviceSynchronize();
+    for (auto& kv : a.cache) {
+        for (void* p : kv.second) {
+            (void)hipFree(p);
+            a.stats.bytes_cached -= kv.first;
+            a.stats.bytes_reserved -= kv.first;
+        }
+        kv.second.clear();
+    }
+}
+
+}  // namespace
+
+void* scratch(size_t bytes) {
+    static std::mutex mu;
+    static void* buf = nullptr;
+    static size_t cap = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    if (bytes <= cap) return buf;
+    size_t want = cap * 2 > bytes ? cap * 2 : bytes;
+    void* p = nullptr;
+    if (ehip_arena_alloc(want, &p) != EHIP_OK) return nullptr;
+    if (buf != nullptr) ehip_arena_free(buf);
+    buf = p;
+    cap = want;
+    return buf;
+}
+
+}  // namespace ehip
+
+using namespace ehip;
+
+extern "C" {
+
+const char* ehip_last_error(void) { return g_error.c_str(); }
+
+int ehip_init(void) {
+    std::call_once(g_init_once, init_once);
+    if (!g_ctx.ok) return fail(g_ctx.status, "%s", g_ctx.why.c_str());
+    return EHIP_OK;
+}
+
+int ehip_available(void) { return ehip_init() == EHIP_OK ? 1 : 0; }
+
+int ehip_enabled(void) { return g_enabled.load(); }
+
+void ehip_set_enabled(int on) {
+    std::call_once(g_init_once, init_once);
+    g_enabled = on ? 1 : 0;
+}
+
+int ehip_device_info(ehip_device_info_t* out) {
+    if (out == nullptr) return fail(EHIP_EINVAL, "ehip_device_info: null output");
+    if (int rc = ehip_init()) return rc;
+    const hipDeviceProp_t& p = g_ctx.prop;
+    std::memset(out, 0, sizeof *out);
+    std::snprintf(out->name, sizeof out->name, "%s", p.name);
+    std::snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
+    out->compute_units = p.multiProcessorCount;
+    out->clock_khz = p.clockRate;
+    out->memory_clock_khz = p.memoryClockRate;
+    out->memory_bus_width_bits = p.memoryBusWidth;
+    out->total_memory = p.totalGlobalMem;
+    out->lds_per_block = p.sharedMemPerBlock;
+    out->l2_bytes = p.l2CacheSize;
+    // fp32 MFMA retires 256 FLOP per clock per CU on CDNA4.
+    out->peak_fp32_mfma_gflops = double(p.multiProcessorCount) * 256.0 * double(p.clockRate) * 1e-6;
+    out->peak_hbm_gbs = 2.0 * double(p.memoryClockRate) * 1e3 * double(p.memoryBusWidth) / 8.0 * 1e-9;
+    return EHIP_OK;
+}
+
+int ehip_synchronize(void) {
+    if (int rc = ehip_init()) return rc;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return fail(EHIP_ELAUNCH, "synchronize: %s", hipGetErrorString(e));
+    return EHIP_OK;
+}
+
+int ehip_stream_synchronize(void* stream) {
+    if (int rc = ehip_init()) return rc;
+    hipError_t e = hipStreamSynchronize(as_stream(stream));
+    if (e != hipSuccess) return fail(EHIP_ELAUNCH, "stream synchronize: %s", hipGetErrorString(e));
+    return EHIP_OK;
+}
+
+uint64_t ehip_kernels_launched(void) { return g_launched.load(); }
+uint64_t ehip_kernels_failed(void) { return g_failed.load(); }
+void ehip_reset_counters(void) {
+    g_launched = 0;
+    g_failed = 0;
+}
+
+void ehip_transfer_stats(ehip_transfer_stats_t* out) {
+    if (out == nullptr) return;
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    *out = g_stats;
+}
+
+void ehip_reset_transfer_stats(void) {
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    g_stats = ehip_transfer_stats_t{};
+}
+
+int ehip_arena_alloc(size_t bytes, void** out) {
+    if (out == nullptr) return fail(EHIP_EINVAL, "ehip_arena_alloc: null output");
+    *out = nullptr;
+    if (int rc = ehip_init()) return rc;
+    const size_t cls = size_class(bytes);
+    Arena& a = arena();
+    std::lock_guard<std::mutex> lock(a.mu);
+    ++a.stats.allocations;
+    auto it = a.cache.find(cls);
+    if (it != a.cache.end() && !it->second.empty()) {
+        void* p = it->second.back();
+        it->second.pop_back();
+        a.live[p] = cls;
+        a.stats.bytes_cached -= cls;
+        a.stats.bytes_in_use += cls;
+        *out = p;
+        return EHIP_OK;
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, cls);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        release_cache(a);
+        e = hipMalloc(&p, cls);
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(EHIP_ENOMEM, "hipMalloc(%zu): %s", cls, hipGetErrorString(e));
+    }
+    ++a.stats.driver_allocations;
+    a.stats.bytes_reserved += cls;
+    a.stats.bytes_in_use += cls;
+    a.live[p] = cls;
+    *out = p;
+    return EHIP_OK;
+}
+
+void ehip_arena_free(void* ptr) {
+    if (ptr == nullptr) return;
+    Arena& a = arena();
+    std::lock_guard<std::mutex> lock(a.mu);
+    auto it = a.live.find(ptr);
+    if (it == a.live.end()) {
+        std::fprintf(stderr, "ehip_arena_free: %p was not allocated by the arena\n", ptr);
+        return;
+    }
+    const size_t cls = it->second;
+    a.live.erase(it);
+    a.cache[cls].push_back(ptr);
+    a.stats.bytes_in_use -= cls;
+    a.stats.bytes_cached += cls;
+}
+
+int ehip_arena_trim(void) {
+    if (int rc = ehip_init()) return rc;
+    Arena& a = arena();
+    std::lock_guard<std::mutex> lock(a.mu);
+    release_cache(a);
+    return EHIP_OK;
+}
+
+void ehip_arena_stats(ehip_arena_stats_t* out) {
+    if (out == nullptr) return;
+    Arena& a = arena();
+    std::lock_guard<std::mutex> lock(a.mu);
+    *out = a.stats;
+}
+
+namespace {
+
+int copy(void* dst, const void* src, size_t bytes, void* stream, hipMemcpyKind kind) {
+    if (int rc = ehip_init()) return rc;
+    if (bytes == 0) return EHIP_OK;
+    if (dst == nullptr || src == nullptr) return fail(EHIP_EINVAL, "memcpy: null pointer");
+    const auto t0 = std::chrono::steady_clock::now();
+    hipStream_t s = as_stream(stream);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, s);
+    if (e == hipSuccess && kind != hipMemcpyDeviceToDevice) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(EHIP_ELAUNCH, "memcpy: %s", hipGetErrorString(e));
+    const double sec =
+        std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    if (kind == hipMemcpyHostToDevice) {
+        g_stats.to_device_bytes += bytes;
+        ++g_stats.to_device_count;
+        g_stats.to_device_seconds += sec;
+    } else if (kind == hipMemcpyDeviceToHost) {
+        g_stats.to_host_bytes += bytes;
+        ++g_stats.to_host_count;
+        g_stats.to_host_seconds += sec;
+    } else {
+        g_stats.device_to_device_bytes += bytes;
+        ++g_stats.device_to_device_count;
+    }
+    return EHIP_OK;
+}
+
+}  // namespace
+
+int ehip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+    return copy(dst, src, bytes, stream, hipMemcpyHostToDevice);
+}
+int ehip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+    return copy(dst, src, bytes, stream, hipMemcpyDeviceToHost);
+}
+int ehip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    return copy(dst, src, bytes, stream, hipMemcpyDeviceToDevice);
+}
+
+}  // extern "C"

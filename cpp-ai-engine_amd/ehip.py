@@ -1,0 +1,371 @@
+"""ctypes binding of libehip.so, the C ABI declared in include/ehip.h.
+
+The library takes raw device pointers; this module accepts torch tensors that
+live on the GPU (torch is only the allocator and stream provider here) and
+turns every nonzero status into a RuntimeError carrying ehip_last_error().
+Loading fails loudly if the library is not built: there is no fallback.
+"""
+import ctypes as C
+import os
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(ROOT, "lib", "libehip.so")
+HEADER = os.path.join(os.path.dirname(ROOT), "include", "ehip.h")
+
+_vp, _i, _i64, _f, _sz = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
+
+ADD, SUB, MUL, DIV = 0, 1, 2, 3
+
+
+class Window(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in (
+        "batch", "channels", "height", "width", "kernel_h", "kernel_w", "stride", "padding",
+        "out_h", "out_w")]
+
+
+def window(n, c, h, w, kh, kw, stride, pad):
+    return Window(n, c, h, w, kh, kw, stride, pad, (h + 2 * pad - kh) // stride + 1,
+                  (w + 2 * pad - kw) // stride + 1)
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 256), ("arch", C.c_char * 64), ("compute_units", C.c_int),
+                ("clock_khz", C.c_int), ("memory_clock_khz", C.c_int),
+                ("memory_bus_width_bits", C.c_int), ("total_memory", C.c_size_t),
+                ("lds_per_block", C.c_size_t), ("l2_bytes", C.c_int),
+                ("peak_fp32_mfma_gflops", C.c_double), ("peak_hbm_gbs", C.c_double)]
+
+
+class ArenaStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("bytes_in_use", "bytes_cached", "bytes_reserved",
+                                         "allocations", "driver_allocations")]
+
+
+class TransferStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "to_device_bytes", "to_host_bytes", "device_to_device_bytes", "to_device_count",
+        "to_host_count", "device_to_device_count")] + [
+        ("to_device_seconds", C.c_double), ("to_host_seconds", C.c_double)]
+
+
+# name -> argtypes (all return int unless listed in _RESTYPES)
+_SIGS = {
+    "ehip_init": [], "ehip_available": [], "ehip_enabled": [], "ehip_set_enabled": [_i],
+    "ehip_device_info": [C.POINTER(DeviceInfo)], "ehip_synchronize": [],
+    "ehip_stream_synchronize": [_vp], "ehip_kernels_launched": [], "ehip_kernels_failed": [],
+    "ehip_reset_counters": [], "ehip_transfer_stats": [C.POINTER(TransferStats)],
+    "ehip_reset_transfer_stats": [], "ehip_arena_alloc": [_sz, C.POINTER(_vp)],
+    "ehip_arena_free": [_vp], "ehip_arena_trim": [], "ehip_arena_stats": [C.POINTER(ArenaStats)],
+    "ehip_memcpy_h2d": [_vp, _vp, _sz, _vp], "ehip_memcpy_d2h": [_vp, _vp, _sz, _vp],
+    "ehip_memcpy_d2d": [_vp, _vp, _sz, _vp],
+    "ehip_gemm_f32": [_i, _i, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _f, _vp,
+                      _i64, _i64, _vp],
+    "ehip_binary_f32": [_i, _vp, _vp, _vp, _i64, _i64, _vp],
+    "ehip_scalar_f32": [_vp, _vp, _i64, _f, _f, _vp],
+    "ehip_relu_f32": [_vp, _vp, _i64, _vp],
+    "ehip_relu_backward_f32": [_vp, _vp, _vp, _i64, _vp],
+    "ehip_accumulate_grad_f32": [_vp, _vp, _i64, _i, _vp],
+    "ehip_add_backward_f32": [_vp, _vp, _vp, _i64, _i, _i, _vp],
+    "ehip_fill_f32": [_vp, _i64, _f, _vp],
+    "ehip_scale_f32": [_vp, _i64, _f, _vp],
+    "ehip_sgd_f32": [_vp, _vp, _vp, _i64, _f, _f, _f, _vp],
+    "ehip_adam_f32": [_vp, _vp, _vp, _vp, _i64] + [_f] * 7 + [_vp],
+    "ehip_permute_f32": [_vp, _vp, _i, C.POINTER(_i64), C.POINTER(_i64), _vp],
+    "ehip_transpose_f32": [_vp, _vp, _i64, _i64, _i64, _vp],
+    "ehip_im2col_f32": [_vp, _vp, C.POINTER(Window), _vp],
+    "ehip_col2im_f32": [_vp, _vp, C.POINTER(Window), _vp],
+    "ehip_maxpool_f32": [_vp, _vp, _vp, C.POINTER(Window), _vp],
+    "ehip_maxpool_backward_f32": [_vp, _vp, _vp, C.POINTER(Window), _vp],
+    "ehip_select_rows_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "ehip_scatter_add_rows_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp],
+    "ehip_sum_axis_f32": [_vp, _vp, _i64, _i64, _i64, _vp],
+    "ehip_reduce_sum_f32": [_vp, _i64, _i, _vp, _vp, _vp],
+    "ehip_softmax_f32": [_vp, _vp, _i64, _i64, _vp],
+    "ehip_softmax_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp],
+    "ehip_layernorm_f32": [_vp] * 6 + [_i64, _i64, _f, _vp],
+    "ehip_layernorm_backward_f32": [_vp] * 7 + [_i64, _i64, _vp],
+    "ehip_cross_entropy_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
+    "ehip_cross_entropy_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
+    "ehip_softmax_xent_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
+    "ehip_last_error": [],
+}
+_RESTYPES = {"ehip_last_error": C.c_char_p, "ehip_kernels_launched": C.c_uint64,
+             "ehip_kernels_failed": C.c_uint64, "ehip_reset_counters": None,
+             "ehip_set_enabled": None, "ehip_transfer_stats": None,
+             "ehip_reset_transfer_stats": None, "ehip_arena_free": None,
+             "ehip_arena_stats": None}
+
+
+def load_library(path=LIB_PATH):
+    """Loads libehip.so and declares every entry point; no GPU needed."""
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build() or "
+                                f"make -C cpp-ai-engine_amd")
+    lib = C.CDLL(path)
+    for name, args in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPES.get(name, C.c_int)
+    return lib
+
+
+def header_symbols(path=HEADER):
+    """Names of every function include/ehip.h declares."""
+    import re
+    text = open(path).read()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int|void|uint64_t)\s+(ehip_\w+)\(", text,
+                                 re.M)))
+
+
+class Backend:
+    """The device ops over torch CUDA tensors. Raises if no gfx950 device."""
+
+    def __init__(self, path=LIB_PATH):
+        import torch
+        self.torch = torch
+        self.lib = load_library(path)
+        rc = self.lib.ehip_init()
+        if rc != 0:
+            raise RuntimeError(f"ehip_init failed ({rc}): {self.error()}")
+
+    # ---------------------------------------------------------- plumbing
+    def error(self):
+        return self.lib.ehip_last_error().decode()
+
+    def ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed ({rc}): {self.error()}")
+
+    def stream(self):
+        return _vp(self.torch.cuda.current_stream().cuda_stream)
+
+    @staticmethod
+    def p(t):
+        if t is None:
+            return None
+        assert t.is_cuda and t.is_contiguous(), "device tensors must be contiguous on the GPU"
+        return _vp(t.data_ptr())
+
+    def f32(self, shape):
+        return self.torch.empty(shape, dtype=self.torch.float32, device="cuda")
+
+    def device_info(self):
+        info = DeviceInfo()
+        self.ok(self.lib.ehip_device_info(C.byref(info)), "device_info")
+        return info
+
+    def launched(self):
+        return self.lib.ehip_kernels_launched()
+
+    def arena_stats(self):
+        s = ArenaStats()
+        self.lib.ehip_arena_stats(C.byref(s))
+        return s
+
+    # ---------------------------------------------------------- dense
+    def gemm(self, a, b, c=None, trans_a=False, trans_b=False, beta=0.0):
+        """c = op(a) op(b) + beta c; a, b 2-D or 3-D (batched), 2-D operands shared."""
+        ab, bb = a.dim() == 3, b.dim() == 3
+        batch = a.shape[0] if ab else (b.shape[0] if bb else 1)
+        am, ak = a.shape[-2:]
+        m, k = (ak, am) if trans_a else (am, ak)
+        bk, bn = b.shape[-2:]
+        kb, n = (bn, bk) if trans_b else (bk, bn)
+        assert k == kb, (a.shape, b.shape, trans_a, trans_b)
+        if c is None:
+            c = self.f32((batch, m, n) if (ab or bb) else (m, n))
+        self.ok(self.lib.ehip_gemm_f32(int(trans_a), int(trans_b), batch, m, n, k, self.p(a),
+                                       a.shape[-1], am * ak if ab else 0, self.p(b), b.shape[-1],
+                                       bk * bn if bb else 0, beta, self.p(c), n,
+                                       m * n if (ab or bb) else 0, self.stream()), "gemm")
+        return c
+
+    # ---------------------------------------------------------- element-wise
+    def binary(self, op, a, b, out=None):
+        out = self.f32(a.shape) if out is None else out
+        inner = b.numel()
+        self.ok(self.lib.ehip_binary_f32(op, self.p(a), self.p(b), self.p(out), inner,
+                                         a.numel() // inner, self.stream()), "binary")
+        return out
+
+    def scalar(self, x, mul, add):
+        out = self.f32(x.shape)
+        self.ok(self.lib.ehip_scalar_f32(self.p(x), self.p(out), x.numel(), mul, add,
+                                         self.stream()), "scalar")
+        return out
+
+    def relu(self, x):
+        y = self.f32(x.shape)
+        self.ok(self.lib.ehip_relu_f32(self.p(x), self.p(y), x.numel(), self.stream()), "relu")
+        return y
+
+    def relu_backward(self, x, g, dx=None):
+        dx = self.f32(x.shape) if dx is None else dx
+        self.ok(self.lib.ehip_relu_backward_f32(self.p(x), self.p(g), self.p(dx), x.numel(),
+                                                self.stream()), "relu_backward")
+        return dx
+
+    def accumulate_grad(self, grad, g, initialize):
+        self.ok(self.lib.ehip_accumulate_grad_f32(self.p(grad), self.p(g), g.numel(),
+                                                  int(initialize), self.stream()),
+                "accumulate_grad")
+        return grad
+
+    def add_backward(self, g, da, db, acc_a, acc_b):
+        self.ok(self.lib.ehip_add_backward_f32(self.p(g), self.p(da), self.p(db), g.numel(),
+                                               int(acc_a), int(acc_b), self.stream()),
+                "add_backward")
+
+    def fill(self, x, value):
+        self.ok(self.lib.ehip_fill_f32(self.p(x), x.numel(), value, self.stream()), "fill")
+        return x
+
+    def scale(self, x, factor):
+        self.ok(self.lib.ehip_scale_f32(self.p(x), x.numel(), factor, self.stream()), "scale")
+        return x
+
+    def sgd(self, p, g, vel, lr, momentum, wd):
+        self.ok(self.lib.ehip_sgd_f32(self.p(p), self.p(g), self.p(vel), p.numel(), lr, momentum,
+                                      wd, self.stream()), "sgd")
+
+    def adam(self, p, g, m, v, lr, b1, b2, eps, wd, c1, c2):
+        self.ok(self.lib.ehip_adam_f32(self.p(p), self.p(g), self.p(m), self.p(v), p.numel(), lr,
+                                       b1, b2, eps, wd, c1, c2, self.stream()), "adam")
+
+    # ---------------------------------------------------------- layout
+    def permute(self, x, order):
+        shape = list(x.shape)
+        in_stride = [1] * len(shape)
+        for d in range(len(shape) - 2, -1, -1):
+            in_stride[d] = in_stride[d + 1] * shape[d + 1]
+        out_shape = [shape[o] for o in order]
+        src = [in_stride[o] for o in order]
+        out = self.f32(out_shape)
+        arr = C.c_int64 * len(shape)
+        self.ok(self.lib.ehip_permute_f32(self.p(x), self.p(out), len(shape), arr(*out_shape),
+                                          arr(*src), self.stream()), "permute")
+        return out
+
+    def transpose(self, x):
+        rows, cols = x.shape[-2:]
+        batch = x.numel() // max(1, rows * cols)
+        out = self.f32(tuple(x.shape[:-2]) + (cols, rows))
+        self.ok(self.lib.ehip_transpose_f32(self.p(x), self.p(out), batch, rows, cols,
+                                            self.stream()), "transpose")
+        return out
+
+    def im2col(self, x, kh, kw, stride, pad):
+        w = window(*x.shape, kh, kw, stride, pad)
+        cols = self.f32((w.batch * w.out_h * w.out_w, w.channels * kh * kw))
+        self.ok(self.lib.ehip_im2col_f32(self.p(x), self.p(cols), C.byref(w), self.stream()),
+                "im2col")
+        return cols
+
+    def col2im(self, cols, shape, kh, kw, stride, pad):
+        w = window(*shape, kh, kw, stride, pad)
+        x = self.f32(shape)
+        self.ok(self.lib.ehip_col2im_f32(self.p(cols), self.p(x), C.byref(w), self.stream()),
+                "col2im")
+        return x
+
+    def maxpool(self, x, k, stride, pad=0):
+        w = window(*x.shape, k, k, stride, pad)
+        y = self.f32((w.batch, w.channels, w.out_h, w.out_w))
+        am = self.torch.empty(y.shape, dtype=self.torch.int32, device="cuda")
+        self.ok(self.lib.ehip_maxpool_f32(self.p(x), self.p(y), self.p(am), C.byref(w),
+                                          self.stream()), "maxpool")
+        return y, am
+
+    def maxpool_backward(self, argmax, g, in_shape, k, stride, pad=0):
+        w = window(*in_shape, k, k, stride, pad)
+        dx = self.f32(in_shape)
+        self.ok(self.lib.ehip_maxpool_backward_f32(self.p(argmax), self.p(g), self.p(dx),
+                                                   C.byref(w), self.stream()), "maxpool_backward")
+        return dx
+
+    def select_rows(self, x, idx):
+        rs = x.numel() // x.shape[0]
+        out = self.f32((idx.numel(),) + tuple(x.shape[1:]))
+        self.ok(self.lib.ehip_select_rows_f32(self.p(x), self.p(idx), self.p(out), idx.numel(),
+                                              rs, x.shape[0], self.stream()), "select_rows")
+        return out
+
+    def scatter_add_rows(self, g, row_ptr, pos, dx, accumulate=False):
+        rs = dx.numel() // dx.shape[0]
+        self.ok(self.lib.ehip_scatter_add_rows_f32(self.p(g), self.p(row_ptr), self.p(pos),
+                                                   self.p(dx), dx.shape[0], rs, g.shape[0],
+                                                   int(accumulate), self.stream()),
+                "scatter_add_rows")
+        return dx
+
+    # ---------------------------------------------------------- reductions
+    def sum_axis(self, x, outer, axis_len, inner):
+        out = self.f32((outer * inner,))
+        self.ok(self.lib.ehip_sum_axis_f32(self.p(x), self.p(out), outer, axis_len, inner,
+                                           self.stream()), "sum_axis")
+        return out
+
+    def reduce_sum(self, x, squares=False):
+        d = self.torch.empty(1, dtype=self.torch.float64, device="cuda")
+        f = self.f32((1,))
+        self.ok(self.lib.ehip_reduce_sum_f32(self.p(x), x.numel(), int(squares), self.p(d),
+                                             self.p(f), self.stream()), "reduce_sum")
+        return d, f
+
+    # ---------------------------------------------------------- rows
+    def softmax(self, x):
+        cols = x.shape[-1]
+        y = self.f32(x.shape)
+        self.ok(self.lib.ehip_softmax_f32(self.p(x), self.p(y), x.numel() // cols, cols,
+                                          self.stream()), "softmax")
+        return y
+
+    def softmax_backward(self, y, g):
+        cols = y.shape[-1]
+        dx = self.f32(y.shape)
+        self.ok(self.lib.ehip_softmax_backward_f32(self.p(y), self.p(g), self.p(dx),
+                                                   y.numel() // cols, cols, self.stream()),
+                "softmax_backward")
+        return dx
+
+    def layernorm(self, x, gamma, beta, eps=1e-5):
+        d = x.shape[-1]
+        rows = x.numel() // d
+        out, xhat, inv = self.f32(x.shape), self.f32(x.shape), self.f32((rows,))
+        self.ok(self.lib.ehip_layernorm_f32(self.p(x), self.p(gamma), self.p(beta), self.p(out),
+                                            self.p(xhat), self.p(inv), rows, d, eps,
+                                            self.stream()), "layernorm")
+        return out, xhat, inv
+
+    def layernorm_backward(self, dy, xhat, gamma, inv):
+        d = dy.shape[-1]
+        dx, dg, db = self.f32(dy.shape), self.f32((d,)), self.f32((d,))
+        self.ok(self.lib.ehip_layernorm_backward_f32(self.p(dy), self.p(xhat), self.p(gamma),
+                                                     self.p(inv), self.p(dx), self.p(dg),
+                                                     self.p(db), dy.numel() // d, d,
+                                                     self.stream()), "layernorm_backward")
+        return dx, dg, db
+
+    def cross_entropy(self, logits, targets):
+        rows, cols = logits.shape
+        probs, loss = self.f32(logits.shape), self.f32((1,))
+        self.ok(self.lib.ehip_cross_entropy_f32(self.p(logits), self.p(targets), self.p(probs),
+                                                self.p(loss), rows, cols, self.stream()),
+                "cross_entropy")
+        return loss, probs
+
+    def cross_entropy_backward(self, probs, targets, grad):
+        rows, cols = probs.shape
+        dx = self.f32(probs.shape)
+        self.ok(self.lib.ehip_cross_entropy_backward_f32(self.p(probs), self.p(targets),
+                                                         self.p(dx), rows, cols, self.p(grad),
+                                                         self.stream()), "cross_entropy_backward")
+        return dx
+
+    def softmax_xent_backward(self, logits, targets, grad, dx=None):
+        rows, cols = logits.shape
+        dx = self.f32(logits.shape) if dx is None else dx
+        self.ok(self.lib.ehip_softmax_xent_backward_f32(self.p(logits), self.p(targets),
+                                                        self.p(dx), rows, cols, self.p(grad),
+                                                        self.stream()), "softmax_xent_backward")
+        return dx

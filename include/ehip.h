@@ -1,0 +1,324 @@
+/*
+ * ehip.h -- the C ABI of the MI355X (gfx950) backend for cpp-ai-engine's fp32
+ * training path.
+ *
+ * This is the drop-in boundary. It replaces the reference's device seam
+ * `engine::cuda::ops` (include/engine/detail/cuda_ops.hpp:25-203), its runtime
+ * control API (include/engine/cuda.hpp:23-218) and its memory primitives
+ * (include/engine/cuda.hpp:229-236). Paths in citations are relative to the
+ * reference repository root.
+ *
+ * Conventions
+ *   - Every pointer argument named like a tensor is a DEVICE pointer to fp32
+ *     (or int32 where stated), row-major and contiguous unless a leading
+ *     dimension says otherwise. Shape and geometry arguments are host values.
+ *   - `stream` is a hipStream_t passed as void*; NULL is the null stream. Work
+ *     is ordered on that stream; nothing here synchronises unless stated.
+ *   - Every entry point returns an int status: EHIP_OK (0) when the work was
+ *     enqueued, nonzero when it was refused (bad geometry, backend disabled)
+ *     or failed to launch. No C++ exception crosses this boundary.
+ *     ehip_last_error() gives the message of the last failure on the calling
+ *     thread. This is the reference's bool contract (true = the device took the
+ *     work, cuda_ops.hpp:14-23) with the reason kept.
+ *   - Results that the reference CPU path produces bit-for-bit (moves, index
+ *     maps, ordered sums, element-wise arithmetic without fused multiply-add,
+ *     the optimiser updates) are produced bit-for-bit here; the comment of each
+ *     entry point says which it is.
+ */
+#ifndef EHIP_H
+#define EHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ----------------------------------------------------------------- status */
+
+enum {
+    EHIP_OK = 0,
+    EHIP_EINVAL = 1,   /* refused: bad geometry, null pointer, size limit  */
+    EHIP_ELAUNCH = 2,  /* the kernel launch failed                         */
+    EHIP_ENODEV = 3,   /* no usable gfx950 device                          */
+    EHIP_ENOMEM = 4,   /* device allocation failed                         */
+    EHIP_EDISABLED = 5 /* the backend was switched off (ehip_set_enabled)  */
+};
+
+/* Message of the last nonzero status returned on this thread ("" if none). */
+const char* ehip_last_error(void);
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Selects device 0, checks that it is gfx950 and builds the context. Called
+ * implicitly by every other entry point. Replaces cuda::available()
+ * (include/engine/cuda.hpp:23; src/cuda/runtime.cu:77-151). */
+int ehip_init(void);
+int ehip_available(void);
+
+/* Runtime switch: when off, every kernel entry point returns EHIP_EDISABLED
+ * without launching (cuda::enabled/set_enabled, include/engine/cuda.hpp:28-29).
+ * The environment variable ENGINE_HIP=0 starts the process switched off. */
+int ehip_enabled(void);
+void ehip_set_enabled(int on);
+
+typedef struct {
+    char name[256];
+    char arch[64];              /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int compute_units;
+    int clock_khz;              /* peak engine clock                          */
+    int memory_clock_khz;
+    int memory_bus_width_bits;
+    size_t total_memory;
+    size_t lds_per_block;
+    int l2_bytes;
+    double peak_fp32_mfma_gflops; /* CUs x 256 FLOP/clk x clock            */
+    double peak_hbm_gbs;          /* 2 x memory clock x bus width / 8      */
+} ehip_device_info_t;
+
+/* cuda::device_info, peak_fp32_gflops, peak_bandwidth_gbs
+ * (include/engine/cuda.hpp:49, 93-95). */
+int ehip_device_info(ehip_device_info_t* out);
+
+/* Waits for all work on the device (cuda::synchronize, include/engine/cuda.hpp:53). */
+int ehip_synchronize(void);
+/* Waits for one stream. */
+int ehip_stream_synchronize(void* stream);
+
+/* Launch counters (cuda::kernels_launched/failed/reset_kernel_counters,
+ * include/engine/cuda.hpp:79-81). */
+uint64_t ehip_kernels_launched(void);
+uint64_t ehip_kernels_failed(void);
+void ehip_reset_counters(void);
+
+typedef struct {
+    uint64_t to_device_bytes, to_host_bytes, device_to_device_bytes;
+    uint64_t to_device_count, to_host_count, device_to_device_count;
+    double to_device_seconds, to_host_seconds;
+} ehip_transfer_stats_t;
+
+/* cuda::transfer_stats / reset_transfer_stats (include/engine/cuda.hpp:209-218). */
+void ehip_transfer_stats(ehip_transfer_stats_t* out);
+void ehip_reset_transfer_stats(void);
+
+/* ------------------------------------------------------- HBM arena, copies */
+
+/* Pooled device allocator: sizes are rounded up to a size class (256-byte
+ * granules, then quarter-powers of two), freed blocks are cached per class
+ * and reused, and nothing goes back to the driver until ehip_arena_trim().
+ * Freeing is stream-ordered with respect to the engine's one stream: a block
+ * freed while queued kernels still use it is only handed to later work on the
+ * same stream. Replaces cuda::detail::device_alloc/device_free
+ * (include/engine/cuda.hpp:229-230; src/cuda/runtime.cu:137-143, 352-387) and
+ * the host BufferPool (src/storage.cpp:44-128). */
+int ehip_arena_alloc(size_t bytes, void** out);
+void ehip_arena_free(void* ptr);
+int ehip_arena_trim(void);
+
+typedef struct {
+    uint64_t bytes_in_use;     /* rounded sizes of live blocks      */
+    uint64_t bytes_cached;     /* rounded sizes of cached free blocks */
+    uint64_t bytes_reserved;   /* everything obtained from the driver */
+    uint64_t allocations;      /* ehip_arena_alloc calls              */
+    uint64_t driver_allocations; /* misses that reached hipMalloc    */
+} ehip_arena_stats_t;
+void ehip_arena_stats(ehip_arena_stats_t* out);
+
+/* Copies of `bytes` bytes. Host-to-device and device-to-host return once the
+ * host buffer may be reused / read (cuda::detail::copy_to_device/copy_to_host/
+ * copy_device_to_device, include/engine/cuda.hpp:231-236). Device-to-device is
+ * stream-ordered and asynchronous. */
+int ehip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int ehip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int ehip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+
+/* ------------------------------------------------------------ dense GEMM */
+
+/* C[b] = op(A[b]) . op(B[b]) + beta * C[b], b in [0, batch).
+ * op(A) is m x k: A is m x k (lda >= k) when trans_a == 0, or k x m (lda >= m)
+ * when trans_a != 0; likewise op(B) is k x n. stride_* is the element distance
+ * between batch matrices; 0 shares one matrix across the batch (the reference's
+ * unbatched operand). beta == 0 overwrites C without reading it.
+ * fp32 MFMA (v_mfma_f32_32x32x2f32) with LDS-staged tiles; deterministic (a
+ * fixed summation order per shape), not bit-equal to the CPU's serial sums.
+ * Replaces cuda::ops::matmul (include/engine/detail/cuda_ops.hpp:46-47); the
+ * transposed modes replace the materialised transposes of the backward pass
+ * (src/tensor_ops.cpp:570-585). */
+int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n, int64_t k,
+                  const float* a, int64_t lda, int64_t stride_a, const float* b, int64_t ldb,
+                  int64_t stride_b, float beta, float* c, int64_t ldc, int64_t stride_c,
+                  void* stream);
+
+/* --------------------------------------------------------- element-wise */
+
+enum { EHIP_ADD = 0, EHIP_SUB = 1, EHIP_MUL = 2, EHIP_DIV = 3 };
+
+/* out[r*inner + j] = a[r*inner + j] op b[j], r < repeat (suffix broadcast).
+ * Bit-exact. cuda::ops::binary (cuda_ops.hpp:30-31). */
+int ehip_binary_f32(int op, const float* a, const float* b, float* out, int64_t inner,
+                    int64_t repeat, void* stream);
+
+/* out = x * mul + add (two roundings, no fma). Bit-exact.
+ * cuda::ops::scalar (cuda_ops.hpp:67). */
+int ehip_scalar_f32(const float* x, float* out, int64_t n, float mul, float add, void* stream);
+
+/* y = (0 < x) ? x : 0 and dx = (x > 0) ? g : 0. Bit-exact.
+ * cuda::ops::relu / relu_backward (cuda_ops.hpp:49-50). */
+int ehip_relu_f32(const float* x, float* y, int64_t n, void* stream);
+int ehip_relu_backward_f32(const float* x, const float* g, float* dx, int64_t n, void* stream);
+
+/* grad = g (initialize != 0) or grad += g. Bit-exact.
+ * cuda::ops::accumulate_grad (cuda_ops.hpp:61). */
+int ehip_accumulate_grad_f32(float* grad, const float* g, int64_t n, int initialize,
+                             void* stream);
+
+/* The backward of out = a + b for same-shape operands, fused: the upstream
+ * gradient g goes to both operand gradients in one pass, each either
+ * initialised (accumulate_* == 0: da = g) or accumulated (da += g).
+ * Bit-exact. Replaces the two accumulate_grad launches of the add node
+ * (src/tensor_ops.cpp:81-102 -> src/tensor.cpp:168-203). */
+int ehip_add_backward_f32(const float* g, float* da, float* db, int64_t n, int accumulate_a,
+                          int accumulate_b, void* stream);
+
+/* x[i] = value. A kernel, not a memset, so it is safe inside graph capture. */
+int ehip_fill_f32(float* x, int64_t n, float value, void* stream);
+
+/* x *= factor in place. cuda::ops::scale_in_place (cuda_ops.hpp:144). */
+int ehip_scale_f32(float* x, int64_t n, float factor, void* stream);
+
+/* ------------------------------------------------------------- optimisers */
+
+/* SGD with optional momentum and weight decay, in place; velocity may be NULL
+ * when momentum == 0. Bit-exact with src/optim.cpp:71-84.
+ * cuda::ops::sgd_step (cuda_ops.hpp:165-166). */
+int ehip_sgd_f32(float* p, const float* g, float* velocity, int64_t n, float lr, float momentum,
+                 float weight_decay, void* stream);
+
+/* Adam in place: m = b1 m + (1-b1) g; v = b2 v + (1-b2) g g;
+ * p -= lr (m/c1) / (sqrt(v/c2) + eps). bias_c1/bias_c2 come from the host
+ * (1 - pow(beta, t) in float, src/optim.cpp:119-120). Bit-exact with
+ * src/optim.cpp:147-160. cuda::ops::adam_step (cuda_ops.hpp:167-168). */
+int ehip_adam_f32(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1,
+                  float beta2, float eps, float weight_decay, float bias_c1, float bias_c2,
+                  void* stream);
+
+/* ------------------------------------------------------ layout and index maps */
+
+/* out[flat] = x[sum_d coord_d(flat, out_shape) * src_strides[d]], ndim <= 8.
+ * out_shape and src_strides are HOST arrays. A pure move: bit-exact.
+ * cuda::ops::permute (cuda_ops.hpp:75-76). */
+int ehip_permute_f32(const float* x, float* out, int ndim, const int64_t* out_shape,
+                     const int64_t* src_strides, void* stream);
+
+/* out[b][j][i] = x[b][i][j]: the last-two-axes transpose, LDS-tiled.
+ * Bit-exact (src/tensor_ops.cpp:335-370). */
+int ehip_transpose_f32(const float* x, float* out, int64_t batch, int64_t rows, int64_t cols,
+                       void* stream);
+
+/* Window geometry: the fields of cuda::ops::WindowShape (cuda_ops.hpp:86-90). */
+typedef struct {
+    int64_t batch, channels, height, width;
+    int64_t kernel_h, kernel_w, stride, padding;
+    int64_t out_h, out_w;
+} ehip_window_t;
+
+/* im2col: (N,C,H,W) -> (N*oH*oW, C*kH*kW), zero in the padding. Bit-exact.
+ * col2im: the adjoint; each pixel sums its covering windows in (oh, ow)
+ * ascending order from zero, as src/conv.cpp:183-214 does: bit-exact.
+ * cuda::ops::im2col / col2im (cuda_ops.hpp:99-100). */
+int ehip_im2col_f32(const float* x, float* cols, const ehip_window_t* w, void* stream);
+int ehip_col2im_f32(const float* cols, float* x, const ehip_window_t* w, void* stream);
+
+/* Max pooling with the flat input index of the first strict maximum as int32
+ * (src/conv.cpp:410-442); backward sums, per input pixel, the gradients of the
+ * windows that chose it in output order (src/conv.cpp:461-469). Bit-exact.
+ * cuda::ops::maxpool / maxpool_backward (cuda_ops.hpp:116-118); the argmax is
+ * int32 here where the reference's device path stores it as float. */
+int ehip_maxpool_f32(const float* x, float* y, int32_t* argmax, const ehip_window_t* w,
+                     void* stream);
+int ehip_maxpool_backward_f32(const int32_t* argmax, const float* g, float* dx,
+                              const ehip_window_t* w, void* stream);
+
+/* out[i] = x[idx[i]] row by row (rows of row_size floats); an index outside
+ * [0, n_rows) yields a row of NaN instead of a read out of bounds.
+ * Tensor::select_rows forward (src/tensor.cpp:556-585). Bit-exact. */
+int ehip_select_rows_f32(const float* x, const int32_t* idx, float* out, int64_t n_idx,
+                         int64_t row_size, int64_t n_rows, void* stream);
+
+/* Scatter-add adjoint of select_rows in CSR form: for every destination row r,
+ * S = sum of g rows pos[p] for p in [row_ptr[r], row_ptr[r+1]) taken in that
+ * order from zero, and dx[r] = S (accumulate == 0) or dx[r] + S. g has n_src
+ * rows; a position outside [0, n_src) makes the row NaN instead of a wild read.
+ * With pos listing each row's source positions in ascending order this is the
+ * reference's zeroed `dX[idx[i]] += g[i]` for i ascending followed by add_grad
+ * (src/tensor.cpp:593-601): bit-exact. */
+int ehip_scatter_add_rows_f32(const float* g, const int32_t* row_ptr, const int32_t* pos,
+                              float* dx, int64_t n_rows, int64_t row_size, int64_t n_src,
+                              int accumulate, void* stream);
+
+/* ------------------------------------------------------------- reductions */
+
+/* Sum over the middle axis of an (outer, axis_len, inner) view.
+ * Bit-exact (a ascending from zero, src/tensor.cpp:347-356) when
+ * axis_len <= 64 or outer * inner >= 16384; above that, a deterministic
+ * two-stage sum over fixed chunks of the axis (the same result on every run,
+ * within fp32 rounding of the serial sum). cuda::ops::sum_axis (cuda_ops.hpp:80). */
+int ehip_sum_axis_f32(const float* x, float* out, int64_t outer, int64_t axis_len, int64_t inner,
+                      void* stream);
+
+/* Whole-buffer sum of x (squares == 0) or of x*x, accumulated in double over a
+ * fixed partition (deterministic). Writes the double to out_d and its float
+ * cast to out_f (either may be NULL): both DEVICE pointers, so no
+ * synchronisation. cuda::ops::reduce_sum / reduce_sum_squares
+ * (cuda_ops.hpp:137-138). */
+int ehip_reduce_sum_f32(const float* x, int64_t n, int squares, double* out_d, float* out_f,
+                        void* stream);
+
+/* ---------------------------------------------------------------- row ops */
+
+/* Row softmax over `cols` contiguous values and its derivative from the saved
+ * output y: dx = y (g - sum(g y)). cuda::ops::softmax / softmax_backward
+ * (cuda_ops.hpp:200-203). */
+int ehip_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
+int ehip_softmax_backward_f32(const float* y, const float* g, float* dx, int64_t rows,
+                              int64_t cols, void* stream);
+
+/* LayerNorm over the last axis (two-pass mean and variance, eps inside the
+ * square root) saving xhat and inv_std, and its derivative; dgamma and dbeta
+ * are summed over rows in a fixed order (deterministic, no atomics).
+ * cuda::ops::layernorm / layernorm_backward (cuda_ops.hpp:193-197). */
+int ehip_layernorm_f32(const float* x, const float* gamma, const float* beta, float* out,
+                       float* xhat, float* inv_std, int64_t rows, int64_t cols, float eps,
+                       void* stream);
+int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float* gamma,
+                                const float* inv_std, float* dx, float* dgamma, float* dbeta,
+                                int64_t rows, int64_t cols, void* stream);
+
+/* Fused log-softmax + NLL over (rows, cols) logits with int32 targets: probs
+ * receives the row softmax and loss[0] the mean of -log p[target] (summed in
+ * double over a fixed partition). A target outside [0, cols) makes loss NaN.
+ * The reference has no device kernel for this: it replaces the host loop of
+ * nn::cross_entropy_loss (src/nn.cpp:324-380). */
+int ehip_cross_entropy_f32(const float* logits, const int32_t* targets, float* probs, float* loss,
+                           int64_t rows, int64_t cols, void* stream);
+
+/* dx = (probs - onehot(target)) * (grad[0] / rows), grad a DEVICE scalar (the
+ * upstream gradient of the loss). src/nn.cpp:386-405. Bit-exact given probs. */
+int ehip_cross_entropy_backward_f32(const float* probs, const int32_t* targets, float* dx,
+                                    int64_t rows, int64_t cols, const float* grad, void* stream);
+
+/* The softmax-cross-entropy backward straight from the logits, one pass:
+ * recomputes each row's softmax in registers and writes
+ * (softmax - onehot) * (grad[0] / rows). Reads 4 and writes 4 bytes per
+ * element; equal bit-for-bit to ehip_cross_entropy_f32 followed by
+ * ehip_cross_entropy_backward_f32. Replaces src/nn.cpp:352-405 for the
+ * backward pass. */
+int ehip_softmax_xent_backward_f32(const float* logits, const int32_t* targets, float* dx,
+                                   int64_t rows, int64_t cols, const float* grad, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EHIP_H */

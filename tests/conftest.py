@@ -4,11 +4,11 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-if ROOT not in sys.path:
-    sys.path.insert(0, ROOT)
+PKG = os.path.join(ROOT, "cpp-ai-engine_amd")
 TESTS = os.path.dirname(os.path.abspath(__file__))
-if TESTS not in sys.path:
-    sys.path.insert(0, TESTS)
+for p in (ROOT, PKG, TESTS):
+    if p not in sys.path:
+        sys.path.insert(0, p)
 
 
 def pytest_configure(config):

@@ -1,0 +1,53 @@
+"""The C ABI without a GPU: the library loads, exports exactly what include/ehip.h
+declares, and reports a missing device as an error status instead of crashing."""
+import ctypes
+import os
+
+import pytest
+
+import ehip as E
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return E.load_library()
+
+
+def test_header_declares_the_boundary():
+    names = E.header_symbols()
+    assert len(names) >= 45, names
+    for must in ("ehip_gemm_f32", "ehip_adam_f32", "ehip_softmax_xent_backward_f32",
+                 "ehip_im2col_f32", "ehip_col2im_f32", "ehip_maxpool_f32",
+                 "ehip_layernorm_backward_f32", "ehip_arena_alloc"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in E.header_symbols() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_the_header():
+    assert set(E.header_symbols()) == set(E._SIGS), \
+        set(E.header_symbols()) ^ set(E._SIGS)
+
+
+def test_header_has_no_torch_or_hip_types():
+    import re
+    text = re.sub(r"/\*.*?\*/", "", open(E.HEADER).read(), flags=re.S)
+    for banned in ("torch", "at::", "hipStream_t", "c10", "std::", "hip/"):
+        assert banned not in text, banned
+
+
+def test_no_device_is_an_error_not_a_crash(lib):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert lib.ehip_init() == 3  # EHIP_ENODEV
+    assert b"device" in lib.ehip_last_error()
+    assert lib.ehip_available() == 0
+    assert lib.ehip_relu_f32(None, None, 16, None) == 3
+    p = ctypes.c_void_p()
+    assert lib.ehip_arena_alloc(1024, ctypes.byref(p)) == 3 and not p.value

@@ -1,0 +1,392 @@
+"""Kernel-level parity of the HIP backend against the CPU oracle, through the C ABI.
+
+Each test feeds the same seeded inputs to the device kernel (libehip.so via ctypes) and
+to the oracle's restatement of the reference loop it replaces, and compares with the rule
+named in tests/_hip.py: `exact` where the reference's result is reproducible bit for bit,
+`ref_close` (the reference's |d|/max(1,|want|) metric) where the device sums in another
+order or uses the device exp/log.
+"""
+import numpy as np
+import pytest
+
+from _hip import backend, dev, exact, host, k_tol, print_case, ref_close, ref_err
+from _oracle import oracle_or_skip
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hip():
+    return backend()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return oracle_or_skip()
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def randn(r, *shape):
+    return r.standard_normal(shape, dtype=np.float32)
+
+
+# ------------------------------------------------------------------ GEMM
+
+GEMM_SHAPES = [(1, 1, 1), (7, 5, 3), (33, 17, 65), (64, 64, 64), (128, 9, 8), (5, 300, 2),
+               (130, 257, 129), (256, 256, 256), (512, 512, 512), (2048, 96, 96),
+               (64, 784, 10), (9, 4096, 8), (72, 3000, 16)]
+
+
+@pytest.mark.parametrize("m,k,n", GEMM_SHAPES)
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_modes_vs_oracle(hip, orc, m, k, n, ta, tb):
+    print_case("gemm", m, k, n, ta, tb)
+    r = rng(m * 7919 + k * 31 + n + 2 * ta + tb)
+    a = randn(r, m, k)
+    b = randn(r, k, n)
+    a_st = np.ascontiguousarray(a.T) if ta else a
+    b_st = np.ascontiguousarray(b.T) if tb else b
+    got = host(hip.gemm(dev(a_st), dev(b_st), trans_a=ta, trans_b=tb))
+    want = orc.matmul(a, b)
+    ref_close(got, want, k_tol(k), f"gemm {m}x{k}x{n} ta={ta} tb={tb}")
+    # The device error against the exact product stays within a small multiple
+    # of the CPU's own serial-sum error (fp64 as the arbiter).
+    exact64 = a.astype(np.float64) @ b.astype(np.float64)
+    e_gpu = np.sqrt(np.mean((got - exact64) ** 2))
+    e_cpu = np.sqrt(np.mean((want - exact64) ** 2))
+    assert e_gpu <= 4.0 * e_cpu + 1e-7, (e_gpu, e_cpu)
+
+
+@pytest.mark.parametrize("m,k,n", [(37, 53, 29), (256, 512, 128), (9, 50176, 8)])
+def test_gemm_integer_inputs_exact(hip, m, k, n):
+    """Small-integer operands: every partial sum is exact in fp32, so any summation order
+    must give the exact product (tests/test_cuda_parity.cpp:344-363 of the reference)."""
+    print_case("gemm-int", m, k, n)
+    r = rng(11)
+    a = r.integers(-3, 4, (m, k)).astype(np.float32)
+    b = r.integers(-3, 4, (k, n)).astype(np.float32)
+    want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    exact(host(hip.gemm(dev(a), dev(b))), want, "integer gemm")
+
+
+@pytest.mark.parametrize("ab,bb", [(True, True), (True, False), (False, True)])
+def test_gemm_batched_shared(hip, orc, ab, bb):
+    print_case("gemm-batched", ab, bb)
+    r = rng(5)
+    a = randn(r, 6, 40, 24) if ab else randn(r, 40, 24)
+    b = randn(r, 6, 24, 33) if bb else randn(r, 24, 33)
+    got = host(hip.gemm(dev(a), dev(b)))
+    ref_close(got, orc.matmul(a, b), k_tol(24), "batched gemm")
+
+
+def test_gemm_beta_accumulates(hip, orc):
+    """beta = 1 onto a nonzero destination (tests/test_cuda_parity.cpp:263-290)."""
+    print_case("gemm-beta")
+    r = rng(9)
+    a, b, c0 = randn(r, 70, 45), randn(r, 45, 90), randn(r, 70, 90)
+    c = dev(c0)
+    hip.gemm(dev(a), dev(b), c=c, beta=1.0)
+    want = orc.binary("add", orc.matmul(a, b), c0)
+    ref_close(host(c), want, k_tol(45) + 1e-6, "beta=1")
+
+
+def test_gemm_splitk_beta(hip, orc):
+    print_case("gemm-splitk-beta")
+    r = rng(10)
+    a, b, c0 = randn(r, 16, 8192), randn(r, 8192, 8), randn(r, 16, 8)
+    c = dev(c0)
+    hip.gemm(dev(a), dev(b), c=c, beta=1.0)
+    ref_close(host(c), orc.binary("add", orc.matmul(a, b), c0), k_tol(8192), "split-K beta")
+
+
+def test_gemm_deterministic(hip):
+    print_case("gemm-determinism")
+    r = rng(12)
+    a, b = dev(randn(r, 300, 700)), dev(randn(r, 700, 200))
+    exact(host(hip.gemm(a, b)), host(hip.gemm(a, b)), "repeat")
+
+
+def test_gemm_backward_products(hip, orc):
+    """cfg 1: C = A B and both backward products at 512^3, N(0,1) from one seed, against
+    the reference's graph (materialised transposes, src/tensor_ops.cpp:570-585)."""
+    print_case("gemm-cfg1")
+    r = rng(1)
+    a, b, dc = randn(r, 512, 512), randn(r, 512, 512), randn(r, 512, 512)
+    A, B, dC = dev(a), dev(b), dev(dc)
+    ref_close(host(hip.gemm(A, B)), orc.matmul(a, b), k_tol(512), "C")
+    ref_close(host(hip.gemm(dC, B, trans_b=True)), orc.matmul(dc, orc.transpose(b)), k_tol(512),
+              "dA")
+    ref_close(host(hip.gemm(A, dC, trans_a=True)), orc.matmul(orc.transpose(a), dc), k_tol(512),
+              "dB")
+
+
+# ------------------------------------------------------------------ element-wise
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+@pytest.mark.parametrize("shape,inner", [((1000,), 1000), ((50176, 8), 8), ((33, 7), 7),
+                                         ((64, 96), 96), ((4, 3, 5), 15)])
+def test_binary_exact(hip, orc, op, shape, inner):
+    print_case("binary", op, shape, inner)
+    r = rng(len(shape) * 100 + inner)
+    a = randn(r, *shape)
+    b = randn(r, inner) + (3.0 if op == "div" else 0.0)
+    code = {"add": 0, "sub": 1, "mul": 2, "div": 3}[op]
+    exact(host(hip.binary(code, dev(a), dev(b))), orc.binary(op, a, b).reshape(shape), op)
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 1023, 4096 * 4 + 5, 1 << 20])
+def test_unary_exact(hip, orc, n):
+    print_case("unary", n)
+    r = rng(n)
+    x, g = randn(r, n), randn(r, n)
+    x[::7] = 0.0
+    x[1::11] = -0.0
+    X, G = dev(x), dev(g)
+    exact(host(hip.relu(X)), orc.relu(x), "relu")
+    exact(host(hip.relu_backward(X, G)), orc.relu_backward(x, g), "relu_backward")
+    exact(host(hip.scalar(X, 0.125, 0.0)), orc.scalar_mul(x, 0.125), "t*k")
+    exact(host(hip.scalar(X, 1.0, 2.5)), orc.scalar_add(x, 2.5), "t+k")
+
+
+@pytest.mark.parametrize("n", [5, 4096, 100003])
+def test_accumulate_and_add_backward_exact(hip, orc, n):
+    print_case("accumulate", n)
+    r = rng(n + 1)
+    g, base = randn(r, n), randn(r, n)
+    g[::5] = -0.0
+    zero = np.zeros(n, np.float32)
+    want_init = orc.accumulate(zero.copy(), g)
+    want_acc = orc.accumulate(base.copy(), g)
+    exact(host(hip.accumulate_grad(dev(zero), dev(g), True)), want_init, "init")
+    exact(host(hip.accumulate_grad(dev(base), dev(g), False)), want_acc, "accumulate")
+    for acc_a in (False, True):
+        for acc_b in (False, True):
+            da, db = dev(base), dev(base * 2)
+            hip.add_backward(dev(g), da, db, acc_a, acc_b)
+            exact(host(da), want_acc if acc_a else want_init, f"da {acc_a}{acc_b}")
+            exact(host(db), orc.accumulate((base * 2).copy(), g) if acc_b else want_init,
+                  f"db {acc_a}{acc_b}")
+
+
+@pytest.mark.parametrize("n", [7, 4096, 65537])
+def test_adam_trajectory_exact(hip, orc, n):
+    """Ten Adam steps, bias corrections from the host as in src/optim.cpp:119-120."""
+    print_case("adam", n)
+    r = rng(n + 2)
+    p = randn(r, n)
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    P, M, V = dev(p), dev(m), dev(v)
+    for t in range(1, 11):
+        g = randn(r, n)
+        c1, c2 = orc.adam_bias(0.9, 0.999, t)
+        orc.adam(p, g, m, v, 1e-3, 0.9, 0.999, 1e-8, 0.01 if t % 2 else 0.0, c1, c2)
+        hip.adam(P, dev(g), M, V, 1e-3, 0.9, 0.999, 1e-8, 0.01 if t % 2 else 0.0, c1, c2)
+    exact(host(P), p, "p")
+    exact(host(M), m, "m")
+    exact(host(V), v, "v")
+
+
+def test_sgd_exact(hip, orc):
+    print_case("sgd")
+    r = rng(3)
+    p = randn(r, 1001)
+    vel = np.zeros_like(p)
+    P, VEL = dev(p), dev(vel)
+    for _ in range(5):
+        g = randn(r, 1001)
+        orc.sgd(p, g, vel, 0.05, 0.9, 1e-4)
+        hip.sgd(P, dev(g), VEL, 0.05, 0.9, 1e-4)
+    exact(host(P), p, "p")
+    exact(host(VEL), vel, "velocity")
+
+
+def test_fill_scale(hip):
+    print_case("fill-scale")
+    x = dev(np.zeros(1027, np.float32))
+    hip.fill(x, 1.5)
+    hip.scale(x, 3.0)
+    exact(host(x), np.full(1027, 4.5, np.float32), "fill*scale")
+
+
+# ------------------------------------------------------------------ layout
+
+@pytest.mark.parametrize("shape,order", [((32, 64, 4, 24), (0, 2, 1, 3)),
+                                         ((3, 5, 7), (2, 0, 1)), ((64, 784, 8), (0, 2, 1)),
+                                         ((2, 3, 4, 5, 6), (4, 2, 0, 3, 1)),
+                                         ((16, 32, 8, 64), (0, 2, 1, 3))])
+def test_permute_exact(hip, orc, shape, order):
+    print_case("permute", shape, order)
+    x = randn(rng(4), *shape)
+    exact(host(hip.permute(dev(x), order)), orc.permute(x, order), "permute")
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (5, 3), (65, 130), (3, 96, 121), (128, 24, 64)])
+def test_transpose_exact(hip, orc, shape):
+    print_case("transpose", shape)
+    x = randn(rng(6), *shape)
+    exact(host(hip.transpose(dev(x))), orc.transpose(x), "transpose")
+
+
+WINDOWS = [((64, 1, 28, 28), 3, 1, 1), ((64, 8, 14, 14), 3, 1, 1), ((2, 3, 9, 7), 3, 2, 0),
+           ((2, 2, 8, 8), 2, 2, 0), ((1, 4, 11, 13), 5, 3, 2), ((3, 2, 6, 6), 3, 1, 0)]
+
+
+@pytest.mark.parametrize("shape,k,stride,pad", WINDOWS)
+def test_im2col_col2im_exact(hip, orc, shape, k, stride, pad):
+    print_case("im2col", shape, k, stride, pad)
+    r = rng(sum(shape) + k)
+    x = randn(r, *shape)
+    cols = orc.im2col(x, k, k, stride, pad)
+    exact(host(hip.im2col(dev(x), k, k, stride, pad)), cols, "im2col")
+    g = randn(r, *cols.shape)
+    exact(host(hip.col2im(dev(g), shape, k, k, stride, pad)),
+          orc.col2im(g, shape, k, k, stride, pad), "col2im")
+
+
+@pytest.mark.parametrize("shape,k,stride", [((64, 8, 28, 28), 2, 2), ((64, 16, 14, 14), 2, 2),
+                                            ((2, 3, 9, 9), 3, 2), ((2, 2, 7, 7), 3, 1)])
+def test_maxpool_exact(hip, orc, shape, k, stride):
+    """Overlapping windows and ties included: the first strict maximum wins."""
+    print_case("maxpool", shape, k, stride)
+    r = rng(sum(shape))
+    x = np.round(randn(r, *shape) * 2) / 2  # many ties
+    y, am = orc.maxpool(x, k, stride)
+    Y, AM = hip.maxpool(dev(x), k, stride)
+    exact(host(Y), y, "max")
+    exact(host(AM), am, "argmax")
+    g = randn(r, *y.shape)
+    exact(host(hip.maxpool_backward(AM, dev(g), shape, k, stride)),
+          orc.maxpool_backward(am, g, shape), "maxpool backward")
+
+
+def test_select_and_scatter_rows_exact(hip, orc):
+    print_case("select-scatter")
+    r = rng(8)
+    table = randn(r, 121, 96)
+    idx = r.integers(0, 121, 2048)
+    out = host(hip.select_rows(dev(table), dev(idx.astype(np.int32))))
+    exact(out, orc.select_rows(table, idx), "select_rows")
+    g = randn(r, 2048, 96)
+    order = np.argsort(idx, kind="stable")
+    counts = np.bincount(idx, minlength=121)
+    row_ptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    dx = dev(np.zeros((121, 96), np.float32))
+    hip.scatter_add_rows(dev(g), dev(row_ptr), dev(order.astype(np.int32)), dx)
+    exact(host(dx), orc.scatter_add_rows(g, idx, (121, 96)), "scatter_add_rows")
+
+
+# ------------------------------------------------------------------ reductions
+
+@pytest.mark.parametrize("outer,axis_len,inner", [(1, 50, 8), (4, 10, 4096), (1, 50176, 8),
+                                                  (1, 2048, 96), (1, 8192, 1024), (3, 1000, 7)])
+def test_sum_axis(hip, orc, outer, axis_len, inner):
+    print_case("sum_axis", outer, axis_len, inner)
+    x = randn(rng(axis_len), outer, axis_len, inner)
+    got = host(hip.sum_axis(dev(x), outer, axis_len, inner)).reshape(outer, inner)
+    want = orc.sum_axis(x, 1).reshape(outer, inner)
+    if axis_len <= 64 or outer * inner >= 16384:
+        exact(got, want, "serial sum_axis")
+    else:
+        ref_close(got, want, k_tol(axis_len), "chunked sum_axis")
+
+
+@pytest.mark.parametrize("n", [1, 1000, 1 << 20])
+def test_reduce_sum(hip, orc, n):
+    print_case("reduce_sum", n)
+    x = randn(rng(n), n)
+    d, f = hip.reduce_sum(dev(x))
+    assert abs(float(host(d)[0]) - orc.sum(x)) <= 1e-9 * max(1.0, np.abs(x).sum())
+    d2, _ = hip.reduce_sum(dev(x), squares=True)
+    assert abs(float(host(d2)[0]) - orc.sum_squares(x)) <= 1e-9 * orc.sum_squares(x)
+    assert host(f)[0] == np.float32(host(d)[0])
+
+
+# ------------------------------------------------------------------ rows
+
+@pytest.mark.parametrize("rows,cols", [(8192, 64), (64, 512), (3, 5), (17, 2048), (4, 4000),
+                                       (2, 8192), (3, 30000), (2, 40000), (5, 1000)])
+def test_softmax(hip, orc, rows, cols):
+    print_case("softmax", rows, cols)
+    r = rng(rows * cols)
+    x, g = randn(r, rows, cols) * 3, randn(r, rows, cols)
+    y = hip.softmax(dev(x))
+    want = orc.softmax(x)
+    # The row sum is `cols` long: the reference's K-scaled tolerance applies.
+    ref_close(host(y), want, k_tol(cols), "softmax")
+    # fp64 arbiter: the device is at least as close to the exact softmax as the CPU is.
+    x64 = x.astype(np.float64)
+    e64 = np.exp(x64 - x64.max(axis=1, keepdims=True))
+    exact64 = e64 / e64.sum(axis=1, keepdims=True)
+    assert np.abs(host(y) - exact64).max() <= 2 * np.abs(want - exact64).max() + 1e-7
+    yh = host(y)
+    ref_close(host(hip.softmax_backward(y, dev(g))), orc.softmax_backward(yh, g), k_tol(cols),
+              "softmax backward")
+
+
+@pytest.mark.parametrize("rows,d", [(2048, 96), (512, 64), (7, 1024), (33, 100), (4, 3000)])
+def test_layernorm(hip, orc, rows, d):
+    print_case("layernorm", rows, d)
+    r = rng(rows + d)
+    x = randn(r, rows, d) * 2 + 0.5
+    gamma, beta, dy = randn(r, d), randn(r, d), randn(r, rows, d)
+    out, xhat, inv = hip.layernorm(dev(x), dev(gamma), dev(beta))
+    o, xh, iv = orc.layernorm(x, gamma, beta)
+    ref_close(host(out), o, k_tol(d), "out")
+    ref_close(host(xhat), xh, k_tol(d), "xhat")
+    ref_close(host(inv), iv, k_tol(d), "inv_std")
+    dx, dg, db = hip.layernorm_backward(dev(dy), dev(xh), dev(gamma), dev(iv))
+    wdx, wdg, wdb = orc.layernorm_backward(dy, xh, gamma, iv)
+    ref_close(host(dx), wdx, k_tol(d), "dx")
+    ref_close(host(dg), wdg, k_tol(rows), "dgamma")
+    ref_close(host(db), wdb, k_tol(rows), "dbeta")
+    # dgamma is bit-identical across runs (tests/test_cuda_parity.cpp:644-740).
+    dx2, dg2, db2 = hip.layernorm_backward(dev(dy), dev(xh), dev(gamma), dev(iv))
+    exact(host(dg2), host(dg), "dgamma repeat")
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 10), (2048, 121), (8, 5), (16, 32000), (3, 40000),
+                                       (100, 256)])
+def test_cross_entropy(hip, orc, rows, cols):
+    print_case("xent", rows, cols)
+    r = rng(rows * 3 + cols)
+    logits = randn(r, rows, cols) * 2
+    t = r.integers(0, cols, rows)
+    T = dev(t.astype(np.int32))
+    loss, probs = hip.cross_entropy(dev(logits), T)
+    want_loss, want_probs = orc.cross_entropy(logits, t)
+    ref_close(host(probs), want_probs, k_tol(cols), "probs")
+    assert abs(float(host(loss)[0]) - want_loss) <= k_tol(max(rows, cols)) * max(1.0, abs(want_loss))
+    one = dev(np.ones(1, np.float32))
+    dx = host(hip.cross_entropy_backward(probs, T, one))
+    exact(dx, orc.cross_entropy_backward(host(probs), t, 1.0), "backward from device probs")
+    fused = host(hip.softmax_xent_backward(dev(logits), T, one))
+    exact(fused, dx, "fused == two-kernel")
+    ref_close(fused, orc.cross_entropy_backward(want_probs, t, 1.0), k_tol(cols), "vs oracle")
+
+
+def test_cross_entropy_bad_label_is_nan(hip):
+    print_case("xent-bad-label")
+    logits = dev(np.zeros((2, 4), np.float32))
+    loss, _ = hip.cross_entropy(logits, dev(np.array([1, 9], np.int32)))
+    assert np.isnan(host(loss)[0])
+
+
+def test_refusals_are_errors(hip):
+    """Refused geometry comes back as an error status, never a launch."""
+    print_case("refusals")
+    x = dev(np.zeros(16, np.float32))
+    before = hip.launched()
+    with pytest.raises(RuntimeError, match="do not match the window"):
+        import ehip as E
+        w = E.window(1, 1, 4, 4, 3, 3, 1, 0)
+        w.out_h = 7
+        import ctypes
+        hip.ok(hip.lib.ehip_im2col_f32(hip.p(x), hip.p(x), ctypes.byref(w), hip.stream()),
+               "im2col")
+    with pytest.raises(RuntimeError, match="layernorm"):
+        hip.ok(hip.lib.ehip_layernorm_f32(hip.p(x), hip.p(x), hip.p(x), hip.p(x), hip.p(x),
+                                          hip.p(x), 1, 9000, 1e-5, hip.stream()), "layernorm")
+    assert hip.launched() == before
