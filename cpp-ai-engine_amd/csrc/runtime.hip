@@ -313,14 +313,85 @@ void ehip_arena_stats(ehip_arena_stats_t* out) {
 
 namespace {
 
+// Host-to-device uploads up to a quarter of the ring go through a pinned
+// staging ring: the bytes are copied into it on the host and the device copy
+// is enqueued asynchronously, so an upload in the middle of a training step
+// (labels, gather indices) neither waits for the queued kernels nor for the
+// transfer. A ring region is reused only after the event recorded behind its
+// copy has completed.
+struct Staging {
+    std::mutex mu;
+    char* base = nullptr;
+    size_t cap = size_t(64) << 20;
+    size_t head = 0;
+    struct Pending {
+        size_t begin, end;
+        hipEvent_t done;
+    };
+    std::vector<Pending> inflight;
+};
+
+Staging& staging() {
+    static Staging* s = new Staging();
+    return *s;
+}
+
+// Returns hipSuccess and sets *used when the upload went through the ring.
+hipError_t staged_upload(void* dst, const void* src, size_t bytes, hipStream_t s, bool* used) {
+    *used = false;
+    Staging& st = staging();
+    if (bytes > st.cap / 4) return hipSuccess;
+    std::lock_guard<std::mutex> lock(st.mu);
+    if (st.base == nullptr) {
+        hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&st.base), st.cap, 0);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            st.base = nullptr;
+            return hipSuccess;  // no pinned memory: the caller copies synchronously
+        }
+    }
+    const size_t len = (bytes + 255) & ~size_t(255);
+    if (st.head + len > st.cap) st.head = 0;
+    const size_t b = st.head, e_ = st.head + len;
+    for (auto it = st.inflight.begin(); it != st.inflight.end();) {
+        const bool overlaps = it->begin < e_ && b < it->end;
+        if (overlaps || hipEventQuery(it->done) == hipSuccess) {
+            if (overlaps) {
+                hipError_t e = hipEventSynchronize(it->done);
+                if (e != hipSuccess) return e;
+            }
+            (void)hipEventDestroy(it->done);
+            it = st.inflight.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    std::memcpy(st.base + b, src, bytes);
+    hipError_t e = hipMemcpyAsync(dst, st.base + b, bytes, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return e;
+    hipEvent_t done;
+    e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(done, s);
+    if (e != hipSuccess) return e;
+    st.inflight.push_back({b, e_, done});
+    st.head = e_;
+    *used = true;
+    return hipSuccess;
+}
+
 int copy(void* dst, const void* src, size_t bytes, void* stream, hipMemcpyKind kind) {
     if (int rc = ehip_init()) return rc;
     if (bytes == 0) return EHIP_OK;
     if (dst == nullptr || src == nullptr) return fail(EHIP_EINVAL, "memcpy: null pointer");
     const auto t0 = std::chrono::steady_clock::now();
     hipStream_t s = as_stream(stream);
-    hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, s);
-    if (e == hipSuccess && kind != hipMemcpyDeviceToDevice) e = hipStreamSynchronize(s);
+    bool staged = false;
+    hipError_t e = hipSuccess;
+    if (kind == hipMemcpyHostToDevice) e = staged_upload(dst, src, bytes, s, &staged);
+    if (e == hipSuccess && !staged) {
+        e = hipMemcpyAsync(dst, src, bytes, kind, s);
+        if (e == hipSuccess && kind != hipMemcpyDeviceToDevice) e = hipStreamSynchronize(s);
+    }
     if (e != hipSuccess) return fail(EHIP_ELAUNCH, "memcpy: %s", hipGetErrorString(e));
     const double sec =
         std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();

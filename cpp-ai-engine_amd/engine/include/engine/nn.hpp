@@ -1,0 +1,124 @@
+// nn.hpp -- modules and losses of the training path, mirroring the
+// reference's include/engine/nn.hpp (Module, Linear, ReLU, Softmax,
+// Sequential, make, mse_loss, cross_entropy_loss, argmax_rows, accuracy).
+// Sigmoid, Tanh, GELU and Dropout are not provided: no configuration of this
+// backend trains through them.
+#ifndef ENGINE_NN_HPP
+#define ENGINE_NN_HPP
+
+#include <memory>
+#include <string>
+#include <type_traits>
+#include <utility>
+#include <vector>
+
+#include "engine/tensor.hpp"
+
+namespace engine {
+namespace nn {
+
+class Module {
+public:
+    virtual ~Module() = default;
+    virtual Tensor forward(const Tensor& input) = 0;
+    Tensor operator()(const Tensor& input) { return forward(input); }
+    virtual std::vector<Tensor> parameters() { return {}; }
+    virtual std::vector<std::pair<std::string, Tensor>> named_parameters(
+        const std::string& prefix = "");
+    virtual void train(bool mode = true) { training_ = mode; }
+    void eval() { train(false); }
+    bool is_training() const noexcept { return training_; }
+    virtual std::string name() const { return "Module"; }
+    void zero_grad();
+    size_t num_parameters();
+
+protected:
+    bool training_ = true;
+};
+
+// y = x W + b with W of shape (in, out), Xavier-uniform, b (1, out) zero
+// (the reference's src/nn.cpp:85-130); inputs of more than two dimensions are
+// viewed as rows.
+class Linear : public Module {
+public:
+    Linear(size_t in_features, size_t out_features, bool use_bias = true);
+    Tensor forward(const Tensor& input) override;
+    std::vector<Tensor> parameters() override;
+    std::string name() const override;
+    Tensor& weight() { return weight_; }
+    Tensor& bias() { return bias_; }
+    size_t in_features() const noexcept { return in_features_; }
+    size_t out_features() const noexcept { return out_features_; }
+
+private:
+    size_t in_features_;
+    size_t out_features_;
+    bool use_bias_;
+    Tensor weight_;
+    Tensor bias_;
+};
+
+class ReLU : public Module {
+public:
+    Tensor forward(const Tensor& input) override { return input.relu(); }
+    std::string name() const override { return "ReLU"; }
+};
+
+class Softmax : public Module {
+public:
+    Tensor forward(const Tensor& input) override { return input.softmax(); }
+    std::string name() const override { return "Softmax"; }
+};
+
+class Sequential : public Module {
+public:
+    Sequential() = default;
+    template <typename... Layers,
+              typename =
+                  std::enable_if_t<(std::is_convertible_v<Layers, std::unique_ptr<Module>> && ...)>>
+    explicit Sequential(Layers&&... layers) {
+        (add(std::forward<Layers>(layers)), ...);
+    }
+    Sequential& add(std::unique_ptr<Module> layer);
+    Tensor forward(const Tensor& input) override;
+    std::vector<Tensor> parameters() override;
+    std::vector<std::pair<std::string, Tensor>> named_parameters(
+        const std::string& prefix = "") override;
+    void train(bool mode = true) override;
+    std::string name() const override { return "Sequential"; }
+    size_t size() const noexcept { return layers_.size(); }
+    Module& at(size_t index);
+
+private:
+    std::vector<std::unique_ptr<Module>> layers_;
+};
+
+template <typename T, typename... Args>
+std::unique_ptr<T> make(Args&&... args) {
+    return std::make_unique<T>(std::forward<Args>(args)...);
+}
+
+Tensor mse_loss(const Tensor& prediction, const Tensor& target);
+
+// Fused log-softmax + NLL over (N, C) logits (the reference's
+// src/nn.cpp:324-408), computed on the device; the loss stays on the device
+// until read.
+Tensor cross_entropy_loss(const Tensor& logits, const std::vector<size_t>& targets);
+
+class CrossEntropyLoss {
+public:
+    Tensor forward(const Tensor& logits, const std::vector<size_t>& targets) const {
+        return cross_entropy_loss(logits, targets);
+    }
+    Tensor operator()(const Tensor& logits, const std::vector<size_t>& targets) const {
+        return forward(logits, targets);
+    }
+};
+
+std::vector<size_t> argmax_rows(const Tensor& logits);
+float accuracy(const Tensor& logits, const std::vector<size_t>& targets);
+
+}  // namespace nn
+}  // namespace engine
+
+#endif  // ENGINE_NN_HPP

@@ -1,0 +1,125 @@
+// tensor.hpp -- the engine's N-d fp32 Tensor, device-resident on MI355X.
+//
+// The public API mirrors the reference's include/engine/tensor.hpp:28-203
+// (same names, argument meaning and exceptions) so that models written
+// against the reference compile against this engine. Every operation runs as
+// a HIP kernel through the C ABI of include/ehip.h; there is no CPU compute
+// path, and an operation the device refuses throws std::runtime_error.
+// data() is the door to the host copy: it downloads when the host copy is
+// stale.
+//
+// Not provided (not on the training path of any configuration this backend
+// serves): slice, concat, stack and max(axis).
+#ifndef ENGINE_TENSOR_HPP
+#define ENGINE_TENSOR_HPP
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "engine/detail/tensor_impl.hpp"
+
+namespace engine {
+
+// Seeds the global std::mt19937 used by rand()/randn() and layer
+// initialisation (the reference's src/tensor.cpp:24-31).
+void manual_seed(uint64_t seed);
+
+class Tensor {
+private:
+    std::shared_ptr<TensorImpl> impl_;
+    explicit Tensor(std::shared_ptr<TensorImpl> impl);
+
+public:
+    Tensor();
+    explicit Tensor(const std::vector<size_t>& shape, float fill_value = 0.0f,
+                    bool requires_grad = false);
+    Tensor(const std::vector<size_t>& shape, const std::vector<float>& data,
+           bool requires_grad = false);
+
+    static Tensor from_impl(std::shared_ptr<TensorImpl> impl);
+
+    static Tensor zeros(const std::vector<size_t>& shape, bool requires_grad = false);
+    static Tensor ones(const std::vector<size_t>& shape, bool requires_grad = false);
+    static Tensor rand(const std::vector<size_t>& shape, float min_val = -1.0f,
+                       float max_val = 1.0f, bool requires_grad = false);
+    static Tensor randn(const std::vector<size_t>& shape, float mean = 0.0f, float stddev = 1.0f,
+                        bool requires_grad = false);
+
+    [[nodiscard]] bool requires_grad() const;
+    void set_requires_grad(bool requires_grad);
+    [[nodiscard]] Tensor grad() const;
+    [[nodiscard]] bool has_grad() const;
+    void zero_grad();
+    void add_grad(const Tensor& g);
+    void backward();
+    void backward(const Tensor& grad_output);
+
+    [[nodiscard]] Storage& storage() noexcept { return impl_->storage; }
+    [[nodiscard]] const Storage& storage() const noexcept { return impl_->storage; }
+    [[nodiscard]] const std::shared_ptr<TensorImpl>& get_impl() const noexcept { return impl_; }
+
+    [[nodiscard]] size_t get_flat_index(const std::vector<size_t>& indices) const;
+    float& operator()(const std::vector<size_t>& indices);
+    [[nodiscard]] const float& operator()(const std::vector<size_t>& indices) const;
+    float& operator()(size_t row, size_t col);
+    [[nodiscard]] const float& operator()(size_t row, size_t col) const;
+    float& at(size_t flat_index);
+    [[nodiscard]] const float& at(size_t flat_index) const;
+
+    [[nodiscard]] const std::vector<size_t>& shape() const;
+    [[nodiscard]] const std::vector<size_t>& strides() const;
+    [[nodiscard]] const float* data() const;
+    [[nodiscard]] float* data();
+    [[nodiscard]] std::vector<float> to_vector() const;
+    [[nodiscard]] size_t size() const;
+    [[nodiscard]] size_t ndim() const;
+    [[nodiscard]] std::string shape_str() const;
+
+    // Element-wise with suffix broadcast of the right operand.
+    [[nodiscard]] Tensor operator+(const Tensor& other) const;
+    [[nodiscard]] Tensor operator-(const Tensor& other) const;
+    [[nodiscard]] Tensor operator*(const Tensor& other) const;
+    [[nodiscard]] Tensor operator/(const Tensor& other) const;
+
+    [[nodiscard]] Tensor operator+(float scalar) const;
+    [[nodiscard]] Tensor operator-(float scalar) const;
+    [[nodiscard]] Tensor operator*(float scalar) const;
+    [[nodiscard]] Tensor operator/(float scalar) const;
+
+    [[nodiscard]] Tensor matmul(const Tensor& other) const;
+    [[nodiscard]] Tensor transpose() const;
+    [[nodiscard]] Tensor permute(const std::vector<size_t>& order) const;
+    [[nodiscard]] Tensor relu() const;
+    [[nodiscard]] Tensor softmax() const;
+    [[nodiscard]] Tensor reshape(const std::vector<size_t>& new_shape) const;
+    [[nodiscard]] Tensor sum() const;
+    [[nodiscard]] Tensor mean() const;
+    [[nodiscard]] Tensor sum(size_t axis, bool keepdim = false) const;
+    [[nodiscard]] Tensor mean(size_t axis, bool keepdim = false) const;
+
+    [[nodiscard]] Tensor select_rows(const std::vector<size_t>& indices) const;
+    [[nodiscard]] Tensor detach() const;
+
+    void print(const std::string& name = "") const;
+};
+
+[[nodiscard]] Tensor operator+(float scalar, const Tensor& t);
+[[nodiscard]] Tensor operator-(float scalar, const Tensor& t);
+[[nodiscard]] Tensor operator*(float scalar, const Tensor& t);
+
+namespace ops {
+
+// Products the backward passes and attention use without materialising a
+// transpose: A^T B, A B^T (both operands 2-D or batched like matmul). They
+// are graph nodes with their own derivatives, equal in value to
+// a.transpose().matmul(b) and a.matmul(b.transpose()).
+Tensor matmul_tn(const Tensor& a, const Tensor& b);
+Tensor matmul_nt(const Tensor& a, const Tensor& b);
+
+}  // namespace ops
+
+}  // namespace engine
+
+#endif  // ENGINE_TENSOR_HPP

@@ -1,0 +1,188 @@
+// conv.cpp -- im2col/col2im, Conv2d as im2col + one GEMM, MaxPool2d and
+// Flatten (the reference's src/conv.cpp).
+#include "engine/conv.hpp"
+
+#include <cmath>
+#include <stdexcept>
+
+#include "detail.hpp"
+
+namespace engine {
+namespace nn {
+
+using namespace detail;
+
+namespace {
+
+size_t output_size(size_t in_size, size_t kernel, size_t stride, size_t padding) {
+    const size_t padded = in_size + 2 * padding;
+    if (kernel > padded)
+        throw std::invalid_argument("The kernel (" + std::to_string(kernel) +
+                                    ") does not fit the padded input dimension (" +
+                                    std::to_string(padded) + ").");
+    return (padded - kernel) / stride + 1;
+}
+
+ehip_window_t window_of(const std::vector<size_t>& shape, const Window2d& w) {
+    ehip_window_t s;
+    s.batch = int64_t(shape[0]);
+    s.channels = int64_t(shape[1]);
+    s.height = int64_t(shape[2]);
+    s.width = int64_t(shape[3]);
+    s.kernel_h = int64_t(w.kernel_h);
+    s.kernel_w = int64_t(w.kernel_w);
+    s.stride = int64_t(w.stride);
+    s.padding = int64_t(w.padding);
+    s.out_h = int64_t(w.out_h(shape[2]));
+    s.out_w = int64_t(w.out_w(shape[3]));
+    return s;
+}
+
+// im2col as a graph node: its derivative is col2im (src/conv.cpp:234-253).
+Tensor im2col_node(const Tensor& input, const Window2d& window) {
+    Tensor cols = im2col(input, window);
+    if (!autograd::grad_enabled() || !input.requires_grad()) return cols;
+    cols.set_requires_grad(true);
+    cols.get_impl()->parents = {input.get_impl()};
+    Tensor input_copy = input;
+    const std::vector<size_t> in_shape = input.shape();
+    const Window2d win = window;
+    cols.get_impl()->backward_fn = [input_copy, in_shape, win](const Tensor& g) mutable {
+        input_copy.add_grad(col2im(g, in_shape, win));
+    };
+    return cols;
+}
+
+}  // namespace
+
+size_t Window2d::out_h(size_t in_h) const { return output_size(in_h, kernel_h, stride, padding); }
+size_t Window2d::out_w(size_t in_w) const { return output_size(in_w, kernel_w, stride, padding); }
+
+void Window2d::validate(size_t in_h, size_t in_w) const {
+    if (kernel_h == 0 || kernel_w == 0 || stride == 0)
+        throw std::invalid_argument("The window needs a kernel and a stride greater than zero.");
+    (void)out_h(in_h);
+    (void)out_w(in_w);
+}
+
+Tensor im2col(const Tensor& input, const Window2d& window) {
+    if (input.ndim() != 4)
+        throw std::invalid_argument("im2col expects (N, C, H, W), received " + input.shape_str() + ".");
+    window.validate(input.shape()[2], input.shape()[3]);
+    const ehip_window_t w = window_of(input.shape(), window);
+    Tensor cols({size_t(w.batch * w.out_h * w.out_w), size_t(w.channels * w.kernel_h * w.kernel_w)},
+                0.0f, false);
+    hip::check(ehip_im2col_f32(dptr(input), dout(cols), &w, nullptr), "im2col");
+    return cols;
+}
+
+Tensor col2im(const Tensor& cols, const std::vector<size_t>& input_shape, const Window2d& window) {
+    if (input_shape.size() != 4) throw std::invalid_argument("col2im expects a 4D input shape.");
+    window.validate(input_shape[2], input_shape[3]);
+    const ehip_window_t w = window_of(input_shape, window);
+    if (cols.size() != size_t(w.batch * w.out_h * w.out_w * w.channels * w.kernel_h * w.kernel_w))
+        throw std::invalid_argument("col2im: columns " + cols.shape_str() +
+                                    " do not match the window over the input.");
+    Tensor x(input_shape, 0.0f, false);
+    hip::check(ehip_col2im_f32(dptr(cols), dout(x), &w, nullptr), "col2im");
+    return x;
+}
+
+// Xavier-uniform over (fan_in + fan_out) x receptive field, zero bias
+// (src/conv.cpp:257-277).
+Conv2d::Conv2d(size_t in_channels, size_t out_channels, const Window2d& window, bool use_bias)
+    : in_channels_(in_channels), out_channels_(out_channels), window_(window), use_bias_(use_bias) {
+    if (in_channels == 0 || out_channels == 0)
+        throw std::invalid_argument("Conv2d requires in_channels and out_channels greater than zero.");
+    if (window_.kernel_h == 0 || window_.kernel_w == 0 || window_.stride == 0)
+        throw std::invalid_argument("Conv2d requires a kernel and a stride greater than zero.");
+    const size_t receptive = window_.kernel_h * window_.kernel_w;
+    const float fan_in = static_cast<float>(in_channels * receptive);
+    const float fan_out = static_cast<float>(out_channels * receptive);
+    const float limit = std::sqrt(6.0f / (fan_in + fan_out));
+    autograd::NoGradGuard no_grad;
+    weight_ = Tensor::rand({out_channels, in_channels, window_.kernel_h, window_.kernel_w}, -limit,
+                           limit, true);
+    bias_ = Tensor({out_channels}, 0.0f, use_bias);
+}
+
+// im2col -> cols (W reshaped to (outC, K))^T -> + bias -> (N, outC, oH, oW)
+// (src/conv.cpp:280-338). The product reads W in place through the GEMM's
+// transposed mode, so its derivative needs no transpose either.
+Tensor Conv2d::forward(const Tensor& input) {
+    if (input.ndim() != 4)
+        throw std::invalid_argument("Conv2d expects a 4D volume (N, C, H, W), received " +
+                                    input.shape_str() + ".");
+    if (input.shape()[1] != in_channels_)
+        throw std::invalid_argument("Conv2d with in_channels=" + std::to_string(in_channels_) +
+                                    " received an input " + input.shape_str() + ".");
+    const size_t N = input.shape()[0], H = input.shape()[2], W = input.shape()[3];
+    const size_t oH = window_.out_h(H), oW = window_.out_w(W);
+    const size_t K = in_channels_ * window_.kernel_h * window_.kernel_w;
+    Tensor cols = im2col_node(input, window_);
+    Tensor out = ops::matmul_nt(cols, weight_.reshape({out_channels_, K}));
+    if (use_bias_) out = out + bias_;
+    return out.reshape({N, oH * oW, out_channels_})
+        .permute({0, 2, 1})
+        .reshape({N, out_channels_, oH, oW});
+}
+
+std::vector<Tensor> Conv2d::parameters() {
+    if (use_bias_) return {weight_, bias_};
+    return {weight_};
+}
+
+std::string Conv2d::name() const {
+    return "Conv2d(" + std::to_string(in_channels_) + " -> " + std::to_string(out_channels_) +
+           ", k=" + std::to_string(window_.kernel_h) + "x" + std::to_string(window_.kernel_w) +
+           ", s=" + std::to_string(window_.stride) + ", p=" + std::to_string(window_.padding) + ")";
+}
+
+MaxPool2d::MaxPool2d(const Window2d& window) : window_(window) {
+    if (window_.padding >= window_.kernel_h || window_.padding >= window_.kernel_w)
+        throw std::invalid_argument("MaxPool2d requires padding smaller than the kernel.");
+}
+
+MaxPool2d::MaxPool2d(size_t kernel, size_t stride) : window_(kernel, kernel, stride, 0) {}
+
+// Window max with the int32 index of the first strict maximum; the backward
+// gathers per input pixel (src/conv.cpp:367-473).
+Tensor MaxPool2d::forward(const Tensor& input) {
+    if (input.ndim() != 4)
+        throw std::invalid_argument("MaxPool2d expects a 4D volume (N, C, H, W), received " +
+                                    input.shape_str() + ".");
+    window_.validate(input.shape()[2], input.shape()[3]);
+    const ehip_window_t w = window_of(input.shape(), window_);
+    Tensor out({size_t(w.batch), size_t(w.channels), size_t(w.out_h), size_t(w.out_w)}, 0.0f, false);
+    auto argmax = std::make_shared<DeviceInts>(out.size());
+    hip::check(ehip_maxpool_f32(dptr(input), dout(out), argmax->get(), &w, nullptr), "maxpool");
+    if (track(input.requires_grad())) {
+        out.set_requires_grad(true);
+        out.get_impl()->parents = {input.get_impl()};
+        Tensor input_copy = input;
+        out.get_impl()->backward_fn = [input_copy, argmax, w](const Tensor& g) mutable {
+            Tensor dX(input_copy.shape(), 0.0f, false);
+            hip::check(ehip_maxpool_backward_f32(argmax->get(), dptr(g), dout(dX), &w, nullptr),
+                       "maxpool backward");
+            input_copy.add_grad(dX);
+        };
+    }
+    return out;
+}
+
+std::string MaxPool2d::name() const {
+    return "MaxPool2d(k=" + std::to_string(window_.kernel_h) + ", s=" +
+           std::to_string(window_.stride) + ")";
+}
+
+Tensor Flatten::forward(const Tensor& input) {
+    if (input.ndim() < 2)
+        throw std::invalid_argument("Flatten expects at least 2 dimensions, received " +
+                                    input.shape_str() + ".");
+    const size_t N = input.shape()[0];
+    if (N == 0) throw std::invalid_argument("Flatten received an empty batch.");
+    return input.reshape({N, input.size() / N});
+}
+
+}  // namespace nn
+}  // namespace engine

@@ -1,0 +1,88 @@
+// detail.hpp -- helpers shared by the engine's translation units: graph
+// tracking, shape arithmetic, the suffix-broadcast plan and the fold of a
+// broadcast gradient (the reference's src/tensor_detail.hpp:111-262).
+#ifndef ENGINE_SRC_DETAIL_HPP
+#define ENGINE_SRC_DETAIL_HPP
+
+#include <cstdint>
+#include <vector>
+
+#include "ehip.h"
+#include "engine/autograd.hpp"
+#include "engine/hip.hpp"
+#include "engine/tensor.hpp"
+
+namespace engine {
+namespace detail {
+
+inline bool track(bool requires_grad) { return requires_grad && autograd::grad_enabled(); }
+
+inline size_t product(const std::vector<size_t>& dims, size_t from = 0) {
+    size_t total = 1;
+    for (size_t i = from; i < dims.size(); ++i) total *= dims[i];
+    return total;
+}
+
+// Suffix broadcast: `other`, stripped of leading 1s, must equal the trailing
+// axes of `base`; it then repeats `repeat` times over blocks of `inner`.
+struct BroadcastPlan {
+    bool valid = false;
+    size_t inner = 1;
+    size_t repeat = 1;
+};
+
+inline BroadcastPlan plan_broadcast(const std::vector<size_t>& base,
+                                    const std::vector<size_t>& other) {
+    BroadcastPlan plan;
+    size_t first = 0;
+    while (first < other.size() && other[first] == 1) ++first;
+    const size_t core = other.size() - first;
+    if (core > base.size()) return plan;
+    const size_t offset = base.size() - core;
+    for (size_t i = 0; i < core; ++i)
+        if (base[offset + i] != other[first + i]) return plan;
+    plan.valid = true;
+    plan.inner = product(base, offset);
+    plan.repeat = plan.inner == 0 ? 0 : product(base) / plan.inner;
+    return plan;
+}
+
+inline const float* dptr(const Tensor& t) { return t.storage().device(); }
+inline float* dout(Tensor& t) { return t.storage().device_write(); }
+
+// A tensor viewing `src` with a new shape (no copy).
+inline Tensor view_with_shape(const Storage& src, const std::vector<size_t>& shape, bool req) {
+    auto impl = std::make_shared<TensorImpl>();
+    impl->storage = src.share();
+    impl->shape = shape;
+    impl->compute_strides();
+    impl->requires_grad = req;
+    return Tensor::from_impl(impl);
+}
+
+// Sum of `full` over its leading blocks down to `target` (src/tensor_detail.hpp:182-206).
+inline Tensor fold_leading(const Tensor& full, const std::vector<size_t>& target) {
+    const size_t inner = product(target);
+    const size_t repeat = inner == 0 ? 0 : full.size() / inner;
+    Tensor folded(target, 0.0f, false);
+    hip::check(ehip_sum_axis_f32(dptr(full), dout(folded), 1, int64_t(repeat), int64_t(inner),
+                                 nullptr),
+               "fold_leading");
+    return folded;
+}
+
+// out[o][a][i] = g[o][i]: the gradient of a sum over the middle axis, as a
+// strided move (stride 0 over the summed axis).
+inline Tensor broadcast_middle(const Tensor& g, const std::vector<size_t>& out_shape,
+                               size_t outer, size_t axis_len, size_t inner) {
+    Tensor out(out_shape, 0.0f, false);
+    const int64_t shape[3] = {int64_t(outer), int64_t(axis_len), int64_t(inner)};
+    const int64_t strides[3] = {int64_t(inner), 0, 1};
+    hip::check(ehip_permute_f32(dptr(g), dout(out), 3, shape, strides, nullptr), "broadcast");
+    return out;
+}
+
+}  // namespace detail
+}  // namespace engine
+
+#endif  // ENGINE_SRC_DETAIL_HPP

@@ -1,0 +1,62 @@
+// hip_runtime.cpp -- engine::hip, the control API over include/ehip.h.
+#include "engine/hip.hpp"
+
+#include <stdexcept>
+#include <string>
+
+#include "ehip.h"
+
+namespace engine {
+namespace hip {
+
+void check(int rc, const char* what) {
+    if (rc != EHIP_OK)
+        throw std::runtime_error(std::string(what) + ": " + ehip_last_error() + " (status " +
+                                 std::to_string(rc) + ")");
+}
+
+bool available() { return ehip_available() != 0; }
+
+std::optional<DeviceInfo> device_info() {
+    ehip_device_info_t info;
+    if (ehip_device_info(&info) != EHIP_OK) return std::nullopt;
+    DeviceInfo d;
+    d.name = info.name;
+    d.arch = info.arch;
+    d.compute_units = info.compute_units;
+    d.total_memory = info.total_memory;
+    return d;
+}
+
+void synchronize() { check(ehip_synchronize(), "synchronize"); }
+size_t kernels_launched() { return size_t(ehip_kernels_launched()); }
+size_t kernels_failed() { return size_t(ehip_kernels_failed()); }
+void reset_kernel_counters() { ehip_reset_counters(); }
+
+double peak_fp32_gflops() {
+    ehip_device_info_t info;
+    return ehip_device_info(&info) == EHIP_OK ? info.peak_fp32_mfma_gflops : 0.0;
+}
+
+double peak_bandwidth_gbs() {
+    ehip_device_info_t info;
+    return ehip_device_info(&info) == EHIP_OK ? info.peak_hbm_gbs : 0.0;
+}
+
+TransferStats transfer_stats() {
+    ehip_transfer_stats_t s;
+    ehip_transfer_stats(&s);
+    TransferStats t;
+    t.to_device_bytes = size_t(s.to_device_bytes);
+    t.to_host_bytes = size_t(s.to_host_bytes);
+    t.to_device_count = size_t(s.to_device_count);
+    t.to_host_count = size_t(s.to_host_count);
+    t.to_device_seconds = s.to_device_seconds;
+    t.to_host_seconds = s.to_host_seconds;
+    return t;
+}
+
+void reset_transfer_stats() { ehip_reset_transfer_stats(); }
+
+}  // namespace hip
+}  // namespace engine

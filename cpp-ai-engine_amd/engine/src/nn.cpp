@@ -1,0 +1,180 @@
+// nn.cpp -- Module plumbing, Linear, Sequential, the losses and the accuracy
+// helpers (the reference's src/nn.cpp).
+#include "engine/nn.hpp"
+
+#include <cmath>
+#include <stdexcept>
+
+#include "detail.hpp"
+
+namespace engine {
+namespace nn {
+
+using namespace detail;
+
+std::vector<std::pair<std::string, Tensor>> Module::named_parameters(const std::string& prefix) {
+    std::vector<std::pair<std::string, Tensor>> out;
+    const std::vector<Tensor> params = parameters();
+    for (size_t i = 0; i < params.size(); ++i)
+        out.emplace_back(prefix + std::to_string(i), params[i]);
+    return out;
+}
+
+void Module::zero_grad() {
+    for (Tensor& p : parameters()) p.zero_grad();
+}
+
+size_t Module::num_parameters() {
+    size_t total = 0;
+    for (const Tensor& p : parameters()) total += p.size();
+    return total;
+}
+
+// Xavier-uniform weight (in, out), zero bias (1, out): src/nn.cpp:85-99.
+Linear::Linear(size_t in_features, size_t out_features, bool use_bias)
+    : in_features_(in_features), out_features_(out_features), use_bias_(use_bias) {
+    if (in_features == 0 || out_features == 0)
+        throw std::invalid_argument("Linear requires in_features and out_features greater than zero.");
+    const float limit = std::sqrt(6.0f / static_cast<float>(in_features + out_features));
+    autograd::NoGradGuard no_grad;
+    weight_ = Tensor::rand({in_features, out_features}, -limit, limit, true);
+    bias_ = Tensor({1, out_features}, 0.0f, use_bias);
+}
+
+Tensor Linear::forward(const Tensor& input) {
+    if (input.ndim() < 2)
+        throw std::invalid_argument("Linear expects at least 2 dimensions (..., in_features), received " +
+                                    input.shape_str() + ".");
+    if (input.shape().back() != in_features_)
+        throw std::invalid_argument("Linear with in_features=" + std::to_string(in_features_) +
+                                    " received an input " + input.shape_str() + ".");
+    const bool needs_reshape = input.ndim() > 2;
+    Tensor flat = needs_reshape ? input.reshape({input.size() / in_features_, in_features_}) : input;
+    Tensor out = flat.matmul(weight_);
+    if (use_bias_) out = out + bias_;
+    if (needs_reshape) {
+        std::vector<size_t> out_shape = input.shape();
+        out_shape.back() = out_features_;
+        out = out.reshape(out_shape);
+    }
+    return out;
+}
+
+std::vector<Tensor> Linear::parameters() {
+    if (use_bias_) return {weight_, bias_};
+    return {weight_};
+}
+
+std::string Linear::name() const {
+    return "Linear(" + std::to_string(in_features_) + " -> " + std::to_string(out_features_) +
+           (use_bias_ ? ", bias=true)" : ", bias=false)");
+}
+
+Sequential& Sequential::add(std::unique_ptr<Module> layer) {
+    if (!layer) throw std::invalid_argument("Sequential::add received a null layer.");
+    layers_.push_back(std::move(layer));
+    return *this;
+}
+
+Tensor Sequential::forward(const Tensor& input) {
+    Tensor x = input;
+    for (auto& layer : layers_) x = layer->forward(x);
+    return x;
+}
+
+std::vector<Tensor> Sequential::parameters() {
+    std::vector<Tensor> out;
+    for (auto& layer : layers_)
+        for (const Tensor& p : layer->parameters()) out.push_back(p);
+    return out;
+}
+
+std::vector<std::pair<std::string, Tensor>> Sequential::named_parameters(const std::string& prefix) {
+    std::vector<std::pair<std::string, Tensor>> out;
+    for (size_t i = 0; i < layers_.size(); ++i)
+        for (auto& np : layers_[i]->named_parameters(prefix + std::to_string(i) + "."))
+            out.push_back(np);
+    return out;
+}
+
+void Sequential::train(bool mode) {
+    Module::train(mode);
+    for (auto& layer : layers_) layer->train(mode);
+}
+
+Module& Sequential::at(size_t index) {
+    if (index >= layers_.size()) throw std::out_of_range("Sequential::at: index out of range.");
+    return *layers_[index];
+}
+
+Tensor mse_loss(const Tensor& prediction, const Tensor& target) {
+    if (prediction.shape() != target.shape())
+        throw std::invalid_argument("mse_loss: shapes " + prediction.shape_str() + " and " +
+                                    target.shape_str() + " differ.");
+    Tensor diff = prediction - target;
+    return (diff * diff).mean();
+}
+
+// Probabilities, per-row losses and their mean are computed on the device
+// (the reference computes them serially on the host, src/nn.cpp:346-380);
+// the loss is read back only when host code asks for it.
+Tensor cross_entropy_loss(const Tensor& logits, const std::vector<size_t>& targets) {
+    if (logits.ndim() != 2)
+        throw std::invalid_argument("cross_entropy_loss expects 2D logits (batch, classes), received " +
+                                    logits.shape_str() + ".");
+    const size_t N = logits.shape()[0], C = logits.shape()[1];
+    if (targets.size() != N)
+        throw std::invalid_argument("cross_entropy_loss received " + std::to_string(targets.size()) +
+                                    " labels for a batch of " + std::to_string(N) + ".");
+    if (N == 0) throw std::invalid_argument("cross_entropy_loss received an empty batch.");
+    std::vector<int32_t> t(N);
+    for (size_t i = 0; i < N; ++i) {
+        if (targets[i] >= C)
+            throw std::out_of_range("Label " + std::to_string(targets[i]) +
+                                    " outside the range of " + std::to_string(C) + " classes.");
+        t[i] = static_cast<int32_t>(targets[i]);
+    }
+    auto d_t = std::make_shared<DeviceInts>(t);
+    Tensor probs(logits.shape(), 0.0f, false);
+    const bool req_g = logits.requires_grad() && autograd::grad_enabled();
+    Tensor loss({1}, 0.0f, false);
+    hip::check(ehip_cross_entropy_f32(dptr(logits), d_t->get(), dout(probs), dout(loss),
+                                      int64_t(N), int64_t(C), nullptr),
+               "cross_entropy_loss");
+    if (req_g) {
+        loss.set_requires_grad(true);
+        loss.get_impl()->parents = {logits.get_impl()};
+        Tensor logits_copy = logits;
+        loss.get_impl()->backward_fn = [logits_copy, probs, d_t, N, C](const Tensor& g) mutable {
+            Tensor dX(logits_copy.shape(), 0.0f, false);
+            hip::check(ehip_cross_entropy_backward_f32(dptr(probs), d_t->get(), dout(dX),
+                                                       int64_t(N), int64_t(C), dptr(g), nullptr),
+                       "cross_entropy_loss backward");
+            logits_copy.add_grad(dX);
+        };
+    }
+    return loss;
+}
+
+std::vector<size_t> argmax_rows(const Tensor& logits) {
+    if (logits.ndim() != 2) throw std::invalid_argument("argmax_rows expects 2D logits.");
+    const size_t N = logits.shape()[0], C = logits.shape()[1];
+    const float* v = logits.data();
+    std::vector<size_t> out(N, 0);
+    for (size_t i = 0; i < N; ++i)
+        for (size_t j = 1; j < C; ++j)
+            if (v[i * C + j] > v[i * C + out[i]]) out[i] = j;
+    return out;
+}
+
+float accuracy(const Tensor& logits, const std::vector<size_t>& targets) {
+    const std::vector<size_t> pred = argmax_rows(logits);
+    if (pred.size() != targets.size()) throw std::invalid_argument("accuracy: size mismatch.");
+    if (pred.empty()) return 0.0f;
+    size_t hit = 0;
+    for (size_t i = 0; i < pred.size(); ++i) hit += pred[i] == targets[i];
+    return static_cast<float>(hit) / static_cast<float>(pred.size());
+}
+
+}  // namespace nn
+}  // namespace engine

@@ -1,0 +1,110 @@
+// optim.cpp -- SGD and Adam as one fused kernel per parameter, and
+// clip_grad_norm over the device reductions (the reference's src/optim.cpp).
+#include "engine/optim.hpp"
+
+#include <cmath>
+#include <stdexcept>
+
+#include "detail.hpp"
+
+namespace engine {
+namespace optim {
+
+using namespace detail;
+
+Optimizer::Optimizer(std::vector<Tensor> parameters) : params_(std::move(parameters)) {}
+
+void Optimizer::zero_grad() {
+    for (Tensor& p : params_) p.zero_grad();
+}
+
+SGD::SGD(std::vector<Tensor> parameters, float lr, float momentum, float weight_decay)
+    : Optimizer(std::move(parameters)), momentum_(momentum), weight_decay_(weight_decay) {
+    if (lr <= 0.0f) throw std::invalid_argument("SGD requires a positive learning rate.");
+    if (momentum < 0.0f) throw std::invalid_argument("SGD requires a non-negative momentum.");
+    lr_ = lr;
+    if (momentum_ != 0.0f)
+        for (const Tensor& p : params_) velocity_.emplace_back(p.size(), 0.0f);
+}
+
+void SGD::step() {
+    autograd::NoGradGuard no_grad;
+    for (size_t i = 0; i < params_.size(); ++i) {
+        Tensor& p = params_[i];
+        if (!p.requires_grad() || !p.has_grad()) continue;
+        const Tensor g = p.grad();
+        float* vel = momentum_ != 0.0f ? velocity_[i].device_mut() : nullptr;
+        hip::check(ehip_sgd_f32(p.storage().device_mut(), dptr(g), vel, int64_t(p.size()), lr_,
+                                momentum_, weight_decay_, nullptr),
+                   "sgd step");
+    }
+}
+
+Adam::Adam(std::vector<Tensor> parameters, float lr, float beta1, float beta2, float eps,
+           float weight_decay)
+    : Optimizer(std::move(parameters)), beta1_(beta1), beta2_(beta2), eps_(eps),
+      weight_decay_(weight_decay) {
+    if (lr <= 0.0f) throw std::invalid_argument("Adam requires a positive learning rate.");
+    if (beta1 < 0.0f || beta1 >= 1.0f || beta2 < 0.0f || beta2 >= 1.0f)
+        throw std::invalid_argument("Adam requires beta1 and beta2 in the interval [0, 1).");
+    lr_ = lr;
+    for (const Tensor& p : params_) {
+        m_.emplace_back(p.size(), 0.0f);
+        v_.emplace_back(p.size(), 0.0f);
+    }
+}
+
+// Bias corrections in float with std::pow on the host, then one fused update
+// per parameter (src/optim.cpp:113-162).
+void Adam::step() {
+    autograd::NoGradGuard no_grad;
+    ++t_;
+    const float bias_c1 = 1.0f - std::pow(beta1_, static_cast<float>(t_));
+    const float bias_c2 = 1.0f - std::pow(beta2_, static_cast<float>(t_));
+    for (size_t i = 0; i < params_.size(); ++i) {
+        Tensor& p = params_[i];
+        if (!p.requires_grad() || !p.has_grad()) continue;
+        const Tensor g = p.grad();
+        hip::check(ehip_adam_f32(p.storage().device_mut(), dptr(g), m_[i].device_mut(),
+                                 v_[i].device_mut(), int64_t(p.size()), lr_, beta1_, beta2_, eps_,
+                                 weight_decay_, bias_c1, bias_c2, nullptr),
+                   "adam step");
+    }
+}
+
+// src/optim.cpp:168-208: the norm needs one host read (it decides whether to scale).
+float clip_grad_norm(const std::vector<Tensor>& parameters, float max_norm) {
+    if (max_norm <= 0.0f) throw std::invalid_argument("clip_grad_norm needs a positive max_norm.");
+    autograd::NoGradGuard no_grad;
+    std::vector<double*> partials;
+    void* block = nullptr;
+    hip::check(ehip_arena_alloc(parameters.size() * sizeof(double) + 8, &block), "clip alloc");
+    double* d = static_cast<double*>(block);
+    size_t k = 0;
+    for (const Tensor& p : parameters) {
+        if (!p.has_grad()) continue;
+        const Tensor g = p.grad();
+        hip::check(ehip_reduce_sum_f32(dptr(g), int64_t(g.size()), 1, d + k, nullptr, nullptr),
+                   "clip norm");
+        ++k;
+    }
+    std::vector<double> host(k);
+    if (k > 0) hip::check(ehip_memcpy_d2h(host.data(), d, k * sizeof(double), nullptr), "clip read");
+    ehip_arena_free(block);
+    double total = 0.0;
+    for (double v : host) total += v;
+    const float norm = static_cast<float>(std::sqrt(total));
+    if (norm > max_norm) {
+        const float scale = max_norm / (norm + 1e-6f);
+        for (const Tensor& p : parameters) {
+            if (!p.has_grad()) continue;
+            Tensor g = p.grad();
+            hip::check(ehip_scale_f32(g.storage().device_mut(), int64_t(g.size()), scale, nullptr),
+                       "clip scale");
+        }
+    }
+    return norm;
+}
+
+}  // namespace optim
+}  // namespace engine

@@ -1,0 +1,417 @@
+// tensor_ops.cpp -- arithmetic with suffix broadcast, scalar ops, matmul and
+// its transposed-operand forms, transpose/permute/reshape, ReLU and softmax,
+// each with its derivative (the reference's src/tensor_ops.cpp). Every value
+// is computed by a kernel of libehip on the engine's stream.
+#include <cmath>
+#include <stdexcept>
+#include <string>
+
+#include "detail.hpp"
+#include "engine/tensor.hpp"
+
+namespace engine {
+
+using namespace detail;
+
+namespace {
+
+// out = a op b with the suffix broadcast of b.
+Tensor binary_values(int op, const Tensor& a, const Tensor& b, const char* what) {
+    const bool broadcast = a.shape() != b.shape();
+    size_t inner = a.size(), repeat = 1;
+    if (broadcast) {
+        const BroadcastPlan plan = plan_broadcast(a.shape(), b.shape());
+        if (!plan.valid)
+            throw std::invalid_argument(std::string("Incompatible shapes for tensor ") + what +
+                                        ": " + a.shape_str() + " and " + b.shape_str() + ".");
+        inner = plan.inner;
+        repeat = plan.repeat;
+    }
+    Tensor res(a.shape(), 0.0f, false);
+    if (inner > 0)
+        hip::check(ehip_binary_f32(op, dptr(a), dptr(b), dout(res), int64_t(inner),
+                                   int64_t(repeat), nullptr),
+                   what);
+    return res;
+}
+
+void attach(Tensor& res, std::vector<std::shared_ptr<TensorImpl>> parents,
+            std::function<void(const Tensor&)> fn) {
+    res.set_requires_grad(true);
+    res.get_impl()->parents = std::move(parents);
+    res.get_impl()->backward_fn = std::move(fn);
+}
+
+Tensor reduce_to(const Tensor& d, const Tensor& target) {
+    return d.shape() == target.shape() ? d : fold_leading(d, target.shape());
+}
+
+// The batch geometry of a product: 2-D operands are shared across the batch.
+struct Batch {
+    std::vector<size_t> dims;
+    size_t count = 1;
+    bool a_batched = false, b_batched = false;
+};
+
+Batch batch_of(const Tensor& a, const Tensor& b) {
+    if (a.ndim() < 2 || b.ndim() < 2)
+        throw std::invalid_argument("MatMul requires at least 2 dimensions in both operands.");
+    const std::vector<size_t> ba(a.shape().begin(), a.shape().end() - 2);
+    const std::vector<size_t> bb(b.shape().begin(), b.shape().end() - 2);
+    Batch r;
+    r.a_batched = !ba.empty();
+    r.b_batched = !bb.empty();
+    if (r.a_batched && r.b_batched && ba != bb)
+        throw std::invalid_argument("Batched MatMul needs identical batch axes: " + a.shape_str() +
+                                    " and " + b.shape_str() + ".");
+    r.dims = r.a_batched ? ba : bb;
+    r.count = product(r.dims);
+    return r;
+}
+
+// C = op(A) op(B), batched; returns a fresh tensor of shape dims + (m, n).
+Tensor gemm(bool ta, bool tb, const Tensor& a, const Tensor& b, const Batch& bt, size_t m,
+            size_t n, size_t k) {
+    std::vector<size_t> shape = bt.dims;
+    shape.push_back(m);
+    shape.push_back(n);
+    Tensor c(shape, 0.0f, false);
+    const size_t a_rows = a.shape()[a.ndim() - 2], a_cols = a.shape()[a.ndim() - 1];
+    const size_t b_rows = b.shape()[b.ndim() - 2], b_cols = b.shape()[b.ndim() - 1];
+    hip::check(ehip_gemm_f32(ta ? 1 : 0, tb ? 1 : 0, int64_t(bt.count), int64_t(m), int64_t(n),
+                             int64_t(k), dptr(a), int64_t(a_cols),
+                             bt.a_batched ? int64_t(a_rows * a_cols) : 0, dptr(b), int64_t(b_cols),
+                             bt.b_batched ? int64_t(b_rows * b_cols) : 0, 0.0f, dout(c),
+                             int64_t(n), int64_t(m * n), nullptr),
+               "matmul");
+    return c;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ element-wise
+
+Tensor Tensor::operator+(const Tensor& other) const {
+    Tensor res = binary_values(EHIP_ADD, *this, other, "addition");
+    if (track(requires_grad() || other.requires_grad())) {
+        Tensor self_copy = *this, other_copy = other;
+        attach(res, {impl_, other.impl_}, [self_copy, other_copy](const Tensor& g) mutable {
+            // Both operand gradients fresh and the same shape: one fused pass
+            // hands g to both (it equals two add_grad calls bit for bit).
+            const bool same = self_copy.shape() == other_copy.shape();
+            auto& sg = self_copy.get_impl()->grad;
+            auto& og = other_copy.get_impl()->grad;
+            if (same && self_copy.requires_grad() && other_copy.requires_grad() &&
+                self_copy.get_impl() != other_copy.get_impl()) {
+                const bool init_a = !sg || sg->storage.pending_zero();
+                const bool init_b = !og || og->storage.pending_zero();
+                if (!sg) sg = std::make_shared<TensorImpl>(self_copy.shape(), 0.0f, false);
+                if (!og) og = std::make_shared<TensorImpl>(other_copy.shape(), 0.0f, false);
+                const float* src = dptr(g);
+                float* da = init_a ? sg->storage.device_write() : sg->storage.device_mut();
+                float* db = init_b ? og->storage.device_write() : og->storage.device_mut();
+                hip::check(ehip_add_backward_f32(src, da, db, int64_t(g.size()), init_a ? 0 : 1,
+                                                 init_b ? 0 : 1, nullptr),
+                           "add backward");
+                return;
+            }
+            if (self_copy.requires_grad()) self_copy.add_grad(g);
+            if (other_copy.requires_grad()) other_copy.add_grad(reduce_to(g, other_copy));
+        });
+    }
+    return res;
+}
+
+Tensor Tensor::operator-(const Tensor& other) const {
+    Tensor res = binary_values(EHIP_SUB, *this, other, "subtraction");
+    if (track(requires_grad() || other.requires_grad())) {
+        Tensor self_copy = *this, other_copy = other;
+        attach(res, {impl_, other.impl_}, [self_copy, other_copy](const Tensor& g) mutable {
+            if (self_copy.requires_grad()) self_copy.add_grad(g);
+            if (other_copy.requires_grad()) other_copy.add_grad(reduce_to(g * -1.0f, other_copy));
+        });
+    }
+    return res;
+}
+
+Tensor Tensor::operator*(const Tensor& other) const {
+    Tensor res = binary_values(EHIP_MUL, *this, other, "multiplication");
+    if (track(requires_grad() || other.requires_grad())) {
+        Tensor self_copy = *this, other_copy = other;
+        attach(res, {impl_, other.impl_}, [self_copy, other_copy](const Tensor& g) mutable {
+            // g * expand(other) is the broadcast product itself.
+            if (self_copy.requires_grad()) self_copy.add_grad(binary_values(EHIP_MUL, g, other_copy, "mul"));
+            if (other_copy.requires_grad())
+                other_copy.add_grad(reduce_to(binary_values(EHIP_MUL, g, self_copy, "mul"), other_copy));
+        });
+    }
+    return res;
+}
+
+Tensor Tensor::operator/(const Tensor& other) const {
+    Tensor res = binary_values(EHIP_DIV, *this, other, "division");
+    if (track(requires_grad() || other.requires_grad())) {
+        Tensor self_copy = *this, other_copy = other;
+        attach(res, {impl_, other.impl_}, [self_copy, other_copy](const Tensor& g) mutable {
+            if (self_copy.requires_grad()) self_copy.add_grad(binary_values(EHIP_DIV, g, other_copy, "div"));
+            if (other_copy.requires_grad()) {
+                // (g * x * -1) / (rhs * rhs), rhs broadcast (src/tensor_ops.cpp:251-256).
+                Tensor num = binary_values(EHIP_MUL, g, self_copy, "mul") * -1.0f;
+                Tensor r2 = binary_values(EHIP_MUL, other_copy, other_copy, "mul");
+                other_copy.add_grad(reduce_to(binary_values(EHIP_DIV, num, r2, "div"), other_copy));
+            }
+        });
+    }
+    return res;
+}
+
+Tensor Tensor::operator+(float scalar) const {
+    Tensor res(shape(), 0.0f, false);
+    hip::check(ehip_scalar_f32(dptr(*this), dout(res), int64_t(size()), 1.0f, scalar, nullptr),
+               "scalar add");
+    if (track(requires_grad())) {
+        Tensor self_copy = *this;
+        attach(res, {impl_}, [self_copy](const Tensor& g) mutable { self_copy.add_grad(g); });
+    }
+    return res;
+}
+
+Tensor Tensor::operator-(float scalar) const { return (*this) + (-scalar); }
+
+Tensor Tensor::operator*(float scalar) const {
+    Tensor res(shape(), 0.0f, false);
+    if (scalar == 1.0f) {  // x * 1 is x exactly (ehip_scalar_f32 would add 0)
+        if (size() > 0)
+            hip::check(ehip_memcpy_d2d(dout(res), dptr(*this), size() * sizeof(float), nullptr),
+                       "copy");
+    } else {
+        hip::check(ehip_scalar_f32(dptr(*this), dout(res), int64_t(size()), scalar, 0.0f, nullptr),
+                   "scalar mul");
+    }
+    if (track(requires_grad())) {
+        Tensor self_copy = *this;
+        attach(res, {impl_},
+               [self_copy, scalar](const Tensor& g) mutable { self_copy.add_grad(g * scalar); });
+    }
+    return res;
+}
+
+Tensor Tensor::operator/(float scalar) const {
+    if (scalar == 0.0f) throw std::invalid_argument("Division by zero.");
+    return (*this) * (1.0f / scalar);
+}
+
+Tensor operator+(float scalar, const Tensor& t) { return t + scalar; }
+Tensor operator*(float scalar, const Tensor& t) { return t * scalar; }
+Tensor operator-(float scalar, const Tensor& t) { return (t * -1.0f) + scalar; }
+
+// ------------------------------------------------------------------ products
+
+// src/tensor_ops.cpp:475-588. The backward products read the operands in
+// place through the GEMM's transposed modes instead of materialising B^T and
+// A^T; a shared operand's gradient is folded over the batch.
+Tensor Tensor::matmul(const Tensor& B) const {
+    const Batch bt = batch_of(*this, B);
+    const size_t M = shape()[ndim() - 2], K = shape()[ndim() - 1];
+    const size_t K2 = B.shape()[B.ndim() - 2], N = B.shape()[B.ndim() - 1];
+    if (K != K2)
+        throw std::invalid_argument("Incompatible dimensions for MatMul: " + shape_str() + " and " +
+                                    B.shape_str() + ".");
+    Tensor C = gemm(false, false, *this, B, bt, M, N, K);
+    if (track(requires_grad() || B.requires_grad())) {
+        Tensor a = *this, b = B;
+        attach(C, {impl_, B.impl_}, [a, b, bt, M, N, K](const Tensor& g) mutable {
+            Batch gb = bt;
+            gb.a_batched = true;  // g always carries the batch
+            if (a.requires_grad()) {
+                Batch db = gb;
+                db.b_batched = bt.b_batched;
+                a.add_grad(reduce_to(gemm(false, true, g, b, db, M, K, N), a));  // g B^T
+            }
+            if (b.requires_grad()) {
+                Batch db;
+                db.dims = bt.dims;
+                db.count = bt.count;
+                db.a_batched = bt.a_batched;
+                db.b_batched = true;
+                b.add_grad(reduce_to(gemm(true, false, a, g, db, K, N, M), b));  // A^T g
+            }
+        });
+    }
+    return C;
+}
+
+namespace ops {
+
+// C = A B^T: A (.., m, k), B (.., n, k).
+Tensor matmul_nt(const Tensor& A, const Tensor& B) {
+    const Batch bt = batch_of(A, B);
+    const size_t M = A.shape()[A.ndim() - 2], K = A.shape()[A.ndim() - 1];
+    const size_t N = B.shape()[B.ndim() - 2];
+    if (B.shape()[B.ndim() - 1] != K)
+        throw std::invalid_argument("Incompatible dimensions for A B^T: " + A.shape_str() + " and " +
+                                    B.shape_str() + ".");
+    Tensor C = gemm(false, true, A, B, bt, M, N, K);
+    if (track(A.requires_grad() || B.requires_grad())) {
+        Tensor a = A, b = B;
+        attach(C, {A.get_impl(), B.get_impl()}, [a, b, bt, M, N, K](const Tensor& g) mutable {
+            if (a.requires_grad()) {  // dA = g B
+                Batch db = bt;
+                db.a_batched = true;
+                a.add_grad(reduce_to(gemm(false, false, g, b, db, M, K, N), a));
+            }
+            if (b.requires_grad()) {  // dB = g^T A
+                Batch db = bt;
+                db.a_batched = true;
+                db.b_batched = bt.a_batched;
+                b.add_grad(reduce_to(gemm(true, false, g, a, db, N, K, M), b));
+            }
+        });
+    }
+    return C;
+}
+
+// C = A^T B: A (.., k, m), B (.., k, n).
+Tensor matmul_tn(const Tensor& A, const Tensor& B) {
+    const Batch bt = batch_of(A, B);
+    const size_t K = A.shape()[A.ndim() - 2], M = A.shape()[A.ndim() - 1];
+    const size_t N = B.shape()[B.ndim() - 1];
+    if (B.shape()[B.ndim() - 2] != K)
+        throw std::invalid_argument("Incompatible dimensions for A^T B: " + A.shape_str() + " and " +
+                                    B.shape_str() + ".");
+    Tensor C = gemm(true, false, A, B, bt, M, N, K);
+    if (track(A.requires_grad() || B.requires_grad())) {
+        Tensor a = A, b = B;
+        attach(C, {A.get_impl(), B.get_impl()}, [a, b, bt, M, N, K](const Tensor& g) mutable {
+            if (a.requires_grad()) {  // dA = B g^T
+                Batch db = bt;
+                db.a_batched = bt.b_batched;
+                db.b_batched = true;
+                a.add_grad(reduce_to(gemm(false, true, b, g, db, K, M, N), a));
+            }
+            if (b.requires_grad()) {  // dB = A g
+                Batch db = bt;
+                db.b_batched = true;
+                b.add_grad(reduce_to(gemm(false, false, a, g, db, K, N, M), b));
+            }
+        });
+    }
+    return C;
+}
+
+}  // namespace ops
+
+// ------------------------------------------------------------------ layout
+
+Tensor Tensor::transpose() const {
+    if (ndim() < 2)
+        throw std::invalid_argument("Transpose requires at least 2 dimensions; this tensor is " +
+                                    shape_str() + ".");
+    const size_t rows = shape()[ndim() - 2], cols = shape()[ndim() - 1];
+    const size_t batch = rows * cols == 0 ? 0 : size() / (rows * cols);
+    std::vector<size_t> out_shape = shape();
+    std::swap(out_shape[ndim() - 2], out_shape[ndim() - 1]);
+    Tensor res(out_shape, 0.0f, false);
+    if (size() > 0)
+        hip::check(ehip_transpose_f32(dptr(*this), dout(res), int64_t(batch), int64_t(rows),
+                                      int64_t(cols), nullptr),
+                   "transpose");
+    if (track(requires_grad())) {
+        Tensor self_copy = *this;
+        attach(res, {impl_},
+               [self_copy](const Tensor& g) mutable { self_copy.add_grad(g.transpose()); });
+    }
+    return res;
+}
+
+Tensor Tensor::permute(const std::vector<size_t>& order) const {
+    const size_t nd = ndim();
+    if (order.size() != nd)
+        throw std::invalid_argument("permute needs an order of " + std::to_string(nd) +
+                                    " axes for a tensor " + shape_str() + ".");
+    std::vector<bool> seen(nd, false);
+    for (size_t axis : order) {
+        if (axis >= nd || seen[axis])
+            throw std::invalid_argument("permute needs a valid permutation of the axes.");
+        seen[axis] = true;
+    }
+    std::vector<size_t> out_shape(nd);
+    std::vector<int64_t> oshape(nd), src(nd);
+    for (size_t i = 0; i < nd; ++i) {
+        out_shape[i] = shape()[order[i]];
+        oshape[i] = int64_t(out_shape[i]);
+        src[i] = int64_t(strides()[order[i]]);
+    }
+    Tensor res(out_shape, 0.0f, false);
+    if (size() > 0)
+        hip::check(ehip_permute_f32(dptr(*this), dout(res), int(nd), oshape.data(), src.data(),
+                                    nullptr),
+                   "permute");
+    if (track(requires_grad())) {
+        Tensor self_copy = *this;
+        std::vector<size_t> inverse(nd);
+        for (size_t i = 0; i < nd; ++i) inverse[order[i]] = i;
+        attach(res, {impl_}, [self_copy, inverse](const Tensor& g) mutable {
+            self_copy.add_grad(g.permute(inverse));
+        });
+    }
+    return res;
+}
+
+Tensor Tensor::reshape(const std::vector<size_t>& new_shape) const {
+    if (product(new_shape) != size())
+        throw std::invalid_argument("Incompatible element count for Reshape.");
+    const bool req_g = track(requires_grad());
+    Tensor res = view_with_shape(impl_->storage, new_shape, false);
+    if (req_g) {
+        Tensor self_copy = *this;
+        attach(res, {impl_}, [self_copy](const Tensor& g) mutable {
+            self_copy.add_grad(g.reshape(self_copy.shape()));
+        });
+    }
+    return res;
+}
+
+// ------------------------------------------------------------------ activations
+
+Tensor Tensor::relu() const {
+    Tensor res(shape(), 0.0f, false);
+    hip::check(ehip_relu_f32(dptr(*this), dout(res), int64_t(size()), nullptr), "relu");
+    if (track(requires_grad())) {
+        Tensor self_copy = *this;
+        attach(res, {impl_}, [self_copy](const Tensor& g) mutable {
+            Tensor dX(self_copy.shape(), 0.0f, false);
+            hip::check(ehip_relu_backward_f32(dptr(self_copy), dptr(g), dout(dX),
+                                              int64_t(self_copy.size()), nullptr),
+                       "relu backward");
+            self_copy.add_grad(dX);
+        });
+    }
+    return res;
+}
+
+// Row softmax over the last axis. The backward keeps a view of the output
+// (the reference keeps a detached copy, src/tensor_ops.cpp:652-654; nothing
+// writes into an op's output, so the view holds the same values).
+Tensor Tensor::softmax() const {
+    if (ndim() == 0 || size() == 0) throw std::invalid_argument("Softmax needs a non-empty tensor.");
+    const size_t cols = shape().back();
+    const size_t rows = size() / cols;
+    Tensor res(shape(), 0.0f, false);
+    hip::check(ehip_softmax_f32(dptr(*this), dout(res), int64_t(rows), int64_t(cols), nullptr),
+               "softmax");
+    if (track(requires_grad())) {
+        Tensor self_copy = *this;
+        Tensor saved = view_with_shape(res.storage(), res.shape(), false);
+        attach(res, {impl_}, [self_copy, saved, rows, cols](const Tensor& g) mutable {
+            Tensor dX(self_copy.shape(), 0.0f, false);
+            hip::check(ehip_softmax_backward_f32(dptr(saved), dptr(g), dout(dX), int64_t(rows),
+                                                 int64_t(cols), nullptr),
+                       "softmax backward");
+            self_copy.add_grad(dX);
+        });
+    }
+    return res;
+}
+
+}  // namespace engine

@@ -125,10 +125,13 @@ typedef struct {
 } ehip_arena_stats_t;
 void ehip_arena_stats(ehip_arena_stats_t* out);
 
-/* Copies of `bytes` bytes. Host-to-device and device-to-host return once the
- * host buffer may be reused / read (cuda::detail::copy_to_device/copy_to_host/
- * copy_device_to_device, include/engine/cuda.hpp:231-236). Device-to-device is
- * stream-ordered and asynchronous. */
+/* Copies of `bytes` bytes (cuda::detail::copy_to_device/copy_to_host/
+ * copy_device_to_device, include/engine/cuda.hpp:231-236). All three are
+ * ordered on `stream`. Host-to-device returns once the host buffer may be
+ * reused: uploads up to 16 MiB are staged through a pinned ring and complete
+ * asynchronously; larger ones wait for the stream. Device-to-host waits for
+ * the stream and returns with the data in place. Device-to-device is
+ * asynchronous. */
 int ehip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int ehip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int ehip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
