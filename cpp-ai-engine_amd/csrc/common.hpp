@@ -32,12 +32,23 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // Grow-only device scratch owned by the library (never shrinks; replaced by a
 // larger block when asked for more). Work is ordered on one stream, so a
 // buffer released while queued kernels still use it is reused only by later
-// work on that stream. Returns nullptr (with the error recorded) on failure.
-void* scratch(size_t bytes);
+// work on that stream. Slots are independent buffers: an entry point uses
+// slot 0, and helpers it calls (column_sums) use slot 1, so the two never
+// overlap. Returns nullptr (with the error recorded) on failure.
+constexpr int kScratchSlots = 2;
+void* scratch(size_t bytes, int slot = 0);
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Column sums of `slabs` row-major (rows, cols) matrices with row pitch `ld`,
+// slab pitch x_slab, into out[slab][cols]. Deterministic: the summation order
+// depends only on the shape (reduce.hip).
+int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
+                int64_t x_slab, float* out, hipStream_t s);
+
+__host__ __device__ inline bool aligned16(const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
 
 }  // namespace ehip
 

@@ -13,6 +13,8 @@
 
 #include "common.hpp"
 
+#include <vector>
+
 namespace ehip {
 namespace {
 
@@ -305,6 +307,55 @@ struct Adam {
     }
 };
 
+// Multi-tensor Adam: the tensors are cut into chunks of kAdamChunk elements
+// (one chunk per workgroup, kUnroll float4 per thread); a workgroup finds its
+// tensor by binary search over the chunk prefix of the slot table.
+struct AdamSlot {
+    float* p;
+    const float* g;
+    float* m;
+    float* v;
+    int64_t n;
+    int64_t first_chunk;
+};
+constexpr int64_t kAdamChunk = int64_t(kThreads) * kUnroll * 4;
+
+__global__ __launch_bounds__(kThreads) void adam_multi(const AdamSlot* __restrict__ slots,
+                                                       int count, float lr, float b1, float b2,
+                                                       float eps, float wd, float c1, float c2) {
+    const int64_t b = blockIdx.x;
+    int lo = 0, hi = count - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (slots[mid].first_chunk <= b)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const AdamSlot s = slots[lo];
+    const Adam op{s.p, s.g, s.m, s.v, lr, b1, b2, eps, wd, c1, c2};
+    const int64_t begin = (b - s.first_chunk) * kAdamChunk;
+    const int64_t end = min(begin + kAdamChunk, s.n);
+    const bool vec = aligned16(s.p) && aligned16(s.g) && aligned16(s.m) && aligned16(s.v);
+    int64_t tail = begin;
+    if (vec) {
+        const int64_t v0 = begin >> 2, v1 = end >> 2;  // whole float4 vectors in the chunk
+        float4 r[kUnroll][4];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t v = v0 + int64_t(u) * kThreads + threadIdx.x;
+            if (v < v1) op.load(v, r[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t v = v0 + int64_t(u) * kThreads + threadIdx.x;
+            if (v < v1) op.store(v, r[u]);
+        }
+        tail = v1 << 2;
+    }
+    for (int64_t i = tail + threadIdx.x; i < end; i += kThreads) op.scalar(i);
+}
+
 template <int OP>
 int binary_op(const float* a, const float* b, float* out, int64_t inner, int64_t repeat,
               hipStream_t s) {
@@ -416,6 +467,36 @@ int ehip_adam_f32(float* p, const float* g, float* m, float* v, int64_t n, float
     return launch_stream("adam",
                          Adam{p, g, m, v, lr, beta1, beta2, eps, weight_decay, bias_c1, bias_c2},
                          n, vec, as_stream(stream));
+}
+
+int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, float beta1,
+                        float beta2, float eps, float weight_decay, float bias_c1,
+                        float bias_c2, void* stream) {
+    EHIP_READY();
+    if (count < 0 || (count > 0 && tensors == nullptr))
+        return fail(EHIP_EINVAL, "adam_multi: bad tensor list");
+    std::vector<AdamSlot> slots;
+    slots.reserve(size_t(count));
+    int64_t chunks = 0;
+    for (int i = 0; i < count; ++i) {
+        const ehip_adam_tensor_t& t = tensors[i];
+        if (t.n < 0) return fail(EHIP_EINVAL, "adam_multi: tensor %d has a negative size", i);
+        if (t.n == 0) continue;
+        if (!t.p || !t.g || !t.m || !t.v)
+            return fail(EHIP_EINVAL, "adam_multi: tensor %d has a null pointer", i);
+        slots.push_back({t.p, t.g, t.m, t.v, t.n, chunks});
+        chunks += ceil_div(t.n, kAdamChunk);
+    }
+    if (slots.empty()) return EHIP_OK;
+    if (chunks > 0x7fffffff) return fail(EHIP_EINVAL, "adam_multi: too many elements");
+    hipStream_t s = as_stream(stream);
+    const size_t bytes = slots.size() * sizeof(AdamSlot);
+    AdamSlot* table = static_cast<AdamSlot*>(scratch(bytes));
+    if (table == nullptr) return EHIP_ENOMEM;
+    if (int rc = ehip_memcpy_h2d(table, slots.data(), bytes, stream)) return rc;
+    EHIP_LAUNCH("adam_multi", adam_multi, dim3(unsigned(chunks)), dim3(kThreads), 0, s, table,
+                int(slots.size()), lr, beta1, beta2, eps, weight_decay, bias_c1, bias_c2);
+    return EHIP_OK;
 }
 
 }  // extern "C"

@@ -243,8 +243,19 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
     if (e >= mn * batch) return;
     const int64_t b = e / mn, rc = e % mn;
     const int64_t row = rc / n, col = rc % n;
-    float acc = w[(0 * batch + b) * mn + rc];
-    for (int s = 1; s < splits; ++s) acc += w[(int64_t(s) * batch + b) * mn + rc];
+    // Splits ascending; the loads are issued eight at a time ahead of the adds.
+    const float* p = w + b * mn + rc;
+    const int64_t step = batch * mn;
+    float acc = p[0];
+    int s = 1;
+    for (; s + 8 <= splits; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[int64_t(s + u) * step];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; s < splits; ++s) acc += p[int64_t(s) * step];
     float* dst = c + b * stride_c + row * ldc + col;
     if (beta != 0.0f) acc = acc + beta * *dst;
     *dst = acc;
@@ -257,13 +268,14 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
     g.tiles_m = int(ceil_div(g.m, BM));
     g.tiles_n = int(ceil_div(g.n, BN));
     const int64_t tiles = int64_t(g.tiles_m) * g.tiles_n;
-    // Split K when the tile grid alone cannot fill the chip and K is long.
+    // Split K when the tile grid alone cannot fill the chip (256 CUs) and K is
+    // long: aim for ~512 workgroups, each at least 8 K steps long.
     int splits = 1;
-    if (tiles * batch < 128 && g.k >= 4 * BK * 8) {
-        int64_t want = ceil_div(256, tiles * batch);
-        int64_t max_by_k = g.k / (4 * BK);
+    if (tiles * batch < 256 && g.k >= 16 * BK) {
+        int64_t want = ceil_div(512, tiles * batch);
+        const int64_t max_by_k = g.k / (8 * BK);
         if (want > max_by_k) want = max_by_k;
-        if (want > 64) want = 64;
+        if (want > 256) want = 256;
         if (want > 1) splits = int(want);
     }
     g.k_chunk = ceil_div(ceil_div(g.k, splits), BK) * BK;
@@ -297,8 +309,10 @@ int gemm_modes(const GemmArgs& g, int64_t batch, hipStream_t s) {
     // The unchecked kernels need whole tiles and 16-byte aligned float4 rows.
     const bool aligned = aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
                          g.stride_a % 4 == 0 && g.stride_b % 4 == 0;
+    // 128 x 128 tiles when the grid fills the chip, or when K is long enough
+    // for split-K to make up the difference; 64 x 64 otherwise.
     const int64_t big_tiles = ceil_div(g.m, 128) * ceil_div(g.n, 128);
-    if (big_tiles * batch >= 192) {
+    if (big_tiles * batch >= 192 || (big_tiles * batch >= 32 && g.k >= 2048)) {
         const bool check = !(aligned && g.m % 128 == 0 && g.n % 128 == 0 && g.k % 16 == 0);
         return launch_cfg<128, 128, 16, 64, 64, TA, TB>(g, batch, check, s);
     }

@@ -11,6 +11,22 @@ namespace {
 
 constexpr int kThreads = 256;
 
+// Adds p[0], p[step], ..., p[(n-1) step] to acc in that order. Loads are
+// issued eight at a time ahead of the additions, which stay in index order.
+__device__ __forceinline__ float ordered_sum(float acc, const float* __restrict__ p, int64_t n,
+                                             int64_t step) {
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[(i + u) * step];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; i < n; ++i) acc += p[i * step];
+    return acc;
+}
+
 // One thread per output element, axis ascending from zero: exactly the order
 // of src/tensor.cpp:347-356, so the result is bit-identical to the CPU.
 __global__ __launch_bounds__(kThreads) void sum_axis_serial(const float* __restrict__ x,
@@ -20,31 +36,39 @@ __global__ __launch_bounds__(kThreads) void sum_axis_serial(const float* __restr
     const int64_t e = int64_t(blockIdx.x) * kThreads + threadIdx.x;
     if (e >= n_out) return;
     const int64_t o = e / inner, i = e % inner;
-    const float* p = x + o * axis_len * inner + i;
-    float acc = 0.0f;
-    for (int64_t a = 0; a < axis_len; ++a) acc += p[a * inner];
-    out[e] = acc;
+    out[e] = ordered_sum(0.0f, x + o * axis_len * inner + i, axis_len, inner);
 }
 
-// Stage 1 of the chunked sum: partial[o][c][i] = serial sum of the c-th chunk
-// of the axis.
-__global__ __launch_bounds__(kThreads) void sum_axis_chunks(const float* __restrict__ x,
-                                                            float* __restrict__ partial,
-                                                            int64_t axis_len, int64_t inner,
-                                                            int64_t chunks, int64_t chunk_len,
-                                                            int64_t n_part) {
-    const int64_t e = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (e >= n_part) return;
-    const int64_t i = e % inner;
-    const int64_t t = e / inner;
-    const int64_t c = t % chunks, o = t / chunks;
-    const int64_t a0 = c * chunk_len;
-    int64_t a1 = a0 + chunk_len;
-    if (a1 > axis_len) a1 = axis_len;
-    const float* p = x + o * axis_len * inner + i;
+// Column sums over a block of rows, for the long-axis / few-outputs case
+// (bias gradients: thousands of rows, 8 to 4096 columns). The 256 threads
+// form RL row lanes x CW columns (CW = min(64, cols rounded up to a power of
+// two)); block (b, t, o) covers rows [b*rpb, (b+1)*rpb) and columns
+// [t*CW, (t+1)*CW) of slab o. Lane l adds rows r0+l, r0+l+RL, ... in order;
+// then one thread per column adds the RL lane sums in lane order. The order
+// depends only on the shape.
+__global__ __launch_bounds__(kThreads) void sum_cols(const float* __restrict__ x,
+                                                     float* __restrict__ out, int64_t rows,
+                                                     int64_t cols, int64_t ld, int64_t rpb,
+                                                     int64_t x_slab, int64_t out_slab, int cw) {
+    __shared__ float lanes[kThreads];
+    const int rl = kThreads / cw;
+    const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
+    const int64_t c = int64_t(blockIdx.y) * cw + cl;
+    const int64_t r0 = int64_t(blockIdx.x) * rpb;
+    int64_t r1 = r0 + rpb;
+    if (r1 > rows) r1 = rows;
+    const float* xs = x + int64_t(blockIdx.z) * x_slab;
     float acc = 0.0f;
-    for (int64_t a = a0; a < a1; ++a) acc += p[a * inner];
-    partial[e] = acc;
+    if (c < cols && r0 + lane < r1)
+        acc = ordered_sum(0.0f, xs + (r0 + lane) * ld + c, (r1 - r0 - lane + rl - 1) / rl,
+                          int64_t(rl) * ld);
+    lanes[threadIdx.x] = acc;
+    __syncthreads();
+    if (lane == 0 && c < cols) {
+        float s = 0.0f;
+        for (int l = 0; l < rl; ++l) s += lanes[l * cw + cl];
+        out[int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c] = s;
+    }
 }
 
 // Whole-buffer sum in double: a fixed grid of blocks, each thread striding by
@@ -88,6 +112,41 @@ __global__ __launch_bounds__(kThreads) void reduce_stage2(const double* __restri
 }
 
 }  // namespace
+
+// Two passes of sum_cols: row blocks into partials, then the partials of each
+// slab. The row blocks are sized so that the first pass has about a thousand
+// workgroups and the second adds at most 64 partials per lane.
+int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
+                int64_t x_slab, float* out, hipStream_t s) {
+    if (slabs == 0 || cols == 0) return EHIP_OK;
+    int cw = 1;
+    while (cw < cols && cw < 64) cw *= 2;
+    const int64_t tiles = ceil_div(cols, cw);
+    if (tiles > 65535 || slabs > 65535) return fail(EHIP_EINVAL, "column_sums: too many columns");
+    const int rl = kThreads / cw;
+    int64_t blocks = ceil_div(1024, tiles * slabs);
+    const int64_t max_blocks = ceil_div(rows, 2 * rl);  // at least two rows per lane
+    if (blocks > max_blocks) blocks = max_blocks;
+    if (blocks > 64 * rl) blocks = 64 * rl;
+    if (blocks < 1) blocks = 1;
+    const int64_t rpb = ceil_div(rows, blocks);
+    blocks = ceil_div(rows, rpb);
+    if (blocks == 1) {
+        EHIP_LAUNCH("column_sums", sum_cols, dim3(1, unsigned(tiles), unsigned(slabs)),
+                    dim3(kThreads), 0, s, x, out, rows, cols, ld, rows, x_slab, cols, cw);
+        return EHIP_OK;
+    }
+    float* partial =
+        static_cast<float*>(scratch(size_t(slabs * blocks * cols) * sizeof(float), 1));
+    if (partial == nullptr) return EHIP_ENOMEM;
+    EHIP_LAUNCH("column_sums_blocks", sum_cols, dim3(unsigned(blocks), unsigned(tiles), unsigned(slabs)),
+                dim3(kThreads), 0, s, x, partial, rows, cols, ld, rpb, x_slab, blocks * cols, cw);
+    EHIP_LAUNCH("column_sums_final", sum_cols, dim3(1, unsigned(tiles), unsigned(slabs)),
+                dim3(kThreads), 0, s, partial, out, blocks, cols, cols, blocks, blocks * cols,
+                cols, cw);
+    return EHIP_OK;
+}
+
 }  // namespace ehip
 
 using namespace ehip;
@@ -107,21 +166,8 @@ int ehip_sum_axis_f32(const float* x, float* out, int64_t outer, int64_t axis_le
                     dim3(kThreads), 0, s, x, out, axis_len, inner, n_out);
         return EHIP_OK;
     }
-    // Enough chunks to give ~64k threads, each chunk at least 32 long.
-    int64_t chunks = ceil_div(65536, n_out);
-    if (chunks > axis_len / 32) chunks = axis_len / 32;
-    if (chunks > 1024) chunks = 1024;
-    if (chunks < 2) chunks = 2;
-    const int64_t chunk_len = ceil_div(axis_len, chunks);
-    chunks = ceil_div(axis_len, chunk_len);
-    const int64_t n_part = n_out * chunks;
-    float* partial = static_cast<float*>(scratch(size_t(n_part) * sizeof(float)));
-    if (partial == nullptr) return EHIP_ENOMEM;
-    EHIP_LAUNCH("sum_axis_chunks", sum_axis_chunks, dim3(unsigned(ceil_div(n_part, kThreads))),
-                dim3(kThreads), 0, s, x, partial, axis_len, inner, chunks, chunk_len, n_part);
-    EHIP_LAUNCH("sum_axis", sum_axis_serial, dim3(unsigned(ceil_div(n_out, kThreads))),
-                dim3(kThreads), 0, s, partial, out, chunks, inner, n_out);
-    return EHIP_OK;
+    if (outer > 65535) return fail(EHIP_EINVAL, "sum_axis: outer %lld > 65535", (long long)outer);
+    return column_sums(x, outer, axis_len, inner, inner, axis_len * inner, out, s);
 }
 
 int ehip_reduce_sum_f32(const float* x, int64_t n, int squares, double* out_d, float* out_f,

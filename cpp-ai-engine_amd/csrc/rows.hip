@@ -435,19 +435,6 @@ __global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows_backward(
     }
 }
 
-// dgamma[c] = sum over groups of partial[g][0][c], groups ascending; dbeta likewise.
-__global__ __launch_bounds__(256) void layernorm_reduce_partials(const float* __restrict__ partial,
-                                                                 float* __restrict__ dgamma,
-                                                                 float* __restrict__ dbeta,
-                                                                 int64_t groups, int64_t cols) {
-    const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (e >= 2 * cols) return;
-    const int64_t which = e / cols, c = e % cols;
-    float acc = 0.0f;
-    for (int64_t g = 0; g < groups; ++g) acc += partial[(g * 2 + which) * cols + c];
-    (which == 0 ? dgamma : dbeta)[c] = acc;
-}
-
 // ------------------------------------------------------------ dispatch
 
 unsigned row_grid(int64_t rows, int per_block) {
@@ -704,10 +691,8 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
     else if (cols <= 4096) EHIP_LNB(256, 16);
     else EHIP_LNB(256, 32);
 #undef EHIP_LNB
-    EHIP_LAUNCH("layernorm_backward_reduce", layernorm_reduce_partials,
-                dim3(unsigned(ceil_div(2 * cols, 256))), dim3(256), 0, s, partial, dgamma, dbeta,
-                groups, cols);
-    return EHIP_OK;
+    if (int rc = column_sums(partial, 1, groups, cols, 2 * cols, 0, dgamma, s)) return rc;
+    return column_sums(partial + cols, 1, groups, cols, 2 * cols, 0, dbeta, s);
 }
 
 }  // extern "C"

@@ -153,19 +153,19 @@ void release_cache(Arena& a) {
 
 }  // namespace
 
-void* scratch(size_t bytes) {
+void* scratch(size_t bytes, int slot) {
     static std::mutex mu;
-    static void* buf = nullptr;
-    static size_t cap = 0;
+    static void* buf[kScratchSlots] = {};
+    static size_t cap[kScratchSlots] = {};
     std::lock_guard<std::mutex> lock(mu);
-    if (bytes <= cap) return buf;
-    size_t want = cap * 2 > bytes ? cap * 2 : bytes;
+    if (bytes <= cap[slot]) return buf[slot];
+    const size_t want = cap[slot] * 2 > bytes ? cap[slot] * 2 : bytes;
     void* p = nullptr;
     if (ehip_arena_alloc(want, &p) != EHIP_OK) return nullptr;
-    if (buf != nullptr) ehip_arena_free(buf);
-    buf = p;
-    cap = want;
-    return buf;
+    if (buf[slot] != nullptr) ehip_arena_free(buf[slot]);
+    buf[slot] = p;
+    cap[slot] = want;
+    return p;
 }
 
 }  // namespace ehip
@@ -311,6 +311,8 @@ void ehip_arena_stats(ehip_arena_stats_t* out) {
     *out = a.stats;
 }
 
+}  // extern "C"
+
 namespace {
 
 // Host-to-device uploads up to a quarter of the ring go through a pinned
@@ -412,6 +414,8 @@ int copy(void* dst, const void* src, size_t bytes, void* stream, hipMemcpyKind k
 }
 
 }  // namespace
+
+extern "C" {
 
 int ehip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
     return copy(dst, src, bytes, stream, hipMemcpyHostToDevice);

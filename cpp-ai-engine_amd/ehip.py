@@ -28,6 +28,11 @@ def window(n, c, h, w, kh, kw, stride, pad):
                   (w + 2 * pad - kw) // stride + 1)
 
 
+class AdamTensor(C.Structure):
+    _fields_ = [("p", C.c_void_p), ("g", C.c_void_p), ("m", C.c_void_p), ("v", C.c_void_p),
+                ("n", C.c_int64)]
+
+
 class DeviceInfo(C.Structure):
     _fields_ = [("name", C.c_char * 256), ("arch", C.c_char * 64), ("compute_units", C.c_int),
                 ("clock_khz", C.c_int), ("memory_clock_khz", C.c_int),
@@ -70,6 +75,7 @@ _SIGS = {
     "ehip_scale_f32": [_vp, _i64, _f, _vp],
     "ehip_sgd_f32": [_vp, _vp, _vp, _i64, _f, _f, _f, _vp],
     "ehip_adam_f32": [_vp, _vp, _vp, _vp, _i64] + [_f] * 7 + [_vp],
+    "ehip_adam_multi_f32": [C.POINTER(AdamTensor), _i] + [_f] * 7 + [_vp],
     "ehip_permute_f32": [_vp, _vp, _i, C.POINTER(_i64), C.POINTER(_i64), _vp],
     "ehip_transpose_f32": [_vp, _vp, _i64, _i64, _i64, _vp],
     "ehip_im2col_f32": [_vp, _vp, C.POINTER(Window), _vp],
@@ -231,6 +237,14 @@ class Backend:
     def adam(self, p, g, m, v, lr, b1, b2, eps, wd, c1, c2):
         self.ok(self.lib.ehip_adam_f32(self.p(p), self.p(g), self.p(m), self.p(v), p.numel(), lr,
                                        b1, b2, eps, wd, c1, c2, self.stream()), "adam")
+
+    def adam_multi(self, groups, lr, b1, b2, eps, wd, c1, c2):
+        """groups: list of (p, g, m, v) device tensors."""
+        arr = (AdamTensor * len(groups))(*[
+            AdamTensor(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel())
+            for p, g, m, v in groups])
+        self.ok(self.lib.ehip_adam_multi_f32(arr, len(groups), lr, b1, b2, eps, wd, c1, c2,
+                                             self.stream()), "adam_multi")
 
     # ---------------------------------------------------------- layout
     def permute(self, x, order):

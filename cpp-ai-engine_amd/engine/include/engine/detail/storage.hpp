@@ -42,6 +42,10 @@ public:
     std::vector<float>& host_mut();
 
     bool resident_on_device() const noexcept;
+    // True when no other Storage shares this buffer. The engine mutates a
+    // buffer in place only when it is exclusive (gradient buffers may be
+    // shared after add_grad adopts a temporary).
+    bool exclusive() const noexcept;
     // True while the buffer is a pending fill of zeros: add_grad uses it to
     // initialise a zeroed gradient without materialising the zeros first.
     bool pending_zero() const noexcept;

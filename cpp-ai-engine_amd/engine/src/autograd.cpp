@@ -63,9 +63,15 @@ void backward(Tensor& root_tensor) {
         if (node != root && node->backward_fn) node->grad = nullptr;
     for (auto it = order.rbegin(); it != order.rend(); ++it) {
         const auto& node = *it;
-        if (node->backward_fn && node->grad) {
+        if (!node->backward_fn || !node->grad) continue;
+        if (node == root) {
             node->backward_fn(Tensor::from_impl(node->grad));
-            if (node != root) node->grad = nullptr;
+        } else {
+            // The gradient is handed over, not shared: inside backward_fn it is
+            // referenced only by the argument, so add_grad can adopt its buffer.
+            const Tensor g = Tensor::from_impl(std::move(node->grad));
+            node->grad = nullptr;
+            node->backward_fn(g);
         }
     }
 }

@@ -48,6 +48,11 @@ inline BroadcastPlan plan_broadcast(const std::vector<size_t>& base,
 }
 
 inline const float* dptr(const Tensor& t) { return t.storage().device(); }
+
+// add_grad of g into `target`, where g has the target's element count but may
+// carry another shape (the backward of a reshape): g's buffer is adopted under
+// the target's shape when nothing else references it. Defined in tensor.cpp.
+void add_grad_reshaped(Tensor& target, const Tensor& g);
 inline float* dout(Tensor& t) { return t.storage().device_write(); }
 
 // A tensor viewing `src` with a new shape (no copy).

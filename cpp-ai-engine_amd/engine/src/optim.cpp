@@ -61,22 +61,26 @@ void Adam::step() {
     ++t_;
     const float bias_c1 = 1.0f - std::pow(beta1_, static_cast<float>(t_));
     const float bias_c2 = 1.0f - std::pow(beta2_, static_cast<float>(t_));
+    // Every parameter in one multi-tensor launch; the arithmetic per element is
+    // the single-tensor update's.
+    std::vector<ehip_adam_tensor_t> table;
+    table.reserve(params_.size());
     for (size_t i = 0; i < params_.size(); ++i) {
         Tensor& p = params_[i];
         if (!p.requires_grad() || !p.has_grad()) continue;
         const Tensor g = p.grad();
-        hip::check(ehip_adam_f32(p.storage().device_mut(), dptr(g), m_[i].device_mut(),
-                                 v_[i].device_mut(), int64_t(p.size()), lr_, beta1_, beta2_, eps_,
-                                 weight_decay_, bias_c1, bias_c2, nullptr),
-                   "adam step");
+        table.push_back({p.storage().device_mut(), dptr(g), m_[i].device_mut(), v_[i].device_mut(),
+                         int64_t(p.size())});
     }
+    hip::check(ehip_adam_multi_f32(table.data(), int(table.size()), lr_, beta1_, beta2_, eps_,
+                                   weight_decay_, bias_c1, bias_c2, nullptr),
+               "adam step");
 }
 
 // src/optim.cpp:168-208: the norm needs one host read (it decides whether to scale).
 float clip_grad_norm(const std::vector<Tensor>& parameters, float max_norm) {
     if (max_norm <= 0.0f) throw std::invalid_argument("clip_grad_norm needs a positive max_norm.");
     autograd::NoGradGuard no_grad;
-    std::vector<double*> partials;
     void* block = nullptr;
     hip::check(ehip_arena_alloc(parameters.size() * sizeof(double) + 8, &block), "clip alloc");
     double* d = static_cast<double*>(block);
@@ -99,6 +103,7 @@ float clip_grad_norm(const std::vector<Tensor>& parameters, float max_norm) {
         for (const Tensor& p : parameters) {
             if (!p.has_grad()) continue;
             Tensor g = p.grad();
+            if (!g.storage().exclusive()) g.storage() = g.storage().clone();
             hip::check(ehip_scale_f32(g.storage().device_mut(), int64_t(g.size()), scale, nullptr),
                        "clip scale");
         }

@@ -112,6 +112,8 @@ std::vector<float>& Storage::host_mut() {
 
 bool Storage::resident_on_device() const noexcept { return buf_ && buf_->device_valid; }
 
+bool Storage::exclusive() const noexcept { return buf_ && buf_.use_count() == 1; }
+
 bool Storage::pending_zero() const noexcept {
     return buf_ && buf_->pending && buf_->fill_value == 0.0f &&
            !buf_->device_valid && !buf_->host_valid;

@@ -115,23 +115,66 @@ Tensor Tensor::grad() const {
 bool Tensor::has_grad() const { return impl_->grad != nullptr; }
 
 // Lazy: the next add_grad initialises the zeroed gradient without a fill
-// (src/tensor.cpp:157-166 assigns zeros without copying either).
+// (src/tensor.cpp:157-166 assigns zeros without copying either). A shared
+// gradient buffer is replaced rather than zeroed, so no other holder sees it.
 void Tensor::zero_grad() {
-    if (impl_->grad) impl_->grad->storage.assign(0.0f);
+    if (!impl_->grad) return;
+    Storage& s = impl_->grad->storage;
+    if (s.exclusive())
+        s.assign(0.0f);
+    else
+        s = Storage(s.size(), 0.0f);
 }
 
 // The first write is 0 + g, later writes grad += g (src/tensor.cpp:168-203).
+//
+// A first write from a temporary that nothing else references adopts its
+// buffer instead of copying it (every gradient edge of the backward pass is
+// such a temporary); the only difference from 0 + g is that a -0.0 element
+// stays -0.0. Accumulating into a buffer that is still shared writes the sum
+// into a fresh buffer (copy on write), so adopted buffers are never mutated
+// under another holder.
 void Tensor::add_grad(const Tensor& g) {
     if (!requires_grad()) return;
     if (g.shape() != shape())
         throw std::invalid_argument("Gradient shape " + g.shape_str() +
                                     " incompatible with the tensor's " + shape_str() + ".");
+    detail::add_grad_reshaped(*this, g);
+}
+
+void detail::add_grad_reshaped(Tensor& target, const Tensor& g) {
+    const std::shared_ptr<TensorImpl>& impl_ = target.get_impl();
+    if (!impl_->requires_grad) return;
+    if (g.size() != target.size())
+        throw std::invalid_argument("Gradient of " + std::to_string(g.size()) +
+                                    " elements for a tensor of " + std::to_string(target.size()) +
+                                    ".");
+    const std::vector<size_t>& shape = impl_->shape;
+    const size_t n = target.size();
     const bool initialize = !impl_->grad || impl_->grad->storage.pending_zero();
-    if (!impl_->grad) impl_->grad = std::make_shared<TensorImpl>(shape(), 0.0f, false);
+    if (initialize && g.get_impl().use_count() == 1 && g.storage().exclusive() &&
+        g.storage().resident_on_device()) {
+        if (!impl_->grad) {
+            impl_->grad = std::make_shared<TensorImpl>();
+            impl_->grad->shape = shape;
+            impl_->grad->compute_strides();
+        }
+        impl_->grad->storage = g.storage().share();
+        return;
+    }
+    if (!impl_->grad) impl_->grad = std::make_shared<TensorImpl>(shape, 0.0f, false);
     Storage& acc = impl_->grad->storage;
     const float* src = g.storage().device();
+    if (!initialize && !acc.exclusive()) {
+        Storage sum(acc.size(), 0.0f);
+        hip::check(ehip_binary_f32(EHIP_ADD, acc.device(), src, sum.device_write(), int64_t(n), 1,
+                                   nullptr),
+                   "add_grad");
+        acc = sum;
+        return;
+    }
     float* dst = initialize ? acc.device_write() : acc.device_mut();
-    hip::check(ehip_accumulate_grad_f32(dst, src, int64_t(size()), initialize ? 1 : 0, nullptr),
+    hip::check(ehip_accumulate_grad_f32(dst, src, int64_t(n), initialize ? 1 : 0, nullptr),
                "add_grad");
 }
 

@@ -42,8 +42,11 @@ void attach(Tensor& res, std::vector<std::shared_ptr<TensorImpl>> parents,
     res.get_impl()->backward_fn = std::move(fn);
 }
 
-Tensor reduce_to(const Tensor& d, const Tensor& target) {
-    return d.shape() == target.shape() ? d : fold_leading(d, target.shape());
+// By value, so that a temporary passed in is moved through and stays the only
+// handle on its buffer (add_grad then adopts it instead of copying).
+Tensor reduce_to(Tensor d, const Tensor& target) {
+    if (d.shape() == target.shape()) return d;
+    return fold_leading(d, target.shape());
 }
 
 // The batch geometry of a product: 2-D operands are shared across the batch.
@@ -96,15 +99,20 @@ Tensor Tensor::operator+(const Tensor& other) const {
     if (track(requires_grad() || other.requires_grad())) {
         Tensor self_copy = *this, other_copy = other;
         attach(res, {impl_, other.impl_}, [self_copy, other_copy](const Tensor& g) mutable {
-            // Both operand gradients fresh and the same shape: one fused pass
-            // hands g to both (it equals two add_grad calls bit for bit).
+            // When g's buffer can be adopted, the first operand takes it and the
+            // second gets a copy (8 bytes per element). Otherwise, for two
+            // same-shape operands, one fused pass writes both (12 bytes per
+            // element instead of 16); it equals two add_grad calls bit for bit.
             const bool same = self_copy.shape() == other_copy.shape();
             auto& sg = self_copy.get_impl()->grad;
             auto& og = other_copy.get_impl()->grad;
-            if (same && self_copy.requires_grad() && other_copy.requires_grad() &&
-                self_copy.get_impl() != other_copy.get_impl()) {
-                const bool init_a = !sg || sg->storage.pending_zero();
-                const bool init_b = !og || og->storage.pending_zero();
+            const bool init_a = !sg || sg->storage.pending_zero();
+            const bool init_b = !og || og->storage.pending_zero();
+            const bool adoptable = g.get_impl().use_count() == 1 && g.storage().exclusive() &&
+                                   init_a && self_copy.requires_grad();
+            if (!adoptable && same && self_copy.requires_grad() && other_copy.requires_grad() &&
+                self_copy.get_impl() != other_copy.get_impl() &&
+                (init_a || sg->storage.exclusive()) && (init_b || og->storage.exclusive())) {
                 if (!sg) sg = std::make_shared<TensorImpl>(self_copy.shape(), 0.0f, false);
                 if (!og) og = std::make_shared<TensorImpl>(other_copy.shape(), 0.0f, false);
                 const float* src = dptr(g);
@@ -365,9 +373,8 @@ Tensor Tensor::reshape(const std::vector<size_t>& new_shape) const {
     Tensor res = view_with_shape(impl_->storage, new_shape, false);
     if (req_g) {
         Tensor self_copy = *this;
-        attach(res, {impl_}, [self_copy](const Tensor& g) mutable {
-            self_copy.add_grad(g.reshape(self_copy.shape()));
-        });
+        attach(res, {impl_},
+               [self_copy](const Tensor& g) mutable { add_grad_reshaped(self_copy, g); });
     }
     return res;
 }

@@ -206,6 +206,24 @@ int ehip_adam_f32(float* p, const float* g, float* m, float* v, int64_t n, float
                   float beta2, float eps, float weight_decay, float bias_c1, float bias_c2,
                   void* stream);
 
+/* One parameter tensor of a multi-tensor Adam step (DEVICE pointers). */
+typedef struct {
+    float* p;
+    const float* g;
+    float* m;
+    float* v;
+    int64_t n;
+} ehip_adam_tensor_t;
+
+/* The Adam update of ehip_adam_f32 applied to `count` tensors in ONE launch:
+ * `tensors` is a HOST array (copied to the device, stream-ordered, before the
+ * call returns). Element for element the same arithmetic as ehip_adam_f32,
+ * so bit-exact with src/optim.cpp:147-160. Replaces the per-parameter loop of
+ * Adam::step (src/optim.cpp:122-161), which launches once per parameter. */
+int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, float beta1,
+                        float beta2, float eps, float weight_decay, float bias_c1,
+                        float bias_c2, void* stream);
+
 /* ------------------------------------------------------ layout and index maps */
 
 /* out[flat] = x[sum_d coord_d(flat, out_shape) * src_strides[d]], ndim <= 8.

@@ -189,6 +189,40 @@ def test_adam_trajectory_exact(hip, orc, n):
     exact(host(V), v, "v")
 
 
+def test_adam_multi_exact(hip, orc):
+    """One launch over tensors of ragged sizes (tails, chunk boundaries, an unaligned view)
+    equals the per-tensor update bit for bit."""
+    print_case("adam-multi")
+    import torch
+    r = rng(44)
+    sizes = [1, 3, 4, 4096, 4097, 12289, 100003]
+    host = [[randn(r, n), randn(r, n), np.zeros(n, np.float32), np.zeros(n, np.float32)]
+            for n in sizes]
+    devs = [[dev(a) for a in t] for t in host]
+    # an unaligned view: element 1 of a larger buffer
+    big = [dev(randn(r, 1001)), dev(randn(r, 1001)), dev(np.zeros(1001, np.float32)),
+           dev(np.zeros(1001, np.float32))]
+    views = [b[1:] for b in big]
+    vhost = [host_of(b)[1:].copy() for b in big]
+    for t in range(1, 4):
+        c1, c2 = orc.adam_bias(0.9, 0.999, t)
+        for h in host + [vhost]:
+            orc.adam(h[0], h[1], h[2], h[3], 1e-3, 0.9, 0.999, 1e-8, 0.0, c1, c2)
+        hip.adam_multi([tuple(d) for d in devs] + [tuple(views)], 1e-3, 0.9, 0.999, 1e-8, 0.0,
+                       c1, c2)
+    for h, d in zip(host, devs):
+        exact(host_of(d[0]), h[0], "p")
+        exact(host_of(d[2]), h[2], "m")
+        exact(host_of(d[3]), h[3], "v")
+    exact(host_of(views[0]), vhost[0], "unaligned p")
+
+
+def host_of(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
 def test_sgd_exact(hip, orc):
     print_case("sgd")
     r = rng(3)
