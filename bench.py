@@ -104,6 +104,20 @@ class Timer:
         torch.cuda.synchronize()
         return start.elapsed_time(stop) * 1e-3 / steps  # seconds per call
 
+    def time_batch(self, enqueue, reps, warmup):
+        """enqueue(n) puts n launches on the stream from native code in one call, so the
+        events see back-to-back kernels rather than Python's launch gaps."""
+        torch = self.torch
+        enqueue(warmup)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        enqueue(reps)
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) * 1e-3 / reps
+
 
 def roofline(name, bound, work, seconds, traffic=None):
     if bound == "hbm":
@@ -144,7 +158,7 @@ def headline(engine_mod, timer, steps, warmup):
     return sec, first, last
 
 
-def dominant_kernel(hip, timer, torch):
+def dominant_kernel(eng, timer, torch):
     """The CNN step's largest kernel by total time (rocprofv3 --kernel-trace --stats of
     this benchmark, profiles/cnn_step_kernels.md): the conv1 weight-gradient product
     dW = g^T cols, g (50176 x 8), cols (50176 x 9), a K = 50176 split-K GEMM that streams
@@ -154,7 +168,7 @@ def dominant_kernel(hip, timer, torch):
     g = torch.randn(50176, 8, device="cuda", generator=r)
     cols = torch.randn(50176, 9, device="cuda", generator=r)
     out = torch.empty(8, 9, device="cuda")
-    sec = timer.time(lambda: hip.gemm(g, cols, c=out, trans_a=True), 200, 20)
+    sec = timer.time_batch(lambda n: eng.repeat_gemm(n, g, cols, out, trans_a=True), 500, 50)
     work = 4 * (50176 * 8 + 50176 * 9 + 8 * 9)
     return roofline("gemm_kernel<64,64,16,32,32,TA>+splitk_reduce (conv1 dW, 8x9x50176)",
                     "hbm", work, sec, committed_traffic("conv1_dw"))
@@ -181,7 +195,7 @@ def cpu_baseline(seconds_target):
                       f"-march) on {threads} host threads, {dt:.1f} s"}
 
 
-def extras(hip, engine_mod, timer, torch):
+def extras(hip, eng, engine_mod, timer, torch):
     out = {}
     # cfg 1: C = A B and both backward products at 512^3 (805.3 MFLOP per trio), and 4096^3.
     for n in (512, 4096):
@@ -192,11 +206,11 @@ def extras(hip, engine_mod, timer, torch):
         c, da, db = (torch.empty(n, n, device="cuda") for _ in range(3))
         fl = 2.0 * n ** 3
         modes = {
-            "fwd C=AB": lambda: hip.gemm(a, b, c=c),
-            "bwd dA=dC B^T": lambda: hip.gemm(dc, b, c=da, trans_b=True),
-            "bwd dB=A^T dC": lambda: hip.gemm(a, dc, c=db, trans_a=True),
+            "fwd C=AB": lambda r: eng.repeat_gemm(r, a, b, c),
+            "bwd dA=dC B^T": lambda r: eng.repeat_gemm(r, dc, b, da, trans_b=True),
+            "bwd dB=A^T dC": lambda r: eng.repeat_gemm(r, a, dc, db, trans_a=True),
         }
-        sec = {k: timer.time(f, 20 if n == 4096 else 200, 3 if n == 4096 else 20)
+        sec = {k: timer.time_batch(f, 20 if n == 4096 else 500, 3 if n == 4096 else 50)
                for k, f in modes.items()}
         total = sum(sec.values())
         out[f"gemm_{n}^3"] = {
@@ -235,7 +249,6 @@ def extras(hip, engine_mod, timer, torch):
     out["bandwidth_cfg4"] = bw
     torch.cuda.empty_cache()
     # cfg 3 and cfg 5: Transformer training steps.
-    eng = engine_mod.Engine()
     for tag, (b, s, vocab, d, h, ff, layers, steps, warm) in {
             "charlm_cfg3": (32, 64, 121, 96, 4, 384, 2, 100, 10),
             "transformer_cfg5": (16, 512, 256, 1024, 16, 4096, 12, 5, 2)}.items():
@@ -272,13 +285,14 @@ def main():
     import engine_capi
     import ehip
     hip = ehip.Backend()
+    eng = engine_capi.Engine()
     timer = Timer(torch)
 
     log("bench: cfg2 CNN training step")
     sec, first, last = headline(engine_capi, timer, args.steps, args.warmup)
     log(f"bench: {sec * 1e3:.4f} ms/step, loss {first:.5f} -> {last:.5f}")
     log("bench: dominant kernel")
-    roof = dominant_kernel(hip, timer, torch)
+    roof = dominant_kernel(eng, timer, torch)
     cpu = None
     if not args.no_cpu:
         log("bench: reference CPU baseline")
@@ -286,7 +300,7 @@ def main():
     extra = None
     if not args.no_extra:
         log("bench: other configurations")
-        extra = extras(hip, engine_capi, timer, torch)
+        extra = extras(hip, eng, engine_capi, timer, torch)
     info = hip.device_info()
     line = {
         "metric": metric_name(),

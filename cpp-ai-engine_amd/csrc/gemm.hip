@@ -27,239 +27,12 @@
 // shape. It is not bit-equal to the reference's serial i-k-j loop
 // (src/tensor_ops.cpp:539-562); the parity tests bound the difference.
 
-#include "common.hpp"
+#include "gemm_kernel.hpp"
 
 namespace ehip {
 namespace {
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
-struct GemmArgs {
-    const float* a;
-    const float* b;
-    float* c;  // the output, or the split-K workspace
-    int64_t m, n, k;
-    int64_t lda, ldb, ldc;
-    int64_t stride_a, stride_b, stride_c;
-    float beta;
-    int tiles_m, tiles_n;
-    int splits;        // K is cut into `splits` chunks of k_chunk (a multiple of BK)
-    int64_t k_chunk;
-};
-
-template <int BM, int BN, int BK, int WM, int WN>
-struct Cfg {
-    static constexpr int kWavesM = BM / WM, kWavesN = BN / WN;
-    static constexpr int kThreads = kWavesM * kWavesN * 64;
-    static constexpr int kFM = WM / 32, kFN = WN / 32;
-    static constexpr int kLdsA = BM + 4;  // row pitch of the [k][m] A buffer
-    static constexpr int kLdsB = BN + 4;
-    static constexpr int kA4 = BM * BK / 4;  // float4 loads per tile
-    static constexpr int kB4 = BN * BK / 4;
-    static constexpr int kALoads = (kA4 + kThreads - 1) / kThreads;
-    static constexpr int kBLoads = (kB4 + kThreads - 1) / kThreads;
-    static_assert(BM % WM == 0 && BN % WN == 0 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
-    static_assert(BK % 4 == 0, "BK");
-};
-
-// Loads a BM x BK tile of op(A) into registers. TA: A is stored K x M.
-// CHECK: zero-fill outside the matrix and use scalar loads.
-template <class C, int BM, int BK, bool TRANS, bool CHECK>
-__device__ __forceinline__ void load_tile(const float* __restrict__ p, int64_t ld, int64_t rows,
-                                          int64_t kdim, int64_t r0, int64_t k0, float4* reg,
-                                          int loads, int total) {
-#pragma unroll
-    for (int i = 0; i < loads; ++i) {
-        const int q = threadIdx.x + i * C::kThreads;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (q < total) {
-            int64_t r, kk;
-            if (!TRANS) {  // stored rows x K, 4 consecutive k
-                r = r0 + q / (BK / 4);
-                kk = k0 + 4 * (q % (BK / 4));
-                const float* src = p + r * ld + kk;
-                if (!CHECK) {
-                    v = *reinterpret_cast<const float4*>(src);
-                } else if (r < rows) {
-                    v.x = kk < kdim ? src[0] : 0.f;
-                    v.y = kk + 1 < kdim ? src[1] : 0.f;
-                    v.z = kk + 2 < kdim ? src[2] : 0.f;
-                    v.w = kk + 3 < kdim ? src[3] : 0.f;
-                }
-            } else {  // stored K x rows, 4 consecutive rows
-                kk = k0 + q / (BM / 4);
-                r = r0 + 4 * (q % (BM / 4));
-                const float* src = p + kk * ld + r;
-                if (!CHECK) {
-                    v = *reinterpret_cast<const float4*>(src);
-                } else if (kk < kdim) {
-                    v.x = r < rows ? src[0] : 0.f;
-                    v.y = r + 1 < rows ? src[1] : 0.f;
-                    v.z = r + 2 < rows ? src[2] : 0.f;
-                    v.w = r + 3 < rows ? src[3] : 0.f;
-                }
-            }
-        }
-        reg[i] = v;
-    }
-}
-
-// Stores the registers of load_tile into an LDS buffer laid out [k][row].
-template <class C, int BM, int BK, int LDS, bool TRANS>
-__device__ __forceinline__ void store_tile(float* __restrict__ s, const float4* reg, int loads,
-                                           int total) {
-#pragma unroll
-    for (int i = 0; i < loads; ++i) {
-        const int q = threadIdx.x + i * C::kThreads;
-        if (q < total) {
-            if (!TRANS) {
-                const int r = q / (BK / 4), kk = 4 * (q % (BK / 4));
-                s[(kk + 0) * LDS + r] = reg[i].x;
-                s[(kk + 1) * LDS + r] = reg[i].y;
-                s[(kk + 2) * LDS + r] = reg[i].z;
-                s[(kk + 3) * LDS + r] = reg[i].w;
-            } else {
-                const int kk = q / (BM / 4), r = 4 * (q % (BM / 4));
-                *reinterpret_cast<float4*>(s + kk * LDS + r) = reg[i];
-            }
-        }
-    }
-}
-
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool CHECK>
-__global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kernel(GemmArgs g) {
-    using C = Cfg<BM, BN, BK, WM, WN>;
-    __shared__ float lds_a[2][BK * C::kLdsA];
-    __shared__ float lds_b[2][BK * C::kLdsB];
-
-    // Tile coordinates: XCD-contiguous renumbering, then GROUP_M-row groups.
-    const int tiles = g.tiles_m * g.tiles_n;
-    int bid = blockIdx.x;
-    if (tiles % 8 == 0) bid = (bid % 8) * (tiles / 8) + bid / 8;
-    constexpr int kGroupM = 8;
-    const int group = bid / (kGroupM * g.tiles_n);
-    const int first_m = group * kGroupM;
-    const int gsz = min(g.tiles_m - first_m, kGroupM);
-    const int in_group = bid % (kGroupM * g.tiles_n);
-    const int tm = first_m + in_group % gsz;
-    const int tn = in_group / gsz;
-
-    const int split = blockIdx.y;
-    const int64_t batch = blockIdx.z;
-    const float* A = g.a + batch * g.stride_a;
-    const float* B = g.b + batch * g.stride_b;
-    const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
-    const int64_t k_begin = int64_t(split) * g.k_chunk;
-    int64_t k_end = k_begin + g.k_chunk;
-    if (k_end > g.k) k_end = g.k;
-
-    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-    const int wm0 = (wave / C::kWavesN) * WM, wn0 = (wave % C::kWavesN) * WN;
-
-    floatx16 acc[C::kFM][C::kFN];
-#pragma unroll
-    for (int i = 0; i < C::kFM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::kFN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    float4 ra[C::kALoads], rb[C::kBLoads];
-    const int64_t steps = (k_end - k_begin + BK - 1) / BK;
-    if (steps > 0) {
-        load_tile<C, BM, BK, TA, CHECK>(A, g.lda, g.m, k_end, m0, k_begin, ra, C::kALoads, C::kA4);
-        load_tile<C, BN, BK, !TB, CHECK>(B, g.ldb, g.n, k_end, n0, k_begin, rb, C::kBLoads, C::kB4);
-        store_tile<C, BM, BK, C::kLdsA, TA>(lds_a[0], ra, C::kALoads, C::kA4);
-        store_tile<C, BN, BK, C::kLdsB, !TB>(lds_b[0], rb, C::kBLoads, C::kB4);
-        __syncthreads();
-    }
-    for (int64_t s = 0; s < steps; ++s) {
-        const int cur = int(s & 1);
-        const bool more = s + 1 < steps;
-        if (more) {
-            const int64_t kn = k_begin + (s + 1) * BK;
-            load_tile<C, BM, BK, TA, CHECK>(A, g.lda, g.m, k_end, m0, kn, ra, C::kALoads, C::kA4);
-            load_tile<C, BN, BK, !TB, CHECK>(B, g.ldb, g.n, k_end, n0, kn, rb, C::kBLoads,
-                                             C::kB4);
-        }
-        const float* sa = lds_a[cur];
-        const float* sb = lds_b[cur];
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 2) {
-            float fa[C::kFM], fb[C::kFN];
-            const int krow = kk + lane / 32;
-#pragma unroll
-            for (int i = 0; i < C::kFM; ++i) fa[i] = sa[krow * C::kLdsA + wm0 + 32 * i + lane % 32];
-#pragma unroll
-            for (int j = 0; j < C::kFN; ++j) fb[j] = sb[krow * C::kLdsB + wn0 + 32 * j + lane % 32];
-#pragma unroll
-            for (int i = 0; i < C::kFM; ++i)
-#pragma unroll
-                for (int j = 0; j < C::kFN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
-        }
-        if (more) {
-            store_tile<C, BM, BK, C::kLdsA, TA>(lds_a[cur ^ 1], ra, C::kALoads, C::kA4);
-            store_tile<C, BN, BK, C::kLdsB, !TB>(lds_b[cur ^ 1], rb, C::kBLoads, C::kB4);
-        }
-        __syncthreads();
-    }
-
-    // Epilogue. With splits > 1, c is the workspace [split][batch][m][n] and
-    // beta is applied by the reduction kernel.
-    float* Cp;
-    int64_t ldc;
-    if (g.splits > 1) {
-        Cp = g.c + (int64_t(split) * gridDim.z + batch) * g.m * g.n;
-        ldc = g.n;
-    } else {
-        Cp = g.c + batch * g.stride_c;
-        ldc = g.ldc;
-    }
-    const bool use_beta = g.splits == 1 && g.beta != 0.0f;
-#pragma unroll
-    for (int i = 0; i < C::kFM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::kFN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm0 + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-                const int64_t col = n0 + wn0 + 32 * j + lane % 32;
-                if (CHECK && (row >= g.m || col >= g.n)) continue;
-                float v = acc[i][j][r];
-                float* dst = Cp + row * ldc + col;
-                if (use_beta) v = v + g.beta * *dst;
-                *dst = v;
-            }
-}
-
-// C[b] = sum over splits (ascending) of W[s][b] (+ beta C[b]).
-__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w, float* c,
-                                                     int64_t m, int64_t n, int64_t ldc,
-                                                     int64_t stride_c, int64_t batch, int splits,
-                                                     float beta) {
-    const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t mn = m * n;
-    if (e >= mn * batch) return;
-    const int64_t b = e / mn, rc = e % mn;
-    const int64_t row = rc / n, col = rc % n;
-    // Splits ascending; the loads are issued eight at a time ahead of the adds.
-    const float* p = w + b * mn + rc;
-    const int64_t step = batch * mn;
-    float acc = p[0];
-    int s = 1;
-    for (; s + 8 <= splits; s += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = p[int64_t(s + u) * step];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc += v[u];
-    }
-    for (; s < splits; ++s) acc += p[int64_t(s) * step];
-    float* dst = c + b * stride_c + row * ldc + col;
-    if (beta != 0.0f) acc = acc + beta * *dst;
-    *dst = acc;
-}
+using namespace gemm_detail;
 
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
 int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
@@ -304,20 +77,39 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
     return EHIP_OK;
 }
 
+// Tile choice, largest first (measured on MI355X, fp32 MFMA):
+//   L  256 x 256 x 16, 8 waves of 128 x 64   ~135 TFLOP/s at 4096^3
+//   M  128 x 128 x 32, 8 waves of  64 x 32   ~120-130 on 8192 x 1024 x K
+//   S  128 x  64 x 32, 8 waves of  32 x 32   thin outputs (N = 64 attention products)
+//   T   64 x  64 x 16, 4 waves of  32 x 32   small problems
+// A tile size is taken when its grid fills the 256 CUs (with split-K where K
+// is long) and the padding it adds to the output stays small.
+double padding(int64_t m, int64_t n, int bm, int bn) {
+    return double(ceil_div(m, bm) * bm) * double(ceil_div(n, bn) * bn) / (double(m) * double(n)) - 1.0;
+}
+
 template <bool TA, bool TB>
-int gemm_modes(const GemmArgs& g, int64_t batch, hipStream_t s) {
-    // The unchecked kernels need whole tiles and 16-byte aligned float4 rows.
+int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s) {
+    // The unchecked kernels need whole tiles and 16-byte aligned float4 rows;
+    // the checked ones still load whole float4s away from the edges when the
+    // rows are aligned.
     const bool aligned = aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
                          g.stride_a % 4 == 0 && g.stride_b % 4 == 0;
-    // 128 x 128 tiles when the grid fills the chip, or when K is long enough
-    // for split-K to make up the difference; 64 x 64 otherwise.
-    const int64_t big_tiles = ceil_div(g.m, 128) * ceil_div(g.n, 128);
-    if (big_tiles * batch >= 192 || (big_tiles * batch >= 32 && g.k >= 2048)) {
-        const bool check = !(aligned && g.m % 128 == 0 && g.n % 128 == 0 && g.k % 16 == 0);
-        return launch_cfg<128, 128, 16, 64, 64, TA, TB>(g, batch, check, s);
-    }
-    const bool check = !(aligned && g.m % 64 == 0 && g.n % 64 == 0 && g.k % 16 == 0);
-    return launch_cfg<64, 64, 16, 32, 32, TA, TB>(g, batch, check, s);
+    g.vec = aligned ? 1 : 0;
+    const auto whole = [&](int bm, int bn, int bk) {
+        return aligned && g.m % bm == 0 && g.n % bn == 0 && g.k % bk == 0;
+    };
+    const int64_t tl = ceil_div(g.m, 256) * ceil_div(g.n, 256) * batch;
+    const int64_t tm = ceil_div(g.m, 128) * ceil_div(g.n, 128) * batch;
+    const int64_t ts = ceil_div(g.m, 128) * ceil_div(g.n, 64) * batch;
+    const bool long_k = g.k >= 2048;
+    if (tl >= 256 && padding(g.m, g.n, 256, 256) < 0.15 && g.k >= 256)
+        return launch_cfg<256, 256, 16, 128, 64, TA, TB>(g, batch, !whole(256, 256, 16), s);
+    if ((tm >= 128 || (tm >= 32 && long_k)) && padding(g.m, g.n, 128, 128) < 0.25)
+        return launch_cfg<128, 128, 32, 64, 32, TA, TB>(g, batch, !whole(128, 128, 32), s);
+    if ((ts >= 128 || (ts >= 32 && long_k)) && padding(g.m, g.n, 128, 64) < 0.25)
+        return launch_cfg<128, 64, 32, 32, 32, TA, TB>(g, batch, !whole(128, 64, 32), s);
+    return launch_cfg<64, 64, 16, 32, 32, TA, TB>(g, batch, !whole(64, 64, 16), s);
 }
 
 }  // namespace

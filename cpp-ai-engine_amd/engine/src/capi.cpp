@@ -474,6 +474,23 @@ int64_t eng_charlm_num_params(int64_t vocab, int64_t seq, int64_t d, int64_t hea
     return vocab * d + layers * eng_block_num_params(d, heads, ff) + d * vocab + vocab + 0 * seq;
 }
 
+// ------------------------------------------------------------------ timing
+
+// Enqueues `reps` back-to-back ehip_gemm_f32 calls on `stream` (device pointers,
+// the arguments of ehip_gemm_f32), so that a caller can time one kernel with
+// events around the whole batch without host launch overhead between calls.
+int eng_repeat_gemm(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n, int64_t k,
+                    const float* a, int64_t lda, int64_t stride_a, const float* b, int64_t ldb,
+                    int64_t stride_b, float beta, float* c, int64_t ldc, int64_t stride_c,
+                    void* stream, int reps) {
+    return guarded([&] {
+        for (int r = 0; r < reps; ++r)
+            engine::hip::check(ehip_gemm_f32(trans_a, trans_b, batch, m, n, k, a, lda, stride_a, b,
+                                             ldb, stride_b, beta, c, ldc, stride_c, stream),
+                               "gemm");
+    });
+}
+
 // ------------------------------------------------------------------ trainers
 
 void* eng_trainer_cnn(const float* x, const int64_t* labels, int64_t batch, int64_t in_c,

@@ -73,6 +73,21 @@ class Engine:
     def synchronize(self):
         self._ok(self.lib.eng_synchronize())
 
+    def repeat_gemm(self, reps, a, b, c, trans_a=False, trans_b=False, beta=0.0):
+        """Enqueues `reps` ehip_gemm_f32 calls from C++ on torch's current stream: a, b, c
+        are 2-D contiguous CUDA tensors, c = op(a) op(b) + beta c."""
+        import torch
+        am, ak = a.shape
+        m, k = (ak, am) if trans_a else (am, ak)
+        bk, bn = b.shape
+        n = bk if trans_b else bn
+        f = self.lib.eng_repeat_gemm
+        f.argtypes = [C.c_int, C.c_int] + [_i64] * 4 + [C.c_void_p, _i64, _i64] * 2 + [
+            C.c_float, C.c_void_p, _i64, _i64, C.c_void_p, C.c_int]
+        self._ok(f(int(trans_a), int(trans_b), 1, m, n, k, a.data_ptr(), a.shape[1], 0,
+                   b.data_ptr(), b.shape[1], 0, beta, c.data_ptr(), n, 0,
+                   torch.cuda.current_stream().cuda_stream, reps))
+
     def matmul(self, a, b):
         a, b = _f32(a), _f32(b)
         ab, bb = a.ndim > 2, b.ndim > 2
