@@ -174,6 +174,18 @@ def dominant_kernel(eng, timer, torch):
                     "hbm", work, sec, committed_traffic("conv1_dw"))
 
 
+def kernel_only(eng, hip, timer, torch):
+    """For counter runs: 100 launches of the dominant kernel, then 100 launches of the
+    gradient-initialise kernel over 16 Mi floats (reads 64 MiB, writes 64 MiB), the copy
+    of known size that scales FETCH_SIZE / WRITE_SIZE to bytes."""
+    roof = dominant_kernel(eng, timer, torch)
+    n = 1 << 24
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty(n, device="cuda")
+    sec = timer.time(lambda: hip.accumulate_grad(dst, src, True), 100, 0)
+    print(json.dumps({"dominant": roof, "copy_64MiB_us": round(sec * 1e6, 3)}), flush=True)
+
+
 def cpu_baseline(seconds_target):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from _oracle import Ref
@@ -273,6 +285,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="run only the dominant kernel and a copy kernel of known size (for "
+                         "rocprofv3 --pmc runs) and print their timings")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -287,6 +302,10 @@ def main():
     hip = ehip.Backend()
     eng = engine_capi.Engine()
     timer = Timer(torch)
+
+    if args.kernel_only:
+        kernel_only(eng, hip, timer, torch)
+        return
 
     log("bench: cfg2 CNN training step")
     sec, first, last = headline(engine_capi, timer, args.steps, args.warmup)

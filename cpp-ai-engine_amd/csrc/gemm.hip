@@ -69,10 +69,15 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
                     dim3(C::kThreads), 0, s, g);
     }
     if (splits > 1) {
+        // Split lanes: up to 16, about one per 8 splits, so that no lane chain
+        // is longer than ~8 loads deep when the outputs are few.
+        int rl = 1;
+        while (rl < 16 && rl * 8 < splits) rl *= 2;
         const int64_t total = batch * g.m * g.n;
-        EHIP_LAUNCH("gemm_splitk_reduce", splitk_reduce, dim3(unsigned(ceil_div(total, 256))),
-                    dim3(256), 0, s, g.c, out, g.m, g.n, g0.ldc, g0.stride_c, batch, splits,
-                    g0.beta);
+        const int64_t per_block = 256 / rl;
+        EHIP_LAUNCH("gemm_splitk_reduce", splitk_reduce,
+                    dim3(unsigned(ceil_div(total, per_block))), dim3(256), 0, s, g.c, out, g.m,
+                    g.n, g0.ldc, g0.stride_c, batch, splits, rl, g0.beta);
     }
     return EHIP_OK;
 }

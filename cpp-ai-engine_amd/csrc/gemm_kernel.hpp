@@ -212,34 +212,49 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
             }
 }
 
-// C[b] = sum over splits (ascending) of W[s][b] (+ beta C[b]).
+// C[b] = sum over splits of W[s][b] (+ beta C[b]). A block is RL split lanes x
+// (256 / RL) outputs: lane l adds splits l, l + RL, ... in order, then one
+// thread per output adds the RL lane sums in lane order. RL grows with the
+// number of splits, so a few outputs with many splits still spread over the
+// block instead of one long serial chain per output; the order depends only
+// on the shape.
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w, float* c,
                                                      int64_t m, int64_t n, int64_t ldc,
                                                      int64_t stride_c, int64_t batch, int splits,
-                                                     float beta) {
-    const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+                                                     int rl, float beta) {
+    __shared__ float lanes[256];
+    const int cw = 256 / rl;
+    const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
     const int64_t mn = m * n;
-    if (e >= mn * batch) return;
-    const int64_t b = e / mn, rc = e % mn;
-    const int64_t row = rc / n, col = rc % n;
-    // Splits ascending; the loads are issued eight at a time ahead of the adds.
-    const float* p = w + b * mn + rc;
+    const int64_t e = int64_t(blockIdx.x) * cw + cl;
     const int64_t step = batch * mn;
-    float acc = p[0];
-    int s = 1;
-    for (; s + 8 <= splits; s += 8) {
-        float v[8];
+    float acc = 0.0f;
+    if (e < step && lane < splits) {
+        const float* p = w + e + int64_t(lane) * step;
+        const int64_t stride = int64_t(rl) * step;
+        const int count = (splits - lane + rl - 1) / rl;
+        acc = p[0];
+        int s = 1;
+        for (; s + 8 <= count; s += 8) {
+            float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = p[int64_t(s + u) * step];
+            for (int u = 0; u < 8; ++u) v[u] = p[int64_t(s + u) * stride];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc += v[u];
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; s < count; ++s) acc += p[int64_t(s) * stride];
     }
-    for (; s < splits; ++s) acc += p[int64_t(s) * step];
-    float* dst = c + b * stride_c + row * ldc + col;
-    if (beta != 0.0f) acc = acc + beta * *dst;
-    *dst = acc;
+    lanes[threadIdx.x] = acc;
+    __syncthreads();
+    if (lane == 0 && e < step) {
+        float sum = lanes[cl];
+        for (int l = 1; l < rl && l < splits; ++l) sum += lanes[l * cw + cl];
+        const int64_t b = e / mn, rc = e % mn;
+        float* dst = c + b * stride_c + (rc / n) * ldc + rc % n;
+        if (beta != 0.0f) sum = sum + beta * *dst;
+        *dst = sum;
+    }
 }
-
 
 }  // namespace gemm_detail
 }  // namespace ehip

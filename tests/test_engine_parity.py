@@ -332,3 +332,39 @@ def test_charlm_training_trajectory(eng, orc, cpu):
     print("charlm loss rel err per step:", rel)
     assert np.all(rel <= 1e-5), rel
     assert np.max(np.abs(out - want_out)) <= steps * 1e-3 * 2
+
+
+def test_transformer_medium_trajectory(eng, orc, cpu):
+    """A deeper, wider stack than cfg 3 (4 pre-LN blocks, d 256, 8 heads, FFN 1024, context
+    128, vocab 256, batch 8), so the larger GEMM tiles and longer reductions of cfg 5 run
+    inside a training step; three Adam steps, per-step loss within 1e-5 relative."""
+    print_case("transformer medium")
+    r = rng(5)
+    vocab, d, heads, ff, layers, b, s = 256, 256, 8, 1024, 4, 8, 128
+    shapes = K.charlm_param_shapes(vocab, d, ff, layers)
+    params = []
+    for shp in shapes:
+        size = int(np.prod(shp))
+        if len(shp) == 1:
+            params.append(np.ones(size, np.float32) if len(params) % 2 == 1 else
+                          np.zeros(size, np.float32))
+        elif shp[0] == 1:
+            params.append(np.zeros(size, np.float32))
+        else:
+            lim = np.sqrt(6.0 / (shp[0] + shp[1]))
+            params.append(r.uniform(-lim, lim, size).astype(np.float32))
+    params = np.concatenate(params)
+    ids = r.integers(0, vocab, (b, s)).astype(np.float32)
+    targets = r.integers(0, vocab, b * s)
+    steps = 3 if cpu is not None else 1
+    losses, out = eng.charlm_train(ids, targets, vocab, d, heads, ff, layers, params, steps, 1e-3)
+    if cpu is not None:
+        want, want_out = cpu.charlm_train(ids, targets, vocab, d, heads, ff, layers, params,
+                                          steps, 1e-3)
+    else:
+        want, want_out = K.charlm_train(orc, ids, targets, params, vocab, d, heads, ff, layers,
+                                        steps, 1e-3)
+    rel = np.abs(losses - want) / np.abs(want)
+    print("medium loss", losses, "rel err", rel)
+    assert np.all(rel <= 1e-5), rel
+    assert np.max(np.abs(out - want_out)) <= steps * 1e-3 * 2

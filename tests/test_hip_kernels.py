@@ -60,7 +60,42 @@ def test_gemm_modes_vs_oracle(hip, orc, m, k, n, ta, tb):
     assert e_gpu <= 4.0 * e_cpu + 1e-7, (e_gpu, e_cpu)
 
 
-@pytest.mark.parametrize("m,k,n", [(37, 53, 29), (256, 512, 128), (9, 50176, 8)])
+# Shapes that select each tile configuration of the dispatcher (gemm.hip): the 256 x 256
+# tiles (grid >= 256 tiles), 128 x 128 x 32, 128 x 64 x 32 (thin, batched), each also with
+# ragged edges (the checked kernels) and split-K. The CPU oracle is too slow at these sizes,
+# so float64 is the arbiter, with the reference's K-scaled tolerance.
+TILE_CASES = [
+    ("L 256x256", 1, 4096, 256, 4096), ("L ragged", 1, 4100, 300, 4096),
+    ("M 128x128x32", 1, 2048, 512, 1024), ("M ragged", 1, 2050, 515, 1030),
+    ("M split-K", 1, 1024, 8192, 1024), ("S 128x64 batched", 32, 512, 512, 64),
+    ("S ragged batched", 16, 500, 77, 60), ("M batched K=64", 256, 512, 64, 512),
+]
+
+
+@pytest.mark.parametrize("name,batch,m,k,n", TILE_CASES)
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False)])
+def test_gemm_tile_configs_vs_fp64(hip, name, batch, m, k, n, ta, tb):
+    import torch
+    print_case("gemm-tiles", name, batch, m, k, n, ta, tb)
+    g = torch.Generator(device="cuda").manual_seed(m + n + k + batch)
+    a = torch.randn(batch, m, k, device="cuda", generator=g)
+    b = torch.randn(batch, k, n, device="cuda", generator=g)
+    a_st = a.transpose(1, 2).contiguous() if ta else a
+    b_st = b.transpose(1, 2).contiguous() if tb else b
+    got = hip.gemm(a_st if batch > 1 else a_st[0], b_st if batch > 1 else b_st[0], trans_a=ta,
+                   trans_b=tb)
+    want = torch.matmul(a.double(), b.double()).reshape(got.shape)
+    # The worst-case error of any fp32 summation order of K products is
+    # (K + 2) u sum_k |a_ik| |b_kj| (u = 2^-24): a bound every correct kernel meets, and one
+    # that a wrong index or a dropped term (an error of the size of the values) breaks.
+    bound = (k + 2) * 2.0 ** -24 * torch.matmul(a.double().abs(), b.double().abs()).reshape(
+        got.shape)
+    ratio = ((got.double() - want).abs() / bound.clamp(min=1e-30)).max().item()
+    assert ratio <= 1.0, f"{name}: error reaches {ratio:.3f} of the fp32 summation bound"
+
+
+@pytest.mark.parametrize("m,k,n", [(37, 53, 29), (256, 512, 128), (9, 50176, 8),
+                                   (4096, 64, 4096), (4096, 256, 4096)])
 def test_gemm_integer_inputs_exact(hip, m, k, n):
     """Small-integer operands: every partial sum is exact in fp32, so any summation order
     must give the exact product (tests/test_cuda_parity.cpp:344-363 of the reference)."""
@@ -68,7 +103,7 @@ def test_gemm_integer_inputs_exact(hip, m, k, n):
     r = rng(11)
     a = r.integers(-3, 4, (m, k)).astype(np.float32)
     b = r.integers(-3, 4, (k, n)).astype(np.float32)
-    want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)  # exact: |sums| < 2^53
     exact(host(hip.gemm(dev(a), dev(b))), want, "integer gemm")
 
 
