@@ -146,10 +146,12 @@ __global__ __launch_bounds__(kThreads) void col2im_kernel(const float* __restric
 }
 
 // One thread per output; the first strict maximum in window order wins
-// (src/conv.cpp:410-442).
+// (src/conv.cpp:410-442). Idx is int32_t, or float for the reference's float
+// argmax storage (exact for flat indices below 2^24).
+template <typename Idx>
 __global__ __launch_bounds__(kThreads) void maxpool_kernel(const float* __restrict__ x,
                                                            float* __restrict__ y,
-                                                           int32_t* __restrict__ argmax,
+                                                           Idx* __restrict__ argmax,
                                                            ehip_window_t w, int64_t n) {
     const int64_t step = int64_t(gridDim.x) * kThreads;
     for (int64_t o = int64_t(blockIdx.x) * kThreads + threadIdx.x; o < n; o += step) {
@@ -176,14 +178,15 @@ __global__ __launch_bounds__(kThreads) void maxpool_kernel(const float* __restri
             }
         }
         y[o] = best;
-        argmax[o] = static_cast<int32_t>(best_idx);
+        argmax[o] = static_cast<Idx>(best_idx);
     }
 }
 
 // One thread per input pixel: the gradients of the windows that chose it, in
 // output order from zero (src/conv.cpp:461-469 visits outputs ascending).
+template <typename Idx>
 __global__ __launch_bounds__(kThreads) void maxpool_backward_kernel(
-    const int32_t* __restrict__ argmax, const float* __restrict__ g, float* __restrict__ dx,
+    const Idx* __restrict__ argmax, const float* __restrict__ g, float* __restrict__ dx,
     ehip_window_t w, int64_t n) {
     const int64_t step = int64_t(gridDim.x) * kThreads;
     for (int64_t e = int64_t(blockIdx.x) * kThreads + threadIdx.x; e < n; e += step) {
@@ -198,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void maxpool_backward_kernel(
         for (int64_t oh = oh_lo; oh <= oh_hi; ++oh)
             for (int64_t ow = ow_lo; ow <= ow_hi; ++ow) {
                 const int64_t o = (plane * w.out_h + oh) * w.out_w + ow;
-                if (argmax[o] == e) acc += g[o];
+                if (argmax[o] == static_cast<Idx>(e)) acc += g[o];
             }
         dx[e] = acc;
     }
@@ -252,6 +255,39 @@ int check_window(const char* name, const ehip_window_t* w) {
     if (w->height + 2 * w->padding < w->kernel_h || w->width + 2 * w->padding < w->kernel_w ||
         oh != w->out_h || ow != w->out_w)
         return fail(EHIP_EINVAL, "%s: out_h/out_w do not match the window", name);
+    return EHIP_OK;
+}
+
+template <typename Idx>
+int maxpool_forward(const char* name, const float* x, float* y, Idx* argmax,
+                    const ehip_window_t* w, int64_t max_in, void* stream) {
+    EHIP_READY();
+    if (int rc = check_window(name, w)) return rc;
+    if (!x || !y || !argmax) return fail(EHIP_EINVAL, "%s: null pointer", name);
+    const int64_t n_in = w->batch * w->channels * w->height * w->width;
+    if (n_in > max_in)
+        return fail(EHIP_EINVAL, "%s: %lld input elements beyond exact indices (%lld)", name,
+                    (long long)n_in, (long long)max_in);
+    const int64_t n = w->batch * w->channels * w->out_h * w->out_w;
+    if (n == 0) return EHIP_OK;
+    EHIP_LAUNCH(name, maxpool_kernel<Idx>, dim3(grid_for(n)), dim3(kThreads), 0,
+                as_stream(stream), x, y, argmax, *w, n);
+    return EHIP_OK;
+}
+
+template <typename Idx>
+int maxpool_backward(const char* name, const Idx* argmax, const float* g, float* dx,
+                     const ehip_window_t* w, int64_t max_in, void* stream) {
+    EHIP_READY();
+    if (int rc = check_window(name, w)) return rc;
+    if (!argmax || !g || !dx) return fail(EHIP_EINVAL, "%s: null pointer", name);
+    const int64_t n = w->batch * w->channels * w->height * w->width;
+    if (n > max_in)
+        return fail(EHIP_EINVAL, "%s: %lld input elements beyond exact indices (%lld)", name,
+                    (long long)n, (long long)max_in);
+    if (n == 0) return EHIP_OK;
+    EHIP_LAUNCH(name, maxpool_backward_kernel<Idx>, dim3(grid_for(n)), dim3(kThreads), 0,
+                as_stream(stream), argmax, g, dx, *w, n);
     return EHIP_OK;
 }
 
@@ -333,29 +369,22 @@ int ehip_col2im_f32(const float* cols, float* x, const ehip_window_t* w, void* s
 
 int ehip_maxpool_f32(const float* x, float* y, int32_t* argmax, const ehip_window_t* w,
                      void* stream) {
-    EHIP_READY();
-    if (int rc = check_window("maxpool", w)) return rc;
-    if (!x || !y || !argmax) return fail(EHIP_EINVAL, "maxpool: null pointer");
-    const int64_t n_in = w->batch * w->channels * w->height * w->width;
-    if (n_in > 0x7fffffff) return fail(EHIP_EINVAL, "maxpool: input beyond int32 indices");
-    const int64_t n = w->batch * w->channels * w->out_h * w->out_w;
-    if (n == 0) return EHIP_OK;
-    EHIP_LAUNCH("maxpool", maxpool_kernel, dim3(grid_for(n)), dim3(kThreads), 0,
-                as_stream(stream), x, y, argmax, *w, n);
-    return EHIP_OK;
+    return maxpool_forward("maxpool", x, y, argmax, w, 0x7fffffff, stream);
 }
 
 int ehip_maxpool_backward_f32(const int32_t* argmax, const float* g, float* dx,
                               const ehip_window_t* w, void* stream) {
-    EHIP_READY();
-    if (int rc = check_window("maxpool_backward", w)) return rc;
-    if (!argmax || !g || !dx) return fail(EHIP_EINVAL, "maxpool_backward: null pointer");
-    const int64_t n = w->batch * w->channels * w->height * w->width;
-    if (n > 0x7fffffff) return fail(EHIP_EINVAL, "maxpool_backward: input beyond int32 indices");
-    if (n == 0) return EHIP_OK;
-    EHIP_LAUNCH("maxpool_backward", maxpool_backward_kernel, dim3(grid_for(n)), dim3(kThreads), 0,
-                as_stream(stream), argmax, g, dx, *w, n);
-    return EHIP_OK;
+    return maxpool_backward("maxpool_backward", argmax, g, dx, w, 0x7fffffff, stream);
+}
+
+int ehip_maxpool_fidx_f32(const float* x, float* y, float* argmax, const ehip_window_t* w,
+                          void* stream) {
+    return maxpool_forward("maxpool_fidx", x, y, argmax, w, int64_t(1) << 24, stream);
+}
+
+int ehip_maxpool_backward_fidx_f32(const float* argmax, const float* g, float* dx,
+                                   const ehip_window_t* w, void* stream) {
+    return maxpool_backward("maxpool_backward_fidx", argmax, g, dx, w, int64_t(1) << 24, stream);
 }
 
 int ehip_select_rows_f32(const float* x, const int32_t* idx, float* out, int64_t n_idx,

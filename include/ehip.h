@@ -260,6 +260,18 @@ int ehip_maxpool_f32(const float* x, float* y, int32_t* argmax, const ehip_windo
                      void* stream);
 int ehip_maxpool_backward_f32(const int32_t* argmax, const float* g, float* dx,
                               const ehip_window_t* w, void* stream);
+/* The same pair with the argmax stored as float, the layout of the reference's
+ * device path (a float Storage holding flat input indices: maxpool_windows and
+ * maxpool_windows_grad, src/cuda/kernels.cu:482-549, behind
+ * cuda_ops.hpp:116-118), so an
+ * adapter can hand over the reference's argmax Storage as is. Indices are
+ * exact below 2^24; larger inputs are refused with EHIP_EINVAL, as the
+ * reference's admission rule refuses inputs beyond 2^24 elements
+ * (src/cuda/kernels.cu:1100-1103). Bit-exact. */
+int ehip_maxpool_fidx_f32(const float* x, float* y, float* argmax, const ehip_window_t* w,
+                          void* stream);
+int ehip_maxpool_backward_fidx_f32(const float* argmax, const float* g, float* dx,
+                                   const ehip_window_t* w, void* stream);
 
 /* out[i] = x[idx[i]] row by row (rows of row_size floats); an index outside
  * [0, n_rows) yields a row of NaN instead of a read out of bounds.

@@ -317,15 +317,17 @@ def test_im2col_col2im_exact(hip, orc, shape, k, stride, pad):
 
 @pytest.mark.parametrize("shape,k,stride", [((64, 8, 28, 28), 2, 2), ((64, 16, 14, 14), 2, 2),
                                             ((2, 3, 9, 9), 3, 2), ((2, 2, 7, 7), 3, 1)])
-def test_maxpool_exact(hip, orc, shape, k, stride):
-    """Overlapping windows and ties included: the first strict maximum wins."""
-    print_case("maxpool", shape, k, stride)
+@pytest.mark.parametrize("float_index", [False, True])
+def test_maxpool_exact(hip, orc, shape, k, stride, float_index):
+    """Overlapping windows and ties included: the first strict maximum wins. The
+    float-index variant stores the argmax as float, as the reference's device path does."""
+    print_case("maxpool", shape, k, stride, float_index)
     r = rng(sum(shape))
     x = np.round(randn(r, *shape) * 2) / 2  # many ties
     y, am = orc.maxpool(x, k, stride)
-    Y, AM = hip.maxpool(dev(x), k, stride)
+    Y, AM = hip.maxpool(dev(x), k, stride, float_index=float_index)
     exact(host(Y), y, "max")
-    exact(host(AM), am, "argmax")
+    exact(host(AM), am.astype(np.float32) if float_index else am, "argmax")
     g = randn(r, *y.shape)
     exact(host(hip.maxpool_backward(AM, dev(g), shape, k, stride)),
           orc.maxpool_backward(am, g, shape), "maxpool backward")
@@ -458,4 +460,10 @@ def test_refusals_are_errors(hip):
     with pytest.raises(RuntimeError, match="layernorm"):
         hip.ok(hip.lib.ehip_layernorm_f32(hip.p(x), hip.p(x), hip.p(x), hip.p(x), hip.p(x),
                                           hip.p(x), 1, 9000, 1e-5, hip.stream()), "layernorm")
+    with pytest.raises(RuntimeError, match="beyond exact indices"):
+        import ehip as E
+        import ctypes
+        w = E.window(1, 1, 4097, 4097, 2, 2, 2, 0)  # 2^24 + 8193 inputs: float index inexact
+        hip.ok(hip.lib.ehip_maxpool_fidx_f32(hip.p(x), hip.p(x), hip.p(x), ctypes.byref(w),
+                                             hip.stream()), "maxpool_fidx")
     assert hip.launched() == before
