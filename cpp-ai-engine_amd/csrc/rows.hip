@@ -52,63 +52,87 @@ __device__ __forceinline__ float group_reduce(float v, float* sh) {
 
 // ------------------------------------------------------------ row fragments
 
+// Rows of at least this many elements in total are streamed with non-temporal
+// loads and stores (no reuse; 64 MiB per operand is past every cache level).
+constexpr int64_t kNontemporalMin = int64_t(1) << 24;
+
+typedef float nf4 __attribute__((ext_vector_type(4)));
+
 // V values of one row held by thread `tid` of a T-thread group. VEC4 loads
 // 128 bits at a time: value t sits at column 4 * (tid + T * (t / 4)) + t % 4;
-// otherwise at column tid + T * t.
-template <int T, int V, bool VEC4>
+// otherwise at column tid + T * t. Column arithmetic is 32-bit (register rows
+// are at most 32768 wide), which keeps the register count low enough for two
+// 1024-thread groups per CU.
+template <int T, int V, bool VEC4, bool NT = false>
 struct Frag {
     float v[V];
-    __device__ static int64_t col(int tid, int t) {
-        return VEC4 ? 4 * (int64_t(tid) + int64_t(T) * (t / 4)) + (t % 4)
-                    : int64_t(tid) + int64_t(T) * t;
+    __device__ static int col(int tid, int t) {
+        return VEC4 ? 4 * (tid + T * (t / 4)) + (t % 4) : tid + T * t;
     }
-    __device__ void load(const float* row, int64_t cols, int tid, float fill) {
+    // Slot of column c in the fragment of the thread that owns it, or -1 when
+    // this thread does not own c.
+    __device__ static int slot(int tid, int64_t c) {
+        if (c < 0) return -1;
+        const int ci = int(c);
         if (VEC4) {
+            const int c4 = ci >> 2;
+            return (c4 % T == tid) ? 4 * (c4 / T) + (ci & 3) : -1;
+        }
+        return (ci % T == tid) ? ci / T : -1;
+    }
+    __device__ void load(const float* row, int cols, int tid, float fill) {
+        if (VEC4) {
+            const nf4* r4 = reinterpret_cast<const nf4*>(row);
 #pragma unroll
             for (int q = 0; q < V / 4; ++q) {
-                const int64_t c4 = int64_t(tid) + int64_t(T) * q;
+                const int c4 = tid + T * q;
+                nf4 x = {fill, fill, fill, fill};
+                if (4 * c4 < cols) x = NT ? __builtin_nontemporal_load(r4 + c4) : r4[c4];
+                v[4 * q] = x.x;
+                v[4 * q + 1] = x.y;
+                v[4 * q + 2] = x.z;
+                v[4 * q + 3] = x.w;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < V; ++t) {
+                const int c = col(tid, t);
+                v[t] = c < cols ? row[c] : fill;
+            }
+        }
+    }
+    __device__ void store(float* row, int cols, int tid) const {
+        if (VEC4) {
+            nf4* r4 = reinterpret_cast<nf4*>(row);
+#pragma unroll
+            for (int q = 0; q < V / 4; ++q) {
+                const int c4 = tid + T * q;
                 if (4 * c4 < cols) {
-                    const float4 x = reinterpret_cast<const float4*>(row)[c4];
-                    v[4 * q] = x.x;
-                    v[4 * q + 1] = x.y;
-                    v[4 * q + 2] = x.z;
-                    v[4 * q + 3] = x.w;
-                } else {
-                    v[4 * q] = v[4 * q + 1] = v[4 * q + 2] = v[4 * q + 3] = fill;
+                    const nf4 x = {v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                    if (NT)
+                        __builtin_nontemporal_store(x, r4 + c4);
+                    else
+                        r4[c4] = x;
                 }
             }
         } else {
 #pragma unroll
             for (int t = 0; t < V; ++t) {
-                const int64_t c = col(tid, t);
-                v[t] = c < cols ? row[c] : fill;
-            }
-        }
-    }
-    __device__ void store(float* row, int64_t cols, int tid) const {
-        if (VEC4) {
-#pragma unroll
-            for (int q = 0; q < V / 4; ++q) {
-                const int64_t c4 = int64_t(tid) + int64_t(T) * q;
-                if (4 * c4 < cols)
-                    reinterpret_cast<float4*>(row)[c4] =
-                        make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < V; ++t) {
-                const int64_t c = col(tid, t);
+                const int c = col(tid, t);
                 if (c < cols) row[c] = v[t];
             }
         }
     }
 };
 
-// Group geometry inside a block of max(T, 256) threads.
+// Group geometry inside a block of max(T, 256) threads. kMinWaves asks the
+// compiler for two 1024-thread groups per CU (8 waves per SIMD) in kernels
+// that hold one fragment.
 template <int T>
 struct Group {
     static constexpr int kBlock = T < 256 ? 256 : T;
     static constexpr int kPerBlock = kBlock / T;
+    static constexpr int kMinWaves = T == 1024 ? 8 : 1;
     __device__ static int tid() { return threadIdx.x % T; }
     __device__ static int64_t first_row() { return int64_t(blockIdx.x) * kPerBlock + threadIdx.x / T; }
     __device__ static int64_t row_step() { return int64_t(gridDim.x) * kPerBlock; }
@@ -116,8 +140,12 @@ struct Group {
 
 // Softmax of the fragment in place; returns the row max and the sum of
 // exponentials through m and s. Columns past the end hold -inf and give 0.
-template <int T, int V, bool VEC4>
-__device__ __forceinline__ void frag_softmax(Frag<T, V, VEC4>& f, float* sh, float& m, float& s) {
+// The exponentials are scaled by one correctly rounded reciprocal of the sum
+// (within an ulp of dividing each, and a division per element costs more than
+// the row's HBM traffic).
+template <int T, int V, bool VEC4, bool NT>
+__device__ __forceinline__ void frag_softmax(Frag<T, V, VEC4, NT>& f, float* sh, float& m,
+                                             float& s) {
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < V; ++t) mx = fmaxf(mx, f.v[t]);
@@ -129,44 +157,44 @@ __device__ __forceinline__ void frag_softmax(Frag<T, V, VEC4>& f, float* sh, flo
         sum += f.v[t];
     }
     sum = group_reduce<T, false>(sum, sh);
+    const float rs = 1.0f / sum;
 #pragma unroll
-    for (int t = 0; t < V; ++t) f.v[t] = f.v[t] / sum;
+    for (int t = 0; t < V; ++t) f.v[t] = f.v[t] * rs;
     m = mx;
     s = sum;
 }
 
 // ------------------------------------------------------------ softmax
 
-template <int T, int V, bool VEC4>
-__global__ __launch_bounds__(Group<T>::kBlock) void softmax_rows(const float* __restrict__ x,
-                                                                 float* __restrict__ y,
-                                                                 int64_t rows, int64_t cols) {
+template <int T, int V, bool VEC4, bool NT>
+__global__ __launch_bounds__(Group<T>::kBlock, Group<T>::kMinWaves) void softmax_rows(
+    const float* __restrict__ x, float* __restrict__ y, int64_t rows, int64_t cols) {
     __shared__ float sh[Group<T>::kBlock / 64];
     for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
-        Frag<T, V, VEC4> f;
-        f.load(x + r * cols, cols, Group<T>::tid(), -INFINITY);
+        Frag<T, V, VEC4, NT> f;
+        f.load(x + r * cols, int(cols), Group<T>::tid(), -INFINITY);
         float m, s;
-        frag_softmax<T, V, VEC4>(f, sh, m, s);
-        f.store(y + r * cols, cols, Group<T>::tid());
+        frag_softmax(f, sh, m, s);
+        f.store(y + r * cols, int(cols), Group<T>::tid());
     }
 }
 
-template <int T, int V, bool VEC4>
+template <int T, int V, bool VEC4, bool NT>
 __global__ __launch_bounds__(Group<T>::kBlock) void softmax_rows_backward(
     const float* __restrict__ y, const float* __restrict__ g, float* __restrict__ dx, int64_t rows,
     int64_t cols) {
     __shared__ float sh[Group<T>::kBlock / 64];
     for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
-        Frag<T, V, VEC4> fy, fg;
-        fy.load(y + r * cols, cols, Group<T>::tid(), 0.0f);
-        fg.load(g + r * cols, cols, Group<T>::tid(), 0.0f);
+        Frag<T, V, VEC4, NT> fy, fg;
+        fy.load(y + r * cols, int(cols), Group<T>::tid(), 0.0f);
+        fg.load(g + r * cols, int(cols), Group<T>::tid(), 0.0f);
         float dot = 0.0f;
 #pragma unroll
         for (int t = 0; t < V; ++t) dot += fg.v[t] * fy.v[t];
         dot = group_reduce<T, false>(dot, sh);
 #pragma unroll
         for (int t = 0; t < V; ++t) fg.v[t] = fy.v[t] * (fg.v[t] - dot);
-        fg.store(dx + r * cols, cols, Group<T>::tid());
+        fg.store(dx + r * cols, int(cols), Group<T>::tid());
     }
 }
 
@@ -198,7 +226,8 @@ __global__ __launch_bounds__(kLoopThreads) void softmax_rows_loop(const float* _
         float sum = 0.0f;
         for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) sum += expf(xr[c] - mx);
         sum = block_reduce_loop(sum, sh, false);
-        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) yr[c] = expf(xr[c] - mx) / sum;
+        const float rs = 1.0f / sum;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) yr[c] = expf(xr[c] - mx) * rs;
     }
 }
 
@@ -221,19 +250,17 @@ __global__ __launch_bounds__(kLoopThreads) void softmax_rows_backward_loop(
 
 // probs = softmax(logits); row_loss[r] = -((x[t] - max) - log(sum)), the
 // expression of src/nn.cpp:371-373. An out-of-range target gives NaN.
-template <int T, int V, bool VEC4>
-__global__ __launch_bounds__(Group<T>::kBlock) void xent_rows(const float* __restrict__ logits,
-                                                              const int32_t* __restrict__ targets,
-                                                              float* __restrict__ probs,
-                                                              float* __restrict__ row_loss,
-                                                              int64_t rows, int64_t cols) {
+template <int T, int V, bool VEC4, bool NT>
+__global__ __launch_bounds__(Group<T>::kBlock, Group<T>::kMinWaves) void xent_rows(
+    const float* __restrict__ logits, const int32_t* __restrict__ targets,
+    float* __restrict__ probs, float* __restrict__ row_loss, int64_t rows, int64_t cols) {
     __shared__ float sh[Group<T>::kBlock / 64];
     for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
-        Frag<T, V, VEC4> f;
-        f.load(logits + r * cols, cols, Group<T>::tid(), -INFINITY);
+        Frag<T, V, VEC4, NT> f;
+        f.load(logits + r * cols, int(cols), Group<T>::tid(), -INFINITY);
         float m, s;
-        frag_softmax<T, V, VEC4>(f, sh, m, s);
-        f.store(probs + r * cols, cols, Group<T>::tid());
+        frag_softmax(f, sh, m, s);
+        f.store(probs + r * cols, int(cols), Group<T>::tid());
         if (Group<T>::tid() == 0) {
             const int64_t t = targets[r];
             row_loss[r] = (t >= 0 && t < cols) ? -((logits[r * cols + t] - m) - logf(s)) : NAN;
@@ -244,25 +271,28 @@ __global__ __launch_bounds__(Group<T>::kBlock) void xent_rows(const float* __res
 // dx = (softmax - onehot) * (grad / rows), from the logits in one pass. The
 // softmax is the same code as xent_rows, so the result equals the two-kernel
 // path bit for bit.
-template <int T, int V, bool VEC4>
-__global__ __launch_bounds__(Group<T>::kBlock) void xent_rows_backward_fused(
+template <int T, int V, bool VEC4, bool NT>
+__global__ __launch_bounds__(Group<T>::kBlock, Group<T>::kMinWaves) void xent_rows_backward_fused(
     const float* __restrict__ logits, const int32_t* __restrict__ targets, float* __restrict__ dx,
     int64_t rows, int64_t cols, const float* __restrict__ grad) {
     __shared__ float sh[Group<T>::kBlock / 64];
     const float scale = grad[0] / static_cast<float>(rows);
+    const int tid = Group<T>::tid();
     for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
-        Frag<T, V, VEC4> f;
-        f.load(logits + r * cols, cols, Group<T>::tid(), -INFINITY);
+        Frag<T, V, VEC4, NT> f;
+        f.load(logits + r * cols, int(cols), tid, -INFINITY);
         float m, s;
-        frag_softmax<T, V, VEC4>(f, sh, m, s);
+        frag_softmax(f, sh, m, s);
         const int64_t t = targets[r];
+        // Only the thread holding the target column subtracts the one-hot.
+        const int ts = t < cols ? Frag<T, V, VEC4, NT>::slot(tid, t) : -1;
 #pragma unroll
         for (int q = 0; q < V; ++q) {
             float p = f.v[q];
-            if (Frag<T, V, VEC4>::col(Group<T>::tid(), q) == t) p -= 1.0f;
+            if (q == ts) p -= 1.0f;
             f.v[q] = p * scale;
         }
-        f.store(dx + r * cols, cols, Group<T>::tid());
+        f.store(dx + r * cols, int(cols), tid);
     }
 }
 
@@ -280,8 +310,9 @@ __global__ __launch_bounds__(kLoopThreads) void xent_rows_loop(const float* __re
         float sum = 0.0f;
         for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) sum += expf(xr[c] - mx);
         sum = block_reduce_loop(sum, sh, false);
+        const float rs = 1.0f / sum;
         for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads)
-            probs[r * cols + c] = expf(xr[c] - mx) / sum;
+            probs[r * cols + c] = expf(xr[c] - mx) * rs;
         if (threadIdx.x == 0) {
             const int64_t t = targets[r];
             row_loss[r] = (t >= 0 && t < cols) ? -((xr[t] - mx) - logf(sum)) : NAN;
@@ -303,8 +334,9 @@ __global__ __launch_bounds__(kLoopThreads) void xent_rows_backward_loop(
         for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) sum += expf(xr[c] - mx);
         sum = block_reduce_loop(sum, sh, false);
         const int64_t t = targets[r];
+        const float rs = 1.0f / sum;
         for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) {
-            float p = expf(xr[c] - mx) / sum;
+            float p = expf(xr[c] - mx) * rs;
             if (c == t) p -= 1.0f;
             dx[r * cols + c] = p * scale;
         }
@@ -355,7 +387,7 @@ __global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows(
     const int tid = Group<T>::tid();
     for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
         Frag<T, V, false> f;
-        f.load(x + r * cols, cols, tid, 0.0f);
+        f.load(x + r * cols, int(cols), tid, 0.0f);
         float s = 0.0f;
 #pragma unroll
         for (int t = 0; t < V; ++t) s += f.v[t];
@@ -401,8 +433,8 @@ __global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows_backward(
     }
     for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
         Frag<T, V, false> fd, fh;
-        fd.load(dy + r * cols, cols, tid, 0.0f);
-        fh.load(xhat + r * cols, cols, tid, 0.0f);
+        fd.load(dy + r * cols, int(cols), tid, 0.0f);
+        fh.load(xhat + r * cols, int(cols), tid, 0.0f);
         float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
         for (int t = 0; t < V; ++t) {
@@ -421,7 +453,7 @@ __global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows_backward(
             dg[t] = dg[t] + fd.v[t] * fh.v[t];
             db[t] = db[t] + fd.v[t];
         }
-        fo.store(dx + r * cols, cols, tid);
+        fo.store(dx + r * cols, int(cols), tid);
     }
     const int64_t group = Group<T>::first_row();  // group index == its first row
     float* pg = partial + group * 2 * cols;
@@ -445,19 +477,35 @@ unsigned row_grid(int64_t rows, int per_block) {
 
 // Calls f.template operator()<T, V, VEC4>() for the register path that holds
 // `cols`, or returns false when the row needs the looped fallback.
+// Calls f.template run<T, V, VEC4, NT>() for the register path that holds
+// `cols`, or returns false when the row needs the looped fallback. Rows whose
+// width is a multiple of 4 (and 16-byte aligned) load 128 bits at a time;
+// large totals stream non-temporally.
+template <int T, int V, class F>
+bool run_vec(bool nt, F& f) {
+    return nt ? f.template run<T, V, true, true>() : f.template run<T, V, true, false>();
+}
+
 template <class F>
-bool dispatch_row(int64_t cols, bool vec_ok, F&& f) {
-    if (cols <= 64) return f.template run<64, 1, false>();
-    if (cols <= 128) return f.template run<64, 2, false>();
-    if (cols <= 256) return f.template run<64, 4, false>();
-    if (cols <= 512) return f.template run<64, 8, false>();
-    if (cols <= 1024) return f.template run<64, 16, false>();
-    if (cols <= 2048) return f.template run<64, 32, false>();
-    if (!vec_ok) return false;
-    if (cols <= 4096) return f.template run<256, 16, true>();
-    if (cols <= 8192) return f.template run<256, 32, true>();
-    if (cols <= 16384) return f.template run<1024, 16, true>();
-    if (cols <= 32768) return f.template run<1024, 32, true>();
+bool dispatch_row(int64_t rows, int64_t cols, bool vec_ok, F&& f) {
+    const bool nt = rows * cols >= kNontemporalMin;
+    if (cols <= 64) return f.template run<64, 1, false, false>();
+    if (cols <= 128) return f.template run<64, 2, false, false>();
+    if (!vec_ok) {
+        if (cols <= 256) return f.template run<64, 4, false, false>();
+        if (cols <= 512) return f.template run<64, 8, false, false>();
+        if (cols <= 1024) return f.template run<64, 16, false, false>();
+        if (cols <= 2048) return f.template run<64, 32, false, false>();
+        return false;
+    }
+    if (cols <= 256) return run_vec<64, 4>(nt, f);
+    if (cols <= 512) return run_vec<64, 8>(nt, f);
+    if (cols <= 1024) return run_vec<64, 16>(nt, f);
+    if (cols <= 2048) return run_vec<64, 32>(nt, f);
+    if (cols <= 4096) return run_vec<256, 16>(nt, f);
+    if (cols <= 8192) return run_vec<256, 32>(nt, f);
+    if (cols <= 16384) return run_vec<1024, 16>(nt, f);
+    if (cols <= 32768) return run_vec<1024, 32>(nt, f);
     return false;
 }
 
@@ -467,11 +515,11 @@ struct SoftmaxLaunch {
     int64_t rows, cols;
     hipStream_t s;
     int* rc;
-    template <int T, int V, bool VEC4>
+    template <int T, int V, bool VEC4, bool NT>
     bool run() {
         constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
         *rc = [&] {
-            EHIP_LAUNCH("softmax", (softmax_rows<T, V, VEC4>), dim3(row_grid(rows, G)), dim3(B), 0,
+            EHIP_LAUNCH("softmax", (softmax_rows<T, V, VEC4, NT>), dim3(row_grid(rows, G)), dim3(B), 0,
                         s, x, y, rows, cols);
             return int(EHIP_OK);
         }();
@@ -486,11 +534,11 @@ struct SoftmaxBackwardLaunch {
     int64_t rows, cols;
     hipStream_t s;
     int* rc;
-    template <int T, int V, bool VEC4>
+    template <int T, int V, bool VEC4, bool NT>
     bool run() {
         constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
         *rc = [&] {
-            EHIP_LAUNCH("softmax_backward", (softmax_rows_backward<T, V, VEC4>),
+            EHIP_LAUNCH("softmax_backward", (softmax_rows_backward<T, V, VEC4, NT>),
                         dim3(row_grid(rows, G)), dim3(B), 0, s, y, g, dx, rows, cols);
             return int(EHIP_OK);
         }();
@@ -506,11 +554,11 @@ struct XentLaunch {
     int64_t rows, cols;
     hipStream_t s;
     int* rc;
-    template <int T, int V, bool VEC4>
+    template <int T, int V, bool VEC4, bool NT>
     bool run() {
         constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
         *rc = [&] {
-            EHIP_LAUNCH("cross_entropy", (xent_rows<T, V, VEC4>), dim3(row_grid(rows, G)), dim3(B),
+            EHIP_LAUNCH("cross_entropy", (xent_rows<T, V, VEC4, NT>), dim3(row_grid(rows, G)), dim3(B),
                         0, s, logits, targets, probs, row_loss, rows, cols);
             return int(EHIP_OK);
         }();
@@ -526,11 +574,11 @@ struct XentBackwardLaunch {
     const float* grad;
     hipStream_t s;
     int* rc;
-    template <int T, int V, bool VEC4>
+    template <int T, int V, bool VEC4, bool NT>
     bool run() {
         constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
         *rc = [&] {
-            EHIP_LAUNCH("softmax_xent_backward", (xent_rows_backward_fused<T, V, VEC4>),
+            EHIP_LAUNCH("softmax_xent_backward", (xent_rows_backward_fused<T, V, VEC4, NT>),
                         dim3(row_grid(rows, G)), dim3(B), 0, s, logits, targets, dx, rows, cols,
                         grad);
             return int(EHIP_OK);
@@ -562,7 +610,7 @@ int ehip_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols, void*
     if (rows == 0) return EHIP_OK;
     hipStream_t s = as_stream(stream);
     int rc = EHIP_OK;
-    if (dispatch_row(cols, rows_vec_ok(cols, {x, y}), SoftmaxLaunch{x, y, rows, cols, s, &rc}))
+    if (dispatch_row(rows, cols, rows_vec_ok(cols, {x, y}), SoftmaxLaunch{x, y, rows, cols, s, &rc}))
         return rc;
     EHIP_LAUNCH("softmax", softmax_rows_loop, dim3(loop_grid(rows)), dim3(kLoopThreads), 0, s, x, y,
                 rows, cols);
@@ -577,7 +625,7 @@ int ehip_softmax_backward_f32(const float* y, const float* g, float* dx, int64_t
     if (rows == 0) return EHIP_OK;
     hipStream_t s = as_stream(stream);
     int rc = EHIP_OK;
-    if (dispatch_row(cols, rows_vec_ok(cols, {y, g, dx}),
+    if (dispatch_row(rows, cols, rows_vec_ok(cols, {y, g, dx}),
                      SoftmaxBackwardLaunch{y, g, dx, rows, cols, s, &rc}))
         return rc;
     EHIP_LAUNCH("softmax_backward", softmax_rows_backward_loop, dim3(loop_grid(rows)),
@@ -595,7 +643,7 @@ int ehip_cross_entropy_f32(const float* logits, const int32_t* targets, float* p
     float* row_loss = static_cast<float*>(scratch(size_t(rows) * sizeof(float)));
     if (row_loss == nullptr) return EHIP_ENOMEM;
     int rc = EHIP_OK;
-    if (!dispatch_row(cols, rows_vec_ok(cols, {logits, probs}),
+    if (!dispatch_row(rows, cols, rows_vec_ok(cols, {logits, probs}),
                       XentLaunch{logits, targets, probs, row_loss, rows, cols, s, &rc})) {
         EHIP_LAUNCH("cross_entropy", xent_rows_loop, dim3(loop_grid(rows)), dim3(kLoopThreads), 0,
                     s, logits, targets, probs, row_loss, rows, cols);
@@ -626,7 +674,7 @@ int ehip_softmax_xent_backward_f32(const float* logits, const int32_t* targets, 
         return fail(EHIP_EINVAL, "softmax_xent_backward: null pointer");
     hipStream_t s = as_stream(stream);
     int rc = EHIP_OK;
-    if (dispatch_row(cols, rows_vec_ok(cols, {logits, dx}),
+    if (dispatch_row(rows, cols, rows_vec_ok(cols, {logits, dx}),
                      XentBackwardLaunch{logits, targets, dx, rows, cols, grad, s, &rc}))
         return rc;
     EHIP_LAUNCH("softmax_xent_backward", xent_rows_backward_loop, dim3(loop_grid(rows)),

@@ -162,7 +162,7 @@ def test_gemm_backward_products(hip, orc):
 
 @pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
 @pytest.mark.parametrize("shape,inner", [((1000,), 1000), ((50176, 8), 8), ((33, 7), 7),
-                                         ((64, 96), 96), ((4, 3, 5), 15)])
+                                         ((64, 96), 96), ((4, 3, 5), 15), ((1 << 22, 4), 4)])
 def test_binary_exact(hip, orc, op, shape, inner):
     print_case("binary", op, shape, inner)
     r = rng(len(shape) * 100 + inner)
@@ -172,7 +172,7 @@ def test_binary_exact(hip, orc, op, shape, inner):
     exact(host(hip.binary(code, dev(a), dev(b))), orc.binary(op, a, b).reshape(shape), op)
 
 
-@pytest.mark.parametrize("n", [1, 3, 4, 1023, 4096 * 4 + 5, 1 << 20])
+@pytest.mark.parametrize("n", [1, 3, 4, 1023, 4096 * 4 + 5, 1 << 20, (1 << 24) + 6])
 def test_unary_exact(hip, orc, n):
     print_case("unary", n)
     r = rng(n)
@@ -186,7 +186,7 @@ def test_unary_exact(hip, orc, n):
     exact(host(hip.scalar(X, 1.0, 2.5)), orc.scalar_add(x, 2.5), "t+k")
 
 
-@pytest.mark.parametrize("n", [5, 4096, 100003])
+@pytest.mark.parametrize("n", [5, 4096, 100003, (1 << 24) + 2])
 def test_accumulate_and_add_backward_exact(hip, orc, n):
     print_case("accumulate", n)
     r = rng(n + 1)
@@ -206,7 +206,7 @@ def test_accumulate_and_add_backward_exact(hip, orc, n):
                   f"db {acc_a}{acc_b}")
 
 
-@pytest.mark.parametrize("n", [7, 4096, 65537])
+@pytest.mark.parametrize("n", [7, 4096, 65537, (1 << 24) + 3])
 def test_adam_trajectory_exact(hip, orc, n):
     """Ten Adam steps, bias corrections from the host as in src/optim.cpp:119-120."""
     print_case("adam", n)
@@ -378,7 +378,8 @@ def test_reduce_sum(hip, orc, n):
 # ------------------------------------------------------------------ rows
 
 @pytest.mark.parametrize("rows,cols", [(8192, 64), (64, 512), (3, 5), (17, 2048), (4, 4000),
-                                       (2, 8192), (3, 30000), (2, 40000), (5, 1000)])
+                                       (2, 8192), (3, 30000), (2, 40000), (5, 1000), (9, 130),
+                                       (4096, 4096), (32768, 512)])
 def test_softmax(hip, orc, rows, cols):
     print_case("softmax", rows, cols)
     r = rng(rows * cols)
@@ -419,7 +420,7 @@ def test_layernorm(hip, orc, rows, d):
 
 
 @pytest.mark.parametrize("rows,cols", [(64, 10), (2048, 121), (8, 5), (16, 32000), (3, 40000),
-                                       (100, 256)])
+                                       (100, 256), (600, 32000), (9, 1002)])
 def test_cross_entropy(hip, orc, rows, cols):
     print_case("xent", rows, cols)
     r = rng(rows * 3 + cols)
