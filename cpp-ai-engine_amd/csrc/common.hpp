@@ -46,6 +46,19 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
                 int64_t x_slab, float* out, hipStream_t s);
 
+// Validates a window: positive extents, non-negative padding, and out_h/out_w
+// equal to the geometry's (layout.hip). Refusals carry `name`.
+int check_window(const char* name, const ehip_window_t* w);
+
+// First and last window index along one axis whose window covers position p.
+__host__ __device__ __forceinline__ void covering(int64_t p, int64_t pad, int64_t k, int64_t s,
+                                         int64_t out, int64_t& lo, int64_t& hi) {
+    const int64_t t = p + pad - (k - 1);
+    lo = t <= 0 ? 0 : (t + s - 1) / s;
+    hi = (p + pad) / s;
+    if (hi > out - 1) hi = out - 1;
+}
+
 __host__ __device__ inline bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }

@@ -1,0 +1,634 @@
+// conv.hip -- direct 2-D convolution for narrow layers: forward, input
+// gradient, and the fused weight + bias gradient, with no im2col columns in
+// HBM and the output written straight in (N, C, H, W).
+//
+// The reference composes Conv2d::forward from im2col, a product with the
+// transposed weight, a broadcast bias add and a permute (src/conv.cpp:280-338);
+// autograd derives the backward from those four nodes. Here each direction is
+// one kernel (the weight gradient two: per-chunk partials and their ordered
+// reduction), so a conv layer costs three to four launches per step instead of
+// ten, and the columns (kH * kW times the input) never touch HBM.
+//
+// Exactness. The forward sums the K = C_in kH kW products of each output in
+// k-ascending order from zero, skipping zero inputs, then adds the bias: the
+// reference's i-k-j loop with its zero skip (src/tensor_ops.cpp:553-560) and
+// its separately rounded bias add, so the result is bit-identical. The input
+// gradient computes, for every window that covers a pixel (oh then ow
+// ascending), the C_out-term dot product of that column entry (co ascending,
+// zero gradients skipped) and adds those in order from zero: the reference's
+// product dcols = g W followed by col2im (src/conv.cpp:183-214), bit for bit.
+// The weight and bias gradients are sums over all N oH oW pixels; they are
+// split into chunks and reduced in a fixed order (deterministic, within the
+// K-term tolerance of the reference's serial sums).
+//
+// Narrow means out_channels * C_in * kH * kW <= 8192 (the weights fit in
+// 32 KiB of LDS): the cfg2 layers (8 x 9 and 16 x 72). Wider layers go through
+// im2col and the MFMA GEMM, where the product dominates.
+
+#include "common.hpp"
+
+namespace ehip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kCoGroup = 4;              // output channels per thread in the forward
+constexpr int64_t kMaxWeights = 8192;    // out_channels * K
+constexpr size_t kMaxLds = 64 * 1024;    // bytes of LDS per weight-gradient block
+
+struct Geo {
+    int n, cin, h, w, kh, kw, stride, pad, oh, ow, cout, k;
+};
+
+Geo geo_of(const ehip_window_t& win, int64_t cout) {
+    Geo g;
+    g.n = int(win.batch);
+    g.cin = int(win.channels);
+    g.h = int(win.height);
+    g.w = int(win.width);
+    g.kh = int(win.kernel_h);
+    g.kw = int(win.kernel_w);
+    g.stride = int(win.stride);
+    g.pad = int(win.padding);
+    g.oh = int(win.out_h);
+    g.ow = int(win.out_w);
+    g.cout = int(cout);
+    g.k = g.cin * g.kh * g.kw;
+    return g;
+}
+
+// One thread per output pixel and group of kCoGroup output channels; the group
+// is blockIdx.y, so every weight read is uniform across the block (scalar
+// loads). x is read through the caches, kH kW times per pixel at most.
+__global__ __launch_bounds__(kThreads) void conv_forward_direct(const float* __restrict__ x,
+                                                                const float* __restrict__ wt,
+                                                                const float* __restrict__ bias,
+                                                                float* __restrict__ out, Geo g) {
+    const int64_t pixels = int64_t(g.n) * g.oh * g.ow;
+    const int64_t m = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    const int co0 = int(blockIdx.y) * kCoGroup;
+    if (m >= pixels) return;
+    const int ow = int(m % g.ow);
+    const int64_t t = m / g.ow;
+    const int oh = int(t % g.oh);
+    const int n = int(t / g.oh);
+    float c[kCoGroup];
+#pragma unroll
+    for (int q = 0; q < kCoGroup; ++q) c[q] = 0.0f;
+    const float* xn = x + int64_t(n) * g.cin * g.h * g.w;
+    int k = 0;
+    for (int ci = 0; ci < g.cin; ++ci) {
+        const float* xc = xn + int64_t(ci) * g.h * g.w;
+        for (int i = 0; i < g.kh; ++i) {
+            const int h = oh * g.stride + i - g.pad;
+            for (int j = 0; j < g.kw; ++j, ++k) {
+                const int v = ow * g.stride + j - g.pad;
+                const float a = (h >= 0 && h < g.h && v >= 0 && v < g.w) ? xc[h * g.w + v] : 0.0f;
+#pragma unroll
+                for (int q = 0; q < kCoGroup; ++q) {
+                    if (co0 + q < g.cout) {
+                        const float b = wt[int64_t(co0 + q) * g.k + k];
+                        c[q] = (a != 0.0f) ? c[q] + a * b : c[q];
+                    }
+                }
+            }
+        }
+    }
+    const int64_t plane = int64_t(g.oh) * g.ow;
+    float* on = out + int64_t(n) * g.cout * plane + int64_t(oh) * g.ow + ow;
+#pragma unroll
+    for (int q = 0; q < kCoGroup; ++q) {
+        const int co = co0 + q;
+        if (co < g.cout) on[int64_t(co) * plane] = bias ? c[q] + bias[co] : c[q];
+    }
+}
+
+// One thread per input element (n, ci, h, w); the weights sit in LDS.
+__global__ __launch_bounds__(kThreads) void conv_backward_input_direct(
+    const float* __restrict__ gout, const float* __restrict__ wt, float* __restrict__ dx, Geo g) {
+    extern __shared__ float ws[];
+    const int nw = g.cout * g.k;
+    for (int e = threadIdx.x; e < nw; e += kThreads) ws[e] = wt[e];
+    __syncthreads();
+    const int64_t n_in = int64_t(g.n) * g.cin * g.h * g.w;
+    const int64_t plane = int64_t(g.oh) * g.ow;
+    const int64_t step = int64_t(gridDim.x) * kThreads;
+    for (int64_t e = int64_t(blockIdx.x) * kThreads + threadIdx.x; e < n_in; e += step) {
+        const int v = int(e % g.w);
+        int64_t t = e / g.w;
+        const int h = int(t % g.h);
+        t /= g.h;
+        const int ci = int(t % g.cin);
+        const int n = int(t / g.cin);
+        int64_t oh_lo, oh_hi, ow_lo, ow_hi;
+        covering(h, g.pad, g.kh, g.stride, g.oh, oh_lo, oh_hi);
+        covering(v, g.pad, g.kw, g.stride, g.ow, ow_lo, ow_hi);
+        const float* gn = gout + int64_t(n) * g.cout * plane;
+        const float* wc = ws + ci * g.kh * g.kw;
+        float acc = 0.0f;
+        for (int64_t oh = oh_lo; oh <= oh_hi; ++oh) {
+            const int i = int(h + g.pad - oh * g.stride);
+            for (int64_t ow = ow_lo; ow <= ow_hi; ++ow) {
+                const int j = int(v + g.pad - ow * g.stride);
+                const float* gp = gn + oh * g.ow + ow;
+                const float* wp = wc + i * g.kw + j;
+                float d = 0.0f;
+                for (int co = 0; co < g.cout; ++co) {
+                    const float gv = gp[int64_t(co) * plane];
+                    d = (gv != 0.0f) ? d + gv * wp[co * g.k] : d;
+                }
+                acc += d;
+            }
+        }
+        dx[e] = acc;
+    }
+}
+
+// Staging helper: copies n elements into LDS, U independent global loads in
+// flight per thread before any LDS store. value(e) returns the element e (and
+// does its own bounds checks); dst(e) is its LDS slot.
+template <int U, class Value, class Dst>
+__device__ __forceinline__ void stage(int n, Value value, Dst dst) {
+    for (int base = 0; base < n; base += U * kThreads) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = base + u * kThreads + int(threadIdx.x);
+            v[u] = e < n ? value(e) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int e = base + u * kThreads + int(threadIdx.x);
+            if (e < n) *dst(e) = v[u];
+        }
+    }
+}
+
+// Forward over a tile of `rows` output rows of one image and CG output
+// channels (blockIdx.y). The input rows the tile reads, zero-padded on every
+// side, and the weights of the CG channels (laid out [k][CG], one 128-bit
+// broadcast read per k) sit in LDS; each thread then computes whole pixels
+// (all CG channels) from LDS in the same k order and with the same zero skip
+// as conv_forward_direct. The skip is a select after an unconditional
+// multiply-add, so no LDS read waits behind a branch. KH = KW = 0 reads the
+// kernel size at run time; 3 x 3 is compiled unrolled. blockIdx.x = n * tiles
+// + tile.
+template <int CG, int KH, int KW>
+__global__ __launch_bounds__(kThreads) void conv_forward_tiled(const float* __restrict__ x,
+                                                               const float* __restrict__ wt,
+                                                               const float* __restrict__ bias,
+                                                               float* __restrict__ out, Geo g,
+                                                               int rows, int tiles) {
+    extern __shared__ float sm[];
+    const int kh = KH ? KH : g.kh, kw = KW ? KW : g.kw;
+    const int n = int(blockIdx.x) / tiles, tile = int(blockIdx.x) % tiles;
+    const int co0 = int(blockIdx.y) * CG;
+    const int oh0 = tile * rows;
+    const int oh1 = min(oh0 + rows, g.oh);
+    const int r0 = oh0 * g.stride - g.pad;               // first input row read
+    const int rows_in = (oh1 - oh0 - 1) * g.stride + kh;
+    const int wp = g.w + 2 * g.pad;                      // padded row pitch
+    float* w_s = sm;                                     // [K][CG]
+    float* x_s = sm + CG * g.k;                          // [cin][rows_in][wp]
+    const float* xn = x + int64_t(n) * g.cin * g.h * g.w;
+    const int plane_in = rows_in * wp;
+    stage<4>(
+        CG * g.k,
+        [&](int e) {
+            const int co = co0 + e % CG;
+            return co < g.cout ? wt[co * g.k + e / CG] : 0.0f;
+        },
+        [&](int e) { return w_s + e; });
+    stage<8>(
+        g.cin * plane_in,
+        [&](int e) {
+            const unsigned ci = unsigned(e) / unsigned(plane_in);
+            const unsigned rem = unsigned(e) - ci * unsigned(plane_in);
+            const unsigned rr = rem / unsigned(wp);
+            const int h = r0 + int(rr), v = int(rem - rr * unsigned(wp)) - g.pad;
+            return (h >= 0 && h < g.h && v >= 0 && v < g.w) ? xn[(int(ci) * g.h + h) * g.w + v]
+                                                            : 0.0f;
+        },
+        [&](int e) { return x_s + e; });
+    __syncthreads();
+    const int npix = (oh1 - oh0) * g.ow;
+    const int64_t plane = int64_t(g.oh) * g.ow;
+    for (int p = threadIdx.x; p < npix; p += kThreads) {
+        const int ohl = p / g.ow, ow = p - ohl * g.ow;
+        float c[CG];
+#pragma unroll
+        for (int q = 0; q < CG; ++q) c[q] = 0.0f;
+        const float* wk = w_s;
+        for (int ci = 0; ci < g.cin; ++ci) {
+            const float* xr = x_s + (ci * rows_in + ohl * g.stride) * wp + ow * g.stride;
+#pragma unroll
+            for (int i = 0; i < (KH ? KH : 1); ++i) {
+                for (int ii = 0; ii < (KH ? 1 : kh); ++ii) {
+                    const float* xi = xr + (KH ? i : ii) * wp;
+#pragma unroll
+                    for (int j = 0; j < (KW ? KW : 1); ++j) {
+                        for (int jj = 0; jj < (KW ? 1 : kw); ++jj, wk += CG) {
+                            const float a = xi[KW ? j : jj];
+                            float wv[CG];
+#pragma unroll
+                            for (int q = 0; q < CG; ++q) wv[q] = wk[q];
+#pragma unroll
+                            for (int q = 0; q < CG; ++q) {
+                                const float t = c[q] + a * wv[q];
+                                c[q] = (a != 0.0f) ? t : c[q];
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        float* on = out + int64_t(n) * g.cout * plane + int64_t(oh0 + ohl) * g.ow + ow;
+#pragma unroll
+        for (int q = 0; q < CG; ++q) {
+            const int co = co0 + q;
+            if (co < g.cout) on[int64_t(co) * plane] = bias ? c[q] + bias[co] : c[q];
+        }
+    }
+}
+
+// Input gradient over a tile of `rows` input rows of one image and CG input
+// channels (blockIdx.y). The output-gradient rows whose windows cover the tile
+// (all out_channels) and the weights of the CG channels sit in LDS; each
+// thread computes whole input elements in the order of
+// conv_backward_input_direct (zero gradients skipped by a select after an
+// unconditional multiply-add). blockIdx.x = n * tiles + tile.
+template <int CG>
+__global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
+    const float* __restrict__ gout, const float* __restrict__ wt, float* __restrict__ dx, Geo g,
+    int rows, int tiles) {
+    extern __shared__ float sm[];
+    const int n = int(blockIdx.x) / tiles, tile = int(blockIdx.x) % tiles;
+    const int ci0 = int(blockIdx.y) * CG;
+    const int h0 = tile * rows;
+    const int h1 = min(h0 + rows, g.h);
+    int64_t lo, hi, lo2, hi2;
+    covering(h0, g.pad, g.kh, g.stride, g.oh, lo, hi);
+    covering(h1 - 1, g.pad, g.kh, g.stride, g.oh, lo2, hi2);
+    const int oh_first = int(lo);
+    const int oh_rows = max(0, int(hi2) - oh_first + 1);
+    const int khw = g.kh * g.kw;
+    const int gplane = oh_rows * g.ow;
+    float* g_s = sm;                                   // [cout][oh_rows][ow]
+    float* w_s = sm + g.cout * gplane;                 // [CG][kh][kw][cout]
+    const int64_t plane = int64_t(g.oh) * g.ow;
+    const float* gn = gout + int64_t(n) * g.cout * plane + int64_t(oh_first) * g.ow;
+    stage<8>(
+        g.cout * gplane,
+        [&](int e) {
+            const unsigned co = unsigned(e) / unsigned(gplane);
+            return gn[int64_t(co) * plane + (unsigned(e) - co * unsigned(gplane))];
+        },
+        [&](int e) { return g_s + e; });
+    stage<4>(
+        CG * khw * g.cout,
+        [&](int e) {
+            const int co = e % g.cout, r = e / g.cout;    // r = cl * khw + tap
+            const int ci = ci0 + r / khw;
+            return ci < g.cin ? wt[(co * g.cin + ci) * khw + r % khw] : 0.0f;
+        },
+        [&](int e) { return w_s + e; });
+    __syncthreads();
+    const int band = (h1 - h0) * g.w;
+    const int nel = CG * band;
+    for (int e = threadIdx.x; e < nel; e += kThreads) {
+        const int cl = e / band, rem = e - cl * band;
+        const int ci = ci0 + cl;
+        if (ci >= g.cin) continue;
+        const int hl = rem / g.w;
+        const int h = h0 + hl, v = rem - hl * g.w;
+        int64_t oh_lo, oh_hi, ow_lo, ow_hi;
+        covering(h, g.pad, g.kh, g.stride, g.oh, oh_lo, oh_hi);
+        covering(v, g.pad, g.kw, g.stride, g.ow, ow_lo, ow_hi);
+        const float* wc = w_s + cl * khw * g.cout;
+        float acc = 0.0f;
+        for (int oh = int(oh_lo); oh <= int(oh_hi); ++oh) {
+            const int i = h + g.pad - oh * g.stride;
+            for (int ow = int(ow_lo); ow <= int(ow_hi); ++ow) {
+                const int j = v + g.pad - ow * g.stride;
+                const float* gp = g_s + (oh - oh_first) * g.ow + ow;
+                const float* wp = wc + (i * g.kw + j) * g.cout;
+                float d = 0.0f;
+                int co = 0;
+                for (; co + 4 <= g.cout; co += 4) {
+                    float gv[4], wv[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        gv[u] = gp[(co + u) * gplane];
+                        wv[u] = wp[co + u];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float t = d + gv[u] * wv[u];
+                        d = (gv[u] != 0.0f) ? t : d;
+                    }
+                }
+                for (; co < g.cout; ++co) {
+                    const float gv = gp[co * gplane];
+                    const float t = d + gv * wp[co];
+                    d = (gv != 0.0f) ? t : d;
+                }
+                acc += d;
+            }
+        }
+        dx[((int64_t(n) * g.cin + ci) * g.h + h) * g.w + v] = acc;
+    }
+}
+
+// Partial weight and bias gradients of one chunk of P output pixels. The
+// chunk's gradients (cout x P) and columns ((K + 1) x P, the last column all
+// ones so that its row is the bias gradient) are staged in LDS with a padded
+// pitch; output o = co (K + 1) + k sums its P products. With fewer outputs
+// than threads, G thread groups split the pixels and are combined in group
+// order. partial[chunk][o]; the order of every sum depends only on the shape.
+__global__ __launch_bounds__(kThreads) void conv_weight_partial(const float* __restrict__ x,
+                                                                const float* __restrict__ gout,
+                                                                float* __restrict__ partial,
+                                                                Geo g, int P) {
+    extern __shared__ float sm[];
+    const int ld = P + 1;
+    const int K1 = g.k + 1;
+    float* dy_s = sm;
+    float* col_s = sm + g.cout * ld;
+    float* red = col_s + K1 * ld;
+    const int64_t pixels = int64_t(g.n) * g.oh * g.ow;
+    const int64_t plane = int64_t(g.oh) * g.ow;
+    const int64_t m0 = int64_t(blockIdx.x) * P;
+    stage<8>(
+        g.cout * P,
+        [&](int e) {
+            const int co = e / P, p = e - co * P;
+            const int64_t m = m0 + p;
+            if (m >= pixels) return 0.0f;
+            const unsigned mu = unsigned(m), pl = unsigned(plane);
+            const unsigned n = mu / pl, r = mu - n * pl;
+            return gout[(int64_t(n) * g.cout + co) * plane + r];
+        },
+        [&](int e) { return dy_s + (e / P) * ld + e % P; });
+    stage<8>(
+        K1 * P,
+        [&](int e) {
+            const int k = e / P, p = e - k * P;
+            const int64_t m = m0 + p;
+            if (m >= pixels) return 0.0f;
+            if (k == g.k) return 1.0f;
+            const unsigned mu = unsigned(m);
+            const unsigned t = mu / unsigned(g.ow), ow = mu - t * unsigned(g.ow);
+            const unsigned n = t / unsigned(g.oh), oh = t - n * unsigned(g.oh);
+            const int ij = k % (g.kh * g.kw), ci = k / (g.kh * g.kw);
+            const int i = ij / g.kw, j = ij - i * g.kw;
+            const int h = int(oh) * g.stride + i - g.pad, v = int(ow) * g.stride + j - g.pad;
+            return (h >= 0 && h < g.h && v >= 0 && v < g.w)
+                       ? x[((int64_t(n) * g.cin + ci) * g.h + h) * g.w + v]
+                       : 0.0f;
+        },
+        [&](int e) { return col_s + (e / P) * ld + e % P; });
+    __syncthreads();
+    const int O = g.cout * K1;
+    float* pc = partial + int64_t(blockIdx.x) * O;
+    if (O >= kThreads) {
+        for (int o = threadIdx.x; o < O; o += kThreads) {
+            const float* a = dy_s + (o / K1) * ld;
+            const float* b = col_s + (o % K1) * ld;
+            float acc = 0.0f;
+            for (int p = 0; p < P; ++p) acc += a[p] * b[p];
+            pc[o] = acc;
+        }
+    } else {
+        const int G = kThreads / O;
+        const int o = threadIdx.x % O, grp = threadIdx.x / O;
+        float acc = 0.0f;
+        if (grp < G) {
+            const float* a = dy_s + (o / K1) * ld;
+            const float* b = col_s + (o % K1) * ld;
+            for (int p = grp; p < P; p += G) acc += a[p] * b[p];
+        }
+        red[threadIdx.x] = acc;
+        __syncthreads();
+        if (threadIdx.x < O) {
+            float s = red[threadIdx.x];
+            for (int q = 1; q < G; ++q) s += red[q * O + threadIdx.x];
+            pc[threadIdx.x] = s;
+        }
+    }
+}
+
+// out[o] = sum over chunks of partial[chunk][o] in a fixed order: rl lanes per
+// output take chunks l, l + rl, ... and lane results are added in lane order.
+// Outputs o = co (K + 1) + k go to dw[co][k] for k < K and to db[co] for k == K.
+__global__ __launch_bounds__(256) void conv_weight_reduce(const float* __restrict__ partial,
+                                                          float* __restrict__ dw,
+                                                          float* __restrict__ db, int cout,
+                                                          int k, int chunks, int rl) {
+    __shared__ float lanes[256];
+    const int K1 = k + 1, O = cout * K1;
+    const int cw = 256 / rl;
+    const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
+    const int o = int(blockIdx.x) * cw + cl;
+    float acc = 0.0f;
+    if (o < O && lane < chunks) {
+        const float* p = partial + o + int64_t(lane) * O;
+        const int64_t stride = int64_t(rl) * O;
+        const int count = (chunks - lane + rl - 1) / rl;
+        acc = p[0];
+        int s = 1;
+        for (; s + 8 <= count; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p[int64_t(s + u) * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; s < count; ++s) acc += p[int64_t(s) * stride];
+    }
+    lanes[threadIdx.x] = acc;
+    __syncthreads();
+    if (lane == 0 && o < O) {
+        float sum = lanes[cl];
+        for (int l = 1; l < rl && l < chunks; ++l) sum += lanes[l * cw + cl];
+        const int co = o / K1, kk = o % K1;
+        if (kk < k)
+            dw[int64_t(co) * k + kk] = sum;
+        else if (db != nullptr)
+            db[co] = sum;
+    }
+}
+
+constexpr size_t kTileLds = 48 * 1024;   // bytes of LDS per tiled block
+
+// Rows per tile so that n * groups * tiles reaches about 256 blocks.
+int rows_for_fill(int64_t n_groups, int extent) {
+    int64_t tiles = ceil_div(256, n_groups < 1 ? 1 : n_groups);
+    if (tiles > extent) tiles = extent;
+    if (tiles < 1) tiles = 1;
+    return int(ceil_div(extent, tiles));
+}
+
+size_t forward_lds(const Geo& g, int cg, int rows) {
+    const size_t rows_in = size_t(rows - 1) * g.stride + g.kh;
+    return (size_t(g.cin) * rows_in * (g.w + 2 * g.pad) + size_t(cg) * g.k) * sizeof(float);
+}
+
+// Largest number of output-gradient rows any tile of `rows` input rows needs.
+int grad_rows_for(const Geo& g, int rows) {
+    int most = 0;
+    for (int h0 = 0; h0 < g.h; h0 += rows) {
+        const int h1 = h0 + rows < g.h ? h0 + rows : g.h;
+        int64_t lo, hi, lo2, hi2;
+        covering(h0, g.pad, g.kh, g.stride, g.oh, lo, hi);
+        covering(h1 - 1, g.pad, g.kh, g.stride, g.oh, lo2, hi2);
+        const int r = int(hi2 - lo + 1);
+        if (r > most) most = r;
+    }
+    return most;
+}
+
+size_t backward_input_lds(const Geo& g, int cg, int rows) {
+    return (size_t(g.cout) * grad_rows_for(g, rows) * g.ow + size_t(g.cout) * cg * g.kh * g.kw) *
+           sizeof(float);
+}
+
+template <int CG>
+int forward_tiled(const float* x, const float* wt, const float* bias, float* out, const Geo& g,
+                  hipStream_t s) {
+    const int groups = int(ceil_div(g.cout, CG));
+    int rows = rows_for_fill(int64_t(g.n) * groups, g.oh);
+    while (rows > 1 && forward_lds(g, CG, rows) > kTileLds) rows = (rows + 1) / 2;
+    const int tiles = int(ceil_div(g.oh, rows));
+    const dim3 grid{unsigned(int64_t(g.n) * tiles), unsigned(groups)};
+    const size_t lds = forward_lds(g, CG, rows);
+    if (g.kh == 3 && g.kw == 3)
+        EHIP_LAUNCH("conv2d_forward", (conv_forward_tiled<CG, 3, 3>), grid, dim3(kThreads), lds, s,
+                    x, wt, bias, out, g, rows, tiles);
+    else
+        EHIP_LAUNCH("conv2d_forward", (conv_forward_tiled<CG, 0, 0>), grid, dim3(kThreads), lds, s,
+                    x, wt, bias, out, g, rows, tiles);
+    return EHIP_OK;
+}
+
+template <int CG>
+int backward_input_tiled(const float* gout, const float* wt, float* dx, const Geo& g,
+                         hipStream_t s) {
+    const int groups = int(ceil_div(g.cin, CG));
+    int rows = rows_for_fill(int64_t(g.n) * groups, g.h);
+    while (rows > 1 && backward_input_lds(g, CG, rows) > kTileLds) rows = (rows + 1) / 2;
+    const int tiles = int(ceil_div(g.h, rows));
+    const dim3 grid{unsigned(int64_t(g.n) * tiles), unsigned(groups)};
+    EHIP_LAUNCH("conv2d_backward_input", conv_backward_input_tiled<CG>, grid, dim3(kThreads),
+                backward_input_lds(g, CG, rows), s, gout, wt, dx, g, rows, tiles);
+    return EHIP_OK;
+}
+
+int check_conv(const char* name, const ehip_window_t* w, int64_t cout) {
+    if (int rc = check_window(name, w)) return rc;
+    if (cout <= 0) return fail(EHIP_EINVAL, "%s: out_channels must be positive", name);
+    const int64_t k = w->channels * w->kernel_h * w->kernel_w;
+    if (cout * k > kMaxWeights)
+        return fail(EHIP_EINVAL,
+                    "%s: out_channels * C_in * kH * kW = %lld exceeds the direct path's %lld",
+                    name, (long long)(cout * k), (long long)kMaxWeights);
+    const int64_t n_in = w->batch * w->channels * w->height * w->width;
+    const int64_t n_out = w->batch * cout * w->out_h * w->out_w;
+    if (n_in > 0x7fffffff || n_out > 0x7fffffff)
+        return fail(EHIP_EINVAL, "%s: tensors beyond 2^31 elements", name);
+    return EHIP_OK;
+}
+
+}  // namespace
+}  // namespace ehip
+
+using namespace ehip;
+
+extern "C" {
+
+int ehip_conv2d_direct_supported(const ehip_window_t* w, int64_t out_channels) {
+    if (w == nullptr || out_channels <= 0) return 0;
+    return out_channels * w->channels * w->kernel_h * w->kernel_w <= kMaxWeights ? 1 : 0;
+}
+
+int ehip_conv2d_forward_f32(const float* x, const float* weight, const float* bias, float* out,
+                            const ehip_window_t* w, int64_t out_channels, void* stream) {
+    EHIP_READY();
+    if (int rc = check_conv("conv2d_forward", w, out_channels)) return rc;
+    if (!x || !weight || !out) return fail(EHIP_EINVAL, "conv2d_forward: null pointer");
+    const Geo g = geo_of(*w, out_channels);
+    const int64_t pixels = int64_t(g.n) * g.oh * g.ow;
+    if (pixels == 0) return EHIP_OK;
+    hipStream_t s = as_stream(stream);
+    // LDS tiles when one input row band fits; the per-pixel kernel otherwise.
+    const int cg = g.cout >= 3 ? 4 : g.cout;
+    if (forward_lds(g, cg, 1) <= kTileLds && int64_t(g.n) * g.oh <= 0x7fffffff) {
+        if (cg == 4) return forward_tiled<4>(x, weight, bias, out, g, s);
+        if (cg == 2) return forward_tiled<2>(x, weight, bias, out, g, s);
+        return forward_tiled<1>(x, weight, bias, out, g, s);
+    }
+    const dim3 grid{unsigned(ceil_div(pixels, kThreads)), unsigned(ceil_div(g.cout, kCoGroup))};
+    EHIP_LAUNCH("conv2d_forward", conv_forward_direct, grid, dim3(kThreads), 0, s, x, weight, bias,
+                out, g);
+    return EHIP_OK;
+}
+
+int ehip_conv2d_backward_input_f32(const float* grad_out, const float* weight, float* dx,
+                                   const ehip_window_t* w, int64_t out_channels, void* stream) {
+    EHIP_READY();
+    if (int rc = check_conv("conv2d_backward_input", w, out_channels)) return rc;
+    if (!grad_out || !weight || !dx) return fail(EHIP_EINVAL, "conv2d_backward_input: null pointer");
+    const Geo g = geo_of(*w, out_channels);
+    const int64_t n_in = int64_t(g.n) * g.cin * g.h * g.w;
+    if (n_in == 0) return EHIP_OK;
+    hipStream_t s = as_stream(stream);
+    const int cg = g.cin >= 2 ? 2 : 1;
+    if (backward_input_lds(g, cg, 1) <= kTileLds && int64_t(g.n) * g.h <= 0x7fffffff) {
+        if (cg == 2) return backward_input_tiled<2>(grad_out, weight, dx, g, s);
+        return backward_input_tiled<1>(grad_out, weight, dx, g, s);
+    }
+    int64_t grid = ceil_div(n_in, kThreads);
+    if (grid > 65536) grid = 65536;
+    const size_t lds = size_t(g.cout) * g.k * sizeof(float);
+    EHIP_LAUNCH("conv2d_backward_input", conv_backward_input_direct, dim3(unsigned(grid)),
+                dim3(kThreads), lds, s, grad_out, weight, dx, g);
+    return EHIP_OK;
+}
+
+int ehip_conv2d_backward_weight_f32(const float* x, const float* grad_out, float* dweight,
+                                    float* dbias, const ehip_window_t* w, int64_t out_channels,
+                                    void* stream) {
+    EHIP_READY();
+    if (int rc = check_conv("conv2d_backward_weight", w, out_channels)) return rc;
+    if (!x || !grad_out || !dweight)
+        return fail(EHIP_EINVAL, "conv2d_backward_weight: null pointer");
+    const Geo g = geo_of(*w, out_channels);
+    const int64_t pixels = int64_t(g.n) * g.oh * g.ow;
+    const int O = g.cout * (g.k + 1);
+    hipStream_t s = as_stream(stream);
+    if (pixels == 0) {
+        if (int rc = ehip_fill_f32(dweight, int64_t(g.cout) * g.k, 0.0f, stream)) return rc;
+        return dbias ? ehip_fill_f32(dbias, g.cout, 0.0f, stream) : EHIP_OK;
+    }
+    // Chunk size: about 256 chunks to fill the CUs, 16..256 pixels each, and the
+    // staged chunk within the LDS budget.
+    int P = 16;
+    while (P < 256 && ceil_div(pixels, P) > 256) P *= 2;
+    const auto lds_for = [&](int p) {
+        return (size_t(g.cout) + size_t(g.k) + 1) * size_t(p + 1) * sizeof(float) +
+               kThreads * sizeof(float);
+    };
+    while (P > 1 && lds_for(P) > kMaxLds) P /= 2;
+    const int64_t chunks = ceil_div(pixels, P);
+    if (chunks > 0x7fffffff) return fail(EHIP_EINVAL, "conv2d_backward_weight: too many pixels");
+    float* partial = static_cast<float*>(scratch(size_t(chunks) * O * sizeof(float)));
+    if (partial == nullptr) return EHIP_ENOMEM;
+    EHIP_LAUNCH("conv2d_weight_partial", conv_weight_partial, dim3(unsigned(chunks)),
+                dim3(kThreads), lds_for(P), s, x, grad_out, partial, g, P);
+    int rl = 1;
+    while (rl < 16 && rl * 8 < chunks) rl *= 2;
+    const int per_block = 256 / rl;
+    EHIP_LAUNCH("conv2d_weight_reduce", conv_weight_reduce, dim3(unsigned(ceil_div(O, per_block))),
+                dim3(256), 0, s, partial, dweight, dbias, g.cout, g.k, int(chunks), rl);
+    return EHIP_OK;
+}
+
+}  // extern "C"

@@ -107,15 +107,6 @@ __global__ __launch_bounds__(kThreads) void im2col_kernel(const float* __restric
     }
 }
 
-// First and last window index along one axis whose window covers position p.
-__device__ __forceinline__ void covering(int64_t p, int64_t pad, int64_t k, int64_t s,
-                                         int64_t out, int64_t& lo, int64_t& hi) {
-    const int64_t t = p + pad - (k - 1);
-    lo = t <= 0 ? 0 : (t + s - 1) / s;
-    hi = (p + pad) / s;
-    if (hi > out - 1) hi = out - 1;
-}
-
 // One thread per input pixel, summing its windows with oh then ow ascending
 // from zero: the per-pixel order of src/conv.cpp:183-214.
 __global__ __launch_bounds__(kThreads) void col2im_kernel(const float* __restrict__ cols,
@@ -245,19 +236,6 @@ unsigned grid_for(int64_t n) {
     return unsigned(g);
 }
 
-int check_window(const char* name, const ehip_window_t* w) {
-    if (w == nullptr) return fail(EHIP_EINVAL, "%s: null window", name);
-    if (w->batch < 0 || w->channels <= 0 || w->height <= 0 || w->width <= 0 ||
-        w->kernel_h <= 0 || w->kernel_w <= 0 || w->stride <= 0 || w->padding < 0)
-        return fail(EHIP_EINVAL, "%s: bad window geometry", name);
-    const int64_t oh = (w->height + 2 * w->padding - w->kernel_h) / w->stride + 1;
-    const int64_t ow = (w->width + 2 * w->padding - w->kernel_w) / w->stride + 1;
-    if (w->height + 2 * w->padding < w->kernel_h || w->width + 2 * w->padding < w->kernel_w ||
-        oh != w->out_h || ow != w->out_w)
-        return fail(EHIP_EINVAL, "%s: out_h/out_w do not match the window", name);
-    return EHIP_OK;
-}
-
 template <typename Idx>
 int maxpool_forward(const char* name, const float* x, float* y, Idx* argmax,
                     const ehip_window_t* w, int64_t max_in, void* stream) {
@@ -292,6 +270,20 @@ int maxpool_backward(const char* name, const Idx* argmax, const float* g, float*
 }
 
 }  // namespace
+
+int check_window(const char* name, const ehip_window_t* w) {
+    if (w == nullptr) return fail(EHIP_EINVAL, "%s: null window", name);
+    if (w->batch < 0 || w->channels <= 0 || w->height <= 0 || w->width <= 0 ||
+        w->kernel_h <= 0 || w->kernel_w <= 0 || w->stride <= 0 || w->padding < 0)
+        return fail(EHIP_EINVAL, "%s: bad window geometry", name);
+    const int64_t oh = (w->height + 2 * w->padding - w->kernel_h) / w->stride + 1;
+    const int64_t ow = (w->width + 2 * w->padding - w->kernel_w) / w->stride + 1;
+    if (w->height + 2 * w->padding < w->kernel_h || w->width + 2 * w->padding < w->kernel_w ||
+        oh != w->out_h || ow != w->out_w)
+        return fail(EHIP_EINVAL, "%s: out_h/out_w do not match the window", name);
+    return EHIP_OK;
+}
+
 }  // namespace ehip
 
 using namespace ehip;

@@ -84,6 +84,10 @@ _SIGS = {
     "ehip_maxpool_backward_f32": [_vp, _vp, _vp, C.POINTER(Window), _vp],
     "ehip_maxpool_fidx_f32": [_vp, _vp, _vp, C.POINTER(Window), _vp],
     "ehip_maxpool_backward_fidx_f32": [_vp, _vp, _vp, C.POINTER(Window), _vp],
+    "ehip_conv2d_direct_supported": [C.POINTER(Window), _i64],
+    "ehip_conv2d_forward_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
+    "ehip_conv2d_backward_input_f32": [_vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
+    "ehip_conv2d_backward_weight_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_select_rows_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "ehip_scatter_add_rows_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp],
     "ehip_sum_axis_f32": [_vp, _vp, _i64, _i64, _i64, _vp],
@@ -308,6 +312,36 @@ class Backend:
         self.ok(f(self.p(argmax), self.p(g), self.p(dx), C.byref(w), self.stream()),
                 "maxpool_backward")
         return dx
+
+    def conv2d(self, x, weight, bias, stride, pad):
+        """Direct convolution, NCHW in and out; bias may be None."""
+        co, ci, kh, kw = weight.shape
+        w = window(*x.shape, kh, kw, stride, pad)
+        out = self.f32((w.batch, co, w.out_h, w.out_w))
+        self.ok(self.lib.ehip_conv2d_forward_f32(self.p(x), self.p(weight),
+                                                 self.p(bias) if bias is not None else None,
+                                                 self.p(out), C.byref(w), co, self.stream()),
+                "conv2d_forward")
+        return out
+
+    def conv2d_backward_input(self, g, weight, in_shape, stride, pad):
+        co, ci, kh, kw = weight.shape
+        w = window(*in_shape, kh, kw, stride, pad)
+        dx = self.f32(in_shape)
+        self.ok(self.lib.ehip_conv2d_backward_input_f32(self.p(g), self.p(weight), self.p(dx),
+                                                        C.byref(w), co, self.stream()),
+                "conv2d_backward_input")
+        return dx
+
+    def conv2d_backward_weight(self, x, g, weight_shape, stride, pad, bias=True):
+        co, ci, kh, kw = weight_shape
+        w = window(*x.shape, kh, kw, stride, pad)
+        dw = self.f32(weight_shape)
+        db = self.f32((co,)) if bias else None
+        self.ok(self.lib.ehip_conv2d_backward_weight_f32(
+            self.p(x), self.p(g), self.p(dw), self.p(db) if bias else None, C.byref(w), co,
+            self.stream()), "conv2d_backward_weight")
+        return dw, db
 
     def select_rows(self, x, idx):
         rs = x.numel() // x.shape[0]

@@ -1,5 +1,5 @@
-// conv.cpp -- im2col/col2im, Conv2d as im2col + one GEMM, MaxPool2d and
-// Flatten (the reference's src/conv.cpp).
+// conv.cpp -- im2col/col2im, Conv2d (direct kernels for narrow layers, im2col +
+// one GEMM otherwise), MaxPool2d and Flatten (the reference's src/conv.cpp).
 #include "engine/conv.hpp"
 
 #include <cmath>
@@ -51,6 +51,54 @@ Tensor im2col_node(const Tensor& input, const Window2d& window) {
         input_copy.add_grad(col2im(g, in_shape, win));
     };
     return cols;
+}
+
+// The direct convolution node (narrow layers): one forward kernel, and a
+// backward that makes the input gradient (when the input needs one) and the
+// weight and bias gradients (one fused pass plus an ordered reduction). The
+// values are those of the reference's composition (src/conv.cpp:280-338):
+// forward and input gradient bit for bit, weight and bias gradients within
+// the tolerance of their long sums.
+Tensor conv2d_direct(const Tensor& input, const Tensor& weight, const Tensor& bias,
+                     bool use_bias, const ehip_window_t& w) {
+    const size_t co = weight.shape()[0];
+    Tensor out({size_t(w.batch), co, size_t(w.out_h), size_t(w.out_w)}, 0.0f, false);
+    hip::check(ehip_conv2d_forward_f32(dptr(input), dptr(weight), use_bias ? dptr(bias) : nullptr,
+                                       dout(out), &w, int64_t(co), nullptr),
+               "conv2d");
+    const bool need_x = input.requires_grad();
+    const bool need_w = weight.requires_grad();
+    const bool need_b = use_bias && bias.requires_grad();
+    if (!track(need_x || need_w || need_b)) return out;
+    out.set_requires_grad(true);
+    auto& parents = out.get_impl()->parents;
+    if (need_x) parents.push_back(input.get_impl());
+    if (need_w) parents.push_back(weight.get_impl());
+    if (need_b) parents.push_back(bias.get_impl());
+    Tensor x_copy = input, w_copy = weight, b_copy = bias;
+    out.get_impl()->backward_fn = [x_copy, w_copy, b_copy, need_x, need_w, need_b,
+                                   w](const Tensor& g) mutable {
+        const int64_t co = int64_t(w_copy.shape()[0]);
+        if (need_x) {
+            Tensor dx(x_copy.shape(), 0.0f, false);
+            hip::check(ehip_conv2d_backward_input_f32(dptr(g), dptr(w_copy), dout(dx), &w, co,
+                                                      nullptr),
+                       "conv2d backward input");
+            x_copy.add_grad(dx);
+        }
+        if (need_w || need_b) {
+            Tensor dw(w_copy.shape(), 0.0f, false);
+            Tensor db;
+            if (need_b) db = Tensor({size_t(co)}, 0.0f, false);
+            hip::check(ehip_conv2d_backward_weight_f32(dptr(x_copy), dptr(g), dout(dw),
+                                                       need_b ? dout(db) : nullptr, &w, co,
+                                                       nullptr),
+                       "conv2d backward weight");
+            if (need_w) w_copy.add_grad(dw);
+            if (need_b) b_copy.add_grad(db);
+        }
+    };
+    return out;
 }
 
 }  // namespace
@@ -106,9 +154,10 @@ Conv2d::Conv2d(size_t in_channels, size_t out_channels, const Window2d& window, 
     bias_ = Tensor({out_channels}, 0.0f, use_bias);
 }
 
-// im2col -> cols (W reshaped to (outC, K))^T -> + bias -> (N, outC, oH, oW)
-// (src/conv.cpp:280-338). The product reads W in place through the GEMM's
-// transposed mode, so its derivative needs no transpose either.
+// Narrow layers take the direct kernels. Wider ones compose as the reference
+// does: im2col -> cols (W reshaped to (outC, K))^T -> + bias -> (N, outC, oH, oW)
+// (src/conv.cpp:280-338), the product on MFMA reading W in place through the
+// GEMM's transposed mode, so its derivative needs no transpose either.
 Tensor Conv2d::forward(const Tensor& input) {
     if (input.ndim() != 4)
         throw std::invalid_argument("Conv2d expects a 4D volume (N, C, H, W), received " +
@@ -117,8 +166,12 @@ Tensor Conv2d::forward(const Tensor& input) {
         throw std::invalid_argument("Conv2d with in_channels=" + std::to_string(in_channels_) +
                                     " received an input " + input.shape_str() + ".");
     const size_t N = input.shape()[0], H = input.shape()[2], W = input.shape()[3];
+    window_.validate(H, W);
     const size_t oH = window_.out_h(H), oW = window_.out_w(W);
     const size_t K = in_channels_ * window_.kernel_h * window_.kernel_w;
+    const ehip_window_t w = window_of(input.shape(), window_);
+    if (ehip_conv2d_direct_supported(&w, int64_t(out_channels_)))
+        return conv2d_direct(input, weight_, bias_, use_bias_, w);
     Tensor cols = im2col_node(input, window_);
     Tensor out = ops::matmul_nt(cols, weight_.reshape({out_channels_, K}));
     if (use_bias_) out = out + bias_;

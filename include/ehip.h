@@ -273,6 +273,35 @@ int ehip_maxpool_fidx_f32(const float* x, float* y, float* argmax, const ehip_wi
 int ehip_maxpool_backward_fidx_f32(const float* argmax, const float* g, float* dx,
                                    const ehip_window_t* w, void* stream);
 
+/* Direct convolution for narrow layers (out_channels * C_in * kH * kW <= 8192,
+ * ehip_conv2d_direct_supported() says 1): x (N, C_in, H, W), weight
+ * (out_channels, C_in, kH, kW), output (N, out_channels, oH, oW), all dense
+ * row-major; the window's channels field is C_in. Together the three replace
+ * the node chain Conv2d::forward builds -- im2col, the product with the
+ * transposed weight, the broadcast bias add, the (N, oH*oW, C) -> (N, C, oH*oW)
+ * permute -- and its autograd backward (src/conv.cpp:280-338; im2col/col2im
+ * src/conv.cpp:61-217), with no columns in HBM and no permute.
+ *   forward: out = sum_k x_col[k] w[co][k] in k order from zero, zero inputs
+ *     skipped, then + bias[co] (bias may be NULL): the reference's i-k-j loop
+ *     (src/tensor_ops.cpp:553-560) and bias add, bit-exact.
+ *   backward_input: dx = col2im of (grad_out . w), each column entry a co-order
+ *     sum with zero gradients skipped and the windows of a pixel added in
+ *     (oh, ow) order from zero: bit-exact with the reference's two steps.
+ *     dx is overwritten.
+ *   backward_weight: dweight[co][k] = sum over pixels of grad_out . x_col[k],
+ *     dbias[co] = sum over pixels of grad_out (dbias may be NULL), overwritten;
+ *     chunked partials reduced in a fixed order: deterministic, within the
+ *     K-term tolerance of the reference's serial sums.
+ * Wider layers are refused with EHIP_EINVAL (use im2col + ehip_gemm_f32). */
+int ehip_conv2d_direct_supported(const ehip_window_t* w, int64_t out_channels);
+int ehip_conv2d_forward_f32(const float* x, const float* weight, const float* bias, float* out,
+                            const ehip_window_t* w, int64_t out_channels, void* stream);
+int ehip_conv2d_backward_input_f32(const float* grad_out, const float* weight, float* dx,
+                                   const ehip_window_t* w, int64_t out_channels, void* stream);
+int ehip_conv2d_backward_weight_f32(const float* x, const float* grad_out, float* dweight,
+                                    float* dbias, const ehip_window_t* w, int64_t out_channels,
+                                    void* stream);
+
 /* out[i] = x[idx[i]] row by row (rows of row_size floats); an index outside
  * [0, n_rows) yields a row of NaN instead of a read out of bounds.
  * Tensor::select_rows forward (src/tensor.cpp:556-585). Bit-exact. */

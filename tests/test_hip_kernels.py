@@ -315,6 +315,66 @@ def test_im2col_col2im_exact(hip, orc, shape, k, stride, pad):
           orc.col2im(g, shape, k, k, stride, pad), "col2im")
 
 
+CONV_CASES = [((64, 1, 28, 28), 8, 3, 1, 1), ((64, 8, 14, 14), 16, 3, 1, 1),
+              ((2, 3, 9, 7), 5, 3, 2, 0), ((3, 2, 11, 13), 4, 5, 3, 2), ((1, 4, 6, 6), 7, 2, 2, 0),
+              ((2, 5, 8, 8), 3, 1, 1, 0),
+              ((1, 2, 3, 2100), 4, 3, 1, 1)]  # rows too wide for an LDS tile: per-pixel kernels
+
+
+@pytest.mark.parametrize("shape,co,k,stride,pad", CONV_CASES)
+@pytest.mark.parametrize("bias", [True, False])
+def test_conv2d_direct(hip, orc, shape, co, k, stride, pad, bias):
+    """The direct kernels against the reference's composition (im2col, product with the
+    transposed weight, bias add, permute; autograd backward), replayed on the oracle:
+    forward and input gradient bit for bit, weight and bias gradients within the bound of
+    any fp32 summation order of their N oH oW terms."""
+    import _compose as K
+    print_case("conv2d-direct", shape, co, k, stride, pad, bias)
+    r = rng(sum(shape) * 13 + co * 7 + k + stride + pad)
+    x = randn(r, *shape)
+    x[..., ::5] = 0.0  # zero inputs take the reference's skip
+    w = randn(r, co, shape[1], k, k) * 0.5
+    b = randn(r, co) if bias else None
+    y, cache = K.conv2d_fwd(orc, x, w, b, stride, pad)
+    Y = hip.conv2d(dev(x), dev(w), dev(b) if bias else None, stride, pad)
+    exact(host(Y), y, "forward")
+    g = randn(r, *y.shape)
+    g[:, :, ::3] = 0.0  # zero gradients take the skip of the dcols product
+    dx, dw, db = K.conv2d_bwd(orc, g, cache)
+    exact(host(hip.conv2d_backward_input(dev(g), dev(w), shape, stride, pad)), dx, "dx")
+    DW, DB = hip.conv2d_backward_weight(dev(x), dev(g), w.shape, stride, pad, bias)
+    terms = y.shape[0] * y.shape[2] * y.shape[3]
+    ref_close(host(DW), dw, k_tol(terms), "dweight")
+    # rigorous per-element bound against fp64: (terms + 2) u sum |g| |x_col|
+    cols = orc.im2col(x, k, k, stride, pad).astype(np.float64)
+    g2 = g.reshape(shape[0], co, -1).transpose(0, 2, 1).reshape(-1, co).astype(np.float64)
+    exact_dw = (g2.T @ cols).reshape(w.shape)
+    bound = (terms + 2) * 2.0 ** -24 * (np.abs(g2).T @ np.abs(cols)).reshape(w.shape)
+    assert np.all(np.abs(host(DW) - exact_dw) <= bound + 1e-30), "dweight beyond the fp32 bound"
+    if bias:
+        ref_close(host(DB), db, k_tol(terms), "dbias")
+        bound_b = (terms + 2) * 2.0 ** -24 * np.abs(g2).sum(axis=0)
+        assert np.all(np.abs(host(DB) - g2.sum(axis=0)) <= bound_b + 1e-30), "dbias bound"
+    # deterministic: a second call gives the same bits
+    DW2, _ = hip.conv2d_backward_weight(dev(x), dev(g), w.shape, stride, pad, bias)
+    exact(host(DW2), host(DW), "dweight repeat")
+
+
+def test_conv2d_direct_refuses_wide_layers(hip):
+    import ctypes
+    import ehip as E
+    print_case("conv2d-wide")
+    w = E.window(1, 64, 8, 8, 3, 3, 1, 1)
+    assert hip.lib.ehip_conv2d_direct_supported(ctypes.byref(w), 256) == 0
+    assert hip.lib.ehip_conv2d_direct_supported(ctypes.byref(w), 8) == 1
+    x = dev(np.zeros(16, np.float32))
+    before = hip.launched()
+    with pytest.raises(RuntimeError, match="direct path"):
+        hip.ok(hip.lib.ehip_conv2d_forward_f32(hip.p(x), hip.p(x), None, hip.p(x),
+                                               ctypes.byref(w), 256, hip.stream()), "conv")
+    assert hip.launched() == before
+
+
 @pytest.mark.parametrize("shape,k,stride", [((64, 8, 28, 28), 2, 2), ((64, 16, 14, 14), 2, 2),
                                             ((2, 3, 9, 9), 3, 2), ((2, 2, 7, 7), 3, 1)])
 @pytest.mark.parametrize("float_index", [False, True])
