@@ -144,24 +144,28 @@ __global__ __launch_bounds__(kThreads) void conv_backward_input_direct(
 }
 
 // Staging helper: copies n elements into LDS, U independent global loads in
-// flight per thread before any LDS store. value(e) returns the element e (and
-// does its own bounds checks); dst(e) is its LDS slot.
-template <int U, class Value, class Dst>
-__device__ __forceinline__ void stage(int n, Value value, Dst dst) {
-    for (int base = 0; base < n; base += U * kThreads) {
+// flight per thread before any LDS store. at(e, slot) returns element e (doing
+// its own bounds checks) and sets its LDS slot in `base`.
+template <int U, class At>
+__device__ __forceinline__ void stage(int n, float* base, At at) {
+    for (int first = 0; first < n; first += U * kThreads) {
         float v[U];
+        int slot[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int e = base + u * kThreads + int(threadIdx.x);
-            v[u] = e < n ? value(e) : 0.0f;
+            const int e = first + u * kThreads + int(threadIdx.x);
+            slot[u] = -1;
+            v[u] = e < n ? at(e, slot[u]) : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int e = base + u * kThreads + int(threadIdx.x);
-            if (e < n) *dst(e) = v[u];
-        }
+        for (int u = 0; u < U; ++u)
+            if (slot[u] >= 0) base[slot[u]] = v[u];
     }
 }
+
+// LDS pitches: odd, so rows, planes and channels that are a power-of-two
+// multiple apart do not fall in the same bank.
+__device__ __forceinline__ int odd(int v) { return v | 1; }
 
 // Forward over a tile of `rows` output rows of one image and CG output
 // channels (blockIdx.y). The input rows the tile reads, zero-padded on every
@@ -186,29 +190,25 @@ __global__ __launch_bounds__(kThreads) void conv_forward_tiled(const float* __re
     const int oh1 = min(oh0 + rows, g.oh);
     const int r0 = oh0 * g.stride - g.pad;               // first input row read
     const int rows_in = (oh1 - oh0 - 1) * g.stride + kh;
-    const int wp = g.w + 2 * g.pad;                      // padded row pitch
+    const int wp = g.w + 2 * g.pad;                      // padded row width
+    const int wps = odd(wp), plane_s = odd(rows_in * wps); // LDS pitches
     float* w_s = sm;                                     // [K][CG]
-    float* x_s = sm + CG * g.k;                          // [cin][rows_in][wp]
+    float* x_s = sm + CG * g.k;                          // [cin][rows_in][wps]
     const float* xn = x + int64_t(n) * g.cin * g.h * g.w;
     const int plane_in = rows_in * wp;
-    stage<4>(
-        CG * g.k,
-        [&](int e) {
-            const int co = co0 + e % CG;
-            return co < g.cout ? wt[co * g.k + e / CG] : 0.0f;
-        },
-        [&](int e) { return w_s + e; });
-    stage<8>(
-        g.cin * plane_in,
-        [&](int e) {
-            const unsigned ci = unsigned(e) / unsigned(plane_in);
-            const unsigned rem = unsigned(e) - ci * unsigned(plane_in);
-            const unsigned rr = rem / unsigned(wp);
-            const int h = r0 + int(rr), v = int(rem - rr * unsigned(wp)) - g.pad;
-            return (h >= 0 && h < g.h && v >= 0 && v < g.w) ? xn[(int(ci) * g.h + h) * g.w + v]
-                                                            : 0.0f;
-        },
-        [&](int e) { return x_s + e; });
+    stage<4>(CG * g.k, w_s, [&](int e, int& slot) {
+        const int co = co0 + e % CG;
+        slot = e;
+        return co < g.cout ? wt[co * g.k + e / CG] : 0.0f;
+    });
+    stage<8>(g.cin * plane_in, x_s, [&](int e, int& slot) {
+        const unsigned ci = unsigned(e) / unsigned(plane_in);
+        const unsigned rem = unsigned(e) - ci * unsigned(plane_in);
+        const unsigned rr = rem / unsigned(wp), cc = rem - rr * unsigned(wp);
+        slot = int(ci) * plane_s + int(rr) * wps + int(cc);
+        const int h = r0 + int(rr), v = int(cc) - g.pad;
+        return (h >= 0 && h < g.h && v >= 0 && v < g.w) ? xn[(int(ci) * g.h + h) * g.w + v] : 0.0f;
+    });
     __syncthreads();
     const int npix = (oh1 - oh0) * g.ow;
     const int64_t plane = int64_t(g.oh) * g.ow;
@@ -219,11 +219,11 @@ __global__ __launch_bounds__(kThreads) void conv_forward_tiled(const float* __re
         for (int q = 0; q < CG; ++q) c[q] = 0.0f;
         const float* wk = w_s;
         for (int ci = 0; ci < g.cin; ++ci) {
-            const float* xr = x_s + (ci * rows_in + ohl * g.stride) * wp + ow * g.stride;
+            const float* xr = x_s + ci * plane_s + ohl * g.stride * wps + ow * g.stride;
 #pragma unroll
             for (int i = 0; i < (KH ? KH : 1); ++i) {
                 for (int ii = 0; ii < (KH ? 1 : kh); ++ii) {
-                    const float* xi = xr + (KH ? i : ii) * wp;
+                    const float* xi = xr + (KH ? i : ii) * wps;
 #pragma unroll
                     for (int j = 0; j < (KW ? KW : 1); ++j) {
                         for (int jj = 0; jj < (KW ? 1 : kw); ++jj, wk += CG) {
@@ -250,12 +250,27 @@ __global__ __launch_bounds__(kThreads) void conv_forward_tiled(const float* __re
     }
 }
 
+// First and last window index along one axis whose window covers position p,
+// in 32-bit arithmetic (stride 1 needs no division).
+__device__ __forceinline__ void cover32(int p, int pad, int k, int s, int out, int& lo, int& hi) {
+    const int t = p + pad - (k - 1);
+    if (s == 1) {
+        lo = t <= 0 ? 0 : t;
+        hi = p + pad;
+    } else {
+        lo = t <= 0 ? 0 : (t + s - 1) / s;
+        hi = (p + pad) / s;
+    }
+    if (hi > out - 1) hi = out - 1;
+}
+
 // Input gradient over a tile of `rows` input rows of one image and CG input
 // channels (blockIdx.y). The output-gradient rows whose windows cover the tile
-// (all out_channels) and the weights of the CG channels sit in LDS; each
-// thread computes whole input elements in the order of
-// conv_backward_input_direct (zero gradients skipped by a select after an
-// unconditional multiply-add). blockIdx.x = n * tiles + tile.
+// (all out_channels) and the weights of the CG channels (laid out
+// [tap][cout][CG]) sit in LDS; each thread computes one input pixel for all
+// CG channels, every channel in the order of conv_backward_input_direct (zero
+// gradients skipped by a select after an unconditional multiply-add).
+// blockIdx.x = n * tiles + tile.
 template <int CG>
 __global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
     const float* __restrict__ gout, const float* __restrict__ wt, float* __restrict__ dx, Geo g,
@@ -265,76 +280,208 @@ __global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
     const int ci0 = int(blockIdx.y) * CG;
     const int h0 = tile * rows;
     const int h1 = min(h0 + rows, g.h);
-    int64_t lo, hi, lo2, hi2;
-    covering(h0, g.pad, g.kh, g.stride, g.oh, lo, hi);
-    covering(h1 - 1, g.pad, g.kh, g.stride, g.oh, lo2, hi2);
-    const int oh_first = int(lo);
-    const int oh_rows = max(0, int(hi2) - oh_first + 1);
+    int lo, hi, lo2, hi2;
+    cover32(h0, g.pad, g.kh, g.stride, g.oh, lo, hi);
+    cover32(h1 - 1, g.pad, g.kh, g.stride, g.oh, lo2, hi2);
+    const int oh_first = lo;
+    const int oh_rows = max(0, hi2 - oh_first + 1);
     const int khw = g.kh * g.kw;
     const int gplane = oh_rows * g.ow;
+    const int gplane_s = odd(gplane), tap_s = odd(g.cout * CG);   // LDS pitches
     float* g_s = sm;                                   // [cout][oh_rows][ow]
-    float* w_s = sm + g.cout * gplane;                 // [CG][kh][kw][cout]
+    float* w_s = sm + g.cout * gplane_s;               // [tap][cout][CG]
     const int64_t plane = int64_t(g.oh) * g.ow;
     const float* gn = gout + int64_t(n) * g.cout * plane + int64_t(oh_first) * g.ow;
-    stage<8>(
-        g.cout * gplane,
-        [&](int e) {
-            const unsigned co = unsigned(e) / unsigned(gplane);
-            return gn[int64_t(co) * plane + (unsigned(e) - co * unsigned(gplane))];
-        },
-        [&](int e) { return g_s + e; });
-    stage<4>(
-        CG * khw * g.cout,
-        [&](int e) {
-            const int co = e % g.cout, r = e / g.cout;    // r = cl * khw + tap
-            const int ci = ci0 + r / khw;
-            return ci < g.cin ? wt[(co * g.cin + ci) * khw + r % khw] : 0.0f;
-        },
-        [&](int e) { return w_s + e; });
+    stage<8>(g.cout * gplane, g_s, [&](int e, int& slot) {
+        const unsigned co = unsigned(e) / unsigned(gplane);
+        const unsigned r = unsigned(e) - co * unsigned(gplane);
+        slot = int(co) * gplane_s + int(r);
+        return gn[int64_t(co) * plane + r];
+    });
+    stage<4>(khw * g.cout * CG, w_s, [&](int e, int& slot) {
+        const int cl = e % CG, r = e / CG;             // r = tap * cout + co
+        const int co = r % g.cout, tap = r / g.cout;
+        const int ci = ci0 + cl;
+        slot = tap * tap_s + co * CG + cl;
+        return ci < g.cin ? wt[(co * g.cin + ci) * khw + tap] : 0.0f;
+    });
     __syncthreads();
     const int band = (h1 - h0) * g.w;
-    const int nel = CG * band;
-    for (int e = threadIdx.x; e < nel; e += kThreads) {
-        const int cl = e / band, rem = e - cl * band;
-        const int ci = ci0 + cl;
-        if (ci >= g.cin) continue;
-        const int hl = rem / g.w;
-        const int h = h0 + hl, v = rem - hl * g.w;
-        int64_t oh_lo, oh_hi, ow_lo, ow_hi;
-        covering(h, g.pad, g.kh, g.stride, g.oh, oh_lo, oh_hi);
-        covering(v, g.pad, g.kw, g.stride, g.ow, ow_lo, ow_hi);
-        const float* wc = w_s + cl * khw * g.cout;
-        float acc = 0.0f;
-        for (int oh = int(oh_lo); oh <= int(oh_hi); ++oh) {
+    for (int e = threadIdx.x; e < band; e += kThreads) {
+        const int hl = e / g.w;
+        const int h = h0 + hl, v = e - hl * g.w;
+        int oh_lo, oh_hi, ow_lo, ow_hi;
+        cover32(h, g.pad, g.kh, g.stride, g.oh, oh_lo, oh_hi);
+        cover32(v, g.pad, g.kw, g.stride, g.ow, ow_lo, ow_hi);
+        float acc[CG];
+#pragma unroll
+        for (int cl = 0; cl < CG; ++cl) acc[cl] = 0.0f;
+        for (int oh = oh_lo; oh <= oh_hi; ++oh) {
             const int i = h + g.pad - oh * g.stride;
-            for (int ow = int(ow_lo); ow <= int(ow_hi); ++ow) {
+            for (int ow = ow_lo; ow <= ow_hi; ++ow) {
                 const int j = v + g.pad - ow * g.stride;
                 const float* gp = g_s + (oh - oh_first) * g.ow + ow;
-                const float* wp = wc + (i * g.kw + j) * g.cout;
-                float d = 0.0f;
+                const float* wp = w_s + (i * g.kw + j) * tap_s;
+                float d[CG];
+#pragma unroll
+                for (int cl = 0; cl < CG; ++cl) d[cl] = 0.0f;
                 int co = 0;
-                for (; co + 4 <= g.cout; co += 4) {
-                    float gv[4], wv[4];
+                for (; co + 8 <= g.cout; co += 8) {
+                    float gv[8], wv[8][CG];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        gv[u] = gp[(co + u) * gplane];
-                        wv[u] = wp[co + u];
+                    for (int u = 0; u < 8; ++u) {
+                        gv[u] = gp[(co + u) * gplane_s];
+#pragma unroll
+                        for (int cl = 0; cl < CG; ++cl) wv[u][cl] = wp[(co + u) * CG + cl];
                     }
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const float t = d + gv[u] * wv[u];
-                        d = (gv[u] != 0.0f) ? t : d;
-                    }
+                    for (int u = 0; u < 8; ++u)
+#pragma unroll
+                        for (int cl = 0; cl < CG; ++cl) {
+                            const float t = d[cl] + gv[u] * wv[u][cl];
+                            d[cl] = (gv[u] != 0.0f) ? t : d[cl];
+                        }
                 }
                 for (; co < g.cout; ++co) {
-                    const float gv = gp[co * gplane];
-                    const float t = d + gv * wp[co];
-                    d = (gv != 0.0f) ? t : d;
+                    const float gv = gp[co * gplane_s];
+#pragma unroll
+                    for (int cl = 0; cl < CG; ++cl) {
+                        const float t = d[cl] + gv * wp[co * CG + cl];
+                        d[cl] = (gv != 0.0f) ? t : d[cl];
+                    }
                 }
-                acc += d;
+#pragma unroll
+                for (int cl = 0; cl < CG; ++cl) acc[cl] += d[cl];
             }
         }
-        dx[((int64_t(n) * g.cin + ci) * g.h + h) * g.w + v] = acc;
+#pragma unroll
+        for (int cl = 0; cl < CG; ++cl)
+            if (ci0 + cl < g.cin)
+                dx[((int64_t(n) * g.cin + ci0 + cl) * g.h + h) * g.w + v] = acc[cl];
+    }
+}
+
+// Weight and bias gradient partials over a band of `rows` output rows of one
+// image: the input rows the band reads (zero-padded) and its output gradient
+// rows are staged in LDS; a thread owns a CT x KT tile of (output channel,
+// column k) sums -- column K is the bias, whose "input" is 1 -- over one of PG
+// pixel groups, and the groups are combined in group order. partial[block][o],
+// o = co (K + 1) + k, is then reduced over blocks by conv_weight_reduce. The
+// order of every sum depends only on the shape.
+template <int CT, int KT>
+__global__ __launch_bounds__(kThreads) void conv_weight_band(const float* __restrict__ x,
+                                                             const float* __restrict__ gout,
+                                                             float* __restrict__ partial, Geo g,
+                                                             int rows, int bands) {
+    extern __shared__ float sm[];
+    const int n = int(blockIdx.x) / bands, band = int(blockIdx.x) % bands;
+    const int oh0 = band * rows;
+    const int oh1 = min(oh0 + rows, g.oh);
+    const int np = (oh1 - oh0) * g.ow;
+    const int rows_in = (oh1 - oh0 - 1) * g.stride + g.kh;
+    const int wp = g.w + 2 * g.pad;
+    const int K1 = g.k + 1;
+    const int tiles_k = (K1 + KT - 1) / KT, tiles = ((g.cout + CT - 1) / CT) * tiles_k;
+    const int PG = tiles >= kThreads ? 1 : kThreads / tiles;
+    const int wps = odd(wp), plane_s = odd(rows_in * wps), nps = odd(np);   // LDS pitches
+    float* x_s = sm;                                   // [cin][rows_in][wps]
+    float* dy_s = x_s + g.cin * plane_s;               // [cout][nps]
+    float* red = dy_s + g.cout * nps;                  // [PG][tiles][CT * KT]
+    const int r0 = oh0 * g.stride - g.pad;
+    const float* xn = x + int64_t(n) * g.cin * g.h * g.w;
+    const int plane_in = rows_in * wp;
+    stage<8>(g.cin * plane_in, x_s, [&](int e, int& slot) {
+        const unsigned ci = unsigned(e) / unsigned(plane_in);
+        const unsigned rem = unsigned(e) - ci * unsigned(plane_in);
+        const unsigned rr = rem / unsigned(wp), cc = rem - rr * unsigned(wp);
+        slot = int(ci) * plane_s + int(rr) * wps + int(cc);
+        const int h = r0 + int(rr), v = int(cc) - g.pad;
+        return (h >= 0 && h < g.h && v >= 0 && v < g.w) ? xn[(int(ci) * g.h + h) * g.w + v] : 0.0f;
+    });
+    const int64_t plane = int64_t(g.oh) * g.ow;
+    const float* gn = gout + int64_t(n) * g.cout * plane + int64_t(oh0) * g.ow;
+    stage<8>(g.cout * np, dy_s, [&](int e, int& slot) {
+        const unsigned co = unsigned(e) / unsigned(np);
+        const unsigned r = unsigned(e) - co * unsigned(np);
+        slot = int(co) * nps + int(r);
+        return gn[int64_t(co) * plane + r];
+    });
+    __syncthreads();
+    const int khw = g.kh * g.kw;
+    for (int tbase = 0; tbase < tiles; tbase += kThreads) {
+        const int t = tbase + int(threadIdx.x) % (tiles >= kThreads ? kThreads : tiles);
+        const int pg = tiles >= kThreads ? 0 : int(threadIdx.x) / tiles;
+        const bool active = t < tiles && pg < PG;
+        float acc[CT][KT];
+#pragma unroll
+        for (int q = 0; q < CT; ++q)
+#pragma unroll
+            for (int kk = 0; kk < KT; ++kk) acc[q][kk] = 0.0f;
+        const int co_base = (t / tiles_k) * CT, k_base = (t % tiles_k) * KT;
+        int xoff[KT];   // offset of column k within the band for pixel (0, 0); -1 bias; -2 none
+#pragma unroll
+        for (int kk = 0; kk < KT; ++kk) {
+            const int k = k_base + kk;
+            if (k < g.k) {
+                const int ci = k / khw, ij = k - ci * khw;
+                const int i = ij / g.kw, j = ij - i * g.kw;
+                xoff[kk] = ci * plane_s + i * wps + j;
+            } else {
+                xoff[kk] = k == g.k ? -1 : -2;
+            }
+        }
+        if (active) {
+            int ohl = pg / g.ow, ow = pg - (pg / g.ow) * g.ow;
+            for (int p = pg; p < np; p += PG) {
+                const int pix = ohl * g.stride * wps + ow * g.stride;
+                float xv[KT], dv[CT];
+#pragma unroll
+                for (int kk = 0; kk < KT; ++kk)
+                    xv[kk] = xoff[kk] >= 0 ? x_s[xoff[kk] + pix] : (xoff[kk] == -1 ? 1.0f : 0.0f);
+#pragma unroll
+                for (int q = 0; q < CT; ++q)
+                    dv[q] = co_base + q < g.cout ? dy_s[(co_base + q) * nps + p] : 0.0f;
+#pragma unroll
+                for (int q = 0; q < CT; ++q)
+#pragma unroll
+                    for (int kk = 0; kk < KT; ++kk) acc[q][kk] = fmaf(dv[q], xv[kk], acc[q][kk]);
+                ow += PG;
+                while (ow >= g.ow) {
+                    ow -= g.ow;
+                    ++ohl;
+                }
+            }
+        }
+        if (PG > 1) {
+            // All PG groups park their tiles in LDS; every thread then adds the
+            // groups of a few outputs in group order.
+            if (active) {
+                float* r = red + (pg * tiles + t) * (CT * KT);
+#pragma unroll
+                for (int q = 0; q < CT; ++q)
+#pragma unroll
+                    for (int kk = 0; kk < KT; ++kk) r[q * KT + kk] = acc[q][kk];
+            }
+            __syncthreads();
+            float* pc = partial + int64_t(blockIdx.x) * g.cout * K1;
+            const int span = tiles * CT * KT;
+            for (int o = threadIdx.x; o < span; o += kThreads) {
+                float sum = red[o];
+                for (int g2 = 1; g2 < PG; ++g2) sum += red[g2 * span + o];
+                const int tt = o / (CT * KT), e = o % (CT * KT);
+                const int co = (tt / tiles_k) * CT + e / KT, k = (tt % tiles_k) * KT + e % KT;
+                if (co < g.cout && k < K1) pc[co * K1 + k] = sum;
+            }
+        } else if (active) {
+            float* pc = partial + int64_t(blockIdx.x) * g.cout * K1;
+#pragma unroll
+            for (int q = 0; q < CT; ++q)
+#pragma unroll
+                for (int kk = 0; kk < KT; ++kk) {
+                    const int co = co_base + q, k = k_base + kk;
+                    if (co < g.cout && k < K1) pc[co * K1 + k] = acc[q][kk];
+                }
+        }
     }
 }
 
@@ -357,35 +504,31 @@ __global__ __launch_bounds__(kThreads) void conv_weight_partial(const float* __r
     const int64_t pixels = int64_t(g.n) * g.oh * g.ow;
     const int64_t plane = int64_t(g.oh) * g.ow;
     const int64_t m0 = int64_t(blockIdx.x) * P;
-    stage<8>(
-        g.cout * P,
-        [&](int e) {
-            const int co = e / P, p = e - co * P;
-            const int64_t m = m0 + p;
-            if (m >= pixels) return 0.0f;
-            const unsigned mu = unsigned(m), pl = unsigned(plane);
-            const unsigned n = mu / pl, r = mu - n * pl;
-            return gout[(int64_t(n) * g.cout + co) * plane + r];
-        },
-        [&](int e) { return dy_s + (e / P) * ld + e % P; });
-    stage<8>(
-        K1 * P,
-        [&](int e) {
-            const int k = e / P, p = e - k * P;
-            const int64_t m = m0 + p;
-            if (m >= pixels) return 0.0f;
-            if (k == g.k) return 1.0f;
-            const unsigned mu = unsigned(m);
-            const unsigned t = mu / unsigned(g.ow), ow = mu - t * unsigned(g.ow);
-            const unsigned n = t / unsigned(g.oh), oh = t - n * unsigned(g.oh);
-            const int ij = k % (g.kh * g.kw), ci = k / (g.kh * g.kw);
-            const int i = ij / g.kw, j = ij - i * g.kw;
-            const int h = int(oh) * g.stride + i - g.pad, v = int(ow) * g.stride + j - g.pad;
-            return (h >= 0 && h < g.h && v >= 0 && v < g.w)
-                       ? x[((int64_t(n) * g.cin + ci) * g.h + h) * g.w + v]
-                       : 0.0f;
-        },
-        [&](int e) { return col_s + (e / P) * ld + e % P; });
+    stage<8>(g.cout * P, dy_s, [&](int e, int& slot) {
+        const int co = e / P, p = e - co * P;
+        slot = co * ld + p;
+        const int64_t m = m0 + p;
+        if (m >= pixels) return 0.0f;
+        const unsigned mu = unsigned(m), pl = unsigned(plane);
+        const unsigned n = mu / pl, r = mu - n * pl;
+        return gout[(int64_t(n) * g.cout + co) * plane + r];
+    });
+    stage<8>(K1 * P, col_s, [&](int e, int& slot) {
+        const int k = e / P, p = e - k * P;
+        slot = k * ld + p;
+        const int64_t m = m0 + p;
+        if (m >= pixels) return 0.0f;
+        if (k == g.k) return 1.0f;
+        const unsigned mu = unsigned(m);
+        const unsigned t = mu / unsigned(g.ow), ow = mu - t * unsigned(g.ow);
+        const unsigned n = t / unsigned(g.oh), oh = t - n * unsigned(g.oh);
+        const int ij = k % (g.kh * g.kw), ci = k / (g.kh * g.kw);
+        const int i = ij / g.kw, j = ij - i * g.kw;
+        const int h = int(oh) * g.stride + i - g.pad, v = int(ow) * g.stride + j - g.pad;
+        return (h >= 0 && h < g.h && v >= 0 && v < g.w)
+                   ? x[((int64_t(n) * g.cin + ci) * g.h + h) * g.w + v]
+                   : 0.0f;
+    });
     __syncthreads();
     const int O = g.cout * K1;
     float* pc = partial + int64_t(blockIdx.x) * O;
@@ -459,17 +602,22 @@ __global__ __launch_bounds__(256) void conv_weight_reduce(const float* __restric
 
 constexpr size_t kTileLds = 48 * 1024;   // bytes of LDS per tiled block
 
-// Rows per tile so that n * groups * tiles reaches about 256 blocks.
+// Rows per tile so that n * groups * tiles reaches about 512 blocks: two per
+// CU, whose waves hide each other's LDS and load latency (measured best for
+// the cfg2 layers over 128..3584 blocks).
 int rows_for_fill(int64_t n_groups, int extent) {
-    int64_t tiles = ceil_div(256, n_groups < 1 ? 1 : n_groups);
+    int64_t tiles = ceil_div(512, n_groups < 1 ? 1 : n_groups);
     if (tiles > extent) tiles = extent;
     if (tiles < 1) tiles = 1;
     return int(ceil_div(extent, tiles));
 }
 
+size_t odd_h(size_t v) { return v | 1; }
+
 size_t forward_lds(const Geo& g, int cg, int rows) {
     const size_t rows_in = size_t(rows - 1) * g.stride + g.kh;
-    return (size_t(g.cin) * rows_in * (g.w + 2 * g.pad) + size_t(cg) * g.k) * sizeof(float);
+    return (size_t(g.cin) * odd_h(rows_in * odd_h(g.w + 2 * g.pad)) + size_t(cg) * g.k) *
+           sizeof(float);
 }
 
 // Largest number of output-gradient rows any tile of `rows` input rows needs.
@@ -486,8 +634,30 @@ int grad_rows_for(const Geo& g, int rows) {
     return most;
 }
 
+// Tile edge (CT = KT = t) of the weight-gradient band kernel: the largest of
+// 4, 2, 1 that still gives at least 64 tiles, so at most four pixel groups
+// share a tile.
+int weight_tile(const Geo& g) {
+    for (int t : {4, 2}) {
+        if (ceil_div(g.cout, t) * ceil_div(g.k + 1, t) >= 64) return t;
+    }
+    return 1;
+}
+
+size_t weight_band_lds(const Geo& g, int rows) {
+    const size_t rows_in = size_t(rows - 1) * g.stride + g.kh;
+    const size_t np = size_t(rows) * g.ow;
+    const int t = weight_tile(g);
+    const size_t tiles = size_t(ceil_div(g.cout, t)) * size_t(ceil_div(g.k + 1, t));
+    const size_t red = tiles >= kThreads ? 0 : (kThreads / tiles) * tiles * size_t(t * t);
+    return (size_t(g.cin) * odd_h(rows_in * odd_h(g.w + 2 * g.pad)) + size_t(g.cout) * odd_h(np) +
+            red) *
+           sizeof(float);
+}
+
 size_t backward_input_lds(const Geo& g, int cg, int rows) {
-    return (size_t(g.cout) * grad_rows_for(g, rows) * g.ow + size_t(g.cout) * cg * g.kh * g.kw) *
+    return (size_t(g.cout) * odd_h(size_t(grad_rows_for(g, rows)) * g.ow) +
+            size_t(g.kh) * g.kw * odd_h(size_t(g.cout) * cg)) *
            sizeof(float);
 }
 
@@ -608,21 +778,47 @@ int ehip_conv2d_backward_weight_f32(const float* x, const float* grad_out, float
         if (int rc = ehip_fill_f32(dweight, int64_t(g.cout) * g.k, 0.0f, stream)) return rc;
         return dbias ? ehip_fill_f32(dbias, g.cout, 0.0f, stream) : EHIP_OK;
     }
-    // Chunk size: about 256 chunks to fill the CUs, 16..256 pixels each, and the
-    // staged chunk within the LDS budget.
-    int P = 16;
-    while (P < 256 && ceil_div(pixels, P) > 256) P *= 2;
-    const auto lds_for = [&](int p) {
-        return (size_t(g.cout) + size_t(g.k) + 1) * size_t(p + 1) * sizeof(float) +
-               kThreads * sizeof(float);
-    };
-    while (P > 1 && lds_for(P) > kMaxLds) P /= 2;
-    const int64_t chunks = ceil_div(pixels, P);
-    if (chunks > 0x7fffffff) return fail(EHIP_EINVAL, "conv2d_backward_weight: too many pixels");
-    float* partial = static_cast<float*>(scratch(size_t(chunks) * O * sizeof(float)));
-    if (partial == nullptr) return EHIP_ENOMEM;
-    EHIP_LAUNCH("conv2d_weight_partial", conv_weight_partial, dim3(unsigned(chunks)),
-                dim3(kThreads), lds_for(P), s, x, grad_out, partial, g, P);
+    int64_t chunks = 0;
+    float* partial = nullptr;
+    // Bands of output rows (one image each, about 256 blocks) when a band's input
+    // rows and gradient rows fit in LDS; otherwise chunks of P pixels with their
+    // im2col columns staged.
+    int rows = rows_for_fill(g.n, g.oh);
+    while (rows > 1 && weight_band_lds(g, rows) > kTileLds) rows = (rows + 1) / 2;
+    if (weight_band_lds(g, rows) <= kTileLds && int64_t(g.n) * g.oh <= 0x7fffffff) {
+        const int bands = int(ceil_div(g.oh, rows));
+        chunks = int64_t(g.n) * bands;
+        partial = static_cast<float*>(scratch(size_t(chunks) * O * sizeof(float)));
+        if (partial == nullptr) return EHIP_ENOMEM;
+        const size_t lds = weight_band_lds(g, rows);
+        const int t = weight_tile(g);
+        if (t == 4)
+            EHIP_LAUNCH("conv2d_weight_band", (conv_weight_band<4, 4>), dim3(unsigned(chunks)),
+                        dim3(kThreads), lds, s, x, grad_out, partial, g, rows, bands);
+        else if (t == 2)
+            EHIP_LAUNCH("conv2d_weight_band", (conv_weight_band<2, 2>), dim3(unsigned(chunks)),
+                        dim3(kThreads), lds, s, x, grad_out, partial, g, rows, bands);
+        else
+            EHIP_LAUNCH("conv2d_weight_band", (conv_weight_band<1, 1>), dim3(unsigned(chunks)),
+                        dim3(kThreads), lds, s, x, grad_out, partial, g, rows, bands);
+    } else {
+        // Chunk size: about 256 chunks to fill the CUs, 16..256 pixels each, and
+        // the staged chunk within the LDS budget.
+        int P = 16;
+        while (P < 256 && ceil_div(pixels, P) > 256) P *= 2;
+        const auto lds_for = [&](int p) {
+            return (size_t(g.cout) + size_t(g.k) + 1) * size_t(p + 1) * sizeof(float) +
+                   kThreads * sizeof(float);
+        };
+        while (P > 1 && lds_for(P) > kMaxLds) P /= 2;
+        chunks = ceil_div(pixels, P);
+        if (chunks > 0x7fffffff)
+            return fail(EHIP_EINVAL, "conv2d_backward_weight: too many pixels");
+        partial = static_cast<float*>(scratch(size_t(chunks) * O * sizeof(float)));
+        if (partial == nullptr) return EHIP_ENOMEM;
+        EHIP_LAUNCH("conv2d_weight_partial", conv_weight_partial, dim3(unsigned(chunks)),
+                    dim3(kThreads), lds_for(P), s, x, grad_out, partial, g, P);
+    }
     int rl = 1;
     while (rl < 16 && rl * 8 < chunks) rl *= 2;
     const int per_block = 256 / rl;

@@ -117,6 +117,126 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s) {
     return launch_cfg<64, 64, 16, 32, 32, TA, TB>(g, batch, !whole(64, 64, 16), s);
 }
 
+// ------------------------------------------------------------ small products
+//
+// Products too small to fill the chip with MFMA tiles are latency-bound: a
+// 64 x 784 x 10 layer is one 64 x 64 tile, split six ways along K, and spends
+// its time in load round trips rather than matrix math. Two vector kernels
+// take them instead:
+//   thread per output (K <= 128): the K products summed in k order from zero,
+//     zero A elements skipped -- the reference's i-k-j loop
+//     (src/tensor_ops.cpp:553-560) term for term, so the result is
+//     bit-identical to the CPU's;
+//   wave per output (few outputs, long K): lane l sums k = l, l + 64, ... and
+//     the lanes are combined by a fixed butterfly: deterministic, within the
+//     K-term tolerance.
+// Both apply beta as C = acc + beta C.
+
+// Measured on MI355X: the vector kernels win while the whole product is about
+// a million multiply-adds or less (cfg2's 64 x 784 x 10 layer: 4 + 6 + 4 us
+// against 16 + 11 + 5 for the MFMA tiles); larger ones go to MFMA, and K
+// beyond 2048 to split-K MFMA, which spreads one output over many CUs.
+constexpr int64_t kSmallThreadK = 128;
+constexpr int64_t kSmallThreadWork = int64_t(1) << 21;  // outputs * K
+constexpr int64_t kSmallWaveOutputs = 16384;
+constexpr int64_t kSmallWaveMaxK = 2048;
+constexpr int64_t kSmallWaveWork = int64_t(1) << 21;
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256) void gemm_small_thread(GemmArgs g, unsigned total) {
+    const unsigned n = unsigned(g.n), m = unsigned(g.m);
+    const unsigned step = gridDim.x * 256u;
+    for (unsigned o = blockIdx.x * 256u + threadIdx.x; o < total; o += step) {
+        const unsigned t = o / n, j = o - t * n;
+        const unsigned bi = t / m, i = t - bi * m;
+        const float* a = g.a + int64_t(bi) * g.stride_a + (TA ? int64_t(i) : int64_t(i) * g.lda);
+        const float* b = g.b + int64_t(bi) * g.stride_b + (TB ? int64_t(j) * g.ldb : int64_t(j));
+        const int64_t ak = TA ? g.lda : 1, bk = TB ? 1 : g.ldb;
+        float acc = 0.0f;
+        int64_t k = 0;
+        for (; k + 8 <= g.k; k += 8) {
+            float av[8], bv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                av[u] = a[(k + u) * ak];
+                bv[u] = b[(k + u) * bk];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float s = acc + av[u] * bv[u];
+                acc = av[u] != 0.0f ? s : acc;
+            }
+        }
+        for (; k < g.k; ++k) {
+            const float av = a[k * ak];
+            const float s = acc + av * b[k * bk];
+            acc = av != 0.0f ? s : acc;
+        }
+        float* dst = g.c + int64_t(bi) * g.stride_c + int64_t(i) * g.ldc + j;
+        if (g.beta != 0.0f) acc = acc + g.beta * *dst;
+        *dst = acc;
+    }
+}
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256) void gemm_small_wave(GemmArgs g, unsigned total) {
+    const unsigned lane = threadIdx.x % 64u;
+    const unsigned o = blockIdx.x * 4u + threadIdx.x / 64u;
+    if (o >= total) return;  // whole waves leave together
+    const unsigned n = unsigned(g.n), m = unsigned(g.m);
+    const unsigned t = o / n, j = o - t * n;
+    const unsigned bi = t / m, i = t - bi * m;
+    const float* a = g.a + int64_t(bi) * g.stride_a + (TA ? int64_t(i) : int64_t(i) * g.lda);
+    const float* b = g.b + int64_t(bi) * g.stride_b + (TB ? int64_t(j) * g.ldb : int64_t(j));
+    const int64_t ak = TA ? g.lda : 1, bk = TB ? 1 : g.ldb;
+    float acc = 0.0f;
+    int64_t k = lane;
+    for (; k + 192 < g.k; k += 256) {
+        float av[4], bv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            av[u] = a[(k + 64 * u) * ak];
+            bv[u] = b[(k + 64 * u) * bk];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc += av[u] * bv[u];
+    }
+    for (; k < g.k; k += 64) acc += a[k * ak] * b[k * bk];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) {
+        float* dst = g.c + int64_t(bi) * g.stride_c + int64_t(i) * g.ldc + j;
+        if (g.beta != 0.0f) acc = acc + g.beta * *dst;
+        *dst = acc;
+    }
+}
+
+template <bool TA, bool TB>
+int gemm_small(const GemmArgs& g, int64_t batch, bool wave, hipStream_t s) {
+    const int64_t total = batch * g.m * g.n;
+    if (wave) {
+        EHIP_LAUNCH("gemm_small", (gemm_small_wave<TA, TB>), dim3(unsigned(ceil_div(total, 4))),
+                    dim3(256), 0, s, g, unsigned(total));
+    } else {
+        int64_t grid = ceil_div(total, 256);
+        if (grid > 65536) grid = 65536;
+        EHIP_LAUNCH("gemm_small", (gemm_small_thread<TA, TB>), dim3(unsigned(grid)), dim3(256), 0,
+                    s, g, unsigned(total));
+    }
+    return EHIP_OK;
+}
+
+// Which small kernel, if any: 0 none, 1 thread per output, 2 wave per output.
+int small_kind(int64_t batch, int64_t m, int64_t n, int64_t k) {
+    const int64_t outputs = batch * m * n;
+    if (outputs > 0xffffffffLL / 2) return 0;
+    if (k <= kSmallThreadK && outputs * k <= kSmallThreadWork) return 1;
+    if (outputs >= 64 && outputs <= kSmallWaveOutputs && k >= 256 && k <= kSmallWaveMaxK &&
+        outputs * k <= kSmallWaveWork)
+        return 2;
+    return 0;
+}
+
 }  // namespace
 }  // namespace ehip
 
@@ -169,6 +289,13 @@ int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
     g.stride_b = stride_b;
     g.stride_c = stride_c;
     g.beta = beta;
+    if (const int kind = small_kind(batch, m, n, k)) {
+        const bool wave = kind == 2;
+        if (!trans_a && !trans_b) return gemm_small<false, false>(g, batch, wave, s);
+        if (!trans_a && trans_b) return gemm_small<false, true>(g, batch, wave, s);
+        if (trans_a && !trans_b) return gemm_small<true, false>(g, batch, wave, s);
+        return gemm_small<true, true>(g, batch, wave, s);
+    }
     if (!trans_a && !trans_b) return gemm_modes<false, false>(g, batch, s);
     if (!trans_a && trans_b) return gemm_modes<false, true>(g, batch, s);
     if (trans_a && !trans_b) return gemm_modes<true, false>(g, batch, s);

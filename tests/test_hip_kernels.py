@@ -107,6 +107,55 @@ def test_gemm_integer_inputs_exact(hip, m, k, n):
     exact(host(hip.gemm(dev(a), dev(b))), want, "integer gemm")
 
 
+SMALL_EXACT = [(7, 5, 3), (64, 10, 784), (784, 64, 10), (200, 96, 96), (33, 128, 65),
+               (1, 1, 1), (3, 100, 2)]
+
+
+@pytest.mark.parametrize("m,k,n", SMALL_EXACT)
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_small_k_bitexact(hip, orc, m, k, n, ta, tb):
+    """Products with K <= 128 take the thread-per-output kernel: k order from zero with the
+    zero skip of the reference's i-k-j loop, so they equal the CPU bit for bit."""
+    print_case("gemm-small-exact", m, k, n, ta, tb)
+    r = rng(m * 31 + k * 7 + n + 2 * ta + tb)
+    a = randn(r, m, k)
+    a[:, ::3] = 0.0  # zero A entries take the skip
+    b = randn(r, k, n)
+    a_st = np.ascontiguousarray(a.T) if ta else a
+    b_st = np.ascontiguousarray(b.T) if tb else b
+    got = host(hip.gemm(dev(a_st), dev(b_st), trans_a=ta, trans_b=tb))
+    exact(got, orc.matmul(a, b), f"small gemm {m}x{k}x{n} ta={ta} tb={tb}")
+
+
+def test_gemm_small_batched_bitexact(hip, orc):
+    """Attention-shaped batched products (cfg3's head shapes, 8 heads' worth)."""
+    print_case("gemm-small-batched")
+    r = rng(77)
+    q, kt = randn(r, 8, 64, 24), randn(r, 8, 24, 64)
+    exact(host(hip.gemm(dev(q), dev(kt))), orc.matmul(q, kt), "scores")
+    p, v = randn(r, 8, 64, 64), randn(r, 8, 64, 24)
+    exact(host(hip.gemm(dev(p), dev(v))), orc.matmul(p, v), "probs x V")
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("m,k,n", [(64, 784, 10), (10, 2048, 9), (96, 512, 20)])
+def test_gemm_small_wave(hip, orc, m, k, n, ta, tb):
+    """Few outputs, long K: the wave-per-output kernel, within the fp32 summation bound and
+    deterministic."""
+    print_case("gemm-small-wave", m, k, n, ta, tb)
+    r = rng(m + k + n + ta * 2 + tb)
+    a, b = randn(r, m, k), randn(r, k, n)
+    a_st = np.ascontiguousarray(a.T) if ta else a
+    b_st = np.ascontiguousarray(b.T) if tb else b
+    got = host(hip.gemm(dev(a_st), dev(b_st), trans_a=ta, trans_b=tb))
+    ref_close(got, orc.matmul(a, b), k_tol(k), "wave gemm")
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    bound = (k + 2) * 2.0 ** -24 * (np.abs(a64) @ np.abs(b64))
+    assert np.all(np.abs(got - a64 @ b64) <= bound), "beyond the fp32 summation bound"
+    again = host(hip.gemm(dev(a_st), dev(b_st), trans_a=ta, trans_b=tb))
+    exact(again, got, "repeat")
+
+
 @pytest.mark.parametrize("ab,bb", [(True, True), (True, False), (False, True)])
 def test_gemm_batched_shared(hip, orc, ab, bb):
     print_case("gemm-batched", ab, bb)
