@@ -13,6 +13,8 @@
 
 #include "common.hpp"
 
+#include <cstring>
+#include <mutex>
 #include <vector>
 
 namespace ehip {
@@ -535,10 +537,33 @@ int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, 
     if (slots.empty()) return EHIP_OK;
     if (chunks > 0x7fffffff) return fail(EHIP_EINVAL, "adam_multi: too many elements");
     hipStream_t s = as_stream(stream);
+    // The slot table lives in a buffer of its own and is uploaded only when it
+    // differs from the previous call's: an optimiser stepping the same
+    // parameters every iteration pays no host-to-device copy per step. Work is
+    // ordered on one stream, so a new upload lands after the kernels that read
+    // the old table.
+    static std::mutex table_mu;
+    static std::vector<AdamSlot> last;
+    static AdamSlot* table = nullptr;
+    static size_t table_cap = 0;
+    std::lock_guard<std::mutex> lock(table_mu);
     const size_t bytes = slots.size() * sizeof(AdamSlot);
-    AdamSlot* table = static_cast<AdamSlot*>(scratch(bytes));
-    if (table == nullptr) return EHIP_ENOMEM;
-    if (int rc = ehip_memcpy_h2d(table, slots.data(), bytes, stream)) return rc;
+    const bool same = table != nullptr && last.size() == slots.size() &&
+                      std::memcmp(last.data(), slots.data(), bytes) == 0;
+    if (!same) {
+        if (bytes > table_cap) {
+            if (table != nullptr) ehip_arena_free(table);
+            table = nullptr;
+            table_cap = 0;
+            void* p = nullptr;
+            if (int rc = ehip_arena_alloc(bytes, &p)) return rc;
+            table = static_cast<AdamSlot*>(p);
+            table_cap = bytes;
+        }
+        last.clear();  // a failed upload leaves no table marked as current
+        if (int rc = ehip_memcpy_h2d(table, slots.data(), bytes, stream)) return rc;
+        last = slots;
+    }
     if (chunks * kAdamChunk >= kNontemporalMin)
         EHIP_LAUNCH("adam_multi", adam_multi<true>, dim3(unsigned(chunks)), dim3(kThreads), 0, s,
                     table, int(slots.size()), lr, beta1, beta2, eps, weight_decay, bias_c1,

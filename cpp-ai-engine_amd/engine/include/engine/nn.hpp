@@ -105,6 +105,24 @@ Tensor mse_loss(const Tensor& prediction, const Tensor& target);
 // until read.
 Tensor cross_entropy_loss(const Tensor& logits, const std::vector<size_t>& targets);
 
+// Class labels uploaded once and kept on the device, for a batch that is
+// reused (a resident batch, or labels produced on the device).
+class Labels {
+public:
+    Labels() = default;
+    explicit Labels(const std::vector<size_t>& targets);
+    size_t size() const noexcept { return n_; }
+    size_t max_label() const noexcept { return max_; }
+    const DeviceInts& device() const noexcept { return dev_; }
+
+private:
+    DeviceInts dev_;
+    size_t n_ = 0, max_ = 0;
+};
+
+// The same loss with device-resident labels: no upload per call.
+Tensor cross_entropy_loss(const Tensor& logits, const Labels& targets);
+
 class CrossEntropyLoss {
 public:
     Tensor forward(const Tensor& logits, const std::vector<size_t>& targets) const {

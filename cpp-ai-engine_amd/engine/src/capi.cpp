@@ -121,6 +121,7 @@ struct Trainer {
     Tensor x;     // images (cnn) or ids (lm)
     Tensor mask;  // lm only
     std::vector<size_t> labels;
+    nn::Labels device_labels;  // the batch's labels, resident like x
     size_t rows = 0, classes = 0;
     Tensor loss;
 
@@ -129,7 +130,7 @@ struct Trainer {
     void step() {
         opt->zero_grad();
         Tensor logits = cnn ? (*cnn)(x) : lm->forward(x, mask).reshape({rows, classes});
-        loss = nn::cross_entropy_loss(logits, labels);
+        loss = nn::cross_entropy_loss(logits, device_labels);
         loss.backward();
         opt->step();
     }
@@ -505,6 +506,7 @@ void* eng_trainer_cnn(const float* x, const int64_t* labels, int64_t batch, int6
         tr->x = make({size_t(batch), size_t(in_c), size_t(hw), size_t(hw)}, x, false);
         (void)tr->x.storage().device();
         tr->labels = labels_of(labels, batch);
+        tr->device_labels = nn::Labels(tr->labels);
         tr->rows = size_t(batch);
         tr->classes = size_t(classes);
         t = tr.release();
@@ -527,6 +529,7 @@ void* eng_trainer_charlm(const float* ids, const int64_t* targets, int64_t batch
         (void)tr->mask.storage().device();
         (void)tr->lm->positions.storage().device();
         tr->labels = labels_of(targets, batch * seq);
+        tr->device_labels = nn::Labels(tr->labels);
         tr->rows = size_t(batch * seq);
         tr->classes = size_t(vocab);
         t = tr.release();

@@ -118,23 +118,10 @@ Tensor mse_loss(const Tensor& prediction, const Tensor& target) {
 // Probabilities, per-row losses and their mean are computed on the device
 // (the reference computes them serially on the host, src/nn.cpp:346-380);
 // the loss is read back only when host code asks for it.
-Tensor cross_entropy_loss(const Tensor& logits, const std::vector<size_t>& targets) {
-    if (logits.ndim() != 2)
-        throw std::invalid_argument("cross_entropy_loss expects 2D logits (batch, classes), received " +
-                                    logits.shape_str() + ".");
+namespace {
+
+Tensor cross_entropy_device(const Tensor& logits, std::shared_ptr<DeviceInts> d_t) {
     const size_t N = logits.shape()[0], C = logits.shape()[1];
-    if (targets.size() != N)
-        throw std::invalid_argument("cross_entropy_loss received " + std::to_string(targets.size()) +
-                                    " labels for a batch of " + std::to_string(N) + ".");
-    if (N == 0) throw std::invalid_argument("cross_entropy_loss received an empty batch.");
-    std::vector<int32_t> t(N);
-    for (size_t i = 0; i < N; ++i) {
-        if (targets[i] >= C)
-            throw std::out_of_range("Label " + std::to_string(targets[i]) +
-                                    " outside the range of " + std::to_string(C) + " classes.");
-        t[i] = static_cast<int32_t>(targets[i]);
-    }
-    auto d_t = std::make_shared<DeviceInts>(t);
     Tensor probs(logits.shape(), 0.0f, false);
     const bool req_g = logits.requires_grad() && autograd::grad_enabled();
     Tensor loss({1}, 0.0f, false);
@@ -154,6 +141,52 @@ Tensor cross_entropy_loss(const Tensor& logits, const std::vector<size_t>& targe
         };
     }
     return loss;
+}
+
+void check_logits(const Tensor& logits, size_t n_targets) {
+    if (logits.ndim() != 2)
+        throw std::invalid_argument("cross_entropy_loss expects 2D logits (batch, classes), received " +
+                                    logits.shape_str() + ".");
+    const size_t N = logits.shape()[0];
+    if (n_targets != N)
+        throw std::invalid_argument("cross_entropy_loss received " + std::to_string(n_targets) +
+                                    " labels for a batch of " + std::to_string(N) + ".");
+    if (N == 0) throw std::invalid_argument("cross_entropy_loss received an empty batch.");
+}
+
+}  // namespace
+
+Tensor cross_entropy_loss(const Tensor& logits, const std::vector<size_t>& targets) {
+    check_logits(logits, targets.size());
+    const size_t N = logits.shape()[0], C = logits.shape()[1];
+    std::vector<int32_t> t(N);
+    for (size_t i = 0; i < N; ++i) {
+        if (targets[i] >= C)
+            throw std::out_of_range("Label " + std::to_string(targets[i]) +
+                                    " outside the range of " + std::to_string(C) + " classes.");
+        t[i] = static_cast<int32_t>(targets[i]);
+    }
+    return cross_entropy_device(logits, std::make_shared<DeviceInts>(t));
+}
+
+Labels::Labels(const std::vector<size_t>& targets) : n_(targets.size()) {
+    std::vector<int32_t> t(targets.size());
+    for (size_t i = 0; i < targets.size(); ++i) {
+        if (targets[i] > size_t(INT32_MAX))
+            throw std::out_of_range("Label " + std::to_string(targets[i]) + " beyond int32.");
+        t[i] = static_cast<int32_t>(targets[i]);
+        if (targets[i] > max_) max_ = targets[i];
+    }
+    dev_ = DeviceInts(t);
+}
+
+Tensor cross_entropy_loss(const Tensor& logits, const Labels& targets) {
+    check_logits(logits, targets.size());
+    const size_t C = logits.shape()[1];
+    if (targets.size() > 0 && targets.max_label() >= C)
+        throw std::out_of_range("Label " + std::to_string(targets.max_label()) +
+                                " outside the range of " + std::to_string(C) + " classes.");
+    return cross_entropy_device(logits, std::make_shared<DeviceInts>(targets.device()));
 }
 
 std::vector<size_t> argmax_rows(const Tensor& logits) {
