@@ -250,6 +250,139 @@ __global__ __launch_bounds__(kThreads) void conv_forward_tiled(const float* __re
     }
 }
 
+// Conv2d -> ReLU -> MaxPool2d (disjoint pk x pk windows) over a tile of
+// `prows` pooled rows of one image and CG output channels. The convolution
+// values of the tile's windows are computed exactly as conv_forward_tiled does
+// and kept in LDS; each window is then ReLU'd and reduced to its first strict
+// maximum in window order (src/conv.cpp:410-442), written with its flat index
+// into the (N, C, oH, oW) convolution output. Only the pooled tensor reaches
+// HBM. blockIdx.x = n * tiles + tile.
+template <int CG, int KH, int KW>
+__global__ __launch_bounds__(kThreads) void conv_relu_pool_tiled(
+    const float* __restrict__ x, const float* __restrict__ wt, const float* __restrict__ bias,
+    float* __restrict__ pooled, int32_t* __restrict__ argmax, Geo g, int pk, int ph, int pw,
+    int prows, int tiles) {
+    extern __shared__ float sm[];
+    const int kh = KH ? KH : g.kh, kw = KW ? KW : g.kw;
+    const int n = int(blockIdx.x) / tiles, tile = int(blockIdx.x) % tiles;
+    const int co0 = int(blockIdx.y) * CG;
+    const int pr0 = tile * prows;
+    const int pr1 = min(pr0 + prows, ph);
+    const int oh0 = pr0 * pk, crows = (pr1 - pr0) * pk, ccols = pw * pk;
+    const int r0 = oh0 * g.stride - g.pad;
+    const int rows_in = (crows - 1) * g.stride + kh;
+    const int wp = g.w + 2 * g.pad;
+    const int wps = odd(wp), plane_s = odd(rows_in * wps);
+    float* w_s = sm;                                     // [K][CG]
+    float* x_s = w_s + CG * g.k;                         // [cin][rows_in][wps]
+    float* y_s = x_s + g.cin * plane_s;                  // [CG][crows][ccols]
+    const float* xn = x + int64_t(n) * g.cin * g.h * g.w;
+    const int plane_in = rows_in * wp;
+    stage<4>(CG * g.k, w_s, [&](int e, int& slot) {
+        const int co = co0 + e % CG;
+        slot = e;
+        return co < g.cout ? wt[co * g.k + e / CG] : 0.0f;
+    });
+    stage<8>(g.cin * plane_in, x_s, [&](int e, int& slot) {
+        const unsigned ci = unsigned(e) / unsigned(plane_in);
+        const unsigned rem = unsigned(e) - ci * unsigned(plane_in);
+        const unsigned rr = rem / unsigned(wp), cc = rem - rr * unsigned(wp);
+        slot = int(ci) * plane_s + int(rr) * wps + int(cc);
+        const int h = r0 + int(rr), v = int(cc) - g.pad;
+        return (h >= 0 && h < g.h && v >= 0 && v < g.w) ? xn[(int(ci) * g.h + h) * g.w + v] : 0.0f;
+    });
+    __syncthreads();
+    const int npix = crows * ccols;
+    for (int p = threadIdx.x; p < npix; p += kThreads) {
+        const int ohl = p / ccols, ow = p - ohl * ccols;
+        float c[CG];
+#pragma unroll
+        for (int q = 0; q < CG; ++q) c[q] = 0.0f;
+        const float* wk = w_s;
+        for (int ci = 0; ci < g.cin; ++ci) {
+            const float* xr = x_s + ci * plane_s + ohl * g.stride * wps + ow * g.stride;
+#pragma unroll
+            for (int i = 0; i < (KH ? KH : 1); ++i) {
+                for (int ii = 0; ii < (KH ? 1 : kh); ++ii) {
+                    const float* xi = xr + (KH ? i : ii) * wps;
+#pragma unroll
+                    for (int j = 0; j < (KW ? KW : 1); ++j) {
+                        for (int jj = 0; jj < (KW ? 1 : kw); ++jj, wk += CG) {
+                            const float a = xi[KW ? j : jj];
+                            float wv[CG];
+#pragma unroll
+                            for (int q = 0; q < CG; ++q) wv[q] = wk[q];
+#pragma unroll
+                            for (int q = 0; q < CG; ++q) {
+                                const float t = c[q] + a * wv[q];
+                                c[q] = (a != 0.0f) ? t : c[q];
+                            }
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < CG; ++q) {
+            const int co = co0 + q;
+            const float v = (bias && co < g.cout) ? c[q] + bias[co] : c[q];
+            y_s[(q * crows + ohl) * ccols + ow] = (0.0f < v) ? v : 0.0f;  // ReLU
+        }
+    }
+    __syncthreads();
+    const int nwin = CG * (pr1 - pr0) * pw;
+    for (int e = threadIdx.x; e < nwin; e += kThreads) {
+        const int q = e / ((pr1 - pr0) * pw), r = e - q * ((pr1 - pr0) * pw);
+        const int co = co0 + q;
+        if (co >= g.cout) continue;
+        const int prl = r / pw, pc = r - prl * pw;
+        float best = 0.0f;
+        int bi = 0, bj = 0;
+        bool found = false;
+        for (int i = 0; i < pk; ++i)
+            for (int j = 0; j < pk; ++j) {
+                const float v = y_s[(q * crows + prl * pk + i) * ccols + pc * pk + j];
+                if (!found || v > best) {
+                    best = v;
+                    bi = i;
+                    bj = j;
+                    found = true;
+                }
+            }
+        const int64_t plane_c = int64_t(n) * g.cout + co;
+        const int64_t o = (plane_c * ph + pr0 + prl) * pw + pc;
+        pooled[o] = best;
+        argmax[o] = int32_t((plane_c * g.oh + oh0 + prl * pk + bi) * g.ow + pc * pk + bj);
+    }
+}
+
+// A ReLU and a max pool with disjoint pk x pk windows after the convolution
+// (Conv2d -> ReLU -> MaxPool2d fused): the pooled output, its gradient and the
+// argmax (flat index into the convolution's output) replace the convolution's
+// own output gradient, which is gathered on the fly.
+struct PoolGather {
+    const float* gp;        // gradient of the pooled output (N, C, ph, pw)
+    const float* pooled;    // the pooled output
+    const int32_t* argmax;  // flat index of each window's maximum in (N, C, oH, oW)
+    int pk, ph, pw;
+};
+
+// The convolution's output gradient at (n, co, oh, ow): the reference's
+// maxpool backward (src/conv.cpp:461-469, one window per position here) then
+// its ReLU backward (src/tensor_ops.cpp:603-615). The pooled value is the
+// chosen position's ReLU output, so "pooled > 0" is "conv output > 0" there,
+// and every other position's gradient is zero either way: bit-exact.
+template <bool POOL>
+__device__ __forceinline__ float out_grad(const float* gout, const PoolGather& pg, const Geo& g,
+                                          int n, int co, int oh, int ow) {
+    const int64_t flat = ((int64_t(n) * g.cout + co) * g.oh + oh) * g.ow + ow;
+    if (!POOL) return gout[flat];
+    const int pr = oh / pg.pk, pc = ow / pg.pk;
+    if (pr >= pg.ph || pc >= pg.pw) return 0.0f;
+    const int64_t o = ((int64_t(n) * g.cout + co) * pg.ph + pr) * pg.pw + pc;
+    return (pg.argmax[o] == flat && pg.pooled[o] > 0.0f) ? pg.gp[o] : 0.0f;
+}
+
 // First and last window index along one axis whose window covers position p,
 // in 32-bit arithmetic (stride 1 needs no division).
 __device__ __forceinline__ void cover32(int p, int pad, int k, int s, int out, int& lo, int& hi) {
@@ -271,10 +404,10 @@ __device__ __forceinline__ void cover32(int p, int pad, int k, int s, int out, i
 // CG channels, every channel in the order of conv_backward_input_direct (zero
 // gradients skipped by a select after an unconditional multiply-add).
 // blockIdx.x = n * tiles + tile.
-template <int CG>
+template <int CG, bool POOL>
 __global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
-    const float* __restrict__ gout, const float* __restrict__ wt, float* __restrict__ dx, Geo g,
-    int rows, int tiles) {
+    const float* __restrict__ gout, PoolGather pgat, const float* __restrict__ wt,
+    float* __restrict__ dx, Geo g, int rows, int tiles) {
     extern __shared__ float sm[];
     const int n = int(blockIdx.x) / tiles, tile = int(blockIdx.x) % tiles;
     const int ci0 = int(blockIdx.y) * CG;
@@ -291,11 +424,16 @@ __global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
     float* g_s = sm;                                   // [cout][oh_rows][ow]
     float* w_s = sm + g.cout * gplane_s;               // [tap][cout][CG]
     const int64_t plane = int64_t(g.oh) * g.ow;
-    const float* gn = gout + int64_t(n) * g.cout * plane + int64_t(oh_first) * g.ow;
+    const float* gn = POOL ? nullptr : gout + int64_t(n) * g.cout * plane + int64_t(oh_first) * g.ow;
     stage<8>(g.cout * gplane, g_s, [&](int e, int& slot) {
         const unsigned co = unsigned(e) / unsigned(gplane);
         const unsigned r = unsigned(e) - co * unsigned(gplane);
         slot = int(co) * gplane_s + int(r);
+        if (POOL) {
+            const unsigned rr = r / unsigned(g.ow);
+            return out_grad<true>(gout, pgat, g, n, int(co), oh_first + int(rr),
+                                  int(r - rr * unsigned(g.ow)));
+        }
         return gn[int64_t(co) * plane + r];
     });
     stage<4>(khw * g.cout * CG, w_s, [&](int e, int& slot) {
@@ -368,9 +506,10 @@ __global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
 // pixel groups, and the groups are combined in group order. partial[block][o],
 // o = co (K + 1) + k, is then reduced over blocks by conv_weight_reduce. The
 // order of every sum depends only on the shape.
-template <int CT, int KT>
+template <int CT, int KT, bool POOL>
 __global__ __launch_bounds__(kThreads) void conv_weight_band(const float* __restrict__ x,
                                                              const float* __restrict__ gout,
+                                                             PoolGather pgat,
                                                              float* __restrict__ partial, Geo g,
                                                              int rows, int bands) {
     extern __shared__ float sm[];
@@ -399,11 +538,16 @@ __global__ __launch_bounds__(kThreads) void conv_weight_band(const float* __rest
         return (h >= 0 && h < g.h && v >= 0 && v < g.w) ? xn[(int(ci) * g.h + h) * g.w + v] : 0.0f;
     });
     const int64_t plane = int64_t(g.oh) * g.ow;
-    const float* gn = gout + int64_t(n) * g.cout * plane + int64_t(oh0) * g.ow;
+    const float* gn = POOL ? nullptr : gout + int64_t(n) * g.cout * plane + int64_t(oh0) * g.ow;
     stage<8>(g.cout * np, dy_s, [&](int e, int& slot) {
         const unsigned co = unsigned(e) / unsigned(np);
         const unsigned r = unsigned(e) - co * unsigned(np);
         slot = int(co) * nps + int(r);
+        if (POOL) {
+            const unsigned rr = r / unsigned(g.ow);
+            return out_grad<true>(gout, pgat, g, n, int(co), oh0 + int(rr),
+                                  int(r - rr * unsigned(g.ow)));
+        }
         return gn[int64_t(co) * plane + r];
     });
     __syncthreads();
@@ -679,16 +823,159 @@ int forward_tiled(const float* x, const float* wt, const float* bias, float* out
     return EHIP_OK;
 }
 
-template <int CG>
-int backward_input_tiled(const float* gout, const float* wt, float* dx, const Geo& g,
-                         hipStream_t s) {
+template <int CG, bool POOL>
+int backward_input_tiled(const float* gout, const PoolGather& pg, const float* wt, float* dx,
+                         const Geo& g, hipStream_t s) {
     const int groups = int(ceil_div(g.cin, CG));
     int rows = rows_for_fill(int64_t(g.n) * groups, g.h);
     while (rows > 1 && backward_input_lds(g, CG, rows) > kTileLds) rows = (rows + 1) / 2;
     const int tiles = int(ceil_div(g.h, rows));
     const dim3 grid{unsigned(int64_t(g.n) * tiles), unsigned(groups)};
-    EHIP_LAUNCH("conv2d_backward_input", conv_backward_input_tiled<CG>, grid, dim3(kThreads),
-                backward_input_lds(g, CG, rows), s, gout, wt, dx, g, rows, tiles);
+    EHIP_LAUNCH("conv2d_backward_input", (conv_backward_input_tiled<CG, POOL>), grid,
+                dim3(kThreads), backward_input_lds(g, CG, rows), s, gout, pg, wt, dx, g, rows,
+                tiles);
+    return EHIP_OK;
+}
+
+bool input_tiles_fit(const Geo& g) {
+    const int cg = g.cin >= 2 ? 2 : 1;
+    return backward_input_lds(g, cg, 1) <= kTileLds && int64_t(g.n) * g.h <= 0x7fffffff;
+}
+
+// The input gradient; POOL gathers the output gradient through a fused pool.
+template <bool POOL>
+int backward_input(const float* gout, const PoolGather& pg, const float* wt, float* dx,
+                   const Geo& g, hipStream_t s) {
+    const int64_t n_in = int64_t(g.n) * g.cin * g.h * g.w;
+    if (n_in == 0) return EHIP_OK;
+    if (input_tiles_fit(g)) {
+        if (g.cin >= 2) return backward_input_tiled<2, POOL>(gout, pg, wt, dx, g, s);
+        return backward_input_tiled<1, POOL>(gout, pg, wt, dx, g, s);
+    }
+    if (POOL) return fail(EHIP_EINVAL, "conv2d: the fused pool needs LDS tiles");
+    int64_t grid = ceil_div(n_in, kThreads);
+    if (grid > 65536) grid = 65536;
+    const size_t lds = size_t(g.cout) * g.k * sizeof(float);
+    EHIP_LAUNCH("conv2d_backward_input", conv_backward_input_direct, dim3(unsigned(grid)),
+                dim3(kThreads), lds, s, gout, wt, dx, g);
+    return EHIP_OK;
+}
+
+int band_rows(const Geo& g) {
+    int rows = rows_for_fill(g.n, g.oh);
+    while (rows > 1 && weight_band_lds(g, rows) > kTileLds) rows = (rows + 1) / 2;
+    return rows;
+}
+
+bool weight_bands_fit(const Geo& g) {
+    return weight_band_lds(g, band_rows(g)) <= kTileLds && int64_t(g.n) * g.oh <= 0x7fffffff;
+}
+
+template <int T, bool POOL>
+int launch_band(const float* x, const float* gout, const PoolGather& pg, float* partial,
+                const Geo& g, int rows, int bands, hipStream_t s) {
+    EHIP_LAUNCH("conv2d_weight_band", (conv_weight_band<T, T, POOL>),
+                dim3(unsigned(int64_t(g.n) * bands)), dim3(kThreads), weight_band_lds(g, rows), s,
+                x, gout, pg, partial, g, rows, bands);
+    return EHIP_OK;
+}
+
+// Weight and bias gradients: per-band (or per-chunk) partials, then their
+// ordered reduction. POOL gathers the output gradient through a fused pool.
+template <bool POOL>
+int backward_weight(const float* x, const float* gout, const PoolGather& pg, float* dweight,
+                    float* dbias, const Geo& g, hipStream_t s) {
+    const int64_t pixels = int64_t(g.n) * g.oh * g.ow;
+    const int O = g.cout * (g.k + 1);
+    if (pixels == 0) {
+        if (int rc = ehip_fill_f32(dweight, int64_t(g.cout) * g.k, 0.0f, s)) return rc;
+        return dbias ? ehip_fill_f32(dbias, g.cout, 0.0f, s) : EHIP_OK;
+    }
+    int64_t chunks = 0;
+    float* partial = nullptr;
+    // Bands of output rows (one image each, about 512 blocks) when a band's
+    // input rows and gradient rows fit in LDS; otherwise chunks of P pixels
+    // with their im2col columns staged.
+    if (weight_bands_fit(g)) {
+        const int rows = band_rows(g);
+        const int bands = int(ceil_div(g.oh, rows));
+        chunks = int64_t(g.n) * bands;
+        partial = static_cast<float*>(scratch(size_t(chunks) * O * sizeof(float)));
+        if (partial == nullptr) return EHIP_ENOMEM;
+        const int t = weight_tile(g);
+        const int rc = t == 4   ? launch_band<4, POOL>(x, gout, pg, partial, g, rows, bands, s)
+                       : t == 2 ? launch_band<2, POOL>(x, gout, pg, partial, g, rows, bands, s)
+                                : launch_band<1, POOL>(x, gout, pg, partial, g, rows, bands, s);
+        if (rc != EHIP_OK) return rc;
+    } else {
+        if (POOL) return fail(EHIP_EINVAL, "conv2d: the fused pool needs LDS bands");
+        // Chunk size: about 256 chunks to fill the CUs, 16..256 pixels each, and
+        // the staged chunk within the LDS budget.
+        int P = 16;
+        while (P < 256 && ceil_div(pixels, P) > 256) P *= 2;
+        const auto lds_for = [&](int p) {
+            return (size_t(g.cout) + size_t(g.k) + 1) * size_t(p + 1) * sizeof(float) +
+                   kThreads * sizeof(float);
+        };
+        while (P > 1 && lds_for(P) > kMaxLds) P /= 2;
+        chunks = ceil_div(pixels, P);
+        if (chunks > 0x7fffffff)
+            return fail(EHIP_EINVAL, "conv2d_backward_weight: too many pixels");
+        partial = static_cast<float*>(scratch(size_t(chunks) * O * sizeof(float)));
+        if (partial == nullptr) return EHIP_ENOMEM;
+        EHIP_LAUNCH("conv2d_weight_partial", conv_weight_partial, dim3(unsigned(chunks)),
+                    dim3(kThreads), lds_for(P), s, x, gout, partial, g, P);
+    }
+    int rl = 1;
+    while (rl < 16 && rl * 8 < chunks) rl *= 2;
+    const int per_block = 256 / rl;
+    EHIP_LAUNCH("conv2d_weight_reduce", conv_weight_reduce, dim3(unsigned(ceil_div(O, per_block))),
+                dim3(256), 0, s, partial, dweight, dbias, g.cout, g.k, int(chunks), rl);
+    return EHIP_OK;
+}
+
+size_t pool_forward_lds(const Geo& g, int cg, int pk, int pw, int prows) {
+    const size_t crows = size_t(prows) * pk;
+    const size_t rows_in = (crows - 1) * g.stride + g.kh;
+    return (size_t(cg) * g.k + size_t(g.cin) * odd_h(rows_in * odd_h(g.w + 2 * g.pad)) +
+            size_t(cg) * crows * size_t(pw) * pk) *
+           sizeof(float);
+}
+
+// Validates the pool window of a fused Conv2d -> ReLU -> MaxPool2d: disjoint
+// square windows (kernel == stride, no padding) over the convolution output.
+int check_pool(const char* name, const ehip_window_t* c, int64_t cout, const ehip_window_t* p) {
+    if (int rc = check_window(name, p)) return rc;
+    if (p->kernel_h != p->kernel_w || p->kernel_h != p->stride || p->padding != 0)
+        return fail(EHIP_EINVAL, "%s: the pool must have kernel == stride and no padding", name);
+    if (p->batch != c->batch || p->channels != cout || p->height != c->out_h ||
+        p->width != c->out_w)
+        return fail(EHIP_EINVAL, "%s: the pool window does not match the convolution output",
+                    name);
+    return EHIP_OK;
+}
+
+bool fused_fits(const Geo& g, const ehip_window_t& p) {
+    const int cg = g.cout >= 3 ? 4 : g.cout;
+    return pool_forward_lds(g, cg, int(p.kernel_h), int(p.out_w), 1) <= kTileLds &&
+           input_tiles_fit(g) && weight_bands_fit(g) && int64_t(g.n) * g.oh <= 0x7fffffff;
+}
+
+template <int CG>
+int pool_forward_tiled(const float* x, const float* wt, const float* bias, float* pooled,
+                       int32_t* argmax, const Geo& g, int pk, int ph, int pw, hipStream_t s) {
+    const int groups = int(ceil_div(g.cout, CG));
+    int prows = rows_for_fill(int64_t(g.n) * groups, ph);
+    while (prows > 1 && pool_forward_lds(g, CG, pk, pw, prows) > kTileLds) prows = (prows + 1) / 2;
+    const int tiles = int(ceil_div(ph, prows));
+    const dim3 grid{unsigned(int64_t(g.n) * tiles), unsigned(groups)};
+    const size_t lds = pool_forward_lds(g, CG, pk, pw, prows);
+    if (g.kh == 3 && g.kw == 3)
+        EHIP_LAUNCH("conv2d_relu_maxpool", (conv_relu_pool_tiled<CG, 3, 3>), grid, dim3(kThreads),
+                    lds, s, x, wt, bias, pooled, argmax, g, pk, ph, pw, prows, tiles);
+    else
+        EHIP_LAUNCH("conv2d_relu_maxpool", (conv_relu_pool_tiled<CG, 0, 0>), grid, dim3(kThreads),
+                    lds, s, x, wt, bias, pooled, argmax, g, pk, ph, pw, prows, tiles);
     return EHIP_OK;
 }
 
@@ -746,21 +1033,8 @@ int ehip_conv2d_backward_input_f32(const float* grad_out, const float* weight, f
     EHIP_READY();
     if (int rc = check_conv("conv2d_backward_input", w, out_channels)) return rc;
     if (!grad_out || !weight || !dx) return fail(EHIP_EINVAL, "conv2d_backward_input: null pointer");
-    const Geo g = geo_of(*w, out_channels);
-    const int64_t n_in = int64_t(g.n) * g.cin * g.h * g.w;
-    if (n_in == 0) return EHIP_OK;
-    hipStream_t s = as_stream(stream);
-    const int cg = g.cin >= 2 ? 2 : 1;
-    if (backward_input_lds(g, cg, 1) <= kTileLds && int64_t(g.n) * g.h <= 0x7fffffff) {
-        if (cg == 2) return backward_input_tiled<2>(grad_out, weight, dx, g, s);
-        return backward_input_tiled<1>(grad_out, weight, dx, g, s);
-    }
-    int64_t grid = ceil_div(n_in, kThreads);
-    if (grid > 65536) grid = 65536;
-    const size_t lds = size_t(g.cout) * g.k * sizeof(float);
-    EHIP_LAUNCH("conv2d_backward_input", conv_backward_input_direct, dim3(unsigned(grid)),
-                dim3(kThreads), lds, s, grad_out, weight, dx, g);
-    return EHIP_OK;
+    return backward_input<false>(grad_out, PoolGather{}, weight, dx, geo_of(*w, out_channels),
+                                 as_stream(stream));
 }
 
 int ehip_conv2d_backward_weight_f32(const float* x, const float* grad_out, float* dweight,
@@ -770,60 +1044,67 @@ int ehip_conv2d_backward_weight_f32(const float* x, const float* grad_out, float
     if (int rc = check_conv("conv2d_backward_weight", w, out_channels)) return rc;
     if (!x || !grad_out || !dweight)
         return fail(EHIP_EINVAL, "conv2d_backward_weight: null pointer");
-    const Geo g = geo_of(*w, out_channels);
-    const int64_t pixels = int64_t(g.n) * g.oh * g.ow;
-    const int O = g.cout * (g.k + 1);
+    return backward_weight<false>(x, grad_out, PoolGather{}, dweight, dbias,
+                                  geo_of(*w, out_channels), as_stream(stream));
+}
+
+int ehip_conv2d_relu_maxpool_supported(const ehip_window_t* conv, int64_t out_channels,
+                                       const ehip_window_t* pool) {
+    if (conv == nullptr || pool == nullptr || out_channels <= 0) return 0;
+    if (!ehip_conv2d_direct_supported(conv, out_channels)) return 0;
+    if (pool->kernel_h != pool->kernel_w || pool->kernel_h != pool->stride || pool->padding != 0 ||
+        pool->kernel_h <= 0)
+        return 0;
+    if (pool->batch != conv->batch || pool->channels != out_channels ||
+        pool->height != conv->out_h || pool->width != conv->out_w)
+        return 0;
+    const int64_t n_out = conv->batch * out_channels * conv->out_h * conv->out_w;
+    if (n_out > 0x7fffffff) return 0;
+    return fused_fits(geo_of(*conv, out_channels), *pool) ? 1 : 0;
+}
+
+int ehip_conv2d_relu_maxpool_f32(const float* x, const float* weight, const float* bias,
+                                 float* out, int32_t* argmax, const ehip_window_t* conv,
+                                 int64_t out_channels, const ehip_window_t* pool, void* stream) {
+    EHIP_READY();
+    if (int rc = check_conv("conv2d_relu_maxpool", conv, out_channels)) return rc;
+    if (int rc = check_pool("conv2d_relu_maxpool", conv, out_channels, pool)) return rc;
+    if (!x || !weight || !out || !argmax)
+        return fail(EHIP_EINVAL, "conv2d_relu_maxpool: null pointer");
+    const Geo g = geo_of(*conv, out_channels);
+    if (!fused_fits(g, *pool))
+        return fail(EHIP_EINVAL, "conv2d_relu_maxpool: the layer does not fit the LDS tiles");
+    const int pk = int(pool->kernel_h), ph = int(pool->out_h), pw = int(pool->out_w);
+    if (int64_t(g.n) * g.cout * ph * pw == 0) return EHIP_OK;
     hipStream_t s = as_stream(stream);
-    if (pixels == 0) {
-        if (int rc = ehip_fill_f32(dweight, int64_t(g.cout) * g.k, 0.0f, stream)) return rc;
-        return dbias ? ehip_fill_f32(dbias, g.cout, 0.0f, stream) : EHIP_OK;
-    }
-    int64_t chunks = 0;
-    float* partial = nullptr;
-    // Bands of output rows (one image each, about 256 blocks) when a band's input
-    // rows and gradient rows fit in LDS; otherwise chunks of P pixels with their
-    // im2col columns staged.
-    int rows = rows_for_fill(g.n, g.oh);
-    while (rows > 1 && weight_band_lds(g, rows) > kTileLds) rows = (rows + 1) / 2;
-    if (weight_band_lds(g, rows) <= kTileLds && int64_t(g.n) * g.oh <= 0x7fffffff) {
-        const int bands = int(ceil_div(g.oh, rows));
-        chunks = int64_t(g.n) * bands;
-        partial = static_cast<float*>(scratch(size_t(chunks) * O * sizeof(float)));
-        if (partial == nullptr) return EHIP_ENOMEM;
-        const size_t lds = weight_band_lds(g, rows);
-        const int t = weight_tile(g);
-        if (t == 4)
-            EHIP_LAUNCH("conv2d_weight_band", (conv_weight_band<4, 4>), dim3(unsigned(chunks)),
-                        dim3(kThreads), lds, s, x, grad_out, partial, g, rows, bands);
-        else if (t == 2)
-            EHIP_LAUNCH("conv2d_weight_band", (conv_weight_band<2, 2>), dim3(unsigned(chunks)),
-                        dim3(kThreads), lds, s, x, grad_out, partial, g, rows, bands);
-        else
-            EHIP_LAUNCH("conv2d_weight_band", (conv_weight_band<1, 1>), dim3(unsigned(chunks)),
-                        dim3(kThreads), lds, s, x, grad_out, partial, g, rows, bands);
-    } else {
-        // Chunk size: about 256 chunks to fill the CUs, 16..256 pixels each, and
-        // the staged chunk within the LDS budget.
-        int P = 16;
-        while (P < 256 && ceil_div(pixels, P) > 256) P *= 2;
-        const auto lds_for = [&](int p) {
-            return (size_t(g.cout) + size_t(g.k) + 1) * size_t(p + 1) * sizeof(float) +
-                   kThreads * sizeof(float);
-        };
-        while (P > 1 && lds_for(P) > kMaxLds) P /= 2;
-        chunks = ceil_div(pixels, P);
-        if (chunks > 0x7fffffff)
-            return fail(EHIP_EINVAL, "conv2d_backward_weight: too many pixels");
-        partial = static_cast<float*>(scratch(size_t(chunks) * O * sizeof(float)));
-        if (partial == nullptr) return EHIP_ENOMEM;
-        EHIP_LAUNCH("conv2d_weight_partial", conv_weight_partial, dim3(unsigned(chunks)),
-                    dim3(kThreads), lds_for(P), s, x, grad_out, partial, g, P);
-    }
-    int rl = 1;
-    while (rl < 16 && rl * 8 < chunks) rl *= 2;
-    const int per_block = 256 / rl;
-    EHIP_LAUNCH("conv2d_weight_reduce", conv_weight_reduce, dim3(unsigned(ceil_div(O, per_block))),
-                dim3(256), 0, s, partial, dweight, dbias, g.cout, g.k, int(chunks), rl);
+    const int cg = g.cout >= 3 ? 4 : g.cout;
+    if (cg == 4) return pool_forward_tiled<4>(x, weight, bias, out, argmax, g, pk, ph, pw, s);
+    if (cg == 2) return pool_forward_tiled<2>(x, weight, bias, out, argmax, g, pk, ph, pw, s);
+    return pool_forward_tiled<1>(x, weight, bias, out, argmax, g, pk, ph, pw, s);
+}
+
+int ehip_conv2d_relu_maxpool_backward_f32(const float* x, const float* weight,
+                                          const float* grad_out, const float* out,
+                                          const int32_t* argmax, float* dx, float* dweight,
+                                          float* dbias, const ehip_window_t* conv,
+                                          int64_t out_channels, const ehip_window_t* pool,
+                                          void* stream) {
+    EHIP_READY();
+    if (int rc = check_conv("conv2d_relu_maxpool_backward", conv, out_channels)) return rc;
+    if (int rc = check_pool("conv2d_relu_maxpool_backward", conv, out_channels, pool)) return rc;
+    if (!grad_out || !out || !argmax || (dx && !weight) || ((dweight || dbias) && !x))
+        return fail(EHIP_EINVAL, "conv2d_relu_maxpool_backward: null pointer");
+    if (dbias && !dweight)
+        return fail(EHIP_EINVAL, "conv2d_relu_maxpool_backward: dbias needs dweight");
+    const Geo g = geo_of(*conv, out_channels);
+    if (!fused_fits(g, *pool))
+        return fail(EHIP_EINVAL, "conv2d_relu_maxpool_backward: the layer does not fit the LDS tiles");
+    const PoolGather pg{grad_out, out, argmax, int(pool->kernel_h), int(pool->out_h),
+                        int(pool->out_w)};
+    hipStream_t s = as_stream(stream);
+    if (dx)
+        if (int rc = backward_input<true>(nullptr, pg, weight, dx, g, s)) return rc;
+    if (dweight) return backward_weight<true>(x, nullptr, pg, dweight, dbias, g, s);
     return EHIP_OK;
 }
 

@@ -88,6 +88,11 @@ _SIGS = {
     "ehip_conv2d_forward_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_backward_input_f32": [_vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_backward_weight_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
+    "ehip_conv2d_relu_maxpool_supported": [C.POINTER(Window), _i64, C.POINTER(Window)],
+    "ehip_conv2d_relu_maxpool_f32": [_vp, _vp, _vp, _vp, _vp, C.POINTER(Window), _i64,
+                                     C.POINTER(Window), _vp],
+    "ehip_conv2d_relu_maxpool_backward_f32": [_vp] * 8 + [C.POINTER(Window), _i64,
+                                                          C.POINTER(Window), _vp],
     "ehip_select_rows_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "ehip_scatter_add_rows_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp],
     "ehip_sum_axis_f32": [_vp, _vp, _i64, _i64, _i64, _vp],
@@ -342,6 +347,36 @@ class Backend:
             self.p(x), self.p(g), self.p(dw), self.p(db) if bias else None, C.byref(w), co,
             self.stream()), "conv2d_backward_weight")
         return dw, db
+
+    def conv_relu_pool_windows(self, x_shape, weight_shape, stride, pad, pk):
+        co, ci, kh, kw = weight_shape
+        cw = window(*x_shape, kh, kw, stride, pad)
+        pw = window(cw.batch, co, cw.out_h, cw.out_w, pk, pk, pk, 0)
+        return cw, pw
+
+    def conv2d_relu_maxpool(self, x, weight, bias, stride, pad, pk):
+        """Fused Conv2d -> ReLU -> MaxPool2d(pk, pk); returns (pooled, argmax int32)."""
+        cw, pw = self.conv_relu_pool_windows(x.shape, weight.shape, stride, pad, pk)
+        co = weight.shape[0]
+        out = self.f32((pw.batch, co, pw.out_h, pw.out_w))
+        am = self.torch.empty(out.shape, dtype=self.torch.int32, device="cuda")
+        self.ok(self.lib.ehip_conv2d_relu_maxpool_f32(
+            self.p(x), self.p(weight), self.p(bias) if bias is not None else None, self.p(out),
+            self.p(am), C.byref(cw), co, C.byref(pw), self.stream()), "conv2d_relu_maxpool")
+        return out, am
+
+    def conv2d_relu_maxpool_backward(self, x, weight, g, out, am, stride, pad, pk, need_dx=True,
+                                     bias=True):
+        cw, pw = self.conv_relu_pool_windows(x.shape, weight.shape, stride, pad, pk)
+        co = weight.shape[0]
+        dx = self.f32(x.shape) if need_dx else None
+        dw = self.f32(weight.shape)
+        db = self.f32((co,)) if bias else None
+        self.ok(self.lib.ehip_conv2d_relu_maxpool_backward_f32(
+            self.p(x), self.p(weight), self.p(g), self.p(out), self.p(am),
+            self.p(dx) if need_dx else None, self.p(dw), self.p(db) if bias else None,
+            C.byref(cw), co, C.byref(pw), self.stream()), "conv2d_relu_maxpool_backward")
+        return dx, dw, db
 
     def select_rows(self, x, idx):
         rs = x.numel() // x.shape[0]

@@ -36,6 +36,8 @@ public:
     std::string name() const override;
     Tensor& weight() { return weight_; }
     Tensor& bias() { return bias_; }
+    bool has_bias() const { return use_bias_; }
+    size_t out_channels() const { return out_channels_; }
     const Window2d& window() const { return window_; }
 
 private:
@@ -53,10 +55,18 @@ public:
     MaxPool2d(size_t kernel, size_t stride);
     Tensor forward(const Tensor& input) override;
     std::string name() const override;
+    const Window2d& window() const { return window_; }
 
 private:
     Window2d window_;
 };
+
+// Conv2d -> ReLU -> MaxPool2d as one node when the layers allow it (a narrow
+// convolution, a pool with kernel == stride and no padding): the values of the
+// three separate nodes, without the convolution output in HBM. Returns false
+// (and leaves `out` alone) when the layers must run one by one. Sequential
+// uses it for that layer pattern.
+bool conv2d_relu_maxpool(const Tensor& input, Conv2d& conv, const MaxPool2d& pool, Tensor& out);
 
 class Flatten : public Module {
 public:

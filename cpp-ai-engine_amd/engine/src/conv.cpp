@@ -223,6 +223,65 @@ Tensor MaxPool2d::forward(const Tensor& input) {
     return out;
 }
 
+bool conv2d_relu_maxpool(const Tensor& input, Conv2d& conv, const MaxPool2d& pool, Tensor& out) {
+    if (input.ndim() != 4 || input.shape()[1] * conv.window().kernel_h * conv.window().kernel_w *
+                                     conv.out_channels() !=
+                                 conv.weight().size())
+        return false;
+    const size_t H = input.shape()[2], W = input.shape()[3];
+    conv.window().validate(H, W);
+    const ehip_window_t cw = window_of(input.shape(), conv.window());
+    const size_t co = conv.out_channels();
+    const std::vector<size_t> conv_shape{size_t(cw.batch), co, size_t(cw.out_h), size_t(cw.out_w)};
+    const Window2d& pwin = pool.window();
+    if (pwin.kernel_h != pwin.kernel_w || pwin.kernel_h != pwin.stride || pwin.padding != 0)
+        return false;
+    if (pwin.kernel_h > conv_shape[2] || pwin.kernel_w > conv_shape[3]) return false;
+    const ehip_window_t pw = window_of(conv_shape, pwin);
+    if (!ehip_conv2d_relu_maxpool_supported(&cw, int64_t(co), &pw)) return false;
+    Tensor& weight = conv.weight();
+    Tensor& bias = conv.bias();
+    const bool use_bias = conv.has_bias();
+    Tensor res({size_t(pw.batch), co, size_t(pw.out_h), size_t(pw.out_w)}, 0.0f, false);
+    auto argmax = std::make_shared<DeviceInts>(res.size());
+    hip::check(ehip_conv2d_relu_maxpool_f32(dptr(input), dptr(weight),
+                                            use_bias ? dptr(bias) : nullptr, dout(res),
+                                            argmax->get(), &cw, int64_t(co), &pw, nullptr),
+               "conv2d_relu_maxpool");
+    const bool need_x = input.requires_grad();
+    const bool need_w = weight.requires_grad();
+    const bool need_b = use_bias && bias.requires_grad();
+    if (track(need_x || need_w || need_b)) {
+        res.set_requires_grad(true);
+        auto& parents = res.get_impl()->parents;
+        if (need_x) parents.push_back(input.get_impl());
+        if (need_w) parents.push_back(weight.get_impl());
+        if (need_b) parents.push_back(bias.get_impl());
+        Tensor x_copy = input, w_copy = weight, b_copy = bias;
+        // The pooled values are read through their storage: holding the output
+        // tensor itself inside its own backward would keep it alive forever.
+        Storage pooled = res.storage().share();
+        res.get_impl()->backward_fn = [x_copy, w_copy, b_copy, pooled, argmax, cw, pw, need_x,
+                                       need_w, need_b](const Tensor& g) mutable {
+            const int64_t co = int64_t(w_copy.shape()[0]);
+            Tensor dx, dw, db;
+            if (need_x) dx = Tensor(x_copy.shape(), 0.0f, false);
+            if (need_w || need_b) dw = Tensor(w_copy.shape(), 0.0f, false);
+            if (need_b) db = Tensor({size_t(co)}, 0.0f, false);
+            hip::check(ehip_conv2d_relu_maxpool_backward_f32(
+                           dptr(x_copy), dptr(w_copy), dptr(g), pooled.device(), argmax->get(),
+                           need_x ? dout(dx) : nullptr, (need_w || need_b) ? dout(dw) : nullptr,
+                           need_b ? dout(db) : nullptr, &cw, co, &pw, nullptr),
+                       "conv2d_relu_maxpool backward");
+            if (need_x) x_copy.add_grad(dx);
+            if (need_w) w_copy.add_grad(dw);
+            if (need_b) b_copy.add_grad(db);
+        };
+    }
+    out = res;
+    return true;
+}
+
 std::string MaxPool2d::name() const {
     return "MaxPool2d(k=" + std::to_string(window_.kernel_h) + ", s=" +
            std::to_string(window_.stride) + ")";

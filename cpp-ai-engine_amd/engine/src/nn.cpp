@@ -1,6 +1,7 @@
 // nn.cpp -- Module plumbing, Linear, Sequential, the losses and the accuracy
 // helpers (the reference's src/nn.cpp).
 #include "engine/nn.hpp"
+#include "engine/conv.hpp"
 
 #include <cmath>
 #include <stdexcept>
@@ -76,9 +77,26 @@ Sequential& Sequential::add(std::unique_ptr<Module> layer) {
     return *this;
 }
 
+// Layer by layer, as the reference does (src/nn.cpp); a Conv2d -> ReLU ->
+// MaxPool2d run is handed to the fused node when it qualifies (same values,
+// one forward launch instead of three, the pool and ReLU backward folded into
+// the convolution's).
 Tensor Sequential::forward(const Tensor& input) {
     Tensor x = input;
-    for (auto& layer : layers_) x = layer->forward(x);
+    for (size_t i = 0; i < layers_.size(); ++i) {
+        if (i + 2 < layers_.size()) {
+            auto* conv = dynamic_cast<Conv2d*>(layers_[i].get());
+            auto* relu = dynamic_cast<ReLU*>(layers_[i + 1].get());
+            auto* pool = dynamic_cast<MaxPool2d*>(layers_[i + 2].get());
+            Tensor fused;
+            if (conv && relu && pool && conv2d_relu_maxpool(x, *conv, *pool, fused)) {
+                x = fused;
+                i += 2;
+                continue;
+            }
+        }
+        x = layers_[i]->forward(x);
+    }
     return x;
 }
 

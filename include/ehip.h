@@ -302,6 +302,35 @@ int ehip_conv2d_backward_weight_f32(const float* x, const float* grad_out, float
                                     float* dbias, const ehip_window_t* w, int64_t out_channels,
                                     void* stream);
 
+/* Conv2d -> ReLU -> MaxPool2d fused, for a narrow convolution followed by a
+ * max pool with disjoint square windows (kernel == stride, no padding): the
+ * Sequential pattern of the reference's CNN (conv, ReLU, pool, twice). `conv`
+ * is the convolution's window over x; `pool` is the pool's window over the
+ * convolution output (batch, channels = out_channels, height = conv out_h,
+ * width = conv out_w). ehip_conv2d_relu_maxpool_supported() says whether a
+ * layer qualifies (1) or must run unfused (0).
+ *   forward: out = the pooled ReLU of the convolution, argmax = the flat index
+ *     into the (N, out_channels, oH, oW) convolution output of each window's
+ *     first strict maximum -- bit-exact with the three reference nodes
+ *     (src/conv.cpp:280-338, src/tensor_ops.cpp:591-600, src/conv.cpp:367-442).
+ *     The convolution output never reaches HBM.
+ *   backward: from the pooled gradient grad_out, the saved out and argmax:
+ *     dx (NULL to skip; bit-exact, as ehip_conv2d_backward_input_f32) and
+ *     dweight/dbias (NULL to skip; as ehip_conv2d_backward_weight_f32), the
+ *     pool and ReLU backward (src/conv.cpp:454-472, src/tensor_ops.cpp:603-615)
+ *     folded into the gradient the two read. All outputs are overwritten. */
+int ehip_conv2d_relu_maxpool_supported(const ehip_window_t* conv, int64_t out_channels,
+                                       const ehip_window_t* pool);
+int ehip_conv2d_relu_maxpool_f32(const float* x, const float* weight, const float* bias,
+                                 float* out, int32_t* argmax, const ehip_window_t* conv,
+                                 int64_t out_channels, const ehip_window_t* pool, void* stream);
+int ehip_conv2d_relu_maxpool_backward_f32(const float* x, const float* weight,
+                                          const float* grad_out, const float* out,
+                                          const int32_t* argmax, float* dx, float* dweight,
+                                          float* dbias, const ehip_window_t* conv,
+                                          int64_t out_channels, const ehip_window_t* pool,
+                                          void* stream);
+
 /* out[i] = x[idx[i]] row by row (rows of row_size floats); an index outside
  * [0, n_rows) yields a row of NaN instead of a read out of bounds.
  * Tensor::select_rows forward (src/tensor.cpp:556-585). Bit-exact. */

@@ -409,6 +409,65 @@ def test_conv2d_direct(hip, orc, shape, co, k, stride, pad, bias):
     exact(host(DW2), host(DW), "dweight repeat")
 
 
+POOL_CASES = [((64, 1, 28, 28), 8, 3, 1, 1, 2), ((64, 8, 14, 14), 16, 3, 1, 1, 2),
+              ((2, 3, 9, 7), 5, 3, 1, 1, 2), ((2, 2, 12, 12), 4, 3, 1, 1, 3),
+              ((3, 2, 11, 10), 3, 2, 2, 0, 2)]
+
+
+@pytest.mark.parametrize("shape,co,k,stride,pad,pk", POOL_CASES)
+@pytest.mark.parametrize("bias_shift", [0.0, -2.0])
+def test_conv2d_relu_maxpool_fused(hip, orc, shape, co, k, stride, pad, pk, bias_shift):
+    """Fused Conv2d -> ReLU -> MaxPool2d against the reference's three nodes replayed on the
+    oracle: pooled values, argmax and the input gradient bit for bit, weight and bias
+    gradients within the fp32 summation bound. A negative bias makes whole windows ReLU to
+    zero, where the first element wins and the gradient is masked."""
+    import _compose as K
+    print_case("conv-relu-pool", shape, co, k, stride, pad, pk, bias_shift)
+    r = rng(sum(shape) + co * 3 + k + pk + int(bias_shift))
+    x = randn(r, *shape)
+    x[..., ::7] = 0.0
+    w = randn(r, co, shape[1], k, k) * 0.5
+    b = randn(r, co) + bias_shift
+    y, cache = K.conv2d_fwd(orc, x, w, b, stride, pad)
+    ry = orc.relu(y)
+    pooled, am = orc.maxpool(ry, pk, pk)
+    P, AM = hip.conv2d_relu_maxpool(dev(x), dev(w), dev(b), stride, pad, pk)
+    exact(host(P), pooled, "pooled")
+    exact(host(AM), am, "argmax")
+    g = randn(r, *pooled.shape)
+    dry = orc.maxpool_backward(am, g, ry.shape)
+    dy = orc.relu_backward(y, dry)
+    dx, dw, db = K.conv2d_bwd(orc, dy, cache)
+    DX, DW, DB = hip.conv2d_relu_maxpool_backward(dev(x), dev(w), dev(g), P, AM, stride, pad, pk)
+    exact(host(DX), dx, "dx")
+    terms = y.shape[0] * y.shape[2] * y.shape[3]
+    ref_close(host(DW), dw, k_tol(terms), "dweight")
+    ref_close(host(DB), db, k_tol(terms), "dbias")
+    cols = orc.im2col(x, k, k, stride, pad).astype(np.float64)
+    g2 = dy.reshape(shape[0], co, -1).transpose(0, 2, 1).reshape(-1, co).astype(np.float64)
+    bound = (terms + 2) * 2.0 ** -24 * (np.abs(g2).T @ np.abs(cols)).reshape(w.shape)
+    assert np.all(np.abs(host(DW) - (g2.T @ cols).reshape(w.shape)) <= bound + 1e-30)
+
+
+def test_conv2d_relu_maxpool_refusals(hip):
+    import ctypes
+    import ehip as E
+    print_case("conv-relu-pool-refusals")
+    cw = E.window(2, 3, 8, 8, 3, 3, 1, 1)
+    overlapping = E.window(2, 4, 8, 8, 3, 3, 2, 0)   # kernel 3, stride 2
+    assert hip.lib.ehip_conv2d_relu_maxpool_supported(ctypes.byref(cw), 4,
+                                                      ctypes.byref(overlapping)) == 0
+    good = E.window(2, 4, 8, 8, 2, 2, 2, 0)
+    assert hip.lib.ehip_conv2d_relu_maxpool_supported(ctypes.byref(cw), 4, ctypes.byref(good)) == 1
+    x = dev(np.zeros(16, np.float32))
+    before = hip.launched()
+    with pytest.raises(RuntimeError, match="kernel == stride"):
+        hip.ok(hip.lib.ehip_conv2d_relu_maxpool_f32(hip.p(x), hip.p(x), None, hip.p(x), hip.p(x),
+                                                    ctypes.byref(cw), 4, ctypes.byref(overlapping),
+                                                    hip.stream()), "fused")
+    assert hip.launched() == before
+
+
 def test_conv2d_direct_refuses_wide_layers(hip):
     import ctypes
     import ehip as E
