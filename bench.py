@@ -158,27 +158,38 @@ def headline(engine_mod, timer, steps, warmup):
     return sec, first, last
 
 
-def dominant_kernel(eng, timer, torch):
+def dominant_kernel(eng, hip, timer, torch):
     """The CNN step's largest kernel by total time (rocprofv3 --kernel-trace --stats of
-    this benchmark, profiles/cnn_step_kernels.md): the conv1 weight-gradient product
-    dW = g^T cols, g (50176 x 8), cols (50176 x 9), a K = 50176 split-K GEMM that streams
-    its two operands once. It is HBM-bound: algorithmic bytes = both operands read once
-    plus the 8 x 9 result written."""
+    this benchmark, profiles/cnn_step_kernels.md): the weight and bias gradient of a fused
+    Conv2d -> ReLU -> MaxPool2d block -- conv_weight_band (per-band partials, the pooled
+    gradient routed through the argmax and the ReLU on the fly) and conv_weight_reduce
+    (their ordered sum) -- timed on the conv1 layer (64 x 1 x 28 x 28 input, 8 3x3
+    filters, 2x2 pool) as one launch pair. HBM-bound by its data, latency-bound at this
+    size: algorithmic bytes = x, the pooled gradient, the pooled values and the argmax read
+    once, dW and db written once."""
+    import ehip as E
     r = torch.Generator(device="cuda").manual_seed(5)
-    g = torch.randn(50176, 8, device="cuda", generator=r)
-    cols = torch.randn(50176, 9, device="cuda", generator=r)
-    out = torch.empty(8, 9, device="cuda")
-    sec = timer.time_batch(lambda n: eng.repeat_gemm(n, g, cols, out, trans_a=True), 500, 50)
-    work = 4 * (50176 * 8 + 50176 * 9 + 8 * 9)
-    return roofline("gemm_kernel<64,64,16,32,32,TA>+splitk_reduce (conv1 dW, 8x9x50176)",
-                    "hbm", work, sec, committed_traffic("conv1_dw"))
+    x = torch.rand(64, 1, 28, 28, device="cuda", generator=r)
+    w = torch.rand(8, 1, 3, 3, device="cuda", generator=r) * 0.6 - 0.3
+    b = torch.zeros(8, device="cuda")
+    out, am = hip.conv2d_relu_maxpool(x, w, b, 1, 1, 2)
+    g = torch.randn(out.shape, device="cuda", generator=r)
+    dw, db = torch.empty_like(w), torch.empty_like(b)
+    cw, pw = hip.conv_relu_pool_windows(x.shape, w.shape, 1, 1, 2)
+    sec = timer.time_batch(
+        lambda n: eng.repeat_conv_relu_pool_backward(n, x, w, g, out, am, dw, db, cw, pw), 500,
+        50)
+    work = 4 * (x.numel() + 3 * out.numel() + w.numel() + b.numel())
+    return roofline("conv_weight_band<1,1,pool>+conv_weight_reduce (conv1 block dW/db, "
+                    "64x1x28x28, 8 filters 3x3, pool 2)", "hbm", work, sec,
+                    committed_traffic("conv1_block_wgrad"))
 
 
 def kernel_only(eng, hip, timer, torch):
     """For counter runs: 100 launches of the dominant kernel, then 100 launches of the
     gradient-initialise kernel over 16 Mi floats (reads 64 MiB, writes 64 MiB), the copy
     of known size that scales FETCH_SIZE / WRITE_SIZE to bytes."""
-    roof = dominant_kernel(eng, timer, torch)
+    roof = dominant_kernel(eng, hip, timer, torch)
     n = 1 << 24
     src = torch.randn(n, device="cuda")
     dst = torch.empty(n, device="cuda")
@@ -207,7 +218,31 @@ def cpu_baseline(seconds_target):
                       f"-march) on {threads} host threads, {dt:.1f} s"}
 
 
-def extras(hip, eng, engine_mod, timer, torch):
+def cpu_charlm_baseline(ids, targets, dims, params, seconds_target):
+    """The char-Transformer (cfg3) step of the reference engine itself on the host cores,
+    from the same initial parameters as the GPU run; a bounded sample of steps."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from _oracle import Ref
+    vocab, d, h, ff, layers = dims
+    threads = int(os.environ.get("BENCH_CPU_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    ref = Ref()
+    ref.set_threads(threads)
+    t0 = time.perf_counter()
+    ref.charlm_train(ids, targets, vocab, d, h, ff, layers, params, 1, 1e-3)
+    per = time.perf_counter() - t0
+    n = max(2, min(500, int(seconds_target / max(per, 1e-6))))
+    t0 = time.perf_counter()
+    losses, _ = ref.charlm_train(ids, targets, vocab, d, h, ff, layers, params, n, 1e-3)
+    dt = time.perf_counter() - t0
+    assert np.all(np.isfinite(losses))
+    return {"value": round(n / dt, 3), "unit": "steps/s", "cores": threads, "kind": "reference",
+            "sample": f"cfg3 char-Transformer step (batch 32 x 64, Adam), {n} consecutive steps "
+                      f"of the reference engine compiled from its own sources (oracle/_ref, -O3, "
+                      f"no -march) on {threads} host threads from the GPU run's initial "
+                      f"parameters, {dt:.1f} s"}
+
+
+def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
     out = {}
     # cfg 1: C = A B and both backward products at 512^3 (805.3 MFLOP per trio), and 4096^3.
     for n in (512, 4096):
@@ -266,6 +301,7 @@ def extras(hip, eng, engine_mod, timer, torch):
             "transformer_cfg5": (16, 512, 256, 1024, 16, 4096, 12, 5, 2)}.items():
         ids, targets = lm_inputs(3, b, s, vocab)
         tr = engine_mod.Trainer.charlm(eng, ids, targets, vocab, d, h, ff, layers, lr=1e-3)
+        p0 = tr.params() if (tag == "charlm_cfg3" and cpu_seconds > 0) else None
         sec = timer.time(tr.step, steps, warm)
         fl = lm_step_flops(b, s, d, ff, vocab, layers)
         out[tag] = {"steps_per_s": round(1.0 / sec, 3), "ms_per_step": round(sec * 1e3, 3),
@@ -274,6 +310,11 @@ def extras(hip, eng, engine_mod, timer, torch):
                     "frac_of_mfma_peak": round(fl / sec / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
                     "loss_after": round(tr.loss(), 5)}
         tr.close()
+        if p0 is not None:
+            log("bench: reference CPU baseline, cfg3")
+            cpu = cpu_charlm_baseline(ids, targets, (vocab, d, h, ff, layers), p0, cpu_seconds)
+            out[tag]["cpu_baseline"] = cpu
+            out[tag]["gpu_over_cpu"] = round(out[tag]["steps_per_s"] / cpu["value"], 1)
     return out
 
 
@@ -311,7 +352,7 @@ def main():
     sec, first, last = headline(engine_capi, timer, args.steps, args.warmup)
     log(f"bench: {sec * 1e3:.4f} ms/step, loss {first:.5f} -> {last:.5f}")
     log("bench: dominant kernel")
-    roof = dominant_kernel(eng, timer, torch)
+    roof = dominant_kernel(eng, hip, timer, torch)
     cpu = None
     if not args.no_cpu:
         log("bench: reference CPU baseline")
@@ -319,7 +360,8 @@ def main():
     extra = None
     if not args.no_extra:
         log("bench: other configurations")
-        extra = extras(hip, eng, engine_capi, timer, torch)
+        extra = extras(hip, eng, engine_capi, timer, torch,
+                       0.0 if args.no_cpu else args.cpu_seconds)
     info = hip.device_info()
     line = {
         "metric": metric_name(),

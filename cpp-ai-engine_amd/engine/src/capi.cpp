@@ -326,6 +326,34 @@ int eng_adam_steps(float* p, const float* grads, int64_t n, int64_t steps, float
     });
 }
 
+// clip_grad_norm over `count` parameters: parameter i has |sizes[i]| elements
+// and, when sizes[i] > 0, the gradient taken from `grads` (concatenated); a
+// negative size is a parameter without a gradient. The clipped gradients are
+// written back over `grads` and the norm to *norm.
+int eng_clip_grad_norm(float* grads, const int64_t* sizes, int count, float max_norm,
+                       float* norm) {
+    return guarded([&] {
+        std::vector<Tensor> ps;
+        size_t off = 0;
+        for (int i = 0; i < count; ++i) {
+            const size_t n = size_t(sizes[i] < 0 ? -sizes[i] : sizes[i]);
+            Tensor P({n}, 0.0f, true);
+            if (sizes[i] > 0) {
+                P.add_grad(make({n}, grads + off, false));
+                off += n;
+            }
+            ps.push_back(P);
+        }
+        *norm = optim::clip_grad_norm(ps, max_norm);
+        off = 0;
+        for (int i = 0; i < count; ++i) {
+            if (sizes[i] <= 0) continue;
+            put(ps[size_t(i)].grad(), grads + off);
+            off += size_t(sizes[i]);
+        }
+    });
+}
+
 int eng_attention_fwd_bwd(const float* q, const float* k, const float* v, const float* mask,
                           int64_t b, int64_t h, int64_t s, int64_t dk, const float* dy, float* y,
                           float* weights, float* dq, float* dkk, float* dv) {
@@ -489,6 +517,24 @@ int eng_repeat_gemm(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t 
             engine::hip::check(ehip_gemm_f32(trans_a, trans_b, batch, m, n, k, a, lda, stride_a, b,
                                              ldb, stride_b, beta, c, ldc, stride_c, stream),
                                "gemm");
+    });
+}
+
+// Enqueues `reps` back-to-back ehip_conv2d_relu_maxpool_backward_f32 calls on
+// `stream` (device pointers; the windows are the entry point's), for timing
+// the fused block's backward kernels with events around the batch.
+int eng_repeat_conv_relu_pool_backward(const float* x, const float* weight, const float* grad_out,
+                                       const float* out, const int32_t* argmax, float* dx,
+                                       float* dweight, float* dbias, const ehip_window_t* conv,
+                                       int64_t out_channels, const ehip_window_t* pool,
+                                       void* stream, int reps) {
+    return guarded([&] {
+        for (int r = 0; r < reps; ++r)
+            engine::hip::check(
+                ehip_conv2d_relu_maxpool_backward_f32(x, weight, grad_out, out, argmax, dx,
+                                                      dweight, dbias, conv, out_channels, pool,
+                                                      stream),
+                "conv2d_relu_maxpool backward");
     });
 }
 

@@ -88,6 +88,18 @@ class Engine:
                    b.data_ptr(), b.shape[1], 0, beta, c.data_ptr(), n, 0,
                    torch.cuda.current_stream().cuda_stream, reps))
 
+    def repeat_conv_relu_pool_backward(self, reps, x, weight, g, out, argmax, dweight, dbias,
+                                       conv_window, pool_window, dx=None):
+        """Enqueues `reps` fused conv-block backward calls from C++ on torch's current stream
+        (torch CUDA tensors; windows are ehip.Window structures)."""
+        import torch
+        f = self.lib.eng_repeat_conv_relu_pool_backward
+        f.argtypes = [C.c_void_p] * 8 + [C.c_void_p, _i64, C.c_void_p, C.c_void_p, C.c_int]
+        ptr = lambda t: t.data_ptr() if t is not None else None
+        self._ok(f(ptr(x), ptr(weight), ptr(g), ptr(out), ptr(argmax), ptr(dx), ptr(dweight),
+                   ptr(dbias), C.addressof(conv_window), weight.shape[0],
+                   C.addressof(pool_window), torch.cuda.current_stream().cuda_stream, reps))
+
     def matmul(self, a, b):
         a, b = _f32(a), _f32(b)
         ab, bb = a.ndim > 2, b.ndim > 2
@@ -225,6 +237,16 @@ class Engine:
         self._ok(self.lib.eng_adam_steps(_fp(p), _fp(grads), p.size, grads.size // p.size, lr,
                                          b1, b2, eps, wd))
         return p
+
+    def clip_grad_norm(self, grads, sizes, max_norm):
+        """grads: concatenated gradients of the parameters whose size is positive; a
+        negative size is a parameter without a gradient. Returns (norm, clipped)."""
+        g = _f32(grads).copy()
+        sz = np.ascontiguousarray(sizes, np.int64)
+        norm = C.c_float()
+        self._ok(self.lib.eng_clip_grad_norm(_fp(g), _ip(sz), len(sz), C.c_float(max_norm),
+                                             C.byref(norm)))
+        return norm.value, g
 
     def attention_fwd_bwd(self, q, k, v, mask, dy):
         q, k, v, dy = _f32(q), _f32(k), _f32(v), _f32(dy)

@@ -317,6 +317,34 @@ int ref_adam_steps(float* p, const float* grads, int64_t n, int64_t steps, float
     });
 }
 
+// optim::clip_grad_norm over `count` parameters: parameter i has |sizes[i]|
+// elements and, when sizes[i] > 0, the gradient taken from `grads`
+// (concatenated); a negative size is a parameter without a gradient. Clipped
+// gradients are written back over `grads`, the norm to *norm.
+int ref_clip_grad_norm(float* grads, const int64_t* sizes, int count, float max_norm,
+                       float* norm) {
+    return guarded([&] {
+        std::vector<Tensor> ps;
+        size_t off = 0;
+        for (int i = 0; i < count; ++i) {
+            const size_t n = size_t(sizes[i] < 0 ? -sizes[i] : sizes[i]);
+            Tensor P({n}, 0.0f, true);
+            if (sizes[i] > 0) {
+                P.add_grad(make({n}, grads + off, false));
+                off += n;
+            }
+            ps.push_back(P);
+        }
+        *norm = optim::clip_grad_norm(ps, max_norm);
+        off = 0;
+        for (int i = 0; i < count; ++i) {
+            if (sizes[i] <= 0) continue;
+            put(ps[size_t(i)].grad(), grads + off);
+            off += size_t(sizes[i]);
+        }
+    });
+}
+
 // Scaled dot-product attention with an optional mask (S,S), forward and
 // backward: q,k,v (B,H,S,dk).
 int ref_attention_fwd_bwd(const float* q, const float* k, const float* v, const float* mask,

@@ -437,6 +437,16 @@ class Ref:
                                          b2, eps, wd))
         return p
 
+    def clip_grad_norm(self, grads, sizes, max_norm):
+        """grads: concatenated gradients of the parameters whose size is positive; a
+        negative size is a parameter without a gradient. Returns (norm, clipped)."""
+        g = f32(grads).copy()
+        sz = np.ascontiguousarray(sizes, np.int64)
+        norm = C.c_float()
+        self._ok(self.lib.ref_clip_grad_norm(fp(g), ip(sz), len(sz), C.c_float(max_norm),
+                                             C.byref(norm)))
+        return norm.value, g
+
     def attention_fwd_bwd(self, q, k, v, mask, dy):
         q, k, v, dy = f32(q), f32(k), f32(v), f32(dy)
         b, h, s, dk = q.shape

@@ -198,6 +198,28 @@ def test_fixture_transformer_block(eng):
         off += want.size
 
 
+@pytest.mark.parametrize("max_norm", [0.5, 1e6])
+def test_clip_grad_norm_vs_reference(eng, max_norm):
+    """optim::clip_grad_norm (src/optim.cpp:168-208) against the compiled reference: one
+    global norm over every gradient (a parameter without one is skipped), scaled by
+    max_norm / (norm + 1e-6) only when the norm exceeds max_norm."""
+    from _oracle import ref_or_skip
+    ref = ref_or_skip()
+    print_case("clip-grad-norm", max_norm)
+    r = np.random.default_rng(12)
+    sizes = [1000, -37, 4096, 3, 70001]
+    n = sum(s for s in sizes if s > 0)
+    g = r.standard_normal(n).astype(np.float32)
+    norm, clipped = eng.clip_grad_norm(g, sizes, max_norm)
+    want_norm, want = ref.clip_grad_norm(g, sizes, max_norm)
+    exact64 = float(np.sqrt((g.astype(np.float64) ** 2).sum()))
+    assert abs(norm - want_norm) <= 1e-6 * want_norm, (norm, want_norm)
+    assert abs(norm - exact64) <= 1e-6 * exact64
+    ref_close(clipped, want, 1e-6, "clipped gradients")
+    if max_norm >= exact64:
+        np.testing.assert_array_equal(clipped, g)  # no clipping: untouched
+
+
 def test_fixture_adam_trajectory(eng):
     print_case("fixture adam")
     f = load("adam")
