@@ -45,6 +45,11 @@ public:
          float beta2 = 0.999f, float eps = 1e-8f, float weight_decay = 0.0f);
     void step() override;
     size_t steps() const noexcept { return t_; }
+    // Moments and step count for a checkpoint: state_tensors() holds the
+    // first and second moments of parameter i at 2i and 2i + 1 (views of the
+    // optimizer's buffers); set_state() copies them back (shapes must match).
+    std::vector<Tensor> state_tensors() const;
+    void set_state(size_t t, const std::vector<Tensor>& moments);
 
 private:
     float beta1_;

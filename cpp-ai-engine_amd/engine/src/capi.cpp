@@ -23,6 +23,7 @@
 #include "engine/hip.hpp"
 #include "engine/nn.hpp"
 #include "engine/optim.hpp"
+#include "engine/serialize.hpp"
 #include "engine/tensor.hpp"
 #include "engine/transformer.hpp"
 
@@ -103,6 +104,14 @@ struct CharModel {
         Tensor h = embedding.forward(ids) + positions;
         for (nn::TransformerBlock& b : blocks) h = b.forward(h, &mask);
         return head.forward(h);
+    }
+    engine::NamedTensors named_parameters() {
+        engine::NamedTensors out = embedding.named_parameters("embedding.");
+        for (size_t i = 0; i < blocks.size(); ++i)
+            for (auto& np : blocks[i].named_parameters("block" + std::to_string(i) + "."))
+                out.push_back(np);
+        for (auto& np : head.named_parameters("head.")) out.push_back(np);
+        return out;
     }
     std::vector<Tensor> parameters() {
         std::vector<Tensor> out = embedding.parameters();
@@ -581,6 +590,32 @@ void* eng_trainer_charlm(const float* ids, const int64_t* targets, int64_t batch
         t = tr.release();
     });
     return rc == 0 ? t : nullptr;
+}
+
+// Checkpoints of a trainer: the model's parameters in the reference's weight
+// format at params_path, and (when opt_path is not NULL) the Adam state.
+int eng_trainer_save(void* h, const char* params_path, const char* opt_path) {
+    return guarded([&] {
+        Trainer* t = static_cast<Trainer*>(h);
+        if (t->cnn)
+            engine::save_parameters(*t->cnn, params_path);
+        else
+            engine::save_parameters(t->lm->named_parameters(), params_path);
+        if (opt_path) engine::save_optimizer(*t->opt, opt_path);
+    });
+}
+
+int eng_trainer_load(void* h, const char* params_path, const char* opt_path) {
+    return guarded([&] {
+        Trainer* t = static_cast<Trainer*>(h);
+        if (t->cnn) {
+            engine::load_parameters(*t->cnn, params_path, true);
+        } else {
+            engine::NamedTensors named = t->lm->named_parameters();
+            engine::load_parameters(named, params_path, true);
+        }
+        if (opt_path) engine::load_optimizer(*t->opt, opt_path);
+    });
 }
 
 int eng_trainer_step(void* h) {

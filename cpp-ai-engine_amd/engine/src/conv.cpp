@@ -283,8 +283,8 @@ bool conv2d_relu_maxpool(const Tensor& input, Conv2d& conv, const MaxPool2d& poo
 }
 
 std::string MaxPool2d::name() const {
-    return "MaxPool2d(k=" + std::to_string(window_.kernel_h) + ", s=" +
-           std::to_string(window_.stride) + ")";
+    return "MaxPool2d(k=" + std::to_string(window_.kernel_h) + "x" +
+           std::to_string(window_.kernel_w) + ", s=" + std::to_string(window_.stride) + ")";
 }
 
 Tensor Flatten::forward(const Tensor& input) {

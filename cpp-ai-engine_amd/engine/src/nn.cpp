@@ -17,7 +17,7 @@ std::vector<std::pair<std::string, Tensor>> Module::named_parameters(const std::
     std::vector<std::pair<std::string, Tensor>> out;
     const std::vector<Tensor> params = parameters();
     for (size_t i = 0; i < params.size(); ++i)
-        out.emplace_back(prefix + std::to_string(i), params[i]);
+        out.emplace_back(prefix + name() + "." + std::to_string(i), params[i]);
     return out;
 }
 

@@ -77,6 +77,36 @@ void Adam::step() {
                "adam step");
 }
 
+std::vector<Tensor> Adam::state_tensors() const {
+    std::vector<Tensor> out;
+    out.reserve(2 * m_.size());
+    for (size_t i = 0; i < m_.size(); ++i) {
+        out.push_back(view_with_shape(m_[i], {m_[i].size()}, false));
+        out.push_back(view_with_shape(v_[i], {v_[i].size()}, false));
+    }
+    return out;
+}
+
+void Adam::set_state(size_t t, const std::vector<Tensor>& moments) {
+    if (moments.size() != 2 * m_.size())
+        throw std::invalid_argument("Adam::set_state: " + std::to_string(moments.size()) +
+                                    " moment tensors for " + std::to_string(m_.size()) +
+                                    " parameters.");
+    for (size_t i = 0; i < moments.size(); ++i) {
+        Storage& dst = (i % 2 == 0) ? m_[i / 2] : v_[i / 2];
+        if (moments[i].size() != dst.size())
+            throw std::invalid_argument("Adam::set_state: moment " + std::to_string(i) +
+                                        " has " + std::to_string(moments[i].size()) +
+                                        " values, the optimizer " + std::to_string(dst.size()) +
+                                        ".");
+        if (dst.size() > 0)
+            hip::check(ehip_memcpy_d2d(dst.device_write(), dptr(moments[i]),
+                                       dst.size() * sizeof(float), nullptr),
+                       "Adam::set_state");
+    }
+    t_ = t;
+}
+
 // src/optim.cpp:168-208: the norm needs one host read (it decides whether to scale).
 float clip_grad_norm(const std::vector<Tensor>& parameters, float max_norm) {
     if (max_norm <= 0.0f) throw std::invalid_argument("clip_grad_norm needs a positive max_norm.");

@@ -60,7 +60,7 @@ Tensor LayerNorm::forward(const Tensor& input) {
 std::vector<Tensor> LayerNorm::parameters() { return {gamma_, beta_}; }
 
 std::vector<std::pair<std::string, Tensor>> LayerNorm::named_parameters(const std::string& prefix) {
-    return {{prefix + "gamma", gamma_}, {prefix + "beta", beta_}};
+    return {{prefix + "layernorm.gamma", gamma_}, {prefix + "layernorm.beta", beta_}};
 }
 
 std::string LayerNorm::name() const { return "LayerNorm(" + std::to_string(normalized_size_) + ")"; }
@@ -96,11 +96,11 @@ Tensor Embedding::forward(const Tensor& ids) {
 std::vector<Tensor> Embedding::parameters() { return {weight_}; }
 
 std::vector<std::pair<std::string, Tensor>> Embedding::named_parameters(const std::string& prefix) {
-    return {{prefix + "weight", weight_}};
+    return {{prefix + "embedding.weight", weight_}};
 }
 
 std::string Embedding::name() const {
-    return "Embedding(" + std::to_string(num_embeddings_) + ", " + std::to_string(dim_) + ")";
+    return "Embedding(" + std::to_string(num_embeddings_) + " x " + std::to_string(dim_) + ")";
 }
 
 // Sinusoidal table, float std::pow/sin/cos on the host (src/transformer.cpp:249-267).
@@ -187,16 +187,15 @@ std::vector<std::pair<std::string, Tensor>> MultiHeadAttention::named_parameters
     std::vector<std::pair<std::string, Tensor>> out;
     const char* names[] = {"query.", "key.", "value.", "out."};
     Linear* layers[] = {&w_query_, &w_key_, &w_value_, &w_out_};
-    for (int i = 0; i < 4; ++i) {
-        out.emplace_back(prefix + names[i] + "weight", layers[i]->weight());
-        out.emplace_back(prefix + names[i] + "bias", layers[i]->bias());
-    }
+    for (int i = 0; i < 4; ++i)
+        for (auto& np : layers[i]->named_parameters(prefix + "attn." + names[i])) out.push_back(np);
     return out;
 }
 
 std::string MultiHeadAttention::name() const {
     return "MultiHeadAttention(d_model=" + std::to_string(d_model_) + ", heads=" +
-           std::to_string(num_heads_) + ")";
+           std::to_string(num_heads_) + ", head_dim=" + std::to_string(d_model_ / num_heads_) +
+           ")";
 }
 
 TransformerBlock::TransformerBlock(size_t d_model, size_t num_heads, size_t ff_hidden)
@@ -233,10 +232,8 @@ std::vector<std::pair<std::string, Tensor>> TransformerBlock::named_parameters(
     for (auto& np : norm1_.named_parameters(prefix + "norm1.")) out.push_back(np);
     for (auto& np : norm2_.named_parameters(prefix + "norm2.")) out.push_back(np);
     for (auto& np : attention_.named_parameters(prefix)) out.push_back(np);
-    out.emplace_back(prefix + "ff1.weight", ff1_.weight());
-    out.emplace_back(prefix + "ff1.bias", ff1_.bias());
-    out.emplace_back(prefix + "ff2.weight", ff2_.weight());
-    out.emplace_back(prefix + "ff2.bias", ff2_.bias());
+    for (auto& np : ff1_.named_parameters(prefix + "ff1.")) out.push_back(np);
+    for (auto& np : ff2_.named_parameters(prefix + "ff2.")) out.push_back(np);
     return out;
 }
 

@@ -350,6 +350,19 @@ class Trainer:
         return cls(engine, engine.lib.eng_trainer_charlm(_fp(ids), _ip(targets), b, s, vocab, d,
                                                          heads, ff, layers, p, lr))
 
+    def save(self, params_path, opt_path=None):
+        """Parameters in the reference's weight format; Adam state too when opt_path."""
+        f = self.lib.eng_trainer_save
+        f.argtypes = [C.c_void_p, C.c_char_p, C.c_char_p]
+        if f(self.h, params_path.encode(), opt_path.encode() if opt_path else None) != 0:
+            raise RuntimeError(self.lib.eng_last_error().decode())
+
+    def load(self, params_path, opt_path=None):
+        f = self.lib.eng_trainer_load
+        f.argtypes = [C.c_void_p, C.c_char_p, C.c_char_p]
+        if f(self.h, params_path.encode(), opt_path.encode() if opt_path else None) != 0:
+            raise RuntimeError(self.lib.eng_last_error().decode())
+
     def step(self):
         if self.lib.eng_trainer_step(self.h) != 0:
             raise RuntimeError(self.lib.eng_last_error().decode())

@@ -16,6 +16,7 @@
 #include "engine/nn.hpp"
 #include "engine/optim.hpp"
 #include "engine/parallel.hpp"
+#include "engine/serialize.hpp"
 #include "engine/tensor.hpp"
 #include "engine/transformer.hpp"
 
@@ -395,6 +396,28 @@ int64_t ref_block_num_params(int64_t d, int64_t heads, int64_t ff) {
 
 // cfg 2: the small CNN, `steps` Adam steps on one fixed batch. params is the
 // flat parameters() concatenation; losses receives one value per step.
+// The CNN of cnn_model with the flat parameters `params`, saved by the
+// reference's save_parameters to `path`.
+int ref_cnn_save(const float* params, int64_t in_c, int64_t c1, int64_t c2, int64_t hw,
+                 int64_t classes, const char* path) {
+    return guarded([&] {
+        auto model = cnn_model(size_t(in_c), size_t(c1), size_t(c2), size_t(hw), size_t(classes));
+        load_params(model->parameters(), params);
+        engine::save_parameters(*model, path);
+    });
+}
+
+// A CNN of cnn_model loaded by the reference's load_parameters (strict) from
+// `path`; its flat parameters go to params_out.
+int ref_cnn_load(const char* path, int64_t in_c, int64_t c1, int64_t c2, int64_t hw,
+                 int64_t classes, float* params_out) {
+    return guarded([&] {
+        auto model = cnn_model(size_t(in_c), size_t(c1), size_t(c2), size_t(hw), size_t(classes));
+        engine::load_parameters(*model, path, true);
+        store_params(model->parameters(), params_out);
+    });
+}
+
 int ref_cnn_train(const float* x, const int64_t* labels, int64_t batch, int64_t in_c, int64_t c1,
                   int64_t c2, int64_t hw, int64_t classes, const float* params, int64_t steps,
                   float lr, float* losses, float* params_out) {

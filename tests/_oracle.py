@@ -437,6 +437,19 @@ class Ref:
                                          b2, eps, wd))
         return p
 
+    def cnn_save(self, params, path, in_c=1, c1=8, c2=16, hw=28, classes=10):
+        """The reference's save_parameters of its CNN holding `params`."""
+        p = f32(params)
+        self.lib.ref_cnn_save.argtypes = [_f32p] + [_i64] * 5 + [C.c_char_p]
+        self._ok(self.lib.ref_cnn_save(fp(p), in_c, c1, c2, hw, classes, path.encode()))
+
+    def cnn_load(self, path, n_params, in_c=1, c1=8, c2=16, hw=28, classes=10):
+        """The reference's strict load_parameters into its CNN; the flat parameters."""
+        out = np.empty(n_params, np.float32)
+        self.lib.ref_cnn_load.argtypes = [C.c_char_p] + [_i64] * 5 + [_f32p]
+        self._ok(self.lib.ref_cnn_load(path.encode(), in_c, c1, c2, hw, classes, fp(out)))
+        return out
+
     def clip_grad_norm(self, grads, sizes, max_norm):
         """grads: concatenated gradients of the parameters whose size is positive; a
         negative size is a parameter without a gradient. Returns (norm, clipped)."""

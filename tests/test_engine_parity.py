@@ -390,3 +390,89 @@ def test_transformer_medium_trajectory(eng, orc, cpu):
     print("medium loss", losses, "rel err", rel)
     assert np.all(rel <= 1e-5), rel
     assert np.max(np.abs(out - want_out)) <= steps * 1e-3 * 2
+
+
+# ------------------------------------------------------------------ checkpoints
+
+def test_checkpoint_interop_with_reference(eng, tmp_path):
+    """Parameters saved by the engine load in the compiled reference (strict names and
+    shapes, the reference's weight format) with the same bits, and the other way round."""
+    from engine_capi import Trainer
+    from _oracle import ref_or_skip
+    ref = ref_or_skip()
+    print_case("checkpoint interop")
+    x, labels, params = cnn_inputs()
+    tr = Trainer.cnn(eng, x, labels, params, lr=1e-3)
+    for _ in range(3):
+        tr.step()
+    p3 = tr.params()
+    path = str(tmp_path / "engine.cppaieng")
+    tr.save(path)
+    np.testing.assert_array_equal(ref.cnn_load(path, p3.size), p3)
+    q = (rng(41).standard_normal(p3.size) * 0.1).astype(np.float32)
+    path2 = str(tmp_path / "reference.cppaieng")
+    ref.cnn_save(q, path2)
+    tr2 = Trainer.cnn(eng, x, labels, None, lr=1e-3)
+    tr2.load(path2)
+    np.testing.assert_array_equal(tr2.params(), q)
+    tr.close()
+    tr2.close()
+
+
+def test_checkpoint_exact_resume(eng, tmp_path):
+    """Six Adam steps in one run equal three steps, a save of the parameters and the Adam
+    state, a load into a freshly initialised trainer and three more steps -- bit for bit."""
+    from engine_capi import Trainer
+    print_case("checkpoint resume")
+    x, labels, params = cnn_inputs()
+    whole = Trainer.cnn(eng, x, labels, params, lr=1e-3)
+    for _ in range(6):
+        whole.step()
+    want = whole.params()
+    first = Trainer.cnn(eng, x, labels, params, lr=1e-3)
+    for _ in range(3):
+        first.step()
+    pp, op = str(tmp_path / "p.cppaieng"), str(tmp_path / "adam.cppaieng")
+    first.save(pp, op)
+    second = Trainer.cnn(eng, x, labels, None, lr=1e-3)
+    second.load(pp, op)
+    for _ in range(3):
+        second.step()
+    np.testing.assert_array_equal(second.params(), want)
+    for t in (whole, first, second):
+        t.close()
+
+
+def test_checkpoint_refuses_bad_files(eng, tmp_path):
+    """A truncated file, another format and a shape mismatch are errors, not crashes."""
+    from engine_capi import Trainer
+    print_case("checkpoint refusals")
+    x, labels, params = cnn_inputs()
+    tr = Trainer.cnn(eng, x, labels, params, lr=1e-3)
+    good = tmp_path / "good.cppaieng"
+    tr.save(str(good))
+    data = good.read_bytes()
+    bad = tmp_path / "truncated.cppaieng"
+    bad.write_bytes(data[: len(data) // 2])
+    with pytest.raises(RuntimeError, match="ends inside"):
+        tr.load(str(bad))
+    other = tmp_path / "other.bin"
+    other.write_bytes(b"NOTAFILE" + data[8:])
+    with pytest.raises(RuntimeError, match="not a CPPAIENG"):
+        tr.load(str(other))
+    small = Trainer.cnn(eng, x, labels, None, lr=1e-3, c1=4)
+    with pytest.raises(RuntimeError, match="has no tensor"):  # names carry the layer shapes
+        small.load(str(good))
+    # Same names, same value count, another shape: the first tensor's (8, 1, 3, 3) -> (8, 1, 9, 1).
+    import struct
+    name_len = struct.unpack_from("<I", data, 16)[0]
+    dims_at = 16 + 4 + name_len + 4
+    assert struct.unpack_from("<4Q", data, dims_at) == (8, 1, 3, 3)
+    reshaped = bytearray(data)
+    struct.pack_into("<4Q", reshaped, dims_at, 8, 1, 9, 1)
+    odd = tmp_path / "reshaped.cppaieng"
+    odd.write_bytes(bytes(reshaped))
+    with pytest.raises(RuntimeError, match="in the model and"):
+        tr.load(str(odd))
+    tr.close()
+    small.close()
