@@ -84,6 +84,7 @@ _SIGS = {
     "ehip_maxpool_backward_f32": [_vp, _vp, _vp, C.POINTER(Window), _vp],
     "ehip_maxpool_fidx_f32": [_vp, _vp, _vp, C.POINTER(Window), _vp],
     "ehip_maxpool_backward_fidx_f32": [_vp, _vp, _vp, C.POINTER(Window), _vp],
+    "ehip_dropout_f32": [_vp, _vp, _vp, _i64, _f, C.c_uint64, C.c_uint64, _vp],
     "ehip_conv2d_direct_supported": [C.POINTER(Window), _i64],
     "ehip_conv2d_forward_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_backward_input_f32": [_vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
@@ -377,6 +378,13 @@ class Backend:
             self.p(dx) if need_dx else None, self.p(dw), self.p(db) if bias else None,
             C.byref(cw), co, C.byref(pw), self.stream()), "conv2d_relu_maxpool_backward")
         return dx, dw, db
+
+    def dropout(self, x, p, seed, offset=0, want_mask=True):
+        y = self.f32(x.shape)
+        m = self.f32(x.shape) if want_mask else None
+        self.ok(self.lib.ehip_dropout_f32(self.p(x), self.p(y), self.p(m) if want_mask else None,
+                                          x.numel(), p, seed, offset, self.stream()), "dropout")
+        return y, m
 
     def select_rows(self, x, idx):
         rs = x.numel() // x.shape[0]

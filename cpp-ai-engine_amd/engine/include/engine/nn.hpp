@@ -64,6 +64,23 @@ public:
     std::string name() const override { return "ReLU"; }
 };
 
+// Inverted dropout (the reference's include/engine/nn.hpp Dropout): in
+// training, each element is kept with probability 1 - p and scaled by
+// 1 / (1 - p); in evaluation it is the identity. Masks come from the device
+// generator (Philox, keyed by the engine seed, advanced by a running element
+// counter): reproducible after manual_seed(), but not the reference's host
+// mt19937 stream.
+class Dropout : public Module {
+public:
+    explicit Dropout(float p = 0.5f);
+    Tensor forward(const Tensor& input) override;
+    std::string name() const override;
+    float probability() const noexcept { return p_; }
+
+private:
+    float p_;
+};
+
 class Softmax : public Module {
 public:
     Tensor forward(const Tensor& input) override { return input.softmax(); }

@@ -26,6 +26,16 @@ namespace engine {
 // initialisation (the reference's src/tensor.cpp:24-31).
 void manual_seed(uint64_t seed);
 
+// The device generator behind Dropout: its seed (set by manual_seed, 5489
+// until then) and the counter offset of the next draw; device_rng_take(n)
+// returns the offset for n values and advances it past them (rounded up to a
+// whole Philox block of four).
+struct DeviceRng {
+    uint64_t seed;
+    uint64_t offset;
+};
+DeviceRng device_rng_take(size_t n);
+
 class Tensor {
 private:
     std::shared_ptr<TensorImpl> impl_;

@@ -335,6 +335,22 @@ int eng_adam_steps(float* p, const float* grads, int64_t n, int64_t steps, float
     });
 }
 
+// nn::Dropout(p) after manual_seed(seed), forward and backward on n values
+// (train mode, or eval mode when `eval` is nonzero).
+int eng_dropout_fwd_bwd(const float* x, int64_t n, float p, uint64_t seed, int eval,
+                        const float* dy, float* y, float* dx) {
+    return guarded([&] {
+        engine::manual_seed(seed);
+        nn::Dropout drop(p);
+        drop.train(eval == 0);
+        Tensor X = make({size_t(n)}, x, true);
+        Tensor Y = drop(X);
+        Y.backward(make({size_t(n)}, dy, false));
+        put(Y, y);
+        put(X.grad(), dx);
+    });
+}
+
 // clip_grad_norm over `count` parameters: parameter i has |sizes[i]| elements
 // and, when sizes[i] > 0, the gradient taken from `grads` (concatenated); a
 // negative size is a parameter without a gradient. The clipped gradients are

@@ -77,6 +77,38 @@ Sequential& Sequential::add(std::unique_ptr<Module> layer) {
     return *this;
 }
 
+Dropout::Dropout(float p) : p_(p) {
+    if (!(p >= 0.0f && p < 1.0f))
+        throw std::invalid_argument("Dropout needs a probability in [0, 1).");
+}
+
+// src/nn.cpp:206-244 with the mask drawn on the device; the backward
+// multiplies by the same mask.
+Tensor Dropout::forward(const Tensor& input) {
+    if (!is_training() || p_ == 0.0f) return input;
+    Tensor out(input.shape(), 0.0f, false);
+    Tensor mask(input.shape(), 0.0f, false);
+    const DeviceRng draw = device_rng_take(input.size());
+    hip::check(ehip_dropout_f32(dptr(input), dout(out), dout(mask), int64_t(input.size()), p_,
+                                draw.seed, draw.offset, nullptr),
+               "dropout");
+    if (track(input.requires_grad())) {
+        out.set_requires_grad(true);
+        out.get_impl()->parents = {input.get_impl()};
+        Tensor input_copy = input;
+        out.get_impl()->backward_fn = [input_copy, mask](const Tensor& g) mutable {
+            Tensor dx(input_copy.shape(), 0.0f, false);
+            hip::check(ehip_binary_f32(EHIP_MUL, dptr(g), dptr(mask), dout(dx),
+                                       int64_t(dx.size()), 1, nullptr),
+                       "dropout backward");
+            input_copy.add_grad(dx);
+        };
+    }
+    return out;
+}
+
+std::string Dropout::name() const { return "Dropout(p=" + std::to_string(p_).substr(0, 4) + ")"; }
+
 // Layer by layer, as the reference does (src/nn.cpp); a Conv2d -> ReLU ->
 // MaxPool2d run is handed to the fused node when it qualifies (same values,
 // one forward launch instead of three, the pool and ReLU backward folded into

@@ -22,7 +22,22 @@ std::mt19937& global_rng() {
     return gen;
 }
 
+namespace {
+DeviceRng& device_rng() {
+    static DeviceRng g{5489u, 0u};
+    return g;
+}
+}  // namespace
+
+DeviceRng device_rng_take(size_t n) {
+    DeviceRng& g = device_rng();
+    const DeviceRng now = g;
+    g.offset += (uint64_t(n) + 3) / 4 * 4;
+    return now;
+}
+
 void manual_seed(uint64_t seed) {
+    device_rng() = DeviceRng{seed, 0u};
     global_rng().seed(static_cast<std::mt19937::result_type>(seed));
 }
 

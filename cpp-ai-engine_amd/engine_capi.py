@@ -238,6 +238,14 @@ class Engine:
                                          b1, b2, eps, wd))
         return p
 
+    def dropout_fwd_bwd(self, x, p, seed, dy, eval_mode=False):
+        x, dy = _f32(x), _f32(dy)
+        y, dx = np.empty_like(x), np.empty_like(x)
+        f = self.lib.eng_dropout_fwd_bwd
+        f.argtypes = [_f32p, _i64, C.c_float, C.c_uint64, C.c_int, _f32p, _f32p, _f32p]
+        self._ok(f(_fp(x), x.size, p, seed, int(eval_mode), _fp(dy), _fp(y), _fp(dx)))
+        return y, dx
+
     def clip_grad_norm(self, grads, sizes, max_norm):
         """grads: concatenated gradients of the parameters whose size is positive; a
         negative size is a parameter without a gradient. Returns (norm, clipped)."""

@@ -348,6 +348,17 @@ int ehip_scatter_add_rows_f32(const float* g, const int32_t* row_ptr, const int3
                               float* dx, int64_t n_rows, int64_t row_size, int64_t n_src,
                               int accumulate, void* stream);
 
+/* Dropout: y = x * m with m = 1 / (1 - p) where element i is kept, else 0;
+ * mask (may be NULL) receives m for the backward (dx = g * m, ehip_binary_f32
+ * EHIP_MUL). Element i is kept when the 24-bit uniform drawn for counter value
+ * offset + i by Philox4x32-10 keyed by `seed` (word (offset + i) % 4 of block
+ * (offset + i) / 4) is below 1 - p: reproducible from (seed, offset) on any
+ * device and launch shape. Replaces the mask loop of Dropout::forward
+ * (src/nn.cpp:206-244), whose sequential mt19937 stream it does not reproduce;
+ * the kept values use the reference's arithmetic (x * (1 / keep)). */
+int ehip_dropout_f32(const float* x, float* y, float* mask, int64_t n, float p, uint64_t seed,
+                     uint64_t offset, void* stream);
+
 /* ------------------------------------------------------------- reductions */
 
 /* Sum over the middle axis of an (outer, axis_len, inner) view.

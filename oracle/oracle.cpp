@@ -411,4 +411,44 @@ void orc_causal_mask(float* out, int64_t seq_len, float masked_value) {
         for (int64_t j = 0; j < seq_len; ++j) out[i * seq_len + j] = j > i ? masked_value : 0.0f;
 }
 
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; ++r) {
+        if (r > 0) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        const uint64_t p0 = uint64_t(0xD2511F53u) * c0, p1 = uint64_t(0xCD9E8D57u) * c2;
+        const uint32_t hi0 = uint32_t(p0 >> 32), lo0 = uint32_t(p0);
+        const uint32_t hi1 = uint32_t(p1 >> 32), lo1 = uint32_t(p1);
+        const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+        c0 = n0;
+        c1 = lo1;
+        c2 = n2;
+        c3 = lo0;
+    }
+    out[0] = c0;
+    out[1] = c1;
+    out[2] = c2;
+    out[3] = c3;
+}
+
+void orc_dropout(const float* x, float* y, float* mask, int64_t n, float p, uint64_t seed,
+                 uint64_t offset) {
+    const float keep = 1.0f - p;
+    const float scale = 1.0f / keep;
+    const uint32_t key[2] = {uint32_t(seed), uint32_t(seed >> 32)};
+    for (int64_t i = 0; i < n; ++i) {
+        const uint64_t c = offset + uint64_t(i), b = c / 4;
+        const uint32_t ctr[4] = {uint32_t(b), uint32_t(b >> 32), 0u, 0u};
+        uint32_t w[4];
+        orc_philox4x32_10(ctr, key, w);
+        const float u = float(w[c % 4] >> 8) * (1.0f / 16777216.0f);
+        const float m = u < keep ? scale : 0.0f;
+        mask[i] = m;
+        y[i] = x[i] * m;
+    }
+}
+
 }  // extern "C"

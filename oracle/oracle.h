@@ -132,6 +132,20 @@ void orc_scatter_add_rows(const float* g, const int64_t* idx, float* dx, int64_t
 void orc_positional_encoding(float* out, int64_t seq_len, int64_t d_model);
 void orc_causal_mask(float* out, int64_t seq_len, float masked_value);
 
+/* Philox4x32-10 (Salmon et al., SC'11) on counter {c0..c3} and key {k0, k1}.
+ * Pinned by the published Random123 known-answer vectors
+ * (tests/test_oracle_fixtures.py). */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
+/* Dropout as the device computes it: element i kept when the top 24 bits of
+ * word (offset + i) % 4 of philox((offset + i) / 4; seed), over 2^24, are
+ * below keep = 1 - p; mask[i] = keep ? 1 / keep : 0 and y = x * mask. The
+ * reference (src/nn.cpp:206-244) draws from a sequential mt19937 instead, so
+ * the masks are not the reference's: the checks are the generator's known
+ * answers, the keep rate, and y and the backward given the mask. */
+void orc_dropout(const float* x, float* y, float* mask, int64_t n, float p, uint64_t seed,
+                 uint64_t offset);
+
 #ifdef __cplusplus
 }
 #endif

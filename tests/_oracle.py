@@ -275,6 +275,23 @@ class Oracle:
         self.lib.orc_scatter_add_rows(fp(g), ip(idx), fp(dx), _i64(len(idx)), _i64(rs))
         return dx
 
+    def philox(self, ctr, key):
+        c = np.ascontiguousarray(ctr, np.uint32)
+        k = np.ascontiguousarray(key, np.uint32)
+        out = np.empty(4, np.uint32)
+        u32p = C.POINTER(C.c_uint32)
+        self.lib.orc_philox4x32_10(c.ctypes.data_as(u32p), k.ctypes.data_as(u32p),
+                                   out.ctypes.data_as(u32p))
+        return out
+
+    def dropout(self, x, p, seed, offset=0):
+        x = f32(x)
+        y, m = np.empty_like(x), np.empty_like(x)
+        self.lib.orc_dropout.argtypes = [_f32p, _f32p, _f32p, _i64, C.c_float, C.c_uint64,
+                                         C.c_uint64]
+        self.lib.orc_dropout(fp(x), fp(y), fp(m), x.size, p, seed, offset)
+        return y, m
+
     def positional_encoding(self, s, d):
         out = np.empty((s, d), np.float32)
         self.lib.orc_positional_encoding(fp(out), _i64(s), _i64(d))

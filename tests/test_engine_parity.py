@@ -476,3 +476,23 @@ def test_checkpoint_refuses_bad_files(eng, tmp_path):
         tr.load(str(odd))
     tr.close()
     small.close()
+
+
+# ------------------------------------------------------------------ dropout
+
+@pytest.mark.parametrize("p", [0.1, 0.5])
+def test_dropout_module(eng, orc, p):
+    """nn::Dropout after manual_seed(s): the first draw is the generator's mask at offset
+    0 (the Philox restatement), y = x * mask and dx = dy * mask bit for bit; in evaluation
+    mode the layer is the identity and passes the gradient through."""
+    print_case("dropout module", p)
+    r = rng(8)
+    n = 10007
+    x, dy = r.standard_normal(n).astype(np.float32), r.standard_normal(n).astype(np.float32)
+    y, dx = eng.dropout_fwd_bwd(x, p, 2024, dy)
+    want_y, m = orc.dropout(x, p, 2024, 0)
+    np.testing.assert_array_equal(y, want_y)
+    np.testing.assert_array_equal(dx, (dy * m).astype(np.float32))
+    y2, dx2 = eng.dropout_fwd_bwd(x, p, 2024, dy, eval_mode=True)
+    np.testing.assert_array_equal(y2, x)
+    np.testing.assert_array_equal(dx2, dy)

@@ -501,6 +501,19 @@ def test_maxpool_exact(hip, orc, shape, k, stride, float_index):
           orc.maxpool_backward(am, g, shape), "maxpool backward")
 
 
+@pytest.mark.parametrize("n,p,seed,offset", [(1, 0.5, 7, 0), (1000, 0.1, 2 ** 40 + 3, 0),
+                                           (4097, 0.5, 99, 3), ((1 << 20) + 5, 0.9, 5, 2 ** 33 + 1),
+                                           (777, 0.0, 1, 8)])
+def test_dropout_matches_oracle(hip, orc, n, p, seed, offset):
+    """The device mask, output and kept scale equal the Philox restatement bit for bit."""
+    print_case("dropout", n, p, seed, offset)
+    x = randn(rng(n), n)
+    want_y, want_m = orc.dropout(x, p, seed, offset)
+    y, m = hip.dropout(dev(x), p, seed, offset)
+    exact(host(m), want_m, "mask")
+    exact(host(y), want_y, "y")
+
+
 def test_select_and_scatter_rows_exact(hip, orc):
     print_case("select-scatter")
     r = rng(8)

@@ -221,3 +221,38 @@ def test_positional_encoding_closed_form(orc):
 def test_causal_mask_closed_form(orc):
     m = orc.causal_mask(5)
     assert np.array_equal(m, np.triu(np.full((5, 5), -1e9, np.float32), 1))
+
+
+# Random123's published known-answer vectors for Philox4x32-10 (counter, key, output).
+PHILOX_KAT = [
+    ((0, 0, 0, 0), (0, 0), (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+    ((0xffffffff,) * 4, (0xffffffff, 0xffffffff), (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+    ((0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344), (0xa4093822, 0x299f31d0),
+     (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", PHILOX_KAT)
+def test_philox_known_answers(orc, ctr, key, want):
+    assert tuple(int(v) for v in orc.philox(ctr, key)) == want
+
+
+def test_dropout_oracle_properties(orc):
+    """The dropout restatement: the keep rate is binomial around 1 - p (5 sigma), kept
+    values are x / keep exactly, dropped ones 0, and the mask depends only on the counter
+    (a call at offset k equals the tail of a call at 0)."""
+    r = np.random.default_rng(5)
+    n, p = 1 << 20, 0.3
+    x = r.standard_normal(n).astype(np.float32)
+    y, m = orc.dropout(x, p, seed=1234, offset=0)
+    keep = np.float32(1.0) - np.float32(p)
+    scale = np.float32(1.0) / keep
+    kept = m != 0
+    sigma = np.sqrt(n * keep * (1 - keep))
+    assert abs(kept.sum() - n * keep) < 5 * sigma
+    assert np.all(m[kept] == scale)
+    np.testing.assert_array_equal(y, (x * m).astype(np.float32))
+    y2, m2 = orc.dropout(x[37:], p, seed=1234, offset=37)
+    np.testing.assert_array_equal(m2, m[37:])
+    _, m3 = orc.dropout(x, p, seed=1235, offset=0)
+    assert (m3 != m).mean() > 0.3  # another seed, another mask
