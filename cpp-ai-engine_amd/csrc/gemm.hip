@@ -61,11 +61,18 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
         g.c = ws;
     }
     const dim3 grid{unsigned(tiles), unsigned(splits), unsigned(batch)};
-    if (check) {
-        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, true>), grid,
+    const bool epi = splits == 1 && !plain_epilogue(g);
+    if (check && epi) {
+        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, true, true>), grid,
+                    dim3(C::kThreads), 0, s, g);
+    } else if (check) {
+        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, true, false>), grid,
+                    dim3(C::kThreads), 0, s, g);
+    } else if (epi) {
+        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, false, true>), grid,
                     dim3(C::kThreads), 0, s, g);
     } else {
-        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, false>), grid,
+        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, false, false>), grid,
                     dim3(C::kThreads), 0, s, g);
     }
     if (splits > 1) {
@@ -76,8 +83,8 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
         const int64_t total = batch * g.m * g.n;
         const int64_t per_block = 256 / rl;
         EHIP_LAUNCH("gemm_splitk_reduce", splitk_reduce,
-                    dim3(unsigned(ceil_div(total, per_block))), dim3(256), 0, s, g.c, out, g.m,
-                    g.n, g0.ldc, g0.stride_c, batch, splits, rl, g0.beta);
+                    dim3(unsigned(ceil_div(total, per_block))), dim3(256), 0, s, g.c, out, g0,
+                    batch, splits, rl);
     }
     return EHIP_OK;
 }
@@ -99,7 +106,8 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s) {
     // the checked ones still load whole float4s away from the edges when the
     // rows are aligned.
     const bool aligned = aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
-                         g.stride_a % 4 == 0 && g.stride_b % 4 == 0;
+                         g.stride_a % 4 == 0 && g.stride_b % 4 == 0 &&
+                         (g.inner == 1 || (g.stride_a2 % 4 == 0 && g.stride_b2 % 4 == 0));
     g.vec = aligned ? 1 : 0;
     const auto whole = [&](int bm, int bn, int bk) {
         return aligned && g.m % bm == 0 && g.n % bn == 0 && g.k % bk == 0;
@@ -130,7 +138,7 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s) {
 //   wave per output (few outputs, long K): lane l sums k = l, l + 64, ... and
 //     the lanes are combined by a fixed butterfly: deterministic, within the
 //     K-term tolerance.
-// Both apply beta as C = acc + beta C.
+// Both finish with the MFMA kernel's epilogue (alpha, addend, beta).
 
 // Measured on MI355X: the vector kernels win while the whole product is about
 // a million multiply-adds or less (cfg2's 64 x 784 x 10 layer: 4 + 6 + 4 us
@@ -149,8 +157,10 @@ __global__ __launch_bounds__(256) void gemm_small_thread(GemmArgs g, unsigned to
     for (unsigned o = blockIdx.x * 256u + threadIdx.x; o < total; o += step) {
         const unsigned t = o / n, j = o - t * n;
         const unsigned bi = t / m, i = t - bi * m;
-        const float* a = g.a + int64_t(bi) * g.stride_a + (TA ? int64_t(i) : int64_t(i) * g.lda);
-        const float* b = g.b + int64_t(bi) * g.stride_b + (TB ? int64_t(j) * g.ldb : int64_t(j));
+        const float* a = g.a + batch_offset(bi, g.inner, g.stride_a, g.stride_a2) +
+                         (TA ? int64_t(i) : int64_t(i) * g.lda);
+        const float* b = g.b + batch_offset(bi, g.inner, g.stride_b, g.stride_b2) +
+                         (TB ? int64_t(j) * g.ldb : int64_t(j));
         const int64_t ak = TA ? g.lda : 1, bk = TB ? 1 : g.ldb;
         float acc = 0.0f;
         int64_t k = 0;
@@ -172,9 +182,8 @@ __global__ __launch_bounds__(256) void gemm_small_thread(GemmArgs g, unsigned to
             const float s = acc + av * b[k * bk];
             acc = av != 0.0f ? s : acc;
         }
-        float* dst = g.c + int64_t(bi) * g.stride_c + int64_t(i) * g.ldc + j;
-        if (g.beta != 0.0f) acc = acc + g.beta * *dst;
-        *dst = acc;
+        float* dst = g.c + batch_offset(bi, g.inner, g.stride_c, g.stride_c2) + int64_t(i) * g.ldc + j;
+        *dst = epilogue(g, bi, i, j, acc, dst);
     }
 }
 
@@ -186,8 +195,10 @@ __global__ __launch_bounds__(256) void gemm_small_wave(GemmArgs g, unsigned tota
     const unsigned n = unsigned(g.n), m = unsigned(g.m);
     const unsigned t = o / n, j = o - t * n;
     const unsigned bi = t / m, i = t - bi * m;
-    const float* a = g.a + int64_t(bi) * g.stride_a + (TA ? int64_t(i) : int64_t(i) * g.lda);
-    const float* b = g.b + int64_t(bi) * g.stride_b + (TB ? int64_t(j) * g.ldb : int64_t(j));
+    const float* a = g.a + batch_offset(bi, g.inner, g.stride_a, g.stride_a2) +
+                     (TA ? int64_t(i) : int64_t(i) * g.lda);
+    const float* b = g.b + batch_offset(bi, g.inner, g.stride_b, g.stride_b2) +
+                     (TB ? int64_t(j) * g.ldb : int64_t(j));
     const int64_t ak = TA ? g.lda : 1, bk = TB ? 1 : g.ldb;
     float acc = 0.0f;
     int64_t k = lane;
@@ -205,9 +216,8 @@ __global__ __launch_bounds__(256) void gemm_small_wave(GemmArgs g, unsigned tota
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
     if (lane == 0) {
-        float* dst = g.c + int64_t(bi) * g.stride_c + int64_t(i) * g.ldc + j;
-        if (g.beta != 0.0f) acc = acc + g.beta * *dst;
-        *dst = acc;
+        float* dst = g.c + batch_offset(bi, g.inner, g.stride_c, g.stride_c2) + int64_t(i) * g.ldc + j;
+        *dst = epilogue(g, bi, i, j, acc, dst);
     }
 }
 
@@ -237,6 +247,69 @@ int small_kind(int64_t batch, int64_t m, int64_t n, int64_t k) {
     return 0;
 }
 
+// Validation shared by both entry points, then the kernel choice.
+int gemm_run(const ehip_gemm_ex_t& d, hipStream_t s) {
+    GemmArgs g{};
+    g.a = d.a;
+    g.b = d.b;
+    g.c = d.c;
+    g.m = d.m;
+    g.n = d.n;
+    g.k = d.k;
+    g.lda = d.lda;
+    g.ldb = d.ldb;
+    g.ldc = d.ldc;
+    g.stride_a = d.stride_a;
+    g.stride_b = d.stride_b;
+    g.stride_c = d.stride_c;
+    g.inner = d.inner;
+    g.stride_a2 = d.stride_a_inner;
+    g.stride_b2 = d.stride_b_inner;
+    g.stride_c2 = d.stride_c_inner;
+    g.alpha = d.alpha;
+    g.add = d.addend;
+    g.ld_add = d.ld_addend;
+    g.stride_add = d.stride_addend;
+    g.add_period = d.addend ? d.addend_period : 1;
+    g.beta = d.beta;
+    g.relu = d.relu;
+    const int64_t batch = d.batch;
+    const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
+    // K = 0 (only reached from the extended entry point): acc = 0, then the
+    // epilogue, through the thread-per-output kernel.
+    const int kind = d.k == 0 ? 1 : small_kind(batch, d.m, d.n, d.k);
+    if (kind != 0) {
+        const bool wave = kind == 2;
+        if (!ta && !tb) return gemm_small<false, false>(g, batch, wave, s);
+        if (!ta && tb) return gemm_small<false, true>(g, batch, wave, s);
+        if (ta && !tb) return gemm_small<true, false>(g, batch, wave, s);
+        return gemm_small<true, true>(g, batch, wave, s);
+    }
+    if (!ta && !tb) return gemm_modes<false, false>(g, batch, s);
+    if (!ta && tb) return gemm_modes<false, true>(g, batch, s);
+    if (ta && !tb) return gemm_modes<true, false>(g, batch, s);
+    return gemm_modes<true, true>(g, batch, s);
+}
+
+int check_desc(const ehip_gemm_ex_t& d) {
+    if (d.batch < 0 || d.m < 0 || d.n < 0 || d.k < 0) return fail(EHIP_EINVAL, "gemm: negative extent");
+    if (d.batch == 0 || d.m == 0 || d.n == 0) return EHIP_OK;
+    if (!d.c) return fail(EHIP_EINVAL, "gemm: null C");
+    if (d.k > 0 && (!d.a || !d.b)) return fail(EHIP_EINVAL, "gemm: null operand");
+    if (d.lda < (d.trans_a ? d.m : d.k) || d.ldb < (d.trans_b ? d.k : d.n) || d.ldc < d.n)
+        return fail(EHIP_EINVAL, "gemm: leading dimension too small");
+    if (d.stride_a < 0 || d.stride_b < 0 || d.stride_c < 0 || d.stride_a_inner < 0 ||
+        d.stride_b_inner < 0 || d.stride_c_inner < 0)
+        return fail(EHIP_EINVAL, "gemm: negative batch stride");
+    if (d.inner < 1) return fail(EHIP_EINVAL, "gemm: inner batch count %lld < 1", (long long)d.inner);
+    if (d.addend && (d.ld_addend < 0 || d.stride_addend < 0 || d.addend_period < 1))
+        return fail(EHIP_EINVAL, "gemm: bad addend geometry");
+    if (d.batch > 65535) return fail(EHIP_EINVAL, "gemm: batch %lld > 65535", (long long)d.batch);
+    if (d.m > (int64_t(1) << 31) || d.n > (int64_t(1) << 31))
+        return fail(EHIP_EINVAL, "gemm: extent beyond 2^31");
+    return EHIP_OK;
+}
+
 }  // namespace
 }  // namespace ehip
 
@@ -249,18 +322,27 @@ int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
                   int64_t stride_b, float beta, float* c, int64_t ldc, int64_t stride_c,
                   void* stream) {
     EHIP_READY();
-    if (batch < 0 || m < 0 || n < 0 || k < 0) return fail(EHIP_EINVAL, "gemm: negative extent");
+    ehip_gemm_ex_t d{};
+    d.trans_a = trans_a;
+    d.trans_b = trans_b;
+    d.batch = batch;
+    d.inner = 1;
+    d.m = m;
+    d.n = n;
+    d.k = k;
+    d.a = a;
+    d.lda = lda;
+    d.stride_a = stride_a;
+    d.b = b;
+    d.ldb = ldb;
+    d.stride_b = stride_b;
+    d.c = c;
+    d.ldc = ldc;
+    d.stride_c = stride_c;
+    d.alpha = 1.0f;
+    d.beta = beta;
+    if (int rc = check_desc(d)) return rc;
     if (batch == 0 || m == 0 || n == 0) return EHIP_OK;
-    if (!c) return fail(EHIP_EINVAL, "gemm: null C");
-    if (k > 0 && (!a || !b)) return fail(EHIP_EINVAL, "gemm: null operand");
-    if (lda < (trans_a ? m : k) || ldb < (trans_b ? k : n) || ldc < n)
-        return fail(EHIP_EINVAL, "gemm: leading dimension too small");
-    if (stride_a < 0 || stride_b < 0 || stride_c < 0)
-        return fail(EHIP_EINVAL, "gemm: negative batch stride");
-    if (batch > 65535) return fail(EHIP_EINVAL, "gemm: batch %lld > 65535", (long long)batch);
-    if (m > (int64_t(1) << 31) || n > (int64_t(1) << 31))
-        return fail(EHIP_EINVAL, "gemm: extent beyond 2^31");
-    hipStream_t s = as_stream(stream);
     if (k == 0) {  // C = beta C
         if (beta == 0.0f) {
             for (int64_t bi = 0; bi < batch; ++bi)
@@ -275,31 +357,18 @@ int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
         }
         return EHIP_OK;
     }
-    GemmArgs g{};
-    g.a = a;
-    g.b = b;
-    g.c = c;
-    g.m = m;
-    g.n = n;
-    g.k = k;
-    g.lda = lda;
-    g.ldb = ldb;
-    g.ldc = ldc;
-    g.stride_a = stride_a;
-    g.stride_b = stride_b;
-    g.stride_c = stride_c;
-    g.beta = beta;
-    if (const int kind = small_kind(batch, m, n, k)) {
-        const bool wave = kind == 2;
-        if (!trans_a && !trans_b) return gemm_small<false, false>(g, batch, wave, s);
-        if (!trans_a && trans_b) return gemm_small<false, true>(g, batch, wave, s);
-        if (trans_a && !trans_b) return gemm_small<true, false>(g, batch, wave, s);
-        return gemm_small<true, true>(g, batch, wave, s);
-    }
-    if (!trans_a && !trans_b) return gemm_modes<false, false>(g, batch, s);
-    if (!trans_a && trans_b) return gemm_modes<false, true>(g, batch, s);
-    if (trans_a && !trans_b) return gemm_modes<true, false>(g, batch, s);
-    return gemm_modes<true, true>(g, batch, s);
+    return gemm_run(d, as_stream(stream));
+}
+
+int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream) {
+    EHIP_READY();
+    if (!desc) return fail(EHIP_EINVAL, "gemm_ex: null descriptor");
+    const ehip_gemm_ex_t& d = *desc;
+    if (int rc = check_desc(d)) return rc;
+    if (d.batch == 0 || d.m == 0 || d.n == 0) return EHIP_OK;
+    if (d.k == 0 && d.batch * d.m * d.n > 0x7fffffffLL)
+        return fail(EHIP_EINVAL, "gemm_ex: K = 0 with more than 2^31 outputs");
+    return gemm_run(d, as_stream(stream));
 }
 
 }  // extern "C"

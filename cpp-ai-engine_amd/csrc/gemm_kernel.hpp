@@ -18,13 +18,54 @@ struct GemmArgs {
     float* c;  // the output, or the split-K workspace
     int64_t m, n, k;
     int64_t lda, ldb, ldc;
+    // Product z reads A at a + (z / inner) * stride_a + (z % inner) * stride_a2
+    // (likewise B and C): heads inside a (batch, seq, heads * dim) activation.
     int64_t stride_a, stride_b, stride_c;
+    int64_t inner;
+    int64_t stride_a2, stride_b2, stride_c2;
+    // Epilogue: v = acc; v *= alpha (alpha != 1); v += add[z % add_period]
+    // [i * ld_add + j] (add != null); v += beta * c (beta != 0); ReLU.
+    float alpha;
+    const float* add;
+    int64_t ld_add, stride_add, add_period;
     float beta;
+    int relu;  // then v = max(0, v)
     int tiles_m, tiles_n;
     int splits;        // K is cut into `splits` chunks of k_chunk (a multiple of BK)
     int64_t k_chunk;
     int vec;           // rows 16-byte aligned: checked loads may use float4 inside the edges
 };
+
+// The element offset of product z's matrix.
+__device__ __forceinline__ int64_t batch_offset(int64_t z, int64_t inner, int64_t stride,
+                                                int64_t stride2) {
+    if (inner == 1) return z * stride;
+    const int64_t outer = z / inner;
+    return outer * stride + (z - outer * inner) * stride2;
+}
+
+// The epilogue's arithmetic on one value: each step rounded on its own, so
+// that a fused scale, mask, bias or ReLU equals the separate nodes bit for bit.
+__device__ __forceinline__ float finish(const GemmArgs& g, float v, float add, float old) {
+    if (g.alpha != 1.0f) v = v * g.alpha;
+    if (g.add != nullptr) v = v + add;
+    if (g.beta != 0.0f) v = v + g.beta * old;
+    if (g.relu) v = (0.0f < v) ? v : 0.0f;
+    return v;
+}
+
+// The stored value of product z's output (row, col); dst is that element.
+__device__ __forceinline__ float epilogue(const GemmArgs& g, int64_t z, int64_t row, int64_t col,
+                                          float v, const float* dst) {
+    const float add =
+        g.add ? g.add[(z % g.add_period) * g.stride_add + row * g.ld_add + col] : 0.0f;
+    return finish(g, v, add, g.beta != 0.0f ? *dst : 0.0f);
+}
+
+// True when the stored value is the accumulator itself.
+__host__ __device__ inline bool plain_epilogue(const GemmArgs& g) {
+    return g.alpha == 1.0f && g.add == nullptr && g.beta == 0.0f && !g.relu;
+}
 
 template <int BM, int BN, int BK, int WM, int WN>
 struct Cfg {
@@ -105,7 +146,9 @@ __device__ __forceinline__ void store_tile(float* __restrict__ s, const float4* 
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool CHECK>
+// EPI: the fused epilogue (alpha, addend, beta, ReLU); without it the
+// accumulators are stored as they are (also the split-K partials).
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool CHECK, bool EPI>
 __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kernel(GemmArgs g) {
     using C = Cfg<BM, BN, BK, WM, WN>;
     __shared__ float lds_a[2][BK * C::kLdsA];
@@ -125,8 +168,8 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
 
     const int split = blockIdx.y;
     const int64_t batch = blockIdx.z;
-    const float* A = g.a + batch * g.stride_a;
-    const float* B = g.b + batch * g.stride_b;
+    const float* A = g.a + batch_offset(batch, g.inner, g.stride_a, g.stride_a2);
+    const float* B = g.b + batch_offset(batch, g.inner, g.stride_b, g.stride_b2);
     const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
     const int64_t k_begin = int64_t(split) * g.k_chunk;
     int64_t k_end = k_begin + g.k_chunk;
@@ -185,31 +228,57 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
     }
 
     // Epilogue. With splits > 1, c is the workspace [split][batch][m][n] and
-    // beta is applied by the reduction kernel.
+    // the epilogue is applied by the reduction kernel.
     float* Cp;
     int64_t ldc;
     if (g.splits > 1) {
         Cp = g.c + (int64_t(split) * gridDim.z + batch) * g.m * g.n;
         ldc = g.n;
     } else {
-        Cp = g.c + batch * g.stride_c;
+        Cp = g.c + batch_offset(batch, g.inner, g.stride_c, g.stride_c2);
         ldc = g.ldc;
     }
-    const bool use_beta = g.splits == 1 && g.beta != 0.0f;
+    if (!EPI) {
+#pragma unroll
+        for (int i = 0; i < C::kFM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::kFN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t row = m0 + wm0 + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                    const int64_t col = n0 + wn0 + 32 * j + lane % 32;
+                    if (CHECK && (row >= g.m || col >= g.n)) continue;
+                    Cp[row * ldc + col] = acc[i][j][r];
+                }
+        return;
+    }
+    // The fused epilogue, one 32 x 32 block at a time: the block's addend and
+    // old C values are loaded together first (the compiler cannot move a load
+    // above an earlier store to C, which may alias them), then stored.
+    const float* addp = g.add ? g.add + (int64_t(batch) % g.add_period) * g.stride_add : nullptr;
 #pragma unroll
     for (int i = 0; i < C::kFM; ++i)
 #pragma unroll
-        for (int j = 0; j < C::kFN; ++j)
+        for (int j = 0; j < C::kFN; ++j) {
+            const int64_t row0 = m0 + wm0 + 32 * i + 4 * (lane / 32);
+            const int64_t col = n0 + wn0 + 32 * j + lane % 32;
+            float* cb = Cp + row0 * ldc + col;
+            const float* ab = addp ? addp + row0 * g.ld_add + col : nullptr;
+            float e_add[16], e_old[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm0 + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-                const int64_t col = n0 + wn0 + 32 * j + lane % 32;
-                if (CHECK && (row >= g.m || col >= g.n)) continue;
-                float v = acc[i][j][r];
-                float* dst = Cp + row * ldc + col;
-                if (use_beta) v = v + g.beta * *dst;
-                *dst = v;
+                const int dr = 8 * (r / 4) + (r % 4);
+                const bool in = !CHECK || (row0 + dr < g.m && col < g.n);
+                e_add[r] = (ab && in) ? ab[dr * g.ld_add] : 0.0f;
+                e_old[r] = (g.beta != 0.0f && in) ? cb[dr * ldc] : 0.0f;
             }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dr = 8 * (r / 4) + (r % 4);
+                if (CHECK && (row0 + dr >= g.m || col >= g.n)) continue;
+                cb[dr * ldc] = finish(g, acc[i][j][r], e_add[r], e_old[r]);
+            }
+        }
 }
 
 // C[b] = sum over splits of W[s][b] (+ beta C[b]). A block is RL split lanes x
@@ -219,9 +288,9 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
 // block instead of one long serial chain per output; the order depends only
 // on the shape.
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w, float* c,
-                                                     int64_t m, int64_t n, int64_t ldc,
-                                                     int64_t stride_c, int64_t batch, int splits,
-                                                     int rl, float beta) {
+                                                     GemmArgs g, int64_t batch, int splits,
+                                                     int rl) {
+    const int64_t m = g.m, n = g.n;
     __shared__ float lanes[256];
     const int cw = 256 / rl;
     const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
@@ -250,9 +319,9 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
         float sum = lanes[cl];
         for (int l = 1; l < rl && l < splits; ++l) sum += lanes[l * cw + cl];
         const int64_t b = e / mn, rc = e % mn;
-        float* dst = c + b * stride_c + (rc / n) * ldc + rc % n;
-        if (beta != 0.0f) sum = sum + beta * *dst;
-        *dst = sum;
+        const int64_t row = rc / n, col = rc % n;
+        float* dst = c + batch_offset(b, g.inner, g.stride_c, g.stride_c2) + row * g.ldc + col;
+        *dst = epilogue(g, b, row, col, sum, dst);
     }
 }
 

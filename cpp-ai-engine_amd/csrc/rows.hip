@@ -179,10 +179,11 @@ __global__ __launch_bounds__(Group<T>::kBlock, Group<T>::kMinWaves) void softmax
     }
 }
 
+// dx may alias g: every element of a row is loaded before any is stored.
 template <int T, int V, bool VEC4, bool NT>
 __global__ __launch_bounds__(Group<T>::kBlock) void softmax_rows_backward(
-    const float* __restrict__ y, const float* __restrict__ g, float* __restrict__ dx, int64_t rows,
-    int64_t cols) {
+    const float* __restrict__ y, const float* g, float* dx, int64_t rows, int64_t cols,
+    float scale) {
     __shared__ float sh[Group<T>::kBlock / 64];
     for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
         Frag<T, V, VEC4, NT> fy, fg;
@@ -193,7 +194,7 @@ __global__ __launch_bounds__(Group<T>::kBlock) void softmax_rows_backward(
         for (int t = 0; t < V; ++t) dot += fg.v[t] * fy.v[t];
         dot = group_reduce<T, false>(dot, sh);
 #pragma unroll
-        for (int t = 0; t < V; ++t) fg.v[t] = fy.v[t] * (fg.v[t] - dot);
+        for (int t = 0; t < V; ++t) fg.v[t] = (fy.v[t] * (fg.v[t] - dot)) * scale;
         fg.store(dx + r * cols, int(cols), Group<T>::tid());
     }
 }
@@ -232,8 +233,8 @@ __global__ __launch_bounds__(kLoopThreads) void softmax_rows_loop(const float* _
 }
 
 __global__ __launch_bounds__(kLoopThreads) void softmax_rows_backward_loop(
-    const float* __restrict__ y, const float* __restrict__ g, float* __restrict__ dx, int64_t rows,
-    int64_t cols) {
+    const float* __restrict__ y, const float* g, float* dx, int64_t rows, int64_t cols,
+    float scale) {
     __shared__ float sh[kLoopThreads / 64];
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const float* yr = y + r * cols;
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(kLoopThreads) void softmax_rows_backward_loop(
         for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) dot += gr[c] * yr[c];
         dot = block_reduce_loop(dot, sh, false);
         for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads)
-            dx[r * cols + c] = yr[c] * (gr[c] - dot);
+            dx[r * cols + c] = (yr[c] * (gr[c] - dot)) * scale;
     }
 }
 
@@ -532,6 +533,7 @@ struct SoftmaxBackwardLaunch {
     const float* g;
     float* dx;
     int64_t rows, cols;
+    float scale;
     hipStream_t s;
     int* rc;
     template <int T, int V, bool VEC4, bool NT>
@@ -539,7 +541,7 @@ struct SoftmaxBackwardLaunch {
         constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
         *rc = [&] {
             EHIP_LAUNCH("softmax_backward", (softmax_rows_backward<T, V, VEC4, NT>),
-                        dim3(row_grid(rows, G)), dim3(B), 0, s, y, g, dx, rows, cols);
+                        dim3(row_grid(rows, G)), dim3(B), 0, s, y, g, dx, rows, cols, scale);
             return int(EHIP_OK);
         }();
         return true;
@@ -619,6 +621,11 @@ int ehip_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols, void*
 
 int ehip_softmax_backward_f32(const float* y, const float* g, float* dx, int64_t rows,
                               int64_t cols, void* stream) {
+    return ehip_softmax_backward_scaled_f32(y, g, dx, rows, cols, 1.0f, stream);
+}
+
+int ehip_softmax_backward_scaled_f32(const float* y, const float* g, float* dx, int64_t rows,
+                                     int64_t cols, float scale, void* stream) {
     EHIP_READY();
     if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "softmax_backward: bad shape");
     if (!y || !g || !dx) return fail(EHIP_EINVAL, "softmax_backward: null pointer");
@@ -626,10 +633,10 @@ int ehip_softmax_backward_f32(const float* y, const float* g, float* dx, int64_t
     hipStream_t s = as_stream(stream);
     int rc = EHIP_OK;
     if (dispatch_row(rows, cols, rows_vec_ok(cols, {y, g, dx}),
-                     SoftmaxBackwardLaunch{y, g, dx, rows, cols, s, &rc}))
+                     SoftmaxBackwardLaunch{y, g, dx, rows, cols, scale, s, &rc}))
         return rc;
     EHIP_LAUNCH("softmax_backward", softmax_rows_backward_loop, dim3(loop_grid(rows)),
-                dim3(kLoopThreads), 0, s, y, g, dx, rows, cols);
+                dim3(kLoopThreads), 0, s, y, g, dx, rows, cols, scale);
     return EHIP_OK;
 }
 

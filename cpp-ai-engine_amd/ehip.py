@@ -53,6 +53,19 @@ class TransferStats(C.Structure):
         ("to_device_seconds", C.c_double), ("to_host_seconds", C.c_double)]
 
 
+class GemmEx(C.Structure):
+    """ehip_gemm_ex_t: two-level batch strides and the alpha / addend / beta epilogue."""
+    _fields_ = [("trans_a", C.c_int), ("trans_b", C.c_int), ("batch", C.c_int64),
+                ("inner", C.c_int64), ("m", C.c_int64), ("n", C.c_int64), ("k", C.c_int64),
+                ("a", C.c_void_p), ("lda", C.c_int64), ("stride_a", C.c_int64),
+                ("stride_a_inner", C.c_int64), ("b", C.c_void_p), ("ldb", C.c_int64),
+                ("stride_b", C.c_int64), ("stride_b_inner", C.c_int64), ("c", C.c_void_p),
+                ("ldc", C.c_int64), ("stride_c", C.c_int64), ("stride_c_inner", C.c_int64),
+                ("alpha", C.c_float), ("addend", C.c_void_p), ("ld_addend", C.c_int64),
+                ("stride_addend", C.c_int64), ("addend_period", C.c_int64), ("beta", C.c_float),
+                ("relu", C.c_int)]
+
+
 # name -> argtypes (all return int unless listed in _RESTYPES)
 _SIGS = {
     "ehip_init": [], "ehip_available": [], "ehip_enabled": [], "ehip_set_enabled": [_i],
@@ -65,6 +78,7 @@ _SIGS = {
     "ehip_memcpy_d2d": [_vp, _vp, _sz, _vp],
     "ehip_gemm_f32": [_i, _i, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _f, _vp,
                       _i64, _i64, _vp],
+    "ehip_gemm_ex_f32": [C.POINTER(GemmEx), _vp],
     "ehip_binary_f32": [_i, _vp, _vp, _vp, _i64, _i64, _vp],
     "ehip_scalar_f32": [_vp, _vp, _i64, _f, _f, _vp],
     "ehip_relu_f32": [_vp, _vp, _i64, _vp],
@@ -100,6 +114,7 @@ _SIGS = {
     "ehip_reduce_sum_f32": [_vp, _i64, _i, _vp, _vp, _vp],
     "ehip_softmax_f32": [_vp, _vp, _i64, _i64, _vp],
     "ehip_softmax_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp],
+    "ehip_softmax_backward_scaled_f32": [_vp, _vp, _vp, _i64, _i64, _f, _vp],
     "ehip_layernorm_f32": [_vp] * 6 + [_i64, _i64, _f, _vp],
     "ehip_layernorm_backward_f32": [_vp] * 7 + [_i64, _i64, _vp],
     "ehip_cross_entropy_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
@@ -181,6 +196,10 @@ class Backend:
         return s
 
     # ---------------------------------------------------------- dense
+    def gemm_ex(self, desc):
+        """Runs an ehip_gemm_ex_t (a GemmEx whose pointers are device addresses)."""
+        self.ok(self.lib.ehip_gemm_ex_f32(C.byref(desc), self.stream()), "gemm_ex")
+
     def gemm(self, a, b, c=None, trans_a=False, trans_b=False, beta=0.0):
         """c = op(a) op(b) + beta c; a, b 2-D or 3-D (batched), 2-D operands shared."""
         ab, bb = a.dim() == 3, b.dim() == 3
@@ -423,12 +442,19 @@ class Backend:
                                           self.stream()), "softmax")
         return y
 
-    def softmax_backward(self, y, g):
+    def softmax_backward(self, y, g, scale=None, out=None):
+        """dx = y (g - sum(g y)), times `scale` when given (the scaled entry point);
+        `out` may be g itself."""
         cols = y.shape[-1]
-        dx = self.f32(y.shape)
-        self.ok(self.lib.ehip_softmax_backward_f32(self.p(y), self.p(g), self.p(dx),
-                                                   y.numel() // cols, cols, self.stream()),
-                "softmax_backward")
+        dx = self.f32(y.shape) if out is None else out
+        if scale is None:
+            rc = self.lib.ehip_softmax_backward_f32(self.p(y), self.p(g), self.p(dx),
+                                                    y.numel() // cols, cols, self.stream())
+        else:
+            rc = self.lib.ehip_softmax_backward_scaled_f32(self.p(y), self.p(g), self.p(dx),
+                                                           y.numel() // cols, cols, scale,
+                                                           self.stream())
+        self.ok(rc, "softmax_backward")
         return dx
 
     def layernorm(self, x, gamma, beta, eps=1e-5):

@@ -17,6 +17,14 @@
 namespace engine {
 namespace nn {
 
+// Fused graph nodes, on by default: Linear's product and bias add as one
+// node (the add in the GEMM epilogue), TransformerBlock's feed-forward as one
+// node, MultiHeadAttention's heads read and written in place. Switched off,
+// the modules build the reference's node-by-node graph instead; the values
+// are the same bit for bit either way. Process-wide; set it between steps.
+void set_fused_nodes(bool on);
+bool fused_nodes();
+
 class Module {
 public:
     virtual ~Module() = default;
@@ -47,6 +55,7 @@ public:
     std::string name() const override;
     Tensor& weight() { return weight_; }
     Tensor& bias() { return bias_; }
+    bool has_bias() const noexcept { return use_bias_; }
     size_t in_features() const noexcept { return in_features_; }
     size_t out_features() const noexcept { return out_features_; }
 

@@ -53,6 +53,17 @@ Tensor scaled_dot_product_attention(const Tensor& query, const Tensor& key, cons
                                     const Tensor* mask = nullptr,
                                     Tensor* attention_weights = nullptr);
 
+// The attention of MultiHeadAttention on projected activations, heads read
+// and written in place: query, key and value are (batch, seq, heads * dim)
+// and the result is the merged (batch, seq, heads * dim) tensor. Equal bit
+// for bit to splitting the heads, scaled_dot_product_attention and merging
+// them back, with one autograd node, no permuted copies and the scale and
+// mask applied inside the score product. `mask` must suffix-broadcast over
+// (batch, heads, seq, seq) and take no gradient (attention_heads_supported).
+bool attention_heads_supported(const Tensor& query, size_t heads, const Tensor* mask);
+Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& value, size_t heads,
+                       const Tensor* mask = nullptr, Tensor* attention_weights = nullptr);
+
 class MultiHeadAttention : public Module {
 public:
     MultiHeadAttention(size_t d_model, size_t num_heads);

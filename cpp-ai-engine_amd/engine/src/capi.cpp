@@ -420,6 +420,14 @@ int eng_block_fwd_bwd(const float* x, int64_t b, int64_t s, int64_t d, int64_t h
 
 // nn::Linear forward and backward with given weight (in, out) and bias (1, out);
 // x is (rows, in) or (b, s, in) flattened to rows.
+// nn::set_fused_nodes: 1 builds the fused nodes (the default), 0 the
+// reference's node-by-node graph. Returns the previous setting.
+int eng_set_fused_nodes(int on) {
+    const bool was = nn::fused_nodes();
+    nn::set_fused_nodes(on != 0);
+    return was ? 1 : 0;
+}
+
 int eng_linear_fwd_bwd(const float* x, int64_t rows, int64_t in, int64_t out, const float* w,
                        const float* bias, const float* dy, float* y, float* dx, float* dw,
                        float* db) {
@@ -437,16 +445,28 @@ int eng_linear_fwd_bwd(const float* x, int64_t rows, int64_t in, int64_t out, co
     });
 }
 
-// nn::MultiHeadAttention forward and backward without a mask; params in
-// parameters() order (wq, bq, wk, bk, wv, bv, wo, bo).
+// nn::MultiHeadAttention forward and backward; params in parameters() order
+// (wq, bq, wk, bk, wv, bv, wo, bo). mask (s, s) may be NULL; fuse selects the
+// in-place attention node or the composed path; weights (b, heads, s, s) may
+// be NULL.
 int eng_mha_fwd_bwd(const float* x, int64_t b, int64_t s, int64_t d, int64_t heads,
-                    const float* params, const float* dy, float* y, float* dx, float* dparams) {
+                    const float* params, const float* dy, float* y, float* dx, float* dparams,
+                    const float* mask, int fuse, float* weights) {
     return guarded([&] {
+        struct Restore {
+            bool was = nn::fused_nodes();
+            ~Restore() { nn::set_fused_nodes(was); }
+        } restore;
+        nn::set_fused_nodes(fuse != 0);
         nn::MultiHeadAttention mha{size_t(d), size_t(heads)};
+        mha.keep_attention(weights != nullptr);
         load_params(mha.parameters(), params);
         Tensor X = make({size_t(b), size_t(s), size_t(d)}, x, true);
-        Tensor Y = mha.forward(X, nullptr);
+        Tensor M;
+        if (mask != nullptr) M = make({size_t(s), size_t(s)}, mask, false);
+        Tensor Y = mha.forward(X, mask ? &M : nullptr);
         Y.backward(make(Y.shape(), dy, false));
+        if (weights != nullptr) put(mha.last_attention(), weights);
         put(Y, y);
         put(X.grad(), dx);
         size_t off = 0;

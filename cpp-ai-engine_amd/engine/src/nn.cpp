@@ -3,6 +3,7 @@
 #include "engine/nn.hpp"
 #include "engine/conv.hpp"
 
+#include <atomic>
 #include <cmath>
 #include <stdexcept>
 
@@ -10,6 +11,14 @@
 
 namespace engine {
 namespace nn {
+
+namespace {
+std::atomic<bool> g_fused_nodes{true};
+}  // namespace
+
+void set_fused_nodes(bool on) { g_fused_nodes.store(on); }
+bool fused_nodes() { return g_fused_nodes.load(); }
+
 
 using namespace detail;
 
@@ -51,8 +60,13 @@ Tensor Linear::forward(const Tensor& input) {
                                     " received an input " + input.shape_str() + ".");
     const bool needs_reshape = input.ndim() > 2;
     Tensor flat = needs_reshape ? input.reshape({input.size() / in_features_, in_features_}) : input;
-    Tensor out = flat.matmul(weight_);
-    if (use_bias_) out = out + bias_;
+    Tensor out;
+    if (fused_nodes()) {
+        out = ops::linear(flat, weight_, use_bias_ ? &bias_ : nullptr);
+    } else {
+        out = flat.matmul(weight_);
+        if (use_bias_) out = out + bias_;
+    }
     if (needs_reshape) {
         std::vector<size_t> out_shape = input.shape();
         out_shape.back() = out_features_;

@@ -279,6 +279,143 @@ Tensor matmul_nt(const Tensor& A, const Tensor& B) {
     return C;
 }
 
+namespace {
+
+// out (m, n) = op(a) op(b) over plain 2-D operands, then + bias (a row) and ReLU.
+void gemm_2d(bool ta, bool tb, size_t m, size_t n, size_t k, const float* a, const float* b,
+             float* c, const float* bias, bool relu, const char* what) {
+    ehip_gemm_ex_t d{};
+    d.trans_a = ta ? 1 : 0;
+    d.trans_b = tb ? 1 : 0;
+    d.batch = 1;
+    d.inner = 1;
+    d.m = int64_t(m);
+    d.n = int64_t(n);
+    d.k = int64_t(k);
+    d.a = a;
+    d.lda = int64_t(ta ? m : k);
+    d.b = b;
+    d.ldb = int64_t(tb ? k : n);
+    d.c = c;
+    d.ldc = int64_t(n);
+    d.alpha = 1.0f;
+    d.addend = bias;
+    d.addend_period = 1;  // ld_addend 0: one row over every row
+    d.relu = relu ? 1 : 0;
+    hip::check(ehip_gemm_ex_f32(&d, nullptr), what);
+}
+
+bool row_bias(const Tensor* bias, size_t n) {
+    if (bias == nullptr) return true;
+    return bias->size() == n && (bias->ndim() == 1 || (bias->ndim() == 2 && bias->shape()[0] == 1));
+}
+
+Tensor empty_2d(size_t rows, size_t cols) { return Tensor({rows, cols}, 0.0f, false); }
+
+}  // namespace
+
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias) {
+    if (x.ndim() != 2 || w.ndim() != 2 || x.shape()[1] != w.shape()[0] ||
+        !row_bias(bias, w.shape()[1])) {
+        Tensor out = x.matmul(w);
+        return bias ? out + *bias : out;
+    }
+    const size_t M = x.shape()[0], K = x.shape()[1], N = w.shape()[1];
+    Tensor out = empty_2d(M, N);
+    if (M > 0 && N > 0)
+        gemm_2d(false, false, M, N, K, dptr(x), dptr(w), dout(out), bias ? dptr(*bias) : nullptr,
+                false, "linear");
+    const bool bias_grad = bias != nullptr && bias->requires_grad();
+    if (!track(x.requires_grad() || w.requires_grad() || bias_grad)) return out;
+    Tensor xc = x, wc = w, bc = bias ? *bias : Tensor();
+    std::vector<std::shared_ptr<TensorImpl>> parents = {x.get_impl(), w.get_impl()};
+    if (bias) parents.push_back(bias->get_impl());
+    attach(out, std::move(parents), [xc, wc, bc, M, N, K](const Tensor& g) mutable {
+        // The composed graph's order: the bias add's node, then the product's.
+        if (bc.get_impl() && bc.requires_grad()) bc.add_grad(reduce_to(g, bc));
+        if (xc.requires_grad()) {  // g w^T
+            Tensor dx = empty_2d(M, K);
+            if (M > 0 && K > 0) gemm_2d(false, true, M, K, N, dptr(g), dptr(wc), dout(dx), nullptr,
+                                        false, "linear dx");
+            xc.add_grad(dx);
+        }
+        if (wc.requires_grad()) {  // x^T g
+            Tensor dw = empty_2d(K, N);
+            if (K > 0 && N > 0) gemm_2d(true, false, K, N, M, dptr(xc), dptr(g), dout(dw), nullptr,
+                                        false, "linear dw");
+            wc.add_grad(dw);
+        }
+    });
+    return out;
+}
+
+Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2,
+                         const Tensor& b2) {
+    const bool plain = x.ndim() == 2 && w1.ndim() == 2 && w2.ndim() == 2 &&
+                       x.shape()[1] == w1.shape()[0] && w1.shape()[1] == w2.shape()[0] &&
+                       row_bias(&b1, w1.shape()[1]) && row_bias(&b2, w2.shape()[1]);
+    if (!plain) return linear(linear(x, w1, &b1).relu(), w2, &b2);
+    const size_t M = x.shape()[0], D = x.shape()[1], F = w1.shape()[1], N = w2.shape()[1];
+    Tensor h = empty_2d(M, F);  // relu(x w1 + b1)
+    if (M > 0 && F > 0)
+        gemm_2d(false, false, M, F, D, dptr(x), dptr(w1), dout(h), dptr(b1), true,
+                "feed-forward 1");
+    Tensor out = empty_2d(M, N);
+    if (M > 0 && N > 0)
+        gemm_2d(false, false, M, N, F, dptr(h), dptr(w2), dout(out), dptr(b2), false,
+                "feed-forward 2");
+    if (!track(x.requires_grad() || w1.requires_grad() || b1.requires_grad() ||
+               w2.requires_grad() || b2.requires_grad()))
+        return out;
+    Tensor xc = x, w1c = w1, b1c = b1, w2c = w2, b2c = b2;
+    attach(out, {x.get_impl(), w1.get_impl(), b1.get_impl(), w2.get_impl(), b2.get_impl()},
+           [xc, w1c, b1c, w2c, b2c, h, M, D, F, N](const Tensor& g) mutable {
+               // The composed graph's order: second bias, second product (h,
+               // then w2), ReLU, first bias, first product (x, then w1).
+               if (b2c.requires_grad()) b2c.add_grad(reduce_to(g, b2c));
+               const bool need_dh = xc.requires_grad() || w1c.requires_grad() || b1c.requires_grad();
+               Tensor dh;
+               if (need_dh) {  // g w2^T
+                   dh = empty_2d(M, F);
+                   if (M > 0 && F > 0)
+                       gemm_2d(false, true, M, F, N, dptr(g), dptr(w2c), dout(dh), nullptr, false,
+                               "feed-forward dh");
+               }
+               if (w2c.requires_grad()) {  // h^T g
+                   Tensor dw2 = empty_2d(F, N);
+                   if (F > 0 && N > 0)
+                       gemm_2d(true, false, F, N, M, dptr(h), dptr(g), dout(dw2), nullptr, false,
+                               "feed-forward dw2");
+                   w2c.add_grad(dw2);
+               }
+               if (!need_dh) return;
+               // ReLU's backward from its output: h > 0 exactly where the
+               // pre-activation was positive.
+               Tensor dpre = empty_2d(M, F);
+               if (M > 0 && F > 0)
+                   hip::check(ehip_relu_backward_f32(dptr(h), dptr(dh), dout(dpre),
+                                                     int64_t(M * F), nullptr),
+                              "feed-forward relu backward");
+               dh = Tensor();
+               if (b1c.requires_grad()) b1c.add_grad(reduce_to(dpre, b1c));
+               if (xc.requires_grad()) {  // dpre w1^T
+                   Tensor dx = empty_2d(M, D);
+                   if (M > 0 && D > 0)
+                       gemm_2d(false, true, M, D, F, dptr(dpre), dptr(w1c), dout(dx), nullptr,
+                               false, "feed-forward dx");
+                   xc.add_grad(dx);
+               }
+               if (w1c.requires_grad()) {  // x^T dpre
+                   Tensor dw1 = empty_2d(D, F);
+                   if (D > 0 && F > 0)
+                       gemm_2d(true, false, D, F, M, dptr(xc), dptr(dpre), dout(dw1), nullptr,
+                               false, "feed-forward dw1");
+                   w1c.add_grad(dw1);
+               }
+           });
+    return out;
+}
+
 // C = A^T B: A (.., k, m), B (.., k, n).
 Tensor matmul_tn(const Tensor& A, const Tensor& B) {
     const Batch bt = batch_of(A, B);

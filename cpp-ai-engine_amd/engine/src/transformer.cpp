@@ -141,6 +141,169 @@ Tensor scaled_dot_product_attention(const Tensor& query, const Tensor& key, cons
     return weights.matmul(value);
 }
 
+namespace {
+
+// The addend geometry of a mask suffix-broadcast over (batch, heads, S, S):
+// its core (leading 1s stripped) is (), (S), (S, S), (heads, S, S) or
+// (batch, heads, S, S). False when it is none of these.
+struct MaskPlan {
+    int64_t ld = 0, stride = 0, period = 1;
+};
+
+bool mask_plan(const Tensor& mask, size_t batch, size_t heads, size_t seq, MaskPlan& plan) {
+    const std::vector<size_t> full = {batch, heads, seq, seq};
+    if (!plan_broadcast(full, mask.shape()).valid) return false;
+    size_t first = 0;
+    while (first < mask.ndim() && mask.shape()[first] == 1) ++first;
+    const size_t core = mask.ndim() - first;
+    plan = MaskPlan{};
+    if (core >= 2) {
+        plan.ld = int64_t(seq);
+        plan.stride = int64_t(seq * seq);
+    }
+    if (core == 3) plan.period = int64_t(heads);
+    if (core == 4) plan.period = int64_t(batch * heads);
+    return true;
+}
+
+// The descriptor of a product over the (sample, head) pairs of heads-major
+// operands: z = sample * heads + head.
+struct HeadOperand {
+    const float* p;
+    int64_t ld, stride, stride_inner;
+};
+
+ehip_gemm_ex_t head_product(bool ta, bool tb, size_t batch, size_t heads, size_t m, size_t n,
+                            size_t k, HeadOperand a, HeadOperand b, float* c, int64_t ldc,
+                            int64_t stride_c, int64_t stride_c_inner) {
+    ehip_gemm_ex_t d{};
+    d.trans_a = ta ? 1 : 0;
+    d.trans_b = tb ? 1 : 0;
+    d.batch = int64_t(batch * heads);
+    d.inner = int64_t(heads);
+    d.m = int64_t(m);
+    d.n = int64_t(n);
+    d.k = int64_t(k);
+    d.a = a.p;
+    d.lda = a.ld;
+    d.stride_a = a.stride;
+    d.stride_a_inner = a.stride_inner;
+    d.b = b.p;
+    d.ldb = b.ld;
+    d.stride_b = b.stride;
+    d.stride_b_inner = b.stride_inner;
+    d.c = c;
+    d.ldc = ldc;
+    d.stride_c = stride_c;
+    d.stride_c_inner = stride_c_inner;
+    d.alpha = 1.0f;
+    d.addend_period = 1;
+    return d;
+}
+
+}  // namespace
+
+bool attention_heads_supported(const Tensor& query, size_t heads, const Tensor* mask) {
+    if (query.ndim() != 3 || heads == 0 || query.shape()[2] % heads != 0) return false;
+    if (mask == nullptr) return true;
+    if (track(mask->requires_grad())) return false;
+    MaskPlan plan;
+    return mask_plan(*mask, query.shape()[0], heads, query.shape()[1], plan);
+}
+
+// One node for softmax(Q K^T / sqrt(d) + mask) V over every head
+// (src/transformer.cpp:279-304 under the head split and merge of
+// src/transformer.cpp:320-349). Forward: the score product with the scale and
+// mask in its epilogue, the row softmax, the product with V written straight
+// into the merged layout. Backward: dW = g V^T, dV = W^T g, the softmax
+// derivative with the scale's backward folded in (in place over dW), then
+// dQ = dS K and dK = dS^T Q -- the composed path's products, operand for
+// operand, with each head addressed in place.
+Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& value, size_t heads,
+                       const Tensor* mask, Tensor* attention_weights) {
+    if (!attention_heads_supported(query, heads, mask))
+        throw std::invalid_argument("attention_heads: query " + query.shape_str() + " with " +
+                                    std::to_string(heads) + " heads" +
+                                    (mask ? " and mask " + mask->shape_str() : std::string()) +
+                                    " is not supported.");
+    if (key.shape() != query.shape() || value.shape() != query.shape())
+        throw std::invalid_argument("attention_heads: query, key and value differ: " +
+                                    query.shape_str() + ", " + key.shape_str() + ", " +
+                                    value.shape_str() + ".");
+    const size_t B = query.shape()[0], S = query.shape()[1], D = query.shape()[2];
+    const size_t H = heads, hd = D / heads;
+    const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+    const int64_t sd = int64_t(S * D), ss = int64_t(S * S), hss = int64_t(H * S * S);
+    const auto act = [&](const Tensor& t) { return HeadOperand{dptr(t), int64_t(D), sd, int64_t(hd)}; };
+
+    Tensor scores({B, H, S, S}, 0.0f, false);
+    ehip_gemm_ex_t d = head_product(false, true, B, H, S, S, hd, act(query), act(key),
+                                    dout(scores), int64_t(S), hss, ss);
+    d.alpha = scale;
+    if (mask != nullptr) {
+        MaskPlan plan;
+        mask_plan(*mask, B, H, S, plan);
+        d.addend = dptr(*mask);
+        d.ld_addend = plan.ld;
+        d.stride_addend = plan.stride;
+        d.addend_period = plan.period;
+    }
+    hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention scores");
+    Tensor weights({B, H, S, S}, 0.0f, false);
+    hip::check(ehip_softmax_f32(dptr(scores), dout(weights), int64_t(B * H * S), int64_t(S), nullptr),
+               "attention softmax");
+    scores = Tensor();
+    if (attention_weights != nullptr) *attention_weights = weights.detach();
+
+    Tensor out({B, S, D}, 0.0f, false);
+    d = head_product(false, false, B, H, S, hd, S, HeadOperand{dptr(weights), int64_t(S), hss, ss},
+                     act(value), dout(out), int64_t(D), sd, int64_t(hd));
+    hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention output");
+
+    if (!track(query.requires_grad() || key.requires_grad() || value.requires_grad())) return out;
+    out.set_requires_grad(true);
+    out.get_impl()->parents = {query.get_impl(), key.get_impl(), value.get_impl()};
+    Tensor q = query, k = key, v = value;
+    out.get_impl()->backward_fn = [q, k, v, weights, B, S, D, H, hd, scale, sd, ss,
+                                   hss](const Tensor& g) mutable {
+        const auto head = [&](const Tensor& t) {
+            return HeadOperand{dptr(t), int64_t(D), sd, int64_t(hd)};
+        };
+        const HeadOperand w{dptr(weights), int64_t(S), hss, ss};
+        if (v.requires_grad()) {  // dV = W^T g
+            Tensor dv({B, S, D}, 0.0f, false);
+            ehip_gemm_ex_t d = head_product(true, false, B, H, S, hd, S, w, head(g), dout(dv),
+                                            int64_t(D), sd, int64_t(hd));
+            hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dV");
+            v.add_grad(dv);
+        }
+        if (!q.requires_grad() && !k.requires_grad()) return;
+        Tensor ds({B, H, S, S}, 0.0f, false);  // dW, then dS in place
+        ehip_gemm_ex_t d = head_product(false, true, B, H, S, S, hd, head(g), head(v), dout(ds),
+                                        int64_t(S), hss, ss);
+        hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dW");
+        hip::check(ehip_softmax_backward_scaled_f32(dptr(weights), dptr(ds), dout(ds),
+                                                    int64_t(B * H * S), int64_t(S), scale, nullptr),
+                   "attention softmax backward");
+        const HeadOperand dsh{dptr(ds), int64_t(S), hss, ss};
+        if (q.requires_grad()) {  // dQ = dS K
+            Tensor dq({B, S, D}, 0.0f, false);
+            d = head_product(false, false, B, H, S, hd, S, dsh, head(k), dout(dq), int64_t(D), sd,
+                             int64_t(hd));
+            hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dQ");
+            q.add_grad(dq);
+        }
+        if (k.requires_grad()) {  // dK = dS^T Q
+            Tensor dk({B, S, D}, 0.0f, false);
+            d = head_product(true, false, B, H, S, hd, S, dsh, head(q), dout(dk), int64_t(D), sd,
+                             int64_t(hd));
+            hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dK");
+            k.add_grad(dk);
+        }
+    };
+    return out;
+}
+
 MultiHeadAttention::MultiHeadAttention(size_t d_model, size_t num_heads)
     : d_model_(d_model),
       num_heads_(num_heads),
@@ -163,6 +326,12 @@ Tensor MultiHeadAttention::forward(const Tensor& input, const Tensor* mask) {
         throw std::invalid_argument("MultiHeadAttention expects (batch, seq, " +
                                     std::to_string(d_model_) + "), received " + input.shape_str() + ".");
     const size_t batch = input.shape()[0], seq = input.shape()[1];
+    if (fused_nodes() && attention_heads_supported(input, num_heads_, mask)) {
+        Tensor attended = attention_heads(w_query_(input), w_key_(input), w_value_(input),
+                                          num_heads_, mask,
+                                          keep_attention_ ? &last_attention_ : nullptr);
+        return w_out_(attended);
+    }
     auto split_heads = [&](const Tensor& projected) {
         return projected.reshape({batch, seq, num_heads_, head_dim_}).permute({0, 2, 1, 3});
     };
@@ -214,7 +383,17 @@ Tensor TransformerBlock::forward(const Tensor& input) { return forward(input, nu
 // Pre-LN: h = x + MHA(LN1(x)); out = h + FF2(ReLU(FF1(LN2(h)))) (src/transformer.cpp:409-414).
 Tensor TransformerBlock::forward(const Tensor& input, const Tensor* mask) {
     Tensor h = input + attention_.forward(norm1_(input), mask);
-    return h + ff2_(ff1_(norm2_(h)).relu());
+    Tensor n2 = norm2_(h);
+    if (fused_nodes() && ff1_.has_bias() && ff2_.has_bias()) {
+        const std::vector<size_t> shape = n2.shape();
+        const size_t rows = n2.size() / shape.back();
+        Tensor ff = ops::feed_forward_relu(n2.reshape({rows, shape.back()}), ff1_.weight(),
+                                           ff1_.bias(), ff2_.weight(), ff2_.bias());
+        std::vector<size_t> out_shape = shape;
+        out_shape.back() = ff.shape().back();
+        return h + ff.reshape(out_shape);
+    }
+    return h + ff2_(ff1_(n2).relu());
 }
 
 std::vector<Tensor> TransformerBlock::parameters() {

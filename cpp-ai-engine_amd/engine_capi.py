@@ -279,13 +279,20 @@ class Engine:
                                              _fp(db)))
         return y, dx, dw, db
 
-    def mha_fwd_bwd(self, x, heads, params, dy):
+    def mha_fwd_bwd(self, x, heads, params, dy, mask=None, fuse=True, weights=False):
+        """MultiHeadAttention forward + backward; mask (seq, seq) or None. fuse
+        picks the in-place attention node or the composed split/attend/merge
+        path. weights=True also returns the (b, heads, s, s) attention."""
         x, params, dy = _f32(x), _f32(params), _f32(dy)
         b, s, d = x.shape
         y, dx, dp = np.empty_like(x), np.empty_like(x), np.empty_like(params)
+        mp = None if mask is None else _f32(mask)
+        w = np.empty((b, heads, s, s), np.float32) if weights else None
         self._ok(self.lib.eng_mha_fwd_bwd(_fp(x), _i64(b), _i64(s), _i64(d), _i64(heads),
-                                          _fp(params), _fp(dy), _fp(y), _fp(dx), _fp(dp)))
-        return y, dx, dp
+                                          _fp(params), _fp(dy), _fp(y), _fp(dx), _fp(dp),
+                                          None if mp is None else _fp(mp), int(fuse),
+                                          None if w is None else _fp(w)))
+        return (y, dx, dp, w) if weights else (y, dx, dp)
 
     def mse_adam(self, w0, target, steps, lr):
         w0, target = _f32(w0).ravel().copy(), _f32(target).ravel().copy()
@@ -293,6 +300,11 @@ class Engine:
         self.lib.eng_mse_adam.argtypes = [_f32p, _f32p, _i64, _i64, C.c_float, _f32p]
         self._ok(self.lib.eng_mse_adam(_fp(w0), _fp(target), w0.size, steps, lr, _fp(traj)))
         return traj
+
+    def set_fused_nodes(self, on):
+        """Fused graph nodes on (default) or the reference's node-by-node graph;
+        returns the previous setting."""
+        return bool(self.lib.eng_set_fused_nodes(int(bool(on))))
 
     def block_num_params(self, d, heads, ff):
         return self.lib.eng_block_num_params(_i64(d), _i64(heads), _i64(ff))

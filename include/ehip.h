@@ -153,6 +153,43 @@ int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
                   int64_t stride_b, float beta, float* c, int64_t ldc, int64_t stride_c,
                   void* stream);
 
+/* ehip_gemm_f32 with two-level batch strides and an epilogue, for products
+ * that read and write attention heads in place. Product z in [0, batch) uses
+ *   A at a + (z / inner) * stride_a + (z % inner) * stride_a_inner
+ * (likewise B and C), so that z = (sample, head) walks the heads of a
+ * (batch, seq, heads * head_dim) activation with ld = heads * head_dim and no
+ * permuted copy (the reshape + permute({0, 2, 1, 3}) of
+ * src/transformer.cpp:320-349). The result is stored as
+ *   c = acc;  c = c * alpha (alpha != 1);  c = c + addend[z % addend_period]
+ *   [i * ld_addend + j] (addend != NULL);  c = c + beta * c_old (beta != 0),
+ * each step rounded to fp32 on its own -- the separate `scores * scale` and
+ * `scores + mask` nodes of src/transformer.cpp:285-291, bit for bit; an
+ * addend with ld_addend 0 is Linear's broadcast bias add (src/nn.cpp:119-122).
+ * Then, when relu != 0, c = (0 < c) ? c : 0, std::max(0.0f, c) of
+ * Tensor::relu (src/tensor_ops.cpp:591-600).
+ * addend_period >= 1; consecutive addend matrices are stride_addend apart
+ * (stride_addend 0 broadcasts one mask over every product, ld_addend 0 one
+ * row over every row). inner >= 1. With k == 0, acc is 0 and the epilogue
+ * still runs. */
+typedef struct {
+    int trans_a, trans_b;
+    int64_t batch, inner;
+    int64_t m, n, k;
+    const float* a;
+    int64_t lda, stride_a, stride_a_inner;
+    const float* b;
+    int64_t ldb, stride_b, stride_b_inner;
+    float* c;
+    int64_t ldc, stride_c, stride_c_inner;
+    float alpha;
+    const float* addend;
+    int64_t ld_addend, stride_addend, addend_period;
+    float beta;
+    int relu;
+} ehip_gemm_ex_t;
+
+int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream);
+
 /* --------------------------------------------------------- element-wise */
 
 enum { EHIP_ADD = 0, EHIP_SUB = 1, EHIP_MUL = 2, EHIP_DIV = 3 };
@@ -385,6 +422,13 @@ int ehip_reduce_sum_f32(const float* x, int64_t n, int squares, double* out_d, f
 int ehip_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
 int ehip_softmax_backward_f32(const float* y, const float* g, float* dx, int64_t rows,
                               int64_t cols, void* stream);
+
+/* dx = (y (g - sum(g y))) * scale, the product rounded before the scale: the
+ * softmax derivative followed by the backward of a `scores * scale` node
+ * (src/transformer.cpp:285-289 under src/tensor_ops.cpp's scalar multiply),
+ * in one pass. dx may alias g (each element is read before it is written). */
+int ehip_softmax_backward_scaled_f32(const float* y, const float* g, float* dx, int64_t rows,
+                                     int64_t cols, float scale, void* stream);
 
 /* LayerNorm over the last axis (two-pass mean and variance, eps inside the
  * square root) saving xhat and inv_std, and its derivative; dgamma and dbeta

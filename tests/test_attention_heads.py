@@ -1,0 +1,331 @@
+"""The in-place attention path: ehip_gemm_ex_f32 (two-level head strides, the
+scale / mask / beta epilogue), ehip_softmax_backward_scaled_f32, and the engine's
+attention_heads node.
+
+Each fused product is checked bit for bit against the composition it replaces --
+the heads copied out with a plain permute, the same ehip_gemm_f32 product, then
+the scale and the mask as separate IEEE element-wise steps (torch fp32 on the
+device) -- and against an fp64 product within the K-term tolerance. The engine
+node is checked bit for bit against MultiHeadAttention's composed path (split,
+scaled_dot_product_attention, merge: src/transformer.cpp:279-349) and against
+the oracle composition at the reference's parity metric.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import _compose as K
+from _hip import backend, dev, exact, host, k_tol, print_case, ref_close
+from _oracle import oracle_or_skip
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hip():
+    return backend()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return oracle_or_skip()
+
+
+@pytest.fixture(scope="module")
+def eng():
+    from engine_capi import Engine
+    return Engine()
+
+
+def randn(r, *shape):
+    return r.standard_normal(shape, dtype=np.float32)
+
+
+def heads_of(t, b, s, h, hd):
+    """(b, s, h*hd) device tensor -> (b*h, s, hd) contiguous copy (a plain move)."""
+    return t.reshape(b, s, h, hd).permute(0, 2, 1, 3).contiguous().reshape(b * h, s, hd)
+
+
+def merged_of(t, b, s, h, hd):
+    """(b*h, s, hd) -> (b, s, h*hd) contiguous copy."""
+    return t.reshape(b, h, s, hd).permute(0, 2, 1, 3).contiguous().reshape(b, s, h * hd)
+
+
+def desc(hip, ta, tb, batch, inner, m, n, k, a, lda, sa, sa2, b, ldb, sb, sb2, c, ldc, sc, sc2,
+         alpha=1.0, addend=None, ld_add=0, stride_add=0, period=1, beta=0.0, relu=False):
+    from ehip import GemmEx
+    return GemmEx(int(ta), int(tb), batch, inner, m, n, k, hip.p(a), lda, sa, sa2, hip.p(b), ldb,
+                  sb, sb2, hip.p(c), ldc, sc, sc2, alpha,
+                  None if addend is None else hip.p(addend), ld_add, stride_add, period, beta,
+                  int(relu))
+
+
+# (batch, seq, heads, head_dim): the char model's heads (cfg3), a head_dim that
+# is not a multiple of 4 (checked loads), tiles that the small kernels take,
+# and the 512-token heads of the scaled model.
+SHAPES = [(2, 64, 4, 24), (2, 37, 3, 6), (2, 16, 2, 8), (1, 512, 4, 64), (3, 130, 2, 32)]
+MASKS = ["none", "causal", "per_head", "per_product", "row"]
+
+
+def mask_for(kind, r, b, s, h):
+    """(mask array or None, ld, stride, period) for the suffix-broadcast kinds."""
+    if kind == "none":
+        return None, 0, 0, 1
+    if kind == "causal":
+        m = np.triu(np.full((s, s), -1e9, np.float32), 1)
+        return m, s, 0, 1
+    if kind == "per_head":
+        return randn(r, h, s, s), s, s * s, h
+    if kind == "per_product":
+        return randn(r, b, h, s, s), s, s * s, b * h
+    return randn(r, s), 0, 0, 1  # one row repeated over every row
+
+
+@pytest.mark.parametrize("b,s,h,hd", SHAPES)
+@pytest.mark.parametrize("kind", MASKS)
+def test_scores_epilogue_bitexact(hip, b, s, h, hd, kind):
+    import torch
+    print_case("gemm_ex scores", b, s, h, hd, kind)
+    r = np.random.default_rng(b * 1000 + s * 10 + h + hd + MASKS.index(kind))
+    d = h * hd
+    q, k = dev(randn(r, b, s, d)), dev(randn(r, b, s, d))
+    mask, ld, st, period = mask_for(kind, r, b, s, h)
+    mk = None if mask is None else dev(mask)
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(hd)))
+    c = hip.f32((b, h, s, s))
+    hip.gemm_ex(desc(hip, False, True, b * h, h, s, s, hd, q, d, s * d, hd, k, d, s * d, hd, c, s,
+                     h * s * s, s * s, alpha=scale, addend=mk, ld_add=ld, stride_add=st,
+                     period=period))
+    raw = hip.gemm(heads_of(q, b, s, h, hd), heads_of(k, b, s, h, hd), trans_b=True)
+    want = raw.reshape(b, h, s, s) * torch.tensor(scale, dtype=torch.float32, device="cuda")
+    if mk is not None:
+        want = want + mk
+    exact(host(c), host(want), f"scores {kind}")
+    # The product itself against fp64.
+    qh = host(q).reshape(b, s, h, hd).transpose(0, 2, 1, 3).astype(np.float64)
+    kh = host(k).reshape(b, s, h, hd).transpose(0, 2, 1, 3).astype(np.float64)
+    exp = (qh @ kh.transpose(0, 1, 3, 2)) * scale
+    if mask is not None:
+        exp = exp + mask
+    ref_close(host(c), exp, k_tol(hd) * 4, "scores vs fp64")
+
+
+@pytest.mark.parametrize("b,s,h,hd", SHAPES)
+def test_head_products_bitexact(hip, b, s, h, hd):
+    """The four other products of the node, each writing or reading heads in place."""
+    print_case("gemm_ex head products", b, s, h, hd)
+    r = np.random.default_rng(7 + b + s + h + hd)
+    d = h * hd
+    w = dev(randn(r, b * h, s, s))
+    v, g, q, kk = (dev(randn(r, b, s, d)) for _ in range(4))
+    hs = lambda t: heads_of(t, b, s, h, hd)  # noqa: E731
+    hss, ss, sd = h * s * s, s * s, s * d
+    # out = W V -> merged layout
+    out = hip.f32((b, s, d))
+    hip.gemm_ex(desc(hip, False, False, b * h, h, s, hd, s, w, s, hss, ss, v, d, sd, hd, out, d,
+                     sd, hd))
+    exact(host(out), host(merged_of(hip.gemm(w, hs(v)), b, s, h, hd)), "W V")
+    # dW = g V^T -> heads-major
+    dw = hip.f32((b * h, s, s))
+    hip.gemm_ex(desc(hip, False, True, b * h, h, s, s, hd, g, d, sd, hd, v, d, sd, hd, dw, s, hss,
+                     ss))
+    exact(host(dw), host(hip.gemm(hs(g), hs(v), trans_b=True)), "g V^T")
+    # dV = W^T g -> merged
+    dv = hip.f32((b, s, d))
+    hip.gemm_ex(desc(hip, True, False, b * h, h, s, hd, s, w, s, hss, ss, g, d, sd, hd, dv, d, sd,
+                     hd))
+    exact(host(dv), host(merged_of(hip.gemm(w, hs(g), trans_a=True), b, s, h, hd)), "W^T g")
+    # dQ = dS K, dK = dS^T Q -> merged
+    dq = hip.f32((b, s, d))
+    hip.gemm_ex(desc(hip, False, False, b * h, h, s, hd, s, w, s, hss, ss, kk, d, sd, hd, dq, d,
+                     sd, hd))
+    exact(host(dq), host(merged_of(hip.gemm(w, hs(kk)), b, s, h, hd)), "dS K")
+    dk = hip.f32((b, s, d))
+    hip.gemm_ex(desc(hip, True, False, b * h, h, s, hd, s, w, s, hss, ss, q, d, sd, hd, dk, d, sd,
+                     hd))
+    exact(host(dk), host(merged_of(hip.gemm(w, hs(q), trans_a=True), b, s, h, hd)), "dS^T Q")
+
+
+def test_epilogue_through_split_k(hip):
+    """Few tiles and a long K split the product; the reduction applies the epilogue."""
+    import torch
+    print_case("gemm_ex split-K epilogue")
+    r = np.random.default_rng(11)
+    a, bm = dev(randn(r, 2, 2, 64, 8192)), dev(randn(r, 2, 2, 8192, 64))
+    add = dev(randn(r, 64, 64))
+    c0 = randn(r, 4, 64, 64)
+    c = dev(c0)
+    hip.gemm_ex(desc(hip, False, False, 4, 2, 64, 64, 8192, a, 8192, 2 * 64 * 8192, 64 * 8192,
+                     bm, 64, 2 * 8192 * 64, 8192 * 64, c, 64, 2 * 64 * 64, 64 * 64, alpha=0.375,
+                     addend=add, ld_add=64, stride_add=0, period=1, beta=0.5))
+    acc = hip.gemm(a.reshape(4, 64, 8192), bm.reshape(4, 8192, 64))
+    f = lambda x: torch.tensor(x, dtype=torch.float32, device="cuda")  # noqa: E731
+    want = ((acc * f(0.375)) + add) + f(0.5) * dev(c0)
+    exact(host(c), host(want), "split-K epilogue")
+
+
+def test_epilogue_k_zero(hip):
+    print_case("gemm_ex k=0")
+    r = np.random.default_rng(12)
+    add, c0 = randn(r, 5, 7), randn(r, 3, 5, 7)
+    c = dev(c0)
+    a = dev(np.zeros(1, np.float32))
+    hip.gemm_ex(desc(hip, False, False, 3, 1, 5, 7, 0, a, 1, 0, 0, a, 7, 0, 0, c, 7, 35, 0,
+                     alpha=2.0, addend=dev(add), ld_add=7, stride_add=0, beta=0.5))
+    want = (np.float32(0.0) + add) + np.float32(0.5) * c0
+    exact(host(c), want.astype(np.float32), "k=0 epilogue")
+
+
+def test_gemm_ex_refusals(hip):
+    print_case("gemm_ex refusals")
+    x = dev(np.zeros(64, np.float32))
+    bad = [dict(inner=0), dict(period=0), dict(ld_add=-1)]
+    for kw in bad:
+        inner = kw.get("inner", 1)
+        dsc = desc(hip, False, False, 1, inner, 4, 4, 4, x, 4, 0, 0, x, 4, 0, 0, x, 4, 0, 0,
+                   addend=x, ld_add=kw.get("ld_add", 4), period=kw.get("period", 1))
+        with pytest.raises(RuntimeError):
+            hip.gemm_ex(dsc)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 64), (4096, 37), (256, 512), (3, 5000)])
+def test_softmax_backward_scaled(hip, rows, cols):
+    import torch
+    print_case("softmax_backward_scaled", rows, cols)
+    r = np.random.default_rng(rows + cols)
+    y = hip.softmax(dev(randn(r, rows, cols)))
+    g = dev(randn(r, rows, cols))
+    scale = float(np.float32(1.0) / np.float32(math.sqrt(24.0)))
+    want = hip.softmax_backward(y, g) * torch.tensor(scale, dtype=torch.float32, device="cuda")
+    exact(host(hip.softmax_backward(y, g, scale=scale)), host(want), "scaled")
+    hip.softmax_backward(y, g, scale=scale, out=g)  # in place over g
+    exact(host(g), host(want), "scaled in place")
+
+
+def mha_params(r, d):
+    parts = []
+    for _ in range(4):
+        parts.append((randn(r, d, d) / np.float32(math.sqrt(d))).ravel())
+        parts.append((randn(r, 1, d) * np.float32(0.1)).ravel())
+    return np.concatenate(parts)
+
+
+@pytest.mark.parametrize("b,s,d,heads", [(2, 16, 24, 4), (32, 64, 96, 4), (2, 33, 30, 5),
+                                         (1, 128, 256, 4)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_mha_fused_equals_composed(eng, orc, b, s, d, heads, causal):
+    print_case("mha fused vs composed", b, s, d, heads, causal)
+    r = np.random.default_rng(b * 100 + s + d + heads + causal)
+    x, dy = randn(r, b, s, d), randn(r, b, s, d)
+    params = mha_params(r, d)
+    mask = np.triu(np.full((s, s), -1e9, np.float32), 1) if causal else None
+    fused = eng.mha_fwd_bwd(x, heads, params, dy, mask=mask, fuse=True, weights=True)
+    comp = eng.mha_fwd_bwd(x, heads, params, dy, mask=mask, fuse=False, weights=True)
+    for got, want, what in zip(fused, comp, ("y", "dx", "dparams", "weights")):
+        exact(got, want, f"fused {what}")
+    # And against the oracle composition (the reference's CPU arithmetic).
+    names = ("wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo")
+    shapes = [(d, d), (1, d)] * 4
+    p, off = {}, 0
+    for name, shp in zip(names, shapes):
+        n = int(np.prod(shp))
+        p[name] = params[off:off + n].reshape(shp)
+        off += n
+    y, cache = K.mha_fwd(orc, x, p, heads, mask)
+    dx, grads = K.mha_bwd(orc, dy, cache)
+    tol = 4 * k_tol(max(s, d))
+    ref_close(fused[0], y, tol, "y vs oracle")
+    ref_close(fused[1], dx, tol, "dx vs oracle")
+    off = 0
+    for name, shp in zip(names, shapes):
+        n = int(np.prod(shp))
+        ref_close(fused[2][off:off + n].reshape(shp), grads[name], tol, f"{name} vs oracle")
+        off += n
+
+
+# ------------------------------------------------------- bias / ReLU epilogue
+
+@pytest.mark.parametrize("m,k,n", [(8192, 96, 384), (300, 1024, 257), (64, 8, 10),
+                                   (2048, 4096, 1024), (4096, 1024, 4096)])
+def test_bias_relu_epilogue(hip, m, k, n):
+    """Linear's broadcast bias (ld_addend 0), then ReLU: equal bit for bit to
+    the separate kernels."""
+    print_case("gemm_ex bias/relu", m, k, n)
+    r = np.random.default_rng(m + k + n)
+    a, b = dev(randn(r, m, k)), dev(randn(r, k, n))
+    bias = dev(randn(r, 1, n))
+    pre = hip.gemm(a, b) + bias
+    y = hip.f32((m, n))
+    hip.gemm_ex(desc(hip, False, False, 1, 1, m, n, k, a, k, 0, 0, b, n, 0, 0, y, n, 0, 0,
+                     addend=bias, ld_add=0))
+    exact(host(y), host(pre), "bias")
+    hip.gemm_ex(desc(hip, False, False, 1, 1, m, n, k, a, k, 0, 0, b, n, 0, 0, y, n, 0, 0,
+                     addend=bias, ld_add=0, relu=True))
+    exact(host(y), host(hip.relu(pre)), "bias + relu")
+
+
+def test_relu_epilogue_signs(hip):
+    """-0, NaN and +-inf through the ReLU epilogue match the ReLU kernel."""
+    print_case("gemm_ex relu signs")
+    a = dev(np.array([[1.0], [-1.0], [0.0], [-0.0], [np.nan], [np.inf], [-np.inf], [1e-30]],
+                     np.float32))
+    b = dev(np.ones((1, 3), np.float32))
+    y = hip.f32((8, 3))
+    hip.gemm_ex(desc(hip, False, False, 1, 1, 8, 3, 1, a, 1, 0, 0, b, 3, 0, 0, y, 3, 0, 0,
+                     relu=True))
+    exact(host(y), host(hip.relu(hip.gemm(a, b))), "relu signs")
+
+
+# ------------------------------------------------------- fused vs composed engine graph
+
+def both_graphs(eng, fn):
+    prev = eng.set_fused_nodes(True)
+    try:
+        fused = fn()
+        eng.set_fused_nodes(False)
+        comp = fn()
+    finally:
+        eng.set_fused_nodes(prev)
+    return fused, comp
+
+
+@pytest.mark.parametrize("rows,inp,out", [(64, 8, 10), (8192, 96, 384), (300, 1024, 257)])
+def test_linear_fused_equals_composed(eng, rows, inp, out):
+    print_case("linear fused vs composed", rows, inp, out)
+    r = np.random.default_rng(rows + inp + out)
+    x, w, bias, dy = randn(r, rows, inp), randn(r, inp, out), randn(r, 1, out), randn(r, rows, out)
+    fused, comp = both_graphs(eng, lambda: eng.linear_fwd_bwd(x, w, bias, dy))
+    for got, want, what in zip(fused, comp, ("y", "dx", "dw", "db")):
+        exact(got, want, f"linear {what}")
+
+
+@pytest.mark.parametrize("b,s,d,heads,ff,causal", [(2, 16, 24, 4, 32, True),
+                                                    (32, 64, 96, 4, 384, True),
+                                                    (2, 33, 30, 5, 70, False)])
+def test_block_fused_equals_composed(eng, b, s, d, heads, ff, causal):
+    print_case("block fused vs composed", b, s, d, heads, ff, causal)
+    r = np.random.default_rng(b + s + d + heads + ff)
+    x, dy = randn(r, b, s, d), randn(r, b, s, d)
+    n = eng.block_num_params(d, heads, ff)
+    params = randn(r, n) * np.float32(0.1)
+    fused, comp = both_graphs(eng, lambda: eng.block_fwd_bwd(x, heads, ff, causal, params, dy))
+    for got, want, what in zip(fused, comp, ("y", "dx", "dparams")):
+        exact(got, want, f"block {what}")
+
+
+def test_charlm_training_fused_equals_composed(eng):
+    """Five Adam steps of the cfg3 character model: losses and final weights
+    are identical under both graphs."""
+    import _compose as KC
+    print_case("charlm fused vs composed")
+    vocab, s, d, heads, ff, layers, b = 121, 64, 96, 4, 384, 2, 32
+    r = np.random.default_rng(5)
+    ids = r.integers(0, vocab, (b, s)).astype(np.int64)
+    targets = r.integers(0, vocab, (b, s)).astype(np.int64)
+    shapes = KC.charlm_param_shapes(vocab, d, ff, layers)
+    params = np.concatenate([(randn(r, *shp) * np.float32(0.05)).ravel() for shp in shapes])
+    fused, comp = both_graphs(eng, lambda: eng.charlm_train(ids, targets, vocab, d, heads, ff,
+                                                            layers, params, 5, 1e-3))
+    exact(fused[0], comp[0], "losses")
+    exact(fused[1], comp[1], "weights")
