@@ -295,6 +295,44 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
     del x, g, dx, m, v
     out["bandwidth_cfg4"] = bw
     torch.cuda.empty_cache()
+    # The other bandwidth-bound kernels of the path, at the shapes cfg 5 gives
+    # them (16 x 512 tokens, d 1024, FFN 4096, 16 heads of 512 x 512 scores),
+    # and max-pool at a large image batch. Bytes are the algorithmic ones:
+    # every input read once, every output written once.
+    bt = {}
+    rows, d, ff = 8192, 1024, 4096
+    x = torch.randn(rows, d, device="cuda", generator=r)
+    gam = torch.randn(d, device="cuda", generator=r)
+    bet = torch.randn(d, device="cuda", generator=r)
+    sec = timer.time(lambda: hip.layernorm(x, gam, bet), 20, 3)
+    bt["layernorm 8192x1024"] = roofline("layernorm", "hbm", 12 * x.numel() + 4 * rows, sec)
+    _, xh, inv = hip.layernorm(x, gam, bet)
+    sec = timer.time(lambda: hip.layernorm_backward(x, xh, gam, inv), 20, 3)
+    bt["layernorm_backward 8192x1024"] = roofline("layernorm_backward", "hbm",
+                                                  12 * x.numel() + 4 * rows + 8 * d, sec)
+    del x, xh, inv
+    gb = torch.randn(rows, ff, device="cuda", generator=r)
+    sec = timer.time(lambda: hip.sum_axis(gb, 1, rows, ff), 20, 3)
+    bt["bias_grad_sum 8192x4096"] = roofline("sum_axis", "hbm", 4 * gb.numel() + 4 * ff, sec)
+    del gb
+    sc = torch.randn(16 * 16 * 512, 512, device="cuda", generator=r)
+    sec = timer.time(lambda: hip.softmax(sc), 20, 3)
+    bt["softmax 131072x512"] = roofline("softmax", "hbm", 8 * sc.numel(), sec)
+    y = hip.softmax(sc)
+    sec = timer.time(lambda: hip.softmax_backward(y, sc), 20, 3)
+    bt["softmax_backward 131072x512"] = roofline("softmax_backward", "hbm", 12 * sc.numel(), sec)
+    del sc, y
+    im = torch.randn(64, 64, 112, 112, device="cuda", generator=r)
+    sec = timer.time(lambda: hip.maxpool(im, 2, 2), 20, 3)
+    bt["maxpool 64x64x112x112 k2"] = roofline("maxpool", "hbm", 6 * im.numel(), sec)
+    pooled, am = hip.maxpool(im, 2, 2)
+    gp = torch.randn_like(pooled)
+    sec = timer.time(lambda: hip.maxpool_backward(am, gp, tuple(im.shape), 2, 2), 20, 3)
+    bt["maxpool_backward 64x64x112x112 k2"] = roofline("maxpool_backward", "hbm",
+                                                       6 * im.numel(), sec)
+    del im, pooled, am, gp
+    out["bandwidth_transformer_shapes"] = bt
+    torch.cuda.empty_cache()
     # cfg 3 and cfg 5: Transformer training steps.
     for tag, (b, s, vocab, d, h, ff, layers, steps, warm) in {
             "charlm_cfg3": (32, 64, 121, 96, 4, 384, 2, 100, 10),

@@ -198,6 +198,118 @@ __global__ __launch_bounds__(kThreads) void maxpool_backward_kernel(
     }
 }
 
+// Non-overlapping windows (kernel == stride, no padding), the usual pooling
+// layer: 32-bit index math (every entry point caps the input below 2^31
+// elements) and, in the backward pass, one thread per output that writes its
+// whole window -- each input is covered by at most one window, so the
+// gradient is 0 + g at the window's argmax and 0 elsewhere, which is what the
+// covering-window sum of maxpool_backward_kernel gives. Inputs past the last
+// whole window (H or W not a multiple of k) are written by the last row or
+// column of windows. The forward keeps the first strict maximum in window
+// order.
+template <typename Idx>
+__global__ __launch_bounds__(kThreads) void maxpool_tiles_kernel(const float* __restrict__ x,
+                                                                 float* __restrict__ y,
+                                                                 Idx* __restrict__ argmax,
+                                                                 uint32_t width, uint32_t height,
+                                                                 uint32_t out_w, uint32_t out_h,
+                                                                 uint32_t k, uint32_t n) {
+    const uint32_t step = gridDim.x * kThreads;
+    for (uint32_t o = blockIdx.x * kThreads + threadIdx.x; o < n; o += step) {
+        const uint32_t ow = o % out_w, t = o / out_w;
+        const uint32_t oh = t % out_h, plane = t / out_h;
+        const uint32_t base = (plane * height + oh * k) * width + ow * k;
+        float best = x[base];
+        uint32_t best_idx = base;
+        for (uint32_t i = 0; i < k; ++i)
+            for (uint32_t j = 0; j < k; ++j) {
+                const uint32_t idx = base + i * width + j;
+                const float xv = x[idx];
+                if (xv > best) {
+                    best = xv;
+                    best_idx = idx;
+                }
+            }
+        y[o] = best;
+        argmax[o] = static_cast<Idx>(best_idx);
+    }
+}
+
+template <typename Idx>
+__global__ __launch_bounds__(kThreads) void maxpool_tiles_backward_kernel(
+    const Idx* __restrict__ argmax, const float* __restrict__ g, float* __restrict__ dx,
+    uint32_t width, uint32_t height, uint32_t out_w, uint32_t out_h, uint32_t k, uint32_t n) {
+    const uint32_t step = gridDim.x * kThreads;
+    for (uint32_t o = blockIdx.x * kThreads + threadIdx.x; o < n; o += step) {
+        const uint32_t ow = o % out_w, t = o / out_w;
+        const uint32_t oh = t % out_h, plane = t / out_h;
+        const Idx am = argmax[o];
+        const float gv = 0.0f + g[o];
+        const uint32_t h0 = oh * k, v0 = ow * k;
+        const uint32_t h1 = oh + 1 == out_h ? height : h0 + k;
+        const uint32_t v1 = ow + 1 == out_w ? width : v0 + k;
+        for (uint32_t h = h0; h < h1; ++h)
+            for (uint32_t v = v0; v < v1; ++v) {
+                const uint32_t idx = (plane * height + h) * width + v;
+                const bool in = h < h0 + k && v < v0 + k;
+                dx[idx] = (in && static_cast<Idx>(idx) == am) ? gv : 0.0f;
+            }
+    }
+}
+
+// 2 x 2 windows on even-sized planes: each window row is one aligned float2.
+template <typename Idx>
+__global__ __launch_bounds__(kThreads) void maxpool_2x2_kernel(const float* __restrict__ x,
+                                                               float* __restrict__ y,
+                                                               Idx* __restrict__ argmax,
+                                                               uint32_t width, uint32_t out_w,
+                                                               uint32_t n) {
+    const uint32_t step = gridDim.x * kThreads;
+    for (uint32_t o = blockIdx.x * kThreads + threadIdx.x; o < n; o += step) {
+        const uint32_t ow = o % out_w, row = o / out_w;  // row = plane * out_h + oh
+        const uint32_t base = 2 * row * width + 2 * ow;
+        const float2 a = *reinterpret_cast<const float2*>(x + base);
+        const float2 b = *reinterpret_cast<const float2*>(x + base + width);
+        float best = a.x;
+        uint32_t idx = base;
+        if (a.y > best) { best = a.y; idx = base + 1; }
+        if (b.x > best) { best = b.x; idx = base + width; }
+        if (b.y > best) { best = b.y; idx = base + width + 1; }
+        y[o] = best;
+        argmax[o] = static_cast<Idx>(idx);
+    }
+}
+
+template <typename Idx>
+__global__ __launch_bounds__(kThreads) void maxpool_2x2_backward_kernel(
+    const Idx* __restrict__ argmax, const float* __restrict__ g, float* __restrict__ dx,
+    uint32_t width, uint32_t out_w, uint32_t n) {
+    const uint32_t step = gridDim.x * kThreads;
+    for (uint32_t o = blockIdx.x * kThreads + threadIdx.x; o < n; o += step) {
+        const uint32_t ow = o % out_w, row = o / out_w;
+        const uint32_t base = 2 * row * width + 2 * ow;
+        const Idx am = argmax[o];
+        const float gv = 0.0f + g[o];
+        float2 a, b;
+        a.x = static_cast<Idx>(base) == am ? gv : 0.0f;
+        a.y = static_cast<Idx>(base + 1) == am ? gv : 0.0f;
+        b.x = static_cast<Idx>(base + width) == am ? gv : 0.0f;
+        b.y = static_cast<Idx>(base + width + 1) == am ? gv : 0.0f;
+        *reinterpret_cast<float2*>(dx + base) = a;
+        *reinterpret_cast<float2*>(dx + base + width) = b;
+    }
+}
+
+bool even_2x2(const ehip_window_t* w, const void* p, const void* q) {
+    return w->kernel_h == 2 && w->height % 2 == 0 && w->width % 2 == 0 &&
+           reinterpret_cast<uintptr_t>(p) % 8 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0;
+}
+
+bool tiled_window(const ehip_window_t* w) {
+    return w->kernel_h == w->kernel_w && w->stride == w->kernel_h && w->padding == 0 &&
+           w->out_h > 0 && w->out_w > 0;
+}
+
 // Row gather; an out-of-range index yields NaN rather than a wild read.
 __global__ __launch_bounds__(kThreads) void select_rows_kernel(const float* __restrict__ x,
                                                                const int32_t* __restrict__ idx,
@@ -248,6 +360,18 @@ int maxpool_forward(const char* name, const float* x, float* y, Idx* argmax,
                     (long long)n_in, (long long)max_in);
     const int64_t n = w->batch * w->channels * w->out_h * w->out_w;
     if (n == 0) return EHIP_OK;
+    if (tiled_window(w) && even_2x2(w, x, x)) {
+        EHIP_LAUNCH(name, maxpool_2x2_kernel<Idx>, dim3(grid_for(n)), dim3(kThreads), 0,
+                    as_stream(stream), x, y, argmax, uint32_t(w->width), uint32_t(w->out_w),
+                    uint32_t(n));
+        return EHIP_OK;
+    }
+    if (tiled_window(w)) {
+        EHIP_LAUNCH(name, maxpool_tiles_kernel<Idx>, dim3(grid_for(n)), dim3(kThreads), 0,
+                    as_stream(stream), x, y, argmax, uint32_t(w->width), uint32_t(w->height),
+                    uint32_t(w->out_w), uint32_t(w->out_h), uint32_t(w->kernel_h), uint32_t(n));
+        return EHIP_OK;
+    }
     EHIP_LAUNCH(name, maxpool_kernel<Idx>, dim3(grid_for(n)), dim3(kThreads), 0,
                 as_stream(stream), x, y, argmax, *w, n);
     return EHIP_OK;
@@ -264,6 +388,21 @@ int maxpool_backward(const char* name, const Idx* argmax, const float* g, float*
         return fail(EHIP_EINVAL, "%s: %lld input elements beyond exact indices (%lld)", name,
                     (long long)n, (long long)max_in);
     if (n == 0) return EHIP_OK;
+    if (tiled_window(w) && even_2x2(w, dx, dx)) {
+        const int64_t n_out = w->batch * w->channels * w->out_h * w->out_w;
+        EHIP_LAUNCH(name, maxpool_2x2_backward_kernel<Idx>, dim3(grid_for(n_out)), dim3(kThreads),
+                    0, as_stream(stream), argmax, g, dx, uint32_t(w->width), uint32_t(w->out_w),
+                    uint32_t(n_out));
+        return EHIP_OK;
+    }
+    if (tiled_window(w)) {
+        const int64_t n_out = w->batch * w->channels * w->out_h * w->out_w;
+        EHIP_LAUNCH(name, maxpool_tiles_backward_kernel<Idx>, dim3(grid_for(n_out)),
+                    dim3(kThreads), 0, as_stream(stream), argmax, g, dx, uint32_t(w->width),
+                    uint32_t(w->height), uint32_t(w->out_w), uint32_t(w->out_h),
+                    uint32_t(w->kernel_h), uint32_t(n_out));
+        return EHIP_OK;
+    }
     EHIP_LAUNCH(name, maxpool_backward_kernel<Idx>, dim3(grid_for(n)), dim3(kThreads), 0,
                 as_stream(stream), argmax, g, dx, *w, n);
     return EHIP_OK;

@@ -12,16 +12,25 @@ namespace {
 constexpr int kThreads = 256;
 
 // Adds p[0], p[step], ..., p[(n-1) step] to acc in that order. Loads are
-// issued eight at a time ahead of the additions, which stay in index order.
+// issued sixteen at a time ahead of the additions, which stay in index order:
+// a lane's chain of dependent HBM round trips is n / 16 long.
 __device__ __forceinline__ float ordered_sum(float acc, const float* __restrict__ p, int64_t n,
                                              int64_t step) {
+    constexpr int U = 16;
     int64_t i = 0;
-    for (; i + 8 <= n; i += 8) {
-        float v[8];
+    for (; i + U <= n; i += U) {
+        float v[U];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = p[(i + u) * step];
+        for (int u = 0; u < U; ++u) v[u] = p[(i + u) * step];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc += v[u];
+        for (int u = 0; u < U; ++u) acc += v[u];
+    }
+    for (; i + 4 <= n; i += 4) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = p[(i + u) * step];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc += v[u];
     }
     for (; i < n; ++i) acc += p[i * step];
     return acc;
@@ -68,6 +77,58 @@ __global__ __launch_bounds__(kThreads) void sum_cols(const float* __restrict__ x
         float s = 0.0f;
         for (int l = 0; l < rl; ++l) s += lanes[l * cw + cl];
         out[int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c] = s;
+    }
+}
+
+// sum_cols for CW = 64 with four adjacent columns per thread (float4 loads,
+// 1 KiB per wave and row instead of 256 bytes): the same row lanes, rows per
+// lane and order per column as sum_cols, so the sums are bit-identical.
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+__device__ __forceinline__ float4 ordered_sum4(const float* __restrict__ p, int64_t n,
+                                               int64_t step) {
+    constexpr int U = 16;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int64_t i = 0;
+    for (; i + U <= n; i += U) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = *reinterpret_cast<const float4*>(p + (i + u) * step);
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = add4(acc, v[u]);
+    }
+    for (; i < n; ++i) acc = add4(acc, *reinterpret_cast<const float4*>(p + i * step));
+    return acc;
+}
+
+__global__ __launch_bounds__(kThreads) void sum_cols4(const float* __restrict__ x,
+                                                      float* __restrict__ out, int64_t rows,
+                                                      int64_t cols, int64_t ld, int64_t rpb,
+                                                      int64_t x_slab, int64_t out_slab) {
+    constexpr int kCw = 64, kRl = kThreads / kCw;
+    __shared__ float4 lanes[kThreads];
+    const int lane = threadIdx.x / kCw, cl = threadIdx.x % kCw;
+    const int64_t c = (int64_t(blockIdx.y) * kCw + cl) * 4;
+    const int64_t r0 = int64_t(blockIdx.x) * rpb;
+    int64_t r1 = r0 + rpb;
+    if (r1 > rows) r1 = rows;
+    const float* xs = x + int64_t(blockIdx.z) * x_slab;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (c < cols && r0 + lane < r1)
+        acc = ordered_sum4(xs + (r0 + lane) * ld + c, (r1 - r0 - lane + kRl - 1) / kRl,
+                           int64_t(kRl) * ld);
+    lanes[threadIdx.x] = acc;
+    __syncthreads();
+    if (lane == 0 && c < cols) {
+        float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int l = 0; l < kRl; ++l) sum = add4(sum, lanes[l * kCw + cl]);
+        float* o = out + int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c;
+        o[0] = sum.x;
+        o[1] = sum.y;
+        o[2] = sum.z;
+        o[3] = sum.w;
     }
 }
 
@@ -131,14 +192,32 @@ int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64
     if (blocks < 1) blocks = 1;
     const int64_t rpb = ceil_div(rows, blocks);
     blocks = ceil_div(rows, rpb);
+    // Wide rows of aligned float4s take sum_cols4 (same order, a quarter of
+    // the column tiles).
+    const bool vec = cols >= 256 && cols % 4 == 0 && ld % 4 == 0 && x_slab % 4 == 0 &&
+                     aligned16(x);
+    const unsigned tiles4 = unsigned(ceil_div(cols, 4 * 64));
     if (blocks == 1) {
-        EHIP_LAUNCH("column_sums", sum_cols, dim3(1, unsigned(tiles), unsigned(slabs)),
-                    dim3(kThreads), 0, s, x, out, rows, cols, ld, rows, x_slab, cols, cw);
+        if (vec) {
+            EHIP_LAUNCH("column_sums", sum_cols4, dim3(1, tiles4, unsigned(slabs)), dim3(kThreads),
+                        0, s, x, out, rows, cols, ld, rows, x_slab, cols);
+        } else {
+            EHIP_LAUNCH("column_sums", sum_cols, dim3(1, unsigned(tiles), unsigned(slabs)),
+                        dim3(kThreads), 0, s, x, out, rows, cols, ld, rows, x_slab, cols, cw);
+        }
         return EHIP_OK;
     }
     float* partial =
         static_cast<float*>(scratch(size_t(slabs * blocks * cols) * sizeof(float), 1));
     if (partial == nullptr) return EHIP_ENOMEM;
+    if (vec) {
+        EHIP_LAUNCH("column_sums_blocks", sum_cols4, dim3(unsigned(blocks), tiles4, unsigned(slabs)),
+                    dim3(kThreads), 0, s, x, partial, rows, cols, ld, rpb, x_slab, blocks * cols);
+        EHIP_LAUNCH("column_sums_final", sum_cols4, dim3(1, tiles4, unsigned(slabs)),
+                    dim3(kThreads), 0, s, partial, out, blocks, cols, cols, blocks, blocks * cols,
+                    cols);
+        return EHIP_OK;
+    }
     EHIP_LAUNCH("column_sums_blocks", sum_cols, dim3(unsigned(blocks), unsigned(tiles), unsigned(slabs)),
                 dim3(kThreads), 0, s, x, partial, rows, cols, ld, rpb, x_slab, blocks * cols, cw);
     EHIP_LAUNCH("column_sums_final", sum_cols, dim3(1, unsigned(tiles), unsigned(slabs)),

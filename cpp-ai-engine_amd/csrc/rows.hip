@@ -14,6 +14,7 @@
 
 #include "common.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace ehip {
@@ -378,17 +379,31 @@ __global__ __launch_bounds__(1024) void mean_rows(const float* __restrict__ row_
 
 // src/transformer.cpp:53-73: mean = (sum x) * (1/D); var = (sum (x-mean)^2) * (1/D);
 // inv = 1 / sqrt(var + eps); xhat = (x - mean) * inv; out = gamma * xhat + beta.
-template <int T, int V>
+template <int T, int V, bool VEC4>
 __global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows(
     const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
     float* __restrict__ out, float* __restrict__ xhat, float* __restrict__ inv_std, int64_t rows,
     int64_t cols, float eps) {
+    using F = Frag<T, V, VEC4>;
     __shared__ float sh[Group<T>::kBlock / 64];
     const float inv_d = 1.0f / static_cast<float>(cols);
     const int tid = Group<T>::tid();
-    for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
-        Frag<T, V, false> f;
-        f.load(x + r * cols, int(cols), tid, 0.0f);
+    float gm[V], bt[V];
+#pragma unroll
+    for (int t = 0; t < V; ++t) {
+        const int64_t c = F::col(tid, t);
+        gm[t] = c < cols ? gamma[c] : 0.0f;
+        bt[t] = c < cols ? beta[c] : 0.0f;
+    }
+    // The next row is loaded before the current one is reduced, so a group
+    // keeps loads in flight while it computes and stores.
+    const int64_t step = Group<T>::row_step();
+    int64_t r = Group<T>::first_row();
+    F nf;
+    if (r < rows) nf.load(x + r * cols, int(cols), tid, 0.0f);
+    for (; r < rows; r += step) {
+        const F f = nf;
+        if (r + step < rows) nf.load(x + (r + step) * cols, int(cols), tid, 0.0f);
         float s = 0.0f;
 #pragma unroll
         for (int t = 0; t < V; ++t) s += f.v[t];
@@ -396,46 +411,172 @@ __global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows(
         float q = 0.0f;
 #pragma unroll
         for (int t = 0; t < V; ++t) {
-            const float d = Frag<T, V, false>::col(tid, t) < cols ? f.v[t] - mean : 0.0f;
+            const float d = F::col(tid, t) < cols ? f.v[t] - mean : 0.0f;
             q += d * d;
         }
         const float var = group_reduce<T, false>(q, sh) * inv_d;
         const float inv = 1.0f / sqrtf(var + eps);
         if (tid == 0) inv_std[r] = inv;
+        F fh, fo;
 #pragma unroll
         for (int t = 0; t < V; ++t) {
-            const int64_t c = Frag<T, V, false>::col(tid, t);
-            if (c < cols) {
-                const float h = (f.v[t] - mean) * inv;
-                xhat[r * cols + c] = h;
-                out[r * cols + c] = gamma[c] * h + beta[c];
-            }
+            fh.v[t] = (f.v[t] - mean) * inv;
+            fo.v[t] = gm[t] * fh.v[t] + bt[t];
         }
+        fh.store(xhat + r * cols, int(cols), tid);
+        fo.store(out + r * cols, int(cols), tid);
     }
 }
 
 // dx per row (src/transformer.cpp:147-171); dgamma/dbeta partial sums per
 // group over the rows it visits, ascending, into partial[group][2][cols].
-template <int T, int V>
-__global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows_backward(
+// One group per block of T threads (group = blockIdx.x, rows group, group +
+// groups, ...), so that few groups still spread over every CU; the next two
+// rows' dy and xhat are loaded before the current row is reduced, keeping
+// loads in flight behind the arithmetic of a group's serial row chain.
+template <int T, int V, bool VEC4>
+__global__ __launch_bounds__(T) void layernorm_rows_backward(
     const float* __restrict__ dy, const float* __restrict__ xhat, const float* __restrict__ gamma,
     const float* __restrict__ inv_std, float* __restrict__ dx, float* __restrict__ partial,
     int64_t rows, int64_t cols) {
-    __shared__ float sh[Group<T>::kBlock / 64];
+    using F = Frag<T, V, VEC4>;
+    constexpr int kAhead = 3;  // rows in registers: the current one and two ahead
+    __shared__ float sh[T / 64];
     const float inv_d = 1.0f / static_cast<float>(cols);
-    const int tid = Group<T>::tid();
+    const int tid = threadIdx.x;
+    const int64_t group = blockIdx.x, step = gridDim.x;
     float dg[V], db[V], gm[V];
 #pragma unroll
     for (int t = 0; t < V; ++t) {
         dg[t] = 0.0f;
         db[t] = 0.0f;
-        const int64_t c = Frag<T, V, false>::col(tid, t);
+        const int64_t c = F::col(tid, t);
         gm[t] = c < cols ? gamma[c] : 0.0f;
     }
-    for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
-        Frag<T, V, false> fd, fh;
-        fd.load(dy + r * cols, int(cols), tid, 0.0f);
-        fh.load(xhat + r * cols, int(cols), tid, 0.0f);
+    F fd[kAhead], fh[kAhead];
+    float iv[kAhead];
+#pragma unroll
+    for (int a = 0; a < kAhead - 1; ++a) {
+        const int64_t ra = group + a * step;
+        iv[a] = 0.0f;
+        if (ra < rows) {
+            fd[a].load(dy + ra * cols, int(cols), tid, 0.0f);
+            fh[a].load(xhat + ra * cols, int(cols), tid, 0.0f);
+            iv[a] = inv_std[ra];
+        }
+    }
+    int64_t r = group;
+    for (; r < rows; r += step) {
+        // Rotate by value so the register arrays keep static indices.
+        const int64_t rn = r + (kAhead - 1) * step;
+        iv[kAhead - 1] = 0.0f;
+        if (rn < rows) {
+            fd[kAhead - 1].load(dy + rn * cols, int(cols), tid, 0.0f);
+            fh[kAhead - 1].load(xhat + rn * cols, int(cols), tid, 0.0f);
+            iv[kAhead - 1] = inv_std[rn];
+        }
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+            const float dxh = fd[0].v[t] * gm[t];
+            s1 += dxh;
+            s2 += dxh * fh[0].v[t];
+        }
+        s1 = group_reduce<T, false>(s1, sh);
+        s2 = group_reduce<T, false>(s2, sh);
+        const float inv = iv[0];
+        F fo;
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+            const float dxh = fd[0].v[t] * gm[t];
+            fo.v[t] = inv * (dxh - inv_d * s1 - fh[0].v[t] * inv_d * s2);
+            dg[t] = dg[t] + fd[0].v[t] * fh[0].v[t];
+            db[t] = db[t] + fd[0].v[t];
+        }
+        fo.store(dx + r * cols, int(cols), tid);
+#pragma unroll
+        for (int a = 0; a + 1 < kAhead; ++a) {
+            fd[a] = fd[a + 1];
+            fh[a] = fh[a + 1];
+            iv[a] = iv[a + 1];
+        }
+    }
+    float* pg = partial + group * 2 * cols;
+#pragma unroll
+    for (int t = 0; t < V; ++t) {
+        const int64_t c = F::col(tid, t);
+        if (c < cols) {
+            pg[c] = dg[t];
+            pg[cols + c] = db[t];
+        }
+    }
+}
+
+constexpr int kLnWaves = 8;
+
+// acc of wave 0 += acc of waves 1..kLnWaves-1 by a fixed halving tree
+// (wave w adds wave w + half for half = kLnWaves / 2, ..., 1).
+template <int V>
+__device__ __forceinline__ void combine_waves(float (&acc)[V], float (*tree)[V][64], int wave,
+                                              int lane) {
+#pragma unroll
+    for (int half = kLnWaves / 2; half >= 1; half /= 2) {
+        if (wave >= half && wave < 2 * half) {
+#pragma unroll
+            for (int t = 0; t < V; ++t) tree[wave - half][t][lane] = acc[t];
+        }
+        __syncthreads();
+        if (wave < half) {
+#pragma unroll
+            for (int t = 0; t < V; ++t) acc[t] = acc[t] + tree[wave][t][lane];
+        }
+        __syncthreads();
+    }
+}
+
+// The large-problem form: a group is a block of kLnWaves waves, each taking
+// one row at a time (wave w of group g: rows g + groups (w + kLnWaves i),
+// ascending i, the next row loaded before the current one is reduced), so
+// that every CU holds many independent rows while the partials stay few
+// (one dgamma / dbeta row per group). The waves' partial sums are combined
+// by a fixed tree through LDS (w += w + half, halving), then written to
+// partial[group][2][cols]; layernorm_param_grads adds the groups in order.
+
+template <int V, bool VEC4>
+__global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
+    const float* __restrict__ dy, const float* __restrict__ xhat, const float* __restrict__ gamma,
+    const float* __restrict__ inv_std, float* __restrict__ dx, float* __restrict__ partial,
+    int64_t rows, int64_t cols) {
+    using F = Frag<64, V, VEC4>;
+    __shared__ float tree[kLnWaves / 2][V][64];
+    const float inv_d = 1.0f / static_cast<float>(cols);
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int64_t group = blockIdx.x, groups = gridDim.x;
+    float dg[V], db[V], gm[V];
+#pragma unroll
+    for (int t = 0; t < V; ++t) {
+        dg[t] = 0.0f;
+        db[t] = 0.0f;
+        const int64_t c = F::col(lane, t);
+        gm[t] = c < cols ? gamma[c] : 0.0f;
+    }
+    const int64_t step = groups * kLnWaves;
+    int64_t r = group + groups * wave;
+    F fd, fh;
+    float inv = 0.0f;
+    if (r < rows) {
+        fd.load(dy + r * cols, int(cols), lane, 0.0f);
+        fh.load(xhat + r * cols, int(cols), lane, 0.0f);
+        inv = inv_std[r];
+    }
+    for (; r < rows; r += step) {
+        F nd, nh;
+        float ninv = 0.0f;
+        if (r + step < rows) {
+            nd.load(dy + (r + step) * cols, int(cols), lane, 0.0f);
+            nh.load(xhat + (r + step) * cols, int(cols), lane, 0.0f);
+            ninv = inv_std[r + step];
+        }
         float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
         for (int t = 0; t < V; ++t) {
@@ -443,10 +584,9 @@ __global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows_backward(
             s1 += dxh;
             s2 += dxh * fh.v[t];
         }
-        s1 = group_reduce<T, false>(s1, sh);
-        s2 = group_reduce<T, false>(s2, sh);
-        const float inv = inv_std[r];
-        Frag<T, V, false> fo;
+        s1 = wave_sum(s1);
+        s2 = wave_sum(s2);
+        F fo;
 #pragma unroll
         for (int t = 0; t < V; ++t) {
             const float dxh = fd.v[t] * gm[t];
@@ -454,17 +594,59 @@ __global__ __launch_bounds__(Group<T>::kBlock) void layernorm_rows_backward(
             dg[t] = dg[t] + fd.v[t] * fh.v[t];
             db[t] = db[t] + fd.v[t];
         }
-        fo.store(dx + r * cols, int(cols), tid);
+        fo.store(dx + r * cols, int(cols), lane);
+        fd = nd;
+        fh = nh;
+        inv = ninv;
     }
-    const int64_t group = Group<T>::first_row();  // group index == its first row
-    float* pg = partial + group * 2 * cols;
+    combine_waves<V>(dg, tree, wave, lane);
+    combine_waves<V>(db, tree, wave, lane);
+    if (wave == 0) {
+        float* pg = partial + group * 2 * cols;
 #pragma unroll
-    for (int t = 0; t < V; ++t) {
-        const int64_t c = Frag<T, V, false>::col(tid, t);
-        if (c < cols) {
-            pg[c] = dg[t];
-            pg[cols + c] = db[t];
+        for (int t = 0; t < V; ++t) {
+            const int64_t c = F::col(lane, t);
+            if (c < cols) {
+                pg[c] = dg[t];
+                pg[cols + c] = db[t];
+            }
         }
+    }
+}
+
+// dgamma[c] and dbeta[c] from partial[group][2][cols]: kLanes lanes per
+// column add groups l, l + kLanes, ... in order, then the lanes in order.
+constexpr int kParamLanes = 4;
+
+__global__ __launch_bounds__(256) void layernorm_param_grads(const float* __restrict__ partial,
+                                                             float* __restrict__ dgamma,
+                                                             float* __restrict__ dbeta,
+                                                             int64_t groups, int64_t cols) {
+    __shared__ float sh[kParamLanes][256 / kParamLanes];
+    constexpr int kCols = 256 / kParamLanes;
+    const int l = threadIdx.x / kCols, cl = threadIdx.x % kCols;
+    const int64_t c2 = int64_t(blockIdx.x) * kCols + cl;  // in [0, 2 cols)
+    float acc = 0.0f;
+    if (c2 < 2 * cols) {
+        const float* p = partial + c2;
+        int64_t g = l;
+        for (; g + 15 * kParamLanes < groups; g += 16 * kParamLanes) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = p[(g + u * kParamLanes) * 2 * cols];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) acc += v[u];
+        }
+        for (; g < groups; g += kParamLanes) acc += p[g * 2 * cols];
+    }
+    sh[l][cl] = acc;
+    __syncthreads();
+    if (l == 0 && c2 < 2 * cols) {
+        float sum = sh[0][cl];
+#pragma unroll
+        for (int k = 1; k < kParamLanes; ++k) sum += sh[k][cl];
+        if (c2 < cols) dgamma[c2] = sum;
+        else dbeta[c2 - cols] = sum;
     }
 }
 
@@ -699,18 +881,28 @@ int ehip_layernorm_f32(const float* x, const float* gamma, const float* beta, fl
         return fail(EHIP_EINVAL, "layernorm: null pointer");
     if (rows == 0) return EHIP_OK;
     hipStream_t s = as_stream(stream);
-#define EHIP_LN(T, V)                                                                        \
-    EHIP_LAUNCH("layernorm", (layernorm_rows<T, V>),                                         \
-                dim3(row_grid(rows, Group<T>::kPerBlock)), dim3(Group<T>::kBlock), 0, s, x, \
-                gamma, beta, out, xhat, inv_std, rows, cols, eps)
-    if (cols <= 64) EHIP_LN(64, 1);
-    else if (cols <= 128) EHIP_LN(64, 2);
-    else if (cols <= 256) EHIP_LN(64, 4);
-    else if (cols <= 512) EHIP_LN(64, 8);
-    else if (cols <= 1024) EHIP_LN(64, 16);
-    else if (cols <= 2048) EHIP_LN(64, 32);
-    else if (cols <= 4096) EHIP_LN(256, 16);
-    else EHIP_LN(256, 32);
+    const bool vec = cols >= 256 && rows_vec_ok(cols, {x, gamma, beta, out, xhat});
+    // At most 512 blocks (two per CU): large inputs give each group several rows,
+    // so that its loads of the next row overlap the stores of the current one.
+#define EHIP_LN(T, V, VEC)                                                                   \
+    EHIP_LAUNCH("layernorm", (layernorm_rows<T, V, VEC>),                                    \
+                dim3(std::min(row_grid(rows, Group<T>::kPerBlock), 512u)),                   \
+                dim3(Group<T>::kBlock), 0, s, x, gamma, beta, out, xhat, inv_std, rows, cols, eps)
+    if (vec) {
+        if (cols <= 256) EHIP_LN(64, 4, true);
+        else if (cols <= 512) EHIP_LN(64, 8, true);
+        else if (cols <= 1024) EHIP_LN(64, 16, true);
+        else if (cols <= 2048) EHIP_LN(64, 32, true);
+        else if (cols <= 4096) EHIP_LN(256, 16, true);
+        else EHIP_LN(256, 32, true);
+    } else if (cols <= 64) EHIP_LN(64, 1, false);
+    else if (cols <= 128) EHIP_LN(64, 2, false);
+    else if (cols <= 256) EHIP_LN(64, 4, false);
+    else if (cols <= 512) EHIP_LN(64, 8, false);
+    else if (cols <= 1024) EHIP_LN(64, 16, false);
+    else if (cols <= 2048) EHIP_LN(64, 32, false);
+    else if (cols <= 4096) EHIP_LN(256, 16, false);
+    else EHIP_LN(256, 32, false);
 #undef EHIP_LN
     return EHIP_OK;
 }
@@ -725,26 +917,65 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
     if (!dy || !xhat || !gamma || !inv_std || !dx || !dgamma || !dbeta)
         return fail(EHIP_EINVAL, "layernorm_backward: null pointer");
     hipStream_t s = as_stream(stream);
-    // A fixed number of row groups per shape: about 16 rows each, at most 512.
-    const int per_block = cols <= 2048 ? 4 : 1;
+    // A fixed number of row groups per shape, which fixes the order of the
+    // dgamma / dbeta sums.
+    const bool vec = cols >= 256 && rows_vec_ok(cols, {dy, xhat, gamma, dx});
+    if (rows * cols >= (int64_t(1) << 20) && cols <= 2048) {
+        // Large problems: groups of kLnWaves waves, about 32 rows per group,
+        // at most 256 groups (one per CU), and one launch for the parameter
+        // gradients.
+        int64_t groups = ceil_div(rows, 32);
+        if (groups > 256) groups = 256;
+        float* partial =
+            static_cast<float*>(scratch(size_t(groups) * 2 * size_t(cols) * sizeof(float)));
+        if (partial == nullptr) return EHIP_ENOMEM;
+#define EHIP_LNW(V, VEC)                                                                         \
+    EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC>),                    \
+                dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma, inv_std, dx, \
+                partial, rows, cols)
+        if (vec) {
+            if (cols <= 256) EHIP_LNW(4, true);
+            else if (cols <= 512) EHIP_LNW(8, true);
+            else if (cols <= 1024) EHIP_LNW(16, true);
+            else EHIP_LNW(32, true);
+        } else if (cols <= 64) EHIP_LNW(1, false);
+        else if (cols <= 128) EHIP_LNW(2, false);
+        else if (cols <= 256) EHIP_LNW(4, false);
+        else if (cols <= 512) EHIP_LNW(8, false);
+        else if (cols <= 1024) EHIP_LNW(16, false);
+        else EHIP_LNW(32, false);
+#undef EHIP_LNW
+        constexpr int kCols = 256 / kParamLanes;
+        EHIP_LAUNCH("layernorm_param_grads", layernorm_param_grads,
+                    dim3(unsigned(ceil_div(2 * cols, kCols))), dim3(256), 0, s, partial, dgamma,
+                    dbeta, groups, cols);
+        return EHIP_OK;
+    }
+    // Small problems: one wave per group of about 16 rows (at most 512 groups).
     int64_t groups = ceil_div(rows, 16);
     if (groups > 512) groups = 512;
     if (groups < 1) groups = 1;
-    groups = ceil_div(groups, per_block) * per_block;
-    const unsigned grid = unsigned(groups / per_block);
+    const unsigned grid = unsigned(groups);
     float* partial = static_cast<float*>(scratch(size_t(groups) * 2 * size_t(cols) * sizeof(float)));
     if (partial == nullptr) return EHIP_ENOMEM;
-#define EHIP_LNB(T, V)                                                                          \
-    EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward<T, V>), dim3(grid),              \
-                dim3(Group<T>::kBlock), 0, s, dy, xhat, gamma, inv_std, dx, partial, rows, cols)
-    if (cols <= 64) EHIP_LNB(64, 1);
-    else if (cols <= 128) EHIP_LNB(64, 2);
-    else if (cols <= 256) EHIP_LNB(64, 4);
-    else if (cols <= 512) EHIP_LNB(64, 8);
-    else if (cols <= 1024) EHIP_LNB(64, 16);
-    else if (cols <= 2048) EHIP_LNB(64, 32);
-    else if (cols <= 4096) EHIP_LNB(256, 16);
-    else EHIP_LNB(256, 32);
+#define EHIP_LNB(T, V, VEC)                                                                     \
+    EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward<T, V, VEC>), dim3(grid),         \
+                dim3(T), 0, s, dy, xhat, gamma, inv_std, dx, partial, rows, cols)
+    if (vec) {
+        if (cols <= 256) EHIP_LNB(64, 4, true);
+        else if (cols <= 512) EHIP_LNB(64, 8, true);
+        else if (cols <= 1024) EHIP_LNB(64, 16, true);
+        else if (cols <= 2048) EHIP_LNB(64, 32, true);
+        else if (cols <= 4096) EHIP_LNB(256, 16, true);
+        else EHIP_LNB(256, 32, true);
+    } else if (cols <= 64) EHIP_LNB(64, 1, false);
+    else if (cols <= 128) EHIP_LNB(64, 2, false);
+    else if (cols <= 256) EHIP_LNB(64, 4, false);
+    else if (cols <= 512) EHIP_LNB(64, 8, false);
+    else if (cols <= 1024) EHIP_LNB(64, 16, false);
+    else if (cols <= 2048) EHIP_LNB(64, 32, false);
+    else if (cols <= 4096) EHIP_LNB(256, 16, false);
+    else EHIP_LNB(256, 32, false);
 #undef EHIP_LNB
     if (int rc = column_sums(partial, 1, groups, cols, 2 * cols, 0, dgamma, s)) return rc;
     return column_sums(partial + cols, 1, groups, cols, 2 * cols, 0, dbeta, s);

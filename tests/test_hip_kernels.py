@@ -484,7 +484,10 @@ def test_conv2d_direct_refuses_wide_layers(hip):
 
 
 @pytest.mark.parametrize("shape,k,stride", [((64, 8, 28, 28), 2, 2), ((64, 16, 14, 14), 2, 2),
-                                            ((2, 3, 9, 9), 3, 2), ((2, 2, 7, 7), 3, 1)])
+                                            ((2, 3, 9, 9), 3, 2), ((2, 2, 7, 7), 3, 1),
+                                            ((2, 3, 9, 7), 2, 2), ((1, 2, 10, 11), 3, 3),
+                                            ((3, 1, 5, 5), 5, 5), ((4, 4, 13, 6), 2, 2),
+                                            ((8, 64, 112, 112), 2, 2)])
 @pytest.mark.parametrize("float_index", [False, True])
 def test_maxpool_exact(hip, orc, shape, k, stride, float_index):
     """Overlapping windows and ties included: the first strict maximum wins. The
@@ -497,6 +500,25 @@ def test_maxpool_exact(hip, orc, shape, k, stride, float_index):
     exact(host(Y), y, "max")
     exact(host(AM), am.astype(np.float32) if float_index else am, "argmax")
     g = randn(r, *y.shape)
+    exact(host(hip.maxpool_backward(AM, dev(g), shape, k, stride)),
+          orc.maxpool_backward(am, g, shape), "maxpool backward")
+
+
+@pytest.mark.parametrize("shape,k,stride", [((2, 3, 9, 7), 2, 2), ((2, 2, 7, 7), 3, 1)])
+def test_maxpool_nan_and_signed_zero(hip, orc, shape, k, stride):
+    """NaN inputs and -0 gradients on both kernel paths (non-overlapping tiles and
+    general windows) against the reference's comparisons."""
+    print_case("maxpool nan", shape, k, stride)
+    r = rng(7 + sum(shape))
+    x = np.round(randn(r, *shape) * 2) / 2
+    x.ravel()[::5] = np.nan
+    x.ravel()[1::7] = -0.0
+    y, am = orc.maxpool(x, k, stride)
+    Y, AM = hip.maxpool(dev(x), k, stride)
+    exact(host(Y), y, "max")
+    exact(host(AM), am, "argmax")
+    g = randn(r, *y.shape)
+    g.ravel()[::3] = -0.0
     exact(host(hip.maxpool_backward(AM, dev(g), shape, k, stride)),
           orc.maxpool_backward(am, g, shape), "maxpool backward")
 
@@ -545,6 +567,25 @@ def test_sum_axis(hip, orc, outer, axis_len, inner):
         ref_close(got, want, k_tol(axis_len), "chunked sum_axis")
 
 
+@pytest.mark.parametrize("outer,axis_len,inner", [(1, 8192, 4096), (1, 1000, 256), (3, 500, 1024),
+                                                  (1, 777, 260), (2, 4000, 512)])
+def test_sum_axis_vector_path_bitexact(hip, orc, outer, axis_len, inner):
+    """The float4 column-sum kernel adds every column in the same order as the
+    scalar one: an aligned input (vector path) and the same values at a
+    misaligned address (scalar path) give the same bits."""
+    print_case("sum_axis vector", outer, axis_len, inner)
+    x = randn(rng(axis_len + inner), outer, axis_len, inner)
+    flat = np.concatenate([np.zeros(1, np.float32), x.ravel()])
+    buf = dev(flat)
+    mis = buf[1:]  # 4 bytes past a 16-byte boundary
+    al = dev(x.ravel())
+    got_vec = host(hip.sum_axis(al, outer, axis_len, inner))
+    got_sca = host(hip.sum_axis(mis, outer, axis_len, inner))
+    exact(got_vec, got_sca, "vector vs scalar column sums")
+    want = orc.sum_axis(x, 1).reshape(-1)
+    ref_close(got_vec, want, k_tol(axis_len), "sum_axis vs oracle")
+
+
 @pytest.mark.parametrize("n", [1, 1000, 1 << 20])
 def test_reduce_sum(hip, orc, n):
     print_case("reduce_sum", n)
@@ -579,7 +620,10 @@ def test_softmax(hip, orc, rows, cols):
               "softmax backward")
 
 
-@pytest.mark.parametrize("rows,d", [(2048, 96), (512, 64), (7, 1024), (33, 100), (4, 3000)])
+@pytest.mark.parametrize("rows,d", [(2048, 96), (512, 64), (7, 1024), (33, 100), (4, 3000),
+                                   (8192, 1024), (300, 260), (64, 4096), (16, 8192),
+                                   (2048, 512), (9000, 256), (5000, 257), (700, 2048),
+                                   (600, 2000), (20000, 100)])
 def test_layernorm(hip, orc, rows, d):
     print_case("layernorm", rows, d)
     r = rng(rows + d)
