@@ -55,8 +55,9 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
     splits = int(ceil_div(g.k, g.k_chunk));
     g.splits = splits;
     float* out = g.c;
+    g.ws_stride = batch * g.m * g.n + (g.colsum ? g.n : 0);
     if (splits > 1) {
-        float* ws = static_cast<float*>(scratch(size_t(splits) * batch * g.m * g.n * sizeof(float)));
+        float* ws = static_cast<float*>(scratch(size_t(splits) * size_t(g.ws_stride) * sizeof(float)));
         if (ws == nullptr) return EHIP_ENOMEM;
         g.c = ws;
     }
@@ -80,10 +81,12 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
         // is longer than ~8 loads deep when the outputs are few.
         int rl = 1;
         while (rl < 16 && rl * 8 < splits) rl *= 2;
-        const int64_t total = batch * g.m * g.n;
+        const int64_t total = g.ws_stride;  // C partials, then the column sums
         const int64_t per_block = 256 / rl;
+        GemmArgs gr = g0;  // the caller's output and epilogue, the workspace geometry
+        gr.ws_stride = g.ws_stride;
         EHIP_LAUNCH("gemm_splitk_reduce", splitk_reduce,
-                    dim3(unsigned(ceil_div(total, per_block))), dim3(256), 0, s, g.c, out, g0,
+                    dim3(unsigned(ceil_div(total, per_block))), dim3(256), 0, s, g.c, out, gr,
                     batch, splits, rl);
     }
     return EHIP_OK;
@@ -278,6 +281,17 @@ int gemm_run(const ehip_gemm_ex_t& d, hipStream_t s) {
     // K = 0 (only reached from the extended entry point): acc = 0, then the
     // epilogue, through the thread-per-output kernel.
     const int kind = d.k == 0 ? 1 : small_kind(batch, d.m, d.n, d.k);
+    if (kind != 0 && d.colsum_b != nullptr) {
+        // The vector kernels do not stage B: its column sums are a reduction
+        // of their own (zero for K = 0).
+        if (d.k == 0) {
+            if (int rc = ehip_fill_f32(d.colsum_b, d.n, 0.0f, s)) return rc;
+        } else if (int rc = column_sums(d.b, 1, d.k, d.n, d.ldb, 0, d.colsum_b, s)) {
+            return rc;
+        }
+    } else {
+        g.colsum = d.colsum_b;
+    }
     if (kind != 0) {
         const bool wave = kind == 2;
         if (!ta && !tb) return gemm_small<false, false>(g, batch, wave, s);
@@ -304,6 +318,8 @@ int check_desc(const ehip_gemm_ex_t& d) {
     if (d.inner < 1) return fail(EHIP_EINVAL, "gemm: inner batch count %lld < 1", (long long)d.inner);
     if (d.addend && (d.ld_addend < 0 || d.stride_addend < 0 || d.addend_period < 1))
         return fail(EHIP_EINVAL, "gemm: bad addend geometry");
+    if (d.colsum_b && (d.batch != 1 || d.trans_b))
+        return fail(EHIP_EINVAL, "gemm: column sums need batch 1 and a K x N B");
     if (d.batch > 65535) return fail(EHIP_EINVAL, "gemm: batch %lld > 65535", (long long)d.batch);
     if (d.m > (int64_t(1) << 31) || d.n > (int64_t(1) << 31))
         return fail(EHIP_EINVAL, "gemm: extent beyond 2^31");

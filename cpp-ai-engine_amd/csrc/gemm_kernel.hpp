@@ -30,6 +30,11 @@ struct GemmArgs {
     int64_t ld_add, stride_add, add_period;
     float beta;
     int relu;  // then v = max(0, v)
+    // colsum[j] = sum over k of op(B)[k][j] (batch 1), made by the first
+    // tile-row's workgroups from the B tiles they stage anyway; with split K
+    // each split's sums go after its C partials and the reduction adds them.
+    float* colsum;
+    int64_t ws_stride;  // split-K workspace floats per split
     int tiles_m, tiles_n;
     int splits;        // K is cut into `splits` chunks of k_chunk (a multiple of BK)
     int64_t k_chunk;
@@ -189,6 +194,8 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
 
     float4 ra[C::kALoads], rb[C::kBLoads];
     const int64_t steps = (k_end - k_begin + BK - 1) / BK;
+    const bool colsum_tile = g.colsum != nullptr && tm == 0;
+    float csum = 0.0f;
     if (steps > 0) {
         load_tile<C, BM, BK, TA, CHECK>(A, g.lda, g.m, k_end, m0, k_begin, ra, C::kALoads, C::kA4, g.vec);
         load_tile<C, BN, BK, !TB, CHECK>(B, g.ldb, g.n, k_end, n0, k_begin, rb, C::kBLoads, C::kB4, g.vec);
@@ -236,6 +243,14 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
                                                                      0, 0, 0);
             if (C::kPrio) __builtin_amdgcn_s_setprio(0);
         }
+        if (colsum_tile && threadIdx.x < BN) {
+            // This K step's B rows, in k order, for column n0 + threadIdx.x.
+            const float* col = lds_b[cur] + threadIdx.x;
+            float part = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < BK; ++kk) part += col[kk * C::kLdsB];
+            csum = csum + part;
+        }
         if (more) {
             store_tile<C, BM, BK, C::kLdsA, TA>(lds_a[cur ^ 1], ra, C::kALoads, C::kA4);
             store_tile<C, BN, BK, C::kLdsB, !TB>(lds_b[cur ^ 1], rb, C::kBLoads, C::kB4);
@@ -243,12 +258,20 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
         __syncthreads();
     }
 
-    // Epilogue. With splits > 1, c is the workspace [split][batch][m][n] and
-    // the epilogue is applied by the reduction kernel.
+    if (colsum_tile && threadIdx.x < BN && n0 + threadIdx.x < g.n) {
+        if (g.splits > 1)
+            g.c[int64_t(split) * g.ws_stride + g.m * g.n + n0 + threadIdx.x] = csum;
+        else
+            g.colsum[n0 + threadIdx.x] = csum;
+    }
+
+    // Epilogue. With splits > 1, c is the workspace [split][batch][m][n]
+    // (ws_stride floats per split) and the epilogue is applied by the
+    // reduction kernel.
     float* Cp;
     int64_t ldc;
     if (g.splits > 1) {
-        Cp = g.c + (int64_t(split) * gridDim.z + batch) * g.m * g.n;
+        Cp = g.c + int64_t(split) * g.ws_stride + batch * g.m * g.n;
         ldc = g.n;
     } else {
         Cp = g.c + batch_offset(batch, g.inner, g.stride_c, g.stride_c2);
@@ -297,12 +320,13 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
         }
 }
 
-// C[b] = sum over splits of W[s][b] (+ beta C[b]). A block is RL split lanes x
-// (256 / RL) outputs: lane l adds splits l, l + RL, ... in order, then one
-// thread per output adds the RL lane sums in lane order. RL grows with the
-// number of splits, so a few outputs with many splits still spread over the
-// block instead of one long serial chain per output; the order depends only
-// on the shape.
+// C[b] = sum over splits of W[s][b], then the epilogue; with a column sum,
+// the n values after each split's C partials are summed the same way into
+// colsum. A block is RL split lanes x (256 / RL) outputs: lane l adds splits
+// l, l + RL, ... in order, then one thread per output adds the lanes in
+// order. RL grows with the number of splits, so a few outputs with many
+// splits still spread over the block instead of one long serial chain per
+// output; the order depends only on the shape.
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w, float* c,
                                                      GemmArgs g, int64_t batch, int splits,
                                                      int rl) {
@@ -312,9 +336,10 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
     const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
     const int64_t mn = m * n;
     const int64_t e = int64_t(blockIdx.x) * cw + cl;
-    const int64_t step = batch * mn;
+    const int64_t step = g.ws_stride;
+    const int64_t outputs = batch * mn + (g.colsum ? n : 0);
     float acc = 0.0f;
-    if (e < step && lane < splits) {
+    if (e < outputs && lane < splits) {
         const float* p = w + e + int64_t(lane) * step;
         const int64_t stride = int64_t(rl) * step;
         const int count = (splits - lane + rl - 1) / rl;
@@ -331,9 +356,13 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
     }
     lanes[threadIdx.x] = acc;
     __syncthreads();
-    if (lane == 0 && e < step) {
+    if (lane == 0 && e < outputs) {
         float sum = lanes[cl];
         for (int l = 1; l < rl && l < splits; ++l) sum += lanes[l * cw + cl];
+        if (e >= batch * mn) {
+            g.colsum[e - batch * mn] = sum;
+            return;
+        }
         const int64_t b = e / mn, rc = e % mn;
         const int64_t row = rc / n, col = rc % n;
         float* dst = c + batch_offset(b, g.inner, g.stride_c, g.stride_c2) + row * g.ldc + col;

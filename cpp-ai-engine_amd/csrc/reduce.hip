@@ -54,30 +54,76 @@ __global__ __launch_bounds__(kThreads) void sum_axis_serial(const float* __restr
 // two)); block (b, t, o) covers rows [b*rpb, (b+1)*rpb) and columns
 // [t*CW, (t+1)*CW) of slab o. Lane l adds rows r0+l, r0+l+RL, ... in order;
 // then one thread per column adds the RL lane sums in lane order. The order
-// depends only on the shape.
-__global__ __launch_bounds__(kThreads) void sum_cols(const float* __restrict__ x,
-                                                     float* __restrict__ out, int64_t rows,
-                                                     int64_t cols, int64_t ld, int64_t rpb,
-                                                     int64_t x_slab, int64_t out_slab, int cw) {
-    __shared__ float lanes[kThreads];
+// depends only on the shape. Returns the sum in the lane-0 threads.
+__device__ __forceinline__ float block_rows_sum(const float* __restrict__ xs, int64_t r0,
+                                                int64_t r1, int64_t c, int64_t cols, int64_t ld,
+                                                int cw, float* lanes) {
     const int rl = kThreads / cw;
     const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
-    const int64_t c = int64_t(blockIdx.y) * cw + cl;
-    const int64_t r0 = int64_t(blockIdx.x) * rpb;
-    int64_t r1 = r0 + rpb;
-    if (r1 > rows) r1 = rows;
-    const float* xs = x + int64_t(blockIdx.z) * x_slab;
     float acc = 0.0f;
     if (c < cols && r0 + lane < r1)
         acc = ordered_sum(0.0f, xs + (r0 + lane) * ld + c, (r1 - r0 - lane + rl - 1) / rl,
                           int64_t(rl) * ld);
     lanes[threadIdx.x] = acc;
     __syncthreads();
-    if (lane == 0 && c < cols) {
-        float s = 0.0f;
+    float s = 0.0f;
+    if (lane == 0)
         for (int l = 0; l < rl; ++l) s += lanes[l * cw + cl];
+    __syncthreads();  // lanes may be reused
+    return s;
+}
+
+__global__ __launch_bounds__(kThreads) void sum_cols(const float* __restrict__ x,
+                                                     float* __restrict__ out, int64_t rows,
+                                                     int64_t cols, int64_t ld, int64_t rpb,
+                                                     int64_t x_slab, int64_t out_slab, int cw) {
+    __shared__ float lanes[kThreads];
+    const int64_t c = int64_t(blockIdx.y) * cw + threadIdx.x % cw;
+    const int64_t r0 = int64_t(blockIdx.x) * rpb;
+    const int64_t r1 = r0 + rpb < rows ? r0 + rpb : rows;
+    const float s = block_rows_sum(x + int64_t(blockIdx.z) * x_slab, r0, r1, c, cols, ld, cw, lanes);
+    if (threadIdx.x < cw && c < cols)
         out[int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c] = s;
+}
+
+// Arrival counters of the one-launch column sums, one per (column tile,
+// slab). Zero when the module loads; the last block of each tile returns its
+// counter to zero, so every launch finds them at zero.
+constexpr int kArrivalCounters = 4096;
+__device__ unsigned int g_arrivals[kArrivalCounters];
+
+// True in every thread of the block that arrives last at its tile's counter
+// (after every block of the tile has written its partial sums).
+__device__ __forceinline__ bool last_arrival(int64_t blocks) {
+    __shared__ bool last;
+    __threadfence();  // this block's partials are visible before it arrives
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned int* ctr = &g_arrivals[blockIdx.z * gridDim.y + blockIdx.y];
+        last = atomicAdd(ctr, 1u) == unsigned(blocks - 1);
+        if (last) atomicExch(ctr, 0u);
     }
+    __syncthreads();
+    if (last) __threadfence();  // and the other blocks' partials to this one
+    return last;
+}
+
+// Both passes of column_sums in one launch: every block writes its partial
+// sums as the first pass does; the tile's last block then adds the partials
+// exactly as the second pass does. Same order, same bits, one launch.
+__global__ __launch_bounds__(kThreads) void sum_cols_onepass(
+    const float* __restrict__ x, float* __restrict__ out, float* partial, int64_t rows,
+    int64_t cols, int64_t ld, int64_t rpb, int64_t x_slab, int64_t blocks, int cw) {
+    __shared__ float lanes[kThreads];
+    const int64_t c = int64_t(blockIdx.y) * cw + threadIdx.x % cw;
+    const int64_t r0 = int64_t(blockIdx.x) * rpb;
+    const int64_t r1 = r0 + rpb < rows ? r0 + rpb : rows;
+    const float s = block_rows_sum(x + int64_t(blockIdx.z) * x_slab, r0, r1, c, cols, ld, cw, lanes);
+    float* ps = partial + int64_t(blockIdx.z) * blocks * cols;
+    if (threadIdx.x < cw && c < cols) ps[int64_t(blockIdx.x) * cols + c] = s;
+    if (!last_arrival(blocks)) return;
+    const float t = block_rows_sum(ps, 0, blocks, c, cols, cols, cw, lanes);
+    if (threadIdx.x < cw && c < cols) out[int64_t(blockIdx.z) * cols + c] = t;
 }
 
 // sum_cols for CW = 64 with four adjacent columns per thread (float4 loads,
@@ -103,33 +149,57 @@ __device__ __forceinline__ float4 ordered_sum4(const float* __restrict__ p, int6
     return acc;
 }
 
-__global__ __launch_bounds__(kThreads) void sum_cols4(const float* __restrict__ x,
-                                                      float* __restrict__ out, int64_t rows,
-                                                      int64_t cols, int64_t ld, int64_t rpb,
-                                                      int64_t x_slab, int64_t out_slab) {
+__device__ __forceinline__ float4 block_rows_sum4(const float* __restrict__ xs, int64_t r0,
+                                                  int64_t r1, int64_t c, int64_t cols, int64_t ld,
+                                                  float4* lanes) {
     constexpr int kCw = 64, kRl = kThreads / kCw;
-    __shared__ float4 lanes[kThreads];
     const int lane = threadIdx.x / kCw, cl = threadIdx.x % kCw;
-    const int64_t c = (int64_t(blockIdx.y) * kCw + cl) * 4;
-    const int64_t r0 = int64_t(blockIdx.x) * rpb;
-    int64_t r1 = r0 + rpb;
-    if (r1 > rows) r1 = rows;
-    const float* xs = x + int64_t(blockIdx.z) * x_slab;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (c < cols && r0 + lane < r1)
         acc = ordered_sum4(xs + (r0 + lane) * ld + c, (r1 - r0 - lane + kRl - 1) / kRl,
                            int64_t(kRl) * ld);
     lanes[threadIdx.x] = acc;
     __syncthreads();
-    if (lane == 0 && c < cols) {
-        float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (lane == 0)
         for (int l = 0; l < kRl; ++l) sum = add4(sum, lanes[l * kCw + cl]);
-        float* o = out + int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c;
-        o[0] = sum.x;
-        o[1] = sum.y;
-        o[2] = sum.z;
-        o[3] = sum.w;
-    }
+    __syncthreads();
+    return sum;
+}
+
+__device__ __forceinline__ void store4(float* o, float4 v) {
+    o[0] = v.x;
+    o[1] = v.y;
+    o[2] = v.z;
+    o[3] = v.w;
+}
+
+__global__ __launch_bounds__(kThreads) void sum_cols4(const float* __restrict__ x,
+                                                      float* __restrict__ out, int64_t rows,
+                                                      int64_t cols, int64_t ld, int64_t rpb,
+                                                      int64_t x_slab, int64_t out_slab) {
+    __shared__ float4 lanes[kThreads];
+    const int64_t c = (int64_t(blockIdx.y) * 64 + threadIdx.x % 64) * 4;
+    const int64_t r0 = int64_t(blockIdx.x) * rpb;
+    const int64_t r1 = r0 + rpb < rows ? r0 + rpb : rows;
+    const float4 s = block_rows_sum4(x + int64_t(blockIdx.z) * x_slab, r0, r1, c, cols, ld, lanes);
+    if (threadIdx.x < 64 && c < cols)
+        store4(out + int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c, s);
+}
+
+__global__ __launch_bounds__(kThreads) void sum_cols4_onepass(
+    const float* __restrict__ x, float* __restrict__ out, float* partial, int64_t rows,
+    int64_t cols, int64_t ld, int64_t rpb, int64_t x_slab, int64_t blocks) {
+    __shared__ float4 lanes[kThreads];
+    const int64_t c = (int64_t(blockIdx.y) * 64 + threadIdx.x % 64) * 4;
+    const int64_t r0 = int64_t(blockIdx.x) * rpb;
+    const int64_t r1 = r0 + rpb < rows ? r0 + rpb : rows;
+    const float4 s = block_rows_sum4(x + int64_t(blockIdx.z) * x_slab, r0, r1, c, cols, ld, lanes);
+    float* ps = partial + int64_t(blockIdx.z) * blocks * cols;
+    if (threadIdx.x < 64 && c < cols) store4(ps + int64_t(blockIdx.x) * cols + c, s);
+    if (!last_arrival(blocks)) return;
+    const float4 t = block_rows_sum4(ps, 0, blocks, c, cols, cols, lanes);
+    if (threadIdx.x < 64 && c < cols) store4(out + int64_t(blockIdx.z) * cols + c, t);
 }
 
 // Whole-buffer sum in double: a fixed grid of blocks, each thread striding by
@@ -175,8 +245,9 @@ __global__ __launch_bounds__(kThreads) void reduce_stage2(const double* __restri
 }  // namespace
 
 // Two passes of sum_cols: row blocks into partials, then the partials of each
-// slab. The row blocks are sized so that the first pass has about a thousand
-// workgroups and the second adds at most 64 partials per lane.
+// slab (both in one launch of sum_cols_onepass when the tiles have arrival
+// counters). The row blocks are sized so that the first pass has about a
+// thousand workgroups and the second adds at most 64 partials per lane.
 int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
                 int64_t x_slab, float* out, hipStream_t s) {
     if (slabs == 0 || cols == 0) return EHIP_OK;
@@ -210,6 +281,19 @@ int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64
     float* partial =
         static_cast<float*>(scratch(size_t(slabs * blocks * cols) * sizeof(float), 1));
     if (partial == nullptr) return EHIP_ENOMEM;
+    // Both passes in one launch while there is an arrival counter per tile.
+    if ((vec ? int64_t(tiles4) : tiles) * slabs <= kArrivalCounters) {
+        if (vec) {
+            EHIP_LAUNCH("column_sums", sum_cols4_onepass,
+                        dim3(unsigned(blocks), tiles4, unsigned(slabs)), dim3(kThreads), 0, s, x,
+                        out, partial, rows, cols, ld, rpb, x_slab, blocks);
+        } else {
+            EHIP_LAUNCH("column_sums", sum_cols_onepass,
+                        dim3(unsigned(blocks), unsigned(tiles), unsigned(slabs)), dim3(kThreads), 0,
+                        s, x, out, partial, rows, cols, ld, rpb, x_slab, blocks, cw);
+        }
+        return EHIP_OK;
+    }
     if (vec) {
         EHIP_LAUNCH("column_sums_blocks", sum_cols4, dim3(unsigned(blocks), tiles4, unsigned(slabs)),
                     dim3(kThreads), 0, s, x, partial, rows, cols, ld, rpb, x_slab, blocks * cols);

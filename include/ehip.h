@@ -167,6 +167,12 @@ int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
  * addend with ld_addend 0 is Linear's broadcast bias add (src/nn.cpp:119-122).
  * Then, when relu != 0, c = (0 < c) ? c : 0, std::max(0.0f, c) of
  * Tensor::relu (src/tensor_ops.cpp:591-600).
+ * colsum_b, when not NULL (batch 1, trans_b 0), receives the n column sums
+ * of B over its k rows -- for dW = X^T dY the bias gradient sum_rows(dY) of
+ * Linear's broadcast add (src/tensor_ops.cpp:81-102 through fold_leading,
+ * src/tensor_detail.hpp:182-206) -- made from the B tiles the product stages
+ * anyway: fixed order (k within each K step, the steps, then the K splits),
+ * deterministic, within the K-term tolerance of the reference's serial sum.
  * addend_period >= 1; consecutive addend matrices are stride_addend apart
  * (stride_addend 0 broadcasts one mask over every product, ld_addend 0 one
  * row over every row). inner >= 1. With k == 0, acc is 0 and the epilogue
@@ -186,6 +192,7 @@ typedef struct {
     int64_t ld_addend, stride_addend, addend_period;
     float beta;
     int relu;
+    float* colsum_b;
 } ehip_gemm_ex_t;
 
 int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream);

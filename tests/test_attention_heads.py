@@ -329,3 +329,47 @@ def test_charlm_training_fused_equals_composed(eng):
                                                             layers, params, 5, 1e-3))
     exact(fused[0], comp[0], "losses")
     exact(fused[1], comp[1], "weights")
+
+
+# ------------------------------------------------------- bias gradient from the dW product
+
+@pytest.mark.parametrize("m,n,k", [(96, 96, 2048), (1024, 1024, 8192), (1024, 4096, 8192),
+                                   (100, 257, 3000), (784, 10, 64), (384, 96, 2048),
+                                   (4096, 1024, 8192)])
+def test_colsum_from_dw_product(hip, m, n, k):
+    """dW = X^T dY with colsum_b: the product is unchanged bit for bit, the
+    column sums of dY match fp64 within the K-term tolerance and repeat
+    exactly (split-K, unsplit, edge tiles, and the vector-kernel fallback)."""
+    print_case("gemm_ex colsum", m, n, k)
+    r = np.random.default_rng(m + n + k)
+    x, g = dev(randn(r, k, m)), dev(randn(r, k, n))
+    plain = hip.gemm(x, g, trans_a=True)
+    c, cs = hip.f32((m, n)), hip.f32((n,))
+    d = desc(hip, True, False, 1, 1, m, n, k, x, m, 0, 0, g, n, 0, 0, c, n, 0, 0)
+    d.colsum_b = hip.p(cs)
+    hip.gemm_ex(d)
+    exact(host(c), host(plain), "product with column sums")
+    want = host(g).astype(np.float64).sum(axis=0)
+    ref_close(host(cs), want, 4 * k_tol(k), "column sums")
+    first = host(cs).copy()
+    hip.gemm_ex(d)
+    exact(host(cs), first, "column sums repeat")
+
+
+def test_colsum_refusals_and_k_zero(hip):
+    print_case("gemm_ex colsum refusals")
+    x = dev(np.ones((4, 4), np.float32))
+    cs = dev(np.full(4, 7.0, np.float32))
+    d = desc(hip, False, True, 1, 1, 4, 4, 4, x, 4, 0, 0, x, 4, 0, 0, hip.f32((4, 4)), 4, 0, 0)
+    d.colsum_b = hip.p(cs)
+    with pytest.raises(RuntimeError):  # B stored N x K
+        hip.gemm_ex(d)
+    d = desc(hip, False, False, 2, 1, 4, 4, 4, x, 4, 0, 0, x, 4, 0, 0, hip.f32((2, 4, 4)), 4, 16, 0)
+    d.colsum_b = hip.p(cs)
+    with pytest.raises(RuntimeError):  # batched
+        hip.gemm_ex(d)
+    c = hip.f32((4, 4))
+    d = desc(hip, False, False, 1, 1, 4, 4, 0, x, 1, 0, 0, x, 4, 0, 0, c, 4, 0, 0)
+    d.colsum_b = hip.p(cs)
+    hip.gemm_ex(d)
+    exact(host(cs), np.zeros(4, np.float32), "k = 0 column sums")

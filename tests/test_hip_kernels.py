@@ -586,6 +586,56 @@ def test_sum_axis_vector_path_bitexact(hip, orc, outer, axis_len, inner):
     ref_close(got_vec, want, k_tol(axis_len), "sum_axis vs oracle")
 
 
+def column_sums_emulated(x3):
+    """The fixed summation order of the device column sums (reduce.hip), restated
+    in float32 numpy for x3 (slabs, rows, cols): row blocks of rpb rows, row lanes
+    l, l + RL, ... within a block, lanes added in order, then the block partials
+    the same way."""
+    slabs, rows, cols = x3.shape
+    cw = 1
+    while cw < cols and cw < 64:
+        cw *= 2
+    tiles = -(-cols // cw)
+    rl = 256 // cw
+    blocks = -(-1024 // (tiles * slabs))
+    blocks = max(1, min(blocks, -(-rows // (2 * rl)), 64 * rl))
+    rpb = -(-rows // blocks)
+    blocks = -(-rows // rpb)
+
+    def block_sum(m, r0, r1):
+        s = np.zeros(m.shape[1:], np.float32)
+        for lane in range(rl):
+            acc = np.zeros(m.shape[1:], np.float32)
+            for r in range(r0 + lane, r1, rl):
+                acc = acc + m[r]
+            s = s + acc
+        return s
+
+    out = np.empty((slabs, cols), np.float32)
+    for z in range(slabs):
+        if blocks == 1:
+            out[z] = block_sum(x3[z], 0, rows)
+            continue
+        part = np.stack([block_sum(x3[z], b * rpb, min(rows, (b + 1) * rpb)) for b in range(blocks)])
+        out[z] = block_sum(part, 0, blocks)
+    return out
+
+
+@pytest.mark.parametrize("outer,axis_len,inner", [(1, 2048, 96), (1, 8192, 1024), (1, 8192, 4096),
+                                                  (1, 777, 260), (1, 3000, 121), (1, 100, 5),
+                                                  (3, 500, 1024), (5000, 100, 1)])
+def test_column_sums_order_exact(hip, outer, axis_len, inner):
+    """The one-launch column sums (arrival counter) and the two-launch fallback
+    (more tiles than counters, here 5000 slabs) give exactly the blocked order
+    restated above."""
+    print_case("column sums order", outer, axis_len, inner)
+    x = randn(rng(axis_len * 3 + inner), outer, axis_len, inner)
+    got = host(hip.sum_axis(dev(x), outer, axis_len, inner)).reshape(outer, inner)
+    exact(got, column_sums_emulated(x), "column sums")
+    again = host(hip.sum_axis(dev(x), outer, axis_len, inner)).reshape(outer, inner)
+    exact(again, got, "column sums repeat")
+
+
 @pytest.mark.parametrize("n", [1, 1000, 1 << 20])
 def test_reduce_sum(hip, orc, n):
     print_case("reduce_sum", n)
