@@ -86,46 +86,6 @@ __global__ __launch_bounds__(kThreads) void sum_cols(const float* __restrict__ x
         out[int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c] = s;
 }
 
-// Arrival counters of the one-launch column sums, one per (column tile,
-// slab). Zero when the module loads; the last block of each tile returns its
-// counter to zero, so every launch finds them at zero.
-constexpr int kArrivalCounters = 4096;
-__device__ unsigned int g_arrivals[kArrivalCounters];
-
-// True in every thread of the block that arrives last at its tile's counter
-// (after every block of the tile has written its partial sums).
-__device__ __forceinline__ bool last_arrival(int64_t blocks) {
-    __shared__ bool last;
-    __threadfence();  // this block's partials are visible before it arrives
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned int* ctr = &g_arrivals[blockIdx.z * gridDim.y + blockIdx.y];
-        last = atomicAdd(ctr, 1u) == unsigned(blocks - 1);
-        if (last) atomicExch(ctr, 0u);
-    }
-    __syncthreads();
-    if (last) __threadfence();  // and the other blocks' partials to this one
-    return last;
-}
-
-// Both passes of column_sums in one launch: every block writes its partial
-// sums as the first pass does; the tile's last block then adds the partials
-// exactly as the second pass does. Same order, same bits, one launch.
-__global__ __launch_bounds__(kThreads) void sum_cols_onepass(
-    const float* __restrict__ x, float* __restrict__ out, float* partial, int64_t rows,
-    int64_t cols, int64_t ld, int64_t rpb, int64_t x_slab, int64_t blocks, int cw) {
-    __shared__ float lanes[kThreads];
-    const int64_t c = int64_t(blockIdx.y) * cw + threadIdx.x % cw;
-    const int64_t r0 = int64_t(blockIdx.x) * rpb;
-    const int64_t r1 = r0 + rpb < rows ? r0 + rpb : rows;
-    const float s = block_rows_sum(x + int64_t(blockIdx.z) * x_slab, r0, r1, c, cols, ld, cw, lanes);
-    float* ps = partial + int64_t(blockIdx.z) * blocks * cols;
-    if (threadIdx.x < cw && c < cols) ps[int64_t(blockIdx.x) * cols + c] = s;
-    if (!last_arrival(blocks)) return;
-    const float t = block_rows_sum(ps, 0, blocks, c, cols, cols, cw, lanes);
-    if (threadIdx.x < cw && c < cols) out[int64_t(blockIdx.z) * cols + c] = t;
-}
-
 // sum_cols for CW = 64 with four adjacent columns per thread (float4 loads,
 // 1 KiB per wave and row instead of 256 bytes): the same row lanes, rows per
 // lane and order per column as sum_cols, so the sums are bit-identical.
@@ -187,21 +147,6 @@ __global__ __launch_bounds__(kThreads) void sum_cols4(const float* __restrict__ 
         store4(out + int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c, s);
 }
 
-__global__ __launch_bounds__(kThreads) void sum_cols4_onepass(
-    const float* __restrict__ x, float* __restrict__ out, float* partial, int64_t rows,
-    int64_t cols, int64_t ld, int64_t rpb, int64_t x_slab, int64_t blocks) {
-    __shared__ float4 lanes[kThreads];
-    const int64_t c = (int64_t(blockIdx.y) * 64 + threadIdx.x % 64) * 4;
-    const int64_t r0 = int64_t(blockIdx.x) * rpb;
-    const int64_t r1 = r0 + rpb < rows ? r0 + rpb : rows;
-    const float4 s = block_rows_sum4(x + int64_t(blockIdx.z) * x_slab, r0, r1, c, cols, ld, lanes);
-    float* ps = partial + int64_t(blockIdx.z) * blocks * cols;
-    if (threadIdx.x < 64 && c < cols) store4(ps + int64_t(blockIdx.x) * cols + c, s);
-    if (!last_arrival(blocks)) return;
-    const float4 t = block_rows_sum4(ps, 0, blocks, c, cols, cols, lanes);
-    if (threadIdx.x < 64 && c < cols) store4(out + int64_t(blockIdx.z) * cols + c, t);
-}
-
 // Whole-buffer sum in double: a fixed grid of blocks, each thread striding by
 // the grid, then a fixed-shape tree per block.
 constexpr int kReduceBlocks = 512;
@@ -245,9 +190,10 @@ __global__ __launch_bounds__(kThreads) void reduce_stage2(const double* __restri
 }  // namespace
 
 // Two passes of sum_cols: row blocks into partials, then the partials of each
-// slab (both in one launch of sum_cols_onepass when the tiles have arrival
-// counters). The row blocks are sized so that the first pass has about a
-// thousand workgroups and the second adds at most 64 partials per lane.
+// slab. The row blocks are sized so that the first pass has about a thousand
+// workgroups and the second adds at most 64 partials per lane. (One launch
+// with a last-block-adds pattern measured 25 us instead of 2 x 3: making the
+// partials visible across the XCDs' L2 caches costs an L2 write-back.)
 int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
                 int64_t x_slab, float* out, hipStream_t s) {
     if (slabs == 0 || cols == 0) return EHIP_OK;
@@ -281,19 +227,6 @@ int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64
     float* partial =
         static_cast<float*>(scratch(size_t(slabs * blocks * cols) * sizeof(float), 1));
     if (partial == nullptr) return EHIP_ENOMEM;
-    // Both passes in one launch while there is an arrival counter per tile.
-    if ((vec ? int64_t(tiles4) : tiles) * slabs <= kArrivalCounters) {
-        if (vec) {
-            EHIP_LAUNCH("column_sums", sum_cols4_onepass,
-                        dim3(unsigned(blocks), tiles4, unsigned(slabs)), dim3(kThreads), 0, s, x,
-                        out, partial, rows, cols, ld, rpb, x_slab, blocks);
-        } else {
-            EHIP_LAUNCH("column_sums", sum_cols_onepass,
-                        dim3(unsigned(blocks), unsigned(tiles), unsigned(slabs)), dim3(kThreads), 0,
-                        s, x, out, partial, rows, cols, ld, rpb, x_slab, blocks, cw);
-        }
-        return EHIP_OK;
-    }
     if (vec) {
         EHIP_LAUNCH("column_sums_blocks", sum_cols4, dim3(unsigned(blocks), tiles4, unsigned(slabs)),
                     dim3(kThreads), 0, s, x, partial, rows, cols, ld, rpb, x_slab, blocks * cols);

@@ -625,9 +625,8 @@ def column_sums_emulated(x3):
                                                   (1, 777, 260), (1, 3000, 121), (1, 100, 5),
                                                   (3, 500, 1024), (5000, 100, 1)])
 def test_column_sums_order_exact(hip, outer, axis_len, inner):
-    """The one-launch column sums (arrival counter) and the two-launch fallback
-    (more tiles than counters, here 5000 slabs) give exactly the blocked order
-    restated above."""
+    """The device column sums (scalar and float4 kernels, one slab or many) give
+    exactly the blocked order restated above."""
     print_case("column sums order", outer, axis_len, inner)
     x = randn(rng(axis_len * 3 + inner), outer, axis_len, inner)
     got = host(hip.sum_axis(dev(x), outer, axis_len, inner)).reshape(outer, inner)
