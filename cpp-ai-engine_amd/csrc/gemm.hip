@@ -41,10 +41,14 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
     g.tiles_m = int(ceil_div(g.m, BM));
     g.tiles_n = int(ceil_div(g.n, BN));
     const int64_t tiles = int64_t(g.tiles_m) * g.tiles_n;
-    // Split K when the tile grid alone cannot fill the chip (256 CUs) and K is
-    // long: aim for ~512 workgroups, each at least 8 K steps long.
+    // Split K when the tile grid alone cannot fill the chip and K is long:
+    // aim for ~512 workgroups, each at least 8 K steps long. "Fill" is one
+    // workgroup per CU (256) for the 256 x 256 tile, which runs one per CU,
+    // and two per CU (512) for the smaller tiles, which run two or more (a
+    // 1024 x 4096 x 8192 weight gradient: 600 -> 544 us with two splits).
+    const int64_t fill = BM * BN >= 256 * 256 ? 256 : 512;
     int splits = 1;
-    if (tiles * batch < 256 && g.k >= 16 * BK) {
+    if (tiles * batch < fill && g.k >= 16 * BK) {
         int64_t want = ceil_div(512, tiles * batch);
         const int64_t max_by_k = g.k / (8 * BK);
         if (want > max_by_k) want = max_by_k;
