@@ -27,6 +27,8 @@
 
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace ehip {
 namespace {
 
@@ -405,12 +407,14 @@ __device__ __forceinline__ void cover32(int p, int pad, int k, int s, int out, i
 // gradients skipped by a select after an unconditional multiply-add).
 // blockIdx.x = n * tiles + tile.
 template <int CG, bool POOL>
-__global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
-    const float* __restrict__ gout, PoolGather pgat, const float* __restrict__ wt,
-    float* __restrict__ dx, Geo g, int rows, int tiles) {
-    extern __shared__ float sm[];
-    const int n = int(blockIdx.x) / tiles, tile = int(blockIdx.x) % tiles;
-    const int ci0 = int(blockIdx.y) * CG;
+__device__ __forceinline__ void backward_input_block(const float* __restrict__ gout,
+                                                     const PoolGather& pgat,
+                                                     const float* __restrict__ wt,
+                                                     float* __restrict__ dx, const Geo& g,
+                                                     int rows, int tiles, int bx, int by,
+                                                     float* sm) {
+    const int n = bx / tiles, tile = bx % tiles;
+    const int ci0 = by * CG;
     const int h0 = tile * rows;
     const int h1 = min(h0 + rows, g.h);
     int lo, hi, lo2, hi2;
@@ -499,6 +503,15 @@ __global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
     }
 }
 
+template <int CG, bool POOL>
+__global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
+    const float* __restrict__ gout, PoolGather pgat, const float* __restrict__ wt,
+    float* __restrict__ dx, Geo g, int rows, int tiles) {
+    extern __shared__ float sm[];
+    backward_input_block<CG, POOL>(gout, pgat, wt, dx, g, rows, tiles, int(blockIdx.x),
+                                   int(blockIdx.y), sm);
+}
+
 // Weight and bias gradient partials over a band of `rows` output rows of one
 // image: the input rows the band reads (zero-padded) and its output gradient
 // rows are staged in LDS; a thread owns a CT x KT tile of (output channel,
@@ -507,13 +520,12 @@ __global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
 // o = co (K + 1) + k, is then reduced over blocks by conv_weight_reduce. The
 // order of every sum depends only on the shape.
 template <int CT, int KT, bool POOL>
-__global__ __launch_bounds__(kThreads) void conv_weight_band(const float* __restrict__ x,
-                                                             const float* __restrict__ gout,
-                                                             PoolGather pgat,
-                                                             float* __restrict__ partial, Geo g,
-                                                             int rows, int bands) {
-    extern __shared__ float sm[];
-    const int n = int(blockIdx.x) / bands, band = int(blockIdx.x) % bands;
+__device__ __forceinline__ void weight_band_block(const float* __restrict__ x,
+                                                  const float* __restrict__ gout,
+                                                  const PoolGather& pgat,
+                                                  float* __restrict__ partial, const Geo& g,
+                                                  int rows, int bands, int bx, float* sm) {
+    const int n = bx / bands, band = bx % bands;
     const int oh0 = band * rows;
     const int oh1 = min(oh0 + rows, g.oh);
     const int np = (oh1 - oh0) * g.ow;
@@ -607,7 +619,7 @@ __global__ __launch_bounds__(kThreads) void conv_weight_band(const float* __rest
                     for (int kk = 0; kk < KT; ++kk) r[q * KT + kk] = acc[q][kk];
             }
             __syncthreads();
-            float* pc = partial + int64_t(blockIdx.x) * g.cout * K1;
+            float* pc = partial + int64_t(bx) * g.cout * K1;
             const int span = tiles * CT * KT;
             for (int o = threadIdx.x; o < span; o += kThreads) {
                 float sum = red[o];
@@ -617,7 +629,7 @@ __global__ __launch_bounds__(kThreads) void conv_weight_band(const float* __rest
                 if (co < g.cout && k < K1) pc[co * K1 + k] = sum;
             }
         } else if (active) {
-            float* pc = partial + int64_t(blockIdx.x) * g.cout * K1;
+            float* pc = partial + int64_t(bx) * g.cout * K1;
 #pragma unroll
             for (int q = 0; q < CT; ++q)
 #pragma unroll
@@ -627,6 +639,41 @@ __global__ __launch_bounds__(kThreads) void conv_weight_band(const float* __rest
                 }
         }
     }
+}
+
+template <int CT, int KT, bool POOL>
+__global__ __launch_bounds__(kThreads) void conv_weight_band(const float* __restrict__ x,
+                                                             const float* __restrict__ gout,
+                                                             PoolGather pgat,
+                                                             float* __restrict__ partial, Geo g,
+                                                             int rows, int bands) {
+    extern __shared__ float sm[];
+    weight_band_block<CT, KT, POOL>(x, gout, pgat, partial, g, rows, bands, int(blockIdx.x), sm);
+}
+
+// The input-gradient tiles and the weight-gradient bands of one layer in a
+// single launch: blocks [0, in_blocks) run backward_input_block (x-major over
+// in_x), the rest weight_band_block. The two read the same operands and write
+// disjoint outputs; at these sizes each alone leaves most CUs idle, so
+// together they take about as long as the longer one.
+struct PairGeo {
+    int in_rows, in_tiles, in_x, in_blocks;
+    int band_rows, bands;
+};
+
+template <int CG, int T, bool POOL>
+__global__ __launch_bounds__(kThreads) void conv_backward_pair(
+    const float* __restrict__ x, const float* __restrict__ gout, PoolGather pgat,
+    const float* __restrict__ wt, float* __restrict__ dx, float* __restrict__ partial, Geo g,
+    PairGeo pg) {
+    extern __shared__ float sm[];
+    const int b = int(blockIdx.x);
+    if (b < pg.in_blocks)
+        backward_input_block<CG, POOL>(gout, pgat, wt, dx, g, pg.in_rows, pg.in_tiles,
+                                       b % pg.in_x, b / pg.in_x, sm);
+    else
+        weight_band_block<T, T, POOL>(x, gout, pgat, partial, g, pg.band_rows, pg.bands,
+                                      b - pg.in_blocks, sm);
 }
 
 // Partial weight and bias gradients of one chunk of P output pixels. The
@@ -880,6 +927,18 @@ int launch_band(const float* x, const float* gout, const PoolGather& pg, float* 
     return EHIP_OK;
 }
 
+// dweight / dbias from the per-band (or per-chunk) partials, in chunk order.
+int weight_reduce(const float* partial, float* dweight, float* dbias, const Geo& g,
+                  int64_t chunks, hipStream_t s) {
+    const int O = g.cout * (g.k + 1);
+    int rl = 1;
+    while (rl < 16 && rl * 8 < chunks) rl *= 2;
+    const int per_block = 256 / rl;
+    EHIP_LAUNCH("conv2d_weight_reduce", conv_weight_reduce, dim3(unsigned(ceil_div(O, per_block))),
+                dim3(256), 0, s, partial, dweight, dbias, g.cout, g.k, int(chunks), rl);
+    return EHIP_OK;
+}
+
 // Weight and bias gradients: per-band (or per-chunk) partials, then their
 // ordered reduction. POOL gathers the output gradient through a fused pool.
 template <bool POOL>
@@ -926,12 +985,53 @@ int backward_weight(const float* x, const float* gout, const PoolGather& pg, flo
         EHIP_LAUNCH("conv2d_weight_partial", conv_weight_partial, dim3(unsigned(chunks)),
                     dim3(kThreads), lds_for(P), s, x, gout, partial, g, P);
     }
-    int rl = 1;
-    while (rl < 16 && rl * 8 < chunks) rl *= 2;
-    const int per_block = 256 / rl;
-    EHIP_LAUNCH("conv2d_weight_reduce", conv_weight_reduce, dim3(unsigned(ceil_div(O, per_block))),
-                dim3(256), 0, s, partial, dweight, dbias, g.cout, g.k, int(chunks), rl);
+    return weight_reduce(partial, dweight, dbias, g, chunks, s);
+}
+
+// The input and weight gradients of a fused conv block in one launch
+// (conv_backward_pair), then the weight partials' reduction. Needs both
+// tiled paths to fit.
+template <int CG, int T>
+int launch_pair(const float* x, const PoolGather& pg, const float* wt, float* dx, float* partial,
+                const Geo& g, const PairGeo& pr, size_t lds, hipStream_t s) {
+    EHIP_LAUNCH("conv2d_backward_pair", (conv_backward_pair<CG, T, true>),
+                dim3(unsigned(pr.in_blocks + int64_t(g.n) * pr.bands)), dim3(kThreads), lds, s, x,
+                static_cast<const float*>(nullptr), pg, wt, dx, partial, g, pr);
     return EHIP_OK;
+}
+
+int backward_pair(const float* x, const PoolGather& pg, const float* wt, float* dx,
+                  float* dweight, float* dbias, const Geo& g, hipStream_t s) {
+    const int cg = g.cin >= 2 ? 2 : 1;
+    const int groups = int(ceil_div(g.cin, cg));
+    int in_rows = rows_for_fill(int64_t(g.n) * groups, g.h);
+    while (in_rows > 1 && backward_input_lds(g, cg, in_rows) > kTileLds) in_rows = (in_rows + 1) / 2;
+    PairGeo pr{};
+    pr.in_rows = in_rows;
+    pr.in_tiles = int(ceil_div(g.h, in_rows));
+    pr.in_x = g.n * pr.in_tiles;
+    pr.in_blocks = pr.in_x * groups;
+    pr.band_rows = band_rows(g);
+    pr.bands = int(ceil_div(g.oh, pr.band_rows));
+    const int64_t chunks = int64_t(g.n) * pr.bands;
+    if (int64_t(pr.in_blocks) + chunks > 0x7fffffff)
+        return fail(EHIP_EINVAL, "conv2d_relu_maxpool_backward: too many blocks");
+    const int O = g.cout * (g.k + 1);
+    float* partial = static_cast<float*>(scratch(size_t(chunks) * O * sizeof(float)));
+    if (partial == nullptr) return EHIP_ENOMEM;
+    const size_t lds = std::max(backward_input_lds(g, cg, in_rows), weight_band_lds(g, pr.band_rows));
+    const int t = weight_tile(g);
+    int rc;
+    if (cg == 2)
+        rc = t == 4   ? launch_pair<2, 4>(x, pg, wt, dx, partial, g, pr, lds, s)
+             : t == 2 ? launch_pair<2, 2>(x, pg, wt, dx, partial, g, pr, lds, s)
+                      : launch_pair<2, 1>(x, pg, wt, dx, partial, g, pr, lds, s);
+    else
+        rc = t == 4   ? launch_pair<1, 4>(x, pg, wt, dx, partial, g, pr, lds, s)
+             : t == 2 ? launch_pair<1, 2>(x, pg, wt, dx, partial, g, pr, lds, s)
+                      : launch_pair<1, 1>(x, pg, wt, dx, partial, g, pr, lds, s);
+    if (rc != EHIP_OK) return rc;
+    return weight_reduce(partial, dweight, dbias, g, chunks, s);
 }
 
 size_t pool_forward_lds(const Geo& g, int cg, int pk, int pw, int prows) {
@@ -1102,6 +1202,8 @@ int ehip_conv2d_relu_maxpool_backward_f32(const float* x, const float* weight,
     const PoolGather pg{grad_out, out, argmax, int(pool->kernel_h), int(pool->out_h),
                         int(pool->out_w)};
     hipStream_t s = as_stream(stream);
+    if (dx && dweight && input_tiles_fit(g) && weight_bands_fit(g))
+        return backward_pair(x, pg, weight, dx, dweight, dbias, g, s);
     if (dx)
         if (int rc = backward_input<true>(nullptr, pg, weight, dx, g, s)) return rc;
     if (dweight) return backward_weight<true>(x, nullptr, pg, dweight, dbias, g, s);
