@@ -157,11 +157,12 @@ constexpr int64_t kSmallWaveOutputs = 16384;
 constexpr int64_t kSmallWaveMaxK = 2048;
 constexpr int64_t kSmallWaveWork = int64_t(1) << 21;
 
+// Outputs first, first + step, ... of a thread-per-output product.
 template <bool TA, bool TB>
-__global__ __launch_bounds__(256) void gemm_small_thread(GemmArgs g, unsigned total) {
+__device__ __forceinline__ void small_thread_outputs(const GemmArgs& g, unsigned total,
+                                                     unsigned first, unsigned step) {
     const unsigned n = unsigned(g.n), m = unsigned(g.m);
-    const unsigned step = gridDim.x * 256u;
-    for (unsigned o = blockIdx.x * 256u + threadIdx.x; o < total; o += step) {
+    for (unsigned o = first; o < total; o += step) {
         const unsigned t = o / n, j = o - t * n;
         const unsigned bi = t / m, i = t - bi * m;
         const float* a = g.a + batch_offset(bi, g.inner, g.stride_a, g.stride_a2) +
@@ -191,6 +192,44 @@ __global__ __launch_bounds__(256) void gemm_small_thread(GemmArgs g, unsigned to
         }
         float* dst = g.c + batch_offset(bi, g.inner, g.stride_c, g.stride_c2) + int64_t(i) * g.ldc + j;
         *dst = epilogue(g, bi, i, j, acc, dst);
+    }
+}
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256) void gemm_small_thread(GemmArgs g, unsigned total) {
+    small_thread_outputs<TA, TB>(g, total, blockIdx.x * 256u + threadIdx.x, gridDim.x * 256u);
+}
+
+// The three gradients of a small Linear layer in one launch: blocks
+// [0, bdx) compute dx = dy w^T and [bdx, bdx + bdw) dw = x^T dy as
+// gemm_small_thread does, the rest db[c] = sum over rows of dy[r][c] in row
+// order from zero as sum_axis_serial does -- the separate launches' results
+// bit for bit, in about the time of the longest.
+__global__ __launch_bounds__(256) void linear_backward_small(GemmArgs gdx, unsigned ndx,
+                                                             unsigned bdx, GemmArgs gdw,
+                                                             unsigned ndw, unsigned bdw,
+                                                             const float* __restrict__ dy,
+                                                             float* __restrict__ db, int rows,
+                                                             int cols) {
+    const unsigned b = blockIdx.x;
+    if (b < bdx) {
+        small_thread_outputs<false, true>(gdx, ndx, b * 256u + threadIdx.x, bdx * 256u);
+    } else if (b < bdx + bdw) {
+        small_thread_outputs<true, false>(gdw, ndw, (b - bdx) * 256u + threadIdx.x, bdw * 256u);
+    } else {
+        const int c = int(b - bdx - bdw) * 256 + int(threadIdx.x);
+        if (c >= cols) return;
+        float acc = 0.0f;
+        int r = 0;
+        for (; r + 8 <= rows; r += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = dy[int64_t(r + u) * cols + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; r < rows; ++r) acc += dy[int64_t(r) * cols + c];
+        db[c] = acc;
     }
 }
 
@@ -378,6 +417,57 @@ int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
         return EHIP_OK;
     }
     return gemm_run(d, as_stream(stream));
+}
+
+int ehip_linear_backward_f32(const float* x, const float* w, const float* dy, float* dx,
+                             float* dw, float* db, int64_t rows, int64_t in, int64_t out,
+                             void* stream) {
+    EHIP_READY();
+    if (rows < 0 || in < 0 || out < 0) return fail(EHIP_EINVAL, "linear_backward: negative extent");
+    if (!dy || (dx && !w) || (dw && !x)) return fail(EHIP_EINVAL, "linear_backward: null operand");
+    // One launch when every requested part is a thread-per-output product or
+    // a serial column sum (what the separate calls below would pick).
+    const bool small = rows > 0 && in > 0 && out > 0 && rows <= 0x7fffffff &&
+                       (!dx || small_kind(1, rows, in, out) == 1) &&
+                       (!dw || small_kind(1, in, out, rows) == 1) &&
+                       (!db || ((rows <= 64 || out >= 16384) && out <= 0x7fffffff));
+    if (small) {
+        const auto args = [](const float* a, int64_t lda, const float* b, int64_t ldb, float* c,
+                             int64_t m, int64_t n, int64_t k) {
+            GemmArgs g{};
+            g.a = a;
+            g.b = b;
+            g.c = c;
+            g.m = m;
+            g.n = n;
+            g.k = k;
+            g.lda = lda;
+            g.ldb = ldb;
+            g.ldc = n;
+            g.inner = 1;
+            g.alpha = 1.0f;
+            g.add_period = 1;
+            return g;
+        };
+        const unsigned ndx = dx ? unsigned(rows * in) : 0u, ndw = dw ? unsigned(in * out) : 0u;
+        const unsigned bdx = unsigned(ceil_div(ndx, 256)), bdw = unsigned(ceil_div(ndw, 256));
+        const unsigned bdb = db ? unsigned(ceil_div(out, 256)) : 0u;
+        EHIP_LAUNCH("linear_backward", linear_backward_small, dim3(bdx + bdw + bdb), dim3(256), 0,
+                    as_stream(stream), args(dy, out, w, out, dx, rows, in, out), ndx, bdx,
+                    args(x, in, dy, out, dw, in, out, rows), ndw, bdw, dy, db, int(rows),
+                    int(out));
+        return EHIP_OK;
+    }
+    if (dx)
+        if (int rc = ehip_gemm_f32(0, 1, 1, rows, in, out, dy, out, 0, w, out, 0, 0.0f, dx, in, 0,
+                                   stream))
+            return rc;
+    if (dw)
+        if (int rc = ehip_gemm_f32(1, 0, 1, in, out, rows, x, in, 0, dy, out, 0, 0.0f, dw, out, 0,
+                                   stream))
+            return rc;
+    if (db) return ehip_sum_axis_f32(dy, db, 1, rows, out, stream);
+    return EHIP_OK;
 }
 
 int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream) {

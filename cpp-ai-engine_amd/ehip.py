@@ -79,6 +79,7 @@ _SIGS = {
     "ehip_gemm_f32": [_i, _i, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _f, _vp,
                       _i64, _i64, _vp],
     "ehip_gemm_ex_f32": [C.POINTER(GemmEx), _vp],
+    "ehip_linear_backward_f32": [_vp] * 6 + [_i64, _i64, _i64, _vp],
     "ehip_binary_f32": [_i, _vp, _vp, _vp, _i64, _i64, _vp],
     "ehip_scalar_f32": [_vp, _vp, _i64, _f, _f, _vp],
     "ehip_relu_f32": [_vp, _vp, _i64, _vp],
@@ -199,6 +200,19 @@ class Backend:
     def gemm_ex(self, desc):
         """Runs an ehip_gemm_ex_t (a GemmEx whose pointers are device addresses)."""
         self.ok(self.lib.ehip_gemm_ex_f32(C.byref(desc), self.stream()), "gemm_ex")
+
+    def linear_backward(self, x, w, dy, want=("dx", "dw", "db")):
+        """(dx, dw, db) of y = x w + b through ehip_linear_backward_f32; parts not
+        in `want` are None."""
+        rows, inp = x.shape
+        out = w.shape[1]
+        dx = self.f32((rows, inp)) if "dx" in want else None
+        dw = self.f32((inp, out)) if "dw" in want else None
+        db = self.f32((out,)) if "db" in want else None
+        self.ok(self.lib.ehip_linear_backward_f32(self.p(x), self.p(w), self.p(dy), self.p(dx),
+                                                  self.p(dw), self.p(db), rows, inp, out,
+                                                  self.stream()), "linear_backward")
+        return dx, dw, db
 
     def gemm(self, a, b, c=None, trans_a=False, trans_b=False, beta=0.0):
         """c = op(a) op(b) + beta c; a, b 2-D or 3-D (batched), 2-D operands shared."""

@@ -331,8 +331,27 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias) {
     std::vector<std::shared_ptr<TensorImpl>> parents = {x.get_impl(), w.get_impl()};
     if (bias) parents.push_back(bias->get_impl());
     attach(out, std::move(parents), [xc, wc, bc, M, N, K](const Tensor& g) mutable {
+        const bool want_db = bc.get_impl() && bc.requires_grad();
+        if (M > 0 && K > 0 && N > 0) {
+            // The same three results as the composed graph's add and product
+            // backward (one launch for small layers), added in its order: the
+            // bias, then x, then w.
+            Tensor dx = xc.requires_grad() ? empty_2d(M, K) : Tensor();
+            Tensor dw = wc.requires_grad() ? empty_2d(K, N) : Tensor();
+            Tensor db = want_db ? Tensor(bc.shape(), 0.0f, false) : Tensor();
+            hip::check(ehip_linear_backward_f32(dptr(xc), dptr(wc), dptr(g),
+                                                xc.requires_grad() ? dout(dx) : nullptr,
+                                                wc.requires_grad() ? dout(dw) : nullptr,
+                                                want_db ? dout(db) : nullptr, int64_t(M),
+                                                int64_t(K), int64_t(N), nullptr),
+                       "linear backward");
+            if (want_db) bc.add_grad(db);
+            if (xc.requires_grad()) xc.add_grad(dx);
+            if (wc.requires_grad()) wc.add_grad(dw);
+            return;
+        }
         // The composed graph's order: the bias add's node, then the product's.
-        if (bc.get_impl() && bc.requires_grad()) bc.add_grad(reduce_to(g, bc));
+        if (want_db) bc.add_grad(reduce_to(g, bc));
         if (xc.requires_grad()) {  // g w^T
             Tensor dx = empty_2d(M, K);
             if (M > 0 && K > 0) gemm_2d(false, true, M, K, N, dptr(g), dptr(wc), dout(dx), nullptr,

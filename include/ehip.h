@@ -197,6 +197,18 @@ typedef struct {
 
 int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream);
 
+/* The three gradients of Linear, y = x . w + b with x (rows, in), w (in,
+ * out), dy (rows, out): dx = dy . w^T, dw = x^T . dy, db = the column sums of
+ * dy -- the matmul backward and the broadcast add's backward through
+ * fold_leading (src/tensor_ops.cpp:565-586, 81-102; src/tensor_detail.hpp:
+ * 182-206). Each equals what ehip_gemm_f32 / ehip_sum_axis_f32 compute for it
+ * bit for bit; when all requested parts are small (thread-per-output
+ * products, a serial column sum) they run in one launch. dx, dw and db may
+ * each be NULL. */
+int ehip_linear_backward_f32(const float* x, const float* w, const float* dy, float* dx,
+                             float* dw, float* db, int64_t rows, int64_t in, int64_t out,
+                             void* stream);
+
 /* --------------------------------------------------------- element-wise */
 
 enum { EHIP_ADD = 0, EHIP_SUB = 1, EHIP_MUL = 2, EHIP_DIV = 3 };

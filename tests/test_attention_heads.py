@@ -373,3 +373,25 @@ def test_colsum_refusals_and_k_zero(hip):
     d.colsum_b = hip.p(cs)
     hip.gemm_ex(d)
     exact(host(cs), np.zeros(4, np.float32), "k = 0 column sums")
+
+
+# ------------------------------------------------------- Linear backward in one call
+
+@pytest.mark.parametrize("rows,inp,out", [(64, 784, 10), (64, 8, 10), (33, 100, 7),
+                                          (2048, 96, 384), (300, 1024, 257), (100, 3, 20000)])
+@pytest.mark.parametrize("want", [("dx", "dw", "db"), ("dw", "db"), ("dx",)])
+def test_linear_backward_matches_separate_calls(hip, rows, inp, out, want):
+    """ehip_linear_backward_f32 (one launch for small layers) equals the separate
+    products and column sum bit for bit."""
+    print_case("linear_backward", rows, inp, out, want)
+    r = np.random.default_rng(rows + inp + out + len(want))
+    x = randn(r, rows, inp)
+    x[x < -1.0] = 0.0  # zero-skip terms
+    x, w, dy = dev(x), dev(randn(r, inp, out)), dev(randn(r, rows, out))
+    dx, dw, db = hip.linear_backward(x, w, dy, want)
+    if "dx" in want:
+        exact(host(dx), host(hip.gemm(dy, w, trans_b=True)), "dx")
+    if "dw" in want:
+        exact(host(dw), host(hip.gemm(x, dy, trans_a=True)), "dw")
+    if "db" in want:
+        exact(host(db), host(hip.sum_axis(dy, 1, rows, out)), "db")
