@@ -366,11 +366,17 @@ struct AdamSlot {
 };
 constexpr int64_t kAdamChunk = int64_t(kThreads) * kUnroll * 4;
 
-template <bool NT>
-__global__ __launch_bounds__(kThreads) void adam_multi(const AdamSlot* __restrict__ slots,
-                                                       int count, float lr, float b1, float b2,
-                                                       float eps, float wd, float c1, float c2) {
-    const int64_t b = blockIdx.x;
+// Up to this many tensors travel in the kernel arguments (48 slots of 48
+// bytes), so a model whose gradient buffers change from step to step (the
+// first gradient write adopts a fresh buffer) needs no table upload per step.
+constexpr int kInlineSlots = 48;
+struct AdamInline {
+    AdamSlot s[kInlineSlots];
+};
+
+// The slot whose chunks include chunk b (slots ordered by first_chunk).
+template <class Slots>
+__device__ __forceinline__ AdamSlot find_slot(const Slots& slots, int count, int64_t b) {
     int lo = 0, hi = count - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) / 2;
@@ -379,7 +385,12 @@ __global__ __launch_bounds__(kThreads) void adam_multi(const AdamSlot* __restric
         else
             hi = mid - 1;
     }
-    const AdamSlot s = slots[lo];
+    return slots[lo];
+}
+
+template <bool NT>
+__device__ __forceinline__ void adam_chunk(const AdamSlot& s, int64_t b, float lr, float b1,
+                                           float b2, float eps, float wd, float c1, float c2) {
     const Adam op{s.p, s.g, s.m, s.v, lr, b1, b2, eps, wd, c1, c2};
     const int64_t begin = (b - s.first_chunk) * kAdamChunk;
     const int64_t end = min(begin + kAdamChunk, s.n);
@@ -401,6 +412,23 @@ __global__ __launch_bounds__(kThreads) void adam_multi(const AdamSlot* __restric
         tail = v1 << 2;
     }
     for (int64_t i = tail + threadIdx.x; i < end; i += kThreads) op.scalar(i);
+}
+
+template <bool NT>
+__global__ __launch_bounds__(kThreads) void adam_multi(const AdamSlot* __restrict__ slots,
+                                                       int count, float lr, float b1, float b2,
+                                                       float eps, float wd, float c1, float c2) {
+    const int64_t b = blockIdx.x;
+    adam_chunk<NT>(find_slot(slots, count, b), b, lr, b1, b2, eps, wd, c1, c2);
+}
+
+template <bool NT>
+__global__ __launch_bounds__(kThreads) void adam_multi_inline(AdamInline table, int count,
+                                                              float lr, float b1, float b2,
+                                                              float eps, float wd, float c1,
+                                                              float c2) {
+    const int64_t b = blockIdx.x;
+    adam_chunk<NT>(find_slot(table.s, count, b), b, lr, b1, b2, eps, wd, c1, c2);
 }
 
 template <int OP>
@@ -537,6 +565,20 @@ int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, 
     if (slots.empty()) return EHIP_OK;
     if (chunks > 0x7fffffff) return fail(EHIP_EINVAL, "adam_multi: too many elements");
     hipStream_t s = as_stream(stream);
+    const bool nt = chunks * kAdamChunk >= kNontemporalMin;
+    if (slots.size() <= size_t(kInlineSlots)) {
+        AdamInline inline_table{};
+        std::memcpy(inline_table.s, slots.data(), slots.size() * sizeof(AdamSlot));
+        if (nt)
+            EHIP_LAUNCH("adam_multi", adam_multi_inline<true>, dim3(unsigned(chunks)),
+                        dim3(kThreads), 0, s, inline_table, int(slots.size()), lr, beta1, beta2,
+                        eps, weight_decay, bias_c1, bias_c2);
+        else
+            EHIP_LAUNCH("adam_multi", adam_multi_inline<false>, dim3(unsigned(chunks)),
+                        dim3(kThreads), 0, s, inline_table, int(slots.size()), lr, beta1, beta2,
+                        eps, weight_decay, bias_c1, bias_c2);
+        return EHIP_OK;
+    }
     // The slot table lives in a buffer of its own and is uploaded only when it
     // differs from the previous call's: an optimiser stepping the same
     // parameters every iteration pays no host-to-device copy per step. Work is
@@ -564,7 +606,7 @@ int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, 
         if (int rc = ehip_memcpy_h2d(table, slots.data(), bytes, stream)) return rc;
         last = slots;
     }
-    if (chunks * kAdamChunk >= kNontemporalMin)
+    if (nt)
         EHIP_LAUNCH("adam_multi", adam_multi<true>, dim3(unsigned(chunks)), dim3(kThreads), 0, s,
                     table, int(slots.size()), lr, beta1, beta2, eps, weight_decay, bias_c1,
                     bias_c2);

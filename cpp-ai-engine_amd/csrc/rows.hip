@@ -270,6 +270,44 @@ __global__ __launch_bounds__(Group<T>::kBlock, Group<T>::kMinWaves) void xent_ro
     }
 }
 
+// A classifier head's batch (at most 1024 rows of at most 128 classes) in one
+// block: xent_rows' arithmetic per row (16 wavefronts, one row each at a
+// time), the row losses kept in LDS, then mean_rows' tree over them -- the
+// two launches' results bit for bit, in one.
+constexpr int kXentMeanRows = 1024;
+
+template <int V>
+__global__ __launch_bounds__(1024) void xent_rows_mean(const float* __restrict__ logits,
+                                                       const int32_t* __restrict__ targets,
+                                                       float* __restrict__ probs,
+                                                       float* __restrict__ loss, int rows,
+                                                       int cols) {
+    __shared__ float row_loss[kXentMeanRows];
+    __shared__ double sh[1024];
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    for (int r = wave; r < rows; r += 16) {
+        Frag<64, V, false, false> f;
+        f.load(logits + int64_t(r) * cols, cols, lane, -INFINITY);
+        float m, s;
+        frag_softmax(f, nullptr, m, s);  // one wavefront: no LDS in the reduction
+        f.store(probs + int64_t(r) * cols, cols, lane);
+        if (lane == 0) {
+            const int64_t t = targets[r];
+            row_loss[r] = (t >= 0 && t < cols) ? -((logits[int64_t(r) * cols + t] - m) - logf(s)) : NAN;
+        }
+    }
+    __syncthreads();
+    double acc = 0.0;
+    if (int(threadIdx.x) < rows) acc += row_loss[threadIdx.x];
+    sh[threadIdx.x] = acc;
+    __syncthreads();
+    for (int h = 512; h > 0; h >>= 1) {
+        if (int(threadIdx.x) < h) sh[threadIdx.x] += sh[threadIdx.x + h];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) loss[0] = static_cast<float>(sh[0]) / static_cast<float>(rows);
+}
+
 // dx = (softmax - onehot) * (grad / rows), from the logits in one pass. The
 // softmax is the same code as xent_rows, so the result equals the two-kernel
 // path bit for bit.
@@ -829,6 +867,15 @@ int ehip_cross_entropy_f32(const float* logits, const int32_t* targets, float* p
     if (!logits || !targets || !probs || !loss)
         return fail(EHIP_EINVAL, "cross_entropy: null pointer");
     hipStream_t s = as_stream(stream);
+    if (rows <= kXentMeanRows && cols <= 128) {
+        if (cols <= 64)
+            EHIP_LAUNCH("cross_entropy", xent_rows_mean<1>, dim3(1), dim3(1024), 0, s, logits,
+                        targets, probs, loss, int(rows), int(cols));
+        else
+            EHIP_LAUNCH("cross_entropy", xent_rows_mean<2>, dim3(1), dim3(1024), 0, s, logits,
+                        targets, probs, loss, int(rows), int(cols));
+        return EHIP_OK;
+    }
     float* row_loss = static_cast<float*>(scratch(size_t(rows) * sizeof(float)));
     if (row_loss == nullptr) return EHIP_ENOMEM;
     int rc = EHIP_OK;

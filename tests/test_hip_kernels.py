@@ -694,7 +694,8 @@ def test_layernorm(hip, orc, rows, d):
 
 
 @pytest.mark.parametrize("rows,cols", [(64, 10), (2048, 121), (8, 5), (16, 32000), (3, 40000),
-                                       (100, 256), (600, 32000), (9, 1002)])
+                                       (100, 256), (600, 32000), (9, 1002), (1024, 128),
+                                       (1000, 100), (1025, 10), (1, 1)])
 def test_cross_entropy(hip, orc, rows, cols):
     print_case("xent", rows, cols)
     r = rng(rows * 3 + cols)
