@@ -172,15 +172,30 @@ __device__ __forceinline__ void small_thread_outputs(const GemmArgs& g, unsigned
         const int64_t ak = TA ? g.lda : 1, bk = TB ? 1 : g.ldb;
         float acc = 0.0f;
         int64_t k = 0;
-        for (; k + 8 <= g.k; k += 8) {
-            float av[8], bv[8];
+        // Sixteen terms' loads in flight at a time (the sums stay in k order):
+        // a thread's chain of dependent load round trips is K / 16 long.
+        for (; k + 16 <= g.k; k += 16) {
+            float av[16], bv[16];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < 16; ++u) {
                 av[u] = a[(k + u) * ak];
                 bv[u] = b[(k + u) * bk];
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < 16; ++u) {
+                const float s = acc + av[u] * bv[u];
+                acc = av[u] != 0.0f ? s : acc;
+            }
+        }
+        for (; k + 4 <= g.k; k += 4) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                av[u] = a[(k + u) * ak];
+                bv[u] = b[(k + u) * bk];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
                 const float s = acc + av[u] * bv[u];
                 acc = av[u] != 0.0f ? s : acc;
             }
