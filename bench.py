@@ -160,29 +160,29 @@ def headline(engine_mod, timer, steps, warmup):
 
 def dominant_kernel(eng, hip, timer, torch):
     """The CNN step's largest kernel by total time (rocprofv3 --kernel-trace --stats of
-    this benchmark, profiles/cnn_step_kernels.md): the weight and bias gradient of a fused
-    Conv2d -> ReLU -> MaxPool2d block -- conv_weight_band (per-band partials, the pooled
-    gradient routed through the argmax and the ReLU on the fly) and conv_weight_reduce
-    (their ordered sum) -- timed on the conv1 layer (64 x 1 x 28 x 28 input, 8 3x3
-    filters, 2x2 pool) as one launch pair. HBM-bound by its data, latency-bound at this
-    size: algorithmic bytes = x, the pooled gradient, the pooled values and the argmax read
-    once, dW and db written once."""
-    import ehip as E
+    this benchmark, profiles/cnn_step_kernels.md): the backward of the fused conv2 block
+    (Conv2d 8 -> 16, 3x3, pad 1 -> ReLU -> MaxPool2d 2 on a 64 x 8 x 14 x 14 input) --
+    conv_backward_pair (the input-gradient tiles and the weight-gradient band partials in
+    one launch, the pooled gradient routed through the argmax and the ReLU on the fly) and
+    conv_weight_reduce (the partials' ordered sum) -- timed as that launch pair.
+    HBM-bound by its data, latency-bound at this size: algorithmic bytes = x, the pooled
+    gradient, the pooled values, the argmax and the weights read once, dx, dW and db
+    written once."""
     r = torch.Generator(device="cuda").manual_seed(5)
-    x = torch.rand(64, 1, 28, 28, device="cuda", generator=r)
-    w = torch.rand(8, 1, 3, 3, device="cuda", generator=r) * 0.6 - 0.3
-    b = torch.zeros(8, device="cuda")
+    x = torch.rand(64, 8, 14, 14, device="cuda", generator=r)
+    w = torch.rand(16, 8, 3, 3, device="cuda", generator=r) * 0.6 - 0.3
+    b = torch.zeros(16, device="cuda")
     out, am = hip.conv2d_relu_maxpool(x, w, b, 1, 1, 2)
     g = torch.randn(out.shape, device="cuda", generator=r)
-    dw, db = torch.empty_like(w), torch.empty_like(b)
+    dx, dw, db = torch.empty_like(x), torch.empty_like(w), torch.empty_like(b)
     cw, pw = hip.conv_relu_pool_windows(x.shape, w.shape, 1, 1, 2)
     sec = timer.time_batch(
-        lambda n: eng.repeat_conv_relu_pool_backward(n, x, w, g, out, am, dw, db, cw, pw), 500,
-        50)
-    work = 4 * (x.numel() + 3 * out.numel() + w.numel() + b.numel())
-    return roofline("conv_weight_band<1,1,pool>+conv_weight_reduce (conv1 block dW/db, "
-                    "64x1x28x28, 8 filters 3x3, pool 2)", "hbm", work, sec,
-                    committed_traffic("conv1_block_wgrad"))
+        lambda n: eng.repeat_conv_relu_pool_backward(n, x, w, g, out, am, dw, db, cw, pw, dx=dx),
+        500, 50)
+    work = 4 * (2 * x.numel() + 3 * out.numel() + 2 * w.numel() + b.numel())
+    return roofline("conv_backward_pair<2,4,pool>+conv_weight_reduce (conv2 block dx/dW/db, "
+                    "64x8x14x14, 16 filters 3x3, pool 2)", "hbm", work, sec,
+                    committed_traffic("conv2_block_backward"))
 
 
 def kernel_only(eng, hip, timer, torch):
@@ -240,6 +240,35 @@ def cpu_charlm_baseline(ids, targets, dims, params, seconds_target):
                       f"of the reference engine compiled from its own sources (oracle/_ref, -O3, "
                       f"no -march) on {threads} host threads from the GPU run's initial "
                       f"parameters, {dt:.1f} s"}
+
+
+# (batch, seq, vocab, d_model, heads, ffn, layers, timed steps, warm-up steps)
+LM_CONFIGS = {"charlm_cfg3": (32, 64, 121, 96, 4, 384, 2, 100, 10),
+              "transformer_cfg5": (16, 512, 256, 1024, 16, 4096, 12, 5, 2)}
+
+
+def lm_leg(engine_mod, eng, timer, dims, keep_params=False):
+    """One character-model Transformer training-step measurement (forward +
+    backward + Adam on a resident synthetic batch); returns (record, initial
+    parameters or None)."""
+    b, s, vocab, d, h, ff, layers, steps, warm = dims
+    ids, targets = lm_inputs(3, b, s, vocab)
+    tr = engine_mod.Trainer.charlm(eng, ids, targets, vocab, d, h, ff, layers, lr=1e-3)
+    p0 = tr.params() if keep_params else None
+    first = None
+    if warm > 0:
+        tr.step()
+        first = tr.loss()
+    sec = timer.time(tr.step, steps, max(warm - 1, 0))
+    fl = lm_step_flops(b, s, d, ff, vocab, layers)
+    rec = {"steps_per_s": round(1.0 / sec, 3), "ms_per_step": round(sec * 1e3, 3),
+           "params": int(tr.num_params()), "step_tflop": round(fl / 1e12, 4),
+           "achieved_tflops": round(fl / sec / 1e12, 2),
+           "frac_of_mfma_peak": round(fl / sec / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+           "loss_first_step": None if first is None else round(first, 5),
+           "loss_after": round(tr.loss(), 5)}
+    tr.close()
+    return rec, p0
 
 
 def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
@@ -323,31 +352,23 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
     bt["softmax_backward 131072x512"] = roofline("softmax_backward", "hbm", 12 * sc.numel(), sec)
     del sc, y
     im = torch.randn(64, 64, 112, 112, device="cuda", generator=r)
-    sec = timer.time(lambda: hip.maxpool(im, 2, 2), 20, 3)
+    pooled, am = hip.maxpool(im, 2, 2)  # outputs reused by the timed calls
+    sec = timer.time(lambda: hip.maxpool(im, 2, 2, out=(pooled, am)), 20, 3)
     bt["maxpool 64x64x112x112 k2"] = roofline("maxpool", "hbm", 6 * im.numel(), sec)
-    pooled, am = hip.maxpool(im, 2, 2)
     gp = torch.randn_like(pooled)
-    sec = timer.time(lambda: hip.maxpool_backward(am, gp, tuple(im.shape), 2, 2), 20, 3)
+    dim = torch.empty_like(im)
+    sec = timer.time(lambda: hip.maxpool_backward(am, gp, tuple(im.shape), 2, 2, dx=dim), 20, 3)
     bt["maxpool_backward 64x64x112x112 k2"] = roofline("maxpool_backward", "hbm",
                                                        6 * im.numel(), sec)
-    del im, pooled, am, gp
+    del im, pooled, am, gp, dim
     out["bandwidth_transformer_shapes"] = bt
     torch.cuda.empty_cache()
     # cfg 3 and cfg 5: Transformer training steps.
-    for tag, (b, s, vocab, d, h, ff, layers, steps, warm) in {
-            "charlm_cfg3": (32, 64, 121, 96, 4, 384, 2, 100, 10),
-            "transformer_cfg5": (16, 512, 256, 1024, 16, 4096, 12, 5, 2)}.items():
-        ids, targets = lm_inputs(3, b, s, vocab)
-        tr = engine_mod.Trainer.charlm(eng, ids, targets, vocab, d, h, ff, layers, lr=1e-3)
-        p0 = tr.params() if (tag == "charlm_cfg3" and cpu_seconds > 0) else None
-        sec = timer.time(tr.step, steps, warm)
-        fl = lm_step_flops(b, s, d, ff, vocab, layers)
-        out[tag] = {"steps_per_s": round(1.0 / sec, 3), "ms_per_step": round(sec * 1e3, 3),
-                    "params": int(tr.num_params()), "step_tflop": round(fl / 1e12, 4),
-                    "achieved_tflops": round(fl / sec / 1e12, 2),
-                    "frac_of_mfma_peak": round(fl / sec / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
-                    "loss_after": round(tr.loss(), 5)}
-        tr.close()
+    for tag, dims in LM_CONFIGS.items():
+        ids, targets = lm_inputs(3, dims[0], dims[1], dims[2])
+        out[tag], p0 = lm_leg(engine_mod, eng, timer, dims,
+                              keep_params=tag == "charlm_cfg3" and cpu_seconds > 0)
+        b, s, vocab, d, h, ff, layers, steps, warm = dims
         if p0 is not None:
             log("bench: reference CPU baseline, cfg3")
             cpu = cpu_charlm_baseline(ids, targets, (vocab, d, h, ff, layers), p0, cpu_seconds)
@@ -367,6 +388,9 @@ def main():
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant kernel and a copy kernel of known size (for "
                          "rocprofv3 --pmc runs) and print their timings")
+    ap.add_argument("--transformer-only", action="store_true",
+                    help="run only the cfg5 Transformer step leg (for kernel profiles) and "
+                         "print its record")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -384,6 +408,10 @@ def main():
 
     if args.kernel_only:
         kernel_only(eng, hip, timer, torch)
+        return
+    if args.transformer_only:
+        rec, _ = lm_leg(engine_capi, eng, timer, LM_CONFIGS["transformer_cfg5"])
+        print(json.dumps({"transformer_cfg5": rec}), flush=True)
         return
 
     log("bench: cfg2 CNN training step")

@@ -327,25 +327,29 @@ class Backend:
                 "col2im")
         return x
 
-    def maxpool(self, x, k, stride, pad=0, float_index=False):
-        """float_index selects the float argmax layout of the reference's device path."""
+    def maxpool(self, x, k, stride, pad=0, float_index=False, out=None):
+        """float_index selects the float argmax layout of the reference's device path;
+        out = (y, argmax) reuses preallocated outputs."""
         w = window(*x.shape, k, k, stride, pad)
-        y = self.f32((w.batch, w.channels, w.out_h, w.out_w))
+        if out is not None:
+            y, am = out
+        else:
+            y = self.f32((w.batch, w.channels, w.out_h, w.out_w))
+            am = (self.f32(y.shape) if float_index else
+                  self.torch.empty(y.shape, dtype=self.torch.int32, device="cuda"))
         if float_index:
-            am = self.f32(y.shape)
             rc = self.lib.ehip_maxpool_fidx_f32(self.p(x), self.p(y), self.p(am), C.byref(w),
                                                 self.stream())
         else:
-            am = self.torch.empty(y.shape, dtype=self.torch.int32, device="cuda")
             rc = self.lib.ehip_maxpool_f32(self.p(x), self.p(y), self.p(am), C.byref(w),
                                            self.stream())
         self.ok(rc, "maxpool")
         return y, am
 
-    def maxpool_backward(self, argmax, g, in_shape, k, stride, pad=0):
+    def maxpool_backward(self, argmax, g, in_shape, k, stride, pad=0, dx=None):
         """argmax as returned by maxpool: int32, or float32 for the float layout."""
         w = window(*in_shape, k, k, stride, pad)
-        dx = self.f32(in_shape)
+        dx = self.f32(in_shape) if dx is None else dx
         f = (self.lib.ehip_maxpool_backward_fidx_f32 if argmax.dtype == self.torch.float32
              else self.lib.ehip_maxpool_backward_f32)
         self.ok(f(self.p(argmax), self.p(g), self.p(dx), C.byref(w), self.stream()),
