@@ -676,6 +676,320 @@ __global__ __launch_bounds__(kThreads) void conv_backward_pair(
                                       b - pg.in_blocks, sm);
 }
 
+// Backward of a 3 x 3, stride 1, padding 1 convolution followed by ReLU and a
+// max pool with disjoint pk x pk windows, over a tile of `rows` convolution
+// rows (a multiple of pk, so every pooled cell belongs to one tile) of one
+// image: the input gradient of those rows and the weight and bias gradient
+// partials of those positions, in one block.
+//
+// The convolution's output gradient around the tile (rows r0 - 1 .. r0 +
+// rows, columns -1 .. W, zero wherever there is no output) is built in LDS
+// by scattering each pooled cell's gradient to its argmax position when the
+// pooled value is positive: out_grad() for every position, with a quarter of
+// the loads. The input rows r0 - 1 .. r0 + rows (zero-padded) and, for the
+// input gradient, the weights as [tap][cout][ci] sit beside it.
+//
+// Threads [0, dx_threads) compute the input gradient, one per (pixel, group
+// of CG input channels): for the nine windows in (oh, ow) order, the
+// cout-term dot product in co order with zero gradients skipped, added to the
+// pixel's sum: conv_backward_input_direct's order, so the result is
+// bit-identical. Windows outside the output read the zero border; their dot
+// products are +0 and leave the sum unchanged (a sum that starts at +0 never
+// becomes -0 in round-to-nearest). When every weight is finite a skipped
+// product g * w, g = +-0, is itself +-0, so the skip is dropped with the same
+// bits; a non-finite weight keeps it.
+//
+// The other threads compute the weight and bias partials as
+// weight_band_block does -- CT x CT tiles of (co, k), column K the bias,
+// over pg pixel groups combined in group order -- into partial[block].
+struct PoolTile {
+    int rows, tiles;         // convolution rows per tile (a multiple of pk), tiles per image
+    int dx_threads;          // threads computing dx (a multiple of 64; 0 = no dx)
+    int pg;                  // pixel groups of the weight partials (0 = no weight gradient)
+    int wp, plane;           // LDS row and plane pitch (odd)
+    int cinp;                // input channels padded to CG
+    int xs_off, ws_off, red_off;   // LDS offsets (floats) of the input rows, weights, group sums
+};
+
+// Weights of one (co, input-channel group) in the tile kernel's LDS: nine taps
+// of CG channels, padded to whole 16-byte reads.
+template <int CG>
+constexpr int tap_pitch() { return (9 * CG + 3) / 4 * 4; }
+
+// One thread per (pixel, group of CG channels). The nine windows' dot
+// products run side by side with co as the outer loop (each still sums its
+// co terms in co order), so every round of LDS reads feeds 9 CG products.
+template <int CG, bool FAST>
+__device__ __forceinline__ void pool_tile_dx(const float* gs, const float* ws, float* dx,
+                                             const Geo& g, const PoolTile& pt, int n, int r0,
+                                             int rows, int first, int step) {
+    constexpr int WS = tap_pitch<CG>();
+    const int npx = pt.rows * g.w;
+    const int groups = pt.cinp / CG;
+    const int items = npx * groups;
+    for (int it = first; it < items; it += step) {
+        const int cgi = it / npx, p = it - cgi * npx;
+        const int hl = p / g.w, v = p - hl * g.w;
+        if (hl >= rows) continue;
+        float d[9][CG];
+#pragma unroll
+        for (int t = 0; t < 9; ++t)
+#pragma unroll
+            for (int cl = 0; cl < CG; ++cl) d[t][cl] = 0.0f;
+        const float* gb = gs + hl * pt.wp + v;
+        const float* wb = ws + cgi * WS;
+#pragma unroll 2
+        for (int co = 0; co < g.cout; ++co) {
+            float gv[9];
+#pragma unroll
+            for (int a = 0; a < 3; ++a)
+#pragma unroll
+                for (int b = 0; b < 3; ++b) gv[a * 3 + b] = gb[co * pt.plane + a * pt.wp + b];
+            float wv[WS];
+            const float4* wq = reinterpret_cast<const float4*>(wb + co * groups * WS);
+#pragma unroll
+            for (int q = 0; q < WS / 4; ++q) {
+                const float4 t = wq[q];
+                wv[4 * q] = t.x;
+                wv[4 * q + 1] = t.y;
+                wv[4 * q + 2] = t.z;
+                wv[4 * q + 3] = t.w;
+            }
+            // window (a, b) is (oh, ow) = (h - 1 + a, v - 1 + b), tap (2 - a, 2 - b)
+#pragma unroll
+            for (int a = 0; a < 3; ++a)
+#pragma unroll
+                for (int b = 0; b < 3; ++b) {
+                    const int tap = (2 - a) * 3 + (2 - b);
+                    const float gq = gv[a * 3 + b];
+#pragma unroll
+                    for (int cl = 0; cl < CG; ++cl) {
+                        const float t = d[a * 3 + b][cl] + gq * wv[tap * CG + cl];
+                        d[a * 3 + b][cl] = (FAST || gq != 0.0f) ? t : d[a * 3 + b][cl];
+                    }
+                }
+        }
+        const int h = r0 + hl;
+#pragma unroll
+        for (int cl = 0; cl < CG; ++cl) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 9; ++t) acc += d[t][cl];
+            const int ci = cgi * CG + cl;
+            if (ci < g.cin) dx[((int64_t(n) * g.cin + ci) * g.h + h) * g.w + v] = acc;
+        }
+    }
+}
+
+template <int CG, int CT, int NT>
+__global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restrict__ x,
+                                                          const float* __restrict__ wt,
+                                                          PoolGather pgat, float* __restrict__ dx,
+                                                          float* __restrict__ partial, Geo g,
+                                                          PoolTile pt) {
+    extern __shared__ float sm[];
+    const int tid = int(threadIdx.x);
+    const int n = int(blockIdx.x) / pt.tiles, tile = int(blockIdx.x) % pt.tiles;
+    const int r0 = tile * pt.rows;
+    const int rows = min(pt.rows, g.h - r0);
+    const int srows = pt.rows + 2;
+    const bool want_dx = pt.dx_threads > 0, want_dw = pt.pg > 0;
+    // gs: [cout rounded up to CT][plane], output gradient rows r0 - 1 .. r0 + rows
+    // (planes beyond cout stay zero); xs: [cin + 2][plane], input rows r0 - 1 ..
+    // r0 + rows, then a plane of ones (the bias column) and one of zeros.
+    float* gs = sm;
+    float* xs = sm + pt.xs_off;
+    float* ws = sm + pt.ws_off;       // [cout][cinp / CG][tap_pitch]: tap-major CG channels
+    float* red = sm + pt.red_off;     // [pg][tiles][CT * CT]
+
+    // The zero border and every position no pooled cell selects.
+    const int zero_n = pt.xs_off;
+    for (int e = tid; e < zero_n; e += NT) gs[e] = 0.0f;
+    if (want_dw)
+        for (int e = tid; e < 2 * pt.plane; e += NT)
+            xs[g.cin * pt.plane + e] = e < pt.plane ? 1.0f : 0.0f;
+    if (want_dx && pt.cinp != g.cin)
+        for (int e = tid; e < g.cout * (pt.cinp / CG) * tap_pitch<CG>(); e += NT) ws[e] = 0.0f;
+    __syncthreads();
+
+    // Pooled rows whose windows reach rows r0 - 1 .. r0 + rows.
+    const int pk = pgat.pk, pw = pgat.pw;
+    const int pr_lo = max(r0 / pk - 1, 0), pr_hi = min((r0 + pt.rows) / pk, pgat.ph - 1);
+    const int prn = max(pr_hi - pr_lo + 1, 0);
+    const int cells = g.cout * prn * pw;
+    const int wcols = g.w + 2;
+    const int xn = want_dw ? g.cin * srows * wcols : 0;
+    const int wn = want_dx ? g.cout * g.cin * 9 : 0;
+    const int64_t oplane = int64_t(g.h) * g.w;
+    bool nonfinite = false;
+    // One round issues up to 2 cells (3 loads each), 2 input and 5 weight
+    // loads per thread before any LDS store.
+    for (int rd = 0; rd * 2 * NT < cells || rd * 2 * NT < xn || rd * 5 * NT < wn; ++rd) {
+        int cslot[2];
+        float cval[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int e = rd * 2 * NT + u * NT + tid;
+            cslot[u] = -1;
+            cval[u] = 0.0f;
+            if (e < cells) {
+                const int pc = e % pw, q = e / pw;
+                const int prl = q % prn, co = q / prn;
+                const int pr = pr_lo + prl;
+                const int64_t nc = int64_t(n) * g.cout + co;
+                const int64_t o = (nc * pgat.ph + pr) * pw + pc;
+                const int32_t am = pgat.argmax[o];
+                const float pv = pgat.pooled[o];
+                const float gv = pgat.gp[o];
+                const int64_t off = int64_t(am) - (nc * oplane + int64_t(pr) * pk * g.w + pc * pk);
+                if (pv > 0.0f && off >= 0 && off < int64_t(pk) * g.w) {
+                    const int offi = int(off);
+                    const int dr = offi / g.w, dc = offi - dr * g.w;
+                    const int r = pr * pk + dr;
+                    if (dr < pk && dc < pk && r >= r0 - 1 && r <= r0 + pt.rows) {
+                        cslot[u] = co * pt.plane + (r - r0 + 1) * pt.wp + pc * pk + dc + 1;
+                        cval[u] = gv;
+                    }
+                }
+            }
+        }
+        int xslot[2];
+        float xval[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int e = rd * 2 * NT + u * NT + tid;
+            xslot[u] = -1;
+            xval[u] = 0.0f;
+            if (e < xn) {
+                const int cc = e % wcols, q = e / wcols;
+                const int rr = q % srows, ci = q / srows;
+                const int r = r0 - 1 + rr, c = cc - 1;
+                xslot[u] = ci * pt.plane + rr * pt.wp + cc;
+                if (r >= 0 && r < g.h && c >= 0 && c < g.w)
+                    xval[u] = x[((int64_t(n) * g.cin + ci) * g.h + r) * g.w + c];
+            }
+        }
+        int wslot[5];
+        float wval[5];
+#pragma unroll
+        for (int u = 0; u < 5; ++u) {
+            const int e = rd * 5 * NT + u * NT + tid;
+            wslot[u] = -1;
+            wval[u] = 0.0f;
+            if (e < wn) {
+                const int tap = e % 9, q = e / 9;   // e = (co cin + ci) 9 + tap
+                const int ci = q % g.cin, co = q / g.cin;
+                wval[u] = wt[e];
+                wslot[u] = (co * (pt.cinp / CG) + ci / CG) * tap_pitch<CG>() + tap * CG + ci % CG;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            if (cslot[u] >= 0) gs[cslot[u]] = cval[u];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            if (xslot[u] >= 0) xs[xslot[u]] = xval[u];
+#pragma unroll
+        for (int u = 0; u < 5; ++u)
+            if (wslot[u] >= 0) {
+                ws[wslot[u]] = wval[u];
+                nonfinite |= !isfinite(wval[u]);
+            }
+    }
+    const bool fast = !__syncthreads_or(nonfinite);
+
+    if (tid < pt.dx_threads) {
+        if (fast)
+            pool_tile_dx<CG, true>(gs, ws, dx, g, pt, n, r0, rows, tid, pt.dx_threads);
+        else
+            pool_tile_dx<CG, false>(gs, ws, dx, g, pt, n, r0, rows, tid, pt.dx_threads);
+    }
+    if (!want_dw) return;   // uniform across the block
+
+    const int K1 = g.k + 1;
+    const int tiles_k = (K1 + CT - 1) / CT, tiles = ((g.cout + CT - 1) / CT) * tiles_k;
+    const int wtid = tid - pt.dx_threads;
+    if (wtid >= 0 && wtid < tiles * pt.pg) {
+        const int t = wtid % tiles, pgi = wtid / tiles;
+        const int co_base = (t / tiles_k) * CT, k_base = (t % tiles_k) * CT;
+        int xoff[CT];   // plane offset of column k: an input plane, the ones or the zero plane
+#pragma unroll
+        for (int kk = 0; kk < CT; ++kk) {
+            const int k = k_base + kk;
+            if (k < g.k) {
+                const int ci = k / 9, ij = k - ci * 9;
+                const int i = ij / 3, j = ij - i * 3;
+                xoff[kk] = ci * pt.plane + i * pt.wp + j;
+            } else {
+                xoff[kk] = (k == g.k ? g.cin : g.cin + 1) * pt.plane;
+            }
+        }
+        const float* gq = gs + co_base * pt.plane + pt.wp + 1;
+        float acc[CT][CT];
+#pragma unroll
+        for (int q = 0; q < CT; ++q)
+#pragma unroll
+            for (int kk = 0; kk < CT; ++kk) acc[q][kk] = 0.0f;
+        // Position p of the tile (row p / W, column p % W) sits at p + (p / W)(wp - W)
+        // in a plane; the row is (p + 1/2) * RN(1 / W) rounded down, exact for
+        // p < 2^22 / rows.
+        const int np = rows * g.w, skip = pt.wp - g.w;
+        const float inv_w = 1.0f / float(g.w);
+        const auto at = [&](int q) { return q + int((float(q) + 0.5f) * inv_w) * skip; };
+        // Positions pgi, pgi + pg, ... in that order, two per round of LDS reads.
+        int p = pgi;
+        for (; p + pt.pg < np; p += 2 * pt.pg) {
+            const int pix0 = at(p), pix1 = at(p + pt.pg);
+            float xv[2][CT], dv[2][CT];
+#pragma unroll
+            for (int kk = 0; kk < CT; ++kk) {
+                xv[0][kk] = xs[xoff[kk] + pix0];
+                xv[1][kk] = xs[xoff[kk] + pix1];
+            }
+#pragma unroll
+            for (int q = 0; q < CT; ++q) {
+                dv[0][q] = gq[q * pt.plane + pix0];
+                dv[1][q] = gq[q * pt.plane + pix1];
+            }
+#pragma unroll
+            for (int q = 0; q < CT; ++q)
+#pragma unroll
+                for (int kk = 0; kk < CT; ++kk) acc[q][kk] = fmaf(dv[0][q], xv[0][kk], acc[q][kk]);
+#pragma unroll
+            for (int q = 0; q < CT; ++q)
+#pragma unroll
+                for (int kk = 0; kk < CT; ++kk) acc[q][kk] = fmaf(dv[1][q], xv[1][kk], acc[q][kk]);
+        }
+        if (p < np) {
+            const int pix = at(p);
+            float xv[CT], dv[CT];
+#pragma unroll
+            for (int kk = 0; kk < CT; ++kk) xv[kk] = xs[xoff[kk] + pix];
+#pragma unroll
+            for (int q = 0; q < CT; ++q) dv[q] = gq[q * pt.plane + pix];
+#pragma unroll
+            for (int q = 0; q < CT; ++q)
+#pragma unroll
+                for (int kk = 0; kk < CT; ++kk) acc[q][kk] = fmaf(dv[q], xv[kk], acc[q][kk]);
+        }
+        float* r = red + (pgi * tiles + t) * (CT * CT);
+#pragma unroll
+        for (int q = 0; q < CT; ++q)
+#pragma unroll
+            for (int kk = 0; kk < CT; ++kk) r[q * CT + kk] = acc[q][kk];
+    }
+    __syncthreads();
+    float* pc = partial + int64_t(blockIdx.x) * g.cout * K1;
+    const int span = tiles * CT * CT;
+    for (int o = tid; o < span; o += NT) {
+        float sum = red[o];
+        for (int g2 = 1; g2 < pt.pg; ++g2) sum += red[g2 * span + o];
+        const int tt = o / (CT * CT), e = o % (CT * CT);
+        const int co = (tt / tiles_k) * CT + e / CT, k = (tt % tiles_k) * CT + e % CT;
+        if (co < g.cout && k < K1) pc[co * K1 + k] = sum;
+    }
+}
+
 // Partial weight and bias gradients of one chunk of P output pixels. The
 // chunk's gradients (cout x P) and columns ((K + 1) x P, the last column all
 // ones so that its row is the bias gradient) are staged in LDS with a padded
@@ -1036,6 +1350,130 @@ int backward_pair(const float* x, const PoolGather& pg, const float* wt, float* 
     return weight_reduce(partial, dweight, dbias, g, chunks, s);
 }
 
+// The fused 3 x 3 tile path: a stride-1, padding-1, 3 x 3 convolution (its
+// output as large as its input) and a tile configuration.
+bool conv3_same(const Geo& g) {
+    return g.kh == 3 && g.kw == 3 && g.stride == 1 && g.pad == 1 && g.oh == g.h && g.ow == g.w;
+}
+
+struct PoolTileCfg {
+    int rows;         // convolution rows per tile (a multiple of pk)
+    int cg, ct, nt;   // input channels per dx thread, weight tile edge, threads per block
+    int dx_threads;   // threads computing dx when dx is wanted
+};
+
+int weight_tiles(const Geo& g, int ct) {
+    return int(ceil_div(g.cout, ct) * ceil_div(g.k + 1, ct));
+}
+
+// Fills `pt` and the LDS bytes for `c`; false when the configuration does not
+// fit (too little LDS, too few weight threads, misaligned rows).
+bool pool_tile_plan(const Geo& g, int pk, const PoolTileCfg& c, bool want_dx, bool want_dw,
+                    PoolTile& pt, size_t& lds) {
+    if (c.rows < pk || c.rows % pk != 0 || c.rows > g.h + pk) return false;
+    pt = PoolTile{};
+    pt.rows = c.rows;
+    pt.tiles = int(ceil_div(g.h, c.rows));
+    pt.dx_threads = want_dx ? c.dx_threads : 0;
+    if (want_dx && (c.dx_threads < 64 || c.dx_threads % 64 != 0 || c.dx_threads > c.nt))
+        return false;
+    const int tiles = weight_tiles(g, c.ct);
+    const int wthreads = c.nt - pt.dx_threads;
+    if (want_dw) {
+        if (tiles > wthreads) return false;
+        pt.pg = wthreads / tiles;
+    }
+    pt.wp = int(odd_h(size_t(g.w) + 2));
+    pt.plane = int(odd_h(size_t(c.rows + 2) * pt.wp));
+    pt.cinp = int(ceil_div(g.cin, c.cg) * c.cg);
+    int64_t off = (want_dw ? ceil_div(g.cout, c.ct) * c.ct : int64_t(g.cout)) * pt.plane;
+    pt.xs_off = int(off);
+    if (want_dw) off += int64_t(g.cin + 2) * pt.plane;
+    off = ceil_div(off, 4) * 4;
+    pt.ws_off = int(off);
+    if (want_dx) off += int64_t(g.cout) * (pt.cinp / c.cg) * ((9 * c.cg + 3) / 4 * 4);
+    pt.red_off = int(off);
+    if (want_dw) off += int64_t(pt.pg) * tiles * c.ct * c.ct;
+    lds = size_t(off) * sizeof(float);
+    return lds <= kTileLds && int64_t(g.n) * pt.tiles <= 0x7fffffff;
+}
+
+template <int CG, int CT, int NT>
+int launch_pool_tile(const float* x, const float* wt, const PoolGather& pg, float* dx,
+                     float* partial, const Geo& g, const PoolTile& pt, size_t lds, hipStream_t s) {
+    EHIP_LAUNCH("conv2d_relu_maxpool_backward", (conv3_pool_backward<CG, CT, NT>),
+                dim3(unsigned(int64_t(g.n) * pt.tiles)), dim3(NT), lds, s, x, wt, pg, dx, partial,
+                g, pt);
+    return EHIP_OK;
+}
+
+template <int CG, int CT>
+int launch_pool_tile_nt(const float* x, const float* wt, const PoolGather& pg, float* dx,
+                        float* partial, const Geo& g, const PoolTile& pt, size_t lds, int nt,
+                        hipStream_t s) {
+    if (nt == 512) return launch_pool_tile<CG, CT, 512>(x, wt, pg, dx, partial, g, pt, lds, s);
+    return launch_pool_tile<CG, CT, 256>(x, wt, pg, dx, partial, g, pt, lds, s);
+}
+
+template <int CG>
+int launch_pool_tile_ct(const float* x, const float* wt, const PoolGather& pg, float* dx,
+                        float* partial, const Geo& g, const PoolTile& pt, size_t lds,
+                        const PoolTileCfg& c, hipStream_t s) {
+    if (c.ct == 4) return launch_pool_tile_nt<CG, 4>(x, wt, pg, dx, partial, g, pt, lds, c.nt, s);
+    if (c.ct == 2) return launch_pool_tile_nt<CG, 2>(x, wt, pg, dx, partial, g, pt, lds, c.nt, s);
+    return launch_pool_tile_nt<CG, 1>(x, wt, pg, dx, partial, g, pt, lds, c.nt, s);
+}
+
+// Input gradient (dx may be null) and weight + bias gradients (dweight may be
+// null) of a fused 3 x 3 block with configuration `c`: one tile launch, then
+// the partials' ordered reduction.
+int pool_tile_backward(const float* x, const PoolGather& pg, const float* wt, float* dx,
+                       float* dweight, float* dbias, const Geo& g, const PoolTileCfg& c,
+                       const PoolTile& pt, size_t lds, hipStream_t s) {
+    const int64_t chunks = int64_t(g.n) * pt.tiles;
+    float* partial = nullptr;
+    if (dweight != nullptr) {
+        partial = static_cast<float*>(scratch(size_t(chunks) * g.cout * (g.k + 1) * sizeof(float)));
+        if (partial == nullptr) return EHIP_ENOMEM;
+    }
+    const int rc = c.cg == 4   ? launch_pool_tile_ct<4>(x, wt, pg, dx, partial, g, pt, lds, c, s)
+                   : c.cg == 2 ? launch_pool_tile_ct<2>(x, wt, pg, dx, partial, g, pt, lds, c, s)
+                               : launch_pool_tile_ct<1>(x, wt, pg, dx, partial, g, pt, lds, c, s);
+    if (rc != EHIP_OK || dweight == nullptr) return rc;
+    return weight_reduce(partial, dweight, dbias, g, chunks, s);
+}
+
+// The tile configuration for a layer: about one 512-thread block per CU
+// (fewer rows per tile only when the LDS needs it), two input channels per dx
+// thread, the largest weight tile that still gives 16 tiles, and enough dx
+// threads for one item each (measured best for the cfg2 layers over rows
+// 2..8, 1..4 channels per thread, tiles 1..4, 256 or 512 threads and every dx
+// thread count). Returns false when no configuration fits.
+bool pool_tile_choice(const Geo& g, int pk, bool want_dx, bool want_dw, PoolTileCfg& c,
+                      PoolTile& pt, size_t& lds) {
+    c = PoolTileCfg{};
+    c.nt = 512;
+    c.cg = g.cin >= 2 ? 2 : 1;
+    c.ct = 1;
+    for (int t : {4, 2})
+        if (weight_tiles(g, t) >= 16) {
+            c.ct = t;
+            break;
+        }
+    const int64_t per_image = std::min<int64_t>(ceil_div(256, std::max(g.n, 1)), std::max(g.h, 1));
+    int rows = int(ceil_div(ceil_div(g.h, per_image), pk) * pk);
+    for (;;) {
+        c.rows = rows;
+        const int64_t items = int64_t(rows) * g.w * ceil_div(g.cin, c.cg);
+        const int64_t reserve = want_dw ? ceil_div(weight_tiles(g, c.ct), 64) * 64 : 0;
+        const int64_t room = c.nt - reserve;
+        c.dx_threads = !want_dx ? 0 : int(std::max<int64_t>(64, std::min(ceil_div(items, 64) * 64, room)));
+        if (pool_tile_plan(g, pk, c, want_dx, want_dw, pt, lds)) return true;
+        if (rows <= pk) return false;
+        rows = std::max(pk, rows / 2 / pk * pk);
+    }
+}
+
 size_t pool_forward_lds(const Geo& g, int cg, int pk, int pw, int prows) {
     const size_t crows = size_t(prows) * pk;
     const size_t rows_in = (crows - 1) * g.stride + g.kh;
@@ -1204,6 +1642,22 @@ int ehip_conv2d_relu_maxpool_backward_f32(const float* x, const float* weight,
     const PoolGather pg{grad_out, out, argmax, int(pool->kernel_h), int(pool->out_h),
                         int(pool->out_w)};
     hipStream_t s = as_stream(stream);
+    if (!dx && !dweight) return EHIP_OK;
+    if (int64_t(g.n) * g.h * g.w == 0) {
+        if (dweight) {
+            if (int rc = ehip_fill_f32(dweight, int64_t(g.cout) * g.k, 0.0f, s)) return rc;
+            if (dbias) return ehip_fill_f32(dbias, g.cout, 0.0f, s);
+        }
+        return EHIP_OK;
+    }
+    // 3 x 3 "same" convolutions: one tile launch for dx and the weight partials.
+    if (conv3_same(g)) {
+        PoolTileCfg c;
+        PoolTile pt;
+        size_t lds = 0;
+        if (pool_tile_choice(g, pg.pk, dx != nullptr, dweight != nullptr, c, pt, lds))
+            return pool_tile_backward(x, pg, weight, dx, dweight, dbias, g, c, pt, lds, s);
+    }
     if (dx && dweight && input_tiles_fit(g) && weight_bands_fit(g))
         return backward_pair(x, pg, weight, dx, dweight, dbias, g, s);
     if (dx)

@@ -404,15 +404,16 @@ class Backend:
         return out, am
 
     def conv2d_relu_maxpool_backward(self, x, weight, g, out, am, stride, pad, pk, need_dx=True,
-                                     bias=True):
+                                     bias=True, need_dw=True):
         cw, pw = self.conv_relu_pool_windows(x.shape, weight.shape, stride, pad, pk)
         co = weight.shape[0]
         dx = self.f32(x.shape) if need_dx else None
-        dw = self.f32(weight.shape)
-        db = self.f32((co,)) if bias else None
+        dw = self.f32(weight.shape) if need_dw else None
+        db = self.f32((co,)) if bias and need_dw else None
         self.ok(self.lib.ehip_conv2d_relu_maxpool_backward_f32(
             self.p(x), self.p(weight), self.p(g), self.p(out), self.p(am),
-            self.p(dx) if need_dx else None, self.p(dw), self.p(db) if bias else None,
+            self.p(dx) if need_dx else None, self.p(dw) if need_dw else None,
+            self.p(db) if db is not None else None,
             C.byref(cw), co, C.byref(pw), self.stream()), "conv2d_relu_maxpool_backward")
         return dx, dw, db
 

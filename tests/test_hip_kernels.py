@@ -411,7 +411,9 @@ def test_conv2d_direct(hip, orc, shape, co, k, stride, pad, bias):
 
 POOL_CASES = [((64, 1, 28, 28), 8, 3, 1, 1, 2), ((64, 8, 14, 14), 16, 3, 1, 1, 2),
               ((2, 3, 9, 7), 5, 3, 1, 1, 2), ((2, 2, 12, 12), 4, 3, 1, 1, 3),
-              ((3, 2, 11, 10), 3, 2, 2, 0, 2)]
+              ((3, 2, 11, 10), 3, 2, 2, 0, 2), ((1, 1, 5, 5), 2, 3, 1, 1, 2),
+              ((4, 16, 10, 10), 32, 3, 1, 1, 2), ((3, 5, 13, 6), 7, 3, 1, 1, 2),
+              ((2, 3, 8, 9), 6, 3, 1, 1, 4)]
 
 
 @pytest.mark.parametrize("shape,co,k,stride,pad,pk", POOL_CASES)
@@ -447,6 +449,60 @@ def test_conv2d_relu_maxpool_fused(hip, orc, shape, co, k, stride, pad, pk, bias
     g2 = dy.reshape(shape[0], co, -1).transpose(0, 2, 1).reshape(-1, co).astype(np.float64)
     bound = (terms + 2) * 2.0 ** -24 * (np.abs(g2).T @ np.abs(cols)).reshape(w.shape)
     assert np.all(np.abs(host(DW) - (g2.T @ cols).reshape(w.shape)) <= bound + 1e-30)
+
+
+@pytest.mark.parametrize("need", ["dx", "dw", "both"])
+def test_conv2d_relu_maxpool_partial_outputs(hip, need):
+    """The fused backward with only the input gradient or only the weight gradients: dx the
+    same bits as the call that computes both, the weight gradients (whose pixel split follows
+    the threads left to them) within the fp32 summation tolerance, and each repeatable."""
+    print_case("conv-relu-pool partial outputs", need)
+    r = rng(91)
+    x = randn(r, 4, 6, 10, 10)
+    w = randn(r, 12, 6, 3, 3) * 0.5
+    b = randn(r, 12)
+    P, AM = hip.conv2d_relu_maxpool(dev(x), dev(w), dev(b), 1, 1, 2)
+    g = randn(r, *host(P).shape)
+    DX, DW, DB = hip.conv2d_relu_maxpool_backward(dev(x), dev(w), dev(g), P, AM, 1, 1, 2)
+    dx2, dw2, db2 = hip.conv2d_relu_maxpool_backward(dev(x), dev(w), dev(g), P, AM, 1, 1, 2,
+                                                     need_dx=need != "dw", need_dw=need != "dx")
+    if need != "dw":
+        exact(host(dx2), host(DX), "dx")
+    if need != "dx":
+        terms = 4 * 10 * 10
+        ref_close(host(dw2), host(DW), k_tol(terms), "dweight")
+        ref_close(host(db2), host(DB), k_tol(terms), "dbias")
+        _, dw3, db3 = hip.conv2d_relu_maxpool_backward(dev(x), dev(w), dev(g), P, AM, 1, 1, 2,
+                                                       need_dx=need != "dw")
+        exact(host(dw3), host(dw2), "dweight repeat")
+        exact(host(db3), host(db2), "dbias repeat")
+
+
+def test_conv2d_relu_maxpool_nonfinite_weight(hip, orc):
+    """An infinite weight: the input gradient still skips zero output gradients as the
+    reference's product does (no inf * 0), bit for bit against the oracle."""
+    import _compose as K
+    print_case("conv-relu-pool inf weight")
+    r = rng(57)
+    shape, co = (2, 3, 9, 7), 5
+    x = randn(r, *shape)
+    w = randn(r, co, shape[1], 3, 3) * 0.5
+    b = randn(r, co)
+    y, cache = K.conv2d_fwd(orc, x, w, b, 1, 1)
+    ry = orc.relu(y)
+    pooled, am = orc.maxpool(ry, 2, 2)
+    g = randn(r, *pooled.shape)
+    w_inf = w.copy()
+    w_inf[1, 2, 0, 1] = np.inf
+    w_inf[3, 0, 2, 2] = -np.inf
+    cache_inf = (cache[0], cache[1], cache[2], orc.transpose(w_inf.reshape(co, -1)), 1, 1, True)
+    dry = orc.maxpool_backward(am, g, ry.shape)
+    dy = orc.relu_backward(y, dry)
+    dx, _, _ = K.conv2d_bwd(orc, dy, cache_inf)
+    assert np.isinf(dx).any() and not np.isnan(dx).any()
+    DX, _, _ = hip.conv2d_relu_maxpool_backward(dev(x), dev(w_inf), dev(g), dev(pooled),
+                                                dev(am), 1, 1, 2)
+    exact(host(DX), dx, "dx")
 
 
 def test_conv2d_relu_maxpool_refusals(hip):
