@@ -162,9 +162,10 @@ def dominant_kernel(eng, hip, timer, torch):
     """The CNN step's largest kernel by total time (rocprofv3 --kernel-trace --stats of
     this benchmark, profiles/cnn_step_kernels.md): the backward of the fused conv2 block
     (Conv2d 8 -> 16, 3x3, pad 1 -> ReLU -> MaxPool2d 2 on a 64 x 8 x 14 x 14 input) --
-    conv_backward_pair (the input-gradient tiles and the weight-gradient band partials in
-    one launch, the pooled gradient routed through the argmax and the ReLU on the fly) and
-    conv_weight_reduce (the partials' ordered sum) -- timed as that launch pair.
+    conv3_pool_backward (per tile of four rows: the output gradient scattered from the
+    pooled cells into LDS, the input gradient and the weight-gradient partials in one
+    launch) and conv_weight_reduce (the partials' ordered sum) -- timed as that launch
+    pair.
     HBM-bound by its data, latency-bound at this size: algorithmic bytes = x, the pooled
     gradient, the pooled values, the argmax and the weights read once, dx, dW and db
     written once."""
@@ -180,7 +181,7 @@ def dominant_kernel(eng, hip, timer, torch):
         lambda n: eng.repeat_conv_relu_pool_backward(n, x, w, g, out, am, dw, db, cw, pw, dx=dx),
         500, 50)
     work = 4 * (2 * x.numel() + 3 * out.numel() + 2 * w.numel() + b.numel())
-    return roofline("conv_backward_pair<2,4,pool>+conv_weight_reduce (conv2 block dx/dW/db, "
+    return roofline("conv3_pool_backward<2,4,512>+conv_weight_reduce (conv2 block dx/dW/db, "
                     "64x8x14x14, 16 filters 3x3, pool 2)", "hbm", work, sec,
                     committed_traffic("conv2_block_backward"))
 
@@ -269,6 +270,49 @@ def lm_leg(engine_mod, eng, timer, dims, keep_params=False):
            "loss_after": round(tr.loss(), 5)}
     tr.close()
     return rec, p0
+
+
+def bandwidth_large(hip, timer, torch, r):
+    """LayerNorm forward / backward, the bias-gradient column sum, softmax forward /
+    backward and max-pool forward / backward over 2^28-element tensors, with the
+    algorithmic bytes of the cfg 5 legs."""
+    bl = {}
+    n = 1 << 28
+    rows, d = n // 1024, 1024
+    x = torch.randn(rows, d, device="cuda", generator=r)
+    gam = torch.randn(d, device="cuda", generator=r)
+    bet = torch.randn(d, device="cuda", generator=r)
+    sec = timer.time(lambda: hip.layernorm(x, gam, bet), 20, 3)
+    bl[f"layernorm {rows}x{d}"] = roofline("layernorm", "hbm", 12 * n + 4 * rows, sec)
+    _, xh, inv = hip.layernorm(x, gam, bet)
+    sec = timer.time(lambda: hip.layernorm_backward(x, xh, gam, inv), 20, 3)
+    bl[f"layernorm_backward {rows}x{d}"] = roofline("layernorm_backward", "hbm",
+                                                    12 * n + 4 * rows + 8 * d, sec)
+    del x, xh, inv
+    torch.cuda.empty_cache()
+    rows, ff = n // 4096, 4096
+    gb = torch.randn(rows, ff, device="cuda", generator=r)
+    sec = timer.time(lambda: hip.sum_axis(gb, 1, rows, ff), 20, 3)
+    bl[f"bias_grad_sum {rows}x{ff}"] = roofline("sum_axis", "hbm", 4 * n + 4 * ff, sec)
+    del gb
+    sc = torch.randn(n // 512, 512, device="cuda", generator=r)
+    sec = timer.time(lambda: hip.softmax(sc), 20, 3)
+    bl[f"softmax {n // 512}x512"] = roofline("softmax", "hbm", 8 * n, sec)
+    y = hip.softmax(sc)
+    sec = timer.time(lambda: hip.softmax_backward(y, sc), 20, 3)
+    bl[f"softmax_backward {n // 512}x512"] = roofline("softmax_backward", "hbm", 12 * n, sec)
+    del sc, y
+    torch.cuda.empty_cache()
+    im = torch.randn(256, 64, 128, 128, device="cuda", generator=r)
+    pooled, am = hip.maxpool(im, 2, 2)
+    sec = timer.time(lambda: hip.maxpool(im, 2, 2, out=(pooled, am)), 20, 3)
+    bl["maxpool 256x64x128x128 k2"] = roofline("maxpool", "hbm", 6 * n, sec)
+    gp = torch.randn_like(pooled)
+    dim = torch.empty_like(im)
+    sec = timer.time(lambda: hip.maxpool_backward(am, gp, tuple(im.shape), 2, 2, dx=dim), 20, 3)
+    bl["maxpool_backward 256x64x128x128 k2"] = roofline("maxpool_backward", "hbm", 6 * n, sec)
+    del im, pooled, am, gp, dim
+    return bl
 
 
 def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
@@ -362,6 +406,10 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
                                                        6 * im.numel(), sec)
     del im, pooled, am, gp, dim
     out["bandwidth_transformer_shapes"] = bt
+    torch.cuda.empty_cache()
+    # The same kernels at cfg 4's size, 2^28 elements, where the launch's ramp
+    # and tail are a small part of the time.
+    out["bandwidth_2^28"] = bandwidth_large(hip, timer, torch, r)
     torch.cuda.empty_cache()
     # cfg 3 and cfg 5: Transformer training steps.
     for tag, dims in LM_CONFIGS.items():

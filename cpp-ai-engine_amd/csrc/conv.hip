@@ -358,6 +358,159 @@ __global__ __launch_bounds__(kThreads) void conv_relu_pool_tiled(
     }
 }
 
+// Conv2d (3 x 3, stride 1, padding 1) -> ReLU -> MaxPool2d (disjoint pk x pk
+// windows) over a tile of `rows` convolution rows (a multiple of pk) of one
+// image and every output channel. The input rows r0 - 1 .. r0 + rows
+// (zero-padded) and the weights as [k][cout] sit in LDS once for all output
+// channels; one thread per (pixel, group of CG output channels) sums the K
+// products of each channel in k order from zero, skipping zero inputs, then
+// adds the bias (conv_forward_direct's order, bit-identical), and ReLU'd
+// values go to LDS for the pool. When every weight is finite a skipped product
+// a * w, a = +-0, is +-0 and leaves the sum as it is (a sum that starts at +0
+// never becomes -0), so the skip is dropped with the same bits. Each window is
+// then reduced to its first strict maximum in window order
+// (src/conv.cpp:410-442) and written with its flat index into the (N, C, oH,
+// oW) convolution output.
+struct PoolFwdTile {
+    int rows, tiles;     // convolution rows per tile (a multiple of pk), tiles per image
+    int wp, plane;       // LDS row and plane pitch of the input rows (odd)
+    int coutp;           // output channels padded to CG
+    int ws_off, ys_off;  // LDS offsets (floats) of the weights and the ReLU'd outputs
+};
+
+template <int CG, bool FAST>
+__device__ __forceinline__ void pool_fwd_items(const float* xs, const float* ws,
+                                               const float* __restrict__ bias, float* ys,
+                                               const Geo& g, const PoolFwdTile& ft, int rows,
+                                               int first, int step) {
+    const int npx = ft.rows * g.w;
+    const int items = npx * (ft.coutp / CG);
+    for (int it = first; it < items; it += step) {
+        const int cgi = it / npx, p = it - cgi * npx;
+        const int hl = p / g.w, v = p - hl * g.w;
+        if (hl >= rows) continue;
+        float c[CG];
+#pragma unroll
+        for (int q = 0; q < CG; ++q) c[q] = 0.0f;
+        const float* wk = ws + cgi * CG;
+        for (int ci = 0; ci < g.cin; ++ci) {
+            const float* xr = xs + ci * ft.plane + hl * ft.wp + v;
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+#pragma unroll
+                for (int j = 0; j < 3; ++j, wk += ft.coutp) {
+                    const float a = xr[i * ft.wp + j];
+                    float wv[CG];
+                    if constexpr (CG == 4) {
+                        const float4 t = *reinterpret_cast<const float4*>(wk);
+                        wv[0] = t.x; wv[1] = t.y; wv[2] = t.z; wv[3] = t.w;
+                    } else if constexpr (CG == 2) {
+                        const float2 t = *reinterpret_cast<const float2*>(wk);
+                        wv[0] = t.x; wv[1] = t.y;
+                    } else {
+                        wv[0] = wk[0];
+                    }
+#pragma unroll
+                    for (int q = 0; q < CG; ++q) {
+                        const float t = c[q] + a * wv[q];
+                        c[q] = (FAST || a != 0.0f) ? t : c[q];
+                    }
+                }
+        }
+#pragma unroll
+        for (int q = 0; q < CG; ++q) {
+            const int co = cgi * CG + q;
+            if (co >= g.cout) continue;
+            const float y = bias ? c[q] + bias[co] : c[q];
+            ys[(co * ft.rows + hl) * g.w + v] = (0.0f < y) ? y : 0.0f;   // ReLU
+        }
+    }
+}
+
+template <int CG, int NT>
+__global__ __launch_bounds__(NT) void conv3_relu_pool(const float* __restrict__ x,
+                                                      const float* __restrict__ wt,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ pooled,
+                                                      int32_t* __restrict__ argmax, Geo g, int pk,
+                                                      int ph, int pw, PoolFwdTile ft) {
+    extern __shared__ float sm[];
+    const int tid = int(threadIdx.x);
+    const int n = int(blockIdx.x) / ft.tiles, tile = int(blockIdx.x) % ft.tiles;
+    const int r0 = tile * ft.rows;
+    const int rows = min(ft.rows, g.h - r0);
+    const int srows = ft.rows + 2, wcols = g.w + 2;
+    float* xs = sm;                  // [cin][plane]: input rows r0 - 1 .. r0 + rows
+    float* ws = sm + ft.ws_off;      // [K][coutp]
+    float* ys = sm + ft.ys_off;      // [cout][rows][W]
+    const int xn = g.cin * srows * wcols;
+    const int wn = g.k * ft.coutp;
+    bool nonfinite = false;
+    for (int rd = 0; rd * 4 * NT < xn || rd * 4 * NT < wn; ++rd) {
+        float xv[4], wv[4];
+        int xslot[4], wslot[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = rd * 4 * NT + u * NT + tid;
+            xslot[u] = -1;
+            xv[u] = 0.0f;
+            if (e < xn) {
+                const int cc = e % wcols, q = e / wcols;
+                const int rr = q % srows, ci = q / srows;
+                const int r = r0 - 1 + rr, c = cc - 1;
+                xslot[u] = ci * ft.plane + rr * ft.wp + cc;
+                if (r >= 0 && r < g.h && c >= 0 && c < g.w)
+                    xv[u] = x[((int64_t(n) * g.cin + ci) * g.h + r) * g.w + c];
+            }
+            wslot[u] = -1;
+            wv[u] = 0.0f;
+            if (e < wn) {
+                const int co = e % ft.coutp, k = e / ft.coutp;
+                wslot[u] = e;
+                if (co < g.cout) wv[u] = wt[co * g.k + k];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (xslot[u] >= 0) xs[xslot[u]] = xv[u];
+            if (wslot[u] >= 0) {
+                ws[wslot[u]] = wv[u];
+                nonfinite |= !isfinite(wv[u]);
+            }
+        }
+    }
+    const bool fast = !__syncthreads_or(nonfinite);
+    if (fast)
+        pool_fwd_items<CG, true>(xs, ws, bias, ys, g, ft, rows, tid, NT);
+    else
+        pool_fwd_items<CG, false>(xs, ws, bias, ys, g, ft, rows, tid, NT);
+    __syncthreads();
+    const int pr0 = r0 / pk;
+    const int prn = max(min(pr0 + ft.rows / pk, ph) - pr0, 0);
+    const int nwin = g.cout * prn * pw;
+    for (int e = tid; e < nwin; e += NT) {
+        const int pc = e % pw, q = e / pw;
+        const int prl = q % prn, co = q / prn;
+        float best = 0.0f;
+        int bi = 0, bj = 0;
+        bool found = false;
+        for (int i = 0; i < pk; ++i)
+            for (int j = 0; j < pk; ++j) {
+                const float v = ys[(co * ft.rows + prl * pk + i) * g.w + pc * pk + j];
+                if (!found || v > best) {
+                    best = v;
+                    bi = i;
+                    bj = j;
+                    found = true;
+                }
+            }
+        const int64_t plane_c = int64_t(n) * g.cout + co;
+        const int64_t o = (plane_c * ph + pr0 + prl) * pw + pc;
+        pooled[o] = best;
+        argmax[o] = int32_t((plane_c * g.oh + r0 + prl * pk + bi) * g.ow + pc * pk + bj);
+    }
+}
+
 // A ReLU and a max pool with disjoint pk x pk windows after the convolution
 // (Conv2d -> ReLU -> MaxPool2d fused): the pooled output, its gradient and the
 // argmax (flat index into the convolution's output) replace the convolution's
@@ -1474,6 +1627,69 @@ bool pool_tile_choice(const Geo& g, int pk, bool want_dx, bool want_dw, PoolTile
     }
 }
 
+// The 3 x 3 forward tile: `rows` convolution rows per block, CG output
+// channels per thread. False when it does not fit the LDS budget.
+bool pool_fwd_plan(const Geo& g, int pk, int rows, int cg, PoolFwdTile& ft, size_t& lds) {
+    if (rows < pk || rows % pk != 0 || rows > g.h + pk) return false;
+    ft = PoolFwdTile{};
+    ft.rows = rows;
+    ft.tiles = int(ceil_div(g.h, rows));
+    ft.wp = int(odd_h(size_t(g.w) + 2));
+    ft.plane = int(odd_h(size_t(rows + 2) * ft.wp));
+    ft.coutp = int(ceil_div(g.cout, cg) * cg);
+    int64_t off = ceil_div(int64_t(g.cin) * ft.plane, 4) * 4;
+    ft.ws_off = int(off);
+    off += int64_t(g.k) * ft.coutp;
+    ft.ys_off = int(off);
+    off += int64_t(g.cout) * rows * g.w;
+    lds = size_t(off) * sizeof(float);
+    return lds <= kTileLds && int64_t(g.n) * ft.tiles <= 0x7fffffff;
+}
+
+template <int CG, int NT>
+int launch_pool_fwd(const float* x, const float* wt, const float* bias, float* pooled,
+                    int32_t* argmax, const Geo& g, int pk, int ph, int pw, const PoolFwdTile& ft,
+                    size_t lds, hipStream_t s) {
+    EHIP_LAUNCH("conv2d_relu_maxpool", (conv3_relu_pool<CG, NT>),
+                dim3(unsigned(int64_t(g.n) * ft.tiles)), dim3(NT), lds, s, x, wt, bias, pooled,
+                argmax, g, pk, ph, pw, ft);
+    return EHIP_OK;
+}
+
+int pool_fwd_launch(const float* x, const float* wt, const float* bias, float* pooled,
+                    int32_t* argmax, const Geo& g, int pk, int ph, int pw, const PoolFwdTile& ft,
+                    size_t lds, int cg, int nt, hipStream_t s) {
+    if (nt == 256) {
+        if (cg == 4) return launch_pool_fwd<4, 256>(x, wt, bias, pooled, argmax, g, pk, ph, pw, ft, lds, s);
+        if (cg == 2) return launch_pool_fwd<2, 256>(x, wt, bias, pooled, argmax, g, pk, ph, pw, ft, lds, s);
+        return launch_pool_fwd<1, 256>(x, wt, bias, pooled, argmax, g, pk, ph, pw, ft, lds, s);
+    }
+    if (cg == 4) return launch_pool_fwd<4, 512>(x, wt, bias, pooled, argmax, g, pk, ph, pw, ft, lds, s);
+    if (cg == 2) return launch_pool_fwd<2, 512>(x, wt, bias, pooled, argmax, g, pk, ph, pw, ft, lds, s);
+    return launch_pool_fwd<1, 512>(x, wt, bias, pooled, argmax, g, pk, ph, pw, ft, lds, s);
+}
+
+// Rows per tile for about one 512-thread block per CU (fewer when the LDS
+// needs it) and the fewest output channels per thread that keep a tile's
+// items within the block (measured best for the cfg2 layers over rows 2..8,
+// 1..4 channels per thread and 256 or 512 threads). Returns the rows, or 0
+// when no tile fits.
+int pool_fwd_choice(const Geo& g, int pk, int& cg, PoolFwdTile& ft, size_t& lds) {
+    const int64_t per_image = std::min<int64_t>(ceil_div(256, std::max(g.n, 1)), std::max(g.h, 1));
+    int rows = int(ceil_div(ceil_div(g.h, per_image), pk) * pk);
+    for (;;) {
+        cg = 4;
+        for (int c : {1, 2})
+            if (int64_t(rows) * g.w * ceil_div(g.cout, c) <= 512) {
+                cg = c;
+                break;
+            }
+        if (pool_fwd_plan(g, pk, rows, cg, ft, lds)) return rows;
+        if (rows <= pk) return 0;
+        rows = std::max(pk, rows / 2 / pk * pk);
+    }
+}
+
 size_t pool_forward_lds(const Geo& g, int cg, int pk, int pw, int prows) {
     const size_t crows = size_t(prows) * pk;
     const size_t rows_in = (crows - 1) * g.stride + g.kh;
@@ -1617,6 +1833,15 @@ int ehip_conv2d_relu_maxpool_f32(const float* x, const float* weight, const floa
     const int pk = int(pool->kernel_h), ph = int(pool->out_h), pw = int(pool->out_w);
     if (int64_t(g.n) * g.cout * ph * pw == 0) return EHIP_OK;
     hipStream_t s = as_stream(stream);
+    // 3 x 3 "same" convolutions: every output channel of a tile in one block.
+    if (conv3_same(g)) {
+        PoolFwdTile ft;
+        size_t lds = 0;
+        int cgf = 0;
+        const int rows = pool_fwd_choice(g, pk, cgf, ft, lds);
+        if (rows > 0)
+            return pool_fwd_launch(x, weight, bias, out, argmax, g, pk, ph, pw, ft, lds, cgf, 512, s);
+    }
     const int cg = g.cout >= 3 ? 4 : g.cout;
     if (cg == 4) return pool_forward_tiled<4>(x, weight, bias, out, argmax, g, pk, ph, pw, s);
     if (cg == 2) return pool_forward_tiled<2>(x, weight, bias, out, argmax, g, pk, ph, pw, s);
