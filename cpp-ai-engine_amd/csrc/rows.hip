@@ -276,14 +276,17 @@ __global__ __launch_bounds__(Group<T>::kBlock, Group<T>::kMinWaves) void xent_ro
 // from the lane that holds it), the row losses kept in LDS, then mean_rows'
 // tree over them -- the two launches' results bit for bit, in one. The tree
 // starts at half the smallest power of two >= rows: the levels above it only
-// add the zero entries beyond the rows, which leaves every sum as it is.
+// add the zero entries beyond the rows, which leaves every sum as it is. With
+// dlogits, each row's gradient for an upstream gradient of 1 is written too,
+// as xent_backward_from_probs computes it from the stored probabilities.
 constexpr int kXentMeanRows = 1024;
 
 template <int V>
 __global__ __launch_bounds__(1024) void xent_rows_mean(const float* __restrict__ logits,
                                                        const int32_t* __restrict__ targets,
                                                        float* __restrict__ probs,
-                                                       float* __restrict__ loss, int rows,
+                                                       float* __restrict__ loss,
+                                                       float* __restrict__ dlogits, int rows,
                                                        int cols) {
     constexpr int kAhead = 4;
     __shared__ float row_loss[kXentMeanRows];
@@ -318,6 +321,17 @@ __global__ __launch_bounds__(1024) void xent_rows_mean(const float* __restrict__
             frag_softmax(f[u], nullptr, m, sum);  // one wavefront: no LDS in the reduction
             f[u].store(probs + int64_t(r) * cols, cols, lane);
             if (lane == 0) row_loss[r] = valid ? -((xt - m) - logf(sum)) : NAN;
+            if (dlogits != nullptr) {
+                const float scale = 1.0f / static_cast<float>(rows);
+                const int ts = Frag<64, V, false, false>::slot(lane, t);
+#pragma unroll
+                for (int q = 0; q < V; ++q) {
+                    float p = f[u].v[q];
+                    if (q == ts) p -= 1.0f;
+                    f[u].v[q] = p * scale;
+                }
+                f[u].store(dlogits + int64_t(r) * cols, cols, lane);
+            }
         }
     }
     __syncthreads();
@@ -896,10 +910,10 @@ int ehip_cross_entropy_f32(const float* logits, const int32_t* targets, float* p
     if (rows <= kXentMeanRows && cols <= 128) {
         if (cols <= 64)
             EHIP_LAUNCH("cross_entropy", xent_rows_mean<1>, dim3(1), dim3(1024), 0, s, logits,
-                        targets, probs, loss, int(rows), int(cols));
+                        targets, probs, loss, static_cast<float*>(nullptr), int(rows), int(cols));
         else
             EHIP_LAUNCH("cross_entropy", xent_rows_mean<2>, dim3(1), dim3(1024), 0, s, logits,
-                        targets, probs, loss, int(rows), int(cols));
+                        targets, probs, loss, static_cast<float*>(nullptr), int(rows), int(cols));
         return EHIP_OK;
     }
     float* row_loss = static_cast<float*>(scratch(size_t(rows) * sizeof(float)));
@@ -912,6 +926,29 @@ int ehip_cross_entropy_f32(const float* logits, const int32_t* targets, float* p
     }
     if (rc != EHIP_OK) return rc;
     EHIP_LAUNCH("cross_entropy_mean", mean_rows, dim3(1), dim3(1024), 0, s, row_loss, rows, loss);
+    return EHIP_OK;
+}
+
+int ehip_cross_entropy_fused_supported(int64_t rows, int64_t cols) {
+    return rows > 0 && cols > 0 && rows <= kXentMeanRows && cols <= 128 ? 1 : 0;
+}
+
+int ehip_cross_entropy_fused_f32(const float* logits, const int32_t* targets, float* probs,
+                                 float* loss, float* dlogits, int64_t rows, int64_t cols,
+                                 void* stream) {
+    EHIP_READY();
+    if (!ehip_cross_entropy_fused_supported(rows, cols))
+        return fail(EHIP_EINVAL, "cross_entropy_fused: shape %lld x %lld beyond one block",
+                    (long long)rows, (long long)cols);
+    if (!logits || !targets || !probs || !loss || !dlogits)
+        return fail(EHIP_EINVAL, "cross_entropy_fused: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (cols <= 64)
+        EHIP_LAUNCH("cross_entropy_fused", xent_rows_mean<1>, dim3(1), dim3(1024), 0, s, logits,
+                    targets, probs, loss, dlogits, int(rows), int(cols));
+    else
+        EHIP_LAUNCH("cross_entropy_fused", xent_rows_mean<2>, dim3(1), dim3(1024), 0, s, logits,
+                    targets, probs, loss, dlogits, int(rows), int(cols));
     return EHIP_OK;
 }
 

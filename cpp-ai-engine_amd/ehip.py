@@ -120,6 +120,8 @@ _SIGS = {
     "ehip_layernorm_backward_f32": [_vp] * 7 + [_i64, _i64, _vp],
     "ehip_cross_entropy_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "ehip_cross_entropy_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
+    "ehip_cross_entropy_fused_supported": [_i64, _i64],
+    "ehip_cross_entropy_fused_f32": [_vp] * 5 + [_i64, _i64, _vp],
     "ehip_softmax_xent_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
     "ehip_last_error": [],
 }
@@ -501,6 +503,17 @@ class Backend:
                                                 self.p(loss), rows, cols, self.stream()),
                 "cross_entropy")
         return loss, probs
+
+    def cross_entropy_fused(self, logits, targets):
+        """Forward plus the logits' gradient for an upstream gradient of 1 in one launch;
+        returns (loss, probs, dlogits)."""
+        rows, cols = logits.shape
+        probs, loss, dl = self.f32(logits.shape), self.f32((1,)), self.f32(logits.shape)
+        self.ok(self.lib.ehip_cross_entropy_fused_f32(self.p(logits), self.p(targets),
+                                                      self.p(probs), self.p(loss), self.p(dl),
+                                                      rows, cols, self.stream()),
+                "cross_entropy_fused")
+        return loss, probs, dl
 
     def cross_entropy_backward(self, probs, targets, grad):
         rows, cols = probs.shape

@@ -49,6 +49,9 @@ public:
     // True while the buffer is a pending fill of zeros: add_grad uses it to
     // initialise a zeroed gradient without materialising the zeros first.
     bool pending_zero() const noexcept;
+    // True while the buffer is a pending fill of one value (stored in *value):
+    // a kernel that only needs that constant can take it from the host.
+    bool pending_constant(float* value) const noexcept;
 
     // Sets every element to `value` lazily (the reference's assign,
     // src/storage.cpp:253-269): nothing is copied or launched now.

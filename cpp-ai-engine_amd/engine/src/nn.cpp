@@ -184,19 +184,45 @@ Tensor mse_loss(const Tensor& prediction, const Tensor& target) {
 // the loss is read back only when host code asks for it.
 namespace {
 
+// With fused nodes on and a small head, the forward launch also writes the
+// logits' gradient for an upstream gradient of 1; backward hands it over when
+// the loss is the root of backward (its seed is a pending fill of ones, known
+// on the host), saving the seed's fill and the backward launch. Any other
+// upstream gradient takes the backward kernel; the bits are the same.
 Tensor cross_entropy_device(const Tensor& logits, std::shared_ptr<DeviceInts> d_t) {
     const size_t N = logits.shape()[0], C = logits.shape()[1];
     Tensor probs(logits.shape(), 0.0f, false);
     const bool req_g = logits.requires_grad() && autograd::grad_enabled();
     Tensor loss({1}, 0.0f, false);
-    hip::check(ehip_cross_entropy_f32(dptr(logits), d_t->get(), dout(probs), dout(loss),
-                                      int64_t(N), int64_t(C), nullptr),
-               "cross_entropy_loss");
+    Tensor d_unit;
+    bool unit = false;
+    if (req_g && fused_nodes() && ehip_cross_entropy_fused_supported(int64_t(N), int64_t(C))) {
+        d_unit = Tensor(logits.shape(), 0.0f, false);
+        unit = true;
+        hip::check(ehip_cross_entropy_fused_f32(dptr(logits), d_t->get(), dout(probs), dout(loss),
+                                                dout(d_unit), int64_t(N), int64_t(C), nullptr),
+                   "cross_entropy_loss");
+    } else {
+        hip::check(ehip_cross_entropy_f32(dptr(logits), d_t->get(), dout(probs), dout(loss),
+                                          int64_t(N), int64_t(C), nullptr),
+                   "cross_entropy_loss");
+    }
     if (req_g) {
         loss.set_requires_grad(true);
         loss.get_impl()->parents = {logits.get_impl()};
         Tensor logits_copy = logits;
-        loss.get_impl()->backward_fn = [logits_copy, probs, d_t, N, C](const Tensor& g) mutable {
+        loss.get_impl()->backward_fn = [logits_copy, probs, d_t, N, C, d_unit,
+                                        unit](const Tensor& g) mutable {
+            float seed = 0.0f;
+            if (unit && g.storage().pending_constant(&seed) && seed == 1.0f) {
+                // Handed over (not shared), so add_grad can adopt the buffer; a
+                // second backward over the graph takes the kernel below.
+                Tensor d = std::move(d_unit);
+                d_unit = Tensor();
+                unit = false;
+                logits_copy.add_grad(d);
+                return;
+            }
             Tensor dX(logits_copy.shape(), 0.0f, false);
             hip::check(ehip_cross_entropy_backward_f32(dptr(probs), d_t->get(), dout(dX),
                                                        int64_t(N), int64_t(C), dptr(g), nullptr),

@@ -114,6 +114,12 @@ bool Storage::resident_on_device() const noexcept { return buf_ && buf_->device_
 
 bool Storage::exclusive() const noexcept { return buf_ && buf_.use_count() == 1; }
 
+bool Storage::pending_constant(float* value) const noexcept {
+    if (!buf_ || !buf_->pending || buf_->device_valid || buf_->host_valid) return false;
+    if (value != nullptr) *value = buf_->fill_value;
+    return true;
+}
+
 bool Storage::pending_zero() const noexcept {
     return buf_ && buf_->pending && buf_->fill_value == 0.0f &&
            !buf_->device_valid && !buf_->host_valid;

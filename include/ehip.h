@@ -468,6 +468,18 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
 int ehip_cross_entropy_f32(const float* logits, const int32_t* targets, float* probs, float* loss,
                            int64_t rows, int64_t cols, void* stream);
 
+/* ehip_cross_entropy_f32 plus the logits' gradient for an upstream gradient
+ * of 1 (the loss as the root of backward): dlogits = (probs - onehot(target))
+ * / rows, the same bits as ehip_cross_entropy_backward_f32 with grad[0] = 1,
+ * written by the same launch. The forward and backward of
+ * nn::cross_entropy_loss (src/nn.cpp:324-405) for a classifier head; only
+ * shapes ehip_cross_entropy_fused_supported accepts (rows <= 1024, cols <= 128,
+ * one block), others are refused with EHIP_EINVAL. */
+int ehip_cross_entropy_fused_supported(int64_t rows, int64_t cols);
+int ehip_cross_entropy_fused_f32(const float* logits, const int32_t* targets, float* probs,
+                                 float* loss, float* dlogits, int64_t rows, int64_t cols,
+                                 void* stream);
+
 /* dx = (probs - onehot(target)) * (grad[0] / rows), grad a DEVICE scalar (the
  * upstream gradient of the loss). src/nn.cpp:386-405. Bit-exact given probs. */
 int ehip_cross_entropy_backward_f32(const float* probs, const int32_t* targets, float* dx,

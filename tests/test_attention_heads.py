@@ -331,6 +331,20 @@ def test_charlm_training_fused_equals_composed(eng):
     exact(fused[1], comp[1], "weights")
 
 
+@pytest.mark.parametrize("n,c", [(64, 10), (1024, 128), (2048, 121)])
+def test_cross_entropy_fused_equals_composed(eng, n, c):
+    """The loss as the root of backward: with fused nodes the forward launch also writes the
+    logits' gradient and backward hands it over (small heads); the loss and gradient are the
+    bits of the separate forward and backward kernels."""
+    print_case("cross entropy fused vs composed", n, c)
+    r = np.random.default_rng(n + c)
+    logits = randn(r, n, c) * 2
+    t = r.integers(0, c, n)
+    fused, comp = both_graphs(eng, lambda: eng.cross_entropy(logits, t))
+    exact(np.float32(fused[0]), np.float32(comp[0]), "loss")
+    exact(fused[1], comp[1], "dlogits")
+
+
 # ------------------------------------------------------- bias gradient from the dW product
 
 @pytest.mark.parametrize("m,n,k", [(96, 96, 2048), (1024, 1024, 8192), (1024, 4096, 8192),

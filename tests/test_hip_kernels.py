@@ -770,6 +770,29 @@ def test_cross_entropy(hip, orc, rows, cols):
     ref_close(fused, orc.cross_entropy_backward(want_probs, t, 1.0), k_tol(cols), "vs oracle")
 
 
+@pytest.mark.parametrize("rows,cols", [(64, 10), (1024, 128), (1000, 100), (7, 65), (1, 1)])
+def test_cross_entropy_fused_gradient(hip, rows, cols):
+    """The one-launch forward with the logits' gradient for an upstream gradient of 1: loss
+    and probabilities as ehip_cross_entropy_f32 gives them, the gradient as the backward
+    kernel gives it from those probabilities with grad 1, bit for bit; an out-of-range label
+    still makes the loss NaN and subtracts nothing."""
+    print_case("xent-fused", rows, cols)
+    r = rng(rows * 5 + cols)
+    logits = dev(randn(r, rows, cols) * 2)
+    t = r.integers(0, cols, rows).astype(np.int32)
+    if rows > 2:
+        t[1] = cols + 3
+    T = dev(t)
+    loss, probs = hip.cross_entropy(logits, T)
+    loss2, probs2, dl = hip.cross_entropy_fused(logits, T)
+    exact(host(probs2), host(probs), "probs")
+    exact(host(loss2), host(loss), "loss")
+    one = dev(np.ones(1, np.float32))
+    exact(host(dl), host(hip.cross_entropy_backward(probs, T, one)), "dlogits")
+    assert hip.lib.ehip_cross_entropy_fused_supported(1025, 10) == 0
+    assert hip.lib.ehip_cross_entropy_fused_supported(64, 129) == 0
+
+
 def test_cross_entropy_bad_label_is_nan(hip):
     print_case("xent-bad-label")
     logits = dev(np.zeros((2, 4), np.float32))
