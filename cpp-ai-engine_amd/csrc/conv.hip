@@ -1220,15 +1220,15 @@ __global__ __launch_bounds__(kThreads) void conv_weight_partial(const float* __r
 // out[o] = sum over chunks of partial[chunk][o] in a fixed order: rl lanes per
 // output take chunks l, l + rl, ... and lane results are added in lane order.
 // Outputs o = co (K + 1) + k go to dw[co][k] for k < K and to db[co] for k == K.
-__global__ __launch_bounds__(256) void conv_weight_reduce(const float* __restrict__ partial,
-                                                          float* __restrict__ dw,
-                                                          float* __restrict__ db, int cout,
-                                                          int k, int chunks, int rl) {
-    __shared__ float lanes[256];
+// bx is the block's index among the 256-thread blocks of this reduction.
+__device__ __forceinline__ void weight_reduce_block(const float* __restrict__ partial,
+                                                    float* __restrict__ dw,
+                                                    float* __restrict__ db, int cout, int k,
+                                                    int chunks, int rl, int bx, float* lanes) {
     const int K1 = k + 1, O = cout * K1;
     const int cw = 256 / rl;
     const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
-    const int o = int(blockIdx.x) * cw + cl;
+    const int o = bx * cw + cl;
     float acc = 0.0f;
     if (o < O && lane < chunks) {
         const float* p = partial + o + int64_t(lane) * O;
@@ -1256,6 +1256,40 @@ __global__ __launch_bounds__(256) void conv_weight_reduce(const float* __restric
         else if (db != nullptr)
             db[co] = sum;
     }
+}
+
+__global__ __launch_bounds__(256) void conv_weight_reduce(const float* __restrict__ partial,
+                                                          float* __restrict__ dw,
+                                                          float* __restrict__ db, int cout,
+                                                          int k, int chunks, int rl) {
+    __shared__ float lanes[256];
+    weight_reduce_block(partial, dw, db, cout, k, chunks, rl, int(blockIdx.x), lanes);
+}
+
+// Several layers' reductions in one launch: job j owns blocks [first, next
+// job's first), each with the rl of its own chunk count -- the same sums as
+// one conv_weight_reduce per job.
+constexpr int kMaxReduceJobs = 16;
+
+struct ReduceJob {
+    const float* partial;
+    float* dw;
+    float* db;
+    int cout, k, chunks, rl, first;
+};
+
+struct ReduceBatch {
+    ReduceJob job[kMaxReduceJobs];
+    int count;
+};
+
+__global__ __launch_bounds__(256) void conv_weight_reduce_batch(ReduceBatch b) {
+    __shared__ float lanes[256];
+    int j = 0;
+    while (j + 1 < b.count && int(blockIdx.x) >= b.job[j + 1].first) ++j;
+    const ReduceJob& r = b.job[j];
+    weight_reduce_block(r.partial, r.dw, r.db, r.cout, r.k, r.chunks, r.rl,
+                        int(blockIdx.x) - r.first, lanes);
 }
 
 constexpr size_t kTileLds = 48 * 1024;   // bytes of LDS per tiled block
@@ -1395,11 +1429,16 @@ int launch_band(const float* x, const float* gout, const PoolGather& pg, float* 
 }
 
 // dweight / dbias from the per-band (or per-chunk) partials, in chunk order.
+int reduce_lanes(int64_t chunks) {
+    int rl = 1;
+    while (rl < 16 && rl * 8 < chunks) rl *= 2;
+    return rl;
+}
+
 int weight_reduce(const float* partial, float* dweight, float* dbias, const Geo& g,
                   int64_t chunks, hipStream_t s) {
     const int O = g.cout * (g.k + 1);
-    int rl = 1;
-    while (rl < 16 && rl * 8 < chunks) rl *= 2;
+    const int rl = reduce_lanes(chunks);
     const int per_block = 256 / rl;
     EHIP_LAUNCH("conv2d_weight_reduce", conv_weight_reduce, dim3(unsigned(ceil_div(O, per_block))),
                 dim3(256), 0, s, partial, dweight, dbias, g.cout, g.k, int(chunks), rl);
@@ -1577,6 +1616,14 @@ int launch_pool_tile_ct(const float* x, const float* wt, const PoolGather& pg, f
     return launch_pool_tile_nt<CG, 1>(x, wt, pg, dx, partial, g, pt, lds, c.nt, s);
 }
 
+int pool_tile_launch(const float* x, const PoolGather& pg, const float* wt, float* dx,
+                     float* partial, const Geo& g, const PoolTileCfg& c, const PoolTile& pt,
+                     size_t lds, hipStream_t s) {
+    return c.cg == 4   ? launch_pool_tile_ct<4>(x, wt, pg, dx, partial, g, pt, lds, c, s)
+           : c.cg == 2 ? launch_pool_tile_ct<2>(x, wt, pg, dx, partial, g, pt, lds, c, s)
+                       : launch_pool_tile_ct<1>(x, wt, pg, dx, partial, g, pt, lds, c, s);
+}
+
 // Input gradient (dx may be null) and weight + bias gradients (dweight may be
 // null) of a fused 3 x 3 block with configuration `c`: one tile launch, then
 // the partials' ordered reduction.
@@ -1589,9 +1636,7 @@ int pool_tile_backward(const float* x, const PoolGather& pg, const float* wt, fl
         partial = static_cast<float*>(scratch(size_t(chunks) * g.cout * (g.k + 1) * sizeof(float)));
         if (partial == nullptr) return EHIP_ENOMEM;
     }
-    const int rc = c.cg == 4   ? launch_pool_tile_ct<4>(x, wt, pg, dx, partial, g, pt, lds, c, s)
-                   : c.cg == 2 ? launch_pool_tile_ct<2>(x, wt, pg, dx, partial, g, pt, lds, c, s)
-                               : launch_pool_tile_ct<1>(x, wt, pg, dx, partial, g, pt, lds, c, s);
+    const int rc = pool_tile_launch(x, pg, wt, dx, partial, g, c, pt, lds, s);
     if (rc != EHIP_OK || dweight == nullptr) return rc;
     return weight_reduce(partial, dweight, dbias, g, chunks, s);
 }
@@ -1888,6 +1933,82 @@ int ehip_conv2d_relu_maxpool_backward_f32(const float* x, const float* weight,
     if (dx)
         if (int rc = backward_input<true>(nullptr, pg, weight, dx, g, s)) return rc;
     if (dweight) return backward_weight<true>(x, nullptr, pg, dweight, dbias, g, s);
+    return EHIP_OK;
+}
+
+int64_t ehip_conv2d_relu_maxpool_partials(const ehip_window_t* conv, int64_t out_channels,
+                                          const ehip_window_t* pool, int want_dx,
+                                          int64_t* chunks) {
+    if (chunks != nullptr) *chunks = 0;
+    if (!ehip_conv2d_relu_maxpool_supported(conv, out_channels, pool)) return 0;
+    if (check_window("conv2d_relu_maxpool_partials", conv) != EHIP_OK ||
+        check_window("conv2d_relu_maxpool_partials", pool) != EHIP_OK)
+        return 0;
+    const Geo g = geo_of(*conv, out_channels);
+    if (!conv3_same(g) || int64_t(g.n) * g.h * g.w == 0) return 0;
+    PoolTileCfg c;
+    PoolTile pt;
+    size_t lds = 0;
+    if (!pool_tile_choice(g, int(pool->kernel_h), want_dx != 0, true, c, pt, lds)) return 0;
+    const int64_t ch = int64_t(g.n) * pt.tiles;
+    if (chunks != nullptr) *chunks = ch;
+    return ch * g.cout * (g.k + 1);
+}
+
+int ehip_conv2d_relu_maxpool_backward_partials_f32(
+    const float* x, const float* weight, const float* grad_out, const float* out,
+    const int32_t* argmax, float* dx, float* partials, int64_t chunks, const ehip_window_t* conv,
+    int64_t out_channels, const ehip_window_t* pool, void* stream) {
+    EHIP_READY();
+    const char* name = "conv2d_relu_maxpool_backward_partials";
+    if (int rc = check_conv(name, conv, out_channels)) return rc;
+    if (int rc = check_pool(name, conv, out_channels, pool)) return rc;
+    if (!x || !weight || !grad_out || !out || !argmax || !partials)
+        return fail(EHIP_EINVAL, "%s: null pointer", name);
+    const Geo g = geo_of(*conv, out_channels);
+    PoolTileCfg c;
+    PoolTile pt;
+    size_t lds = 0;
+    if (!fused_fits(g, *pool) || !conv3_same(g) || int64_t(g.n) * g.h * g.w == 0 ||
+        !pool_tile_choice(g, int(pool->kernel_h), dx != nullptr, true, c, pt, lds))
+        return fail(EHIP_EINVAL, "%s: the layer has no tile partials "
+                    "(ehip_conv2d_relu_maxpool_partials returned 0)", name);
+    if (chunks != int64_t(g.n) * pt.tiles)
+        return fail(EHIP_EINVAL, "%s: %lld chunks given, the tile plan has %lld", name,
+                    (long long)chunks, (long long)(int64_t(g.n) * pt.tiles));
+    const PoolGather pg{grad_out, out, argmax, int(pool->kernel_h), int(pool->out_h),
+                        int(pool->out_w)};
+    return pool_tile_launch(x, pg, weight, dx, partials, g, c, pt, lds, as_stream(stream));
+}
+
+int ehip_conv_weight_reduce_f32(const ehip_conv_reduce_t* jobs, int count, void* stream) {
+    EHIP_READY();
+    if (count < 0 || (count > 0 && jobs == nullptr))
+        return fail(EHIP_EINVAL, "conv_weight_reduce: bad job list");
+    hipStream_t s = as_stream(stream);
+    for (int first = 0; first < count; first += kMaxReduceJobs) {
+        ReduceBatch b{};
+        int64_t blocks = 0;
+        for (int j = first; j < count && b.count < kMaxReduceJobs; ++j) {
+            const ehip_conv_reduce_t& q = jobs[j];
+            if (!q.partials || !q.dweight || q.chunks <= 0 || q.out_channels <= 0 || q.k <= 0 ||
+                q.chunks > 0x7fffffff || q.out_channels * (q.k + 1) > 0x7fffffff)
+                return fail(EHIP_EINVAL, "conv_weight_reduce: bad job %d", j);
+            ReduceJob& r = b.job[b.count++];
+            r.partial = q.partials;
+            r.dw = q.dweight;
+            r.db = q.dbias;
+            r.cout = int(q.out_channels);
+            r.k = int(q.k);
+            r.chunks = int(q.chunks);
+            r.rl = reduce_lanes(q.chunks);
+            r.first = int(blocks);
+            blocks += ceil_div(q.out_channels * (q.k + 1), 256 / r.rl);
+        }
+        if (blocks > 0x7fffffff) return fail(EHIP_EINVAL, "conv_weight_reduce: too many outputs");
+        EHIP_LAUNCH("conv_weight_reduce", conv_weight_reduce_batch, dim3(unsigned(blocks)),
+                    dim3(256), 0, s, b);
+    }
     return EHIP_OK;
 }
 

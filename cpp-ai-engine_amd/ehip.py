@@ -53,6 +53,12 @@ class TransferStats(C.Structure):
         ("to_device_seconds", C.c_double), ("to_host_seconds", C.c_double)]
 
 
+class ConvReduce(C.Structure):
+    """ehip_conv_reduce_t: one layer's weight partials and where their sums go."""
+    _fields_ = [("partials", C.c_void_p), ("chunks", C.c_int64), ("out_channels", C.c_int64),
+                ("k", C.c_int64), ("dweight", C.c_void_p), ("dbias", C.c_void_p)]
+
+
 class GemmEx(C.Structure):
     """ehip_gemm_ex_t: two-level batch strides and the alpha / addend / beta epilogue."""
     _fields_ = [("trans_a", C.c_int), ("trans_b", C.c_int), ("batch", C.c_int64),
@@ -109,6 +115,11 @@ _SIGS = {
                                      C.POINTER(Window), _vp],
     "ehip_conv2d_relu_maxpool_backward_f32": [_vp] * 8 + [C.POINTER(Window), _i64,
                                                           C.POINTER(Window), _vp],
+    "ehip_conv2d_relu_maxpool_partials": [C.POINTER(Window), _i64, C.POINTER(Window), _i,
+                                          C.POINTER(_i64)],
+    "ehip_conv2d_relu_maxpool_backward_partials_f32": [_vp] * 7 + [_i64, C.POINTER(Window),
+                                                                   _i64, C.POINTER(Window), _vp],
+    "ehip_conv_weight_reduce_f32": [C.POINTER(ConvReduce), _i, _vp],
     "ehip_select_rows_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "ehip_scatter_add_rows_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i, _vp],
     "ehip_sum_axis_f32": [_vp, _vp, _i64, _i64, _i64, _vp],
@@ -126,6 +137,7 @@ _SIGS = {
     "ehip_last_error": [],
 }
 _RESTYPES = {"ehip_last_error": C.c_char_p, "ehip_kernels_launched": C.c_uint64,
+             "ehip_conv2d_relu_maxpool_partials": C.c_int64,
              "ehip_kernels_failed": C.c_uint64, "ehip_reset_counters": None,
              "ehip_set_enabled": None, "ehip_transfer_stats": None,
              "ehip_reset_transfer_stats": None, "ehip_arena_free": None,
@@ -149,7 +161,7 @@ def header_symbols(path=HEADER):
     """Names of every function include/ehip.h declares."""
     import re
     text = open(path).read()
-    return sorted(set(re.findall(r"^\s*(?:const char\*|int|void|uint64_t)\s+(ehip_\w+)\(", text,
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int|void|uint64_t|int64_t)\s+(ehip_\w+)\(", text,
                                  re.M)))
 
 
@@ -418,6 +430,43 @@ class Backend:
             self.p(db) if db is not None else None,
             C.byref(cw), co, C.byref(pw), self.stream()), "conv2d_relu_maxpool_backward")
         return dx, dw, db
+
+    def conv2d_relu_maxpool_partials(self, x, weight, g, out, am, stride, pad, pk,
+                                     need_dx=True):
+        """The tile kernel alone: returns (dx, partials, chunks), or None when the layer has
+        no tile path."""
+        cw, pw = self.conv_relu_pool_windows(x.shape, weight.shape, stride, pad, pk)
+        co = weight.shape[0]
+        chunks = C.c_int64(0)
+        n = self.lib.ehip_conv2d_relu_maxpool_partials(C.byref(cw), co, C.byref(pw),
+                                                       int(need_dx), C.byref(chunks))
+        if n == 0:
+            return None
+        dx = self.f32(x.shape) if need_dx else None
+        part = self.f32((n,))
+        self.ok(self.lib.ehip_conv2d_relu_maxpool_backward_partials_f32(
+            self.p(x), self.p(weight), self.p(g), self.p(out), self.p(am),
+            self.p(dx) if need_dx else None, self.p(part), chunks.value, C.byref(cw), co,
+            C.byref(pw), self.stream()), "conv2d_relu_maxpool_backward_partials")
+        return dx, part, chunks.value
+
+    def conv_weight_reduce(self, jobs):
+        """jobs: (partials, chunks, weight_shape, with_bias) per layer; one launch. Returns
+        [(dw, db)]."""
+        arr = (ConvReduce * len(jobs))()
+        outs = []
+        for i, (part, chunks, wshape, with_bias) in enumerate(jobs):
+            dw = self.f32(wshape)
+            db = self.f32((wshape[0],)) if with_bias else None
+            k = 1
+            for d in wshape[1:]:
+                k *= int(d)
+            arr[i] = ConvReduce(self.p(part), chunks, wshape[0], k, self.p(dw),
+                                self.p(db) if with_bias else None)
+            outs.append((dw, db))
+        self.ok(self.lib.ehip_conv_weight_reduce_f32(arr, len(jobs), self.stream()),
+                "conv_weight_reduce")
+        return outs
 
     def dropout(self, x, p, seed, offset=0, want_mask=True):
         y = self.f32(x.shape)

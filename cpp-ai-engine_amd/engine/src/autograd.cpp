@@ -9,6 +9,7 @@
 #include <utility>
 #include <vector>
 
+#include "detail.hpp"
 #include "engine/tensor.hpp"
 
 namespace engine {
@@ -61,18 +62,25 @@ void backward(Tensor& root_tensor) {
     std::vector<std::shared_ptr<TensorImpl>> order = topological_sort(root);
     for (const auto& node : order)
         if (node != root && node->backward_fn) node->grad = nullptr;
-    for (auto it = order.rbegin(); it != order.rend(); ++it) {
-        const auto& node = *it;
-        if (!node->backward_fn || !node->grad) continue;
-        if (node == root) {
-            node->backward_fn(Tensor::from_impl(node->grad));
-        } else {
-            // The gradient is handed over, not shared: inside backward_fn it is
-            // referenced only by the argument, so add_grad can adopt its buffer.
-            const Tensor g = Tensor::from_impl(std::move(node->grad));
-            node->grad = nullptr;
-            node->backward_fn(g);
+    try {
+        for (auto it = order.rbegin(); it != order.rend(); ++it) {
+            const auto& node = *it;
+            if (!node->backward_fn || !node->grad) continue;
+            if (node == root) {
+                node->backward_fn(Tensor::from_impl(node->grad));
+            } else {
+                // The gradient is handed over, not shared: inside backward_fn it is
+                // referenced only by the argument, so add_grad can adopt its buffer.
+                const Tensor g = Tensor::from_impl(std::move(node->grad));
+                node->grad = nullptr;
+                node->backward_fn(g);
+            }
         }
+        // Gradient sums the nodes queued (one launch for all of them).
+        detail::flush_deferred();
+    } catch (...) {
+        detail::drop_deferred();
+        throw;
     }
 }
 

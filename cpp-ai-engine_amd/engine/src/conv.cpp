@@ -268,6 +268,32 @@ bool conv2d_relu_maxpool(const Tensor& input, Conv2d& conv, const MaxPool2d& poo
             if (need_x) dx = Tensor(x_copy.shape(), 0.0f, false);
             if (need_w || need_b) dw = Tensor(w_copy.shape(), 0.0f, false);
             if (need_b) db = Tensor({size_t(co)}, 0.0f, false);
+            // With fused nodes, a layer whose weight (and bias) gradients will be
+            // adopted by add_grad writes only its tile partials now; the sums of
+            // every such layer run in one launch at the end of backward (the same
+            // bits as the one-call backward below).
+            int64_t chunks = 0;
+            const int64_t nparts =
+                fused_nodes() && need_w && detail::grad_adoptable(w_copy) &&
+                        (!need_b || detail::grad_adoptable(b_copy))
+                    ? ehip_conv2d_relu_maxpool_partials(&cw, co, &pw, need_x ? 1 : 0, &chunks)
+                    : 0;
+            if (nparts > 0) {
+                Tensor part({size_t(nparts)}, 0.0f, false);
+                hip::check(ehip_conv2d_relu_maxpool_backward_partials_f32(
+                               dptr(x_copy), dptr(w_copy), dptr(g), pooled.device(),
+                               argmax->get(), need_x ? dout(dx) : nullptr, dout(part), chunks,
+                               &cw, co, &pw, nullptr),
+                           "conv2d_relu_maxpool backward");
+                const ehip_conv_reduce_t job{dptr(part), chunks, co,
+                                             int64_t(w_copy.size()) / co, dout(dw),
+                                             need_b ? dout(db) : nullptr};
+                detail::defer_conv_reduce(job, part);
+                if (need_x) x_copy.add_grad(dx);
+                w_copy.add_grad(dw);
+                if (need_b) b_copy.add_grad(db);
+                return;
+            }
             hip::check(ehip_conv2d_relu_maxpool_backward_f32(
                            dptr(x_copy), dptr(w_copy), dptr(g), pooled.device(), argmax->get(),
                            need_x ? dout(dx) : nullptr, (need_w || need_b) ? dout(dw) : nullptr,

@@ -55,6 +55,21 @@ inline const float* dptr(const Tensor& t) { return t.storage().device(); }
 void add_grad_reshaped(Tensor& target, const Tensor& g);
 inline float* dout(Tensor& t) { return t.storage().device_write(); }
 
+// Gradient work queued during backward and finished together at its end: the
+// weight-gradient sums of fused convolution blocks, one launch for every layer
+// (deferred.cpp). `partials` is kept alive until then. The queue is flushed
+// before anything could read a queued gradient: at the end of
+// autograd::backward and before add_grad accumulates into an existing
+// gradient. A gradient may be queued only when add_grad will adopt its buffer
+// (grad_adoptable).
+void defer_conv_reduce(const ehip_conv_reduce_t& job, const Tensor& partials);
+bool deferred_pending();
+void flush_deferred();
+void drop_deferred();
+// True when add_grad of a fresh, unshared gradient buffer into `target` adopts
+// that buffer (no gradient yet, or a pending zero).
+bool grad_adoptable(const Tensor& target);
+
 // A tensor viewing `src` with a new shape (no copy).
 inline Tensor view_with_shape(const Storage& src, const std::vector<size_t>& shape, bool req) {
     auto impl = std::make_shared<TensorImpl>();

@@ -177,6 +177,8 @@ void detail::add_grad_reshaped(Tensor& target, const Tensor& g) {
         impl_->grad->storage = g.storage().share();
         return;
     }
+    // Accumulating reads the existing gradient and g: finish any queued sums first.
+    if (deferred_pending()) flush_deferred();
     if (!impl_->grad) impl_->grad = std::make_shared<TensorImpl>(shape, 0.0f, false);
     Storage& acc = impl_->grad->storage;
     const float* src = g.storage().device();

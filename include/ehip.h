@@ -387,6 +387,40 @@ int ehip_conv2d_relu_maxpool_backward_f32(const float* x, const float* weight,
                                           int64_t out_channels, const ehip_window_t* pool,
                                           void* stream);
 
+/* The fused block's backward in two parts, so that a caller can reduce the
+ * weight gradients of several layers in one launch (the engine does so at the
+ * end of backward). Together they replace what the entry point above
+ * replaces, with the weight-gradient sums -- the product A^T dC of
+ * src/tensor_ops.cpp:565-586 and the bias fold of src/tensor_detail.hpp:196-204
+ * for the conv node of src/conv.cpp:280-338 -- finished by a separate call.
+ *
+ * ehip_conv2d_relu_maxpool_partials returns the number of floats of weight
+ * partials the layer's tile kernel writes (chunks * out_channels * (K + 1), K =
+ * C_in kH kW; *chunks receives the chunk count), or 0 when the layer has no
+ * tile path (then use ehip_conv2d_relu_maxpool_backward_f32). want_dx says
+ * whether dx will be requested: it can change the tiling.
+ * ehip_conv2d_relu_maxpool_backward_partials_f32 writes dx (may be NULL) and
+ * the partials. ehip_conv_weight_reduce_f32 reduces `count` layers' partials
+ * into dweight / dbias (dbias may be NULL) in one launch; the values are the
+ * bits ehip_conv2d_relu_maxpool_backward_f32 gives. */
+typedef struct ehip_conv_reduce {
+    const float* partials;
+    int64_t chunks;
+    int64_t out_channels;
+    int64_t k;               /* C_in * kH * kW */
+    float* dweight;          /* (out_channels, k) */
+    float* dbias;            /* (out_channels) or NULL */
+} ehip_conv_reduce_t;
+
+int64_t ehip_conv2d_relu_maxpool_partials(const ehip_window_t* conv, int64_t out_channels,
+                                          const ehip_window_t* pool, int want_dx,
+                                          int64_t* chunks);
+int ehip_conv2d_relu_maxpool_backward_partials_f32(
+    const float* x, const float* weight, const float* grad_out, const float* out,
+    const int32_t* argmax, float* dx, float* partials, int64_t chunks, const ehip_window_t* conv,
+    int64_t out_channels, const ehip_window_t* pool, void* stream);
+int ehip_conv_weight_reduce_f32(const ehip_conv_reduce_t* jobs, int count, void* stream);
+
 /* out[i] = x[idx[i]] row by row (rows of row_size floats); an index outside
  * [0, n_rows) yields a row of NaN instead of a read out of bounds.
  * Tensor::select_rows forward (src/tensor.cpp:556-585). Bit-exact. */

@@ -478,6 +478,41 @@ def test_conv2d_relu_maxpool_partial_outputs(hip, need):
         exact(host(db3), host(db2), "dbias repeat")
 
 
+def test_conv2d_relu_maxpool_partials_batched(hip):
+    """The two-part backward (tile partials, then one reduction launch for several layers)
+    gives the bits of the one-call backward, for the cfg2 layers and an odd one, with and
+    without dx and the bias."""
+    print_case("conv-relu-pool partials batched")
+    r = rng(33)
+    layers = [((64, 1, 28, 28), 8, True, False), ((64, 8, 14, 14), 16, True, True),
+              ((3, 5, 13, 6), 7, False, True)]
+    jobs, want = [], []
+    for shape, co, bias, need_dx in layers:
+        x = dev(randn(r, *shape))
+        w = dev(randn(r, co, shape[1], 3, 3) * 0.5)
+        b = dev(randn(r, co))
+        P, AM = hip.conv2d_relu_maxpool(x, w, b, 1, 1, 2)
+        g = dev(randn(r, *host(P).shape))
+        DX, DW, DB = hip.conv2d_relu_maxpool_backward(x, w, g, P, AM, 1, 1, 2,
+                                                      need_dx=need_dx, bias=bias)
+        got = hip.conv2d_relu_maxpool_partials(x, w, g, P, AM, 1, 1, 2, need_dx=need_dx)
+        assert got is not None
+        dx, part, chunks = got
+        if need_dx:
+            exact(host(dx), host(DX), "dx")
+        jobs.append((part, chunks, tuple(w.shape), bias))
+        want.append((DW, DB))
+    for (dw, db), (DW, DB) in zip(hip.conv_weight_reduce(jobs), want):
+        exact(host(dw), host(DW), "dweight")
+        if db is not None:
+            exact(host(db), host(DB), "dbias")
+    # a layer without the tile path reports no partials
+    cw, pw = hip.conv_relu_pool_windows((3, 2, 11, 10), (3, 2, 2, 2), 2, 0, 2)
+    import ctypes
+    assert hip.lib.ehip_conv2d_relu_maxpool_partials(ctypes.byref(cw), 3, ctypes.byref(pw), 1,
+                                                     None) == 0
+
+
 def test_conv2d_relu_maxpool_nonfinite_weight(hip, orc):
     """An infinite weight: the input gradient still skips zero output gradients as the
     reference's product does (no inf * 0), bit for bit against the oracle."""
