@@ -184,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void conv_forward_tiled(const float* __re
                                                                const float* __restrict__ bias,
                                                                float* __restrict__ out, Geo g,
                                                                int rows, int tiles) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const int kh = KH ? KH : g.kh, kw = KW ? KW : g.kw;
     const int n = int(blockIdx.x) / tiles, tile = int(blockIdx.x) % tiles;
     const int co0 = int(blockIdx.y) * CG;
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void conv_relu_pool_tiled(
     const float* __restrict__ x, const float* __restrict__ wt, const float* __restrict__ bias,
     float* __restrict__ pooled, int32_t* __restrict__ argmax, Geo g, int pk, int ph, int pw,
     int prows, int tiles) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const int kh = KH ? KH : g.kh, kw = KW ? KW : g.kw;
     const int n = int(blockIdx.x) / tiles, tile = int(blockIdx.x) % tiles;
     const int co0 = int(blockIdx.y) * CG;
@@ -358,6 +358,27 @@ __global__ __launch_bounds__(kThreads) void conv_relu_pool_tiled(
     }
 }
 
+// n / d for 0 <= n < 2^31 with a multiply-high, an add and a shift instead of
+// a division sequence (Granlund and Montgomery, "Division by invariant
+// integers using multiplication", PLDI 1994): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(n, m) + n) >> l. The sum
+// stays below 2^32 because mulhi(n, m) < n < 2^31. The tile kernels decode
+// their staging and item indices with it.
+struct FastDiv {
+    uint32_t d, m, l;
+};
+
+FastDiv fast_div(uint32_t d) {
+    uint32_t l = 0;
+    while ((uint64_t(1) << l) < d) ++l;
+    const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1;
+    return FastDiv{d, uint32_t(m), l};
+}
+
+__device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
+    return int((__umulhi(uint32_t(n), f.m) + uint32_t(n)) >> f.l);
+}
+
 // Conv2d (3 x 3, stride 1, padding 1) -> ReLU -> MaxPool2d (disjoint pk x pk
 // windows) over a tile of `rows` convolution rows (a multiple of pk) of one
 // image and every output channel. The input rows r0 - 1 .. r0 + rows
@@ -376,6 +397,8 @@ struct PoolFwdTile {
     int wp, plane;       // LDS row and plane pitch of the input rows (odd)
     int coutp;           // output channels padded to CG
     int ws_off, ys_off;  // LDS offsets (floats) of the weights and the ReLU'd outputs
+    // divisors: W + 2, rows + 2, coutp, rows * W, W, pw, rows / pk
+    FastDiv wcols, srows, fcoutp, npx, w, pw, prows;
 };
 
 template <int CG, bool FAST>
@@ -386,8 +409,8 @@ __device__ __forceinline__ void pool_fwd_items(const float* xs, const float* ws,
     const int npx = ft.rows * g.w;
     const int items = npx * (ft.coutp / CG);
     for (int it = first; it < items; it += step) {
-        const int cgi = it / npx, p = it - cgi * npx;
-        const int hl = p / g.w, v = p - hl * g.w;
+        const int cgi = fdiv(it, ft.npx), p = it - cgi * npx;
+        const int hl = fdiv(p, ft.w), v = p - hl * g.w;
         if (hl >= rows) continue;
         float c[CG];
 #pragma unroll
@@ -434,7 +457,7 @@ __global__ __launch_bounds__(NT) void conv3_relu_pool(const float* __restrict__ 
                                                       float* __restrict__ pooled,
                                                       int32_t* __restrict__ argmax, Geo g, int pk,
                                                       int ph, int pw, PoolFwdTile ft) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const int tid = int(threadIdx.x);
     const int n = int(blockIdx.x) / ft.tiles, tile = int(blockIdx.x) % ft.tiles;
     const int r0 = tile * ft.rows;
@@ -455,8 +478,8 @@ __global__ __launch_bounds__(NT) void conv3_relu_pool(const float* __restrict__ 
             xslot[u] = -1;
             xv[u] = 0.0f;
             if (e < xn) {
-                const int cc = e % wcols, q = e / wcols;
-                const int rr = q % srows, ci = q / srows;
+                const int q = fdiv(e, ft.wcols), cc = e - q * wcols;
+                const int ci = fdiv(q, ft.srows), rr = q - ci * srows;
                 const int r = r0 - 1 + rr, c = cc - 1;
                 xslot[u] = ci * ft.plane + rr * ft.wp + cc;
                 if (r >= 0 && r < g.h && c >= 0 && c < g.w)
@@ -465,7 +488,7 @@ __global__ __launch_bounds__(NT) void conv3_relu_pool(const float* __restrict__ 
             wslot[u] = -1;
             wv[u] = 0.0f;
             if (e < wn) {
-                const int co = e % ft.coutp, k = e / ft.coutp;
+                const int k = fdiv(e, ft.fcoutp), co = e - k * ft.coutp;
                 wslot[u] = e;
                 if (co < g.cout) wv[u] = wt[co * g.k + k];
             }
@@ -486,11 +509,13 @@ __global__ __launch_bounds__(NT) void conv3_relu_pool(const float* __restrict__ 
         pool_fwd_items<CG, false>(xs, ws, bias, ys, g, ft, rows, tid, NT);
     __syncthreads();
     const int pr0 = r0 / pk;
-    const int prn = max(min(pr0 + ft.rows / pk, ph) - pr0, 0);
-    const int nwin = g.cout * prn * pw;
+    const int prows = ft.rows / pk;
+    const int prn = max(min(pr0 + prows, ph) - pr0, 0);
+    const int nwin = g.cout * prows * pw;
     for (int e = tid; e < nwin; e += NT) {
-        const int pc = e % pw, q = e / pw;
-        const int prl = q % prn, co = q / prn;
+        const int q = fdiv(e, ft.pw), pc = e - q * pw;
+        const int co = fdiv(q, ft.prows), prl = q - co * prows;
+        if (prl >= prn) continue;
         float best = 0.0f;
         int bi = 0, bj = 0;
         bool found = false;
@@ -660,7 +685,7 @@ template <int CG, bool POOL>
 __global__ __launch_bounds__(kThreads) void conv_backward_input_tiled(
     const float* __restrict__ gout, PoolGather pgat, const float* __restrict__ wt,
     float* __restrict__ dx, Geo g, int rows, int tiles) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     backward_input_block<CG, POOL>(gout, pgat, wt, dx, g, rows, tiles, int(blockIdx.x),
                                    int(blockIdx.y), sm);
 }
@@ -800,7 +825,7 @@ __global__ __launch_bounds__(kThreads) void conv_weight_band(const float* __rest
                                                              PoolGather pgat,
                                                              float* __restrict__ partial, Geo g,
                                                              int rows, int bands) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     weight_band_block<CT, KT, POOL>(x, gout, pgat, partial, g, rows, bands, int(blockIdx.x), sm);
 }
 
@@ -819,7 +844,7 @@ __global__ __launch_bounds__(kThreads) void conv_backward_pair(
     const float* __restrict__ x, const float* __restrict__ gout, PoolGather pgat,
     const float* __restrict__ wt, float* __restrict__ dx, float* __restrict__ partial, Geo g,
     PairGeo pg) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const int b = int(blockIdx.x);
     if (b < pg.in_blocks)
         backward_input_block<CG, POOL>(gout, pgat, wt, dx, g, pg.in_rows, pg.in_tiles,
@@ -862,6 +887,11 @@ struct PoolTile {
     int wp, plane;           // LDS row and plane pitch (odd)
     int cinp;                // input channels padded to CG
     int xs_off, ws_off, red_off;   // LDS offsets (floats) of the input rows, weights, group sums
+    int prows;               // pooled rows a tile's halo can reach: rows / pk + 2
+    int own, cells, cell_off;  // the tile's own pooled rows (rows / pk), cout * own * pw
+                               // cells, LDS offset of their positions and gradients
+    // divisors: pw, prows, W + 2, rows + 2, C_in, rows * W, W
+    FastDiv pw, fprows, wcols, srows, cin, npx, w;
 };
 
 // Weights of one (co, input-channel group) in the tile kernel's LDS: nine taps
@@ -881,8 +911,8 @@ __device__ __forceinline__ void pool_tile_dx(const float* gs, const float* ws, f
     const int groups = pt.cinp / CG;
     const int items = npx * groups;
     for (int it = first; it < items; it += step) {
-        const int cgi = it / npx, p = it - cgi * npx;
-        const int hl = p / g.w, v = p - hl * g.w;
+        const int cgi = fdiv(it, pt.npx), p = it - cgi * npx;
+        const int hl = fdiv(p, pt.w), v = p - hl * g.w;
         if (hl >= rows) continue;
         float d[9][CG];
 #pragma unroll
@@ -940,7 +970,7 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
                                                           PoolGather pgat, float* __restrict__ dx,
                                                           float* __restrict__ partial, Geo g,
                                                           PoolTile pt) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const int tid = int(threadIdx.x);
     const int n = int(blockIdx.x) / pt.tiles, tile = int(blockIdx.x) % pt.tiles;
     const int r0 = tile * pt.rows;
@@ -954,10 +984,22 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
     float* xs = sm + pt.xs_off;
     float* ws = sm + pt.ws_off;       // [cout][cinp / CG][tap_pitch]: tap-major CG channels
     float* red = sm + pt.red_off;     // [pg][tiles][CT * CT]
+    // The tile's own pooled cells ([cout][own][pw]): the position of the argmax
+    // in the tile (row * wp + column) and its gradient when it carries one, else
+    // position 0 and gradient 0 (which adds nothing, see the sums below).
+    int* cpos = reinterpret_cast<int*>(sm + pt.cell_off);
+    float* cgrad = sm + pt.cell_off + pt.cells;
+    __shared__ __align__(16) int flags;   // bit 0: a non-finite weight; bit 1: a non-finite input
 
     // The zero border and every position no pooled cell selects.
     const int zero_n = pt.xs_off;
     for (int e = tid; e < zero_n; e += NT) gs[e] = 0.0f;
+    if (want_dw)
+        for (int e = tid; e < pt.cells; e += NT) {
+            cpos[e] = 0;
+            cgrad[e] = 0.0f;
+        }
+    if (tid == 0) flags = 0;
     if (want_dw)
         for (int e = tid; e < 2 * pt.plane; e += NT)
             xs[g.cin * pt.plane + e] = e < pt.plane ? 1.0f : 0.0f;
@@ -969,25 +1011,27 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
     const int pk = pgat.pk, pw = pgat.pw;
     const int pr_lo = max(r0 / pk - 1, 0), pr_hi = min((r0 + pt.rows) / pk, pgat.ph - 1);
     const int prn = max(pr_hi - pr_lo + 1, 0);
-    const int cells = g.cout * prn * pw;
+    const int cells = g.cout * pt.prows * pw;   // rows prl >= prn are skipped
     const int wcols = g.w + 2;
     const int xn = want_dw ? g.cin * srows * wcols : 0;
     const int wn = want_dx ? g.cout * g.cin * 9 : 0;
     const int64_t oplane = int64_t(g.h) * g.w;
-    bool nonfinite = false;
+    bool nonfinite = false, nonfinite_x = false;
     // One round issues up to 2 cells (3 loads each), 2 input and 5 weight
     // loads per thread before any LDS store.
     for (int rd = 0; rd * 2 * NT < cells || rd * 2 * NT < xn || rd * 5 * NT < wn; ++rd) {
-        int cslot[2];
+        int cslot[2], ccell[2], cpix[2];
         float cval[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int e = rd * 2 * NT + u * NT + tid;
             cslot[u] = -1;
+            ccell[u] = -1;
+            cpix[u] = 0;
             cval[u] = 0.0f;
-            if (e < cells) {
-                const int pc = e % pw, q = e / pw;
-                const int prl = q % prn, co = q / prn;
+            const int q = fdiv(e, pt.pw), pc = e - q * pw;
+            const int co = fdiv(q, pt.fprows), prl = q - co * pt.prows;
+            if (e < cells && prl < prn) {
                 const int pr = pr_lo + prl;
                 const int64_t nc = int64_t(n) * g.cout + co;
                 const int64_t o = (nc * pgat.ph + pr) * pw + pc;
@@ -1002,6 +1046,11 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
                     if (dr < pk && dc < pk && r >= r0 - 1 && r <= r0 + pt.rows) {
                         cslot[u] = co * pt.plane + (r - r0 + 1) * pt.wp + pc * pk + dc + 1;
                         cval[u] = gv;
+                        const int own = pr - r0 / pk;
+                        if (want_dw && own >= 0 && own < pt.own) {
+                            ccell[u] = (co * pt.own + own) * pw + pc;
+                            cpix[u] = (r - r0) * pt.wp + pc * pk + dc;
+                        }
                     }
                 }
             }
@@ -1014,8 +1063,8 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
             xslot[u] = -1;
             xval[u] = 0.0f;
             if (e < xn) {
-                const int cc = e % wcols, q = e / wcols;
-                const int rr = q % srows, ci = q / srows;
+                const int q = fdiv(e, pt.wcols), cc = e - q * wcols;
+                const int ci = fdiv(q, pt.srows), rr = q - ci * srows;
                 const int r = r0 - 1 + rr, c = cc - 1;
                 xslot[u] = ci * pt.plane + rr * pt.wp + cc;
                 if (r >= 0 && r < g.h && c >= 0 && c < g.w)
@@ -1030,18 +1079,26 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
             wslot[u] = -1;
             wval[u] = 0.0f;
             if (e < wn) {
-                const int tap = e % 9, q = e / 9;   // e = (co cin + ci) 9 + tap
-                const int ci = q % g.cin, co = q / g.cin;
+                const int q = e / 9, tap = e - q * 9;   // e = (co cin + ci) 9 + tap
+                const int co = fdiv(q, pt.cin), ci = q - co * g.cin;
                 wval[u] = wt[e];
                 wslot[u] = (co * (pt.cinp / CG) + ci / CG) * tap_pitch<CG>() + tap * CG + ci % CG;
             }
         }
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < 2; ++u) {
             if (cslot[u] >= 0) gs[cslot[u]] = cval[u];
+            if (ccell[u] >= 0) {
+                cpos[ccell[u]] = cpix[u];
+                cgrad[ccell[u]] = cval[u];
+            }
+        }
 #pragma unroll
         for (int u = 0; u < 2; ++u)
-            if (xslot[u] >= 0) xs[xslot[u]] = xval[u];
+            if (xslot[u] >= 0) {
+                xs[xslot[u]] = xval[u];
+                nonfinite_x |= !isfinite(xval[u]);
+            }
 #pragma unroll
         for (int u = 0; u < 5; ++u)
             if (wslot[u] >= 0) {
@@ -1049,7 +1106,10 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
                 nonfinite |= !isfinite(wval[u]);
             }
     }
-    const bool fast = !__syncthreads_or(nonfinite);
+    if (nonfinite || nonfinite_x) atomicOr(&flags, (nonfinite ? 1 : 0) | (nonfinite_x ? 2 : 0));
+    __syncthreads();
+    const int fl = flags;
+    const bool fast = (fl & 1) == 0;
 
     if (tid < pt.dx_threads) {
         if (fast)
@@ -1058,8 +1118,84 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
             pool_tile_dx<CG, false>(gs, ws, dx, g, pt, n, r0, rows, tid, pt.dx_threads);
     }
     if (!want_dw) return;   // uniform across the block
-
     const int K1 = g.k + 1;
+
+    // With every input finite, only the positions that carry a gradient (one per
+    // pooled cell at most) add to the weight and bias sums: a thread owns four
+    // columns k of one output channel and adds the channel's cells in cell order,
+    // four cells per round of LDS reads. A cell without a gradient adds 0 * x =
+    // +-0 (x finite), which leaves a sum that starts at +0 as it is. (A
+    // non-finite input times a zero gradient is NaN in the full sum, so such
+    // tiles take the full sum below.)
+    if ((fl & 2) == 0) {
+        const int wtid = tid - pt.dx_threads, wthreads = NT - pt.dx_threads;
+        const int kt = (K1 + 3) / 4, ncell = pt.own * pgat.pw, stiles = g.cout * kt;
+        // sg cell groups per tile when there are fewer tiles than threads; group
+        // r adds cells r, r + sg, ... and the groups are added in group order.
+        const int sg = max(1, wthreads / stiles);
+        float* pc = partial + int64_t(blockIdx.x) * g.cout * K1;
+        for (int t0 = 0; t0 < stiles; t0 += wthreads) {
+            const int t = sg == 1 ? wtid + t0 : wtid % stiles, grp = sg == 1 ? 0 : wtid / stiles;
+            const bool active = wtid >= 0 && t < stiles && grp < sg;
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const int co = active ? t / kt : 0, k0 = active ? (t - co * kt) * 4 : 0;
+            if (active) {
+                int xoff[4];
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const int k = k0 + kk;
+                    if (k < g.k) {
+                        const int ci = k / 9, ij = k - ci * 9;
+                        const int i = ij / 3, j = ij - i * 3;
+                        xoff[kk] = ci * pt.plane + i * pt.wp + j;
+                    } else {
+                        xoff[kk] = (k == g.k ? g.cin : g.cin + 1) * pt.plane;
+                    }
+                }
+                const int* cp = cpos + co * ncell;
+                const float* cv = cgrad + co * ncell;
+                for (int c0 = grp; c0 < ncell; c0 += 4 * sg) {
+                    int pos[4];
+                    float gv[4], xv[4][4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int c = c0 + u * sg;
+                        pos[u] = c < ncell ? cp[c] : 0;
+                        gv[u] = c < ncell ? cv[c] : 0.0f;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) xv[u][kk] = xs[xoff[kk] + pos[u]];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk)
+                            acc[kk] = fmaf(gv[u], xv[u][kk], acc[kk]);
+                }
+            }
+            if (sg == 1) {
+                if (active)
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk)
+                        if (k0 + kk < K1) pc[co * K1 + k0 + kk] = acc[kk];
+            } else {
+                if (active)
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) red[(grp * stiles + t) * 4 + kk] = acc[kk];
+                __syncthreads();
+                for (int o = tid; o < stiles * 4; o += NT) {
+                    float sum = red[o];
+                    for (int r = 1; r < sg; ++r) sum += red[r * stiles * 4 + o];
+                    const int tt = o / 4, kk = o - tt * 4;
+                    const int cco = tt / kt, k = (tt - cco * kt) * 4 + kk;
+                    if (k < K1) pc[cco * K1 + k] = sum;
+                }
+            }
+        }
+        return;
+    }
+
     const int tiles_k = (K1 + CT - 1) / CT, tiles = ((g.cout + CT - 1) / CT) * tiles_k;
     const int wtid = tid - pt.dx_threads;
     if (wtid >= 0 && wtid < tiles * pt.pg) {
@@ -1153,7 +1289,7 @@ __global__ __launch_bounds__(kThreads) void conv_weight_partial(const float* __r
                                                                 const float* __restrict__ gout,
                                                                 float* __restrict__ partial,
                                                                 Geo g, int P) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     const int ld = P + 1;
     const int K1 = g.k + 1;
     float* dy_s = sm;
@@ -1429,9 +1565,11 @@ int launch_band(const float* x, const float* gout, const PoolGather& pg, float* 
 }
 
 // dweight / dbias from the per-band (or per-chunk) partials, in chunk order.
+// Lanes per output of the partials' reduction: at most eight chunks per lane,
+// so each lane's loads go out in one round.
 int reduce_lanes(int64_t chunks) {
     int rl = 1;
-    while (rl < 16 && rl * 8 < chunks) rl *= 2;
+    while (rl < 64 && rl * 8 < chunks) rl *= 2;
     return rl;
 }
 
@@ -1578,6 +1716,14 @@ bool pool_tile_plan(const Geo& g, int pk, const PoolTileCfg& c, bool want_dx, bo
     pt.wp = int(odd_h(size_t(g.w) + 2));
     pt.plane = int(odd_h(size_t(c.rows + 2) * pt.wp));
     pt.cinp = int(ceil_div(g.cin, c.cg) * c.cg);
+    pt.prows = c.rows / pk + 2;
+    pt.pw = fast_div(uint32_t(std::max(g.w / pk, 1)));
+    pt.fprows = fast_div(uint32_t(pt.prows));
+    pt.wcols = fast_div(uint32_t(g.w + 2));
+    pt.srows = fast_div(uint32_t(c.rows + 2));
+    pt.cin = fast_div(uint32_t(g.cin));
+    pt.npx = fast_div(uint32_t(c.rows * g.w));
+    pt.w = fast_div(uint32_t(g.w));
     int64_t off = (want_dw ? ceil_div(g.cout, c.ct) * c.ct : int64_t(g.cout)) * pt.plane;
     pt.xs_off = int(off);
     if (want_dw) off += int64_t(g.cin + 2) * pt.plane;
@@ -1585,7 +1731,12 @@ bool pool_tile_plan(const Geo& g, int pk, const PoolTileCfg& c, bool want_dx, bo
     pt.ws_off = int(off);
     if (want_dx) off += int64_t(g.cout) * (pt.cinp / c.cg) * ((9 * c.cg + 3) / 4 * 4);
     pt.red_off = int(off);
-    if (want_dw) off += int64_t(pt.pg) * tiles * c.ct * c.ct;
+    if (want_dw)
+        off += std::max<int64_t>(int64_t(pt.pg) * tiles * c.ct * c.ct, 4 * int64_t(wthreads));
+    pt.own = c.rows / pk;
+    pt.cells = want_dw ? g.cout * pt.own * (g.w / pk) : 0;
+    pt.cell_off = int(off);
+    off += 2 * int64_t(pt.cells);
     lds = size_t(off) * sizeof(float);
     return lds <= kTileLds && int64_t(g.n) * pt.tiles <= 0x7fffffff;
 }
@@ -1688,6 +1839,13 @@ bool pool_fwd_plan(const Geo& g, int pk, int rows, int cg, PoolFwdTile& ft, size
     ft.ys_off = int(off);
     off += int64_t(g.cout) * rows * g.w;
     lds = size_t(off) * sizeof(float);
+    ft.wcols = fast_div(uint32_t(g.w + 2));
+    ft.srows = fast_div(uint32_t(rows + 2));
+    ft.fcoutp = fast_div(uint32_t(ft.coutp));
+    ft.npx = fast_div(uint32_t(rows * g.w));
+    ft.w = fast_div(uint32_t(g.w));
+    ft.pw = fast_div(uint32_t(std::max(g.w / pk, 1)));
+    ft.prows = fast_div(uint32_t(rows / pk));
     return lds <= kTileLds && int64_t(g.n) * ft.tiles <= 0x7fffffff;
 }
 

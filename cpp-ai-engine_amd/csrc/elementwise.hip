@@ -353,9 +353,12 @@ struct Adam {
     }
 };
 
-// Multi-tensor Adam: the tensors are cut into chunks of kAdamChunk elements
-// (one chunk per workgroup, kUnroll float4 per thread); a workgroup finds its
-// tensor by binary search over the chunk prefix of the slot table.
+// Multi-tensor Adam: the tensors are cut into chunks of U float4 per thread
+// (one chunk per workgroup: kAdamChunk elements with U = kUnroll, a quarter of
+// that for small models, whose few workgroups would otherwise each update
+// sixteen elements per thread one after another); a workgroup finds its tensor
+// by binary search over the chunk prefix of the slot table. Every element's
+// update is the same whatever the chunking.
 struct AdamSlot {
     float* p;
     const float* g;
@@ -388,24 +391,25 @@ __device__ __forceinline__ AdamSlot find_slot(const Slots& slots, int count, int
     return slots[lo];
 }
 
-template <bool NT>
+template <bool NT, int U>
 __device__ __forceinline__ void adam_chunk(const AdamSlot& s, int64_t b, float lr, float b1,
                                            float b2, float eps, float wd, float c1, float c2) {
     const Adam op{s.p, s.g, s.m, s.v, lr, b1, b2, eps, wd, c1, c2};
-    const int64_t begin = (b - s.first_chunk) * kAdamChunk;
-    const int64_t end = min(begin + kAdamChunk, s.n);
+    constexpr int64_t kChunk = int64_t(kThreads) * U * 4;
+    const int64_t begin = (b - s.first_chunk) * kChunk;
+    const int64_t end = min(begin + kChunk, s.n);
     const bool vec = aligned16(s.p) && aligned16(s.g) && aligned16(s.m) && aligned16(s.v);
     int64_t tail = begin;
     if (vec) {
         const int64_t v0 = begin >> 2, v1 = end >> 2;  // whole float4 vectors in the chunk
-        float4 r[kUnroll][4];
+        float4 r[U][4];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int64_t v = v0 + int64_t(u) * kThreads + threadIdx.x;
             if (v < v1) op.template load<NT>(v, r[u]);
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int64_t v = v0 + int64_t(u) * kThreads + threadIdx.x;
             if (v < v1) op.template store<NT>(v, r[u]);
         }
@@ -419,16 +423,16 @@ __global__ __launch_bounds__(kThreads) void adam_multi(const AdamSlot* __restric
                                                        int count, float lr, float b1, float b2,
                                                        float eps, float wd, float c1, float c2) {
     const int64_t b = blockIdx.x;
-    adam_chunk<NT>(find_slot(slots, count, b), b, lr, b1, b2, eps, wd, c1, c2);
+    adam_chunk<NT, kUnroll>(find_slot(slots, count, b), b, lr, b1, b2, eps, wd, c1, c2);
 }
 
-template <bool NT>
+template <bool NT, int U>
 __global__ __launch_bounds__(kThreads) void adam_multi_inline(AdamInline table, int count,
                                                               float lr, float b1, float b2,
                                                               float eps, float wd, float c1,
                                                               float c2) {
     const int64_t b = blockIdx.x;
-    adam_chunk<NT>(find_slot(table.s, count, b), b, lr, b1, b2, eps, wd, c1, c2);
+    adam_chunk<NT, U>(find_slot(table.s, count, b), b, lr, b1, b2, eps, wd, c1, c2);
 }
 
 template <int OP>
@@ -550,31 +554,46 @@ int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, 
     EHIP_READY();
     if (count < 0 || (count > 0 && tensors == nullptr))
         return fail(EHIP_EINVAL, "adam_multi: bad tensor list");
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        if (tensors[i].n < 0)
+            return fail(EHIP_EINVAL, "adam_multi: tensor %d has a negative size", i);
+        total += tensors[i].n;
+    }
+    // Small models (at most 2^20 parameters in at most kInlineSlots tensors)
+    // take chunks of one float4 per thread.
+    int nonempty = 0;
+    for (int i = 0; i < count; ++i) nonempty += tensors[i].n > 0;
+    const bool small = total <= (int64_t(1) << 20) && nonempty <= kInlineSlots;
+    const int64_t chunk = small ? int64_t(kThreads) * 4 : kAdamChunk;
     std::vector<AdamSlot> slots;
     slots.reserve(size_t(count));
     int64_t chunks = 0;
     for (int i = 0; i < count; ++i) {
         const ehip_adam_tensor_t& t = tensors[i];
-        if (t.n < 0) return fail(EHIP_EINVAL, "adam_multi: tensor %d has a negative size", i);
         if (t.n == 0) continue;
         if (!t.p || !t.g || !t.m || !t.v)
             return fail(EHIP_EINVAL, "adam_multi: tensor %d has a null pointer", i);
         slots.push_back({t.p, t.g, t.m, t.v, t.n, chunks});
-        chunks += ceil_div(t.n, kAdamChunk);
+        chunks += ceil_div(t.n, chunk);
     }
     if (slots.empty()) return EHIP_OK;
     if (chunks > 0x7fffffff) return fail(EHIP_EINVAL, "adam_multi: too many elements");
     hipStream_t s = as_stream(stream);
-    const bool nt = chunks * kAdamChunk >= kNontemporalMin;
+    const bool nt = chunks * chunk >= kNontemporalMin;
     if (slots.size() <= size_t(kInlineSlots)) {
         AdamInline inline_table{};
         std::memcpy(inline_table.s, slots.data(), slots.size() * sizeof(AdamSlot));
-        if (nt)
-            EHIP_LAUNCH("adam_multi", adam_multi_inline<true>, dim3(unsigned(chunks)),
+        if (small)
+            EHIP_LAUNCH("adam_multi", (adam_multi_inline<false, 1>), dim3(unsigned(chunks)),
+                        dim3(kThreads), 0, s, inline_table, int(slots.size()), lr, beta1, beta2,
+                        eps, weight_decay, bias_c1, bias_c2);
+        else if (nt)
+            EHIP_LAUNCH("adam_multi", (adam_multi_inline<true, kUnroll>), dim3(unsigned(chunks)),
                         dim3(kThreads), 0, s, inline_table, int(slots.size()), lr, beta1, beta2,
                         eps, weight_decay, bias_c1, bias_c2);
         else
-            EHIP_LAUNCH("adam_multi", adam_multi_inline<false>, dim3(unsigned(chunks)),
+            EHIP_LAUNCH("adam_multi", (adam_multi_inline<false, kUnroll>), dim3(unsigned(chunks)),
                         dim3(kThreads), 0, s, inline_table, int(slots.size()), lr, beta1, beta2,
                         eps, weight_decay, bias_c1, bias_c2);
         return EHIP_OK;
