@@ -540,6 +540,38 @@ def test_conv2d_relu_maxpool_nonfinite_weight(hip, orc):
     exact(host(DX), dx, "dx")
 
 
+def test_conv2d_relu_maxpool_nonfinite_input(hip, orc):
+    """An infinite input: the weight gradients keep the full sum over positions (inf times a
+    zero gradient is NaN, as in the reference's product), so the NaN and inf entries of dW
+    and db fall where the oracle's do, and the finite ones agree within the fp32 bound."""
+    import _compose as K
+    print_case("conv-relu-pool inf input")
+    r = rng(58)
+    shape, co = (2, 3, 9, 8), 5
+    x = randn(r, *shape)
+    w = randn(r, co, shape[1], 3, 3) * 0.5
+    b = randn(r, co)
+    y, cache = K.conv2d_fwd(orc, x, w, b, 1, 1)
+    ry = orc.relu(y)
+    pooled, am = orc.maxpool(ry, 2, 2)
+    g = randn(r, *pooled.shape)
+    x_inf = x.copy()
+    x_inf[1, 2, 4, 5] = np.inf
+    cols = orc.im2col(x_inf, 3, 3, 1, 1)
+    cache_inf = (cache[0], cache[1], cols, cache[3], 1, 1, True)
+    dry = orc.maxpool_backward(am, g, ry.shape)
+    dy = orc.relu_backward(y, dry)
+    _, dw, db = K.conv2d_bwd(orc, dy, cache_inf)
+    _, DW, DB = hip.conv2d_relu_maxpool_backward(dev(x_inf), dev(w), dev(g), dev(pooled),
+                                                 dev(am), 1, 1, 2)
+    DW, DB = host(DW), host(DB)
+    assert np.isnan(dw).any()
+    assert np.array_equal(np.isnan(DW), np.isnan(dw)) and np.array_equal(np.isinf(DW), np.isinf(dw))
+    fin = np.isfinite(dw)
+    ref_close(DW[fin], dw[fin], k_tol(2 * 9 * 8), "dweight finite entries")
+    exact(np.isnan(DB), np.isnan(db), "dbias NaN pattern")
+
+
 def test_conv2d_relu_maxpool_refusals(hip):
     import ctypes
     import ehip as E
