@@ -46,6 +46,48 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
                 int64_t x_slab, float* out, hipStream_t s);
 
+// Ordered sum of partial[chunk][o] over `chunks` chunks of O outputs, as one
+// 256-thread block's share (block bx of ceil(O / (256 / rl))): rl lanes per
+// output take chunks l, l + rl, ... (eight loads in flight), then the lane sums
+// are added in lane order through `lanes` (256 floats of LDS). Returns true in
+// the thread that holds output o's sum. The order depends only on the shape.
+__device__ __forceinline__ bool partial_sums(const float* __restrict__ partial, int O, int chunks,
+                                             int rl, int bx, float* lanes, float& sum, int& o) {
+    const int cw = 256 / rl;
+    const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
+    o = bx * cw + cl;
+    float acc = 0.0f;
+    if (o < O && lane < chunks) {
+        const float* p = partial + o + int64_t(lane) * O;
+        const int64_t stride = int64_t(rl) * O;
+        const int count = (chunks - lane + rl - 1) / rl;
+        acc = p[0];
+        int s = 1;
+        for (; s + 8 <= count; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p[int64_t(s + u) * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; s < count; ++s) acc += p[int64_t(s) * stride];
+    }
+    lanes[threadIdx.x] = acc;
+    __syncthreads();
+    if (lane != 0 || o >= O) return false;
+    sum = lanes[cl];
+    for (int l = 1; l < rl && l < chunks; ++l) sum += lanes[l * cw + cl];
+    return true;
+}
+
+// Lanes per output of partial_sums: at most eight chunks per lane, so each
+// lane's loads go out in one round.
+inline int reduce_lanes(int64_t chunks) {
+    int rl = 1;
+    while (rl < 64 && rl * 8 < chunks) rl *= 2;
+    return rl;
+}
+
 // Validates a window: positive extents, non-negative padding, and out_h/out_w
 // equal to the geometry's (layout.hip). Refusals carry `name`.
 int check_window(const char* name, const ehip_window_t* w);

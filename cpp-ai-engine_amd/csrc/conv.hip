@@ -1353,40 +1353,15 @@ __global__ __launch_bounds__(kThreads) void conv_weight_partial(const float* __r
     }
 }
 
-// out[o] = sum over chunks of partial[chunk][o] in a fixed order: rl lanes per
-// output take chunks l, l + rl, ... and lane results are added in lane order.
-// Outputs o = co (K + 1) + k go to dw[co][k] for k < K and to db[co] for k == K.
-// bx is the block's index among the 256-thread blocks of this reduction.
+// dw / db from the partials (partial_sums in common.hpp gives the order).
 __device__ __forceinline__ void weight_reduce_block(const float* __restrict__ partial,
                                                     float* __restrict__ dw,
                                                     float* __restrict__ db, int cout, int k,
                                                     int chunks, int rl, int bx, float* lanes) {
-    const int K1 = k + 1, O = cout * K1;
-    const int cw = 256 / rl;
-    const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
-    const int o = bx * cw + cl;
-    float acc = 0.0f;
-    if (o < O && lane < chunks) {
-        const float* p = partial + o + int64_t(lane) * O;
-        const int64_t stride = int64_t(rl) * O;
-        const int count = (chunks - lane + rl - 1) / rl;
-        acc = p[0];
-        int s = 1;
-        for (; s + 8 <= count; s += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = p[int64_t(s + u) * stride];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc += v[u];
-        }
-        for (; s < count; ++s) acc += p[int64_t(s) * stride];
-    }
-    lanes[threadIdx.x] = acc;
-    __syncthreads();
-    if (lane == 0 && o < O) {
-        float sum = lanes[cl];
-        for (int l = 1; l < rl && l < chunks; ++l) sum += lanes[l * cw + cl];
-        const int co = o / K1, kk = o % K1;
+    float sum;
+    int o;
+    if (partial_sums(partial, cout * (k + 1), chunks, rl, bx, lanes, sum, o)) {
+        const int co = o / (k + 1), kk = o % (k + 1);
         if (kk < k)
             dw[int64_t(co) * k + kk] = sum;
         else if (db != nullptr)
@@ -1565,13 +1540,6 @@ int launch_band(const float* x, const float* gout, const PoolGather& pg, float* 
 }
 
 // dweight / dbias from the per-band (or per-chunk) partials, in chunk order.
-// Lanes per output of the partials' reduction: at most eight chunks per lane,
-// so each lane's loads go out in one round.
-int reduce_lanes(int64_t chunks) {
-    int rl = 1;
-    while (rl < 64 && rl * 8 < chunks) rl *= 2;
-    return rl;
-}
 
 int weight_reduce(const float* partial, float* dweight, float* dbias, const Geo& g,
                   int64_t chunks, hipStream_t s) {

@@ -435,6 +435,64 @@ __global__ __launch_bounds__(kThreads) void adam_multi_inline(AdamInline table, 
     adam_chunk<NT, U>(find_slot(table.s, count, b), b, lr, b1, b2, eps, wd, c1, c2);
 }
 
+// Adam over the multi-tensor table, launched together with the ordered sums
+// of convolution weight-gradient partials: blocks [0, rb.blocks) each sum a
+// few outputs of one job (partial_sums, the order of conv_weight_reduce), store
+// the gradient and, when the gradient belongs to a parameter of this step,
+// update that element with the same arithmetic as the table's blocks, which
+// take the remaining blocks.
+constexpr int kMaxReduceAdam = 8;
+
+struct ReduceAdamJob {
+    const float* partial;
+    float* grad[2];           // dweight, dbias (or null)
+    float* p[2];              // the parameters those gradients belong to (or null)
+    float* m[2];
+    float* v[2];
+    int cout, k, chunks, rl, first;
+};
+
+struct ReduceAdamBatch {
+    ReduceAdamJob job[kMaxReduceAdam];
+    int count, blocks;
+};
+
+template <bool NT, int U>
+__global__ __launch_bounds__(kThreads) void adam_multi_reduce(ReduceAdamBatch rb, AdamInline table,
+                                                              int count, float lr, float b1,
+                                                              float b2, float eps, float wd,
+                                                              float c1, float c2) {
+    __shared__ float lanes[256];
+    if (int(blockIdx.x) < rb.blocks) {
+        int j = 0;
+        while (j + 1 < rb.count && int(blockIdx.x) >= rb.job[j + 1].first) ++j;
+        const ReduceAdamJob& r = rb.job[j];
+        float sum;
+        int o;
+        if (!partial_sums(r.partial, r.cout * (r.k + 1), r.chunks, r.rl,
+                          int(blockIdx.x) - r.first, lanes, sum, o))
+            return;
+        const int co = o / (r.k + 1), kk = o % (r.k + 1);
+        const int which = kk < r.k ? 0 : 1;
+        if (r.grad[which] == nullptr) return;
+        const int64_t e = which == 0 ? int64_t(co) * r.k + kk : co;
+        r.grad[which][e] = sum;
+        if (r.p[which] != nullptr) {
+            const Adam op{r.p[which], r.grad[which], r.m[which], r.v[which], lr, b1, b2, eps, wd,
+                          c1, c2};
+            float pv = r.p[which][e], mv = r.m[which][e], vv = r.v[which][e];
+            op.one(pv, sum, mv, vv);
+            r.p[which][e] = pv;
+            r.m[which][e] = mv;
+            r.v[which][e] = vv;
+        }
+        return;
+    }
+    if (count == 0) return;
+    const int64_t b = int64_t(blockIdx.x) - rb.blocks;
+    adam_chunk<NT, U>(find_slot(table.s, count, b), b, lr, b1, b2, eps, wd, c1, c2);
+}
+
 template <int OP>
 int binary_op(const float* a, const float* b, float* out, int64_t inner, int64_t repeat,
               hipStream_t s) {
@@ -633,6 +691,84 @@ int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, 
         EHIP_LAUNCH("adam_multi", adam_multi<false>, dim3(unsigned(chunks)), dim3(kThreads), 0, s,
                     table, int(slots.size()), lr, beta1, beta2, eps, weight_decay, bias_c1,
                     bias_c2);
+    return EHIP_OK;
+}
+
+int ehip_adam_multi_reduce_f32(const ehip_adam_tensor_t* tensors, int count,
+                               const ehip_conv_reduce_t* jobs, int njobs, float lr, float beta1,
+                               float beta2, float eps, float weight_decay, float bias_c1,
+                               float bias_c2, void* stream) {
+    EHIP_READY();
+    if (count < 0 || (count > 0 && tensors == nullptr) || njobs < 0 ||
+        (njobs > 0 && jobs == nullptr))
+        return fail(EHIP_EINVAL, "adam_multi_reduce: bad list");
+    hipStream_t s = as_stream(stream);
+    // Beyond one launch's job table: the separate reduction, then the step.
+    if (njobs > kMaxReduceAdam) {
+        if (int rc = ehip_conv_weight_reduce_f32(jobs, njobs, stream)) return rc;
+        return ehip_adam_multi_f32(tensors, count, lr, beta1, beta2, eps, weight_decay, bias_c1,
+                                   bias_c2, stream);
+    }
+    ReduceAdamBatch rb{};
+    std::vector<char> owned(size_t(count), 0);
+    int64_t blocks = 0;
+    for (int j = 0; j < njobs; ++j) {
+        const ehip_conv_reduce_t& q = jobs[j];
+        if (!q.partials || !q.dweight || q.chunks <= 0 || q.out_channels <= 0 || q.k <= 0 ||
+            q.chunks > 0x7fffffff || q.out_channels * (q.k + 1) > 0x7fffffff)
+            return fail(EHIP_EINVAL, "adam_multi_reduce: bad job %d", j);
+        ReduceAdamJob& r = rb.job[rb.count++];
+        r.partial = q.partials;
+        r.grad[0] = q.dweight;
+        r.grad[1] = q.dbias;
+        const int64_t n[2] = {q.out_channels * q.k, q.out_channels};
+        for (int w = 0; w < 2; ++w)
+            for (int i = 0; i < count && r.grad[w] != nullptr; ++i)
+                if (tensors[i].g == r.grad[w] && tensors[i].n == n[w] && !owned[size_t(i)]) {
+                    if (!tensors[i].p || !tensors[i].m || !tensors[i].v)
+                        return fail(EHIP_EINVAL, "adam_multi_reduce: tensor %d has a null pointer", i);
+                    r.p[w] = tensors[i].p;
+                    r.m[w] = tensors[i].m;
+                    r.v[w] = tensors[i].v;
+                    owned[size_t(i)] = 1;
+                    break;
+                }
+        r.cout = int(q.out_channels);
+        r.k = int(q.k);
+        r.chunks = int(q.chunks);
+        r.rl = reduce_lanes(q.chunks);
+        r.first = int(blocks);
+        blocks += ceil_div(q.out_channels * (q.k + 1), 256 / r.rl);
+    }
+    rb.blocks = int(blocks);
+    // The other tensors: the small-model chunking of ehip_adam_multi_f32.
+    std::vector<AdamSlot> slots;
+    int64_t total = 0, chunks = 0;
+    for (int i = 0; i < count; ++i) {
+        if (tensors[i].n < 0) return fail(EHIP_EINVAL, "adam_multi_reduce: tensor %d has a negative size", i);
+        if (!owned[size_t(i)]) total += tensors[i].n;
+    }
+    for (int i = 0; i < count; ++i) {
+        const ehip_adam_tensor_t& t = tensors[i];
+        if (owned[size_t(i)] || t.n == 0) continue;
+        if (!t.p || !t.g || !t.m || !t.v)
+            return fail(EHIP_EINVAL, "adam_multi_reduce: tensor %d has a null pointer", i);
+        slots.push_back({t.p, t.g, t.m, t.v, t.n, chunks});
+        chunks += ceil_div(t.n, int64_t(kThreads) * 4);
+    }
+    if (total > (int64_t(1) << 20) || slots.size() > size_t(kInlineSlots)) {
+        // A large model: the separate reduction, then the step.
+        if (int rc = ehip_conv_weight_reduce_f32(jobs, njobs, stream)) return rc;
+        return ehip_adam_multi_f32(tensors, count, lr, beta1, beta2, eps, weight_decay, bias_c1,
+                                   bias_c2, stream);
+    }
+    AdamInline inline_table{};
+    if (!slots.empty()) std::memcpy(inline_table.s, slots.data(), slots.size() * sizeof(AdamSlot));
+    if (blocks + chunks == 0) return EHIP_OK;
+    if (blocks + chunks > 0x7fffffff) return fail(EHIP_EINVAL, "adam_multi_reduce: too many blocks");
+    EHIP_LAUNCH("adam_multi_reduce", (adam_multi_reduce<false, 1>), dim3(unsigned(blocks + chunks)),
+                dim3(kThreads), 0, s, rb, inline_table, int(slots.size()), lr, beta1, beta2, eps,
+                weight_decay, bias_c1, bias_c2);
     return EHIP_OK;
 }
 

@@ -97,6 +97,8 @@ _SIGS = {
     "ehip_sgd_f32": [_vp, _vp, _vp, _i64, _f, _f, _f, _vp],
     "ehip_adam_f32": [_vp, _vp, _vp, _vp, _i64] + [_f] * 7 + [_vp],
     "ehip_adam_multi_f32": [C.POINTER(AdamTensor), _i] + [_f] * 7 + [_vp],
+    "ehip_adam_multi_reduce_f32": [C.POINTER(AdamTensor), _i, C.POINTER(ConvReduce), _i] +
+                                  [_f] * 7 + [_vp],
     "ehip_permute_f32": [_vp, _vp, _i, C.POINTER(_i64), C.POINTER(_i64), _vp],
     "ehip_transpose_f32": [_vp, _vp, _i64, _i64, _i64, _vp],
     "ehip_im2col_f32": [_vp, _vp, C.POINTER(Window), _vp],
@@ -304,6 +306,20 @@ class Backend:
             for p, g, m, v in groups])
         self.ok(self.lib.ehip_adam_multi_f32(arr, len(groups), lr, b1, b2, eps, wd, c1, c2,
                                              self.stream()), "adam_multi")
+
+    def adam_multi_reduce(self, groups, jobs, lr, b1, b2, eps, wd, c1, c2):
+        """groups: (p, g, m, v) device tensors; jobs: (partials, chunks, dweight, dbias) with
+        dweight shaped (co, ...) -- the sums land in dweight / dbias first."""
+        arr = (AdamTensor * len(groups))(*[
+            AdamTensor(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel())
+            for p, g, m, v in groups])
+        jarr = (ConvReduce * len(jobs))()
+        for i, (part, chunks, dw, db) in enumerate(jobs):
+            jarr[i] = ConvReduce(self.p(part), chunks, dw.shape[0], dw.numel() // dw.shape[0],
+                                 self.p(dw), self.p(db) if db is not None else None)
+        self.ok(self.lib.ehip_adam_multi_reduce_f32(arr, len(groups), jarr, len(jobs), lr, b1, b2,
+                                                    eps, wd, c1, c2, self.stream()),
+                "adam_multi_reduce")
 
     # ---------------------------------------------------------- layout
     def permute(self, x, order):

@@ -59,6 +59,7 @@ void backward(Tensor& root_tensor) {
         root->grad = std::make_shared<TensorImpl>(root->shape, 1.0f, false);
     }
     NoGradGuard no_grad;
+    detail::flush_deferred();   // sums still queued by an earlier backward
     std::vector<std::shared_ptr<TensorImpl>> order = topological_sort(root);
     for (const auto& node : order)
         if (node != root && node->backward_fn) node->grad = nullptr;
@@ -76,8 +77,9 @@ void backward(Tensor& root_tensor) {
                 node->backward_fn(g);
             }
         }
-        // Gradient sums the nodes queued (one launch for all of them).
-        detail::flush_deferred();
+        // The weight sums the nodes queued stay queued: the next reader of a
+        // gradient flushes them in one launch, or Adam::step runs them with
+        // its update.
     } catch (...) {
         detail::drop_deferred();
         throw;

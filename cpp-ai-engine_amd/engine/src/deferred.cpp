@@ -36,6 +36,13 @@ void flush_deferred() {
     // stream is ordered after the launch that reads them.
 }
 
+void take_deferred(std::vector<ehip_conv_reduce_t>& jobs, std::vector<Tensor>& keep) {
+    jobs = std::move(g_pending.jobs);
+    keep = std::move(g_pending.keep);
+    g_pending.jobs.clear();
+    g_pending.keep.clear();
+}
+
 void drop_deferred() {
     g_pending.jobs.clear();
     g_pending.keep.clear();

@@ -55,17 +55,20 @@ inline const float* dptr(const Tensor& t) { return t.storage().device(); }
 void add_grad_reshaped(Tensor& target, const Tensor& g);
 inline float* dout(Tensor& t) { return t.storage().device_write(); }
 
-// Gradient work queued during backward and finished together at its end: the
-// weight-gradient sums of fused convolution blocks, one launch for every layer
-// (deferred.cpp). `partials` is kept alive until then. The queue is flushed
-// before anything could read a queued gradient: at the end of
-// autograd::backward and before add_grad accumulates into an existing
-// gradient. A gradient may be queued only when add_grad will adopt its buffer
-// (grad_adoptable).
+// Gradient work queued during backward: the weight-gradient sums of fused
+// convolution blocks (deferred.cpp). `partials` is kept alive until they run.
+// The queue is flushed -- one launch for every queued layer -- before anything
+// can read a queued gradient: Tensor::grad(), zero_grad(), the start of
+// autograd::backward, and add_grad when it accumulates into an existing
+// gradient; Adam::step instead takes the jobs into its own launch. A gradient
+// may be queued only when add_grad will adopt its buffer (grad_adoptable).
 void defer_conv_reduce(const ehip_conv_reduce_t& job, const Tensor& partials);
 bool deferred_pending();
 void flush_deferred();
 void drop_deferred();
+// Moves the queued jobs (and the buffers they read) to the caller, which must
+// launch them before releasing `keep`.
+void take_deferred(std::vector<ehip_conv_reduce_t>& jobs, std::vector<Tensor>& keep);
 // True when add_grad of a fresh, unshared gradient buffer into `target` adopts
 // that buffer (no gradient yet, or a pending zero).
 bool grad_adoptable(const Tensor& target);

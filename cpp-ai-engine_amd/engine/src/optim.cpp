@@ -65,16 +65,28 @@ void Adam::step() {
     // the single-tensor update's.
     std::vector<ehip_adam_tensor_t> table;
     table.reserve(params_.size());
+    // Weight sums still queued from backward run in the same launch as the
+    // update (their gradients are read from the buffers the sums fill, without
+    // flushing them first through grad()).
+    std::vector<ehip_conv_reduce_t> jobs;
+    std::vector<Tensor> keep;
+    take_deferred(jobs, keep);
     for (size_t i = 0; i < params_.size(); ++i) {
         Tensor& p = params_[i];
         if (!p.requires_grad() || !p.has_grad()) continue;
-        const Tensor g = p.grad();
-        table.push_back({p.storage().device_mut(), dptr(g), m_[i].device_mut(), v_[i].device_mut(),
+        const float* g = p.get_impl()->grad->storage.device();
+        table.push_back({p.storage().device_mut(), g, m_[i].device_mut(), v_[i].device_mut(),
                          int64_t(p.size())});
     }
-    hip::check(ehip_adam_multi_f32(table.data(), int(table.size()), lr_, beta1_, beta2_, eps_,
-                                   weight_decay_, bias_c1, bias_c2, nullptr),
-               "adam step");
+    if (jobs.empty())
+        hip::check(ehip_adam_multi_f32(table.data(), int(table.size()), lr_, beta1_, beta2_, eps_,
+                                       weight_decay_, bias_c1, bias_c2, nullptr),
+                   "adam step");
+    else
+        hip::check(ehip_adam_multi_reduce_f32(table.data(), int(table.size()), jobs.data(),
+                                              int(jobs.size()), lr_, beta1_, beta2_, eps_,
+                                              weight_decay_, bias_c1, bias_c2, nullptr),
+                   "adam step");
 }
 
 std::vector<Tensor> Adam::state_tensors() const {

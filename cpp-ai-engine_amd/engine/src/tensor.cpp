@@ -124,6 +124,7 @@ void Tensor::set_requires_grad(bool req_grad) { impl_->requires_grad = req_grad;
 
 Tensor Tensor::grad() const {
     if (!impl_->grad) throw std::runtime_error("The tensor has no computed gradient.");
+    if (deferred_pending()) flush_deferred();
     return Tensor(impl_->grad);
 }
 
@@ -134,6 +135,9 @@ bool Tensor::has_grad() const { return impl_->grad != nullptr; }
 // gradient buffer is replaced rather than zeroed, so no other holder sees it.
 void Tensor::zero_grad() {
     if (!impl_->grad) return;
+    // A queued sum may still write this buffer: run it before the buffer can
+    // be released or reused.
+    if (deferred_pending()) flush_deferred();
     Storage& s = impl_->grad->storage;
     if (s.exclusive())
         s.assign(0.0f);

@@ -421,6 +421,20 @@ int ehip_conv2d_relu_maxpool_backward_partials_f32(
     int64_t out_channels, const ehip_window_t* pool, void* stream);
 int ehip_conv_weight_reduce_f32(const ehip_conv_reduce_t* jobs, int count, void* stream);
 
+/* The convolution weight-gradient sums of ehip_conv_weight_reduce_f32 and the
+ * Adam step of ehip_adam_multi_f32 in one launch: each job's sums are stored
+ * into its dweight / dbias, and a tensor whose g is one of those buffers (same
+ * size) is updated right there with the sum; the other tensors take the
+ * multi-tensor update. The same bits as the two calls one after the other
+ * (which it makes itself for more than 8 jobs or a model beyond 2^20
+ * parameters). Replaces the bias and weight folds of the conv nodes
+ * (src/tensor_detail.hpp:196-204, src/tensor_ops.cpp:565-586) followed by
+ * Adam::step (src/optim.cpp:113-162). */
+int ehip_adam_multi_reduce_f32(const ehip_adam_tensor_t* tensors, int count,
+                               const ehip_conv_reduce_t* jobs, int njobs, float lr, float beta1,
+                               float beta2, float eps, float weight_decay, float bias_c1,
+                               float bias_c2, void* stream);
+
 /* out[i] = x[idx[i]] row by row (rows of row_size floats); an index outside
  * [0, n_rows) yields a row of NaN instead of a read out of bounds.
  * Tensor::select_rows forward (src/tensor.cpp:556-585). Bit-exact. */

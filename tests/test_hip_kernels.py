@@ -513,6 +513,52 @@ def test_conv2d_relu_maxpool_partials_batched(hip):
                                                      None) == 0
 
 
+def test_adam_multi_reduce_matches_two_calls(hip):
+    """The weight sums and the Adam step in one launch: gradients, parameters and moments
+    equal the separate reduction followed by the multi-tensor step, bit for bit (a tensor
+    whose gradient no job fills, and a job whose gradient is no parameter, included)."""
+    print_case("adam multi reduce")
+    r = rng(71)
+    layers = [((64, 1, 28, 28), 8), ((64, 8, 14, 14), 16)]
+    jobs, params = [], []
+    for shape, co in layers:
+        x = dev(randn(r, *shape))
+        w = dev(randn(r, co, shape[1], 3, 3) * 0.5)
+        b = dev(randn(r, co))
+        P, AM = hip.conv2d_relu_maxpool(x, w, b, 1, 1, 2)
+        g = dev(randn(r, *host(P).shape))
+        _, part, chunks = hip.conv2d_relu_maxpool_partials(x, w, g, P, AM, 1, 1, 2,
+                                                           need_dx=shape[1] > 1)
+        jobs.append((part, chunks, w.shape, b.shape))
+        params += [w, b]
+    lin = dev(randn(r, 10, 784))
+    lin_g = dev(randn(r, 10, 784))
+    hp = dict(lr=1e-3, b1=0.9, b2=0.999, eps=1e-8, wd=0.0, c1=0.1, c2=0.001)
+
+    def run(fused):
+        ps = [t.clone() for t in params] + [lin.clone()]
+        ms = [dev(randn(rng(5 + i), *t.shape) * 0.1) for i, t in enumerate(ps)]
+        vs = [dev(np.abs(randn(rng(9 + i), *t.shape)) * 0.01) for i, t in enumerate(ps)]
+        grads = [hip.f32(t.shape) for t in params] + [lin_g.clone()]
+        js = [(part, chunks, grads[2 * i], grads[2 * i + 1])
+              for i, (part, chunks, _, _) in enumerate(jobs)]
+        # the first layer's bias is left out of the step: its sum is only stored
+        groups = [(ps[i], grads[i], ms[i], vs[i]) for i in range(len(ps)) if i != 1]
+        if fused:
+            hip.adam_multi_reduce(groups, js, **hp)
+        else:
+            outs = hip.conv_weight_reduce([(part, chunks, tuple(g.shape), True)
+                                           for part, chunks, g, _ in js])
+            for (dw, db), (_, _, g, gb) in zip(outs, js):
+                g.copy_(dw)
+                gb.copy_(db)
+            hip.adam_multi(groups, **hp)
+        return [host(t) for t in ps + ms + vs + grads]
+
+    for got, want in zip(run(True), run(False)):
+        exact(got, want, "adam multi reduce")
+
+
 def test_conv2d_relu_maxpool_nonfinite_weight(hip, orc):
     """An infinite weight: the input gradient still skips zero output gradients as the
     reference's product does (no inf * 0), bit for bit against the oracle."""
