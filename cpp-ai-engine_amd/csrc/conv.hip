@@ -379,6 +379,22 @@ __device__ __forceinline__ int fdiv(int n, const FastDiv& f) {
     return int((__umulhi(uint32_t(n), f.m) + uint32_t(n)) >> f.l);
 }
 
+// The (image, tile) of a tile kernel's block. Workgroups go to the 8 XCDs in
+// turn (block b to XCD b % 8), each with its own L2; when the batch is a
+// multiple of 8, the tiles of one image are given blocks on the same XCD, so
+// the rows and pooled cells that neighbouring tiles both stage (halo rows,
+// cache lines shared by short rows) are fetched from HBM once per image.
+__device__ __forceinline__ void image_tile(int b, int tiles, int images, int& n, int& tile) {
+    if (images % 8 == 0) {
+        const int slot = b / 8;
+        n = 8 * (slot / tiles) + b % 8;
+        tile = slot % tiles;
+    } else {
+        n = b / tiles;
+        tile = b % tiles;
+    }
+}
+
 // Conv2d (3 x 3, stride 1, padding 1) -> ReLU -> MaxPool2d (disjoint pk x pk
 // windows) over a tile of `rows` convolution rows (a multiple of pk) of one
 // image and every output channel. The input rows r0 - 1 .. r0 + rows
@@ -459,7 +475,8 @@ __global__ __launch_bounds__(NT) void conv3_relu_pool(const float* __restrict__ 
                                                       int ph, int pw, PoolFwdTile ft) {
     extern __shared__ __align__(16) float sm[];
     const int tid = int(threadIdx.x);
-    const int n = int(blockIdx.x) / ft.tiles, tile = int(blockIdx.x) % ft.tiles;
+    int n, tile;
+    image_tile(int(blockIdx.x), ft.tiles, g.n, n, tile);
     const int r0 = tile * ft.rows;
     const int rows = min(ft.rows, g.h - r0);
     const int srows = ft.rows + 2, wcols = g.w + 2;
@@ -879,7 +896,7 @@ __global__ __launch_bounds__(kThreads) void conv_backward_pair(
 //
 // The other threads compute the weight and bias partials as
 // weight_band_block does -- CT x CT tiles of (co, k), column K the bias,
-// over pg pixel groups combined in group order -- into partial[block].
+// over pg pixel groups combined in group order -- into partial[n * tiles + tile].
 struct PoolTile {
     int rows, tiles;         // convolution rows per tile (a multiple of pk), tiles per image
     int dx_threads;          // threads computing dx (a multiple of 64; 0 = no dx)
@@ -972,7 +989,8 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
                                                           PoolTile pt) {
     extern __shared__ __align__(16) float sm[];
     const int tid = int(threadIdx.x);
-    const int n = int(blockIdx.x) / pt.tiles, tile = int(blockIdx.x) % pt.tiles;
+    int n, tile;
+    image_tile(int(blockIdx.x), pt.tiles, g.n, n, tile);
     const int r0 = tile * pt.rows;
     const int rows = min(pt.rows, g.h - r0);
     const int srows = pt.rows + 2;
@@ -1133,7 +1151,7 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
         // sg cell groups per tile when there are fewer tiles than threads; group
         // r adds cells r, r + sg, ... and the groups are added in group order.
         const int sg = max(1, wthreads / stiles);
-        float* pc = partial + int64_t(blockIdx.x) * g.cout * K1;
+        float* pc = partial + (int64_t(n) * pt.tiles + tile) * g.cout * K1;
         for (int t0 = 0; t0 < stiles; t0 += wthreads) {
             const int t = sg == 1 ? wtid + t0 : wtid % stiles, grp = sg == 1 ? 0 : wtid / stiles;
             const bool active = wtid >= 0 && t < stiles && grp < sg;
@@ -1268,7 +1286,7 @@ __global__ __launch_bounds__(NT) void conv3_pool_backward(const float* __restric
             for (int kk = 0; kk < CT; ++kk) r[q * CT + kk] = acc[q][kk];
     }
     __syncthreads();
-    float* pc = partial + int64_t(blockIdx.x) * g.cout * K1;
+    float* pc = partial + (int64_t(n) * pt.tiles + tile) * g.cout * K1;
     const int span = tiles * CT * CT;
     for (int o = tid; o < span; o += NT) {
         float sum = red[o];
