@@ -499,6 +499,26 @@ int64_t eng_block_num_params(int64_t d, int64_t heads, int64_t ff) {
     return (4 * d) + 4 * (d * d + d) + (d * ff + ff) + (ff * d + d) + 0 * heads;
 }
 
+// One forward and backward of the cfg2 CNN; the gradients are read through
+// Tensor::grad() (which runs any queued weight sums first), in parameter order.
+int eng_cnn_grads(const float* x, const int64_t* labels, int64_t batch, int64_t in_c, int64_t c1,
+                  int64_t c2, int64_t hw, int64_t classes, const float* params, float* loss_out,
+                  float* grads_out) {
+    return guarded([&] {
+        auto model = cnn_model(size_t(in_c), size_t(c1), size_t(c2), size_t(hw), size_t(classes));
+        load_params(model->parameters(), params);
+        Tensor X = make({size_t(batch), size_t(in_c), size_t(hw), size_t(hw)}, x, false);
+        Tensor loss = nn::cross_entropy_loss((*model)(X), labels_of(labels, batch));
+        loss.backward();
+        put(loss, loss_out);
+        size_t off = 0;
+        for (Tensor& p : model->parameters()) {
+            put(p.grad(), grads_out + off);
+            off += p.size();
+        }
+    });
+}
+
 int eng_cnn_train(const float* x, const int64_t* labels, int64_t batch, int64_t in_c, int64_t c1,
                   int64_t c2, int64_t hw, int64_t classes, const float* params, int64_t steps,
                   float lr, float* losses, float* params_out) {

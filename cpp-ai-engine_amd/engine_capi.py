@@ -41,6 +41,7 @@ def load_library(path=LIB_PATH):
     lib.eng_block_num_params.restype = _i64
     lib.eng_charlm_num_params.restype = _i64
     lib.eng_adam_steps.argtypes = [_f32p, _f32p, _i64, _i64] + [C.c_float] * 5
+    lib.eng_cnn_grads.argtypes = [_f32p, _i64p] + [_i64] * 6 + [_f32p, _f32p, _f32p]
     lib.eng_cnn_train.argtypes = [_f32p, _i64p] + [_i64] * 6 + [_f32p, _i64, C.c_float, _f32p,
                                                                  _f32p]
     lib.eng_charlm_train.argtypes = [_f32p, _i64p] + [_i64] * 7 + [_f32p, _i64, C.c_float, _f32p,
@@ -318,6 +319,18 @@ class Engine:
                                             _i64(ff), int(causal), _fp(params), _fp(dy), _fp(y),
                                             _fp(dx), _fp(dp)))
         return y, dx, dp
+
+    def cnn_grads(self, x, labels, params, c1=8, c2=16, classes=10):
+        """One forward and backward of the small CNN: (loss, flat gradients in parameter
+        order)."""
+        x, params = _f32(x), _f32(params)
+        labels = np.ascontiguousarray(labels, np.int64)
+        b, cin, hw, _ = x.shape
+        loss = np.empty(1, np.float32)
+        grads = np.empty_like(params)
+        self._ok(self.lib.eng_cnn_grads(_fp(x), _ip(labels), b, cin, c1, c2, hw, classes,
+                                        _fp(params), _fp(loss), _fp(grads)))
+        return float(loss[0]), grads
 
     def cnn_train(self, x, labels, params, steps, lr, c1=8, c2=16, classes=10):
         x, params = _f32(x), _f32(params)

@@ -34,6 +34,11 @@ def orc():
 
 @pytest.fixture(scope="module")
 def eng():
+    # torch's HIP runtime first, as the other GPU fixtures do: initialised after
+    # the engine library in a fresh process, torch reports no device.
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test ran without a visible GPU")
     from engine_capi import Engine
     return Engine()
 
@@ -329,6 +334,32 @@ def test_charlm_training_fused_equals_composed(eng):
                                                             layers, params, 5, 1e-3))
     exact(fused[0], comp[0], "losses")
     exact(fused[1], comp[1], "weights")
+
+
+def test_cnn_gradients_fused_vs_composed(eng):
+    """cfg2 CNN, one backward: with fused nodes the conv weight sums are queued and run when
+    Tensor::grad() reads them. Loss and Linear gradients are the bits of the node-by-node
+    graph; the conv weight and bias gradients (another summation order) agree within the
+    fp32 bound of their 64 x 28 x 28-term sums."""
+    print_case("cnn grads fused vs composed")
+    r = np.random.default_rng(2)
+    x = r.uniform(0.0, 1.0, (64, 1, 28, 28)).astype(np.float32)
+    labels = r.integers(0, 10, 64)
+    parts = []
+    for shp in K.cnn_param_shapes():  # Kaiming-uniform weights, small random biases
+        if len(shp) == 1 or shp[0] == 1:
+            parts.append(r.uniform(-0.1, 0.1, int(np.prod(shp))).astype(np.float32))
+        else:
+            fan_in = int(np.prod(shp[1:])) if len(shp) == 4 else shp[0]
+            lim = np.sqrt(6.0 / fan_in)
+            parts.append(r.uniform(-lim, lim, int(np.prod(shp))).astype(np.float32))
+    params = np.concatenate(parts)
+    fused, comp = both_graphs(eng, lambda: eng.cnn_grads(x, labels, params))
+    exact(np.float32(fused[0]), np.float32(comp[0]), "loss")
+    conv = 8 * 9 + 8 + 16 * 72 + 16
+    exact(fused[1][conv:], comp[1][conv:], "linear gradients")
+    ref_close(fused[1][:conv], comp[1][:conv], k_tol(64 * 28 * 28), "conv gradients")
+    assert np.abs(fused[1][:conv]).max() > 0
 
 
 @pytest.mark.parametrize("n,c", [(64, 10), (1024, 128), (2048, 121)])
