@@ -590,6 +590,73 @@ __global__ __launch_bounds__(T) void layernorm_rows_backward(
     }
 }
 
+// The same as layernorm_rows_backward<64, V, VEC4> for groups of at most
+// kSplitRows rows, with the group's rows shared by W waves instead of walked
+// by one: wave w takes the group's rows i = w, w + W, ... (row group + i
+// groups), computes dx as above, and parks the row's dy and xhat in LDS; after
+// a barrier one thread per column runs the serial kernel's dgamma / dbeta
+// recurrences over them in row order, with the same expressions, so the sums
+// match it bit for bit.
+constexpr int kSplitRows = 16;
+
+template <int V, bool VEC4, int W>
+__global__ __launch_bounds__(64 * W) void layernorm_rows_backward_split(
+    const float* __restrict__ dy, const float* __restrict__ xhat, const float* __restrict__ gamma,
+    const float* __restrict__ inv_std, float* __restrict__ dx, float* __restrict__ partial,
+    int64_t rows, int64_t cols) {
+    using F = Frag<64, V, VEC4>;
+    constexpr int kC = 64 * V;   // columns the fragment holds
+    __shared__ float rows_dh[kSplitRows][2][kC];
+    const float inv_d = 1.0f / static_cast<float>(cols);
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int64_t group = blockIdx.x, step = gridDim.x;
+    const int nrows = int(group < rows ? (rows - 1 - group) / step + 1 : 0);
+    float gm[V];
+#pragma unroll
+    for (int t = 0; t < V; ++t) {
+        const int64_t c = F::col(lane, t);
+        gm[t] = c < cols ? gamma[c] : 0.0f;
+    }
+    for (int i = wave; i < nrows; i += W) {
+        const int64_t r = group + int64_t(i) * step;
+        F fd, fh;
+        fd.load(dy + r * cols, int(cols), lane, 0.0f);
+        fh.load(xhat + r * cols, int(cols), lane, 0.0f);
+        const float inv = inv_std[r];
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+            const float dxh = fd.v[t] * gm[t];
+            s1 += dxh;
+            s2 += dxh * fh.v[t];
+        }
+        s1 = group_reduce<64, false>(s1, nullptr);
+        s2 = group_reduce<64, false>(s2, nullptr);
+        F fo;
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+            const float dxh = fd.v[t] * gm[t];
+            fo.v[t] = inv * (dxh - inv_d * s1 - fh.v[t] * inv_d * s2);
+            const int c = F::col(lane, t);
+            rows_dh[i][0][c] = fd.v[t];
+            rows_dh[i][1][c] = fh.v[t];
+        }
+        fo.store(dx + r * cols, int(cols), lane);
+    }
+    __syncthreads();
+    float* pg = partial + group * 2 * cols;
+    for (int c = threadIdx.x; c < cols; c += 64 * W) {
+        float dg = 0.0f, db = 0.0f;
+        for (int i = 0; i < nrows; ++i) {
+            const float d = rows_dh[i][0][c], h = rows_dh[i][1][c];
+            dg = dg + d * h;
+            db = db + d;
+        }
+        pg[c] = dg;
+        pg[cols + c] = db;
+    }
+}
+
 constexpr int kLnWaves = 8;
 
 // acc of wave 0 += acc of waves 1..kLnWaves-1 by a fixed halving tree
@@ -1096,7 +1163,18 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
 #define EHIP_LNB(T, V, VEC)                                                                     \
     EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward<T, V, VEC>), dim3(grid),         \
                 dim3(T), 0, s, dy, xhat, gamma, inv_std, dx, partial, rows, cols)
-    if (vec) {
+#define EHIP_LNS(V, VEC)                                                                        \
+    EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_split<V, VEC, 4>), dim3(grid),   \
+                dim3(256), 0, s, dy, xhat, gamma, inv_std, dx, partial, rows, cols)
+    // Groups of at most kSplitRows rows of at most 256 columns: the group's rows
+    // go to four waves side by side (the same bits, a quarter of the serial
+    // row chain).
+    if (ceil_div(rows, groups) <= kSplitRows && cols <= 256) {
+        if (vec) EHIP_LNS(4, true);
+        else if (cols <= 64) EHIP_LNS(1, false);
+        else if (cols <= 128) EHIP_LNS(2, false);
+        else EHIP_LNS(4, false);
+    } else if (vec) {
         if (cols <= 256) EHIP_LNB(64, 4, true);
         else if (cols <= 512) EHIP_LNB(64, 8, true);
         else if (cols <= 1024) EHIP_LNB(64, 16, true);
@@ -1112,6 +1190,7 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
     else if (cols <= 4096) EHIP_LNB(256, 16, false);
     else EHIP_LNB(256, 32, false);
 #undef EHIP_LNB
+#undef EHIP_LNS
     if (int rc = column_sums(partial, 1, groups, cols, 2 * cols, 0, dgamma, s)) return rc;
     return column_sums(partial + cols, 1, groups, cols, 2 * cols, 0, dbeta, s);
 }

@@ -841,7 +841,8 @@ def test_softmax(hip, orc, rows, cols):
 @pytest.mark.parametrize("rows,d", [(2048, 96), (512, 64), (7, 1024), (33, 100), (4, 3000),
                                    (8192, 1024), (300, 260), (64, 4096), (16, 8192),
                                    (2048, 512), (9000, 256), (5000, 257), (700, 2048),
-                                   (600, 2000), (20000, 100)])
+                                   (600, 2000), (20000, 100), (2048, 256), (160, 200),
+                                   (1, 8), (8191, 128)])
 def test_layernorm(hip, orc, rows, d):
     print_case("layernorm", rows, d)
     r = rng(rows + d)
