@@ -45,6 +45,10 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // depends only on the shape (reduce.hip).
 int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
                 int64_t x_slab, float* out, hipStream_t s);
+// column_sums of x into out0 and of x + x_second into out1 (one slab each,
+// the same sums bit for bit) in the launches of one call.
+int column_sums_pair(const float* x, int64_t rows, int64_t cols, int64_t ld, int64_t x_second,
+                     float* out0, float* out1, hipStream_t s);
 
 // Ordered sum of partial[chunk][o] over `chunks` chunks of O outputs, as one
 // 256-thread block's share (block bx of ceil(O / (256 / rl))): rl lanes per

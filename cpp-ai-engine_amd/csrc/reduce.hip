@@ -194,15 +194,18 @@ __global__ __launch_bounds__(kThreads) void reduce_stage2(const double* __restri
 // workgroups and the second adds at most 64 partials per lane. (One launch
 // with a last-block-adds pattern measured 25 us instead of 2 x 3: making the
 // partials visible across the XCDs' L2 caches costs an L2 write-back.)
-int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
-                int64_t x_slab, float* out, hipStream_t s) {
+// Slab o's sums go to out + o * out_slab; plan_slabs is the slab count the
+// row blocks are sized for (the order of every sum depends on it).
+int column_sums_plan(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
+                     int64_t x_slab, float* out, int64_t out_slab, int64_t plan_slabs,
+                     hipStream_t s) {
     if (slabs == 0 || cols == 0) return EHIP_OK;
     int cw = 1;
     while (cw < cols && cw < 64) cw *= 2;
     const int64_t tiles = ceil_div(cols, cw);
     if (tiles > 65535 || slabs > 65535) return fail(EHIP_EINVAL, "column_sums: too many columns");
     const int rl = kThreads / cw;
-    int64_t blocks = ceil_div(1024, tiles * slabs);
+    int64_t blocks = ceil_div(1024, tiles * plan_slabs);
     const int64_t max_blocks = ceil_div(rows, 2 * rl);  // at least two rows per lane
     if (blocks > max_blocks) blocks = max_blocks;
     if (blocks > 64 * rl) blocks = 64 * rl;
@@ -217,10 +220,10 @@ int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64
     if (blocks == 1) {
         if (vec) {
             EHIP_LAUNCH("column_sums", sum_cols4, dim3(1, tiles4, unsigned(slabs)), dim3(kThreads),
-                        0, s, x, out, rows, cols, ld, rows, x_slab, cols);
+                        0, s, x, out, rows, cols, ld, rows, x_slab, out_slab);
         } else {
             EHIP_LAUNCH("column_sums", sum_cols, dim3(1, unsigned(tiles), unsigned(slabs)),
-                        dim3(kThreads), 0, s, x, out, rows, cols, ld, rows, x_slab, cols, cw);
+                        dim3(kThreads), 0, s, x, out, rows, cols, ld, rows, x_slab, out_slab, cw);
         }
         return EHIP_OK;
     }
@@ -232,15 +235,35 @@ int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64
                     dim3(kThreads), 0, s, x, partial, rows, cols, ld, rpb, x_slab, blocks * cols);
         EHIP_LAUNCH("column_sums_final", sum_cols4, dim3(1, tiles4, unsigned(slabs)),
                     dim3(kThreads), 0, s, partial, out, blocks, cols, cols, blocks, blocks * cols,
-                    cols);
+                    out_slab);
         return EHIP_OK;
     }
     EHIP_LAUNCH("column_sums_blocks", sum_cols, dim3(unsigned(blocks), unsigned(tiles), unsigned(slabs)),
                 dim3(kThreads), 0, s, x, partial, rows, cols, ld, rpb, x_slab, blocks * cols, cw);
     EHIP_LAUNCH("column_sums_final", sum_cols, dim3(1, unsigned(tiles), unsigned(slabs)),
                 dim3(kThreads), 0, s, partial, out, blocks, cols, cols, blocks, blocks * cols,
-                cols, cw);
+                out_slab, cw);
     return EHIP_OK;
+}
+
+int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
+                int64_t x_slab, float* out, hipStream_t s) {
+    return column_sums_plan(x, slabs, rows, cols, ld, x_slab, out, cols, slabs, s);
+}
+
+// Two single-slab column sums in the launches of one: the second slab's
+// output is addressed as out0 + (out1 - out0) in floats (both are float
+// arrays in the one flat device address space), and the row blocks are sized
+// for one slab, so each sum has the order a column_sums call of its own gives.
+int column_sums_pair(const float* x, int64_t rows, int64_t cols, int64_t ld, int64_t x_second,
+                     float* out0, float* out1, hipStream_t s) {
+    const intptr_t gap = reinterpret_cast<intptr_t>(out1) - reinterpret_cast<intptr_t>(out0);
+    if (gap % intptr_t(sizeof(float)) != 0) {
+        if (int rc = column_sums(x, 1, rows, cols, ld, 0, out0, s)) return rc;
+        return column_sums(x + x_second, 1, rows, cols, ld, 0, out1, s);
+    }
+    return column_sums_plan(x, 2, rows, cols, ld, x_second, out0,
+                            int64_t(gap / intptr_t(sizeof(float))), 1, s);
 }
 
 }  // namespace ehip

@@ -1191,8 +1191,7 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
     else EHIP_LNB(256, 32, false);
 #undef EHIP_LNB
 #undef EHIP_LNS
-    if (int rc = column_sums(partial, 1, groups, cols, 2 * cols, 0, dgamma, s)) return rc;
-    return column_sums(partial + cols, 1, groups, cols, 2 * cols, 0, dbeta, s);
+    return column_sums_pair(partial, groups, cols, 2 * cols, cols, dgamma, dbeta, s);
 }
 
 }  // extern "C"

@@ -53,6 +53,11 @@ inline const float* dptr(const Tensor& t) { return t.storage().device(); }
 // carry another shape (the backward of a reshape): g's buffer is adopted under
 // the target's shape when nothing else references it. Defined in tensor.cpp.
 void add_grad_reshaped(Tensor& target, const Tensor& g);
+// The device buffer of target's gradient when a product can add into it in
+// place (beta = 1: grad + product, the sum add_grad would form, bit for bit):
+// the gradient exists, holds values (not a pending zero) and is referenced by
+// nothing else. Otherwise nullptr, and the caller goes through add_grad.
+float* grad_in_place(Tensor& target);
 inline float* dout(Tensor& t) { return t.storage().device_write(); }
 
 // Gradient work queued during backward: the weight-gradient sums of fused

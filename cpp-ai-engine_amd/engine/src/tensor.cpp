@@ -199,6 +199,16 @@ void detail::add_grad_reshaped(Tensor& target, const Tensor& g) {
                "add_grad");
 }
 
+float* detail::grad_in_place(Tensor& target) {
+    const std::shared_ptr<TensorImpl>& impl_ = target.get_impl();
+    if (!impl_ || !impl_->requires_grad || !impl_->grad) return nullptr;
+    Storage& acc = impl_->grad->storage;
+    if (acc.pending_zero() || !acc.exclusive() || acc.size() != target.size()) return nullptr;
+    // The product reads the existing gradient: finish any queued sums first.
+    if (deferred_pending()) flush_deferred();
+    return acc.device_mut();
+}
+
 void Tensor::backward() { autograd::backward(*this); }
 
 void Tensor::backward(const Tensor& grad_output) {

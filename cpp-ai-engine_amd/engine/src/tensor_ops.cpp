@@ -312,6 +312,11 @@ bool row_bias(const Tensor* bias, size_t n) {
 
 Tensor empty_2d(size_t rows, size_t cols) { return Tensor({rows, cols}, 0.0f, false); }
 
+// Multiply-adds of g w^T above which Linear's backward no longer runs as one
+// launch (csrc/gemm.hip's thread-per-output limit), so that adding dx into
+// x's gradient in place saves a pass instead of splitting a launch in two.
+constexpr double kInPlaceWork = double(1 << 21);
+
 }  // namespace
 
 Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias) {
@@ -335,18 +340,29 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias) {
         if (M > 0 && K > 0 && N > 0) {
             // The same three results as the composed graph's add and product
             // backward (one launch for small layers), added in its order: the
-            // bias, then x, then w.
-            Tensor dx = xc.requires_grad() ? empty_2d(M, K) : Tensor();
+            // bias, then x, then w. Past the one-launch sizes, g w^T adds
+            // straight into an existing gradient of x (beta = 1, the same sum
+            // as add_grad's, without the separate accumulation pass).
+            float* dx_acc = xc.requires_grad() && double(M) * double(K) * double(N) > kInPlaceWork
+                                ? grad_in_place(xc)
+                                : nullptr;
+            const bool want_dx = xc.requires_grad() && dx_acc == nullptr;
+            Tensor dx = want_dx ? empty_2d(M, K) : Tensor();
             Tensor dw = wc.requires_grad() ? empty_2d(K, N) : Tensor();
             Tensor db = want_db ? Tensor(bc.shape(), 0.0f, false) : Tensor();
+            if (dx_acc)
+                hip::check(ehip_gemm_f32(0, 1, 1, int64_t(M), int64_t(K), int64_t(N), dptr(g),
+                                         int64_t(N), 0, dptr(wc), int64_t(N), 0, 1.0f, dx_acc,
+                                         int64_t(K), 0, nullptr),
+                           "linear backward dx");
             hip::check(ehip_linear_backward_f32(dptr(xc), dptr(wc), dptr(g),
-                                                xc.requires_grad() ? dout(dx) : nullptr,
+                                                want_dx ? dout(dx) : nullptr,
                                                 wc.requires_grad() ? dout(dw) : nullptr,
                                                 want_db ? dout(db) : nullptr, int64_t(M),
                                                 int64_t(K), int64_t(N), nullptr),
                        "linear backward");
             if (want_db) bc.add_grad(db);
-            if (xc.requires_grad()) xc.add_grad(dx);
+            if (want_dx) xc.add_grad(dx);
             if (wc.requires_grad()) wc.add_grad(dw);
             return;
         }

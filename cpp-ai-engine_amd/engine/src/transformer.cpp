@@ -327,7 +327,12 @@ Tensor MultiHeadAttention::forward(const Tensor& input, const Tensor* mask) {
                                     std::to_string(d_model_) + "), received " + input.shape_str() + ".");
     const size_t batch = input.shape()[0], seq = input.shape()[1];
     if (fused_nodes() && attention_heads_supported(input, num_heads_, mask)) {
-        Tensor attended = attention_heads(w_query_(input), w_key_(input), w_value_(input),
+        // One (batch * seq, d_model) view feeds the three projections, so their
+        // input gradients meet in one buffer (the second and third products add
+        // into it in place) before a single reshape hands it to `input`.
+        const Tensor flat = input.reshape({batch * seq, d_model_});
+        auto project = [&](Linear& layer) { return layer(flat).reshape({batch, seq, d_model_}); };
+        Tensor attended = attention_heads(project(w_query_), project(w_key_), project(w_value_),
                                           num_heads_, mask,
                                           keep_attention_ ? &last_attention_ : nullptr);
         return w_out_(attended);
