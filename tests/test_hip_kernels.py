@@ -863,6 +863,28 @@ def test_layernorm(hip, orc, rows, d):
     exact(host(dg2), host(dg), "dgamma repeat")
 
 
+@pytest.mark.parametrize("d", [64, 96, 121])
+def test_layernorm_backward_split_rows_match_serial(hip, orc, d):
+    """dx is row-local: 2048 rows (groups of 16, four waves per group) and the
+    same rows inside 8200 (groups of 17, one wave walking each group; under
+    2^20 elements, so still the small-problem kernels) give the same bits;
+    the split kernel's dgamma/dbeta stay within the K-term tolerance."""
+    print_case("layernorm split vs serial", d)
+    r = rng(d + 7)
+    big = 8200
+    xh = randn(r, big, d)
+    dy = randn(r, big, d)
+    gamma = randn(r, d)
+    inv = (np.abs(randn(r, big)) + 0.5).astype(np.float32)
+    dx_s, dg_s, db_s = hip.layernorm_backward(dev(dy[:2048]), dev(xh[:2048]), dev(gamma),
+                                              dev(inv[:2048]))
+    dx_b, _, _ = hip.layernorm_backward(dev(dy), dev(xh), dev(gamma), dev(inv))
+    exact(host(dx_s), host(dx_b)[:2048], "dx split vs serial")
+    wdx, wdg, wdb = orc.layernorm_backward(dy[:2048], xh[:2048], gamma, inv[:2048])
+    ref_close(host(dg_s), wdg, k_tol(2048), "dgamma")
+    ref_close(host(db_s), wdb, k_tol(2048), "dbeta")
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 10), (2048, 121), (8, 5), (16, 32000), (3, 40000),
                                        (100, 256), (600, 32000), (9, 1002), (1024, 128),
                                        (1000, 100), (1025, 10), (1, 1)])
