@@ -17,8 +17,13 @@
  *   - the compiled reference itself (oracle/_ref, built from the reference
  *     sources by oracle/Makefile), bit-exact on seeded inputs;
  *   - closed forms and brute force on tiny inputs (tests/test_oracle_*.py).
- * Functions with no such check would say "parity unpinned"; at present every
- * function below is pinned by at least one of the three.
+ * Functions with no such check would say "parity unpinned"; every function
+ * below is pinned by at least one of the three. The whole-tensor sums are
+ * pinned through the reference's Tensor::sum()/mean() (orc_sum) and the norm
+ * clip_grad_norm returns (orc_sum_squares), bit for bit after the reference's
+ * own cast to float, and by exact integer closed forms that only a double
+ * accumulator meets; orc_scalar_add/orc_scalar_mul bit for bit against the
+ * reference's t + k and t * k.
  */
 #ifndef ORACLE_H
 #define ORACLE_H

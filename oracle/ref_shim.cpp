@@ -210,6 +210,21 @@ int ref_sum(const float* x, int64_t n, float* out) {
     return guarded([&] { put(make({size_t(n)}, x, false).sum(), out); });
 }
 
+// Tensor::mean() (src/tensor_ops.cpp:706-712): the double sum cast to float,
+// times 1/n in float.
+int ref_mean(const float* x, int64_t n, float* out) {
+    return guarded([&] { put(make({size_t(n)}, x, false).mean(), out); });
+}
+
+// Tensor::operator+(float) (src/tensor_ops.cpp:276-295) when mul is 0, and
+// Tensor::operator*(float) (src/tensor_ops.cpp:303-322) otherwise.
+int ref_scalar(const float* x, int64_t n, float k, int mul, float* out) {
+    return guarded([&] {
+        const Tensor X = make({size_t(n)}, x, false);
+        put(mul ? X * k : X + k, out);
+    });
+}
+
 // nn::im2col and nn::col2im on their own.
 int ref_im2col(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, int64_t kh,
                int64_t kw, int64_t stride, int64_t pad, float* cols) {
@@ -418,6 +433,26 @@ int ref_cnn_load(const char* path, int64_t in_c, int64_t c1, int64_t c2, int64_t
     });
 }
 
+// One forward and backward of the CNN: the loss and every parameter's gradient
+// (flat, parameter order).
+int ref_cnn_grads(const float* x, const int64_t* labels, int64_t batch, int64_t in_c, int64_t c1,
+                  int64_t c2, int64_t hw, int64_t classes, const float* params, float* loss_out,
+                  float* grads_out) {
+    return guarded([&] {
+        auto model = cnn_model(size_t(in_c), size_t(c1), size_t(c2), size_t(hw), size_t(classes));
+        load_params(model->parameters(), params);
+        Tensor X = make({size_t(batch), size_t(in_c), size_t(hw), size_t(hw)}, x, false);
+        Tensor loss = nn::cross_entropy_loss((*model)(X), labels_of(labels, batch));
+        loss.backward();
+        put(loss, loss_out);
+        size_t off = 0;
+        for (const Tensor& p : model->parameters()) {
+            put(p.grad(), grads_out + off);
+            off += p.size();
+        }
+    });
+}
+
 int ref_cnn_train(const float* x, const int64_t* labels, int64_t batch, int64_t in_c, int64_t c1,
                   int64_t c2, int64_t hw, int64_t classes, const float* params, int64_t steps,
                   float lr, float* losses, float* params_out) {
@@ -456,6 +491,39 @@ int ref_charlm_train(const float* ids, const int64_t* targets, int64_t batch, in
             Tensor logits = model.forward(X, mask).reshape({size_t(batch * seq), size_t(vocab)});
             Tensor loss = nn::cross_entropy_loss(logits, y);
             loss.backward();
+            opt.step();
+            if (losses) losses[s] = loss.data()[0];
+        }
+        if (params_out) store_params(model.parameters(), params_out);
+    });
+}
+
+// As ref_charlm_train, and the first step's gradients (after backward, before
+// the update; parameter order) go to grads0 when it is not NULL.
+int ref_charlm_train_grads(const float* ids, const int64_t* targets, int64_t batch, int64_t seq,
+                           int64_t vocab, int64_t d, int64_t heads, int64_t ff, int64_t layers,
+                           const float* params, int64_t steps, float lr, float* losses,
+                           float* grads0, float* params_out) {
+    return guarded([&] {
+        CharModel model{size_t(vocab), size_t(seq), size_t(d), size_t(heads), size_t(ff),
+                        size_t(layers)};
+        load_params(model.parameters(), params);
+        optim::Adam opt(model.parameters(), lr);
+        const Tensor mask = nn::causal_mask(size_t(seq));
+        Tensor X = make({size_t(batch), size_t(seq)}, ids, false);
+        const std::vector<size_t> y = labels_of(targets, batch * seq);
+        for (int64_t s = 0; s < steps; ++s) {
+            opt.zero_grad();
+            Tensor logits = model.forward(X, mask).reshape({size_t(batch * seq), size_t(vocab)});
+            Tensor loss = nn::cross_entropy_loss(logits, y);
+            loss.backward();
+            if (s == 0 && grads0) {
+                size_t off = 0;
+                for (const Tensor& p : model.parameters()) {
+                    put(p.grad(), grads0 + off);
+                    off += p.size();
+                }
+            }
             opt.step();
             if (losses) losses[s] = loss.data()[0];
         }

@@ -63,3 +63,20 @@ def ref_close(got, want, tol=1e-5, what=""):
 
 def k_tol(k):
     return max(1e-5, 2.0 * k / 2.0 ** 24)
+
+
+def gemm_stat_bound(row_norms, col_norms, k, c=2.0):
+    """Per-element bound on the fp32 rounding error of a K-term dot product:
+    c sqrt(K) u ||a_i|| ||b_j|| (u = 2^-24), batched over a leading axis when given.
+
+    Rounding errors of a sum accumulate like a random walk: a serial fp32 sum of N(0,1)
+    products has an error of standard deviation about u K / 5 ~ u ||a_i|| ||b_j|| / 5, and
+    blocked or tree orders less, so c sqrt(K) leaves a wide margin for any correct order
+    while staying far below the worst case (K + 2) u sum_k |a_ik| |b_kj|, which grows like
+    K^2 u. At K = 12544 the bound is about 0.17 for unit-variance operands, so dropping a
+    single product a_ik b_kj (mean magnitude 2 / pi) fails it in most draws, and a wrong
+    index or a systematically dropped term fails it surely."""
+    scale = c * np.sqrt(k) * 2.0 ** -24
+    if isinstance(row_norms, np.ndarray):
+        return scale * np.multiply.outer(row_norms, col_norms)
+    return scale * row_norms.unsqueeze(-1) * col_norms.unsqueeze(-2)  # torch tensors

@@ -318,6 +318,8 @@ class Ref:
                                                                     _f32p, _f32p]
         L.ref_charlm_train.argtypes = [_f32p, _i64p] + [_i64] * 7 + [_f32p, _i64, C.c_float,
                                                                       _f32p, _f32p]
+        L.ref_charlm_train_grads.argtypes = [_f32p, _i64p] + [_i64] * 7 + [
+            _f32p, _i64, C.c_float, _f32p, _f32p, _f32p]
 
     def _ok(self, rc):
         if rc != 0:
@@ -467,6 +469,26 @@ class Ref:
         self._ok(self.lib.ref_cnn_load(path.encode(), in_c, c1, c2, hw, classes, fp(out)))
         return out
 
+    def sum(self, x):
+        """Tensor::sum(): the double accumulation cast to float."""
+        x = f32(x)
+        out = np.empty(1, np.float32)
+        self._ok(self.lib.ref_sum(fp(x), _i64(x.size), fp(out)))
+        return out[0]
+
+    def mean(self, x):
+        x = f32(x)
+        out = np.empty(1, np.float32)
+        self._ok(self.lib.ref_mean(fp(x), _i64(x.size), fp(out)))
+        return out[0]
+
+    def scalar(self, x, k, mul=False):
+        """x + k, or x * k when mul."""
+        x = f32(x)
+        out = np.empty_like(x)
+        self._ok(self.lib.ref_scalar(fp(x), _i64(x.size), C.c_float(k), int(mul), fp(out)))
+        return out
+
     def clip_grad_norm(self, grads, sizes, max_norm):
         """grads: concatenated gradients of the parameters whose size is positive; a
         negative size is a parameter without a gradient. Returns (norm, clipped)."""
@@ -502,6 +524,19 @@ class Ref:
                                             fp(dx), fp(dp)))
         return y, dx, dp
 
+    def cnn_grads(self, x, labels, params, c1=8, c2=16, classes=10):
+        """One forward and backward: (loss, flat gradients in parameter order)."""
+        x, params = f32(x), f32(params)
+        labels = np.ascontiguousarray(labels, np.int64)
+        b, cin, hw, _ = x.shape
+        loss = np.empty(1, np.float32)
+        grads = np.empty_like(params)
+        f = self.lib.ref_cnn_grads
+        f.argtypes = [_f32p, _i64p] + [_i64] * 6 + [_f32p, _f32p, _f32p]
+        self._ok(f(fp(x), ip(labels), b, cin, c1, c2, hw, classes, fp(params), fp(loss),
+                   fp(grads)))
+        return float(loss[0]), grads
+
     def cnn_train(self, x, labels, params, steps, lr, c1=8, c2=16, classes=10):
         x, params = f32(x), f32(params)
         labels = np.ascontiguousarray(labels, np.int64)
@@ -516,15 +551,24 @@ class Ref:
         return self.lib.ref_charlm_num_params(_i64(vocab), _i64(seq), _i64(d), _i64(heads),
                                               _i64(ff), _i64(layers))
 
-    def charlm_train(self, ids, targets, vocab, d, heads, ff, layers, params, steps, lr):
+    def charlm_train(self, ids, targets, vocab, d, heads, ff, layers, params, steps, lr,
+                     grads0=False):
+        """`steps` Adam steps on one batch: per-step losses and the final parameters, and
+        with grads0 the first step's gradients (flat, parameter order) as a third value."""
         ids, params = f32(ids), f32(params)
         targets = np.ascontiguousarray(targets, np.int64)
         b, s = ids.shape
         losses = np.empty(steps, np.float32)
         out = np.empty_like(params)
-        self._ok(self.lib.ref_charlm_train(fp(ids), ip(targets), b, s, vocab, d, heads, ff, layers,
-                                           fp(params), steps, lr, fp(losses), fp(out)))
-        return losses, out
+        if not grads0:
+            self._ok(self.lib.ref_charlm_train(fp(ids), ip(targets), b, s, vocab, d, heads, ff,
+                                               layers, fp(params), steps, lr, fp(losses), fp(out)))
+            return losses, out
+        g0 = np.empty_like(params)
+        self._ok(self.lib.ref_charlm_train_grads(fp(ids), ip(targets), b, s, vocab, d, heads, ff,
+                                                 layers, fp(params), steps, lr, fp(losses),
+                                                 fp(g0), fp(out)))
+        return losses, out, g0
 
 
 def oracle_or_skip():

@@ -9,7 +9,8 @@ order or uses the device exp/log.
 import numpy as np
 import pytest
 
-from _hip import backend, dev, exact, host, k_tol, print_case, ref_close, ref_err
+from _hip import (backend, dev, exact, gemm_stat_bound, host, k_tol, print_case, ref_close,
+                  ref_err)
 from _oracle import oracle_or_skip
 
 pytestmark = pytest.mark.gpu
@@ -85,13 +86,9 @@ def test_gemm_tile_configs_vs_fp64(hip, name, batch, m, k, n, ta, tb):
     got = hip.gemm(a_st if batch > 1 else a_st[0], b_st if batch > 1 else b_st[0], trans_a=ta,
                    trans_b=tb)
     want = torch.matmul(a.double(), b.double()).reshape(got.shape)
-    # The worst-case error of any fp32 summation order of K products is
-    # (K + 2) u sum_k |a_ik| |b_kj| (u = 2^-24): a bound every correct kernel meets, and one
-    # that a wrong index or a dropped term (an error of the size of the values) breaks.
-    bound = (k + 2) * 2.0 ** -24 * torch.matmul(a.double().abs(), b.double().abs()).reshape(
-        got.shape)
+    bound = gemm_stat_bound(a.double().norm(dim=2), b.double().norm(dim=1), k).reshape(got.shape)
     ratio = ((got.double() - want).abs() / bound.clamp(min=1e-30)).max().item()
-    assert ratio <= 1.0, f"{name}: error reaches {ratio:.3f} of the fp32 summation bound"
+    assert ratio <= 1.0, f"{name}: error reaches {ratio:.3f} of the statistical fp32 bound"
 
 
 @pytest.mark.parametrize("m,k,n", [(37, 53, 29), (256, 512, 128), (9, 50176, 8),
@@ -150,8 +147,8 @@ def test_gemm_small_wave(hip, orc, m, k, n, ta, tb):
     got = host(hip.gemm(dev(a_st), dev(b_st), trans_a=ta, trans_b=tb))
     ref_close(got, orc.matmul(a, b), k_tol(k), "wave gemm")
     a64, b64 = a.astype(np.float64), b.astype(np.float64)
-    bound = (k + 2) * 2.0 ** -24 * (np.abs(a64) @ np.abs(b64))
-    assert np.all(np.abs(got - a64 @ b64) <= bound), "beyond the fp32 summation bound"
+    bound = gemm_stat_bound(np.linalg.norm(a64, axis=1), np.linalg.norm(b64, axis=0), k)
+    assert np.all(np.abs(got - a64 @ b64) <= bound), "beyond the statistical fp32 bound"
     again = host(hip.gemm(dev(a_st), dev(b_st), trans_a=ta, trans_b=tb))
     exact(again, got, "repeat")
 
@@ -205,6 +202,12 @@ def test_gemm_backward_products(hip, orc):
               "dA")
     ref_close(host(hip.gemm(A, dC, trans_a=True)), orc.matmul(orc.transpose(a), dc), k_tol(512),
               "dB")
+    a64, b64, dc64 = (x.astype(np.float64) for x in (a, b, dc))
+    for what, got, x, y in (("C", hip.gemm(A, B), a64, b64),
+                            ("dA", hip.gemm(dC, B, trans_b=True), dc64, b64.T),
+                            ("dB", hip.gemm(A, dC, trans_a=True), a64.T, dc64)):
+        bound = gemm_stat_bound(np.linalg.norm(x, axis=1), np.linalg.norm(y, axis=0), 512)
+        assert np.all(np.abs(host(got) - x @ y) <= bound), f"{what}: beyond the statistical bound"
 
 
 # ------------------------------------------------------------------ element-wise

@@ -316,3 +316,88 @@ def test_charlm_train_bitexact(orc, ref):
     olosses, oparams = K.charlm_train(orc, ids, t, flat, vocab, d, heads, ff, layers, 3, 1e-3)
     exact(olosses, losses)
     exact(oparams, params)
+
+
+# ------------------------------------------------------------------ whole-tensor sums, scalars
+
+@pytest.mark.parametrize("n", [1, 1000, 1 << 20])
+def test_sum_and_mean_bitexact(orc, ref, n):
+    """Tensor::sum() / mean() (src/tensor_ops.cpp:679-712): the oracle's double sum, cast to
+    float, is the reference's sum bit for bit; times 1/n in float it is the mean."""
+    r = rng(n + 31)
+    x = (r.standard_normal(n, np.float32) * 3).astype(np.float32)
+    s = np.float32(orc.sum(x))
+    exact(np.array([s]), np.array([ref.sum(x)]))
+    exact(np.array([s * np.float32(1.0 / n)]), np.array([ref.mean(x)]))
+
+
+@pytest.mark.parametrize("n", [1, 1000, 1 << 20])
+def test_sum_squares_bitexact_through_clip_norm(orc, ref, n):
+    """The double sum of squares behind clip_grad_norm (src/optim.cpp:186-193): for one
+    gradient tensor, float(sqrt(oracle)) is the reference's returned norm bit for bit."""
+    r = rng(n + 57)
+    g = r.standard_normal(n, np.float32)
+    norm, _ = ref.clip_grad_norm(g, [n], 1e30)
+    exact(np.array([np.float32(np.sqrt(orc.sum_squares(g)))]), np.array([np.float32(norm)]))
+
+
+def test_sum_closed_forms(orc):
+    """Mathematics that fixes the double accumulator: integer-valued data sums exactly (the
+    total stays below 2^53), and 2^25 followed by a thousand ones keeps every one, which a
+    float accumulator would round away (the float spacing at 2^25 is 4)."""
+    r = rng(3)
+    x = r.integers(-1000, 1001, 1 << 16).astype(np.float32)
+    assert orc.sum(x) == float(int(x.astype(np.int64).sum()))
+    assert orc.sum_squares(x) == float(int((x.astype(np.int64) ** 2).sum()))
+    big = np.concatenate([[np.float32(2 ** 25)], np.ones(1000, np.float32)])
+    assert orc.sum(big) == 2 ** 25 + 1000
+    sq = np.concatenate([[np.float32(2 ** 12)], np.ones(1000, np.float32)])
+    assert orc.sum_squares(sq) == 2 ** 24 + 1000
+    assert orc.sum(np.zeros(0, np.float32)) == 0.0
+    assert orc.sum(np.array([-3.5], np.float32)) == -3.5
+
+
+@pytest.mark.parametrize("n", [1, 1000, 1 << 20])
+@pytest.mark.parametrize("k", [0.37, -1e-3, 3.0, 0.0, 1e30])
+def test_scalar_add_mul_bitexact(orc, ref, n, k):
+    """t + k and t * k (src/tensor_ops.cpp:276-322) bit for bit, with -0, +-inf and NaN in
+    the input."""
+    r = rng(n + 7)
+    x = r.standard_normal(n, np.float32)
+    x[: min(n, 4)] = np.array([-0.0, np.inf, -np.inf, np.nan], np.float32)[: min(n, 4)]
+    exact(orc.scalar_add(x, k), ref.scalar(x, k))
+    exact(orc.scalar_mul(x, k), ref.scalar(x, k, mul=True))
+
+
+def test_scalar_closed_forms(orc):
+    """x + 0 turns -0 into +0 (IEEE round-to-nearest), x + k and x * k are the single
+    correctly rounded float operations."""
+    x = np.array([-0.0, 1.5, -2.25, 3e38, np.float32(1) / 3], np.float32)
+    y = orc.scalar_add(x, 0.0)
+    assert np.signbit(y[0]) == False  # noqa: E712
+    assert np.array_equal(orc.scalar_add(x, 0.25), x + np.float32(0.25))
+    assert np.array_equal(orc.scalar_mul(x, 2.0), x * np.float32(2.0))
+    assert np.isinf(orc.scalar_add(x, 3e38)[3])
+
+
+# ------------------------------------------------------------------ the GEMM test bound
+
+def test_gemm_stat_bound_catches_a_dropped_term(orc):
+    """The statistical bound the GPU GEMM tests apply (tests/_hip.py gemm_stat_bound) admits
+    the reference's own serial fp32 sum at cfg 2's longest weight-gradient length
+    (K = 12544) and rejects the same sum with one product left out: the mistake is planted
+    in the oracle's operand, on the CPU."""
+    from _hip import gemm_stat_bound
+    r = rng(12544)
+    m, k, n = 16, 12544, 16
+    a = r.standard_normal((m, k), np.float32)
+    b = r.standard_normal((k, n), np.float32)
+    exact64 = a.astype(np.float64) @ b.astype(np.float64)
+    bound = gemm_stat_bound(np.linalg.norm(a.astype(np.float64), axis=1),
+                            np.linalg.norm(b.astype(np.float64), axis=0), k)
+    assert np.all(np.abs(orc.matmul(a, b) - exact64) <= bound)
+    planted = a.copy()
+    planted[:, 777] = 0.0  # one product per output dropped
+    err = np.abs(orc.matmul(planted, b) - exact64)
+    caught = np.mean(err > bound)
+    assert caught >= 0.5, caught
