@@ -232,6 +232,10 @@ void ehip_reset_counters(void) {
     g_failed = 0;
 }
 
+void ehip_fail_launch_after(int64_t n) {
+    g_fail_launch_at = n > 0 ? int64_t(g_launch_serial.load()) + n : 0;
+}
+
 void ehip_transfer_stats(ehip_transfer_stats_t* out) {
     if (out == nullptr) return;
     std::lock_guard<std::mutex> lock(g_stats_mu);

@@ -77,7 +77,7 @@ _SIGS = {
     "ehip_init": [], "ehip_available": [], "ehip_enabled": [], "ehip_set_enabled": [_i],
     "ehip_device_info": [C.POINTER(DeviceInfo)], "ehip_synchronize": [],
     "ehip_stream_synchronize": [_vp], "ehip_kernels_launched": [], "ehip_kernels_failed": [],
-    "ehip_reset_counters": [], "ehip_transfer_stats": [C.POINTER(TransferStats)],
+    "ehip_reset_counters": [], "ehip_fail_launch_after": [_i64], "ehip_transfer_stats": [C.POINTER(TransferStats)],
     "ehip_reset_transfer_stats": [], "ehip_arena_alloc": [_sz, C.POINTER(_vp)],
     "ehip_arena_free": [_vp], "ehip_arena_trim": [], "ehip_arena_stats": [C.POINTER(ArenaStats)],
     "ehip_memcpy_h2d": [_vp, _vp, _sz, _vp], "ehip_memcpy_d2h": [_vp, _vp, _sz, _vp],
@@ -141,6 +141,7 @@ _SIGS = {
 _RESTYPES = {"ehip_last_error": C.c_char_p, "ehip_kernels_launched": C.c_uint64,
              "ehip_conv2d_relu_maxpool_partials": C.c_int64,
              "ehip_kernels_failed": C.c_uint64, "ehip_reset_counters": None,
+             "ehip_fail_launch_after": None,
              "ehip_set_enabled": None, "ehip_transfer_stats": None,
              "ehip_reset_transfer_stats": None, "ehip_arena_free": None,
              "ehip_arena_stats": None}

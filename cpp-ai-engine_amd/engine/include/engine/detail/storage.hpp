@@ -12,6 +12,7 @@
 #define ENGINE_DETAIL_STORAGE_HPP
 
 #include <cstddef>
+#include <cstdint>
 #include <memory>
 #include <vector>
 
@@ -59,6 +60,12 @@ public:
 
     Storage share() const;  // a view of the same buffer
     Storage clone() const;  // a new buffer with the same values (device copy if resident)
+    // True when both are views of one buffer.
+    bool same_buffer(const Storage& other) const noexcept { return buf_ && buf_ == other.buf_; }
+    // A counter of the buffer's mutable accesses (device_mut, device_write,
+    // host_mut, assign): equal values mean the contents have not been handed
+    // out for writing in between.
+    uint64_t version() const noexcept;
 
 private:
     struct Buffer;

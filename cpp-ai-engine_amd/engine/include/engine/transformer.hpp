@@ -3,6 +3,7 @@
 #ifndef ENGINE_TRANSFORMER_HPP
 #define ENGINE_TRANSFORMER_HPP
 
+#include <cstdint>
 #include <memory>
 #include <utility>
 #include <vector>
@@ -10,6 +11,10 @@
 #include "engine/nn.hpp"
 
 namespace engine {
+namespace detail {
+struct RowGather;
+}  // namespace detail
+
 namespace nn {
 
 class LayerNorm : public Module {
@@ -45,6 +50,11 @@ private:
     size_t num_embeddings_;
     size_t dim_;
     Tensor weight_;
+    // The device index of the last ids tensor seen, reused while the same
+    // buffer comes back unmodified (a resident batch uploads it once).
+    Storage ids_seen_;
+    uint64_t ids_version_ = 0;
+    std::shared_ptr<const detail::RowGather> gather_;
 };
 
 Tensor positional_encoding(size_t seq_len, size_t d_model);

@@ -519,6 +519,21 @@ int eng_cnn_grads(const float* x, const int64_t* labels, int64_t batch, int64_t 
     });
 }
 
+// Forward and backward of a CNN that is then destroyed without anything
+// reading its gradients: the fused convolution blocks' weight sums stay queued
+// past the model's lifetime, to be run by whatever engine work comes next.
+int eng_cnn_backward_orphan(const float* x, const int64_t* labels, int64_t batch, int64_t in_c,
+                            int64_t c1, int64_t c2, int64_t hw, int64_t classes,
+                            const float* params) {
+    return guarded([&] {
+        auto model = cnn_model(size_t(in_c), size_t(c1), size_t(c2), size_t(hw), size_t(classes));
+        load_params(model->parameters(), params);
+        Tensor X = make({size_t(batch), size_t(in_c), size_t(hw), size_t(hw)}, x, false);
+        Tensor loss = nn::cross_entropy_loss((*model)(X), labels_of(labels, batch));
+        loss.backward();
+    });
+}
+
 int eng_cnn_train(const float* x, const int64_t* labels, int64_t batch, int64_t in_c, int64_t c1,
                   int64_t c2, int64_t hw, int64_t classes, const float* params, int64_t steps,
                   float lr, float* losses, float* params_out) {
@@ -539,10 +554,13 @@ int eng_cnn_train(const float* x, const int64_t* labels, int64_t batch, int64_t 
     });
 }
 
-int eng_charlm_train(const float* ids, const int64_t* targets, int64_t batch, int64_t seq,
-                     int64_t vocab, int64_t d, int64_t heads, int64_t ff, int64_t layers,
-                     const float* params, int64_t steps, float lr, float* losses,
-                     float* params_out) {
+// `steps` Adam steps of the character model on one batch: the loss of every
+// step, the final parameters and, when grads0 is not NULL, the first step's
+// gradients (after backward, before the update; parameter order).
+int eng_charlm_train_grads(const float* ids, const int64_t* targets, int64_t batch, int64_t seq,
+                           int64_t vocab, int64_t d, int64_t heads, int64_t ff, int64_t layers,
+                           const float* params, int64_t steps, float lr, float* losses,
+                           float* grads0, float* params_out) {
     return guarded([&] {
         CharModel model{size_t(vocab), size_t(seq), size_t(d), size_t(heads), size_t(ff),
                         size_t(layers)};
@@ -556,11 +574,26 @@ int eng_charlm_train(const float* ids, const int64_t* targets, int64_t batch, in
             Tensor logits = model.forward(X, mask).reshape({size_t(batch * seq), size_t(vocab)});
             Tensor loss = nn::cross_entropy_loss(logits, y);
             loss.backward();
+            if (s == 0 && grads0) {
+                size_t off = 0;
+                for (Tensor& p : model.parameters()) {
+                    put(p.grad(), grads0 + off);
+                    off += p.size();
+                }
+            }
             opt.step();
             if (losses) losses[s] = loss.data()[0];
         }
         if (params_out) store_params(model.parameters(), params_out);
     });
+}
+
+int eng_charlm_train(const float* ids, const int64_t* targets, int64_t batch, int64_t seq,
+                     int64_t vocab, int64_t d, int64_t heads, int64_t ff, int64_t layers,
+                     const float* params, int64_t steps, float lr, float* losses,
+                     float* params_out) {
+    return eng_charlm_train_grads(ids, targets, batch, seq, vocab, d, heads, ff, layers, params,
+                                  steps, lr, losses, nullptr, params_out);
 }
 
 int64_t eng_charlm_num_params(int64_t vocab, int64_t seq, int64_t d, int64_t heads, int64_t ff,

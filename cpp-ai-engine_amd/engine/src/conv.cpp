@@ -292,6 +292,8 @@ bool conv2d_relu_maxpool(const Tensor& input, Conv2d& conv, const MaxPool2d& poo
                 if (need_x) x_copy.add_grad(dx);
                 w_copy.add_grad(dw);
                 if (need_b) b_copy.add_grad(db);
+                detail::defer_conv_output(w_copy, dw);
+                if (need_b) detail::defer_conv_output(b_copy, db);
                 return;
             }
             hip::check(ehip_conv2d_relu_maxpool_backward_f32(

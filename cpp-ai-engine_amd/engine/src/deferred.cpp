@@ -1,6 +1,8 @@
 // deferred.cpp -- gradient work queued during backward: the weight-gradient
 // sums of fused convolution blocks, reduced for every layer in one launch
 // (ehip_conv_weight_reduce_f32) instead of one launch per layer.
+#include <memory>
+#include <utility>
 #include <vector>
 
 #include "detail.hpp"
@@ -12,16 +14,32 @@ namespace {
 
 struct Pending {
     std::vector<ehip_conv_reduce_t> jobs;
-    std::vector<Tensor> keep;  // the partial buffers, alive until the launch
+    DeferredKeep keep;
 };
 
 thread_local Pending g_pending;
 
 }  // namespace
 
+void DeferredKeep::reset_outputs() {
+    for (auto& out : outputs) {
+        const std::shared_ptr<TensorImpl> param = out.first.lock();
+        if (param && param->grad && param->grad->storage.same_buffer(out.second))
+            param->grad->storage = Storage(out.second.size(), 0.0f);
+    }
+    outputs.clear();
+}
+
 void defer_conv_reduce(const ehip_conv_reduce_t& job, const Tensor& partials) {
     g_pending.jobs.push_back(job);
-    g_pending.keep.push_back(partials);
+    g_pending.keep.partials.push_back(partials);
+}
+
+void defer_conv_output(const Tensor& param, const Tensor& grad) {
+    // An add_grad between the job and this call may have flushed the queue, and
+    // with it the job that writes `grad`: then there is nothing left to own.
+    if (g_pending.jobs.empty()) return;
+    g_pending.keep.outputs.emplace_back(param.get_impl(), grad.storage().share());
 }
 
 bool deferred_pending() { return !g_pending.jobs.empty(); }
@@ -30,22 +48,24 @@ void flush_deferred() {
     if (g_pending.jobs.empty()) return;
     Pending p;
     std::swap(p, g_pending);
-    hip::check(ehip_conv_weight_reduce_f32(p.jobs.data(), int(p.jobs.size()), nullptr),
-               "conv weight-gradient reduction");
-    // The partial buffers return to the arena here; later work on the same
-    // stream is ordered after the launch that reads them.
+    const int rc = ehip_conv_weight_reduce_f32(p.jobs.data(), int(p.jobs.size()), nullptr);
+    if (rc != EHIP_OK) p.keep.reset_outputs();
+    hip::check(rc, "conv weight-gradient reduction");
+    // The buffers return to the arena here; later work on the same stream is
+    // ordered after the launch that reads and writes them.
 }
 
-void take_deferred(std::vector<ehip_conv_reduce_t>& jobs, std::vector<Tensor>& keep) {
+void take_deferred(std::vector<ehip_conv_reduce_t>& jobs, DeferredKeep& keep) {
     jobs = std::move(g_pending.jobs);
     keep = std::move(g_pending.keep);
     g_pending.jobs.clear();
-    g_pending.keep.clear();
+    g_pending.keep = DeferredKeep{};
 }
 
 void drop_deferred() {
+    g_pending.keep.reset_outputs();
     g_pending.jobs.clear();
-    g_pending.keep.clear();
+    g_pending.keep = DeferredKeep{};
 }
 
 bool grad_adoptable(const Tensor& target) {

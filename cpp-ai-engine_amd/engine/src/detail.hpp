@@ -5,6 +5,9 @@
 #define ENGINE_SRC_DETAIL_HPP
 
 #include <cstdint>
+#include <memory>
+#include <string>
+#include <utility>
 #include <vector>
 
 #include "ehip.h"
@@ -60,20 +63,52 @@ void add_grad_reshaped(Tensor& target, const Tensor& g);
 float* grad_in_place(Tensor& target);
 inline float* dout(Tensor& t) { return t.storage().device_write(); }
 
+// A row gather in device form (the forward of select_rows and Embedding): the
+// source row of every output row and, for the backward's ordered scatter, the
+// inverse map in CSR form (row_ptr over the table's rows, positions ascending
+// within each row). Built on the host from validated indices, then only read,
+// so one index can serve every step of a resident batch.
+struct RowGather {
+    DeviceInts idx, row_ptr, pos;
+    size_t n = 0, rows = 0;
+    bool inverse = false;
+};
+std::shared_ptr<const RowGather> make_row_gather(const std::vector<size_t>& indices, size_t rows,
+                                                 const std::string& shape_str, bool with_inverse);
+Tensor gather_rows(const Tensor& table, const std::shared_ptr<const RowGather>& g);
+
 // Gradient work queued during backward: the weight-gradient sums of fused
-// convolution blocks (deferred.cpp). `partials` is kept alive until they run.
-// The queue is flushed -- one launch for every queued layer -- before anything
-// can read a queued gradient: Tensor::grad(), zero_grad(), the start of
-// autograd::backward, and add_grad when it accumulates into an existing
-// gradient; Adam::step instead takes the jobs into its own launch. A gradient
-// may be queued only when add_grad will adopt its buffer (grad_adoptable).
+// convolution blocks (deferred.cpp). The queue is flushed -- one launch for
+// every queued layer -- before anything can read a queued gradient:
+// Tensor::grad(), zero_grad(), the start of autograd::backward, add_grad when
+// it accumulates into an existing gradient, and a product that adds into a
+// gradient in place; Adam::step instead takes the jobs into its own launch. A
+// gradient may be queued only when add_grad will adopt its buffer
+// (grad_adoptable).
+//
+// The queue owns everything its launch touches: the partials it reads (given
+// to defer_conv_reduce) and the buffers it writes (registered by
+// defer_conv_output after add_grad has adopted them, with the parameter that
+// holds each). So a model destroyed before the flush leaves the sums writing
+// into buffers that are still alive, never into released arena blocks. When
+// queued work is abandoned (an exception in backward, or a failed Adam
+// launch), every gradient it would have written that is still the parameter's
+// gradient goes back to a pending zero -- the state it had before the
+// backward, since only a gradient that was absent or a pending zero is queued.
+struct DeferredKeep {
+    std::vector<Tensor> partials;
+    std::vector<std::pair<std::weak_ptr<TensorImpl>, Storage>> outputs;
+    void reset_outputs();
+};
 void defer_conv_reduce(const ehip_conv_reduce_t& job, const Tensor& partials);
+void defer_conv_output(const Tensor& param, const Tensor& grad);
 bool deferred_pending();
 void flush_deferred();
 void drop_deferred();
-// Moves the queued jobs (and the buffers they read) to the caller, which must
-// launch them before releasing `keep`.
-void take_deferred(std::vector<ehip_conv_reduce_t>& jobs, std::vector<Tensor>& keep);
+// Moves the queued jobs (and the buffers they touch) to the caller, which must
+// launch them before releasing `keep` (and call keep.reset_outputs() if the
+// launch fails).
+void take_deferred(std::vector<ehip_conv_reduce_t>& jobs, DeferredKeep& keep);
 // True when add_grad of a fresh, unshared gradient buffer into `target` adopts
 // that buffer (no gradient yet, or a pending zero).
 bool grad_adoptable(const Tensor& target);

@@ -58,9 +58,11 @@ Adam::Adam(std::vector<Tensor> parameters, float lr, float beta1, float beta2, f
 // per parameter (src/optim.cpp:113-162).
 void Adam::step() {
     autograd::NoGradGuard no_grad;
-    ++t_;
-    const float bias_c1 = 1.0f - std::pow(beta1_, static_cast<float>(t_));
-    const float bias_c2 = 1.0f - std::pow(beta2_, static_cast<float>(t_));
+    // The step count advances only once the update has been launched, so a
+    // step whose launch fails leaves the optimiser exactly as it was.
+    const size_t t = t_ + 1;
+    const float bias_c1 = 1.0f - std::pow(beta1_, static_cast<float>(t));
+    const float bias_c2 = 1.0f - std::pow(beta2_, static_cast<float>(t));
     // Every parameter in one multi-tensor launch; the arithmetic per element is
     // the single-tensor update's.
     std::vector<ehip_adam_tensor_t> table;
@@ -69,7 +71,7 @@ void Adam::step() {
     // update (their gradients are read from the buffers the sums fill, without
     // flushing them first through grad()).
     std::vector<ehip_conv_reduce_t> jobs;
-    std::vector<Tensor> keep;
+    DeferredKeep keep;
     take_deferred(jobs, keep);
     for (size_t i = 0; i < params_.size(); ++i) {
         Tensor& p = params_[i];
@@ -78,15 +80,16 @@ void Adam::step() {
         table.push_back({p.storage().device_mut(), g, m_[i].device_mut(), v_[i].device_mut(),
                          int64_t(p.size())});
     }
-    if (jobs.empty())
-        hip::check(ehip_adam_multi_f32(table.data(), int(table.size()), lr_, beta1_, beta2_, eps_,
-                                       weight_decay_, bias_c1, bias_c2, nullptr),
-                   "adam step");
-    else
-        hip::check(ehip_adam_multi_reduce_f32(table.data(), int(table.size()), jobs.data(),
-                                              int(jobs.size()), lr_, beta1_, beta2_, eps_,
-                                              weight_decay_, bias_c1, bias_c2, nullptr),
-                   "adam step");
+    const int rc =
+        jobs.empty()
+            ? ehip_adam_multi_f32(table.data(), int(table.size()), lr_, beta1_, beta2_, eps_,
+                                  weight_decay_, bias_c1, bias_c2, nullptr)
+            : ehip_adam_multi_reduce_f32(table.data(), int(table.size()), jobs.data(),
+                                         int(jobs.size()), lr_, beta1_, beta2_, eps_,
+                                         weight_decay_, bias_c1, bias_c2, nullptr);
+    if (rc != EHIP_OK) keep.reset_outputs();
+    hip::check(rc, "adam step");
+    t_ = t;
 }
 
 std::vector<Tensor> Adam::state_tensors() const {

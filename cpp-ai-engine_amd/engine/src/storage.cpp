@@ -17,6 +17,7 @@ struct Storage::Buffer {
     bool device_valid = false;
     bool pending = false;  // every element equals fill_value; neither side materialised
     float fill_value = 0.0f;
+    uint64_t version = 0;  // advanced by every accessor that may change the values
 
     ~Buffer() {
         if (dev != nullptr) ehip_arena_free(dev);
@@ -81,6 +82,7 @@ const float* Storage::device() const {
 
 float* Storage::device_mut() {
     if (!buf_) return nullptr;
+    ++buf_->version;
     buf_->to_device();
     buf_->host_valid = false;
     buf_->pending = false;
@@ -89,6 +91,7 @@ float* Storage::device_mut() {
 
 float* Storage::device_write() {
     if (!buf_) return nullptr;
+    ++buf_->version;
     buf_->ensure_alloc();
     buf_->device_valid = true;
     buf_->host_valid = false;
@@ -104,6 +107,7 @@ const std::vector<float>& Storage::host() const {
 
 std::vector<float>& Storage::host_mut() {
     if (!buf_) throw std::logic_error("Storage: empty");
+    ++buf_->version;
     buf_->to_host();
     buf_->device_valid = false;
     buf_->pending = false;
@@ -111,6 +115,8 @@ std::vector<float>& Storage::host_mut() {
 }
 
 bool Storage::resident_on_device() const noexcept { return buf_ && buf_->device_valid; }
+
+uint64_t Storage::version() const noexcept { return buf_ ? buf_->version : 0; }
 
 bool Storage::exclusive() const noexcept { return buf_ && buf_.use_count() == 1; }
 
@@ -127,6 +133,7 @@ bool Storage::pending_zero() const noexcept {
 
 void Storage::assign(float value) {
     if (!buf_) return;
+    ++buf_->version;
     buf_->pending = true;
     buf_->fill_value = value;
     buf_->device_valid = false;

@@ -202,10 +202,12 @@ void detail::add_grad_reshaped(Tensor& target, const Tensor& g) {
 float* detail::grad_in_place(Tensor& target) {
     const std::shared_ptr<TensorImpl>& impl_ = target.get_impl();
     if (!impl_ || !impl_->requires_grad || !impl_->grad) return nullptr;
+    // The product reads the existing gradient: finish any queued sums first
+    // (the queue also holds a view of the buffers it writes, so the exclusivity
+    // test below is only meaningful once it has run).
+    if (deferred_pending()) flush_deferred();
     Storage& acc = impl_->grad->storage;
     if (acc.pending_zero() || !acc.exclusive() || acc.size() != target.size()) return nullptr;
-    // The product reads the existing gradient: finish any queued sums first.
-    if (deferred_pending()) flush_deferred();
     return acc.device_mut();
 }
 
@@ -341,51 +343,68 @@ Tensor Tensor::mean(size_t axis, bool keepdim) const {
 // Rows of the first axis (src/tensor.cpp:556-604). The backward scatters in
 // CSR form: every destination row sums the positions that selected it, in
 // ascending order, which is the reference's loop order.
-Tensor Tensor::select_rows(const std::vector<size_t>& indices) const {
-    if (ndim() < 2)
-        throw std::invalid_argument("select_rows requires at least 2 dimensions; this tensor is " +
-                                    shape_str() + ".");
-    if (indices.empty()) throw std::invalid_argument("select_rows received an empty index list.");
-    const size_t rows = shape()[0];
-    const size_t row_size = rows == 0 ? 0 : size() / rows;
+std::shared_ptr<const detail::RowGather> detail::make_row_gather(
+    const std::vector<size_t>& indices, size_t rows, const std::string& shape_str,
+    bool with_inverse) {
     std::vector<int32_t> idx(indices.size());
     for (size_t i = 0; i < indices.size(); ++i) {
         if (indices[i] >= rows)
             throw std::out_of_range("select_rows: row " + std::to_string(indices[i]) +
-                                    " does not exist in a tensor " + shape_str() + ".");
+                                    " does not exist in a tensor " + shape_str + ".");
         idx[i] = static_cast<int32_t>(indices[i]);
     }
-    std::vector<size_t> out_shape = shape();
-    out_shape[0] = indices.size();
-    const bool req_g = track(requires_grad());
-    Tensor res(out_shape, 0.0f, req_g);
-    const DeviceInts d_idx(idx);
-    hip::check(ehip_select_rows_f32(dptr(*this), d_idx.get(), dout(res), int64_t(idx.size()),
-                                    int64_t(row_size), int64_t(rows), nullptr),
-               "select_rows");
-    if (req_g) {
+    auto g = std::make_shared<RowGather>();
+    g->n = idx.size();
+    g->rows = rows;
+    g->idx = DeviceInts(idx);
+    if (with_inverse) {
         // CSR of the inverse map, built once on the host.
         std::vector<int32_t> row_ptr(rows + 1, 0), pos(idx.size());
         for (int32_t r : idx) ++row_ptr[size_t(r) + 1];
         for (size_t r = 0; r < rows; ++r) row_ptr[r + 1] += row_ptr[r];
         std::vector<int32_t> fill(row_ptr.begin(), row_ptr.end() - 1);
         for (size_t i = 0; i < idx.size(); ++i) pos[size_t(fill[size_t(idx[i])]++)] = int32_t(i);
-        auto d_ptr = std::make_shared<DeviceInts>(row_ptr);
-        auto d_pos = std::make_shared<DeviceInts>(pos);
-        res.impl_->parents = {impl_};
-        Tensor self_copy = *this;
-        const size_t n_src = idx.size();
-        res.impl_->backward_fn = [self_copy, d_ptr, d_pos, rows, row_size,
-                                  n_src](const Tensor& grad_out) mutable {
+        g->row_ptr = DeviceInts(row_ptr);
+        g->pos = DeviceInts(pos);
+        g->inverse = true;
+    }
+    return g;
+}
+
+Tensor detail::gather_rows(const Tensor& table, const std::shared_ptr<const RowGather>& g) {
+    const size_t rows = table.shape()[0];
+    const size_t row_size = rows == 0 ? 0 : table.size() / rows;
+    if (g->rows != rows) throw std::logic_error("gather_rows: index built for another table");
+    std::vector<size_t> out_shape = table.shape();
+    out_shape[0] = g->n;
+    const bool req_g = track(table.requires_grad());
+    if (req_g && !g->inverse) throw std::logic_error("gather_rows: index has no inverse map");
+    Tensor res(out_shape, 0.0f, req_g);
+    hip::check(ehip_select_rows_f32(dptr(table), g->idx.get(), dout(res), int64_t(g->n),
+                                    int64_t(row_size), int64_t(rows), nullptr),
+               "select_rows");
+    if (req_g) {
+        res.get_impl()->parents = {table.get_impl()};
+        Tensor self_copy = table;
+        res.get_impl()->backward_fn = [self_copy, g, rows, row_size](const Tensor& grad_out) mutable {
             Tensor dX(self_copy.shape(), 0.0f, false);
-            hip::check(ehip_scatter_add_rows_f32(dptr(grad_out), d_ptr->get(), d_pos->get(),
+            hip::check(ehip_scatter_add_rows_f32(dptr(grad_out), g->row_ptr.get(), g->pos.get(),
                                                  dout(dX), int64_t(rows), int64_t(row_size),
-                                                 int64_t(n_src), 0, nullptr),
+                                                 int64_t(g->n), 0, nullptr),
                        "select_rows backward");
             self_copy.add_grad(dX);
         };
     }
     return res;
+}
+
+Tensor Tensor::select_rows(const std::vector<size_t>& indices) const {
+    if (ndim() < 2)
+        throw std::invalid_argument("select_rows requires at least 2 dimensions; this tensor is " +
+                                    shape_str() + ".");
+    if (indices.empty()) throw std::invalid_argument("select_rows received an empty index list.");
+    return detail::gather_rows(
+        *this, detail::make_row_gather(indices, shape()[0], shape_str(), track(requires_grad())));
 }
 
 Tensor Tensor::detach() const {

@@ -73,24 +73,40 @@ Embedding::Embedding(size_t num_embeddings, size_t dim) : num_embeddings_(num_em
 }
 
 // ids arrive as floats (batch, seq) and are rounded with llround
-// (src/transformer.cpp:206-231); the gather runs on the device.
+// (src/transformer.cpp:206-231); the gather runs on the device. The rounded,
+// validated indices and the backward's inverse map are uploaded once per ids
+// buffer: while the same buffer comes back with its contents untouched
+// (Storage::version), they are reused and the step moves nothing to the
+// device.
 Tensor Embedding::forward(const Tensor& ids) {
     if (ids.ndim() != 2)
         throw std::invalid_argument("Embedding expects indices (batch, sequence), received " +
                                     ids.shape_str() + ".");
     const size_t batch = ids.shape()[0], seq = ids.shape()[1];
-    std::vector<size_t> indices;
-    indices.reserve(ids.size());
-    const float* v = ids.data();
-    for (size_t i = 0; i < ids.size(); ++i) {
-        const long long id = std::llround(v[i]);
-        if (id < 0 || static_cast<size_t>(id) >= num_embeddings_)
-            throw std::out_of_range("Embedding: token " + std::to_string(id) +
-                                    " is outside a vocabulary of " +
-                                    std::to_string(num_embeddings_) + ".");
-        indices.push_back(static_cast<size_t>(id));
+    const bool need_inverse = detail::track(weight_.requires_grad());
+    const bool reuse = gather_ && ids.storage().same_buffer(ids_seen_) &&
+                       ids.storage().version() == ids_version_ && gather_->n == ids.size() &&
+                       (gather_->inverse || !need_inverse);
+    if (!reuse) {
+        std::vector<size_t> indices;
+        indices.reserve(ids.size());
+        const float* v = ids.data();
+        for (size_t i = 0; i < ids.size(); ++i) {
+            const long long id = std::llround(v[i]);
+            if (id < 0 || static_cast<size_t>(id) >= num_embeddings_)
+                throw std::out_of_range("Embedding: token " + std::to_string(id) +
+                                        " is outside a vocabulary of " +
+                                        std::to_string(num_embeddings_) + ".");
+            indices.push_back(static_cast<size_t>(id));
+        }
+        if (indices.empty())
+            throw std::invalid_argument("select_rows received an empty index list.");
+        gather_ = detail::make_row_gather(indices, num_embeddings_, weight_.shape_str(),
+                                          need_inverse);
+        ids_seen_ = ids.storage().share();
+        ids_version_ = ids.storage().version();
     }
-    return weight_.select_rows(indices).reshape({batch, seq, dim_});
+    return detail::gather_rows(weight_, gather_).reshape({batch, seq, dim_});
 }
 
 std::vector<Tensor> Embedding::parameters() { return {weight_}; }

@@ -46,6 +46,8 @@ def load_library(path=LIB_PATH):
                                                                  _f32p]
     lib.eng_charlm_train.argtypes = [_f32p, _i64p] + [_i64] * 7 + [_f32p, _i64, C.c_float, _f32p,
                                                                     _f32p]
+    lib.eng_charlm_train_grads.argtypes = [_f32p, _i64p] + [_i64] * 7 + [
+        _f32p, _i64, C.c_float, _f32p, _f32p, _f32p]
     lib.eng_trainer_cnn.restype = C.c_void_p
     lib.eng_trainer_cnn.argtypes = [_f32p, _i64p] + [_i64] * 6 + [_f32p, C.c_float]
     lib.eng_trainer_charlm.restype = C.c_void_p
@@ -332,6 +334,15 @@ class Engine:
                                         _fp(params), _fp(loss), _fp(grads)))
         return float(loss[0]), grads
 
+    def cnn_backward_orphan(self, x, labels, params, c1=8, c2=16, classes=10):
+        """Forward + backward of a CNN destroyed before its queued weight sums ran."""
+        x, params = _f32(x), _f32(params)
+        labels = np.ascontiguousarray(labels, np.int64)
+        b, cin, hw, _ = x.shape
+        f = self.lib.eng_cnn_backward_orphan
+        f.argtypes = [_f32p, _i64p] + [_i64] * 6 + [_f32p]
+        self._ok(f(_fp(x), _ip(labels), b, cin, c1, c2, hw, classes, _fp(params)))
+
     def cnn_train(self, x, labels, params, steps, lr, c1=8, c2=16, classes=10):
         x, params = _f32(x), _f32(params)
         labels = np.ascontiguousarray(labels, np.int64)
@@ -346,15 +357,20 @@ class Engine:
         return self.lib.eng_charlm_num_params(_i64(vocab), _i64(seq), _i64(d), _i64(heads),
                                               _i64(ff), _i64(layers))
 
-    def charlm_train(self, ids, targets, vocab, d, heads, ff, layers, params, steps, lr):
+    def charlm_train(self, ids, targets, vocab, d, heads, ff, layers, params, steps, lr,
+                     grads0=False):
+        """`steps` Adam steps on one batch: per-step losses and the final parameters, and
+        with grads0 the first step's gradients (flat, parameter order) as a third value."""
         ids, params = _f32(ids), _f32(params)
         targets = np.ascontiguousarray(targets, np.int64)
         b, s = ids.shape
         losses = np.empty(steps, np.float32)
         out = np.empty_like(params)
-        self._ok(self.lib.eng_charlm_train(_fp(ids), _ip(targets), b, s, vocab, d, heads, ff,
-                                           layers, _fp(params), steps, lr, _fp(losses), _fp(out)))
-        return losses, out
+        g0 = np.empty_like(params) if grads0 else None
+        self._ok(self.lib.eng_charlm_train_grads(_fp(ids), _ip(targets), b, s, vocab, d, heads,
+                                                 ff, layers, _fp(params), steps, lr, _fp(losses),
+                                                 _fp(g0) if grads0 else None, _fp(out)))
+        return (losses, out, g0) if grads0 else (losses, out)
 
 
 class Trainer:

@@ -92,6 +92,14 @@ uint64_t ehip_kernels_launched(void);
 uint64_t ehip_kernels_failed(void);
 void ehip_reset_counters(void);
 
+/* Failure injection for tests: the n-th kernel launch counted from this call
+ * (n >= 1) is refused with EHIP_ELAUNCH and counted as failed, as
+ * ENGINE_HIP_FAIL_LAUNCH=n does from process start; n = 0 turns it off. The
+ * run-time form of the reference's launch-failure path (launch_ok,
+ * src/cuda/kernels.cu:81-157), which its parity tests reach by refusing a
+ * kernel configuration. */
+void ehip_fail_launch_after(int64_t n);
+
 typedef struct {
     uint64_t to_device_bytes, to_host_bytes, device_to_device_bytes;
     uint64_t to_device_count, to_host_count, device_to_device_count;
