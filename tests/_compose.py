@@ -214,10 +214,12 @@ def cnn_param_shapes(c1=8, c2=16, hw=28, classes=10, in_c=1):
 
 
 def split_flat(flat, shapes):
+    """Copies of the tensors of a flat parameter vector (the training loops update them in
+    place, so views would train the caller's vector)."""
     out, off = [], 0
     for s in shapes:
         n = int(np.prod(s))
-        out.append(np.ascontiguousarray(flat[off:off + n].reshape(s)))
+        out.append(np.array(flat[off:off + n], np.float32).reshape(s))
         off += n
     return out
 

@@ -1,0 +1,108 @@
+"""Checks of a training trajectory against the compiled reference: step-1 gradients of every
+parameter tensor, then the Adam updates the trajectory made.
+
+Why updates and not parameters element by element: Adam's step lr m / (sqrt(v) + eps)
+normalises each gradient element, so rounding-level differences between two summation orders
+(GPU tiles against the reference's serial loops) reach every parameter at about their relative
+size (1e-7 .. 1e-4), and a parameter that moved by a large fraction of its own value (embedding
+rows, LayerNorm betas and biases starting at 0) then differs by more than 1e-5 of its value
+although the update agrees to 1e-4. The update vector, final minus initial, is what the
+gradients determine, so it is what is compared.
+
+Gradients that vanish in exact arithmetic: the attention key projection's bias. Adding a
+vector c to every key of a sequence adds q.c to every score of a query row, which the row
+softmax removes, so dL/db_key = 0 identically (src/transformer.cpp:279-304, 332-358). Both
+engines produce rounding noise there (about 1e-9 against gradients of order 1e-2), and Adam
+turns noise of either sign into steps of +-lr, so those updates are not comparable; the check
+is instead that both sides' gradients are at that noise floor.
+"""
+import numpy as np
+
+from _hip import k_tol, ref_close
+
+GRAD_REL = 1e-3      # per tensor: |g - g_ref| / |g_ref| (L2); measured <= 1e-4
+UPDATE_REL = 1e-2    # per tensor: |u - u_ref| / |u_ref| (L2) over well-conditioned elements
+ELEMENT_UPD = 1e-2   # per element, well-conditioned: |u - u_ref| <= ELEMENT_UPD * lr * steps
+WELL = 1e-3          # well-conditioned element: |g_ref| >= WELL * rms(g_ref) of its tensor
+ZERO_FLOOR = 1e-5    # vanishing gradient: max |g| <= ZERO_FLOOR * max |g| of the key weight
+
+
+def cnn_layout(c1=8, c2=16, classes=10, flat=784):
+    return [("conv1.weight", (c1, 1, 3, 3)), ("conv1.bias", (c1,)),
+            ("conv2.weight", (c2, c1, 3, 3)), ("conv2.bias", (c2,)),
+            ("linear.weight", (flat, classes)), ("linear.bias", (1, classes))]
+
+
+def lm_layout(vocab, d, ff, layers):
+    import workloads as W
+    return [(n, s) for n, s, _ in W.lm_param_layout(vocab, d, ff, layers)]
+
+
+def vanishing(name):
+    return name.endswith("attn.key.bias")
+
+
+def split(flat, layout):
+    out, off = {}, 0
+    for name, shape in layout:
+        n = int(np.prod(shape))
+        out[name] = np.asarray(flat[off:off + n], np.float64)
+        off += n
+    assert off == len(flat), (off, len(flat))
+    return out
+
+
+def check_gradients(got, want, layout, reduce_len, what):
+    """Step-1 gradients, every tensor: the reference's metric |d| / max(1, |want|) at the
+    K-term bound k_tol(reduce_len), and |d| / |want| <= GRAD_REL in the L2 norm (gradients are
+    mostly far below 1, where the first metric is an absolute one); vanishing gradients at
+    the noise floor on both sides."""
+    g, w = split(got, layout), split(want, layout)
+    worst = 0.0
+    for name, _ in layout:
+        if vanishing(name):
+            key_w = name.replace("bias", "weight")
+            floor = ZERO_FLOOR * np.abs(w[key_w]).max()
+            assert np.abs(g[name]).max() <= floor and np.abs(w[name]).max() <= floor, \
+                f"{what} {name}: a gradient that vanishes identically is above the noise floor"
+            continue
+        ref_close(g[name], w[name], k_tol(reduce_len), f"{what} gradient {name}")
+        nw = np.linalg.norm(w[name])
+        ratio = np.linalg.norm(g[name] - w[name]) / nw if nw > 0 else np.linalg.norm(g[name])
+        worst = max(worst, ratio)
+        assert ratio <= GRAD_REL, f"{what} gradient {name}: |d| / |g| = {ratio:.3e}"
+    print(f"{what}: step-1 gradients, worst |d| / |g| per tensor {worst:.2e}")
+    return worst
+
+
+def check_updates(p0, got, want, grads0, layout, lr, steps, what):
+    """Final parameters after `steps` Adam steps from p0, as updates u = p - p0 against the
+    reference's. Per tensor (vanishing-gradient tensors excepted), over its well-conditioned
+    elements (|g0| >= WELL rms(g0), where rounding noise is under 0.1 % of the gradient):
+    |u - u_ref| / |u_ref| <= UPDATE_REL in the L2 norm and every element within
+    ELEMENT_UPD lr steps. Every element of every tensor within 2 lr steps (Adam's reach)."""
+    P0, G, W, G0 = split(p0, layout), split(got, layout), split(want, layout), split(grads0, layout)
+    worst_norm, worst_elem, cond = 0.0, 0.0, 0
+    total = 0
+    for name, _ in layout:
+        d = np.abs(G[name] - W[name])
+        assert d.max() <= 2 * lr * steps, f"{what} {name}: beyond Adam's reach"
+        total += d.size
+        if vanishing(name):
+            continue
+        g0 = G0[name]
+        rms = np.sqrt(np.mean(g0 ** 2))
+        well = np.abs(g0) >= WELL * rms if rms > 0 else np.zeros(g0.shape, bool)
+        cond += int(well.sum())
+        if not well.any():
+            continue
+        u, uw = G[name][well] - P0[name][well], W[name][well] - P0[name][well]
+        ratio = np.linalg.norm(u - uw) / max(np.linalg.norm(uw), 1e-30)
+        elem = np.abs(u - uw).max() / (lr * steps)
+        worst_norm, worst_elem = max(worst_norm, ratio), max(worst_elem, elem)
+        assert ratio <= UPDATE_REL, f"{what} {name}: |u - u_ref| / |u_ref| = {ratio:.3e}"
+        assert elem <= ELEMENT_UPD, f"{what} {name}: an update is {elem:.3e} lr steps off"
+    print(f"{what}: updates after {steps} steps, worst |du| / |u| per tensor {worst_norm:.2e}, "
+          f"worst element {worst_elem:.2e} lr steps ({cond} of {total} elements "
+          f"well-conditioned)")
+    return worst_norm, worst_elem

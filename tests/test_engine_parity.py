@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 import _compose as K
+import _trajectory as TR
 from _fixtures import load
 from _hip import k_tol, print_case, ref_close, ref_err
 from _oracle import Ref, oracle_or_skip
@@ -302,8 +303,10 @@ def cnn_inputs(seed=2, batch=64):
 
 
 def test_cnn_training_trajectory(eng, orc, cpu):
-    """cfg 2: ten Adam steps (lr 1e-3) of the small CNN on one seeded batch; the loss of
-    every step agrees with the reference CPU path to 1e-5 relative."""
+    """cfg 2: ten Adam steps (lr 1e-3) of the small CNN on one seeded batch. Every step's
+    loss within 1e-5 relative of the reference CPU path; with the compiled reference, the
+    step-1 gradients of every tensor and the ten steps' updates as tests/_trajectory.py
+    states."""
     print_case("cnn train cfg2")
     x, labels, params = cnn_inputs()
     losses, out = eng.cnn_train(x, labels, params, 10, 1e-3)
@@ -314,20 +317,16 @@ def test_cnn_training_trajectory(eng, orc, cpu):
     rel = np.abs(losses - want_losses) / np.abs(want_losses)
     print("cnn loss rel err per step:", rel)
     assert np.all(rel <= 1e-5), rel
-    # Parameters after ten steps: Adam's normalised update turns rounding-level
-    # gradient differences near zero into up to lr-sized steps, so the bound is lr-scaled.
-    assert np.max(np.abs(out - want_out)) <= 10 * 1e-3 * 2
+    if cpu is not None:
+        loss, g = eng.cnn_grads(x, labels, params)
+        want_loss, want_g = cpu.cnn_grads(x, labels, params)
+        assert abs(loss - want_loss) <= 1e-5 * abs(want_loss)
+        layout = TR.cnn_layout()
+        TR.check_gradients(g, want_g, layout, 64 * 28 * 28, "cnn")
+        TR.check_updates(params, out, want_out, want_g, layout, 1e-3, 10, "cnn")
 
 
-def test_charlm_training_trajectory(eng, orc, cpu):
-    """cfg 3: the character Transformer (2 blocks, d 96, 4 heads, FFN 384, context 64,
-    vocab 121, batch 32), ten Adam steps; per-step loss within 1e-5 relative."""
-    print_case("charlm train cfg3")
-    r = rng(3)
-    vocab, d, heads, ff, layers, b, s = 121, 96, 4, 384, 2, 32, 64
-    n = eng.charlm_num_params(vocab, s, d, heads, ff, layers)
-    shapes = K.charlm_param_shapes(vocab, d, ff, layers)
-    assert sum(int(np.prod(p)) for p in shapes) == n
+def charlm_params(r, shapes, vocab, xavier):
     params = []
     for shp in shapes:
         size = int(np.prod(shp))
@@ -336,60 +335,57 @@ def test_charlm_training_trajectory(eng, orc, cpu):
                           np.zeros(size, np.float32))
         elif shp[0] == 1:
             params.append(np.zeros(size, np.float32))
+        elif xavier:
+            lim = np.sqrt(6.0 / (shp[0] + shp[1]))
+            params.append(r.uniform(-lim, lim, size).astype(np.float32))
         else:
             params.append((r.standard_normal(size) * (0.02 if shp[0] == vocab else
                                                       np.sqrt(2.0 / shp[0]))).astype(np.float32))
-    params = np.concatenate(params)
+    return np.concatenate(params)
+
+
+def lm_trajectory(eng, orc, cpu, dims, seed, steps, xavier, what):
+    vocab, d, heads, ff, layers, b, s = dims
+    r = rng(seed)
+    shapes = K.charlm_param_shapes(vocab, d, ff, layers)
+    assert sum(int(np.prod(p)) for p in shapes) == eng.charlm_num_params(vocab, s, d, heads, ff,
+                                                                         layers)
+    params = charlm_params(r, shapes, vocab, xavier)
     ids = r.integers(0, vocab, (b, s)).astype(np.float32)
     targets = r.integers(0, vocab, b * s)
-    steps = 10 if cpu is not None else 3
-    losses, out = eng.charlm_train(ids, targets, vocab, d, heads, ff, layers, params, steps, 1e-3)
+    if cpu is None:  # the restatement is slow: fewer steps, losses only
+        steps = min(steps, 3 if d < 128 else 1)
+    losses, out, g0 = eng.charlm_train(ids, targets, vocab, d, heads, ff, layers, params, steps,
+                                       1e-3, grads0=True)
     if cpu is not None:
-        want, want_out = cpu.charlm_train(ids, targets, vocab, d, heads, ff, layers, params,
-                                          steps, 1e-3)
+        want, want_out, want_g0 = cpu.charlm_train(ids, targets, vocab, d, heads, ff, layers,
+                                                   params, steps, 1e-3, grads0=True)
     else:
         want, want_out = K.charlm_train(orc, ids, targets, params, vocab, d, heads, ff, layers,
                                         steps, 1e-3)
     rel = np.abs(losses - want) / np.abs(want)
-    print("charlm loss rel err per step:", rel)
+    print(f"{what} loss rel err per step:", rel)
     assert np.all(rel <= 1e-5), rel
-    assert np.max(np.abs(out - want_out)) <= steps * 1e-3 * 2
+    if cpu is not None:
+        layout = TR.lm_layout(vocab, d, ff, layers)
+        TR.check_gradients(g0, want_g0, layout, b * s, what)
+        TR.check_updates(params, out, want_out, want_g0, layout, 1e-3, steps, what)
+
+
+def test_charlm_training_trajectory(eng, orc, cpu):
+    """cfg 3: the character Transformer (2 blocks, d 96, 4 heads, FFN 384, context 64,
+    vocab 121, batch 32), ten Adam steps; per-step loss within 1e-5 relative, step-1
+    gradients and the updates as tests/_trajectory.py states."""
+    print_case("charlm train cfg3")
+    lm_trajectory(eng, orc, cpu, (121, 96, 4, 384, 2, 32, 64), 3, 10, False, "charlm")
 
 
 def test_transformer_medium_trajectory(eng, orc, cpu):
     """A deeper, wider stack than cfg 3 (4 pre-LN blocks, d 256, 8 heads, FFN 1024, context
-    128, vocab 256, batch 8), so the larger GEMM tiles and longer reductions of cfg 5 run
-    inside a training step; three Adam steps, per-step loss within 1e-5 relative."""
+    128, vocab 256, batch 8), so the larger GEMM tiles and longer reductions run inside a
+    training step; three Adam steps, checked as the cfg 3 trajectory."""
     print_case("transformer medium")
-    r = rng(5)
-    vocab, d, heads, ff, layers, b, s = 256, 256, 8, 1024, 4, 8, 128
-    shapes = K.charlm_param_shapes(vocab, d, ff, layers)
-    params = []
-    for shp in shapes:
-        size = int(np.prod(shp))
-        if len(shp) == 1:
-            params.append(np.ones(size, np.float32) if len(params) % 2 == 1 else
-                          np.zeros(size, np.float32))
-        elif shp[0] == 1:
-            params.append(np.zeros(size, np.float32))
-        else:
-            lim = np.sqrt(6.0 / (shp[0] + shp[1]))
-            params.append(r.uniform(-lim, lim, size).astype(np.float32))
-    params = np.concatenate(params)
-    ids = r.integers(0, vocab, (b, s)).astype(np.float32)
-    targets = r.integers(0, vocab, b * s)
-    steps = 3 if cpu is not None else 1
-    losses, out = eng.charlm_train(ids, targets, vocab, d, heads, ff, layers, params, steps, 1e-3)
-    if cpu is not None:
-        want, want_out = cpu.charlm_train(ids, targets, vocab, d, heads, ff, layers, params,
-                                          steps, 1e-3)
-    else:
-        want, want_out = K.charlm_train(orc, ids, targets, params, vocab, d, heads, ff, layers,
-                                        steps, 1e-3)
-    rel = np.abs(losses - want) / np.abs(want)
-    print("medium loss", losses, "rel err", rel)
-    assert np.all(rel <= 1e-5), rel
-    assert np.max(np.abs(out - want_out)) <= steps * 1e-3 * 2
+    lm_trajectory(eng, orc, cpu, (256, 256, 8, 1024, 4, 8, 128), 5, 3, True, "medium")
 
 
 # ------------------------------------------------------------------ checkpoints
