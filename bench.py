@@ -1,23 +1,28 @@
 #!/usr/bin/env python3
 """Benchmark of the fp32 training path on one MI355X.
 
-Prints ONE JSON line. The headline workload is BASELINE.json's configs[1]: the small CNN
-training step (conv 1->8 -> ReLU -> pool, conv 8->16 -> ReLU -> pool, linear 784->10,
-softmax cross-entropy, Adam lr 1e-3) on a resident synthetic batch of 64 MNIST-shaped
-images. `value` is training steps per second through the C++ engine (forward, backward and
-the Adam update, all on the GPU), timed with HIP events on the engine's stream over exactly
---steps steps after --warmup untimed steps.
+Prints ONE JSON line. The headline workload is the largest configuration that fits one GPU,
+the scaled Transformer training step (12 pre-LN blocks, d_model
+1024, 16 heads, FFN 4096, context 512, byte vocabulary 256, batch 16, causal; forward,
+backward and Adam lr 1e-3) on a resident synthetic batch, from seeded parameters drawn with
+the reference's initialisers (workloads.py; the same ones tests/test_cfg5_parity.py checks
+against the compiled reference). `value` is training steps per second through the C++ engine,
+timed with HIP events on the engine's stream over exactly --steps steps after --warmup
+untimed steps; every step also carries its own event pair, for the median.
 
 The same line carries:
-  roofline      the step's dominant kernel, timed live in isolation with HIP events at
-                its in-step shape, against its roofline (HBM or fp32 MFMA);
-  cpu_baseline  the reference engine compiled from its own sources (oracle/_ref), running
-                the same training step on the host cores for a bounded sample;
-  extra         the other configurations: cfg 1 GEMMs (512^3 and 4096^3), cfg 3 and cfg 5
-                training steps, cfg 4 bandwidth kernels, each with its roofline fraction.
+  roofline      the step's dominant kernel, the MFMA weight-gradient products dW = X^T dY
+                (gemm_kernel<128,128,32,64,32,true,false>), timed live at their in-step
+                shapes with HIP events, against the fp32 MFMA peak;
+  cpu_baseline  the reference engine compiled from its own sources (oracle/_ref) running a
+                bounded sample of the same training step on the host cores;
+  extra         the other configurations: cfg 2 CNN and cfg 3 char-Transformer steps (each
+                with its own reference CPU baseline), cfg 1 GEMMs (512^3 and 4096^3), cfg 4
+                bandwidth kernels and the path's other bandwidth kernels, each with its
+                roofline fraction.
 
-Only the cpu_baseline leg touches oracle/ (through tests/_oracle.py), as the reference
-being timed; nothing measured on the GPU goes through it.
+Only the cpu_baseline legs touch oracle/ (through tests/_oracle.py), as the reference being
+timed; nothing measured on the GPU goes through it.
 """
 import argparse
 import json
@@ -30,6 +35,8 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(ROOT, "cpp-ai-engine_amd")
 sys.path.insert(0, PKG)
+
+import workloads as W  # noqa: E402
 
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, published
@@ -44,40 +51,8 @@ def metric_name():
         return json.load(f)["metric"]
 
 
-# ------------------------------------------------------------------ inputs
-
-def cnn_inputs(seed=2, batch=64):
-    """Pixels U[0,1], labels U{0..9}, Kaiming-uniform weights, zero biases."""
-    r = np.random.default_rng(seed)
-    x = r.uniform(0.0, 1.0, (batch, 1, 28, 28)).astype(np.float32)
-    labels = r.integers(0, 10, batch)
-    shapes = [(8, 1, 3, 3), (8,), (16, 8, 3, 3), (16,), (784, 10), (1, 10)]
-    params = []
-    for shp in shapes:
-        n = int(np.prod(shp))
-        if len(shp) == 1 or shp[0] == 1:
-            params.append(np.zeros(n, np.float32))
-        else:
-            fan_in = int(np.prod(shp[1:])) if len(shp) == 4 else shp[0]
-            lim = np.sqrt(6.0 / fan_in)
-            params.append(r.uniform(-lim, lim, n).astype(np.float32))
-    return x, labels, np.concatenate(params)
-
-
-def lm_inputs(seed, batch, seq, vocab):
-    r = np.random.default_rng(seed)
-    ids = r.integers(0, vocab, (batch, seq)).astype(np.float32)
-    targets = r.integers(0, vocab, batch * seq)
-    return ids, targets
-
-
-def lm_step_flops(batch, seq, d, ff, vocab, layers):
-    """Algorithmic FLOPs of one training step: every GEMM forward (2mnk) plus its two
-    backward products; the full S x S scores are computed (the mask saves nothing)."""
-    t = batch * seq
-    per_block = 2 * t * d * d * 4 + 2 * t * d * ff * 2 + 2 * batch * seq * seq * d * 2
-    fwd = layers * per_block + 2 * t * d * vocab
-    return 3 * fwd
+# Seeds of the synthetic workloads (workloads.py); the cfg 5 ones are the parity test's.
+CFG5_PARAM_SEED, LM_INPUT_SEED = 11, 3
 
 
 # ------------------------------------------------------------------ timing
@@ -104,6 +79,22 @@ class Timer:
         torch.cuda.synchronize()
         return start.elapsed_time(stop) * 1e-3 / steps  # seconds per call
 
+    def time_steps(self, fn, steps, warmup):
+        """Exactly `steps` calls after `warmup` untimed ones, an event recorded before each
+        call and after the last: (seconds for all of them, [seconds per call])."""
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        ev[0].record()
+        for i in range(steps):
+            fn()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        per = [ev[i].elapsed_time(ev[i + 1]) * 1e-3 for i in range(steps)]
+        return ev[0].elapsed_time(ev[-1]) * 1e-3, per
+
     def time_batch(self, enqueue, reps, warmup):
         """enqueue(n) puts n launches on the stream from native code in one call, so the
         events see back-to-back kernels rather than Python's launch gaps."""
@@ -117,6 +108,11 @@ class Timer:
         stop.record()
         torch.cuda.synchronize()
         return start.elapsed_time(stop) * 1e-3 / reps
+
+    def median_batch(self, enqueue, reps, warmup, repeats=15):
+        """Median over `repeats` timed batches of time_batch (seconds per launch)."""
+        t = [self.time_batch(enqueue, reps, warmup if i == 0 else 0) for i in range(repeats)]
+        return float(np.median(t))
 
 
 def roofline(name, bound, work, seconds, traffic=None):
@@ -140,35 +136,186 @@ def committed_traffic(kernel):
         return json.load(f).get(kernel)
 
 
-# ------------------------------------------------------------------ legs
+def host_info():
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return {"cpu_model": model, "nproc": os.cpu_count(), "usable_cpus": usable}
 
-def headline(engine_mod, timer, steps, warmup):
-    x, labels, params = cnn_inputs()
-    eng = engine_mod.Engine()
+
+def cpu_threads():
+    """All host cores this process may use (BENCH_CPU_THREADS overrides)."""
+    return int(os.environ.get("BENCH_CPU_THREADS", "0")) or host_info()["usable_cpus"] or 1
+
+
+# ------------------------------------------------------------------ cfg 5 (headline)
+
+def lm_step_flops(batch, seq, d, ff, vocab, layers):
+    """Algorithmic FLOPs of one training step: every GEMM forward (2mnk) plus its two
+    backward products; the full S x S scores are computed (the mask saves nothing)."""
+    t = batch * seq
+    per_block = 2 * t * d * d * 4 + 2 * t * d * ff * 2 + 2 * batch * seq * seq * d * 2
+    fwd = layers * per_block + 2 * t * d * vocab
+    return 3 * fwd
+
+
+def cfg5_leg(engine_mod, eng, timer, steps, warmup):
+    """cfg 5 training steps through the engine: forward + backward + Adam on one resident
+    batch; returns the record."""
+    b, s, vocab, d, h, ff, layers = W.TRANSFORMER_CFG5
+    params = W.lm_init_params(CFG5_PARAM_SEED, vocab, d, ff, layers)
+    ids, targets = W.lm_inputs(LM_INPUT_SEED, b, s, vocab)
+    tr = engine_mod.Trainer.charlm(eng, ids, targets, vocab, d, h, ff, layers, params, lr=1e-3)
+    del params
+    tr.step()
+    first = tr.loss()
+    total, per = timer.time_steps(tr.step, steps, max(warmup - 1, 0))
+    last = tr.loss()
+    n_params = int(tr.num_params())
+    tr.close()
+    fl = lm_step_flops(b, s, d, ff, vocab, layers)
+    sec = total / steps
+    return {"seconds": sec, "median_s": float(np.median(per)), "params": n_params,
+            "step_tflop": fl / 1e12, "loss_first_step": first, "loss_last": last,
+            "per_step_ms": [round(x * 1e3, 3) for x in per]}
+
+
+def cfg5_dw_shapes():
+    """The weight-gradient products of one cfg 5 block, dW = X^T dY with X (tokens, in) and
+    dY (tokens, out): (in, out, tokens, count) for the query/key/value/output projections,
+    ff1 and ff2. The engine's Linear backward issues exactly these ehip_gemm_f32 calls
+    (trans_a = 1, beta = 0), 12 blocks per step."""
+    b, s, _, d, _, ff, _ = W.TRANSFORMER_CFG5
+    t = b * s
+    return [(d, d, t, 4), (d, ff, t, 1), (ff, d, t, 1)]
+
+
+def dominant_kernel(eng, timer, torch):
+    """The cfg 5 step's largest kernel by total time (rocprofv3 --kernel-trace --stats of
+    this benchmark, profiles/transformer_cfg5_kernels.md): the weight-gradient products,
+    gemm_kernel<128,128,32,64,32,true,false> (A read transposed), 6 per block. Timed live at
+    their in-step shapes as back-to-back launches from native code between HIP events on
+    the engine's stream (median of 15 batches per shape); splitk_reduce launches, where the
+    dispatcher splits K, are inside the timed region. Algorithmic FLOPs per block =
+    sum over the six products of 2 * in * out * tokens = 206.2 GFLOP; `achieved` = that /
+    the six products' summed time."""
+    r = torch.Generator(device="cuda").manual_seed(6)
+    flops, secs, shapes = 0.0, 0.0, {}
+    for m, n, k, count in cfg5_dw_shapes():
+        x = torch.randn(k, m, device="cuda", generator=r)
+        dy = torch.randn(k, n, device="cuda", generator=r)
+        dw = torch.empty(m, n, device="cuda")
+        sec = timer.median_batch(lambda reps: eng.repeat_gemm(reps, x, dy, dw, trans_a=True),
+                                 10, 3)
+        fl = 2.0 * m * n * k
+        shapes[f"{m}x{n}x{k}"] = {"count_per_block": count, "us": round(sec * 1e6, 2),
+                                  "tflops": round(fl / sec / 1e12, 2)}
+        flops += count * fl
+        secs += count * sec
+        del x, dy, dw
+    roof = roofline("gemm_kernel<128,128,32,64,32,true,false> (+splitk_reduce): cfg5 weight "
+                    "gradients dW = X^T dY, one block's six products (4 x 1024x1024x8192, "
+                    "1024x4096x8192, 4096x1024x8192)", "mfma", flops / 6, secs / 6,
+                    committed_traffic("cfg5_dw_gemm"))
+    roof["flop_per_launch"] = flops / 6
+    roof["shapes"] = shapes
+    return roof
+
+
+def cpu_cfg5_baseline(sample_batch):
+    """A bounded sample of the cfg 5 step on the reference engine (oracle/_ref) on all host
+    cores: the full 12-block model from the same initial parameters, one training step
+    (forward, backward, Adam) over `sample_batch` of the 16 sequences. The step's work is
+    linear in the batch except the Adam update over the 151.7 M parameters, which is timed on
+    its own (the reference's Adam over one flat tensor of that size) and counted once:
+    t(16) = (16 / sample_batch) * (t(sample) - t(adam)) + t(adam)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from _oracle import Ref
+    b, s, vocab, d, h, ff, layers = W.TRANSFORMER_CFG5
+    threads = cpu_threads()
+    ref = Ref()
+    ref.set_threads(threads)
+    params = W.lm_init_params(CFG5_PARAM_SEED, vocab, d, ff, layers)
+    ids, targets = W.lm_inputs(LM_INPUT_SEED, b, s, vocab)
+    ids, targets = ids[:sample_batch], targets[:sample_batch * s]
+    t0 = time.perf_counter()
+    losses, _ = ref.charlm_train(ids, targets, vocab, d, h, ff, layers, params, 1, 1e-3)
+    t_sample = time.perf_counter() - t0
+    assert np.all(np.isfinite(losses))
+    g = np.full(params.size, 1e-3, np.float32)
+    t0 = time.perf_counter()
+    ref.adam_steps(params, g, 1e-3)
+    t_adam = time.perf_counter() - t0
+    t_full = (b / sample_batch) * (t_sample - t_adam) + t_adam
+    return {"value": round(1.0 / t_full, 5), "unit": "steps/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"cfg5 training step of the reference engine compiled from its own sources "
+                      f"(oracle/_ref, g++ -O3, no -march) on {threads} host threads: the full "
+                      f"12-block model from the GPU run's initial parameters, one step (forward, "
+                      f"backward, Adam) over {sample_batch} of the 16 sequences in "
+                      f"{t_sample:.1f} s, of which Adam over 151.7 M parameters {t_adam:.1f} s; "
+                      f"scaled to 16 sequences as (16/{sample_batch})(t - t_adam) + t_adam = "
+                      f"{t_full:.1f} s per step",
+            "seconds_sample": round(t_sample, 2), "seconds_adam": round(t_adam, 2),
+            "seconds_per_step_scaled": round(t_full, 2), **host_info()}
+
+
+def cpu_matmul_threads(threads_list):
+    """cfg 1 on the reference CPU path: C = A B at 512^3 on 1 thread and on all threads."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from _oracle import Ref
+    r = np.random.default_rng(512)
+    a = r.standard_normal((512, 512), np.float32)
+    b = r.standard_normal((512, 512), np.float32)
+    ref = Ref()
+    out = {}
+    for t in threads_list:
+        ref.set_threads(t)
+        ref.matmul(a, b)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 1.0 or reps < 3:
+            ref.matmul(a, b)
+            reps += 1
+        sec = (time.perf_counter() - t0) / reps
+        out[f"{t}_threads"] = {"ms": round(sec * 1e3, 3),
+                               "gflops": round(2 * 512 ** 3 / sec / 1e9, 2)}
+    return out
+
+
+# ------------------------------------------------------------------ cfg 2, cfg 3
+
+def cnn_leg(engine_mod, eng, timer, steps, warmup):
+    x, labels, params = W.cnn_inputs()
     tr = engine_mod.Trainer.cnn(eng, x, labels, params, lr=1e-3)
-    first = None
-    for i in range(2):
-        tr.step()
-        if i == 0:
-            first = tr.loss()
-    sec = timer.time(tr.step, steps, warmup)
+    tr.step()
+    first = tr.loss()
+    total, per = timer.time_steps(tr.step, steps, max(warmup - 1, 0))
     last = tr.loss()
     assert np.isfinite(first) and np.isfinite(last), (first, last)
     tr.close()
-    return sec, first, last
+    sec = total / steps
+    return {"steps_per_s": round(1.0 / sec, 2), "ms_per_step": round(sec * 1e3, 4),
+            "median_ms_per_step": round(float(np.median(per)) * 1e3, 4),
+            "loss_first_step": round(first, 5), "loss_last": round(last, 5)}
 
 
-def dominant_kernel(eng, hip, timer, torch):
-    """The CNN step's largest kernel by total time (rocprofv3 --kernel-trace --stats of
-    this benchmark, profiles/cnn_step_kernels.md): the backward of the fused conv2 block
-    (Conv2d 8 -> 16, 3x3, pad 1 -> ReLU -> MaxPool2d 2 on a 64 x 8 x 14 x 14 input) --
-    conv3_pool_backward (per tile of four rows: the output gradient scattered from the
-    pooled cells into LDS, the input gradient and the weight-gradient partials in one
-    launch) and conv_weight_reduce (the partials' ordered sum) -- timed as that launch
-    pair.
-    HBM-bound by its data, latency-bound at this size: algorithmic bytes = x, the pooled
-    gradient, the pooled values, the argmax and the weights read once, dx, dW and db
-    written once."""
+def cnn_dominant_kernel(eng, hip, timer, torch):
+    """The cfg 2 step's largest kernel by total time (profiles/cnn_step_kernels.md): the
+    backward of the fused conv2 block (Conv2d 8 -> 16, 3x3, pad 1 -> ReLU -> MaxPool2d 2 on a
+    64 x 8 x 14 x 14 input) -- conv3_pool_backward and conv_weight_reduce -- timed as that
+    launch pair. HBM-bound by its data, latency-bound at this size: algorithmic bytes = x,
+    the pooled gradient, the pooled values, the argmax and the weights read once, dx, dW and
+    db written once."""
     r = torch.Generator(device="cuda").manual_seed(5)
     x = torch.rand(64, 8, 14, 14, device="cuda", generator=r)
     w = torch.rand(16, 8, 3, 3, device="cuda", generator=r) * 0.6 - 0.3
@@ -177,32 +324,20 @@ def dominant_kernel(eng, hip, timer, torch):
     g = torch.randn(out.shape, device="cuda", generator=r)
     dx, dw, db = torch.empty_like(x), torch.empty_like(w), torch.empty_like(b)
     cw, pw = hip.conv_relu_pool_windows(x.shape, w.shape, 1, 1, 2)
-    sec = timer.time_batch(
+    sec = timer.median_batch(
         lambda n: eng.repeat_conv_relu_pool_backward(n, x, w, g, out, am, dw, db, cw, pw, dx=dx),
-        500, 50)
+        100, 50)
     work = 4 * (2 * x.numel() + 3 * out.numel() + 2 * w.numel() + b.numel())
-    return roofline("conv3_pool_backward<2,4,512>+conv_weight_reduce (conv2 block dx/dW/db, "
+    return roofline("conv3_pool_backward+conv_weight_reduce (conv2 block dx/dW/db, "
                     "64x8x14x14, 16 filters 3x3, pool 2)", "hbm", work, sec,
                     committed_traffic("conv2_block_backward"))
 
 
-def kernel_only(eng, hip, timer, torch):
-    """For counter runs: 100 launches of the dominant kernel, then 100 launches of the
-    gradient-initialise kernel over 16 Mi floats (reads 64 MiB, writes 64 MiB), the copy
-    of known size that scales FETCH_SIZE / WRITE_SIZE to bytes."""
-    roof = dominant_kernel(eng, hip, timer, torch)
-    n = 1 << 24
-    src = torch.randn(n, device="cuda")
-    dst = torch.empty(n, device="cuda")
-    sec = timer.time(lambda: hip.accumulate_grad(dst, src, True), 100, 0)
-    print(json.dumps({"dominant": roof, "copy_64MiB_us": round(sec * 1e6, 3)}), flush=True)
-
-
-def cpu_baseline(seconds_target):
+def cpu_cnn_baseline(seconds_target):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from _oracle import Ref
-    x, labels, params = cnn_inputs()
-    threads = int(os.environ.get("BENCH_CPU_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    x, labels, params = W.cnn_inputs()
+    threads = cpu_threads()
     ref = Ref()
     ref.set_threads(threads)
     t0 = time.perf_counter()
@@ -225,7 +360,7 @@ def cpu_charlm_baseline(ids, targets, dims, params, seconds_target):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from _oracle import Ref
     vocab, d, h, ff, layers = dims
-    threads = int(os.environ.get("BENCH_CPU_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     ref = Ref()
     ref.set_threads(threads)
     t0 = time.perf_counter()
@@ -243,33 +378,29 @@ def cpu_charlm_baseline(ids, targets, dims, params, seconds_target):
                       f"parameters, {dt:.1f} s"}
 
 
-# (batch, seq, vocab, d_model, heads, ffn, layers, timed steps, warm-up steps)
-LM_CONFIGS = {"charlm_cfg3": (32, 64, 121, 96, 4, 384, 2, 100, 10),
-              "transformer_cfg5": (16, 512, 256, 1024, 16, 4096, 12, 5, 2)}
-
-
-def lm_leg(engine_mod, eng, timer, dims, keep_params=False):
-    """One character-model Transformer training-step measurement (forward +
-    backward + Adam on a resident synthetic batch); returns (record, initial
-    parameters or None)."""
-    b, s, vocab, d, h, ff, layers, steps, warm = dims
-    ids, targets = lm_inputs(3, b, s, vocab)
-    tr = engine_mod.Trainer.charlm(eng, ids, targets, vocab, d, h, ff, layers, lr=1e-3)
-    p0 = tr.params() if keep_params else None
-    first = None
-    if warm > 0:
-        tr.step()
-        first = tr.loss()
-    sec = timer.time(tr.step, steps, max(warm - 1, 0))
+def charlm_leg(engine_mod, eng, timer, cpu_seconds):
+    b, s, vocab, d, h, ff, layers = W.CHARLM_CFG3
+    ids, targets = W.lm_inputs(LM_INPUT_SEED, b, s, vocab)
+    params = W.lm_init_params(CFG5_PARAM_SEED, vocab, d, ff, layers)
+    tr = engine_mod.Trainer.charlm(eng, ids, targets, vocab, d, h, ff, layers, params, lr=1e-3)
+    tr.step()
+    first = tr.loss()
+    total, per = timer.time_steps(tr.step, 100, 9)
     fl = lm_step_flops(b, s, d, ff, vocab, layers)
+    sec = total / 100
     rec = {"steps_per_s": round(1.0 / sec, 3), "ms_per_step": round(sec * 1e3, 3),
+           "median_ms_per_step": round(float(np.median(per)) * 1e3, 4),
            "params": int(tr.num_params()), "step_tflop": round(fl / 1e12, 4),
            "achieved_tflops": round(fl / sec / 1e12, 2),
            "frac_of_mfma_peak": round(fl / sec / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
-           "loss_first_step": None if first is None else round(first, 5),
-           "loss_after": round(tr.loss(), 5)}
+           "loss_first_step": round(first, 5), "loss_last": round(tr.loss(), 5)}
     tr.close()
-    return rec, p0
+    if cpu_seconds > 0:
+        log("bench: reference CPU baseline, cfg3")
+        cpu = cpu_charlm_baseline(ids, targets, (vocab, d, h, ff, layers), params, cpu_seconds)
+        rec["cpu_baseline"] = cpu
+        rec["gpu_over_cpu"] = round(rec["steps_per_s"] / cpu["value"], 1)
+    return rec
 
 
 def bandwidth_large(hip, timer, torch, r):
@@ -317,6 +448,17 @@ def bandwidth_large(hip, timer, torch, r):
 
 def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
     out = {}
+    # cfg 2 and cfg 3: the launch-bound training steps, each with its reference CPU baseline.
+    log("bench: cfg2 CNN training step")
+    out["cnn_cfg2"] = cnn_leg(engine_mod, eng, timer, 200, 20)
+    out["cnn_cfg2"]["roofline"] = cnn_dominant_kernel(eng, hip, timer, torch)
+    if cpu_seconds > 0:
+        log("bench: reference CPU baseline, cfg2")
+        cpu = cpu_cnn_baseline(cpu_seconds)
+        out["cnn_cfg2"]["cpu_baseline"] = cpu
+        out["cnn_cfg2"]["gpu_over_cpu"] = round(out["cnn_cfg2"]["steps_per_s"] / cpu["value"], 1)
+    log("bench: cfg3 char-Transformer training step")
+    out["charlm_cfg3"] = charlm_leg(engine_mod, eng, timer, cpu_seconds)
     # cfg 1: C = A B and both backward products at 512^3 (805.3 MFLOP per trio), and 4096^3.
     for n in (512, 4096):
         r = torch.Generator(device="cuda").manual_seed(n)
@@ -411,40 +553,47 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
     # and tail are a small part of the time.
     out["bandwidth_2^28"] = bandwidth_large(hip, timer, torch, r)
     torch.cuda.empty_cache()
-    # cfg 3 and cfg 5: Transformer training steps.
-    for tag, dims in LM_CONFIGS.items():
-        ids, targets = lm_inputs(3, dims[0], dims[1], dims[2])
-        out[tag], p0 = lm_leg(engine_mod, eng, timer, dims,
-                              keep_params=tag == "charlm_cfg3" and cpu_seconds > 0)
-        b, s, vocab, d, h, ff, layers, steps, warm = dims
-        if p0 is not None:
-            log("bench: reference CPU baseline, cfg3")
-            cpu = cpu_charlm_baseline(ids, targets, (vocab, d, h, ff, layers), p0, cpu_seconds)
-            out[tag]["cpu_baseline"] = cpu
-            out[tag]["gpu_over_cpu"] = round(out[tag]["steps_per_s"] / cpu["value"], 1)
     return out
+
+
+def kernel_only(eng, hip, timer, torch):
+    """For counter runs: the dominant kernel's leg (the six weight-gradient products of a
+    cfg 5 block, launched as in dominant_kernel), then 100 launches of the
+    gradient-initialise kernel over 16 Mi floats (reads 64 MiB, writes 64 MiB), the copy of
+    known size that scales FETCH_SIZE / WRITE_SIZE to bytes."""
+    roof = dominant_kernel(eng, timer, torch)
+    n = 1 << 24
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty(n, device="cuda")
+    sec = timer.time(lambda: hip.accumulate_grad(dst, src, True), 100, 0)
+    print(json.dumps({"dominant": roof, "copy_64MiB_us": round(sec * 1e6, 3)}), flush=True)
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="target length of the cfg 2 / cfg 3 reference CPU samples")
+    ap.add_argument("--cpu-sample-batch", type=int, default=1,
+                    help="sequences of the cfg 5 batch in the reference CPU sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
                     help="run only the dominant kernel and a copy kernel of known size (for "
                          "rocprofv3 --pmc runs) and print their timings")
     ap.add_argument("--transformer-only", action="store_true",
-                    help="run only the cfg5 Transformer step leg (for kernel profiles) and "
-                         "print its record")
+                    help="the cfg 5 step and its dominant kernel only (no CPU baseline, no "
+                         "other configurations): the kernel profile's command")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}, WORLD_SIZE {world}).", file=sys.stderr)
         sys.exit(2)
+    if args.transformer_only:
+        args.no_cpu = args.no_extra = True
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs the GPU"
@@ -457,26 +606,26 @@ def main():
     if args.kernel_only:
         kernel_only(eng, hip, timer, torch)
         return
-    if args.transformer_only:
-        rec, _ = lm_leg(engine_capi, eng, timer, LM_CONFIGS["transformer_cfg5"])
-        print(json.dumps({"transformer_cfg5": rec}), flush=True)
-        return
 
-    log("bench: cfg2 CNN training step")
-    sec, first, last = headline(engine_capi, timer, args.steps, args.warmup)
-    log(f"bench: {sec * 1e3:.4f} ms/step, loss {first:.5f} -> {last:.5f}")
-    log("bench: dominant kernel")
-    roof = dominant_kernel(eng, hip, timer, torch)
+    log("bench: cfg5 Transformer training step")
+    rec = cfg5_leg(engine_capi, eng, timer, args.steps, args.warmup)
+    sec = rec["seconds"]
+    log(f"bench: {sec * 1e3:.3f} ms/step (median {rec['median_s'] * 1e3:.3f}), "
+        f"loss {rec['loss_first_step']:.5f} -> {rec['loss_last']:.5f}")
+    log("bench: dominant kernel (cfg5 weight-gradient products)")
+    roof = dominant_kernel(eng, timer, torch)
     cpu = None
     if not args.no_cpu:
-        log("bench: reference CPU baseline")
-        cpu = cpu_baseline(args.cpu_seconds)
+        log("bench: reference CPU baseline (cfg5 sample)")
+        cpu = cpu_cfg5_baseline(args.cpu_sample_batch)
+        cpu["matmul_512^3"] = cpu_matmul_threads([1, cpu["cores"]])
     extra = None
     if not args.no_extra:
         log("bench: other configurations")
         extra = extras(hip, eng, engine_capi, timer, torch,
                        0.0 if args.no_cpu else args.cpu_seconds)
     info = hip.device_info()
+    fl = rec["step_tflop"] * 1e12
     line = {
         "metric": metric_name(),
         "value": round(1.0 / sec, 3),
@@ -484,18 +633,27 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(sec * 1e3, 4),
+        "ms_per_step": round(sec * 1e3, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "cfg2: small CNN training step (conv 1->8, ReLU, maxpool2, "
-                               "conv 8->16, ReLU, maxpool2, linear 784->10, softmax-CE, Adam "
-                               "lr 1e-3), fp32, resident batch", "global_batch": 64,
-                   "input": "1x28x28", "parallelism": "single GPU"},
+        "config": {"workload": "cfg5: scaled Transformer LM training step (12 pre-LN blocks, "
+                               "d_model 1024, 16 heads, FFN 4096, seq 512, byte vocab 256, "
+                               "causal; forward + backward + Adam lr 1e-3), fp32, resident "
+                               "batch of random token ids, seeded reference-style init",
+                   "global_batch": 16, "seq_len": 512, "parallelism": "single GPU"},
+        "median_ms_per_step": round(rec["median_s"] * 1e3, 3),
+        "step_tflop": round(rec["step_tflop"], 4),
+        "achieved_tflops": round(fl / sec / 1e12, 2),
+        "frac_of_mfma_peak": round(fl / sec / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "params": rec["params"],
+        "loss_first_step": round(rec["loss_first_step"], 5),
+        "loss_last": round(rec["loss_last"], 5),
         "roofline": roof,
         "cpu_baseline": cpu,
+        "gpu_over_cpu": None if cpu is None else round((1.0 / sec) / cpu["value"], 1),
         "device": {"name": info.name.decode(), "arch": info.arch.decode(),
                    "compute_units": info.compute_units},
         "extra": extra,

@@ -1,0 +1,122 @@
+#!/usr/bin/env python3
+"""Writes tests/golden/cfg5_reference.npz: the compiled reference engine (oracle/_ref, built by
+oracle/Makefile from the reference's own sources) training the cfg 5 Transformer.
+
+Workload: the character model of the reference's
+examples/charlm_demo.cpp:57-87 at 12 pre-LN blocks, d_model 1024, 16 heads, FFN 4096,
+context 512, byte vocabulary 256, batch 16, causal mask; parameters from
+workloads.lm_init_params(seed 11) (the reference initialisers' distributions), tokens and
+targets from workloads.lm_inputs(seed 3); STEPS Adam steps at lr 1e-3 on that one batch.
+
+Stored (all arrays, no pickled objects):
+  losses        float32 [STEPS]  the loss of every step (before its update)
+  names         str [T]          every parameter tensor, in parameter order
+  grad_norms    float64 [T]      L2 norm of each tensor's step-1 gradient
+  param_norms   float64 [T]      L2 norm of each tensor after the last step
+  s_<name>_idx  int64            sampled flat indices of a selected tensor (all of it when
+                                 it has at most SAMPLE elements)
+  s_<name>_g    float32          its step-1 gradient at those indices
+  s_<name>_p    float32          its value after the last step at those indices
+  meta          str              JSON: workload, seeds, threads, CPU, wall time
+
+A cfg 5 step of the reference takes minutes on a few host cores, far too long for a GPU test,
+so the GPU test (tests/test_cfg5_parity.py) compares the engine with these vectors; the
+inputs and parameters are regenerated from the seeds on both sides.
+
+Usage: python tests/golden/make_cfg5_golden.py [--steps N] [--threads T]
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+import zlib
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(ROOT, "cpp-ai-engine_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+import workloads as W  # noqa: E402
+
+PARAM_SEED, INPUT_SEED, LR = 11, 3, 1e-3
+SAMPLE = 4096
+SELECTED = ["embedding.weight", "block0.attn.query.weight", "block0.attn.query.bias",
+            "block0.ff1.weight", "block0.ff1.bias", "block5.attn.out.weight",
+            "block5.norm1.beta", "block11.norm2.gamma", "block11.ff2.weight", "head.weight",
+            "head.bias"]
+
+
+def sample_indices(name, size):
+    """All of a small tensor; else SAMPLE distinct indices drawn from a seed fixed by the
+    tensor's name (crc32), sorted."""
+    if size <= SAMPLE:
+        return np.arange(size, dtype=np.int64)
+    r = np.random.default_rng(zlib.crc32(name.encode()))
+    return np.sort(r.choice(size, SAMPLE, replace=False)).astype(np.int64)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--threads", type=int, default=os.cpu_count() or 1)
+    ap.add_argument("--out", default=os.path.join(HERE, "cfg5_reference.npz"))
+    args = ap.parse_args()
+    from _oracle import Ref
+
+    b, s, vocab, d, heads, ff, layers = W.TRANSFORMER_CFG5
+    params = W.lm_init_params(PARAM_SEED, vocab, d, ff, layers)
+    ids, targets = W.lm_inputs(INPUT_SEED, b, s, vocab)
+    ref = Ref()
+    ref.set_threads(args.threads)
+    assert ref.charlm_num_params(vocab, s, d, heads, ff, layers) == params.size
+    t0 = time.time()
+    losses, final, g0 = ref.charlm_train(ids, targets, vocab, d, heads, ff, layers, params,
+                                         args.steps, LR, grads0=True)
+    wall = time.time() - t0
+    print(f"reference cfg5: {args.steps} steps in {wall:.1f} s, losses {losses}", flush=True)
+
+    layout = W.lm_param_layout(vocab, d, ff, layers)
+    names, gn, pn = [], [], []
+    out = {}
+    off = 0
+    for name, shape, _ in layout:
+        n = int(np.prod(shape))
+        g, p = g0[off:off + n], final[off:off + n]
+        names.append(name)
+        gn.append(np.linalg.norm(g.astype(np.float64)))
+        pn.append(np.linalg.norm(p.astype(np.float64)))
+        if name in SELECTED:
+            idx = sample_indices(name, n)
+            out[f"s_{name}_idx"] = idx
+            out[f"s_{name}_g"] = g[idx]
+            out[f"s_{name}_p"] = p[idx]
+        off += n
+    assert off == params.size
+    meta = {"workload": "cfg5 Transformer: 12 pre-LN blocks, d_model 1024, 16 heads, FFN 4096, "
+                        "context 512, vocab 256, batch 16, causal; Adam lr 1e-3",
+            "dims": W.TRANSFORMER_CFG5, "param_seed": PARAM_SEED, "input_seed": INPUT_SEED,
+            "lr": LR, "steps": args.steps, "threads": args.threads, "cpu": cpu_model(),
+            "wall_s": round(wall, 1), "generator": "tests/golden/make_cfg5_golden.py",
+            "reference": "oracle/_ref/libref_engine.so (reference src/*.cpp, g++ -O3, no -march)"}
+    np.savez_compressed(args.out, losses=losses, names=np.array(names), grad_norms=np.array(gn),
+                        param_norms=np.array(pn), meta=np.array(json.dumps(meta)), **out)
+    print(f"wrote {args.out}", flush=True)
+
+
+if __name__ == "__main__":
+    main()
