@@ -27,6 +27,8 @@
 // shape. It is not bit-equal to the reference's serial i-k-j loop
 // (src/tensor_ops.cpp:539-562); the parity tests bound the difference.
 
+#include <mutex>
+
 #include "gemm_kernel.hpp"
 
 namespace ehip {
@@ -34,8 +36,17 @@ namespace {
 
 using namespace gemm_detail;
 
+// Where split-K partials go: the library's grow-only scratch (base == nullptr),
+// or a caller-fixed block of cap_bytes that must hold them (the no-allocation
+// entry point).
+struct Workspace {
+    float* base = nullptr;
+    size_t cap_bytes = 0;
+};
+
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
-int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
+int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s,
+               const Workspace& wsp) {
     using C = Cfg<BM, BN, BK, WM, WN>;
     GemmArgs g = g0;
     g.tiles_m = int(ceil_div(g.m, BM));
@@ -61,8 +72,19 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s) {
     float* out = g.c;
     g.ws_stride = batch * g.m * g.n + (g.colsum ? g.n : 0);
     if (splits > 1) {
-        float* ws = static_cast<float*>(scratch(size_t(splits) * size_t(g.ws_stride) * sizeof(float)));
-        if (ws == nullptr) return EHIP_ENOMEM;
+        const size_t bytes = size_t(splits) * size_t(g.ws_stride) * sizeof(float);
+        float* ws = nullptr;
+        if (wsp.base != nullptr) {
+            if (bytes > wsp.cap_bytes)
+                return fail(EHIP_EINVAL,
+                            "gemm (no allocation): %d K-splits of %lld x %lld need %zu bytes of "
+                            "workspace, more than the fixed %zu",
+                            splits, (long long)g.m, (long long)g.n, bytes, wsp.cap_bytes);
+            ws = wsp.base;
+        } else {
+            ws = static_cast<float*>(scratch(bytes));
+            if (ws == nullptr) return EHIP_ENOMEM;
+        }
         g.c = ws;
     }
     const dim3 grid{unsigned(tiles), unsigned(splits), unsigned(batch)};
@@ -108,7 +130,7 @@ double padding(int64_t m, int64_t n, int bm, int bn) {
 }
 
 template <bool TA, bool TB>
-int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s) {
+int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s, const Workspace& wsp) {
     // The unchecked kernels need whole tiles and 16-byte aligned float4 rows;
     // the checked ones still load whole float4s away from the edges when the
     // rows are aligned.
@@ -124,12 +146,12 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s) {
     const int64_t ts = ceil_div(g.m, 128) * ceil_div(g.n, 64) * batch;
     const bool long_k = g.k >= 2048;
     if (tl >= 256 && padding(g.m, g.n, 256, 256) < 0.15 && g.k >= 256)
-        return launch_cfg<256, 256, 16, 128, 64, TA, TB>(g, batch, !whole(256, 256, 16), s);
+        return launch_cfg<256, 256, 16, 128, 64, TA, TB>(g, batch, !whole(256, 256, 16), s, wsp);
     if ((tm >= 128 || (tm >= 32 && long_k)) && padding(g.m, g.n, 128, 128) < 0.25)
-        return launch_cfg<128, 128, 32, 64, 32, TA, TB>(g, batch, !whole(128, 128, 32), s);
+        return launch_cfg<128, 128, 32, 64, 32, TA, TB>(g, batch, !whole(128, 128, 32), s, wsp);
     if ((ts >= 128 || (ts >= 32 && long_k)) && padding(g.m, g.n, 128, 64) < 0.25)
-        return launch_cfg<128, 64, 32, 32, 32, TA, TB>(g, batch, !whole(128, 64, 32), s);
-    return launch_cfg<64, 64, 16, 32, 32, TA, TB>(g, batch, !whole(64, 64, 16), s);
+        return launch_cfg<128, 64, 32, 32, 32, TA, TB>(g, batch, !whole(128, 64, 32), s, wsp);
+    return launch_cfg<64, 64, 16, 32, 32, TA, TB>(g, batch, !whole(64, 64, 16), s, wsp);
 }
 
 // ------------------------------------------------------------ small products
@@ -309,7 +331,7 @@ int small_kind(int64_t batch, int64_t m, int64_t n, int64_t k) {
 }
 
 // Validation shared by both entry points, then the kernel choice.
-int gemm_run(const ehip_gemm_ex_t& d, hipStream_t s) {
+int gemm_run(const ehip_gemm_ex_t& d, hipStream_t s, const Workspace& wsp = Workspace{}) {
     GemmArgs g{};
     g.a = d.a;
     g.b = d.b;
@@ -357,10 +379,10 @@ int gemm_run(const ehip_gemm_ex_t& d, hipStream_t s) {
         if (ta && !tb) return gemm_small<true, false>(g, batch, wave, s);
         return gemm_small<true, true>(g, batch, wave, s);
     }
-    if (!ta && !tb) return gemm_modes<false, false>(g, batch, s);
-    if (!ta && tb) return gemm_modes<false, true>(g, batch, s);
-    if (ta && !tb) return gemm_modes<true, false>(g, batch, s);
-    return gemm_modes<true, true>(g, batch, s);
+    if (!ta && !tb) return gemm_modes<false, false>(g, batch, s, wsp);
+    if (!ta && tb) return gemm_modes<false, true>(g, batch, s, wsp);
+    if (ta && !tb) return gemm_modes<true, false>(g, batch, s, wsp);
+    return gemm_modes<true, true>(g, batch, s, wsp);
 }
 
 int check_desc(const ehip_gemm_ex_t& d) {
@@ -389,13 +411,52 @@ int check_desc(const ehip_gemm_ex_t& d) {
 
 using namespace ehip;
 
-extern "C" {
+namespace ehip_noalloc {
 
-int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n, int64_t k,
-                  const float* a, int64_t lda, int64_t stride_a, const float* b, int64_t ldb,
-                  int64_t stride_b, float beta, float* c, int64_t ldc, int64_t stride_c,
-                  void* stream) {
-    EHIP_READY();
+// The split-K workspace of ehip_gemm_f32_noalloc: a file-scope device array,
+// so the entry point never allocates. Each GPU the library runs on holds its
+// own copy until the process ends; its address on a device comes from
+// hipGetSymbolAddress (the array's name in host code is only a stand-in).
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_mu;
+void* g_ptr[kMaxDevices] = {};  // the array's device address, per device
+
+// The current device's copy of `scratch`, looked up once per device with that
+// device current.
+int workspace(ehip::Workspace* out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return ehip::fail(EHIP_ENODEV, "gemm (no allocation): hipGetDevice: %s",
+                          hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return ehip::fail(EHIP_ENODEV, "gemm (no allocation): device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (g_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return ehip::fail(EHIP_ENODEV, "gemm (no allocation): hipGetSymbolAddress: %s",
+                              hipGetErrorString(e));
+        g_ptr[dev] = p;
+    }
+    out->base = static_cast<float*>(g_ptr[dev]);
+    out->cap_bytes = kScratchBytes;
+    return EHIP_OK;
+}
+
+}  // namespace ehip_noalloc
+
+namespace ehip {
+namespace {
+
+int gemm_plain(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n, int64_t k,
+               const float* a, int64_t lda, int64_t stride_a, const float* b, int64_t ldb,
+               int64_t stride_b, float beta, float* c, int64_t ldc, int64_t stride_c,
+               void* stream, const Workspace& wsp) {
     ehip_gemm_ex_t d{};
     d.trans_a = trans_a;
     d.trans_b = trans_b;
@@ -431,7 +492,32 @@ int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
         }
         return EHIP_OK;
     }
-    return gemm_run(d, as_stream(stream));
+    return gemm_run(d, as_stream(stream), wsp);
+}
+
+}  // namespace
+}  // namespace ehip
+
+extern "C" {
+
+int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n, int64_t k,
+                  const float* a, int64_t lda, int64_t stride_a, const float* b, int64_t ldb,
+                  int64_t stride_b, float beta, float* c, int64_t ldc, int64_t stride_c,
+                  void* stream) {
+    EHIP_READY();
+    return gemm_plain(trans_a, trans_b, batch, m, n, k, a, lda, stride_a, b, ldb, stride_b, beta,
+                      c, ldc, stride_c, stream, Workspace{});
+}
+
+int ehip_gemm_f32_noalloc(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
+                          int64_t k, const float* a, int64_t lda, int64_t stride_a,
+                          const float* b, int64_t ldb, int64_t stride_b, float beta, float* c,
+                          int64_t ldc, int64_t stride_c, void* stream) {
+    EHIP_READY();
+    Workspace wsp;
+    if (int rc = ehip_noalloc::workspace(&wsp)) return rc;
+    return gemm_plain(trans_a, trans_b, batch, m, n, k, a, lda, stride_a, b, ldb, stride_b, beta,
+                      c, ldc, stride_c, stream, wsp);
 }
 
 int ehip_linear_backward_f32(const float* x, const float* w, const float* dy, float* dx,

@@ -161,6 +161,21 @@ int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
                   int64_t stride_b, float beta, float* c, int64_t ldc, int64_t stride_c,
                   void* stream);
 
+/* ehip_gemm_f32 without any device allocation: the same arguments, the same
+ * kernels and tile plan (so the same bits), with the split-K partials kept in
+ * a fixed 32 MiB device array that the library holds on each GPU it runs on
+ * until the process ends, instead of the library's grow-only scratch. No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). A product whose split-K plan needs more than 32 MiB of
+ * partials is refused with EHIP_EINVAL before anything is launched. Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller. */
+int ehip_gemm_f32_noalloc(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
+                          int64_t k, const float* a, int64_t lda, int64_t stride_a,
+                          const float* b, int64_t ldb, int64_t stride_b, float beta, float* c,
+                          int64_t ldc, int64_t stride_c, void* stream);
+
 /* ehip_gemm_f32 with two-level batch strides and an epilogue, for products
  * that read and write attention heads in place. Product z in [0, batch) uses
  *   A at a + (z / inner) * stride_a + (z % inner) * stride_a_inner
