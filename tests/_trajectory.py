@@ -21,8 +21,10 @@ import numpy as np
 from _hip import k_tol, ref_close
 
 GRAD_REL = 1e-3      # per tensor: |g - g_ref| / |g_ref| (L2); measured <= 1e-4
+GRAD_ELEM = 1e-2     # per element: |g - g_ref| <= GRAD_ELEM * rms(g_ref) of its tensor
 UPDATE_REL = 1e-2    # per tensor: |u - u_ref| / |u_ref| (L2) over well-conditioned elements
-ELEMENT_UPD = 1e-2   # per element, well-conditioned: |u - u_ref| <= ELEMENT_UPD * lr * steps
+ELEMENT_UPD = 1e-2   # well-conditioned element: |u - u_ref| <= ELEMENT_UPD * lr * steps ...
+OUTLIERS = 1e-3      # ... for all but this fraction of a tensor's (at least one element)
 WELL = 1e-3          # well-conditioned element: |g_ref| >= WELL * rms(g_ref) of its tensor
 ZERO_FLOOR = 1e-5    # vanishing gradient: max |g| <= ZERO_FLOOR * max |g| of the key weight
 
@@ -54,11 +56,13 @@ def split(flat, layout):
 
 def check_gradients(got, want, layout, reduce_len, what):
     """Step-1 gradients, every tensor: the reference's metric |d| / max(1, |want|) at the
-    K-term bound k_tol(reduce_len), and |d| / |want| <= GRAD_REL in the L2 norm (gradients are
-    mostly far below 1, where the first metric is an absolute one); vanishing gradients at
-    the noise floor on both sides."""
+    K-term bound k_tol(reduce_len), and, because gradients are mostly far below 1 where that
+    metric is an absolute one, |d| / |want| <= GRAD_REL in the L2 norm and every element
+    within GRAD_ELEM of the tensor's rms gradient (both engines start from the same
+    parameters here, so no element may stray); vanishing gradients at the noise floor on
+    both sides."""
     g, w = split(got, layout), split(want, layout)
-    worst = 0.0
+    worst = worst_elem = 0.0
     for name, _ in layout:
         if vanishing(name):
             key_w = name.replace("bias", "weight")
@@ -71,7 +75,12 @@ def check_gradients(got, want, layout, reduce_len, what):
         ratio = np.linalg.norm(g[name] - w[name]) / nw if nw > 0 else np.linalg.norm(g[name])
         worst = max(worst, ratio)
         assert ratio <= GRAD_REL, f"{what} gradient {name}: |d| / |g| = {ratio:.3e}"
-    print(f"{what}: step-1 gradients, worst |d| / |g| per tensor {worst:.2e}")
+        rms = np.sqrt(np.mean(w[name] ** 2))
+        elem = np.abs(g[name] - w[name]).max() / rms if rms > 0 else np.abs(g[name]).max()
+        worst_elem = max(worst_elem, elem)
+        assert elem <= GRAD_ELEM, f"{what} gradient {name}: an element is {elem:.3e} rms off"
+    print(f"{what}: step-1 gradients, worst |d| / |g| per tensor {worst:.2e}, worst element "
+          f"{worst_elem:.2e} rms")
     return worst
 
 
@@ -79,10 +88,14 @@ def check_updates(p0, got, want, grads0, layout, lr, steps, what):
     """Final parameters after `steps` Adam steps from p0, as updates u = p - p0 against the
     reference's. Per tensor (vanishing-gradient tensors excepted), over its well-conditioned
     elements (|g0| >= WELL rms(g0), where rounding noise is under 0.1 % of the gradient):
-    |u - u_ref| / |u_ref| <= UPDATE_REL in the L2 norm and every element within
-    ELEMENT_UPD lr steps. Every element of every tensor within 2 lr steps (Adam's reach)."""
+    |u - u_ref| / |u_ref| <= UPDATE_REL in the L2 norm, and all but a fraction OUTLIERS of
+    them within ELEMENT_UPD lr steps. A few elements may legitimately go further: a ReLU
+    whose pre-activation lies within rounding of zero can take the other branch in one
+    engine once the parameters differ by rounding, which changes that position's
+    contribution to later gradients. Every element of every tensor within 2 lr steps
+    (Adam's reach)."""
     P0, G, W, G0 = split(p0, layout), split(got, layout), split(want, layout), split(grads0, layout)
-    worst_norm, worst_elem, cond = 0.0, 0.0, 0
+    worst_norm, worst_elem, cond, outliers = 0.0, 0.0, 0, 0
     total = 0
     for name, _ in layout:
         d = np.abs(G[name] - W[name])
@@ -98,11 +111,14 @@ def check_updates(p0, got, want, grads0, layout, lr, steps, what):
             continue
         u, uw = G[name][well] - P0[name][well], W[name][well] - P0[name][well]
         ratio = np.linalg.norm(u - uw) / max(np.linalg.norm(uw), 1e-30)
-        elem = np.abs(u - uw).max() / (lr * steps)
-        worst_norm, worst_elem = max(worst_norm, ratio), max(worst_elem, elem)
+        off = np.abs(u - uw) / (lr * steps)
+        far = int(np.sum(off > ELEMENT_UPD))
+        worst_norm, worst_elem = max(worst_norm, ratio), max(worst_elem, off.max())
+        outliers += far
         assert ratio <= UPDATE_REL, f"{what} {name}: |u - u_ref| / |u_ref| = {ratio:.3e}"
-        assert elem <= ELEMENT_UPD, f"{what} {name}: an update is {elem:.3e} lr steps off"
+        assert far <= max(1, int(OUTLIERS * off.size)), \
+            f"{what} {name}: {far} of {off.size} updates beyond {ELEMENT_UPD} lr steps"
     print(f"{what}: updates after {steps} steps, worst |du| / |u| per tensor {worst_norm:.2e}, "
-          f"worst element {worst_elem:.2e} lr steps ({cond} of {total} elements "
-          f"well-conditioned)")
+          f"{outliers} of {cond} well-conditioned elements beyond {ELEMENT_UPD} lr steps "
+          f"(worst {worst_elem:.2e}; {total} elements in all)")
     return worst_norm, worst_elem
