@@ -459,7 +459,10 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
         out["cnn_cfg2"]["gpu_over_cpu"] = round(out["cnn_cfg2"]["steps_per_s"] / cpu["value"], 1)
     log("bench: cfg3 char-Transformer training step")
     out["charlm_cfg3"] = charlm_leg(engine_mod, eng, timer, cpu_seconds)
-    # cfg 1: C = A B and both backward products at 512^3 (805.3 MFLOP per trio), and 4096^3.
+    # cfg 1: C = A B and its backward (dA = dC B^T, dB = A^T dC) at 512^3 (805.3 MFLOP per
+    # trio), and 4096^3. The backward is one ehip_matmul_backward_f32 call (both products in
+    # one launch where they take the K-sliced tiles, as the engine's matmul backward runs
+    # them); the two products launched one by one are recorded beside it.
     for n in (512, 4096):
         r = torch.Generator(device="cuda").manual_seed(n)
         a = torch.randn(n, n, device="cuda", generator=r)
@@ -467,18 +470,21 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
         dc = torch.randn(n, n, device="cuda", generator=r)
         c, da, db = (torch.empty(n, n, device="cuda") for _ in range(3))
         fl = 2.0 * n ** 3
+        reps, warm = (20, 3) if n == 4096 else (200, 20)
         modes = {
-            "fwd C=AB": lambda r: eng.repeat_gemm(r, a, b, c),
-            "bwd dA=dC B^T": lambda r: eng.repeat_gemm(r, dc, b, da, trans_b=True),
-            "bwd dB=A^T dC": lambda r: eng.repeat_gemm(r, a, dc, db, trans_a=True),
+            "fwd C=AB": (fl, lambda q: eng.repeat_gemm(q, a, b, c)),
+            "bwd dA and dB (one call)": (2 * fl, lambda q: eng.repeat_matmul_backward(
+                q, a, b, dc, da, db)),
+            "bwd dA=dC B^T alone": (fl, lambda q: eng.repeat_gemm(q, dc, b, da, trans_b=True)),
+            "bwd dB=A^T dC alone": (fl, lambda q: eng.repeat_gemm(q, a, dc, db, trans_a=True)),
         }
-        sec = {k: timer.time_batch(f, 20 if n == 4096 else 500, 3 if n == 4096 else 50)
-               for k, f in modes.items()}
-        total = sum(sec.values())
+        sec = {k: timer.median_batch(f, reps, warm) for k, (_, f) in modes.items()}
+        total = sec["fwd C=AB"] + sec["bwd dA and dB (one call)"]
         out[f"gemm_{n}^3"] = {
             "fwd+bwd_tflops": round(3 * fl / total / 1e12, 2),
             "fwd+bwd_frac_of_mfma_peak": round(3 * fl / total / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
-            "per_mode": {k: roofline(k, "mfma", fl, v) for k, v in sec.items()}}
+            "fwd+bwd_us": round(total * 1e6, 3),
+            "per_mode": {k: roofline(k, "mfma", modes[k][0], v) for k, v in sec.items()}}
         del a, b, dc, c, da, db
     # cfg 4: bandwidth-bound kernels at their configured sizes.
     bw = {}

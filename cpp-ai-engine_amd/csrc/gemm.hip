@@ -118,15 +118,92 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s,
     return EHIP_OK;
 }
 
+double padding(int64_t m, int64_t n, int bm, int bn) {
+    return double(ceil_div(m, bm) * bm) * double(ceil_div(n, bn) * bn) / (double(m) * double(n)) - 1.0;
+}
+
+// 32 x 32 tiles with K sliced over the workgroup's waves (gemm_kslice): one
+// launch, no workspace. W, the waves per workgroup, doubles while the grid
+// stays within 2048 waves (8 per CU) and each wave keeps at least 32 k.
+template <int W, bool TA, bool TB>
+int launch_kslice_w(const GemmArgs& g, int64_t batch, bool whole, hipStream_t s) {
+    const dim3 grid{unsigned(int64_t(g.tiles_m) * g.tiles_n), 1u, unsigned(batch)};
+    const bool epi = !plain_epilogue(g);
+    if (whole && !epi)
+        EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, false, false>), grid, dim3(64 * W), 0, s, g);
+    else if (whole)
+        EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, false, true>), grid, dim3(64 * W), 0, s, g);
+    else if (!epi)
+        EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, true, false>), grid, dim3(64 * W), 0, s, g);
+    else
+        EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, true, true>), grid, dim3(64 * W), 0, s, g);
+    return EHIP_OK;
+}
+
+// The waves per workgroup of the K-sliced tiles: W doubles while the grid
+// stays within 2048 waves (8 per CU) and each wave keeps at least 64 k. More
+// waves also shorten each wave's serial accumulation chain: with at most 4
+// per CU (about 5 % faster on 512^3) the char-Transformer's 10-step loss
+// trajectory drifts past 1e-5 of the reference's at step 9; with 8 it stays
+// within 4e-6.
+int kslice_waves(int64_t tiles, int64_t k) {
+    int w = 1;
+    while (w < 8 && tiles * 2 * w <= 2048 && k >= 64 * w) w *= 2;
+    return w;
+}
+
+void kslice_geometry(GemmArgs& g, int w) {
+    g.tiles_m = int(ceil_div(g.m, 32));
+    g.tiles_n = int(ceil_div(g.n, 32));
+    g.k_chunk = ceil_div(ceil_div(g.k, w), 32) * 32;
+    g.splits = 1;
+}
+
+bool kslice_whole(const GemmArgs& g) {
+    return g.vec && g.m % 32 == 0 && g.n % 32 == 0 && g.k % 32 == 0;
+}
+
+template <bool TA, bool TB>
+int launch_kslice(GemmArgs g, int64_t batch, hipStream_t s) {
+    const int w = kslice_waves(ceil_div(g.m, 32) * ceil_div(g.n, 32) * batch, g.k);
+    kslice_geometry(g, w);
+    const bool whole = kslice_whole(g);
+    switch (w) {
+        case 1: return launch_kslice_w<1, TA, TB>(g, batch, whole, s);
+        case 2: return launch_kslice_w<2, TA, TB>(g, batch, whole, s);
+        case 4: return launch_kslice_w<4, TA, TB>(g, batch, whole, s);
+        default: return launch_kslice_w<8, TA, TB>(g, batch, whole, s);
+    }
+}
+
 // Tile choice, largest first (measured on MI355X, fp32 MFMA):
 //   L  256 x 256 x 16, 8 waves of 128 x 64   ~135 TFLOP/s at 4096^3
 //   M  128 x 128 x 32, 8 waves of  64 x 32   ~120-130 on 8192 x 1024 x K
 //   S  128 x  64 x 32, 8 waves of  32 x 32   thin outputs (N = 64 attention products)
-//   T   64 x  64 x 16, 4 waves of  32 x 32   small problems
+//   K  32 x 32 per workgroup, K sliced over its waves: outputs too small for
+//      the larger tiles to fill the chip (512^3, the char-Transformer's layers)
+//   T   64 x  64 x 16, 4 waves of  32 x 32   the rest (few tiles; B column sums)
 // A tile size is taken when its grid fills the 256 CUs (with split-K where K
 // is long) and the padding it adds to the output stays small.
-double padding(int64_t m, int64_t n, int bm, int bn) {
-    return double(ceil_div(m, bm) * bm) * double(ceil_div(n, bn) * bn) / (double(m) * double(n)) - 1.0;
+enum class Tile { L, M, S, K, T };
+
+bool operands_aligned(const GemmArgs& g) {
+    return aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+           g.stride_a % 4 == 0 && g.stride_b % 4 == 0 &&
+           (g.inner == 1 || (g.stride_a2 % 4 == 0 && g.stride_b2 % 4 == 0));
+}
+
+Tile plan_tile(const GemmArgs& g, int64_t batch) {
+    const int64_t tl = ceil_div(g.m, 256) * ceil_div(g.n, 256) * batch;
+    const int64_t tm = ceil_div(g.m, 128) * ceil_div(g.n, 128) * batch;
+    const int64_t ts = ceil_div(g.m, 128) * ceil_div(g.n, 64) * batch;
+    const bool long_k = g.k >= 2048;
+    if (tl >= 256 && padding(g.m, g.n, 256, 256) < 0.15 && g.k >= 256) return Tile::L;
+    if ((tm >= 128 || (tm >= 32 && long_k)) && padding(g.m, g.n, 128, 128) < 0.25) return Tile::M;
+    if ((ts >= 128 || (ts >= 32 && long_k)) && padding(g.m, g.n, 128, 64) < 0.25) return Tile::S;
+    // A B column sum is computed only by the staged tiles.
+    if (g.colsum == nullptr && ceil_div(g.m, 32) * ceil_div(g.n, 32) * batch >= 64) return Tile::K;
+    return Tile::T;
 }
 
 template <bool TA, bool TB>
@@ -134,24 +211,70 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s, const Workspace& wsp) {
     // The unchecked kernels need whole tiles and 16-byte aligned float4 rows;
     // the checked ones still load whole float4s away from the edges when the
     // rows are aligned.
-    const bool aligned = aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
-                         g.stride_a % 4 == 0 && g.stride_b % 4 == 0 &&
-                         (g.inner == 1 || (g.stride_a2 % 4 == 0 && g.stride_b2 % 4 == 0));
-    g.vec = aligned ? 1 : 0;
+    g.vec = operands_aligned(g) ? 1 : 0;
     const auto whole = [&](int bm, int bn, int bk) {
-        return aligned && g.m % bm == 0 && g.n % bn == 0 && g.k % bk == 0;
+        return g.vec && g.m % bm == 0 && g.n % bn == 0 && g.k % bk == 0;
     };
-    const int64_t tl = ceil_div(g.m, 256) * ceil_div(g.n, 256) * batch;
-    const int64_t tm = ceil_div(g.m, 128) * ceil_div(g.n, 128) * batch;
-    const int64_t ts = ceil_div(g.m, 128) * ceil_div(g.n, 64) * batch;
-    const bool long_k = g.k >= 2048;
-    if (tl >= 256 && padding(g.m, g.n, 256, 256) < 0.15 && g.k >= 256)
-        return launch_cfg<256, 256, 16, 128, 64, TA, TB>(g, batch, !whole(256, 256, 16), s, wsp);
-    if ((tm >= 128 || (tm >= 32 && long_k)) && padding(g.m, g.n, 128, 128) < 0.25)
-        return launch_cfg<128, 128, 32, 64, 32, TA, TB>(g, batch, !whole(128, 128, 32), s, wsp);
-    if ((ts >= 128 || (ts >= 32 && long_k)) && padding(g.m, g.n, 128, 64) < 0.25)
-        return launch_cfg<128, 64, 32, 32, 32, TA, TB>(g, batch, !whole(128, 64, 32), s, wsp);
-    return launch_cfg<64, 64, 16, 32, 32, TA, TB>(g, batch, !whole(64, 64, 16), s, wsp);
+    switch (plan_tile(g, batch)) {
+        case Tile::L:
+            return launch_cfg<256, 256, 16, 128, 64, TA, TB>(g, batch, !whole(256, 256, 16), s,
+                                                             wsp);
+        case Tile::M:
+            return launch_cfg<128, 128, 32, 64, 32, TA, TB>(g, batch, !whole(128, 128, 32), s, wsp);
+        case Tile::S:
+            return launch_cfg<128, 64, 32, 32, 32, TA, TB>(g, batch, !whole(128, 64, 32), s, wsp);
+        case Tile::K:
+            return launch_kslice<TA, TB>(g, batch, s);
+        default:
+            return launch_cfg<64, 64, 16, 32, 32, TA, TB>(g, batch, !whole(64, 64, 16), s, wsp);
+    }
+}
+
+// The backward's two products in one launch when both take the K-sliced tiles
+// (g0: dA = dC B^T, g1: dB = A^T dC; plain batch-1 products); returns false
+// when they do not, and the caller runs them one by one.
+bool try_kslice_pair(GemmArgs g0, GemmArgs g1, hipStream_t s, int* rc) {
+    g0.vec = operands_aligned(g0) ? 1 : 0;
+    g1.vec = operands_aligned(g1) ? 1 : 0;
+    if (plan_tile(g0, 1) != Tile::K || plan_tile(g1, 1) != Tile::K) return false;
+    // Each product is sliced as its own launch would slice it (same bits).
+    const int64_t t0 = ceil_div(g0.m, 32) * ceil_div(g0.n, 32);
+    const int64_t t1 = ceil_div(g1.m, 32) * ceil_div(g1.n, 32);
+    const int w0 = kslice_waves(t0, g0.k), w1 = kslice_waves(t1, g1.k);
+    const int w = w0 > w1 ? w0 : w1;
+    kslice_geometry(g0, w0);
+    kslice_geometry(g1, w1);
+    const int64_t tiles = t0 + t1;
+    const bool check = !kslice_whole(g0) || !kslice_whole(g1);
+    const bool epi = !plain_epilogue(g0) || !plain_epilogue(g1);
+    const dim3 grid{unsigned(tiles)};
+#define EHIP_PAIR(W)                                                                               \
+    do {                                                                                           \
+        if (check && epi)                                                                          \
+            EHIP_LAUNCH("gemm_pair", (gemm_kslice_pair<W, true, true>), grid, dim3(64 * W), 0, s,   \
+                        g0, g1, w0, w1);                                                           \
+        else if (check)                                                                            \
+            EHIP_LAUNCH("gemm_pair", (gemm_kslice_pair<W, true, false>), grid, dim3(64 * W), 0, s,  \
+                        g0, g1, w0, w1);                                                           \
+        else if (epi)                                                                              \
+            EHIP_LAUNCH("gemm_pair", (gemm_kslice_pair<W, false, true>), grid, dim3(64 * W), 0, s,  \
+                        g0, g1, w0, w1);                                                           \
+        else                                                                                       \
+            EHIP_LAUNCH("gemm_pair", (gemm_kslice_pair<W, false, false>), grid, dim3(64 * W), 0,    \
+                        s, g0, g1, w0, w1);                                                        \
+        return EHIP_OK;                                                                            \
+    } while (0)
+    const auto launch = [&]() -> int {
+        switch (w) {
+            case 1: EHIP_PAIR(1);
+            case 2: EHIP_PAIR(2);
+            case 4: EHIP_PAIR(4);
+            default: EHIP_PAIR(8);
+        }
+    };
+#undef EHIP_PAIR
+    *rc = launch();
+    return true;
 }
 
 // ------------------------------------------------------------ small products
@@ -520,6 +643,54 @@ int ehip_gemm_f32_noalloc(int trans_a, int trans_b, int64_t batch, int64_t m, in
                       c, ldc, stride_c, stream, wsp);
 }
 
+int ehip_matmul_backward_f32(int64_t m, int64_t k, int64_t n, const float* a, int64_t lda,
+                             const float* b, int64_t ldb, const float* dc, int64_t lddc, float* da,
+                             int64_t ldda, float beta_a, float* db, int64_t lddb, float beta_b,
+                             void* stream) {
+    EHIP_READY();
+    if (m < 0 || k < 0 || n < 0) return fail(EHIP_EINVAL, "matmul_backward: negative extent");
+    if ((da && (!dc || !b)) || (db && (!dc || !a)))
+        return fail(EHIP_EINVAL, "matmul_backward: null operand");
+    if (da && db && m > 0 && k > 0 && n > 0 && lddc >= n && ldb >= n && lda >= k && ldda >= k &&
+        lddb >= n) {
+        // dA = dC B^T (m x k, K = n) and dB = A^T dC (k x n, K = m).
+        const auto args = [](const float* x, int64_t ldx, const float* y, int64_t ldy, float* out,
+                             int64_t ldo, int64_t rows, int64_t cols, int64_t kk, float beta) {
+            GemmArgs g{};
+            g.a = x;
+            g.b = y;
+            g.c = out;
+            g.m = rows;
+            g.n = cols;
+            g.k = kk;
+            g.lda = ldx;
+            g.ldb = ldy;
+            g.ldc = ldo;
+            g.inner = 1;
+            g.alpha = 1.0f;
+            g.add_period = 1;
+            g.beta = beta;
+            return g;
+        };
+        int rc = EHIP_OK;
+        if (small_kind(1, m, k, n) == 0 && small_kind(1, k, n, m) == 0 &&
+            m <= 0x7fffffff && k <= 0x7fffffff && n <= 0x7fffffff &&
+            try_kslice_pair(args(dc, lddc, b, ldb, da, ldda, m, k, n, beta_a),
+                            args(a, lda, dc, lddc, db, lddb, k, n, m, beta_b), as_stream(stream),
+                            &rc))
+            return rc;
+    }
+    if (da)
+        if (int rc = ehip_gemm_f32(0, 1, 1, m, k, n, dc, lddc, 0, b, ldb, 0, beta_a, da, ldda, 0,
+                                   stream))
+            return rc;
+    if (db)
+        if (int rc = ehip_gemm_f32(1, 0, 1, k, n, m, a, lda, 0, dc, lddc, 0, beta_b, db, lddb, 0,
+                                   stream))
+            return rc;
+    return EHIP_OK;
+}
+
 int ehip_linear_backward_f32(const float* x, const float* w, const float* dy, float* dx,
                              float* dw, float* db, int64_t rows, int64_t in, int64_t out,
                              void* stream) {
@@ -559,14 +730,11 @@ int ehip_linear_backward_f32(const float* x, const float* w, const float* dy, fl
                     int(out));
         return EHIP_OK;
     }
-    if (dx)
-        if (int rc = ehip_gemm_f32(0, 1, 1, rows, in, out, dy, out, 0, w, out, 0, 0.0f, dx, in, 0,
-                                   stream))
-            return rc;
-    if (dw)
-        if (int rc = ehip_gemm_f32(1, 0, 1, in, out, rows, x, in, 0, dy, out, 0, 0.0f, dw, out, 0,
-                                   stream))
-            return rc;
+    // dx = dy w^T and dw = x^T dy: the backward of x w, as one entry point (one
+    // launch when both take the K-sliced tiles).
+    if (int rc = ehip_matmul_backward_f32(rows, in, out, x, in, w, out, dy, out, dx, in, 0.0f, dw,
+                                          out, 0.0f, stream))
+        return rc;
     if (db) return ehip_sum_axis_f32(dy, db, 1, rows, out, stream);
     return EHIP_OK;
 }

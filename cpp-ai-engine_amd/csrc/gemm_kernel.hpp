@@ -320,6 +320,198 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
         }
 }
 
+// ------------------------------------------------------------ K-sliced tiles
+//
+// Products whose output is too small to give every CU a 64 x 64 tile (512^3
+// is 64 such tiles; the old plan split K four ways into a workspace and paid a
+// second launch to add the splits): a workgroup computes one 32 x 32 tile of
+// C, and its W waves each take one contiguous slice of K (k_chunk long, a
+// multiple of 8); the waves' accumulators are then added in wave order in LDS,
+// in the same launch. With W = 8 a 512^3 product is 256 workgroups of 8
+// waves, two per SIMD.
+//
+// The MFMA operands come straight from global memory (L2), without LDS: for
+// one block of 8 k values at kb, lane l (row or column r = l % 32, half
+// h = l / 32) holds the four values k = kb + 4h + j, j = 0..3, and instruction
+// j of the block multiplies them, so that across the two lane halves the four
+// instructions cover the 8 k values once. An operand stored with k contiguous
+// (A untransposed, B transposed) is one float4 per lane; an operand stored
+// with rows or columns contiguous (A transposed, B untransposed) is four
+// dword loads, each 32 lanes reading 128 contiguous bytes. Blocks are
+// processed four at a time (32 k), and the next four are loaded before the
+// current ones are multiplied.
+// The pointer is deliberately not __restrict__: a restrict-qualified read-only
+// pointer makes the loads invariant, and the compiler then re-issues them at
+// their uses instead of keeping the prefetched registers.
+template <bool TRANS_K_CONTIG, bool CHECK>
+__device__ __forceinline__ float4 load_kblock(const float* p, int64_t ld,
+                                              int64_t rows, int64_t kdim, int64_t r, int64_t kb,
+                                              bool vec) {
+    // TRANS_K_CONTIG: element (r, k) at p[r * ld + k]; otherwise at p[k * ld + r].
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (TRANS_K_CONTIG) {
+        const float* src = p + r * ld + kb;
+        if (!CHECK || (vec && r < rows && kb + 3 < kdim)) {
+            v = *reinterpret_cast<const float4*>(src);
+        } else if (r < rows) {
+            v.x = kb < kdim ? src[0] : 0.f;
+            v.y = kb + 1 < kdim ? src[1] : 0.f;
+            v.z = kb + 2 < kdim ? src[2] : 0.f;
+            v.w = kb + 3 < kdim ? src[3] : 0.f;
+        }
+    } else {
+        const float* src = p + kb * ld + r;
+        if (!CHECK || r < rows) {
+            v.x = (!CHECK || kb < kdim) ? src[0] : 0.f;
+            v.y = (!CHECK || kb + 1 < kdim) ? src[ld] : 0.f;
+            v.z = (!CHECK || kb + 2 < kdim) ? src[2 * ld] : 0.f;
+            v.w = (!CHECK || kb + 3 < kdim) ? src[3 * ld] : 0.f;
+        }
+    }
+    return v;
+}
+
+// One 32 x 32 tile of product `batch` of g: tile index `bid` before the XCD
+// renumbering, `red` the waves' LDS exchange. The first `wn` of the W waves
+// hold K slices (g.k_chunk long); any others hold none, contribute +0.0 and so
+// change no sum (a sum that starts at +0.0 is never -0.0).
+template <int W, bool TA, bool TB, bool CHECK, bool EPI, int KU>
+__device__ __forceinline__ void kslice_tile(const GemmArgs& g, int bid, int64_t batch,
+                                            float (*red)[16][64], int wn) {
+    constexpr int kU = KU;  // blocks of 8 k per pipeline stage
+
+    // Tile coordinates: XCD-contiguous renumbering, then groups of four tile
+    // rows, so that an XCD's 32 consecutive tiles share 4 A and 8 B panels.
+    const int tiles = g.tiles_m * g.tiles_n;
+    if (tiles % 8 == 0) bid = (bid % 8) * (tiles / 8) + bid / 8;
+    constexpr int kGroupM = 4;
+    const int group = bid / (kGroupM * g.tiles_n);
+    const int first_m = group * kGroupM;
+    const int gsz = min(g.tiles_m - first_m, kGroupM);
+    const int in_group = bid % (kGroupM * g.tiles_n);
+    const int64_t m0 = int64_t(first_m + in_group % gsz) * 32;
+    const int64_t n0 = int64_t(in_group / gsz) * 32;
+
+    const float* A = g.a + batch_offset(batch, g.inner, g.stride_a, g.stride_a2);
+    const float* B = g.b + batch_offset(batch, g.inner, g.stride_b, g.stride_b2);
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int r = lane % 32, h = lane / 32;
+    // Wave w's slice of K. Unchecked kernels need K and k_chunk to be multiples
+    // of 8 KU (whole pipeline stages); checked ones zero-fill past the slice.
+    const int64_t k_begin = wave < wn ? int64_t(wave) * g.k_chunk : g.k;
+    const int64_t k_end = k_begin + g.k_chunk < g.k ? k_begin + g.k_chunk : g.k;
+
+    floatx16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+
+    // Operand A: (m0 + r, k); stored M x K (k contiguous) unless TA.
+    // Operand B: (k, n0 + r); stored K x N (n contiguous) unless TB.
+    const auto load_stage = [&](int64_t kb, float4 (&fa)[kU], float4 (&fb)[kU]) {
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t k = kb + 8 * u + 4 * h;
+            fa[u] = load_kblock<!TA, CHECK>(A, g.lda, g.m, k_end, m0 + r, k, g.vec != 0);
+            fb[u] = load_kblock<TB, CHECK>(B, g.ldb, g.n, k_end, n0 + r, k, g.vec != 0);
+        }
+    };
+    // Two register buffers alternate: a stage's loads are issued before the
+    // previous stage's MFMAs (a scheduling barrier keeps them there). The last
+    // stage re-reads its own addresses (L1 hits) instead of branching around
+    // the prefetch: on a guarded prefetch the compiler's wait counts, merged
+    // over both paths, wait for every load before the MFMAs.
+    const auto mfma_stage = [&](const float4 (&fa)[kU], const float4 (&fb)[kU]) {
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[u].x, fb[u].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[u].y, fb[u].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[u].z, fb[u].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[u].w, fb[u].w, acc, 0, 0, 0);
+        }
+    };
+    constexpr int64_t kStage = 8 * kU;
+    float4 a0[kU], b0[kU], a1[kU], b1[kU];
+    int64_t kb = k_begin;
+    if (kb < k_end) load_stage(kb, a0, b0);
+    while (kb < k_end) {
+        load_stage(kb + kStage < k_end ? kb + kStage : kb, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_stage(a0, b0);
+        kb += kStage;
+        if (kb >= k_end) break;
+        load_stage(kb + kStage < k_end ? kb + kStage : kb, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_stage(a1, b1);
+        kb += kStage;
+    }
+
+    // The waves' sums, added in wave order; wave w then finishes registers
+    // [w * 16 / W, (w + 1) * 16 / W) of every lane.
+    constexpr int kPer = 16 / W;
+    float out[kPer];
+    if (W > 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[wave][i][lane] = acc[i];
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = wave * kPer + q;
+            float v = red[0][i][lane];
+#pragma unroll
+            for (int w = 1; w < W; ++w)
+                if (w < wn) v = v + red[w][i][lane];
+            out[q] = v;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) out[q] = acc[q];
+    }
+    float* Cp = g.c + batch_offset(batch, g.inner, g.stride_c, g.stride_c2);
+    const float* addp = g.add ? g.add + (int64_t(batch) % g.add_period) * g.stride_add : nullptr;
+    const int64_t col = n0 + r;
+    float e_add[kPer], e_old[kPer];
+    if (EPI) {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = wave * kPer + q;
+            const int64_t row = m0 + 8 * (i / 4) + 4 * h + (i % 4);
+            const bool in = !CHECK || (row < g.m && col < g.n);
+            e_add[q] = (addp && in) ? addp[row * g.ld_add + col] : 0.0f;
+            e_old[q] = (g.beta != 0.0f && in) ? Cp[row * g.ldc + col] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int i = wave * kPer + q;
+        const int64_t row = m0 + 8 * (i / 4) + 4 * h + (i % 4);
+        if (CHECK && (row >= g.m || col >= g.n)) continue;
+        Cp[row * g.ldc + col] = EPI ? finish(g, out[q], e_add[q], e_old[q]) : out[q];
+    }
+}
+
+template <int W, bool TA, bool TB, bool CHECK, bool EPI, int KU = 4>
+__global__ __launch_bounds__(64 * W) void gemm_kslice(GemmArgs g) {
+    __shared__ float red[W > 1 ? W : 1][16][64];
+    kslice_tile<W, TA, TB, CHECK, EPI, KU>(g, blockIdx.x, blockIdx.z, red, W);
+}
+
+// The two products of a matmul's backward in one launch: g0 is dA = dC B^T
+// (B read transposed), g1 is dB = A^T dC (A read transposed), one batch each
+// of 32 x 32 tiles; blocks [0, tiles0) compute g0's tiles, the rest g1's.
+// Each product keeps the K slicing (w0 or w1 waves, its k_chunk) that its own
+// launch would use, so the results are that launch's bits. (Linear's
+// dx = g W^T and dW = x^T g have the same two orientations.)
+template <int W, bool CHECK, bool EPI, int KU = 4>
+__global__ __launch_bounds__(64 * W) void gemm_kslice_pair(GemmArgs g0, GemmArgs g1, int w0,
+                                                           int w1) {
+    __shared__ float red[W > 1 ? W : 1][16][64];
+    const int tiles0 = g0.tiles_m * g0.tiles_n;
+    if (int(blockIdx.x) < tiles0)
+        kslice_tile<W, false, true, CHECK, EPI, KU>(g0, blockIdx.x, 0, red, w0);
+    else
+        kslice_tile<W, true, false, CHECK, EPI, KU>(g1, int(blockIdx.x) - tiles0, 0, red, w1);
+}
+
 // C[b] = sum over splits of W[s][b], then the epilogue; with a column sum,
 // the n values after each split's C partials are summed the same way into
 // colsum. A block is RL split lanes x (256 / RL) outputs: lane l adds splits

@@ -84,6 +84,8 @@ _SIGS = {
     "ehip_memcpy_d2d": [_vp, _vp, _sz, _vp],
     "ehip_gemm_f32": [_i, _i, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _f, _vp,
                       _i64, _i64, _vp],
+    "ehip_matmul_backward_f32": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _f,
+                                 _vp, _i64, _f, _vp],
     "ehip_gemm_f32_noalloc": [_i, _i, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                               _f, _vp, _i64, _i64, _vp],
     "ehip_gemm_ex_f32": [C.POINTER(GemmEx), _vp],

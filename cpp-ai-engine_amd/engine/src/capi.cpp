@@ -618,6 +618,18 @@ int eng_repeat_gemm(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t 
     });
 }
 
+// Enqueues `reps` back-to-back ehip_matmul_backward_f32 calls on `stream`
+// (device pointers, contiguous 2-D operands): the backward of C = A B.
+int eng_repeat_matmul_backward(int64_t m, int64_t k, int64_t n, const float* a, const float* b,
+                               const float* dc, float* da, float* db, void* stream, int reps) {
+    return guarded([&] {
+        for (int r = 0; r < reps; ++r)
+            engine::hip::check(ehip_matmul_backward_f32(m, k, n, a, k, b, n, dc, n, da, k, 0.0f, db,
+                                                        n, 0.0f, stream),
+                               "matmul backward");
+    });
+}
+
 // Enqueues `reps` back-to-back ehip_conv2d_relu_maxpool_backward_f32 calls on
 // `stream` (device pointers; the windows are the entry point's), for timing
 // the fused block's backward kernels with events around the batch.

@@ -229,6 +229,20 @@ Tensor Tensor::matmul(const Tensor& B) const {
     if (track(requires_grad() || B.requires_grad())) {
         Tensor a = *this, b = B;
         attach(C, {impl_, B.impl_}, [a, b, bt, M, N, K](const Tensor& g) mutable {
+            if (bt.dims.empty() && a.requires_grad() && b.requires_grad() && M > 0 && N > 0 &&
+                K > 0) {
+                // Plain 2-D operands: both products from one entry point (one launch
+                // when both take the K-sliced tiles; the same bits as two calls).
+                Tensor da({M, K}, 0.0f, false), db({K, N}, 0.0f, false);
+                hip::check(ehip_matmul_backward_f32(int64_t(M), int64_t(K), int64_t(N), dptr(a),
+                                                    int64_t(K), dptr(b), int64_t(N), dptr(g),
+                                                    int64_t(N), dout(da), int64_t(K), 0.0f,
+                                                    dout(db), int64_t(N), 0.0f, nullptr),
+                           "matmul backward");
+                a.add_grad(da);
+                b.add_grad(db);
+                return;
+            }
             Batch gb = bt;
             gb.a_batched = true;  // g always carries the batch
             if (a.requires_grad()) {

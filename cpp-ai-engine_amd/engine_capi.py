@@ -91,6 +91,17 @@ class Engine:
                    b.data_ptr(), b.shape[1], 0, beta, c.data_ptr(), n, 0,
                    torch.cuda.current_stream().cuda_stream, reps))
 
+    def repeat_matmul_backward(self, reps, a, b, dc, da, db):
+        """Enqueues `reps` ehip_matmul_backward_f32 calls (dA = dC B^T, dB = A^T dC) from C++
+        on torch's current stream; 2-D contiguous CUDA tensors."""
+        import torch
+        m, k = a.shape
+        n = b.shape[1]
+        f = self.lib.eng_repeat_matmul_backward
+        f.argtypes = [_i64] * 3 + [C.c_void_p] * 6 + [C.c_int]
+        self._ok(f(m, k, n, a.data_ptr(), b.data_ptr(), dc.data_ptr(), da.data_ptr(),
+                   db.data_ptr(), torch.cuda.current_stream().cuda_stream, reps))
+
     def repeat_conv_relu_pool_backward(self, reps, x, weight, g, out, argmax, dweight, dbias,
                                        conv_window, pool_window, dx=None):
         """Enqueues `reps` fused conv-block backward calls from C++ on torch's current stream

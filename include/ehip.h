@@ -161,6 +161,20 @@ int ehip_gemm_f32(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
                   int64_t stride_b, float beta, float* c, int64_t ldc, int64_t stride_c,
                   void* stream);
 
+/* The backward of C = A . B for 2-D operands (A m x k, B k x n, dC m x n):
+ * dA = dC . B^T + beta_a * dA (m x k) when da is not NULL, and
+ * dB = A^T . dC + beta_b * dB (k x n) when db is not NULL. When both products
+ * take the K-sliced 32 x 32 tiles they run as two block ranges of one launch,
+ * which halves the fixed cost of a kernel boundary (the cache write-back and
+ * invalidation, the first loads' latency) for small products; otherwise they
+ * are ehip_gemm_f32's two calls. Same bits as those calls either way.
+ * Replaces the two products of the matmul backward lambda
+ * (src/tensor_ops.cpp:565-586), without its materialised transposes. */
+int ehip_matmul_backward_f32(int64_t m, int64_t k, int64_t n, const float* a, int64_t lda,
+                             const float* b, int64_t ldb, const float* dc, int64_t lddc, float* da,
+                             int64_t ldda, float beta_a, float* db, int64_t lddb, float beta_b,
+                             void* stream);
+
 /* ehip_gemm_f32 without any device allocation: the same arguments, the same
  * kernels and tile plan (so the same bits), with the split-K partials kept in
  * a fixed 32 MiB device array that the library holds on each GPU it runs on

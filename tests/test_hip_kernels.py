@@ -52,13 +52,23 @@ def test_gemm_modes_vs_oracle(hip, orc, m, k, n, ta, tb):
     b_st = np.ascontiguousarray(b.T) if tb else b
     got = host(hip.gemm(dev(a_st), dev(b_st), trans_a=ta, trans_b=tb))
     want = orc.matmul(a, b)
-    ref_close(got, want, k_tol(k), f"gemm {m}x{k}x{n} ta={ta} tb={tb}")
-    # The device error against the exact product stays within a small multiple
-    # of the CPU's own serial-sum error (fp64 as the arbiter).
     exact64 = a.astype(np.float64) @ b.astype(np.float64)
+    # The reference's metric at the K-term bound; where the device misses it, fp64
+    # arbitrates: the device value must be at least as close to the exact product as the
+    # reference's own serial sum is (the two rounding errors can add up past the bound).
+    err = np.abs(got - want) / np.maximum(1.0, np.abs(want))
+    miss = err > k_tol(k)
+    assert np.all(np.abs(got - exact64)[miss] <= np.abs(want - exact64)[miss]), \
+        f"gemm {m}x{k}x{n} ta={ta} tb={tb}: {int(miss.sum())} elements beyond {k_tol(k):.2e} " \
+        f"and farther from the exact product than the reference"
+    # The device error against the exact product stays within a small multiple
+    # of the CPU's own serial-sum error, and within the statistical bound everywhere.
     e_gpu = np.sqrt(np.mean((got - exact64) ** 2))
     e_cpu = np.sqrt(np.mean((want - exact64) ** 2))
     assert e_gpu <= 4.0 * e_cpu + 1e-7, (e_gpu, e_cpu)
+    bound = gemm_stat_bound(np.linalg.norm(a.astype(np.float64), axis=1),
+                            np.linalg.norm(b.astype(np.float64), axis=0), k)
+    assert np.all(np.abs(got - exact64) <= bound)
 
 
 # Shapes that select each tile configuration of the dispatcher (gemm.hip): the 256 x 256
@@ -70,6 +80,10 @@ TILE_CASES = [
     ("M 128x128x32", 1, 2048, 512, 1024), ("M ragged", 1, 2050, 515, 1030),
     ("M split-K", 1, 1024, 8192, 1024), ("S 128x64 batched", 32, 512, 512, 64),
     ("S ragged batched", 16, 500, 77, 60), ("M batched K=64", 256, 512, 64, 512),
+    # 32 x 32 tiles with K sliced over the waves (gemm_kslice): 8, 2 and 1 waves per
+    # workgroup, whole and ragged tiles, a batch of attention-sized products.
+    ("K-sliced 512^3 W=8", 1, 512, 512, 512), ("K-sliced W=2", 1, 2048, 96, 96),
+    ("K-sliced ragged", 1, 1000, 300, 200), ("K-sliced batched K=24", 128, 64, 24, 64),
 ]
 
 
@@ -163,15 +177,17 @@ def test_gemm_batched_shared(hip, orc, ab, bb):
     ref_close(got, orc.matmul(a, b), k_tol(24), "batched gemm")
 
 
-def test_gemm_beta_accumulates(hip, orc):
-    """beta = 1 onto a nonzero destination (tests/test_cuda_parity.cpp:263-290)."""
-    print_case("gemm-beta")
-    r = rng(9)
-    a, b, c0 = randn(r, 70, 45), randn(r, 45, 90), randn(r, 70, 90)
+@pytest.mark.parametrize("m,k,n", [(70, 45, 90), (512, 128, 256), (500, 100, 130)])
+def test_gemm_beta_accumulates(hip, orc, m, k, n):
+    """beta = 1 onto a nonzero destination (tests/test_cuda_parity.cpp:263-290): the
+    thread-per-output kernel, and the K-sliced tiles whole and ragged."""
+    print_case("gemm-beta", m, k, n)
+    r = rng(9 + m)
+    a, b, c0 = randn(r, m, k), randn(r, k, n), randn(r, m, n)
     c = dev(c0)
     hip.gemm(dev(a), dev(b), c=c, beta=1.0)
     want = orc.binary("add", orc.matmul(a, b), c0)
-    ref_close(host(c), want, k_tol(45) + 1e-6, "beta=1")
+    ref_close(host(c), want, k_tol(k) + 1e-6, "beta=1")
 
 
 def test_gemm_splitk_beta(hip, orc):
@@ -188,6 +204,42 @@ def test_gemm_deterministic(hip):
     r = rng(12)
     a, b = dev(randn(r, 300, 700)), dev(randn(r, 700, 200))
     exact(host(hip.gemm(a, b)), host(hip.gemm(a, b)), "repeat")
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 512, 512), (1000, 300, 200), (2048, 96, 96), (64, 784, 10),
+                                   (96, 2048, 96)])
+@pytest.mark.parametrize("beta", [0.0, 1.0])
+def test_matmul_backward_pair_bits(hip, m, k, n, beta):
+    """ehip_matmul_backward_f32 gives the bits of the two ehip_gemm_f32 calls it replaces
+    (dA = dC B^T, dB = A^T dC), whether the two products share one launch (both on the
+    K-sliced tiles: 512^3, the ragged 1000 x 300 x 200) or not (the others); also with only
+    one of the outputs requested."""
+    import ctypes as C
+    import torch
+    print_case("matmul-backward", m, k, n, beta)
+    g = torch.Generator(device="cuda").manual_seed(m + k + n)
+    a = torch.randn(m, k, device="cuda", generator=g)
+    b = torch.randn(k, n, device="cuda", generator=g)
+    dc = torch.randn(m, n, device="cuda", generator=g)
+    da0 = torch.randn(m, k, device="cuda", generator=g)
+    db0 = torch.randn(k, n, device="cuda", generator=g)
+    p = lambda t: C.c_void_p(t.data_ptr()) if t is not None else None
+
+    def pair(da, db):
+        hip.ok(hip.lib.ehip_matmul_backward_f32(m, k, n, p(a), k, p(b), n, p(dc), n, p(da), k,
+                                                beta, p(db), n, beta, hip.stream()), "pair")
+
+    da, db = da0.clone(), db0.clone()
+    pair(da, db)
+    want_a = hip.gemm(dc, b, c=da0.clone(), trans_b=True, beta=beta)
+    want_b = hip.gemm(a, dc, c=db0.clone(), trans_a=True, beta=beta)
+    exact(host(da), host(want_a), "dA")
+    exact(host(db), host(want_b), "dB")
+    only_a, only_b = da0.clone(), db0.clone()
+    pair(only_a, None)
+    pair(None, only_b)
+    exact(host(only_a), host(want_a), "dA alone")
+    exact(host(only_b), host(want_b), "dB alone")
 
 
 def test_gemm_backward_products(hip, orc):
