@@ -403,47 +403,60 @@ def charlm_leg(engine_mod, eng, timer, cpu_seconds):
     return rec
 
 
-def bandwidth_large(hip, timer, torch, r):
-    """LayerNorm forward / backward, the bias-gradient column sum, softmax forward /
-    backward and max-pool forward / backward over 2^28-element tensors, with the
-    algorithmic bytes of the cfg 5 legs."""
+def bandwidth_legs(hip, eng, timer, torch, r, rows, d, sum_rows, ff, srows, scols, im_shape,
+                   reps):
+    """LayerNorm forward / backward (rows x d), the bias-gradient column sum (sum_rows x ff),
+    softmax forward / backward (srows x scols) and max-pool forward / backward (k 2 over
+    im_shape), each as `reps` back-to-back native launches, median of 15 batches."""
     bl = {}
-    n = 1 << 28
-    rows, d = n // 1024, 1024
+    med = lambda op, ts, ext=(), f=0.0, w=None: timer.median_batch(
+        lambda q: eng.repeat_bandwidth(q, op, ts, ext, f, w), reps, 3)
     x = torch.randn(rows, d, device="cuda", generator=r)
     gam = torch.randn(d, device="cuda", generator=r)
     bet = torch.randn(d, device="cuda", generator=r)
-    sec = timer.time(lambda: hip.layernorm(x, gam, bet), 20, 3)
+    y, xh, inv = hip.layernorm(x, gam, bet)
+    n = x.numel()
+    sec = med("layernorm", [x, gam, bet, y, xh, inv], (rows, d), 1e-5)
     bl[f"layernorm {rows}x{d}"] = roofline("layernorm", "hbm", 12 * n + 4 * rows, sec)
-    _, xh, inv = hip.layernorm(x, gam, bet)
-    sec = timer.time(lambda: hip.layernorm_backward(x, xh, gam, inv), 20, 3)
+    dx = torch.empty_like(x)
+    dg, db = torch.empty(d, device="cuda"), torch.empty(d, device="cuda")
+    sec = med("layernorm_backward", [x, xh, gam, inv, dx, dg, db], (rows, d))
     bl[f"layernorm_backward {rows}x{d}"] = roofline("layernorm_backward", "hbm",
                                                     12 * n + 4 * rows + 8 * d, sec)
-    del x, xh, inv
+    del x, y, xh, inv, dx
     torch.cuda.empty_cache()
-    rows, ff = n // 4096, 4096
-    gb = torch.randn(rows, ff, device="cuda", generator=r)
-    sec = timer.time(lambda: hip.sum_axis(gb, 1, rows, ff), 20, 3)
-    bl[f"bias_grad_sum {rows}x{ff}"] = roofline("sum_axis", "hbm", 4 * n + 4 * ff, sec)
+    gb = torch.randn(sum_rows, ff, device="cuda", generator=r)
+    colsum = torch.empty(ff, device="cuda")
+    sec = med("sum_axis", [gb, colsum], (1, sum_rows, ff))
+    bl[f"bias_grad_sum {sum_rows}x{ff}"] = roofline("sum_axis", "hbm", 4 * gb.numel() + 4 * ff, sec)
     del gb
-    sc = torch.randn(n // 512, 512, device="cuda", generator=r)
-    sec = timer.time(lambda: hip.softmax(sc), 20, 3)
-    bl[f"softmax {n // 512}x512"] = roofline("softmax", "hbm", 8 * n, sec)
-    y = hip.softmax(sc)
-    sec = timer.time(lambda: hip.softmax_backward(y, sc), 20, 3)
-    bl[f"softmax_backward {n // 512}x512"] = roofline("softmax_backward", "hbm", 12 * n, sec)
-    del sc, y
+    sc = torch.randn(srows, scols, device="cuda", generator=r)
+    sy = torch.empty_like(sc)
+    sec = med("softmax", [sc, sy], (srows, scols))
+    bl[f"softmax {srows}x{scols}"] = roofline("softmax", "hbm", 8 * sc.numel(), sec)
+    sdx = torch.empty_like(sc)
+    sec = med("softmax_backward", [sy, sc, sdx], (srows, scols))
+    bl[f"softmax_backward {srows}x{scols}"] = roofline("softmax_backward", "hbm",
+                                                       12 * sc.numel(), sec)
+    del sc, sy, sdx
     torch.cuda.empty_cache()
-    im = torch.randn(256, 64, 128, 128, device="cuda", generator=r)
+    im = torch.randn(*im_shape, device="cuda", generator=r)
     pooled, am = hip.maxpool(im, 2, 2)
-    sec = timer.time(lambda: hip.maxpool(im, 2, 2, out=(pooled, am)), 20, 3)
-    bl["maxpool 256x64x128x128 k2"] = roofline("maxpool", "hbm", 6 * n, sec)
+    w = ehip_window(im_shape)
+    sec = med("maxpool", [im, pooled, am], (), 0.0, w)
+    shape = "x".join(str(v) for v in im_shape)
+    bl[f"maxpool {shape} k2"] = roofline("maxpool", "hbm", 6 * im.numel(), sec)
     gp = torch.randn_like(pooled)
     dim = torch.empty_like(im)
-    sec = timer.time(lambda: hip.maxpool_backward(am, gp, tuple(im.shape), 2, 2, dx=dim), 20, 3)
-    bl["maxpool_backward 256x64x128x128 k2"] = roofline("maxpool_backward", "hbm", 6 * n, sec)
+    sec = med("maxpool_backward", [am, gp, dim], (), 0.0, w)
+    bl[f"maxpool_backward {shape} k2"] = roofline("maxpool_backward", "hbm", 6 * im.numel(), sec)
     del im, pooled, am, gp, dim
     return bl
+
+
+def ehip_window(im_shape, k=2, stride=2, pad=0):
+    import ehip
+    return ehip.window(*im_shape, k, k, stride, pad)
 
 
 def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
@@ -518,46 +531,19 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
     torch.cuda.empty_cache()
     # The other bandwidth-bound kernels of the path, at the shapes cfg 5 gives
     # them (16 x 512 tokens, d 1024, FFN 4096, 16 heads of 512 x 512 scores),
-    # and max-pool at a large image batch. Bytes are the algorithmic ones:
-    # every input read once, every output written once.
-    bt = {}
-    rows, d, ff = 8192, 1024, 4096
-    x = torch.randn(rows, d, device="cuda", generator=r)
-    gam = torch.randn(d, device="cuda", generator=r)
-    bet = torch.randn(d, device="cuda", generator=r)
-    sec = timer.time(lambda: hip.layernorm(x, gam, bet), 20, 3)
-    bt["layernorm 8192x1024"] = roofline("layernorm", "hbm", 12 * x.numel() + 4 * rows, sec)
-    _, xh, inv = hip.layernorm(x, gam, bet)
-    sec = timer.time(lambda: hip.layernorm_backward(x, xh, gam, inv), 20, 3)
-    bt["layernorm_backward 8192x1024"] = roofline("layernorm_backward", "hbm",
-                                                  12 * x.numel() + 4 * rows + 8 * d, sec)
-    del x, xh, inv
-    gb = torch.randn(rows, ff, device="cuda", generator=r)
-    sec = timer.time(lambda: hip.sum_axis(gb, 1, rows, ff), 20, 3)
-    bt["bias_grad_sum 8192x4096"] = roofline("sum_axis", "hbm", 4 * gb.numel() + 4 * ff, sec)
-    del gb
-    sc = torch.randn(16 * 16 * 512, 512, device="cuda", generator=r)
-    sec = timer.time(lambda: hip.softmax(sc), 20, 3)
-    bt["softmax 131072x512"] = roofline("softmax", "hbm", 8 * sc.numel(), sec)
-    y = hip.softmax(sc)
-    sec = timer.time(lambda: hip.softmax_backward(y, sc), 20, 3)
-    bt["softmax_backward 131072x512"] = roofline("softmax_backward", "hbm", 12 * sc.numel(), sec)
-    del sc, y
-    im = torch.randn(64, 64, 112, 112, device="cuda", generator=r)
-    pooled, am = hip.maxpool(im, 2, 2)  # outputs reused by the timed calls
-    sec = timer.time(lambda: hip.maxpool(im, 2, 2, out=(pooled, am)), 20, 3)
-    bt["maxpool 64x64x112x112 k2"] = roofline("maxpool", "hbm", 6 * im.numel(), sec)
-    gp = torch.randn_like(pooled)
-    dim = torch.empty_like(im)
-    sec = timer.time(lambda: hip.maxpool_backward(am, gp, tuple(im.shape), 2, 2, dx=dim), 20, 3)
-    bt["maxpool_backward 64x64x112x112 k2"] = roofline("maxpool_backward", "hbm",
-                                                       6 * im.numel(), sec)
-    del im, pooled, am, gp, dim
-    out["bandwidth_transformer_shapes"] = bt
+    # and max-pool at a large image batch, launched back to back from native
+    # code (a ~20 us kernel launched from Python leaves the GPU idle between
+    # calls). Bytes are the algorithmic ones: every input read once, every
+    # output written once.
+    out["bandwidth_transformer_shapes"] = bandwidth_legs(hip, eng, timer, torch, r, 8192, 1024,
+                                                         8192, 4096, 16 * 16 * 512, 512,
+                                                         (64, 64, 112, 112), 100)
     torch.cuda.empty_cache()
     # The same kernels at cfg 4's size, 2^28 elements, where the launch's ramp
     # and tail are a small part of the time.
-    out["bandwidth_2^28"] = bandwidth_large(hip, timer, torch, r)
+    n = 1 << 28
+    out["bandwidth_2^28"] = bandwidth_legs(hip, eng, timer, torch, r, n // 1024, 1024, n // 4096,
+                                           4096, n // 512, 512, (256, 64, 128, 128), 5)
     torch.cuda.empty_cache()
     return out
 
@@ -582,7 +568,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target length of the cfg 2 / cfg 3 reference CPU samples")
-    ap.add_argument("--cpu-sample-batch", type=int, default=1,
+    ap.add_argument("--cpu-sample-batch", type=int, default=4,
                     help="sequences of the cfg 5 batch in the reference CPU sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")

@@ -241,6 +241,57 @@ struct AddBackward {
     }
 };
 
+// The multiply node's backward in one pass (src/tensor_ops.cpp:199-213, same
+// shapes): da = g * b, db = g * a, each product rounded, then, when the
+// gradient already holds values, added to it (the composed graph's product
+// node followed by add_grad's accumulation, bit for bit). MA / MB: 0 the
+// operand needs no gradient, 1 write the product, 2 add it to the gradient.
+template <int MA, int MB>
+struct MulBackward {
+    static constexpr int kA = MB != 0, kB = MA != 0;  // a feeds db, b feeds da
+    static constexpr int kIn = 1 + kA + kB + (MA == 2) + (MB == 2);
+    const float* g;
+    const float* a;
+    const float* b;
+    float* da;
+    float* db;
+    template <bool NT>
+    __device__ void load(int64_t v, float4* r) const {
+        int q = 0;
+        r[q++] = ld4<NT>(g, v);
+        if (kA) r[q++] = ld4<NT>(a, v);
+        if (kB) r[q++] = ld4<NT>(b, v);
+        if (MA == 2) r[q++] = ld4<NT>(da, v);
+        if (MB == 2) r[q++] = ld4<NT>(db, v);
+    }
+    template <bool NT>
+    __device__ void store(int64_t v, const float4* r) const {
+        const auto mul = [](float x, float y, float) { return x * y; };
+        const auto add = [](float x, float y, float) { return x + y; };
+        const float4 gv = r[0];
+        const int ia = 1, ib = 1 + kA, ida = 1 + kA + kB, idb = ida + (MA == 2);
+        if (MA != 0) {
+            const float4 p = map4(mul, gv, r[ib], gv);
+            st4<NT>(da, v, MA == 2 ? map4(add, r[ida], p, p) : p);
+        }
+        if (MB != 0) {
+            const float4 p = map4(mul, gv, r[ia], gv);
+            st4<NT>(db, v, MB == 2 ? map4(add, r[idb], p, p) : p);
+        }
+    }
+    __device__ void scalar(int64_t i) const {
+        const float gv = g[i];
+        if (MA != 0) {
+            const float p = gv * b[i];
+            da[i] = MA == 2 ? da[i] + p : p;
+        }
+        if (MB != 0) {
+            const float p = gv * a[i];
+            db[i] = MB == 2 ? db[i] + p : p;
+        }
+    }
+};
+
 struct Fill {
     static constexpr int kIn = 1;
     float* x;
@@ -567,6 +618,30 @@ int ehip_add_backward_f32(const float* g, float* da, float* db, int64_t n, int a
     if (accumulate_b)
         return launch_stream("add_backward", AddBackward<false, true>{g, da, db}, n, vec, s);
     return launch_stream("add_backward", AddBackward<false, false>{g, da, db}, n, vec, s);
+}
+
+int ehip_mul_backward_f32(const float* g, const float* a, const float* b, float* da, float* db,
+                          int64_t n, int accumulate_a, int accumulate_b, void* stream) {
+    EHIP_READY();
+    if (!g || (da && !b) || (db && !a)) return fail(EHIP_EINVAL, "mul_backward: null pointer");
+    if (da && da == db) return fail(EHIP_EINVAL, "mul_backward: da and db alias");
+    const int ma = da ? (accumulate_a ? 2 : 1) : 0, mb = db ? (accumulate_b ? 2 : 1) : 0;
+    const bool vec = aligned16(g) && (!a || aligned16(a)) && (!b || aligned16(b)) &&
+                     (!da || aligned16(da)) && (!db || aligned16(db));
+    hipStream_t s = as_stream(stream);
+#define EHIP_MULB(A, B)                                                                            \
+    if (ma == A && mb == B)                                                                        \
+        return launch_stream("mul_backward", MulBackward<A, B>{g, a, b, da, db}, n, vec, s)
+    EHIP_MULB(1, 1);
+    EHIP_MULB(2, 2);
+    EHIP_MULB(1, 2);
+    EHIP_MULB(2, 1);
+    EHIP_MULB(1, 0);
+    EHIP_MULB(2, 0);
+    EHIP_MULB(0, 1);
+    EHIP_MULB(0, 2);
+#undef EHIP_MULB
+    return EHIP_OK;  // neither gradient requested
 }
 
 int ehip_fill_f32(float* x, int64_t n, float value, void* stream) {

@@ -73,8 +73,15 @@ __device__ __forceinline__ float block_rows_sum(const float* __restrict__ xs, in
     return s;
 }
 
+// Slab z's output: out + z * out_slab, or out_second for slab 1 when given
+// (two separate arrays).
+__device__ __forceinline__ float* slab_out(float* out, float* out_second, int64_t out_slab) {
+    return blockIdx.z == 1 && out_second != nullptr ? out_second
+                                                   : out + int64_t(blockIdx.z) * out_slab;
+}
+
 __global__ __launch_bounds__(kThreads) void sum_cols(const float* __restrict__ x,
-                                                     float* __restrict__ out, int64_t rows,
+                                                     float* out, float* out_second, int64_t rows,
                                                      int64_t cols, int64_t ld, int64_t rpb,
                                                      int64_t x_slab, int64_t out_slab, int cw) {
     __shared__ float lanes[kThreads];
@@ -83,7 +90,7 @@ __global__ __launch_bounds__(kThreads) void sum_cols(const float* __restrict__ x
     const int64_t r1 = r0 + rpb < rows ? r0 + rpb : rows;
     const float s = block_rows_sum(x + int64_t(blockIdx.z) * x_slab, r0, r1, c, cols, ld, cw, lanes);
     if (threadIdx.x < cw && c < cols)
-        out[int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c] = s;
+        slab_out(out, out_second, out_slab)[int64_t(blockIdx.x) * cols + c] = s;
 }
 
 // sum_cols for CW = 64 with four adjacent columns per thread (float4 loads,
@@ -135,7 +142,7 @@ __device__ __forceinline__ void store4(float* o, float4 v) {
 }
 
 __global__ __launch_bounds__(kThreads) void sum_cols4(const float* __restrict__ x,
-                                                      float* __restrict__ out, int64_t rows,
+                                                      float* out, float* out_second, int64_t rows,
                                                       int64_t cols, int64_t ld, int64_t rpb,
                                                       int64_t x_slab, int64_t out_slab) {
     __shared__ float4 lanes[kThreads];
@@ -144,7 +151,7 @@ __global__ __launch_bounds__(kThreads) void sum_cols4(const float* __restrict__ 
     const int64_t r1 = r0 + rpb < rows ? r0 + rpb : rows;
     const float4 s = block_rows_sum4(x + int64_t(blockIdx.z) * x_slab, r0, r1, c, cols, ld, lanes);
     if (threadIdx.x < 64 && c < cols)
-        store4(out + int64_t(blockIdx.z) * out_slab + int64_t(blockIdx.x) * cols + c, s);
+        store4(slab_out(out, out_second, out_slab) + int64_t(blockIdx.x) * cols + c, s);
 }
 
 // Whole-buffer sum in double: a fixed grid of blocks, each thread striding by
@@ -198,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void reduce_stage2(const double* __restri
 // row blocks are sized for (the order of every sum depends on it).
 int column_sums_plan(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64_t ld,
                      int64_t x_slab, float* out, int64_t out_slab, int64_t plan_slabs,
-                     hipStream_t s) {
+                     hipStream_t s, float* out_second = nullptr) {
     if (slabs == 0 || cols == 0) return EHIP_OK;
     int cw = 1;
     while (cw < cols && cw < 64) cw *= 2;
@@ -220,10 +227,11 @@ int column_sums_plan(const float* x, int64_t slabs, int64_t rows, int64_t cols, 
     if (blocks == 1) {
         if (vec) {
             EHIP_LAUNCH("column_sums", sum_cols4, dim3(1, tiles4, unsigned(slabs)), dim3(kThreads),
-                        0, s, x, out, rows, cols, ld, rows, x_slab, out_slab);
+                        0, s, x, out, out_second, rows, cols, ld, rows, x_slab, out_slab);
         } else {
             EHIP_LAUNCH("column_sums", sum_cols, dim3(1, unsigned(tiles), unsigned(slabs)),
-                        dim3(kThreads), 0, s, x, out, rows, cols, ld, rows, x_slab, out_slab, cw);
+                        dim3(kThreads), 0, s, x, out, out_second, rows, cols, ld, rows, x_slab,
+                        out_slab, cw);
         }
         return EHIP_OK;
     }
@@ -232,17 +240,19 @@ int column_sums_plan(const float* x, int64_t slabs, int64_t rows, int64_t cols, 
     if (partial == nullptr) return EHIP_ENOMEM;
     if (vec) {
         EHIP_LAUNCH("column_sums_blocks", sum_cols4, dim3(unsigned(blocks), tiles4, unsigned(slabs)),
-                    dim3(kThreads), 0, s, x, partial, rows, cols, ld, rpb, x_slab, blocks * cols);
+                    dim3(kThreads), 0, s, x, partial, nullptr, rows, cols, ld, rpb, x_slab,
+                    blocks * cols);
         EHIP_LAUNCH("column_sums_final", sum_cols4, dim3(1, tiles4, unsigned(slabs)),
-                    dim3(kThreads), 0, s, partial, out, blocks, cols, cols, blocks, blocks * cols,
-                    out_slab);
+                    dim3(kThreads), 0, s, partial, out, out_second, blocks, cols, cols, blocks,
+                    blocks * cols, out_slab);
         return EHIP_OK;
     }
     EHIP_LAUNCH("column_sums_blocks", sum_cols, dim3(unsigned(blocks), unsigned(tiles), unsigned(slabs)),
-                dim3(kThreads), 0, s, x, partial, rows, cols, ld, rpb, x_slab, blocks * cols, cw);
+                dim3(kThreads), 0, s, x, partial, nullptr, rows, cols, ld, rpb, x_slab, blocks * cols,
+                cw);
     EHIP_LAUNCH("column_sums_final", sum_cols, dim3(1, unsigned(tiles), unsigned(slabs)),
-                dim3(kThreads), 0, s, partial, out, blocks, cols, cols, blocks, blocks * cols,
-                out_slab, cw);
+                dim3(kThreads), 0, s, partial, out, out_second, blocks, cols, cols, blocks,
+                blocks * cols, out_slab, cw);
     return EHIP_OK;
 }
 
@@ -251,19 +261,13 @@ int column_sums(const float* x, int64_t slabs, int64_t rows, int64_t cols, int64
     return column_sums_plan(x, slabs, rows, cols, ld, x_slab, out, cols, slabs, s);
 }
 
-// Two single-slab column sums in the launches of one: the second slab's
-// output is addressed as out0 + (out1 - out0) in floats (both are float
-// arrays in the one flat device address space), and the row blocks are sized
-// for one slab, so each sum has the order a column_sums call of its own gives.
+// Two single-slab column sums in the launches of one: slab 1 writes to out1
+// (a separate array, passed to the kernels as such), and the row blocks are
+// sized for one slab, so each sum has the order a column_sums call of its own
+// gives.
 int column_sums_pair(const float* x, int64_t rows, int64_t cols, int64_t ld, int64_t x_second,
                      float* out0, float* out1, hipStream_t s) {
-    const intptr_t gap = reinterpret_cast<intptr_t>(out1) - reinterpret_cast<intptr_t>(out0);
-    if (gap % intptr_t(sizeof(float)) != 0) {
-        if (int rc = column_sums(x, 1, rows, cols, ld, 0, out0, s)) return rc;
-        return column_sums(x + x_second, 1, rows, cols, ld, 0, out1, s);
-    }
-    return column_sums_plan(x, 2, rows, cols, ld, x_second, out0,
-                            int64_t(gap / intptr_t(sizeof(float))), 1, s);
+    return column_sums_plan(x, 2, rows, cols, ld, x_second, out0, 0, 1, s, out1);
 }
 
 }  // namespace ehip

@@ -96,6 +96,7 @@ _SIGS = {
     "ehip_relu_backward_f32": [_vp, _vp, _vp, _i64, _vp],
     "ehip_accumulate_grad_f32": [_vp, _vp, _i64, _i, _vp],
     "ehip_add_backward_f32": [_vp, _vp, _vp, _i64, _i, _i, _vp],
+    "ehip_mul_backward_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _vp],
     "ehip_fill_f32": [_vp, _i64, _f, _vp],
     "ehip_scale_f32": [_vp, _i64, _f, _vp],
     "ehip_sgd_f32": [_vp, _vp, _vp, _i64, _f, _f, _f, _vp],
@@ -282,6 +283,13 @@ class Backend:
                                                   int(initialize), self.stream()),
                 "accumulate_grad")
         return grad
+
+    def mul_backward(self, g, a, b, da=None, db=None, acc_a=False, acc_b=False):
+        """da (+)= g * b, db (+)= g * a in one launch; None skips that gradient."""
+        self.ok(self.lib.ehip_mul_backward_f32(self.p(g), self.p(a), self.p(b), self.p(da),
+                                               self.p(db), g.numel(), int(acc_a), int(acc_b),
+                                               self.stream()), "mul_backward")
+        return da, db
 
     def add_backward(self, g, da, db, acc_a, acc_b):
         self.ok(self.lib.ehip_add_backward_f32(self.p(g), self.p(da), self.p(db), g.numel(),

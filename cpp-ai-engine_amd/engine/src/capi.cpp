@@ -14,6 +14,7 @@
 #include <cstring>
 #include <exception>
 #include <memory>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -615,6 +616,42 @@ int eng_repeat_gemm(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t 
             engine::hip::check(ehip_gemm_f32(trans_a, trans_b, batch, m, n, k, a, lda, stride_a, b,
                                              ldb, stride_b, beta, c, ldc, stride_c, stream),
                                "gemm");
+    });
+}
+
+// Enqueues `reps` back-to-back calls of one bandwidth-bound entry point on
+// `stream`, so that events around the batch time the kernels without host
+// launch gaps. p holds the device pointers and n the extents, in the entry
+// point's argument order:
+//   0 ehip_layernorm_f32          p: x gamma beta out xhat inv    n: rows cols   f: eps
+//   1 ehip_layernorm_backward_f32 p: dy xhat gamma inv dx dg db   n: rows cols
+//   2 ehip_sum_axis_f32           p: x out                        n: outer axis inner
+//   3 ehip_softmax_f32            p: x y                          n: rows cols
+//   4 ehip_softmax_backward_f32   p: y g dx                       n: rows cols
+//   5 ehip_maxpool_f32            p: x y argmax                   w: the window
+//   6 ehip_maxpool_backward_f32   p: argmax g dx                  w: the window
+int eng_repeat_bandwidth(int op, void* const* p, const int64_t* n, float f, const ehip_window_t* w,
+                         void* stream, int reps) {
+    return guarded([&] {
+        const auto F = [&](int i) { return static_cast<float*>(p[i]); };
+        for (int r = 0; r < reps; ++r) {
+            int rc = EHIP_EINVAL;
+            switch (op) {
+                case 0: rc = ehip_layernorm_f32(F(0), F(1), F(2), F(3), F(4), F(5), n[0], n[1], f,
+                                                stream); break;
+                case 1: rc = ehip_layernorm_backward_f32(F(0), F(1), F(2), F(3), F(4), F(5), F(6),
+                                                         n[0], n[1], stream); break;
+                case 2: rc = ehip_sum_axis_f32(F(0), F(1), n[0], n[1], n[2], stream); break;
+                case 3: rc = ehip_softmax_f32(F(0), F(1), n[0], n[1], stream); break;
+                case 4: rc = ehip_softmax_backward_f32(F(0), F(1), F(2), n[0], n[1], stream); break;
+                case 5: rc = ehip_maxpool_f32(F(0), F(1), static_cast<int32_t*>(p[2]), w, stream);
+                        break;
+                case 6: rc = ehip_maxpool_backward_f32(static_cast<const int32_t*>(p[0]), F(1),
+                                                       F(2), w, stream); break;
+                default: throw std::invalid_argument("repeat_bandwidth: unknown op");
+            }
+            engine::hip::check(rc, "repeat_bandwidth");
+        }
     });
 }
 

@@ -147,6 +147,26 @@ Tensor Tensor::operator*(const Tensor& other) const {
     if (track(requires_grad() || other.requires_grad())) {
         Tensor self_copy = *this, other_copy = other;
         attach(res, {impl_, other.impl_}, [self_copy, other_copy](const Tensor& g) mutable {
+            const bool na = self_copy.requires_grad(), nb = other_copy.requires_grad();
+            if (self_copy.shape() == other_copy.shape() &&
+                self_copy.get_impl() != other_copy.get_impl() && g.size() > 0) {
+                // Same shapes: both products in one launch, added in place into a
+                // gradient that already holds values (add_grad's sum), otherwise
+                // written to a fresh buffer that add_grad then takes over.
+                float* acc_a = na ? grad_in_place(self_copy) : nullptr;
+                float* acc_b = nb ? grad_in_place(other_copy) : nullptr;
+                Tensor ta = na && !acc_a ? Tensor(self_copy.shape(), 0.0f, false) : Tensor();
+                Tensor tb = nb && !acc_b ? Tensor(other_copy.shape(), 0.0f, false) : Tensor();
+                hip::check(ehip_mul_backward_f32(dptr(g), dptr(self_copy), dptr(other_copy),
+                                                 na ? (acc_a ? acc_a : dout(ta)) : nullptr,
+                                                 nb ? (acc_b ? acc_b : dout(tb)) : nullptr,
+                                                 int64_t(g.size()), acc_a != nullptr,
+                                                 acc_b != nullptr, nullptr),
+                           "mul backward");
+                if (na && !acc_a) self_copy.add_grad(ta);
+                if (nb && !acc_b) other_copy.add_grad(tb);
+                return;
+            }
             // g * expand(other) is the broadcast product itself.
             if (self_copy.requires_grad()) self_copy.add_grad(binary_values(EHIP_MUL, g, other_copy, "mul"));
             if (other_copy.requires_grad())

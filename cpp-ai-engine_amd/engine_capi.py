@@ -91,6 +91,23 @@ class Engine:
                    b.data_ptr(), b.shape[1], 0, beta, c.data_ptr(), n, 0,
                    torch.cuda.current_stream().cuda_stream, reps))
 
+    BANDWIDTH_OPS = {"layernorm": 0, "layernorm_backward": 1, "sum_axis": 2, "softmax": 3,
+                     "softmax_backward": 4, "maxpool": 5, "maxpool_backward": 6}
+
+    def repeat_bandwidth(self, reps, op, tensors, extents=(), f=0.0, window=None):
+        """Enqueues `reps` calls of a bandwidth-bound ehip entry point from C++ on torch's
+        current stream (see eng_repeat_bandwidth): tensors are CUDA tensors in the entry
+        point's pointer order, extents its integer sizes, window an ehip window struct."""
+        import torch
+        ptrs = (C.c_void_p * len(tensors))(*[t.data_ptr() for t in tensors])
+        ext = (_i64 * max(1, len(extents)))(*extents)
+        fn = self.lib.eng_repeat_bandwidth
+        fn.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_float, C.c_void_p, C.c_void_p,
+                       C.c_int]
+        self._ok(fn(self.BANDWIDTH_OPS[op], ptrs, ext, f,
+                    C.byref(window) if window is not None else None,
+                    torch.cuda.current_stream().cuda_stream, reps))
+
     def repeat_matmul_backward(self, reps, a, b, dc, da, db):
         """Enqueues `reps` ehip_matmul_backward_f32 calls (dA = dC B^T, dB = A^T dC) from C++
         on torch's current stream; 2-D contiguous CUDA tensors."""

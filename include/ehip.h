@@ -269,6 +269,14 @@ int ehip_relu_backward_f32(const float* x, const float* g, float* dx, int64_t n,
 int ehip_accumulate_grad_f32(float* grad, const float* g, int64_t n, int initialize,
                              void* stream);
 
+/* The backward of y = a * b (same shapes) in one pass: da = g * b and db = g * a,
+ * each product rounded, then added to the existing gradient when accumulate_*
+ * is set (otherwise written); either of da / db may be NULL. Replaces the two
+ * products and two add_grad calls of the multiply node's backward
+ * (src/tensor_ops.cpp:199-213): the same bits, one launch. */
+int ehip_mul_backward_f32(const float* g, const float* a, const float* b, float* da, float* db,
+                          int64_t n, int accumulate_a, int accumulate_b, void* stream);
+
 /* The backward of out = a + b for same-shape operands, fused: the upstream
  * gradient g goes to both operand gradients in one pass, each either
  * initialised (accumulate_* == 0: da = g) or accumulated (da += g).

@@ -15,7 +15,7 @@ import _compose as K
 import _trajectory as TR
 from _fixtures import load
 from _hip import k_tol, print_case, ref_close, ref_err
-from _oracle import Ref, oracle_or_skip
+from _oracle import Ref, oracle_or_skip, ref_or_skip
 
 pytestmark = pytest.mark.gpu
 
@@ -270,6 +270,31 @@ def test_block_cfg3_shapes(eng, orc):
     ref_close(y, wy, k_tol(ff), "y")
     ref_close(dx, wdx, k_tol(b * s), "dx")
     ref_close(dp, wdp, k_tol(b * s), "dparams")
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+@pytest.mark.parametrize("shape_a,shape_b", [((64, 96), (64, 96)), ((33, 7), (7,)),
+                                             ((4, 3, 5), (3, 5)), ((1 << 16,), (1 << 16,))])
+def test_binary_nodes_vs_reference(eng, op, shape_a, shape_b):
+    """The four element-wise nodes forward and backward through the engine (the multiply
+    node's backward one fused launch for same shapes) against the compiled reference:
+    equal values (a -0.0 that the engine's adopted gradient keeps compares equal to the
+    reference's +0.0); the broadcast operand's gradient is a sum over rows, at the K-term
+    bound."""
+    ref = ref_or_skip()
+    print_case("binary node", op, shape_a, shape_b)
+    r = rng(len(shape_a) * 10 + len(shape_b))
+    a = r.standard_normal(shape_a, dtype=np.float32)
+    b = r.standard_normal(shape_b, dtype=np.float32) + (3.0 if op == "div" else 0.0)
+    a.ravel()[::9] = 0.0
+    dy = r.standard_normal(shape_a, dtype=np.float32)
+    y, da, db = eng.binary_fwd_bwd(op, a, b, dy)
+    wy, wda, wdb = ref.binary_fwd_bwd(op, a, b, dy)
+    assert np.array_equal(y, wy) and np.array_equal(da, wda)
+    if shape_a == shape_b:
+        assert np.array_equal(db, wdb)
+    else:
+        ref_close(db, wdb, k_tol(a.size // b.size), "db")
 
 
 def test_embedding_exact(eng, orc):

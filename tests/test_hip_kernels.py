@@ -310,6 +310,29 @@ def test_accumulate_and_add_backward_exact(hip, orc, n):
                   f"db {acc_a}{acc_b}")
 
 
+@pytest.mark.parametrize("n", [5, 4096, 100003, (1 << 22) + 3])
+@pytest.mark.parametrize("mode_a,mode_b", [(1, 1), (2, 2), (1, 2), (2, 1), (1, 0), (0, 2)])
+def test_mul_backward_exact(hip, orc, n, mode_a, mode_b):
+    """The fused multiply backward equals the composed node bit for bit: the oracle's
+    product g * b (g * a), added to the existing gradient when accumulating (mode 2),
+    written otherwise (mode 1), skipped (mode 0); with zeros, -0 and unaligned lengths."""
+    print_case("mul-backward", n, mode_a, mode_b)
+    r = rng(n + 10 * mode_a + mode_b)
+    g, a, b = randn(r, n), randn(r, n), randn(r, n)
+    a[::5] = 0.0
+    b[1::7] = -0.0
+    base_a, base_b = randn(r, n), randn(r, n)
+    da = dev(base_a) if mode_a else None
+    db = dev(base_b) if mode_b else None
+    hip.mul_backward(dev(g), dev(a), dev(b), da, db, mode_a == 2, mode_b == 2)
+    if mode_a:
+        p = orc.binary("mul", g, b)
+        exact(host(da), orc.accumulate(base_a.copy(), p) if mode_a == 2 else p, "da")
+    if mode_b:
+        p = orc.binary("mul", g, a)
+        exact(host(db), orc.accumulate(base_b.copy(), p) if mode_b == 2 else p, "db")
+
+
 @pytest.mark.parametrize("n", [7, 4096, 65537, (1 << 24) + 3])
 def test_adam_trajectory_exact(hip, orc, n):
     """Ten Adam steps, bias corrections from the host as in src/optim.cpp:119-120."""
