@@ -423,6 +423,18 @@ def bandwidth_legs(hip, eng, timer, torch, r, rows, d, sum_rows, ff, srows, scol
     sec = med("layernorm_backward", [x, xh, gam, inv, dx, dg, db], (rows, d))
     bl[f"layernorm_backward {rows}x{d}"] = roofline("layernorm_backward", "hbm",
                                                     12 * n + 4 * rows + 8 * d, sec)
+    # As the engine runs it inside a step: the row kernel with the group partials; the
+    # dgamma / dbeta sums of all LayerNorms (and convolution blocks) of a backward run later
+    # in one launch of their own, or inside Adam's.
+    import ctypes
+    groups = ctypes.c_int64(0)
+    nparts = hip.lib.ehip_layernorm_backward_partials(rows, d, ctypes.byref(groups))
+    if nparts > 0:
+        part = torch.empty(nparts, device="cuda")
+        sec = med("layernorm_backward_rows", [x, xh, gam, inv, dx, part], (rows, d, groups.value))
+        bl[f"layernorm_backward {rows}x{d} (engine: sums deferred)"] = roofline(
+            "layernorm_backward_rows", "hbm", 12 * n + 4 * rows + 4 * d, sec)
+        del part
     del x, y, xh, inv, dx
     torch.cuda.empty_cache()
     gb = torch.randn(sum_rows, ff, device="cuda", generator=r)

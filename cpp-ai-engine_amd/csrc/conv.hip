@@ -1398,7 +1398,7 @@ __global__ __launch_bounds__(256) void conv_weight_reduce(const float* __restric
 // Several layers' reductions in one launch: job j owns blocks [first, next
 // job's first), each with the rl of its own chunk count -- the same sums as
 // one conv_weight_reduce per job.
-constexpr int kMaxReduceJobs = 16;
+constexpr int kMaxReduceJobs = 32;
 
 struct ReduceJob {
     const float* partial;

@@ -679,119 +679,97 @@ __device__ __forceinline__ void combine_waves(float (&acc)[V], float (*tree)[V][
     }
 }
 
-// The large-problem form: a group is a block of kLnWaves waves, each taking
-// one row at a time (wave w of group g: rows g + groups (w + kLnWaves i),
-// ascending i, the next row loaded before the current one is reduced), so
-// that every CU holds many independent rows while the partials stay few
-// (one dgamma / dbeta row per group). The waves' partial sums are combined
-// by a fixed tree through LDS (w += w + half, halving), then written to
-// partial[group][2][cols]; layernorm_param_grads adds the groups in order.
-
-template <int V, bool VEC4, bool NT = false>
+// The large-problem form: a group is a block of kLnWaves waves; wave w of
+// group g takes rows g + groups (w + kLnWaves i), ascending i, AHEAD of them at
+// a time with every load issued before the first of them is reduced, so that
+// every CU holds many independent rows while the partials stay few (one
+// dgamma / dbeta row per group). The waves' partial sums are combined by a
+// fixed tree through LDS (w += w + half, halving), then written interleaved,
+// partial[group][c][2] = (dgamma, dbeta): the layout of a convolution
+// weight-gradient job with one weight per output channel, so that the ordered
+// sum over groups is conv_weight_reduce's (here, in ehip_conv_weight_reduce_f32,
+// or inside the Adam launch of ehip_adam_multi_reduce_f32). Measured at
+// 8192 x 1024 (cfg5): four rows ahead with nontemporal accesses 16.6 us against
+// 19.0 us for the previous one-row prefetch; at 2^28 elements one row at a time
+// is faster (545 against 564 us).
+template <int V, bool VEC4, int AHEAD>
 __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
     const float* __restrict__ dy, const float* __restrict__ xhat, const float* __restrict__ gamma,
     const float* __restrict__ inv_std, float* __restrict__ dx, float* __restrict__ partial,
     int64_t rows, int64_t cols) {
-    using F = Frag<64, V, VEC4, NT>;
+    using F = Frag<64, V, VEC4, true>;
     __shared__ float tree[kLnWaves / 2][V][64];
     const float inv_d = 1.0f / static_cast<float>(cols);
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const int64_t group = blockIdx.x, groups = gridDim.x;
-    float dg[V], db[V], gm[V];
+    float dg[V], db[V];
+    F gmf;  // gamma, zero past the row
+    gmf.load(gamma, int(cols), lane, 0.0f);
+    const float* gm = gmf.v;
 #pragma unroll
     for (int t = 0; t < V; ++t) {
         dg[t] = 0.0f;
         db[t] = 0.0f;
-        const int64_t c = F::col(lane, t);
-        gm[t] = c < cols ? gamma[c] : 0.0f;
     }
     const int64_t step = groups * kLnWaves;
-    int64_t r = group + groups * wave;
-    F fd, fh;
-    float inv = 0.0f;
-    if (r < rows) {
-        fd.load(dy + r * cols, int(cols), lane, 0.0f);
-        fh.load(xhat + r * cols, int(cols), lane, 0.0f);
-        inv = inv_std[r];
-    }
-    for (; r < rows; r += step) {
-        F nd, nh;
-        float ninv = 0.0f;
-        if (r + step < rows) {
-            nd.load(dy + (r + step) * cols, int(cols), lane, 0.0f);
-            nh.load(xhat + (r + step) * cols, int(cols), lane, 0.0f);
-            ninv = inv_std[r + step];
-        }
-        float s1 = 0.0f, s2 = 0.0f;
+    for (int64_t r0 = group + groups * wave; r0 < rows; r0 += step * AHEAD) {
+        F fd[AHEAD], fh[AHEAD];
+        float iv[AHEAD];
 #pragma unroll
-        for (int t = 0; t < V; ++t) {
-            const float dxh = fd.v[t] * gm[t];
-            s1 += dxh;
-            s2 += dxh * fh.v[t];
+        for (int a = 0; a < AHEAD; ++a) {
+            const int64_t r = r0 + a * step;
+            iv[a] = 0.0f;
+            if (r < rows) {
+                fd[a].load(dy + r * cols, int(cols), lane, 0.0f);
+                fh[a].load(xhat + r * cols, int(cols), lane, 0.0f);
+                iv[a] = inv_std[r];
+            }
         }
-        s1 = wave_sum(s1);
-        s2 = wave_sum(s2);
-        F fo;
 #pragma unroll
-        for (int t = 0; t < V; ++t) {
-            const float dxh = fd.v[t] * gm[t];
-            fo.v[t] = inv * (dxh - inv_d * s1 - fh.v[t] * inv_d * s2);
-            dg[t] = dg[t] + fd.v[t] * fh.v[t];
-            db[t] = db[t] + fd.v[t];
+        for (int a = 0; a < AHEAD; ++a) {
+            const int64_t r = r0 + a * step;
+            if (r >= rows) break;
+            float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+            for (int t = 0; t < V; ++t) {
+                const float dxh = fd[a].v[t] * gm[t];
+                s1 += dxh;
+                s2 += dxh * fh[a].v[t];
+            }
+            s1 = wave_sum(s1);
+            s2 = wave_sum(s2);
+            F fo;
+#pragma unroll
+            for (int t = 0; t < V; ++t) {
+                const float dxh = fd[a].v[t] * gm[t];
+                fo.v[t] = iv[a] * (dxh - inv_d * s1 - fh[a].v[t] * inv_d * s2);
+                dg[t] = dg[t] + fd[a].v[t] * fh[a].v[t];
+                db[t] = db[t] + fd[a].v[t];
+            }
+            fo.store(dx + r * cols, int(cols), lane);
         }
-        fo.store(dx + r * cols, int(cols), lane);
-        fd = nd;
-        fh = nh;
-        inv = ninv;
     }
     combine_waves<V>(dg, tree, wave, lane);
     combine_waves<V>(db, tree, wave, lane);
     if (wave == 0) {
         float* pg = partial + group * 2 * cols;
+        if (VEC4) {
+            // Columns t and t + 1 of a float4 slot are adjacent: one 16-byte store
+            // (cols is a multiple of 4 here, so a slot is inside or outside whole).
 #pragma unroll
-        for (int t = 0; t < V; ++t) {
-            const int64_t c = F::col(lane, t);
-            if (c < cols) {
-                pg[c] = dg[t];
-                pg[cols + c] = db[t];
+            for (int t = 0; t < V; t += 2) {
+                const int64_t c = F::col(lane, t);
+                if (c < cols)
+                    *reinterpret_cast<float4*>(pg + 2 * c) =
+                        make_float4(dg[t], db[t], dg[t + 1], db[t + 1]);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < V; ++t) {
+                const int64_t c = F::col(lane, t);
+                if (c < cols) *reinterpret_cast<float2*>(pg + 2 * c) = make_float2(dg[t], db[t]);
             }
         }
-    }
-}
-
-// dgamma[c] and dbeta[c] from partial[group][2][cols]: kLanes lanes per
-// column add groups l, l + kLanes, ... in order, then the lanes in order.
-constexpr int kParamLanes = 4;
-
-__global__ __launch_bounds__(256) void layernorm_param_grads(const float* __restrict__ partial,
-                                                             float* __restrict__ dgamma,
-                                                             float* __restrict__ dbeta,
-                                                             int64_t groups, int64_t cols) {
-    __shared__ float sh[kParamLanes][256 / kParamLanes];
-    constexpr int kCols = 256 / kParamLanes;
-    const int l = threadIdx.x / kCols, cl = threadIdx.x % kCols;
-    const int64_t c2 = int64_t(blockIdx.x) * kCols + cl;  // in [0, 2 cols)
-    float acc = 0.0f;
-    if (c2 < 2 * cols) {
-        const float* p = partial + c2;
-        int64_t g = l;
-        for (; g + 15 * kParamLanes < groups; g += 16 * kParamLanes) {
-            float v[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = p[(g + u * kParamLanes) * 2 * cols];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) acc += v[u];
-        }
-        for (; g < groups; g += kParamLanes) acc += p[g * 2 * cols];
-    }
-    sh[l][cl] = acc;
-    __syncthreads();
-    if (l == 0 && c2 < 2 * cols) {
-        float sum = sh[0][cl];
-#pragma unroll
-        for (int k = 1; k < kParamLanes; ++k) sum += sh[k][cl];
-        if (c2 < cols) dgamma[c2] = sum;
-        else dbeta[c2 - cols] = sum;
     }
 }
 
@@ -921,6 +899,48 @@ bool rows_vec_ok(int64_t cols, std::initializer_list<const void*> ptrs) {
     for (const void* p : ptrs)
         if (!aligned16(p)) return false;
     return true;
+}
+
+// Groups of the large-problem form for rows x cols, or 0 when the shape takes
+// the small-problem kernels (fewer than 2^20 elements, or rows beyond 2048
+// columns). About 32 rows per group, at most 256 (one per CU); the group count
+// fixes the order of the dgamma / dbeta sums.
+int64_t ln_wide_groups(int64_t rows, int64_t cols) {
+    if (rows <= 0 || rows * cols < (int64_t(1) << 20) || cols > 2048) return 0;
+    return std::min<int64_t>(ceil_div(rows, 32), 256);
+}
+
+// Launches the large-problem row kernel for `groups` groups.
+int launch_ln_wide(const float* dy, const float* xhat, const float* gamma, const float* inv_std,
+                   float* dx, float* partial, int64_t groups, int64_t rows, int64_t cols,
+                   hipStream_t s) {
+    const bool vec = cols >= 256 && rows_vec_ok(cols, {dy, xhat, gamma, dx});
+    // Four rows ahead below the last-level cache size, one beyond it (2^25 elements).
+    const bool ahead = rows * cols < (int64_t(1) << 25);
+#define EHIP_LNW(V, VEC)                                                                           \
+    do {                                                                                           \
+        if (ahead && V <= 16)                                                                      \
+            EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 4>),           \
+                        dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma,        \
+                        inv_std, dx, partial, rows, cols);                                         \
+        else                                                                                       \
+            EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 1>),           \
+                        dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma,        \
+                        inv_std, dx, partial, rows, cols);                                         \
+    } while (0)
+    if (vec) {
+        if (cols <= 256) EHIP_LNW(4, true);
+        else if (cols <= 512) EHIP_LNW(8, true);
+        else if (cols <= 1024) EHIP_LNW(16, true);
+        else EHIP_LNW(32, true);
+    } else if (cols <= 64) EHIP_LNW(1, false);
+    else if (cols <= 128) EHIP_LNW(2, false);
+    else if (cols <= 256) EHIP_LNW(4, false);
+    else if (cols <= 512) EHIP_LNW(8, false);
+    else if (cols <= 1024) EHIP_LNW(16, false);
+    else EHIP_LNW(32, false);
+#undef EHIP_LNW
+    return EHIP_OK;
 }
 
 unsigned loop_grid(int64_t rows) { return unsigned(rows < 65536 ? rows : 65536); }
@@ -1111,47 +1131,17 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
     // A fixed number of row groups per shape, which fixes the order of the
     // dgamma / dbeta sums.
     const bool vec = cols >= 256 && rows_vec_ok(cols, {dy, xhat, gamma, dx});
-    if (rows * cols >= (int64_t(1) << 20) && cols <= 2048) {
-        // Large problems: groups of kLnWaves waves, about 32 rows per group,
-        // at most 256 groups (one per CU), and one launch for the parameter
-        // gradients.
-        int64_t groups = ceil_div(rows, 32);
-        if (groups > 256) groups = 256;
+    if (const int64_t groups = ln_wide_groups(rows, cols)) {
+        // Large problems: the row kernel with per-group partials, then their
+        // ordered sums (the same as the deferred form of
+        // ehip_layernorm_backward_partials_f32 followed by the job's reduction).
         float* partial =
             static_cast<float*>(scratch(size_t(groups) * 2 * size_t(cols) * sizeof(float)));
         if (partial == nullptr) return EHIP_ENOMEM;
-        // Beyond the last-level cache (2^25 elements and up) the rows stream with
-        // nontemporal loads and stores (73 % of HBM peak at 2^28 elements
-        // against 67 %; slower at 2^23).
-        const bool stream_nt = rows * cols >= (int64_t(1) << 25);
-#define EHIP_LNW(V, VEC)                                                                           \
-    do {                                                                                           \
-        if (stream_nt)                                                                             \
-            EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, true>),        \
-                        dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma,        \
-                        inv_std, dx, partial, rows, cols);                                         \
-        else                                                                                       \
-            EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC>),              \
-                        dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma,        \
-                        inv_std, dx, partial, rows, cols);                                         \
-    } while (0)
-        if (vec) {
-            if (cols <= 256) EHIP_LNW(4, true);
-            else if (cols <= 512) EHIP_LNW(8, true);
-            else if (cols <= 1024) EHIP_LNW(16, true);
-            else EHIP_LNW(32, true);
-        } else if (cols <= 64) EHIP_LNW(1, false);
-        else if (cols <= 128) EHIP_LNW(2, false);
-        else if (cols <= 256) EHIP_LNW(4, false);
-        else if (cols <= 512) EHIP_LNW(8, false);
-        else if (cols <= 1024) EHIP_LNW(16, false);
-        else EHIP_LNW(32, false);
-#undef EHIP_LNW
-        constexpr int kCols = 256 / kParamLanes;
-        EHIP_LAUNCH("layernorm_param_grads", layernorm_param_grads,
-                    dim3(unsigned(ceil_div(2 * cols, kCols))), dim3(256), 0, s, partial, dgamma,
-                    dbeta, groups, cols);
-        return EHIP_OK;
+        if (int rc = launch_ln_wide(dy, xhat, gamma, inv_std, dx, partial, groups, rows, cols, s))
+            return rc;
+        const ehip_conv_reduce_t job{partial, groups, cols, 1, dgamma, dbeta};
+        return ehip_conv_weight_reduce_f32(&job, 1, stream);
     }
     // Small problems: one wave per group of about 16 rows (at most 512 groups).
     int64_t groups = ceil_div(rows, 16);
@@ -1192,6 +1182,30 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
 #undef EHIP_LNB
 #undef EHIP_LNS
     return column_sums_pair(partial, groups, cols, 2 * cols, cols, dgamma, dbeta, s);
+}
+
+
+int64_t ehip_layernorm_backward_partials(int64_t rows, int64_t cols, int64_t* groups) {
+    const int64_t g = cols > 0 ? ln_wide_groups(rows, cols) : 0;
+    if (groups) *groups = g;
+    return g * 2 * (cols > 0 ? cols : 0);
+}
+
+int ehip_layernorm_backward_partials_f32(const float* dy, const float* xhat, const float* gamma,
+                                         const float* inv_std, float* dx, float* partials,
+                                         int64_t groups, int64_t rows, int64_t cols,
+                                         void* stream) {
+    EHIP_READY();
+    if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "layernorm_backward_partials: bad shape");
+    if (!dy || !xhat || !gamma || !inv_std || !dx || !partials)
+        return fail(EHIP_EINVAL, "layernorm_backward_partials: null pointer");
+    const int64_t want = ln_wide_groups(rows, cols);
+    if (want == 0 || groups != want)
+        return fail(EHIP_EINVAL,
+                    "layernorm_backward_partials: %lld groups for %lld x %lld (expected %lld)",
+                    (long long)groups, (long long)rows, (long long)cols, (long long)want);
+    return launch_ln_wide(dy, xhat, gamma, inv_std, dx, partials, groups, rows, cols,
+                          as_stream(stream));
 }
 
 }  // extern "C"

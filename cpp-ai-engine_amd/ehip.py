@@ -136,6 +136,8 @@ _SIGS = {
     "ehip_softmax_backward_scaled_f32": [_vp, _vp, _vp, _i64, _i64, _f, _vp],
     "ehip_layernorm_f32": [_vp] * 6 + [_i64, _i64, _f, _vp],
     "ehip_layernorm_backward_f32": [_vp] * 7 + [_i64, _i64, _vp],
+    "ehip_layernorm_backward_partials": [_i64, _i64, C.POINTER(_i64)],
+    "ehip_layernorm_backward_partials_f32": [_vp] * 6 + [_i64, _i64, _i64, _vp],
     "ehip_cross_entropy_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "ehip_cross_entropy_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
     "ehip_cross_entropy_fused_supported": [_i64, _i64],
@@ -145,6 +147,7 @@ _SIGS = {
 }
 _RESTYPES = {"ehip_last_error": C.c_char_p, "ehip_kernels_launched": C.c_uint64,
              "ehip_conv2d_relu_maxpool_partials": C.c_int64,
+             "ehip_layernorm_backward_partials": C.c_int64,
              "ehip_kernels_failed": C.c_uint64, "ehip_reset_counters": None,
              "ehip_fail_launch_after": None,
              "ehip_set_enabled": None, "ehip_transfer_stats": None,
@@ -573,6 +576,23 @@ class Backend:
                                                      self.p(db), dy.numel() // d, d,
                                                      self.stream()), "layernorm_backward")
         return dx, dg, db
+
+    def layernorm_backward_partials(self, dy, xhat, gamma, inv, groups=None):
+        """dx and the per-group dgamma / dbeta partials ([groups][d][2]) of the deferred
+        LayerNorm backward; returns (dx, partials, groups), or None when the shape is summed
+        in one call only. `groups` overrides the count (to test the refusal)."""
+        d = dy.shape[-1]
+        rows = dy.numel() // d
+        g = _i64(0)
+        n = self.lib.ehip_layernorm_backward_partials(rows, d, C.byref(g))
+        if n == 0 and groups is None:
+            return None
+        dx, part = self.f32(dy.shape), self.f32((max(n, 1),))
+        use = g.value if groups is None else groups
+        self.ok(self.lib.ehip_layernorm_backward_partials_f32(
+            self.p(dy), self.p(xhat), self.p(gamma), self.p(inv), self.p(dx), self.p(part), use,
+            rows, d, self.stream()), "layernorm_backward_partials")
+        return dx, part, g.value
 
     def cross_entropy(self, logits, targets):
         rows, cols = logits.shape

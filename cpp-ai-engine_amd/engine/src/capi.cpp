@@ -630,6 +630,8 @@ int eng_repeat_gemm(int trans_a, int trans_b, int64_t batch, int64_t m, int64_t 
 //   4 ehip_softmax_backward_f32   p: y g dx                       n: rows cols
 //   5 ehip_maxpool_f32            p: x y argmax                   w: the window
 //   6 ehip_maxpool_backward_f32   p: argmax g dx                  w: the window
+//   7 ehip_layernorm_backward_partials_f32 p: dy xhat gamma inv dx partials
+//                                            n: rows cols groups
 int eng_repeat_bandwidth(int op, void* const* p, const int64_t* n, float f, const ehip_window_t* w,
                          void* stream, int reps) {
     return guarded([&] {
@@ -648,6 +650,9 @@ int eng_repeat_bandwidth(int op, void* const* p, const int64_t* n, float f, cons
                         break;
                 case 6: rc = ehip_maxpool_backward_f32(static_cast<const int32_t*>(p[0]), F(1),
                                                        F(2), w, stream); break;
+                case 7: rc = ehip_layernorm_backward_partials_f32(F(0), F(1), F(2), F(3), F(4),
+                                                                  F(5), n[2], n[0], n[1], stream);
+                        break;
                 default: throw std::invalid_argument("repeat_bandwidth: unknown op");
             }
             engine::hip::check(rc, "repeat_bandwidth");

@@ -1,6 +1,7 @@
 // deferred.cpp -- gradient work queued during backward: the weight-gradient
-// sums of fused convolution blocks, reduced for every layer in one launch
-// (ehip_conv_weight_reduce_f32) instead of one launch per layer.
+// sums of fused convolution blocks and the parameter sums of large LayerNorms,
+// reduced for every queued node in one launch (ehip_conv_weight_reduce_f32)
+// instead of one launch per node.
 #include <memory>
 #include <utility>
 #include <vector>
@@ -43,6 +44,12 @@ void defer_conv_output(const Tensor& param, const Tensor& grad) {
 }
 
 bool deferred_pending() { return !g_pending.jobs.empty(); }
+
+bool deferred_writes(const Storage& s) {
+    for (const auto& out : g_pending.keep.outputs)
+        if (out.second.same_buffer(s)) return true;
+    return false;
+}
 
 void flush_deferred() {
     if (g_pending.jobs.empty()) return;

@@ -78,11 +78,12 @@ std::shared_ptr<const RowGather> make_row_gather(const std::vector<size_t>& indi
 Tensor gather_rows(const Tensor& table, const std::shared_ptr<const RowGather>& g);
 
 // Gradient work queued during backward: the weight-gradient sums of fused
-// convolution blocks (deferred.cpp). The queue is flushed -- one launch for
-// every queued layer -- before anything can read a queued gradient:
-// Tensor::grad(), zero_grad(), the start of autograd::backward, add_grad when
-// it accumulates into an existing gradient, and a product that adds into a
-// gradient in place; Adam::step instead takes the jobs into its own launch. A
+// convolution blocks and the dgamma / dbeta sums of large LayerNorms
+// (deferred.cpp). The queue is flushed -- one launch for every queued job --
+// before anything can read or change a queued gradient: Tensor::grad(),
+// zero_grad(), the start of autograd::backward, add_grad when it accumulates
+// into or from a buffer a queued job writes, and a product that adds in place
+// into such a buffer; Adam::step instead takes the jobs into its own launch. A
 // gradient may be queued only when add_grad will adopt its buffer
 // (grad_adoptable).
 //
@@ -103,6 +104,8 @@ struct DeferredKeep {
 void defer_conv_reduce(const ehip_conv_reduce_t& job, const Tensor& partials);
 void defer_conv_output(const Tensor& param, const Tensor& grad);
 bool deferred_pending();
+// True when a queued job writes the buffer of `s` (a registered output).
+bool deferred_writes(const Storage& s);
 void flush_deferred();
 void drop_deferred();
 // Moves the queued jobs (and the buffers they touch) to the caller, which must

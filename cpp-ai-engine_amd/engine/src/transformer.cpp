@@ -22,7 +22,11 @@ LayerNorm::LayerNorm(size_t normalized_size, float eps)
 }
 
 // One fused node: the forward saves xhat and inv_std, the backward produces dx,
-// dgamma and dbeta in two kernels (src/transformer.cpp:82-179).
+// dgamma and dbeta in two kernels (src/transformer.cpp:82-179). With fused
+// nodes, a large LayerNorm whose dgamma and dbeta add_grad will adopt writes
+// only dx and its per-group partials during backward; the sums of every such
+// node (and of the fused convolution blocks) run in one launch afterwards, or
+// inside Adam's, with the same bits as the two-kernel backward.
 Tensor LayerNorm::forward(const Tensor& input) {
     if (input.ndim() < 1 || input.shape().back() != normalized_size_)
         throw std::invalid_argument("LayerNorm of size " + std::to_string(normalized_size_) +
@@ -46,6 +50,28 @@ Tensor LayerNorm::forward(const Tensor& input) {
         Tensor dgamma(gamma_copy.shape(), 0.0f, false);
         Tensor dbeta(beta_copy.shape(), 0.0f, false);
         Tensor dX(input_copy.shape(), 0.0f, false);
+        int64_t groups = 0;
+        const int64_t nparts =
+            nn::fused_nodes() && gamma_copy.requires_grad() && beta_copy.requires_grad() &&
+                    detail::grad_adoptable(gamma_copy) && detail::grad_adoptable(beta_copy)
+                ? ehip_layernorm_backward_partials(int64_t(rows), int64_t(D), &groups)
+                : 0;
+        if (nparts > 0) {
+            Tensor part({size_t(nparts)}, 0.0f, false);
+            hip::check(ehip_layernorm_backward_partials_f32(
+                           dptr(g), dptr(xhat), dptr(gamma_copy), dptr(inv_std), dout(dX),
+                           dout(part), groups, int64_t(rows), int64_t(D), nullptr),
+                       "layernorm backward");
+            const ehip_conv_reduce_t job{dptr(part), groups, int64_t(D), 1, dout(dgamma),
+                                         dout(dbeta)};
+            detail::defer_conv_reduce(job, part);
+            if (input_copy.requires_grad()) input_copy.add_grad(dX);
+            gamma_copy.add_grad(dgamma);
+            beta_copy.add_grad(dbeta);
+            detail::defer_conv_output(gamma_copy, dgamma);
+            detail::defer_conv_output(beta_copy, dbeta);
+            return;
+        }
         hip::check(ehip_layernorm_backward_f32(dptr(g), dptr(xhat), dptr(gamma_copy),
                                                dptr(inv_std), dout(dX), dout(dgamma), dout(dbeta),
                                                int64_t(rows), int64_t(D), nullptr),

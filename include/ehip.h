@@ -553,6 +553,26 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
                                 const float* inv_std, float* dx, float* dgamma, float* dbeta,
                                 int64_t rows, int64_t cols, void* stream);
 
+/* The LayerNorm backward with its parameter sums left for later, for callers
+ * that run several of them into one reduction (the engine sums every
+ * LayerNorm's dgamma / dbeta of a backward in the launch of the conv weight
+ * sums, or inside Adam's). ehip_layernorm_backward_partials returns the floats
+ * of the partial buffer for rows x cols and the group count through *groups,
+ * or 0 when that shape is summed in one call only (fewer than 2^20 elements,
+ * or more than 2048 columns). ehip_layernorm_backward_partials_f32 writes dx
+ * and partials[group][c][2] = (dgamma, dbeta) of each row group; the job
+ * {partials, groups, out_channels = cols, k = 1, dweight = dgamma,
+ * dbias = dbeta} of ehip_conv_weight_reduce_f32 or ehip_adam_multi_reduce_f32
+ * then forms dgamma and dbeta with the same bits as
+ * ehip_layernorm_backward_f32. Refuses a group count other than the one
+ * returned. The backward of the reference's LayerNorm node
+ * (src/transformer.cpp:123-150) with the parameter folds deferred. */
+int64_t ehip_layernorm_backward_partials(int64_t rows, int64_t cols, int64_t* groups);
+int ehip_layernorm_backward_partials_f32(const float* dy, const float* xhat, const float* gamma,
+                                         const float* inv_std, float* dx, float* partials,
+                                         int64_t groups, int64_t rows, int64_t cols,
+                                         void* stream);
+
 /* Fused log-softmax + NLL over (rows, cols) logits with int32 targets: probs
  * receives the row softmax and loss[0] the mean of -log p[target] (summed in
  * double over a fixed partition). A target outside [0, cols) makes loss NaN.

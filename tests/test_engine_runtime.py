@@ -213,3 +213,28 @@ def test_wide_conv2d_im2col_gemm_path(eng, n, c, hw, oc, k, stride, pad):
     ref_close(dx, wdx, k_tol(oc * k * k), "dx")
     ref_close(dw, wdw, k_tol(n * oh * oh), "dw")
     ref_close(db, wdb, k_tol(n * oh * oh), "db")
+
+
+# ------------------------------------------------------------------ queued LayerNorm sums
+
+@pytest.mark.parametrize("rows,d", [(1024, 1024), (2048, 1000)])
+def test_layernorm_queued_sums_match_one_call(eng, hip, rows, d):
+    """A LayerNorm of at least 2^20 elements queues its dgamma / dbeta sums during backward
+    (only dx and the group partials are computed there); reading the gradients runs the
+    queue. The values are the one-call backward's, bit for bit."""
+    print_case("engine layernorm queued", rows, d)
+    import torch
+    r = np.random.default_rng(rows + d)
+    x = (r.standard_normal((rows, d)) * 2 + 0.5).astype(np.float32)
+    gamma = r.standard_normal(d).astype(np.float32)
+    beta = r.standard_normal(d).astype(np.float32)
+    dy = r.standard_normal((rows, d)).astype(np.float32)
+    assert hip.lib.ehip_layernorm_backward_partials(rows, d, None) > 0
+    y, dx, dg, db = eng.layernorm_fwd_bwd(x, gamma, beta, dy)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    out, xhat, inv = hip.layernorm(dev(x), dev(gamma), dev(beta))
+    wdx, wdg, wdb = hip.layernorm_backward(dev(dy), xhat, dev(gamma), inv)
+    exact(y, out.cpu().numpy(), "y")
+    exact(dx, wdx.cpu().numpy(), "dx")
+    exact(dg, wdg.cpu().numpy(), "dgamma")
+    exact(db, wdb.cpu().numpy(), "dbeta")

@@ -963,6 +963,49 @@ def test_layernorm_backward_split_rows_match_serial(hip, orc, d):
     ref_close(host(db_s), wdb, k_tol(2048), "dbeta")
 
 
+@pytest.mark.parametrize("rows,d", [(1024, 1024), (8192, 1024), (700, 2048), (1100, 999),
+                                    (4097, 256)])
+def test_layernorm_backward_partials_match_one_call(hip, orc, rows, d):
+    """The deferred LayerNorm backward (dx and per-group partials now, the dgamma / dbeta
+    sums later as a weight-reduce job with one weight per column) gives the bits of the
+    one-call backward, which takes the same row kernel and reduction; the shapes cover
+    four rows in flight (8192 x 1024), one (700 x 2048, 32 columns a lane), an unaligned
+    width (999) and a row count that leaves the last group short. The reduction is also
+    checked against the oracle, and a wrong group count is refused."""
+    print_case("layernorm partials", rows, d)
+    r = rng(rows + 3 * d)
+    xh, dy = randn(r, rows, d), randn(r, rows, d)
+    gamma = randn(r, d)
+    inv = (np.abs(randn(r, rows)) + 0.5).astype(np.float32)
+    one = hip.layernorm_backward(dev(dy), dev(xh), dev(gamma), dev(inv))
+    got = hip.layernorm_backward_partials(dev(dy), dev(xh), dev(gamma), dev(inv))
+    assert got is not None, "a shape of at least 2^20 elements takes the deferred form"
+    dx, part, groups = got
+    [(dg, db)] = hip.conv_weight_reduce([(part, groups, (d, 1), True)])
+    exact(host(dx), host(one[0]), "dx")
+    exact(host(dg).reshape(d), host(one[1]), "dgamma")
+    exact(host(db), host(one[2]), "dbeta")
+    wdx, wdg, wdb = orc.layernorm_backward(dy, xh, gamma, inv)
+    ref_close(host(dx), wdx, k_tol(d), "dx")
+    ref_close(host(dg).reshape(d), wdg, k_tol(rows), "dgamma")
+    ref_close(host(db), wdb, k_tol(rows), "dbeta")
+    with pytest.raises(RuntimeError, match="groups"):
+        hip.layernorm_backward_partials(dev(dy), dev(xh), dev(gamma), dev(inv), groups=groups + 1)
+
+
+def test_layernorm_backward_partials_small_shapes_refused(hip):
+    """Shapes under 2^20 elements (cfg3's 2048 x 96) or wider than 2048 columns are summed
+    in one call only: the size query returns 0 and the entry point refuses them."""
+    print_case("layernorm partials small")
+    for rows, d in [(2048, 96), (600, 4096)]:
+        x = dev(np.ones((rows, d), np.float32))
+        g = dev(np.ones(d, np.float32))
+        inv = dev(np.ones(rows, np.float32))
+        assert hip.layernorm_backward_partials(x, x, g, inv) is None
+        with pytest.raises(RuntimeError, match="groups"):
+            hip.layernorm_backward_partials(x, x, g, inv, groups=1)
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 10), (2048, 121), (8, 5), (16, 32000), (3, 40000),
                                        (100, 256), (600, 32000), (9, 1002), (1024, 128),
                                        (1000, 100), (1025, 10), (1, 1)])
