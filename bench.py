@@ -562,15 +562,37 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
 
 def kernel_only(eng, hip, timer, torch):
     """For counter runs: the dominant kernel's leg (the six weight-gradient products of a
-    cfg 5 block, launched as in dominant_kernel), then 100 launches of the
+    cfg 5 block, launched as in dominant_kernel), the cfg 2 step's dominant launch pair
+    (cnn_dominant_kernel), LayerNorm forward and the engine's LayerNorm backward row kernel
+    at cfg 5's 8192 x 1024 (100 launches each), then 100 launches of the
     gradient-initialise kernel over 16 Mi floats (reads 64 MiB, writes 64 MiB), the copy of
     known size that scales FETCH_SIZE / WRITE_SIZE to bytes."""
+    import ctypes
     roof = dominant_kernel(eng, timer, torch)
+    cnn = cnn_dominant_kernel(eng, hip, timer, torch)
+    r = torch.Generator(device="cuda").manual_seed(8)
+    rows, d = 8192, 1024
+    x = torch.randn(rows, d, device="cuda", generator=r)
+    gam, bet = torch.randn(d, device="cuda", generator=r), torch.randn(d, device="cuda", generator=r)
+    y, xh, inv = hip.layernorm(x, gam, bet)
+    ln = timer.time_batch(lambda q: eng.repeat_bandwidth(q, "layernorm", [x, gam, bet, y, xh, inv],
+                                                         (rows, d), 1e-5), 100, 3)
+    groups = ctypes.c_int64(0)
+    part = torch.empty(hip.lib.ehip_layernorm_backward_partials(rows, d, ctypes.byref(groups)),
+                       device="cuda")
+    dx = torch.empty_like(x)
+    lnb = timer.time_batch(lambda q: eng.repeat_bandwidth(
+        q, "layernorm_backward_rows", [x, xh, gam, inv, dx, part], (rows, d, groups.value)),
+        100, 3)
+    del x, y, xh, inv, dx, part
     n = 1 << 24
     src = torch.randn(n, device="cuda")
     dst = torch.empty(n, device="cuda")
     sec = timer.time(lambda: hip.accumulate_grad(dst, src, True), 100, 0)
-    print(json.dumps({"dominant": roof, "copy_64MiB_us": round(sec * 1e6, 3)}), flush=True)
+    print(json.dumps({"dominant": roof, "cnn_dominant": cnn,
+                      "layernorm_8192x1024_us": round(ln * 1e6, 3),
+                      "layernorm_backward_rows_8192x1024_us": round(lnb * 1e6, 3),
+                      "copy_64MiB_us": round(sec * 1e6, 3)}), flush=True)
 
 
 def main():

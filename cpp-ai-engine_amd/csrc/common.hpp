@@ -84,6 +84,18 @@ __device__ __forceinline__ bool partial_sums(const float* __restrict__ partial, 
     return true;
 }
 
+// Block order of a partial_sums reduction of `nblocks` blocks: groups of 16
+// are permuted so that the blocks computing outputs 2j and 2j + 1 (with 16
+// outputs a block, the two 64-byte halves of the same 128-byte lines of every
+// chunk) run on one XCD -- the dispatcher hands consecutive blocks to the
+// eight XCDs in turn, so local blocks p and p + 8 share one -- and each line
+// comes into one L2 once instead of into two. A last, incomplete group keeps
+// its order. The sums do not depend on which block computes them.
+__device__ __forceinline__ int xcd_paired_block(int p, int nblocks) {
+    if ((p | 15) >= nblocks) return p;
+    return (p & ~15) | ((p & 7) << 1) | ((p >> 3) & 1);
+}
+
 // Lanes per output of partial_sums: about one per eight chunks, at most 16, so
 // that a block still reads 16 consecutive outputs (64 bytes) of each chunk
 // (32 lanes measured no faster and fetched twice the bytes).

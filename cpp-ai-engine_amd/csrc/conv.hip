@@ -1378,7 +1378,9 @@ __device__ __forceinline__ void weight_reduce_block(const float* __restrict__ pa
                                                     int chunks, int rl, int bx, float* lanes) {
     float sum;
     int o;
-    if (partial_sums(partial, cout * (k + 1), chunks, rl, bx, lanes, sum, o)) {
+    const int nb = (cout * (k + 1) + 256 / rl - 1) / (256 / rl);
+    if (partial_sums(partial, cout * (k + 1), chunks, rl, xcd_paired_block(bx, nb), lanes, sum,
+                     o)) {
         const int co = o / (k + 1), kk = o % (k + 1);
         if (kk < k)
             dw[int64_t(co) * k + kk] = sum;

@@ -520,8 +520,9 @@ __global__ __launch_bounds__(kThreads) void adam_multi_reduce(ReduceAdamBatch rb
         const ReduceAdamJob& r = rb.job[j];
         float sum;
         int o;
-        if (!partial_sums(r.partial, r.cout * (r.k + 1), r.chunks, r.rl,
-                          int(blockIdx.x) - r.first, lanes, sum, o))
+        const int outs = r.cout * (r.k + 1), nb = (outs + 256 / r.rl - 1) / (256 / r.rl);
+        if (!partial_sums(r.partial, outs, r.chunks, r.rl,
+                          xcd_paired_block(int(blockIdx.x) - r.first, nb), lanes, sum, o))
             return;
         const int co = o / (r.k + 1), kk = o % (r.k + 1);
         const int which = kk < r.k ? 0 : 1;
