@@ -137,6 +137,7 @@ _SIGS = {
     "ehip_layernorm_f32": [_vp] * 6 + [_i64, _i64, _f, _vp],
     "ehip_layernorm_backward_f32": [_vp] * 7 + [_i64, _i64, _vp],
     "ehip_layernorm_backward_partials": [_i64, _i64, C.POINTER(_i64)],
+    "ehip_linear_bias_from_dw": [_i],
     "ehip_layernorm_backward_partials_f32": [_vp] * 6 + [_i64, _i64, _i64, _vp],
     "ehip_cross_entropy_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "ehip_cross_entropy_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],

@@ -25,6 +25,19 @@ namespace nn {
 void set_fused_nodes(bool on);
 bool fused_nodes();
 
+// Bias gradients from the weight-gradient product, on by default: Linear and
+// the feed-forward node take db of a mid-sized layer (more than 64 rows, dY of
+// at most 2^21 elements) from the column sums of dY that the dW = X^T dY
+// product forms from the tiles it stages, instead of a separate two-pass
+// column sum (ehip_linear_backward_f32). The sums are the same mathematically,
+// added in another order; the char-Transformer's 10-step trajectory stays
+// within 3e-6 of the reference's loss either way, and the step gets faster
+// (two launch-bound launches fewer per layer). Off, every bias gradient takes
+// the separate column sum. Process-wide (it switches the library's setting);
+// set it between steps.
+void set_fused_bias_grad(bool on);
+bool fused_bias_grad();
+
 class Module {
 public:
     virtual ~Module() = default;

@@ -429,6 +429,12 @@ int eng_set_fused_nodes(int on) {
     return was ? 1 : 0;
 }
 
+int eng_set_fused_bias_grad(int on) {
+    const bool was = nn::fused_bias_grad();
+    nn::set_fused_bias_grad(on != 0);
+    return was ? 1 : 0;
+}
+
 int eng_linear_fwd_bwd(const float* x, int64_t rows, int64_t in, int64_t out, const float* w,
                        const float* bias, const float* dy, float* y, float* dx, float* dw,
                        float* db) {

@@ -18,6 +18,8 @@ std::atomic<bool> g_fused_nodes{true};
 
 void set_fused_nodes(bool on) { g_fused_nodes.store(on); }
 bool fused_nodes() { return g_fused_nodes.load(); }
+void set_fused_bias_grad(bool on) { ehip_linear_bias_from_dw(on ? 1 : 0); }
+bool fused_bias_grad() { return ehip_linear_bias_from_dw(-1) != 0; }
 
 
 using namespace detail;

@@ -440,8 +440,21 @@ Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, co
     attach(out, {x.get_impl(), w1.get_impl(), b1.get_impl(), w2.get_impl(), b2.get_impl()},
            [xc, w1c, b1c, w2c, b2c, h, M, D, F, N](const Tensor& g) mutable {
                // The composed graph's order: second bias, second product (h,
-               // then w2), ReLU, first bias, first product (x, then w1).
-               if (b2c.requires_grad()) b2c.add_grad(reduce_to(g, b2c));
+               // then w2), ReLU, first bias, first product (x, then w1). A bias
+               // and its weight both trained take one ehip_linear_backward_f32
+               // call (db from the dW product where that pays, as in Linear).
+               Tensor dw2;
+               if (b2c.requires_grad() && w2c.requires_grad() && F > 0 && N > 0) {
+                   dw2 = empty_2d(F, N);
+                   Tensor db2(b2c.shape(), 0.0f, false);
+                   hip::check(ehip_linear_backward_f32(dptr(h), dptr(w2c), dptr(g), nullptr,
+                                                       dout(dw2), dout(db2), int64_t(M),
+                                                       int64_t(F), int64_t(N), nullptr),
+                              "feed-forward dw2 and db2");
+                   b2c.add_grad(db2);
+               } else if (b2c.requires_grad()) {
+                   b2c.add_grad(reduce_to(g, b2c));
+               }
                const bool need_dh = xc.requires_grad() || w1c.requires_grad() || b1c.requires_grad();
                Tensor dh;
                if (need_dh) {  // g w2^T
@@ -451,10 +464,12 @@ Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, co
                                "feed-forward dh");
                }
                if (w2c.requires_grad()) {  // h^T g
-                   Tensor dw2 = empty_2d(F, N);
-                   if (F > 0 && N > 0)
-                       gemm_2d(true, false, F, N, M, dptr(h), dptr(g), dout(dw2), nullptr, false,
-                               "feed-forward dw2");
+                   if (!dw2.get_impl()) {
+                       dw2 = empty_2d(F, N);
+                       if (F > 0 && N > 0)
+                           gemm_2d(true, false, F, N, M, dptr(h), dptr(g), dout(dw2), nullptr,
+                                   false, "feed-forward dw2");
+                   }
                    w2c.add_grad(dw2);
                }
                if (!need_dh) return;
@@ -466,7 +481,18 @@ Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, co
                                                      int64_t(M * F), nullptr),
                               "feed-forward relu backward");
                dh = Tensor();
-               if (b1c.requires_grad()) b1c.add_grad(reduce_to(dpre, b1c));
+               Tensor dw1;
+               if (b1c.requires_grad() && w1c.requires_grad() && D > 0 && F > 0) {
+                   dw1 = empty_2d(D, F);
+                   Tensor db1(b1c.shape(), 0.0f, false);
+                   hip::check(ehip_linear_backward_f32(dptr(xc), dptr(w1c), dptr(dpre), nullptr,
+                                                       dout(dw1), dout(db1), int64_t(M),
+                                                       int64_t(D), int64_t(F), nullptr),
+                              "feed-forward dw1 and db1");
+                   b1c.add_grad(db1);
+               } else if (b1c.requires_grad()) {
+                   b1c.add_grad(reduce_to(dpre, b1c));
+               }
                if (xc.requires_grad()) {  // dpre w1^T
                    Tensor dx = empty_2d(M, D);
                    if (M > 0 && D > 0)
@@ -475,10 +501,12 @@ Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, co
                    xc.add_grad(dx);
                }
                if (w1c.requires_grad()) {  // x^T dpre
-                   Tensor dw1 = empty_2d(D, F);
-                   if (D > 0 && F > 0)
-                       gemm_2d(true, false, D, F, M, dptr(xc), dptr(dpre), dout(dw1), nullptr,
-                               false, "feed-forward dw1");
+                   if (!dw1.get_impl()) {
+                       dw1 = empty_2d(D, F);
+                       if (D > 0 && F > 0)
+                           gemm_2d(true, false, D, F, M, dptr(xc), dptr(dpre), dout(dw1), nullptr,
+                                   false, "feed-forward dw1");
+                   }
                    w1c.add_grad(dw1);
                }
            });

@@ -338,6 +338,11 @@ class Engine:
         returns the previous setting."""
         return bool(self.lib.eng_set_fused_nodes(int(bool(on))))
 
+    def set_fused_bias_grad(self, on):
+        """Bias gradients of mid-sized layers from the weight-gradient products' column sums
+        (default on) or the separate column sum; returns the previous setting."""
+        return bool(self.lib.eng_set_fused_bias_grad(int(bool(on))))
+
     def block_num_params(self, d, heads, ff):
         return self.lib.eng_block_num_params(_i64(d), _i64(heads), _i64(ff))
 

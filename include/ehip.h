@@ -238,13 +238,25 @@ int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream);
  * out), dy (rows, out): dx = dy . w^T, dw = x^T . dy, db = the column sums of
  * dy -- the matmul backward and the broadcast add's backward through
  * fold_leading (src/tensor_ops.cpp:565-586, 81-102; src/tensor_detail.hpp:
- * 182-206). Each equals what ehip_gemm_f32 / ehip_sum_axis_f32 compute for it
- * bit for bit; when all requested parts are small (thread-per-output
- * products, a serial column sum) they run in one launch. dx, dw and db may
- * each be NULL. */
+ * 182-206). dx and dw equal what ehip_gemm_f32 computes for them bit for
+ * bit; when all requested parts are small (thread-per-output products, a
+ * serial column sum) they run in one launch. db is ehip_sum_axis_f32's, except
+ * for mid-sized layers (more than 64 rows, dy of at most 2^21 elements, fewer
+ * than 16384 columns, dw requested too, and a dw product that takes staged
+ * MFMA tiles either way), where it is the column sums of dy that the dw
+ * product forms from the tiles it stages (ehip_gemm_ex_f32's colsum_b): the
+ * same sums in another order, two launches fewer. dx, dw and db may each be
+ * NULL. */
 int ehip_linear_backward_f32(const float* x, const float* w, const float* dy, float* dx,
                              float* dw, float* db, int64_t rows, int64_t in, int64_t out,
                              void* stream);
+
+/* Switches the mid-sized-layer bias gradients of ehip_linear_backward_f32
+ * between the dw product's column sums (on = 1, the default) and the separate
+ * column sum (on = 0); on < 0 only queries. Returns the previous setting.
+ * Process-wide; no counterpart in the reference (its fold is always separate,
+ * src/tensor_detail.hpp:196-204). */
+int ehip_linear_bias_from_dw(int on);
 
 /* --------------------------------------------------------- element-wise */
 

@@ -225,8 +225,13 @@ def test_mha_fused_equals_composed(eng, orc, b, s, d, heads, causal):
     x, dy = randn(r, b, s, d), randn(r, b, s, d)
     params = mha_params(r, d)
     mask = np.triu(np.full((s, s), -1e9, np.float32), 1) if causal else None
-    fused = eng.mha_fwd_bwd(x, heads, params, dy, mask=mask, fuse=True, weights=True)
-    comp = eng.mha_fwd_bwd(x, heads, params, dy, mask=mask, fuse=False, weights=True)
+    # Bias gradients from the separate column sums on both sides (see both_graphs).
+    prev_db = eng.set_fused_bias_grad(False)
+    try:
+        fused = eng.mha_fwd_bwd(x, heads, params, dy, mask=mask, fuse=True, weights=True)
+        comp = eng.mha_fwd_bwd(x, heads, params, dy, mask=mask, fuse=False, weights=True)
+    finally:
+        eng.set_fused_bias_grad(prev_db)
     for got, want, what in zip(fused, comp, ("y", "dx", "dparams", "weights")):
         exact(got, want, f"fused {what}")
     # And against the oracle composition (the reference's CPU arithmetic).
@@ -285,13 +290,19 @@ def test_relu_epilogue_signs(hip):
 # ------------------------------------------------------- fused vs composed engine graph
 
 def both_graphs(eng, fn):
+    """fn() with fused nodes, then with the reference's node-by-node graph. Both take every
+    bias gradient from the separate column sum (the composed graph's bias-add node always
+    does): node fusion itself is what must not move a bit; the mid-sized layers' bias sums
+    from the dW products, another order, are tested against the separate sums elsewhere."""
     prev = eng.set_fused_nodes(True)
+    prev_db = eng.set_fused_bias_grad(False)
     try:
         fused = fn()
         eng.set_fused_nodes(False)
         comp = fn()
     finally:
         eng.set_fused_nodes(prev)
+        eng.set_fused_bias_grad(prev_db)
     return fused, comp
 
 
@@ -427,16 +438,46 @@ def test_colsum_refusals_and_k_zero(hip):
 @pytest.mark.parametrize("want", [("dx", "dw", "db"), ("dw", "db"), ("dx",)])
 def test_linear_backward_matches_separate_calls(hip, rows, inp, out, want):
     """ehip_linear_backward_f32 (one launch for small layers) equals the separate
-    products and column sum bit for bit."""
+    products and column sum bit for bit; a mid-sized layer's db (more than 64 rows, dy of
+    at most 2^21 elements) is the column sum the dw product forms from its staged tiles
+    (ehip_gemm_ex_f32's colsum_b) while ehip_linear_bias_from_dw is on (the default), and
+    the separate column sum with it off."""
     print_case("linear_backward", rows, inp, out, want)
     r = np.random.default_rng(rows + inp + out + len(want))
     x = randn(r, rows, inp)
     x[x < -1.0] = 0.0  # zero-skip terms
     x, w, dy = dev(x), dev(randn(r, inp, out)), dev(randn(r, rows, out))
-    dx, dw, db = hip.linear_backward(x, w, dy, want)
-    if "dx" in want:
-        exact(host(dx), host(hip.gemm(dy, w, trans_b=True)), "dx")
-    if "dw" in want:
-        exact(host(dw), host(hip.gemm(x, dy, trans_a=True)), "dw")
-    if "db" in want:
-        exact(host(db), host(hip.sum_axis(dy, 1, rows, out)), "db")
+    from_dw = None  # asked from the library: the rule also depends on the dw product's plan
+    for on in (1, 0):
+        prev = hip.lib.ehip_linear_bias_from_dw(on)
+        try:
+            dx, dw, db = hip.linear_backward(x, w, dy, want)
+        finally:
+            hip.lib.ehip_linear_bias_from_dw(prev)
+        if "dx" in want:
+            exact(host(dx), host(hip.gemm(dy, w, trans_b=True)), "dx")
+        if "dw" in want:
+            exact(host(dw), host(hip.gemm(x, dy, trans_a=True)), "dw")
+        if "db" not in want:
+            continue
+        if on and "dw" in want:
+            # Where the column sums came from: equal to the separate sum, or to the dw
+            # product's staged sums (which must then differ somewhere for these inputs).
+            sep = host(hip.sum_axis(dy, 1, rows, out))
+            from_dw = not np.array_equal(host(db), sep)
+            if "db" in want and (rows, inp, out) == (2048, 96, 384):
+                assert from_dw, "cfg3's feed-forward layer takes db from its dw product"
+            if rows <= 64:
+                assert not from_dw, "up to 64 rows db is the serial column sum"
+        if on and from_dw:
+            cw, cs = hip.f32((inp, out)), hip.f32((out,))
+            d = desc(hip, True, False, 1, 1, inp, out, rows, x, inp, 0, 0, dy, out, 0, 0, cw, out,
+                     0, 0)
+            d.colsum_b = hip.p(cs)
+            hip.gemm_ex(d)
+            exact(host(db), host(cs), "db from the dw product")
+            exact(host(dw), host(cw), "dw of the column-sum product")
+            ref_close(host(db), host(hip.sum_axis(dy, 1, rows, out)).astype(np.float64),
+                      k_tol(rows), "db against the separate sum")
+        else:
+            exact(host(db), host(hip.sum_axis(dy, 1, rows, out)), "db")

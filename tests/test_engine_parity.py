@@ -405,6 +405,20 @@ def test_charlm_training_trajectory(eng, orc, cpu):
     lm_trajectory(eng, orc, cpu, (121, 96, 4, 384, 2, 32, 64), 3, 10, False, "charlm")
 
 
+def test_charlm_trajectory_separate_bias_sums(eng, orc, cpu):
+    """The cfg 3 trajectory with every bias gradient from the separate column sum
+    (nn::set_fused_bias_grad(false)) instead of the default, where the mid-sized layers take
+    theirs from the weight-gradient products' column sums: both orders hold the per-step
+    losses within 1e-5 relative and pass the gradient and update checks."""
+    print_case("charlm train cfg3, separate bias sums")
+    prev = eng.set_fused_bias_grad(False)
+    try:
+        lm_trajectory(eng, orc, cpu, (121, 96, 4, 384, 2, 32, 64), 3, 10, False,
+                      "charlm separate-db")
+    finally:
+        eng.set_fused_bias_grad(prev)
+
+
 def test_transformer_medium_trajectory(eng, orc, cpu):
     """A deeper, wider stack than cfg 3 (4 pre-LN blocks, d 256, 8 heads, FFN 1024, context
     128, vocab 256, batch 8), so the larger GEMM tiles and longer reductions run inside a
