@@ -488,6 +488,7 @@ int gemm_run(const ehip_gemm_ex_t& d, hipStream_t s, const Workspace& wsp = Work
     g.lda = d.lda;
     g.ldb = d.ldb;
     g.ldc = d.ldc;
+    g.causal = d.causal;
     g.stride_a = d.stride_a;
     g.stride_b = d.stride_b;
     g.stride_c = d.stride_c;
@@ -546,6 +547,7 @@ int check_desc(const ehip_gemm_ex_t& d) {
         return fail(EHIP_EINVAL, "gemm: bad addend geometry");
     if (d.colsum_b && (d.batch != 1 || d.trans_b))
         return fail(EHIP_EINVAL, "gemm: column sums need batch 1 and a K x N B");
+    if (d.causal < 0 || d.causal > 3) return fail(EHIP_EINVAL, "gemm: causal mode %d", d.causal);
     if (d.batch > 65535) return fail(EHIP_EINVAL, "gemm: batch %lld > 65535", (long long)d.batch);
     if (d.m > (int64_t(1) << 31) || d.n > (int64_t(1) << 31))
         return fail(EHIP_EINVAL, "gemm: extent beyond 2^31");

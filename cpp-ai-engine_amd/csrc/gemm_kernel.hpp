@@ -39,6 +39,7 @@ struct GemmArgs {
     int splits;        // K is cut into `splits` chunks of k_chunk (a multiple of BK)
     int64_t k_chunk;
     int vec;           // rows 16-byte aligned: checked loads may use float4 inside the edges
+    int causal;        // ehip_gemm_ex_t::causal: 0, or the skipping mode 1, 2 or 3
 };
 
 // The element offset of product z's matrix.
@@ -162,24 +163,46 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
 
     // Tile coordinates: XCD-contiguous renumbering, then GROUP_M-row groups.
     const int tiles = g.tiles_m * g.tiles_n;
-    int bid = blockIdx.x;
-    if (tiles % 8 == 0) bid = (bid % 8) * (tiles / 8) + bid / 8;
-    constexpr int kGroupM = 8;
-    const int group = bid / (kGroupM * g.tiles_n);
-    const int first_m = group * kGroupM;
-    const int gsz = min(g.tiles_m - first_m, kGroupM);
-    const int in_group = bid % (kGroupM * g.tiles_n);
-    const int tm = first_m + in_group % gsz;
-    const int tn = in_group / gsz;
+    int tm, tn;
+    int64_t batch = blockIdx.z;
+    if (g.causal != 0 && gridDim.y == 1) {
+        // Causal skipping makes a tile's work depend on its row band. Workgroups
+        // reach the XCDs (and their CUs) in turn in launch order, so the order
+        // runs over the products first: every XCD and CU then gets tiles of
+        // every band instead of, with few tiles per product, one band only.
+        const int64_t lin = int64_t(blockIdx.z) * gridDim.x + blockIdx.x;
+        batch = lin % gridDim.z;
+        const int t = int(lin / gridDim.z);
+        tm = t / g.tiles_n;
+        tn = t % g.tiles_n;
+    } else {
+        int bid = blockIdx.x;
+        if (tiles % 8 == 0) bid = (bid % 8) * (tiles / 8) + bid / 8;
+        constexpr int kGroupM = 8;
+        const int group = bid / (kGroupM * g.tiles_n);
+        const int first_m = group * kGroupM;
+        const int gsz = min(g.tiles_m - first_m, kGroupM);
+        const int in_group = bid % (kGroupM * g.tiles_n);
+        tm = first_m + in_group % gsz;
+        tn = in_group / gsz;
+    }
 
     const int split = blockIdx.y;
-    const int64_t batch = blockIdx.z;
     const float* A = g.a + batch_offset(batch, g.inner, g.stride_a, g.stride_a2);
     const float* B = g.b + batch_offset(batch, g.inner, g.stride_b, g.stride_b2);
     const int64_t m0 = int64_t(tm) * BM, n0 = int64_t(tn) * BN;
-    const int64_t k_begin = int64_t(split) * g.k_chunk;
+    int64_t k_begin = int64_t(split) * g.k_chunk;
     int64_t k_end = k_begin + g.k_chunk;
     if (k_end > g.k) k_end = g.k;
+    // Causal skipping (modes of ehip_gemm_ex_t::causal); m0 and m0 + BM are
+    // multiples of BK, so the K steps stay aligned.
+    if (g.causal == 1 && n0 >= m0 + BM) {
+        k_end = k_begin;  // wholly above the diagonal: the epilogue of acc = 0
+    } else if (g.causal == 2) {
+        if (k_end > m0 + BM) k_end = k_begin > m0 + BM ? k_begin : m0 + BM;
+    } else if (g.causal == 3) {
+        if (k_begin < m0) k_begin = k_end < m0 ? k_end : m0;
+    }
 
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int wm0 = (wave / C::kWavesN) * WM, wn0 = (wave % C::kWavesN) * WN;

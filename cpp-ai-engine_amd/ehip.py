@@ -69,7 +69,7 @@ class GemmEx(C.Structure):
                 ("ldc", C.c_int64), ("stride_c", C.c_int64), ("stride_c_inner", C.c_int64),
                 ("alpha", C.c_float), ("addend", C.c_void_p), ("ld_addend", C.c_int64),
                 ("stride_addend", C.c_int64), ("addend_period", C.c_int64), ("beta", C.c_float),
-                ("relu", C.c_int), ("colsum_b", C.c_void_p)]
+                ("relu", C.c_int), ("colsum_b", C.c_void_p), ("causal", C.c_int)]
 
 
 # name -> argtypes (all return int unless listed in _RESTYPES)

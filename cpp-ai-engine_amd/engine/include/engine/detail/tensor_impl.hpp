@@ -6,6 +6,7 @@
 #ifndef ENGINE_DETAIL_TENSOR_IMPL_HPP
 #define ENGINE_DETAIL_TENSOR_IMPL_HPP
 
+#include <cstdint>
 #include <functional>
 #include <memory>
 #include <vector>
@@ -26,6 +27,12 @@ struct TensorImpl {
 
     std::vector<std::shared_ptr<TensorImpl>> parents;
     std::function<void(const Tensor&)> backward_fn = nullptr;
+
+    // Set by nn::causal_mask on the tensor it returns: the value above the
+    // diagonal, and the storage version it was written with (a mask written
+    // since then, through this tensor or a view, no longer counts as one).
+    float causal_value = 0.0f;
+    uint64_t causal_version = ~uint64_t(0);
 
     TensorImpl() = default;
     TensorImpl(const std::vector<size_t>& s, float fill_val = 0.0f, bool req_grad = false);

@@ -484,6 +484,33 @@ int eng_mha_fwd_bwd(const float* x, int64_t b, int64_t s, int64_t d, int64_t hea
     });
 }
 
+// Fused MultiHeadAttention forward + backward under a causal mask: tagged != 0
+// passes nn::causal_mask(s) (whose products may skip the masked blocks),
+// tagged == 0 a copy of the same values made as a plain tensor (every product
+// computed in full), so that tests can compare the two.
+int eng_mha_causal_fwd_bwd(const float* x, int64_t b, int64_t s, int64_t d, int64_t heads,
+                           const float* params, const float* dy, float* y, float* dx,
+                           float* dparams, float* weights, int tagged) {
+    return guarded([&] {
+        nn::MultiHeadAttention mha{size_t(d), size_t(heads)};
+        mha.keep_attention(weights != nullptr);
+        load_params(mha.parameters(), params);
+        Tensor X = make({size_t(b), size_t(s), size_t(d)}, x, true);
+        const Tensor causal = nn::causal_mask(size_t(s));
+        const Tensor M = tagged ? causal : make({size_t(s), size_t(s)}, causal.data(), false);
+        Tensor Y = mha.forward(X, &M);
+        Y.backward(make(Y.shape(), dy, false));
+        if (weights != nullptr) put(mha.last_attention(), weights);
+        put(Y, y);
+        put(X.grad(), dx);
+        size_t off = 0;
+        for (const Tensor& p : mha.parameters()) {
+            put(p.grad(), dparams + off);
+            off += p.size();
+        }
+    });
+}
+
 // Adam on mse_loss(w, target) for `steps` steps; traj receives w after each
 // step (the optimiser replays of the reference's tests/test_reference.cpp:387-422).
 int eng_mse_adam(const float* w0, const float* target, int64_t n, int64_t steps, float lr,

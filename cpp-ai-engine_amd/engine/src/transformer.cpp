@@ -162,8 +162,28 @@ Tensor causal_mask(size_t seq_len, float masked_value) {
     std::vector<float> m(seq_len * seq_len, 0.0f);
     for (size_t i = 0; i < seq_len; ++i)
         for (size_t j = i + 1; j < seq_len; ++j) m[i * seq_len + j] = masked_value;
-    return Tensor({seq_len, seq_len}, m, false);
+    Tensor mask({seq_len, seq_len}, m, false);
+    mask.get_impl()->causal_value = masked_value;
+    mask.get_impl()->causal_version = mask.storage().version();
+    return mask;
 }
+
+namespace {
+
+// True when `mask` is a causal mask made by causal_mask for S x S scores and
+// not written since, with a masked value far enough below any finite score
+// that the softmax is exactly 0 above the diagonal (exp underflows to 0 below
+// -104): then the attention products may skip what the mask zeroes
+// (ehip_gemm_ex_t::causal). The skipped products are exact zeros, so the
+// results keep their values while the scores are finite.
+bool skippable_causal(const Tensor* mask, size_t S) {
+    if (mask == nullptr) return false;
+    const auto& impl = mask->get_impl();
+    return impl->causal_value <= -1e9f && impl->causal_version == mask->storage().version() &&
+           mask->ndim() == 2 && mask->shape()[0] == S && mask->shape()[1] == S;
+}
+
+}  // namespace
 
 // softmax(Q K^T / sqrt(d_k) + mask) V, composed as in src/transformer.cpp:279-304;
 // Q K^T reads K in place (no materialised transpose).
@@ -278,10 +298,15 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
     const int64_t sd = int64_t(S * D), ss = int64_t(S * S), hss = int64_t(H * S * S);
     const auto act = [&](const Tensor& t) { return HeadOperand{dptr(t), int64_t(D), sd, int64_t(hd)}; };
 
+    // With a causal mask: score tiles above the diagonal hold the mask value
+    // (their softmax is 0 either way), and the products with the weights skip
+    // the zero blocks above it.
+    const bool causal = skippable_causal(mask, S);
     Tensor scores({B, H, S, S}, 0.0f, false);
     ehip_gemm_ex_t d = head_product(false, true, B, H, S, S, hd, act(query), act(key),
                                     dout(scores), int64_t(S), hss, ss);
     d.alpha = scale;
+    d.causal = causal ? 1 : 0;
     if (mask != nullptr) {
         MaskPlan plan;
         mask_plan(*mask, B, H, S, plan);
@@ -300,14 +325,15 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
     Tensor out({B, S, D}, 0.0f, false);
     d = head_product(false, false, B, H, S, hd, S, HeadOperand{dptr(weights), int64_t(S), hss, ss},
                      act(value), dout(out), int64_t(D), sd, int64_t(hd));
+    d.causal = causal ? 2 : 0;  // W(i, k) = 0 for k > i
     hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention output");
 
     if (!track(query.requires_grad() || key.requires_grad() || value.requires_grad())) return out;
     out.set_requires_grad(true);
     out.get_impl()->parents = {query.get_impl(), key.get_impl(), value.get_impl()};
     Tensor q = query, k = key, v = value;
-    out.get_impl()->backward_fn = [q, k, v, weights, B, S, D, H, hd, scale, sd, ss,
-                                   hss](const Tensor& g) mutable {
+    out.get_impl()->backward_fn = [q, k, v, weights, B, S, D, H, hd, scale, sd, ss, hss,
+                                   causal](const Tensor& g) mutable {
         const auto head = [&](const Tensor& t) {
             return HeadOperand{dptr(t), int64_t(D), sd, int64_t(hd)};
         };
@@ -316,6 +342,7 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
             Tensor dv({B, S, D}, 0.0f, false);
             ehip_gemm_ex_t d = head_product(true, false, B, H, S, hd, S, w, head(g), dout(dv),
                                             int64_t(D), sd, int64_t(hd));
+            d.causal = causal ? 3 : 0;  // W^T(i, k) = W(k, i) = 0 for k < i
             hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dV");
             v.add_grad(dv);
         }
@@ -323,6 +350,9 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
         Tensor ds({B, H, S, S}, 0.0f, false);  // dW, then dS in place
         ehip_gemm_ex_t d = head_product(false, true, B, H, S, S, hd, head(g), head(v), dout(ds),
                                         int64_t(S), hss, ss);
+        // Above the diagonal dW only meets W = 0 in the softmax backward:
+        // whole tiles there are stored as 0 instead of computed.
+        d.causal = causal ? 1 : 0;
         hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dW");
         hip::check(ehip_softmax_backward_scaled_f32(dptr(weights), dptr(ds), dout(ds),
                                                     int64_t(B * H * S), int64_t(S), scale, nullptr),
@@ -332,6 +362,7 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
             Tensor dq({B, S, D}, 0.0f, false);
             d = head_product(false, false, B, H, S, hd, S, dsh, head(k), dout(dq), int64_t(D), sd,
                              int64_t(hd));
+            d.causal = causal ? 2 : 0;  // dS(i, k) = 0 for k > i
             hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dQ");
             q.add_grad(dq);
         }
@@ -339,6 +370,7 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
             Tensor dk({B, S, D}, 0.0f, false);
             d = head_product(true, false, B, H, S, hd, S, dsh, head(q), dout(dk), int64_t(D), sd,
                              int64_t(hd));
+            d.causal = causal ? 3 : 0;  // dS^T(i, k) = dS(k, i) = 0 for k < i
             hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dK");
             k.add_grad(dk);
         }

@@ -326,6 +326,20 @@ class Engine:
                                           None if w is None else _fp(w)))
         return (y, dx, dp, w) if weights else (y, dx, dp)
 
+    def mha_causal_fwd_bwd(self, x, heads, params, dy, tagged=True):
+        """Fused MultiHeadAttention forward + backward under the causal mask of
+        nn::causal_mask (tagged: its products may skip the masked blocks) or under a
+        plain copy of its values (every product in full). Returns y, dx, dparams and
+        the attention weights."""
+        x, params, dy = _f32(x), _f32(params), _f32(dy)
+        b, s, d = x.shape
+        y, dx, dp = np.empty_like(x), np.empty_like(x), np.empty_like(params)
+        w = np.empty((b, heads, s, s), np.float32)
+        self._ok(self.lib.eng_mha_causal_fwd_bwd(_fp(x), _i64(b), _i64(s), _i64(d), _i64(heads),
+                                                 _fp(params), _fp(dy), _fp(y), _fp(dx), _fp(dp),
+                                                 _fp(w), int(bool(tagged))))
+        return y, dx, dp, w
+
     def mse_adam(self, w0, target, steps, lr):
         w0, target = _f32(w0).ravel().copy(), _f32(target).ravel().copy()
         traj = np.empty((steps, w0.size), np.float32)

@@ -213,7 +213,22 @@ int ehip_gemm_f32_noalloc(int trans_a, int trans_b, int64_t batch, int64_t m, in
  * addend_period >= 1; consecutive addend matrices are stride_addend apart
  * (stride_addend 0 broadcasts one mask over every product, ld_addend 0 one
  * row over every row). inner >= 1. With k == 0, acc is 0 and the epilogue
- * still runs. */
+ * still runs.
+ * causal lets the caller of a causal-attention product skip work whose
+ * result it does not need or knows to be zero; each mode holds per product
+ * matrix, with i the row and j the column of C, and k the reduction index:
+ *   1  elements with j > i are don't-cares: tiles lying wholly above the
+ *      diagonal skip their products and store the epilogue of acc = 0 (the
+ *      addend where there is one, else 0);
+ *   2  op(A)(i, k) = 0 whenever k > i: products past a tile's last row are
+ *      skipped;
+ *   3  op(A)(i, k) = 0 whenever k < i: products before a tile's first row are
+ *      skipped.
+ * Skipped products are exact zeros, so every result keeps its value (its bits,
+ * but for the sign of a sum that is exactly zero) as long as the operands are
+ * finite; 0 computes everything. Honoured by the staged MFMA tiles; the other
+ * kernels compute everything. (No counterpart in the reference, which
+ * computes and then masks: src/transformer.cpp:279-304.) */
 typedef struct {
     int trans_a, trans_b;
     int64_t batch, inner;
@@ -230,6 +245,7 @@ typedef struct {
     float beta;
     int relu;
     float* colsum_b;
+    int causal;
 } ehip_gemm_ex_t;
 
 int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream);

@@ -481,3 +481,70 @@ def test_linear_backward_matches_separate_calls(hip, rows, inp, out, want):
                       k_tol(rows), "db against the separate sum")
         else:
             exact(host(db), host(hip.sum_axis(dy, 1, rows, out)), "db")
+
+
+# ------------------------------------------------------- causal skipping
+
+@pytest.mark.parametrize("S,hd,bt", [(512, 64, 32), (256, 32, 64), (300, 64, 48)])
+def test_causal_skipping_modes(hip, S, hd, bt):
+    """ehip_gemm_ex_t::causal on batched head products: with P zero above the diagonal,
+    P V (mode 2) and P^T G (mode 3) give the bits of the full products; Q K^T with the mask
+    (mode 1, scale and mask in the epilogue) and G V^T (mode 1, no epilogue) give the full
+    products' bits on and below the diagonal, and above it either those or the epilogue of
+    zero (the mask value, or 0). 300 is not a multiple of the tiles (edge checks); the
+    batch counts are large enough for every product to take the staged tiles."""
+    print_case("causal modes", S, hd, bt)
+    r = np.random.default_rng(S + hd)
+    q, k, v, g = (randn(r, bt, S, hd) for _ in range(4))
+    p = np.tril(np.abs(randn(r, bt, S, S)) / S).astype(np.float32)
+    mask = np.triu(np.full((S, S), -1e9, np.float32), 1)
+    Q, Kd, V, G, P, M = dev(q), dev(k), dev(v), dev(g), dev(p), dev(mask)
+    ss, sh = S * S, S * hd
+    below = np.tril(np.ones((S, S), bool))
+
+    def run(ta, tb, m, n, kk, a, lda, sa, b, ldb, sb, sc, ldc, causal, **kw):
+        c = hip.f32((bt, m, n))
+        d = desc(hip, ta, tb, bt, 1, m, n, kk, a, lda, sa, 0, b, ldb, sb, 0, c, ldc, sc, 0, **kw)
+        d.causal = causal
+        hip.gemm_ex(d)
+        return host(c)
+
+    scale = 1.0 / math.sqrt(hd)
+    s_full = run(False, True, S, S, hd, Q, hd, sh, Kd, hd, sh, ss, S, 0, alpha=scale,
+                 addend=M, ld_add=S, stride_add=0, period=1)
+    s_skip = run(False, True, S, S, hd, Q, hd, sh, Kd, hd, sh, ss, S, 1, alpha=scale,
+                 addend=M, ld_add=S, stride_add=0, period=1)
+    exact(s_skip[:, below], s_full[:, below], "scores on and below the diagonal")
+    above = s_skip[:, ~below]
+    assert np.all((above == s_full[:, ~below]) | (above == np.float32(-1e9))), "scores above"
+    exact(run(False, False, S, hd, S, P, S, ss, V, hd, sh, sh, hd, 2),
+          run(False, False, S, hd, S, P, S, ss, V, hd, sh, sh, hd, 0), "P V")
+    exact(run(True, False, S, hd, S, P, S, ss, G, hd, sh, sh, hd, 3),
+          run(True, False, S, hd, S, P, S, ss, G, hd, sh, sh, hd, 0), "P^T G")
+    dp_full = run(False, True, S, S, hd, G, hd, sh, V, hd, sh, ss, S, 0)
+    dp_skip = run(False, True, S, S, hd, G, hd, sh, V, hd, sh, ss, S, 1)
+    exact(dp_skip[:, below], dp_full[:, below], "dP on and below the diagonal")
+    above = dp_skip[:, ~below]
+    assert np.all((above == dp_full[:, ~below]) | (above == 0)), "dP above"
+    if S == 512:  # the staged tiles did skip: whole tiles above the diagonal hold the epilogue of 0
+        assert np.all(s_skip[:, :128, 384:] == np.float32(-1e9))
+        assert np.all(dp_skip[:, :128, 384:] == 0)
+    with pytest.raises(RuntimeError, match="causal"):
+        run(False, False, S, hd, S, P, S, ss, V, hd, sh, sh, hd, 4)
+
+
+@pytest.mark.parametrize("b,s,d,heads", [(8, 512, 512, 8), (2, 64, 96, 4), (16, 300, 128, 2)])
+def test_mha_causal_mask_skipping_keeps_values(eng, b, s, d, heads):
+    """The fused attention node under nn::causal_mask (whose score tiles above the diagonal,
+    the products with the weights past it and the matching backward products are skipped)
+    against the same mask values in a plain tensor (every product computed): outputs,
+    input and parameter gradients and attention weights hold the same values (the sign of
+    an exactly zero sum aside, which compares equal)."""
+    print_case("mha causal skipping", b, s, d, heads)
+    r = np.random.default_rng(b * 7 + s + d + heads)
+    x, dy = randn(r, b, s, d), randn(r, b, s, d)
+    params = mha_params(r, d)
+    tagged = eng.mha_causal_fwd_bwd(x, heads, params, dy, tagged=True)
+    plain = eng.mha_causal_fwd_bwd(x, heads, params, dy, tagged=False)
+    for got, want, what in zip(tagged, plain, ("y", "dx", "dparams", "weights")):
+        assert np.array_equal(got, want), f"{what}: {np.sum(got != want)} values differ"
