@@ -167,13 +167,23 @@ __device__ __forceinline__ void frag_softmax(Frag<T, V, VEC4, NT>& f, float* sh,
 
 // ------------------------------------------------------------ softmax
 
+// Columns of row r that are read: all, or with `causal` (rows stacked in
+// cols x cols matrices whose entries right of the diagonal are masked) the
+// first (r mod cols) + 1. A masked entry that is not read counts as -inf in
+// the forward (exp gives 0, as for a masked score far below the row's
+// maximum) and as 0 in the backward (where y is 0), so the sums and the other
+// outputs keep their bits; the masked outputs are stored as 0.
+__device__ __forceinline__ int read_cols(int64_t r, int64_t cols, int causal) {
+    return causal ? int(r % cols) + 1 : int(cols);
+}
+
 template <int T, int V, bool VEC4, bool NT>
 __global__ __launch_bounds__(Group<T>::kBlock, Group<T>::kMinWaves) void softmax_rows(
-    const float* __restrict__ x, float* __restrict__ y, int64_t rows, int64_t cols) {
+    const float* __restrict__ x, float* __restrict__ y, int64_t rows, int64_t cols, int causal) {
     __shared__ float sh[Group<T>::kBlock / 64];
     for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
         Frag<T, V, VEC4, NT> f;
-        f.load(x + r * cols, int(cols), Group<T>::tid(), -INFINITY);
+        f.load(x + r * cols, read_cols(r, cols, causal), Group<T>::tid(), -INFINITY);
         float m, s;
         frag_softmax(f, sh, m, s);
         f.store(y + r * cols, int(cols), Group<T>::tid());
@@ -184,12 +194,13 @@ __global__ __launch_bounds__(Group<T>::kBlock, Group<T>::kMinWaves) void softmax
 template <int T, int V, bool VEC4, bool NT>
 __global__ __launch_bounds__(Group<T>::kBlock) void softmax_rows_backward(
     const float* __restrict__ y, const float* g, float* dx, int64_t rows, int64_t cols,
-    float scale) {
+    float scale, int causal) {
     __shared__ float sh[Group<T>::kBlock / 64];
     for (int64_t r = Group<T>::first_row(); r < rows; r += Group<T>::row_step()) {
         Frag<T, V, VEC4, NT> fy, fg;
-        fy.load(y + r * cols, int(cols), Group<T>::tid(), 0.0f);
-        fg.load(g + r * cols, int(cols), Group<T>::tid(), 0.0f);
+        const int rc = read_cols(r, cols, causal);
+        fy.load(y + r * cols, rc, Group<T>::tid(), 0.0f);
+        fg.load(g + r * cols, rc, Group<T>::tid(), 0.0f);
         float dot = 0.0f;
 #pragma unroll
         for (int t = 0; t < V; ++t) dot += fg.v[t] * fy.v[t];
@@ -821,12 +832,13 @@ struct SoftmaxLaunch {
     int64_t rows, cols;
     hipStream_t s;
     int* rc;
+    int causal;
     template <int T, int V, bool VEC4, bool NT>
     bool run() {
         constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
         *rc = [&] {
             EHIP_LAUNCH("softmax", (softmax_rows<T, V, VEC4, NT>), dim3(row_grid(rows, G)), dim3(B), 0,
-                        s, x, y, rows, cols);
+                        s, x, y, rows, cols, causal);
             return int(EHIP_OK);
         }();
         return true;
@@ -841,12 +853,14 @@ struct SoftmaxBackwardLaunch {
     float scale;
     hipStream_t s;
     int* rc;
+    int causal;
     template <int T, int V, bool VEC4, bool NT>
     bool run() {
         constexpr int B = Group<T>::kBlock, G = Group<T>::kPerBlock;
         *rc = [&] {
             EHIP_LAUNCH("softmax_backward", (softmax_rows_backward<T, V, VEC4, NT>),
-                        dim3(row_grid(rows, G)), dim3(B), 0, s, y, g, dx, rows, cols, scale);
+                        dim3(row_grid(rows, G)), dim3(B), 0, s, y, g, dx, rows, cols, scale,
+                        causal);
             return int(EHIP_OK);
         }();
         return true;
@@ -952,18 +966,59 @@ using namespace ehip;
 
 extern "C" {
 
-int ehip_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int softmax_run(const float* x, float* y, int64_t rows, int64_t cols, int causal, void* stream) {
     EHIP_READY();
     if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "softmax: bad shape");
     if (!x || !y) return fail(EHIP_EINVAL, "softmax: null pointer");
+    if (causal && rows % cols != 0)
+        return fail(EHIP_EINVAL, "softmax (causal): %lld rows are not whole %lld x %lld matrices",
+                    (long long)rows, (long long)cols, (long long)cols);
     if (rows == 0) return EHIP_OK;
     hipStream_t s = as_stream(stream);
     int rc = EHIP_OK;
-    if (dispatch_row(rows, cols, rows_vec_ok(cols, {x, y}), SoftmaxLaunch{x, y, rows, cols, s, &rc}))
+    if (dispatch_row(rows, cols, rows_vec_ok(cols, {x, y}),
+                     SoftmaxLaunch{x, y, rows, cols, s, &rc, causal}))
         return rc;
+    // Rows beyond the register path read every column (the same values).
     EHIP_LAUNCH("softmax", softmax_rows_loop, dim3(loop_grid(rows)), dim3(kLoopThreads), 0, s, x, y,
                 rows, cols);
     return EHIP_OK;
+}
+
+int softmax_backward_run(const float* y, const float* g, float* dx, int64_t rows, int64_t cols,
+                         float scale, int causal, void* stream) {
+    EHIP_READY();
+    if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "softmax_backward: bad shape");
+    if (!y || !g || !dx) return fail(EHIP_EINVAL, "softmax_backward: null pointer");
+    if (causal && rows % cols != 0)
+        return fail(EHIP_EINVAL,
+                    "softmax_backward (causal): %lld rows are not whole %lld x %lld matrices",
+                    (long long)rows, (long long)cols, (long long)cols);
+    if (rows == 0) return EHIP_OK;
+    hipStream_t s = as_stream(stream);
+    int rc = EHIP_OK;
+    if (dispatch_row(rows, cols, rows_vec_ok(cols, {y, g, dx}),
+                     SoftmaxBackwardLaunch{y, g, dx, rows, cols, scale, s, &rc, causal}))
+        return rc;
+    EHIP_LAUNCH("softmax_backward", softmax_rows_backward_loop, dim3(loop_grid(rows)),
+                dim3(kLoopThreads), 0, s, y, g, dx, rows, cols, scale);
+    return EHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ehip_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream) {
+    return softmax_run(x, y, rows, cols, 0, stream);
+}
+
+int ehip_softmax_causal_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream) {
+    return softmax_run(x, y, rows, cols, 1, stream);
 }
 
 int ehip_softmax_backward_f32(const float* y, const float* g, float* dx, int64_t rows,
@@ -973,18 +1028,13 @@ int ehip_softmax_backward_f32(const float* y, const float* g, float* dx, int64_t
 
 int ehip_softmax_backward_scaled_f32(const float* y, const float* g, float* dx, int64_t rows,
                                      int64_t cols, float scale, void* stream) {
-    EHIP_READY();
-    if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "softmax_backward: bad shape");
-    if (!y || !g || !dx) return fail(EHIP_EINVAL, "softmax_backward: null pointer");
-    if (rows == 0) return EHIP_OK;
-    hipStream_t s = as_stream(stream);
-    int rc = EHIP_OK;
-    if (dispatch_row(rows, cols, rows_vec_ok(cols, {y, g, dx}),
-                     SoftmaxBackwardLaunch{y, g, dx, rows, cols, scale, s, &rc}))
-        return rc;
-    EHIP_LAUNCH("softmax_backward", softmax_rows_backward_loop, dim3(loop_grid(rows)),
-                dim3(kLoopThreads), 0, s, y, g, dx, rows, cols, scale);
-    return EHIP_OK;
+    return softmax_backward_run(y, g, dx, rows, cols, scale, 0, stream);
+}
+
+int ehip_softmax_backward_scaled_causal_f32(const float* y, const float* g, float* dx,
+                                            int64_t rows, int64_t cols, float scale,
+                                            void* stream) {
+    return softmax_backward_run(y, g, dx, rows, cols, scale, 1, stream);
 }
 
 int ehip_cross_entropy_f32(const float* logits, const int32_t* targets, float* probs, float* loss,

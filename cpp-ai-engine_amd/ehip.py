@@ -134,6 +134,8 @@ _SIGS = {
     "ehip_softmax_f32": [_vp, _vp, _i64, _i64, _vp],
     "ehip_softmax_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp],
     "ehip_softmax_backward_scaled_f32": [_vp, _vp, _vp, _i64, _i64, _f, _vp],
+    "ehip_softmax_causal_f32": [_vp, _vp, _i64, _i64, _vp],
+    "ehip_softmax_backward_scaled_causal_f32": [_vp, _vp, _vp, _i64, _i64, _f, _vp],
     "ehip_layernorm_f32": [_vp] * 6 + [_i64, _i64, _f, _vp],
     "ehip_layernorm_backward_f32": [_vp] * 7 + [_i64, _i64, _vp],
     "ehip_layernorm_backward_partials": [_i64, _i64, C.POINTER(_i64)],

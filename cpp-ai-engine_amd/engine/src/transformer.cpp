@@ -299,8 +299,9 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
     const auto act = [&](const Tensor& t) { return HeadOperand{dptr(t), int64_t(D), sd, int64_t(hd)}; };
 
     // With a causal mask: score tiles above the diagonal hold the mask value
-    // (their softmax is 0 either way), and the products with the weights skip
-    // the zero blocks above it.
+    // (their softmax is 0 either way), the softmax reads each row up to the
+    // diagonal only, and the products with the weights skip the zero blocks
+    // above it.
     const bool causal = skippable_causal(mask, S);
     Tensor scores({B, H, S, S}, 0.0f, false);
     ehip_gemm_ex_t d = head_product(false, true, B, H, S, S, hd, act(query), act(key),
@@ -317,7 +318,10 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
     }
     hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention scores");
     Tensor weights({B, H, S, S}, 0.0f, false);
-    hip::check(ehip_softmax_f32(dptr(scores), dout(weights), int64_t(B * H * S), int64_t(S), nullptr),
+    hip::check(causal ? ehip_softmax_causal_f32(dptr(scores), dout(weights), int64_t(B * H * S),
+                                                int64_t(S), nullptr)
+                      : ehip_softmax_f32(dptr(scores), dout(weights), int64_t(B * H * S),
+                                         int64_t(S), nullptr),
                "attention softmax");
     scores = Tensor();
     if (attention_weights != nullptr) *attention_weights = weights.detach();
@@ -354,8 +358,12 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
         // whole tiles there are stored as 0 instead of computed.
         d.causal = causal ? 1 : 0;
         hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dW");
-        hip::check(ehip_softmax_backward_scaled_f32(dptr(weights), dptr(ds), dout(ds),
-                                                    int64_t(B * H * S), int64_t(S), scale, nullptr),
+        hip::check(causal ? ehip_softmax_backward_scaled_causal_f32(dptr(weights), dptr(ds),
+                                                                    dout(ds), int64_t(B * H * S),
+                                                                    int64_t(S), scale, nullptr)
+                          : ehip_softmax_backward_scaled_f32(dptr(weights), dptr(ds), dout(ds),
+                                                             int64_t(B * H * S), int64_t(S),
+                                                             scale, nullptr),
                    "attention softmax backward");
         const HeadOperand dsh{dptr(ds), int64_t(S), hss, ss};
         if (q.requires_grad()) {  // dQ = dS K

@@ -570,6 +570,20 @@ int ehip_softmax_backward_f32(const float* y, const float* g, float* dx, int64_t
 int ehip_softmax_backward_scaled_f32(const float* y, const float* g, float* dx, int64_t rows,
                                      int64_t cols, float scale, void* stream);
 
+/* The softmax forward and scaled backward of a causal attention's scores:
+ * rows are stacked cols x cols matrices, and entries right of the diagonal
+ * (column j > row i within a matrix) are masked -- in the forward at least
+ * 104 below the row's maximum (their exponential is 0), in the backward with
+ * y = 0. Masked entries are not read; they are stored as 0. Every other output
+ * equals ehip_softmax_f32's / ehip_softmax_backward_scaled_f32's bit for bit,
+ * and a masked one by value (its sign of zero may differ). rows must be a
+ * multiple of cols. (The reference reads and computes the masked entries:
+ * src/transformer.cpp:279-304 through src/tensor_ops.cpp:621-676.) */
+int ehip_softmax_causal_f32(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
+int ehip_softmax_backward_scaled_causal_f32(const float* y, const float* g, float* dx,
+                                            int64_t rows, int64_t cols, float scale,
+                                            void* stream);
+
 /* LayerNorm over the last axis (two-pass mean and variance, eps inside the
  * square root) saving xhat and inv_std, and its derivative; dgamma and dbeta
  * are summed over rows in a fixed order (deterministic, no atomics).

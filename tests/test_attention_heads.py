@@ -533,6 +533,35 @@ def test_causal_skipping_modes(hip, S, hd, bt):
         run(False, False, S, hd, S, P, S, ss, V, hd, sh, sh, hd, 4)
 
 
+@pytest.mark.parametrize("S,mats", [(512, 8), (64, 40), (300, 3), (1, 5), (2048, 2)])
+def test_causal_softmax_matches_full(hip, S, mats):
+    """The causal softmax pair reads each row only up to the diagonal: on scores whose
+    masked entries are -1e9 + q.k (as the score product writes them), the forward equals
+    ehip_softmax_f32 bit for bit, and the scaled backward with y from it equals
+    ehip_softmax_backward_scaled_f32 by value (a masked output's zero may differ in sign);
+    a row count that is not a whole number of matrices is refused."""
+    print_case("causal softmax", S, mats)
+    r = np.random.default_rng(S + mats)
+    x = randn(r, mats, S, S) * 3
+    x = np.where(np.triu(np.ones((S, S), bool), 1), x + np.float32(-1e9), x).astype(np.float32)
+    X = dev(x)
+    rows = mats * S
+    full = hip.softmax(X)
+    y = hip.f32(X.shape)
+    hip.ok(hip.lib.ehip_softmax_causal_f32(hip.p(X), hip.p(y), rows, S, hip.stream()), "causal")
+    exact(host(y), host(full), "forward")
+    g = dev(randn(r, mats, S, S))
+    want = hip.softmax_backward(full, g, scale=0.125)
+    got = hip.f32(X.shape)
+    hip.ok(hip.lib.ehip_softmax_backward_scaled_causal_f32(hip.p(y), hip.p(g), hip.p(got), rows,
+                                                           S, 0.125, hip.stream()), "causal bwd")
+    assert np.array_equal(host(got), host(want)), "backward values"
+    if S > 1:
+        with pytest.raises(RuntimeError, match="whole"):
+            hip.ok(hip.lib.ehip_softmax_causal_f32(hip.p(X), hip.p(y), rows - 1, S,
+                                                   hip.stream()), "causal")
+
+
 @pytest.mark.parametrize("b,s,d,heads", [(8, 512, 512, 8), (2, 64, 96, 4), (16, 300, 128, 2)])
 def test_mha_causal_mask_skipping_keeps_values(eng, b, s, d, heads):
     """The fused attention node under nn::causal_mask (whose score tiles above the diagonal,
