@@ -541,6 +541,8 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
     del x, g, dx, m, v
     out["bandwidth_cfg4"] = bw
     torch.cuda.empty_cache()
+    log("bench: wide Conv2d layers, implicit GEMM")
+    out["conv_wide_implicit_gemm"] = conv_wide_leg(hip, timer, torch)
     # The other bandwidth-bound kernels of the path, at the shapes cfg 5 gives
     # them (16 x 512 tokens, d 1024, FFN 4096, 16 heads of 512 x 512 scores),
     # and max-pool at a large image batch, launched back to back from native
@@ -558,6 +560,43 @@ def extras(hip, eng, engine_mod, timer, torch, cpu_seconds=0.0):
                                            4096, n // 512, 512, (256, 64, 128, 128), 5)
     torch.cuda.empty_cache()
     return out
+
+
+def conv_wide_leg(hip, timer, torch):
+    """Wide Conv2d layers of ResNet stages through the implicit-GEMM entry points
+    (forward; the backward's dx, dW and db in one call) against the explicit im2col
+    composition's own kernels (im2col + product; dcols product + col2im + dW product,
+    without its bias, permute and copies, so a lower bound on what it costs). FLOPs are
+    2 N oH oW C kH kW C_out per product."""
+    legs = {}
+    for shape, co, k, s, p in [((32, 128, 28, 28), 128, 3, 1, 1), ((16, 64, 56, 56), 128, 3, 2, 1),
+                               ((32, 256, 14, 14), 256, 3, 1, 1)]:
+        n, c, h, w = shape
+        r = torch.Generator(device="cuda").manual_seed(c + co)
+        x = torch.randn(shape, device="cuda", generator=r)
+        wt = torch.randn(co, c, k, k, device="cuda", generator=r) * 0.05
+        b = torch.randn(co, device="cuda", generator=r)
+        oh = (h + 2 * p - k) // s + 1
+        g = torch.randn(n, co, oh, oh, device="cuda", generator=r)
+        kk, pix = c * k * k, oh * oh
+        fl = 2.0 * n * pix * kk * co
+        fwd = timer.time(lambda: hip.conv2d_igemm(x, wt, b, s, p), 20, 3)
+        bwd = timer.time(lambda: hip.conv2d_igemm_backward(x, wt, g, s, p), 20, 3)
+        w2 = wt.reshape(co, kk)
+        g2 = g.reshape(n, co, pix).permute(0, 2, 1).contiguous().reshape(n * pix, co)
+        cols = hip.im2col(x, k, k, s, p)
+        cfwd = timer.time(lambda: hip.gemm(hip.im2col(x, k, k, s, p), w2, trans_b=True), 20, 3)
+        cbwd = timer.time(lambda: (hip.col2im(hip.gemm(g2, w2), shape, k, k, s, p),
+                                   hip.gemm(g2, cols, trans_a=True)), 20, 3)
+        legs[f"{n}x{c}x{h}x{w} -> {co} k{k} s{s} p{p}"] = {
+            "forward": roofline("conv2d_igemm", "mfma", fl, fwd),
+            "backward (dx, dW, db)": roofline("conv2d_igemm_backward", "mfma", 2 * fl, bwd),
+            "im2col_composition_us": {"forward": round(cfwd * 1e6, 2),
+                                      "backward": round(cbwd * 1e6, 2)},
+            "speedup_over_composition": round((cfwd + cbwd) / (fwd + bwd), 2)}
+        del x, wt, b, g, g2, cols
+    torch.cuda.empty_cache()
+    return legs
 
 
 def kernel_only(eng, hip, timer, torch):

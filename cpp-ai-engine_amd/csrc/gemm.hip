@@ -33,6 +33,75 @@
 #include "gemm_kernel.hpp"
 
 namespace ehip {
+namespace gemm_detail {
+
+// C[b] = sum over splits of W[s][b], then the epilogue; with a column sum,
+// the n values after each split's C partials are summed the same way into
+// colsum. A block is RL split lanes x (256 / RL) outputs: lane l adds splits
+// l, l + RL, ... in order, then one thread per output adds the lanes in
+// order. RL grows with the number of splits, so a few outputs with many
+// splits still spread over the block instead of one long serial chain per
+// output; the order depends only on the shape.
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w, float* c,
+                                                     GemmArgs g, int64_t batch, int splits,
+                                                     int rl) {
+    const int64_t m = g.m, n = g.n;
+    __shared__ float lanes[256];
+    const int cw = 256 / rl;
+    const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
+    const int64_t mn = m * n;
+    const int64_t e = int64_t(blockIdx.x) * cw + cl;
+    const int64_t step = g.ws_stride;
+    const int64_t outputs = batch * mn + (g.colsum ? n : 0);
+    float acc = 0.0f;
+    if (e < outputs && lane < splits) {
+        const float* p = w + e + int64_t(lane) * step;
+        const int64_t stride = int64_t(rl) * step;
+        const int count = (splits - lane + rl - 1) / rl;
+        acc = p[0];
+        int s = 1;
+        for (; s + 8 <= count; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p[int64_t(s + u) * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; s < count; ++s) acc += p[int64_t(s) * stride];
+    }
+    lanes[threadIdx.x] = acc;
+    __syncthreads();
+    if (lane == 0 && e < outputs) {
+        float sum = lanes[cl];
+        for (int l = 1; l < rl && l < splits; ++l) sum += lanes[l * cw + cl];
+        if (e >= batch * mn) {
+            g.colsum[e - batch * mn] = sum;
+            return;
+        }
+        const int64_t b = e / mn, rc = e % mn;
+        const int64_t row = rc / n, col = rc % n;
+        float* dst = c + batch_offset(b, g.inner, g.stride_c, g.stride_c2) + row * g.ldc + col;
+        *dst = epilogue(g, b, row, col, sum, dst);
+    }
+}
+
+int splitk_finish(const float* ws, float* out, const GemmArgs& gr, int64_t batch, int splits,
+                  hipStream_t s) {
+    // Split lanes: up to 16, about one per 8 splits, so that no lane chain
+    // is longer than ~8 loads deep when the outputs are few.
+    int rl = 1;
+    while (rl < 16 && rl * 8 < splits) rl *= 2;
+    const int64_t total = gr.ws_stride;  // C partials, then the column sums
+    const int64_t per_block = 256 / rl;
+    EHIP_LAUNCH("gemm_splitk_reduce", splitk_reduce, dim3(unsigned(ceil_div(total, per_block))),
+                dim3(256), 0, s, ws, out, gr, batch, splits, rl);
+    return EHIP_OK;
+}
+
+}  // namespace gemm_detail
+}  // namespace ehip
+
+namespace ehip {
 namespace {
 
 using namespace gemm_detail;
@@ -104,17 +173,9 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s,
                     dim3(C::kThreads), 0, s, g);
     }
     if (splits > 1) {
-        // Split lanes: up to 16, about one per 8 splits, so that no lane chain
-        // is longer than ~8 loads deep when the outputs are few.
-        int rl = 1;
-        while (rl < 16 && rl * 8 < splits) rl *= 2;
-        const int64_t total = g.ws_stride;  // C partials, then the column sums
-        const int64_t per_block = 256 / rl;
         GemmArgs gr = g0;  // the caller's output and epilogue, the workspace geometry
         gr.ws_stride = g.ws_stride;
-        EHIP_LAUNCH("gemm_splitk_reduce", splitk_reduce,
-                    dim3(unsigned(ceil_div(total, per_block))), dim3(256), 0, s, g.c, out, gr,
-                    batch, splits, rl);
+        return splitk_finish(g.c, out, gr, batch, splits, s);
     }
     return EHIP_OK;
 }

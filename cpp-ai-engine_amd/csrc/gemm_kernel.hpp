@@ -28,6 +28,7 @@ struct GemmArgs {
     float alpha;
     const float* add;
     int64_t ld_add, stride_add, add_period;
+    int add_row;  // the addend is one value per row: add[i] (a convolution's bias)
     float beta;
     int relu;  // then v = max(0, v)
     // colsum[j] = sum over k of op(B)[k][j] (batch 1), made by the first
@@ -63,8 +64,9 @@ __device__ __forceinline__ float finish(const GemmArgs& g, float v, float add, f
 // The stored value of product z's output (row, col); dst is that element.
 __device__ __forceinline__ float epilogue(const GemmArgs& g, int64_t z, int64_t row, int64_t col,
                                           float v, const float* dst) {
-    const float add =
-        g.add ? g.add[(z % g.add_period) * g.stride_add + row * g.ld_add + col] : 0.0f;
+    const float add = g.add ? g.add[(z % g.add_period) * g.stride_add +
+                                    (g.add_row ? row : row * g.ld_add + col)]
+                            : 0.0f;
     return finish(g, v, add, g.beta != 0.0f ? *dst : 0.0f);
 }
 
@@ -153,6 +155,91 @@ __device__ __forceinline__ void store_tile(float* __restrict__ s, const float4* 
     }
 }
 
+// The MFMAs of one staged K step: the fragments of k-pair kk + 2 are read
+// from LDS while the MFMAs of kk run (two register sets). Tiles of at most
+// 128 x 128 run four or more waves per SIMD: there the wave issuing its MFMAs
+// also takes priority over the others' loads and LDS traffic, which keeps the
+// matrix pipe fed (measured on MI355X: 5-9% on 8192 x 1024 x K; neither
+// change helps the 256 x 256 tile, nor priority alone).
+template <class C, int BK>
+__device__ __forceinline__ void mfma_stage(floatx16 (&acc)[C::kFM][C::kFN], const float* lds_a,
+                                           const float* lds_b, int wm0, int wn0, int lane) {
+    const float* sa = lds_a + (lane / 32) * C::kLdsA + wm0 + lane % 32;
+    const float* sb = lds_b + (lane / 32) * C::kLdsB + wn0 + lane % 32;
+    float fa[2][C::kFM], fb[2][C::kFN];
+#pragma unroll
+    for (int i = 0; i < C::kFM; ++i) fa[0][i] = sa[32 * i];
+#pragma unroll
+    for (int j = 0; j < C::kFN; ++j) fb[0][j] = sb[32 * j];
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 2) {
+        const int f = (kk / 2) & 1;
+        if (kk + 2 < BK) {
+#pragma unroll
+            for (int i = 0; i < C::kFM; ++i) fa[f ^ 1][i] = sa[(kk + 2) * C::kLdsA + 32 * i];
+#pragma unroll
+            for (int j = 0; j < C::kFN; ++j) fb[f ^ 1][j] = sb[(kk + 2) * C::kLdsB + 32 * j];
+        }
+        if (C::kPrio) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int i = 0; i < C::kFM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::kFN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[f][i], fb[f][j], acc[i][j], 0,
+                                                                 0, 0);
+        if (C::kPrio) __builtin_amdgcn_s_setprio(0);
+    }
+}
+
+// Stores the accumulators of the tile at (m0, n0) into Cp (row pitch ldc):
+// as they are, or through the fused epilogue, one 32 x 32 block at a time --
+// the block's addend and old C values are loaded together first (the compiler
+// cannot move a load above an earlier store to C, which may alias them), then
+// stored. The addend is add[i * ld_add + j], or with add_row add[i].
+template <class C, bool CHECK, bool EPI>
+__device__ __forceinline__ void store_acc(const GemmArgs& g, floatx16 (&acc)[C::kFM][C::kFN],
+                                          float* Cp, int64_t ldc, const float* addp, int64_t m0,
+                                          int64_t n0, int wm0, int wn0, int lane) {
+    if (!EPI) {
+#pragma unroll
+        for (int i = 0; i < C::kFM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::kFN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t row = m0 + wm0 + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+                    const int64_t col = n0 + wn0 + 32 * j + lane % 32;
+                    if (CHECK && (row >= g.m || col >= g.n)) continue;
+                    Cp[row * ldc + col] = acc[i][j][r];
+                }
+        return;
+    }
+    const int64_t ld_add = g.add_row ? 1 : g.ld_add;
+#pragma unroll
+    for (int i = 0; i < C::kFM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::kFN; ++j) {
+            const int64_t row0 = m0 + wm0 + 32 * i + 4 * (lane / 32);
+            const int64_t col = n0 + wn0 + 32 * j + lane % 32;
+            float* cb = Cp + row0 * ldc + col;
+            const float* ab = addp ? addp + row0 * ld_add + (g.add_row ? 0 : col) : nullptr;
+            float e_add[16], e_old[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dr = 8 * (r / 4) + (r % 4);
+                const bool in = !CHECK || (row0 + dr < g.m && col < g.n);
+                e_add[r] = (ab && in) ? ab[dr * ld_add] : 0.0f;
+                e_old[r] = (g.beta != 0.0f && in) ? cb[dr * ldc] : 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dr = 8 * (r / 4) + (r % 4);
+                if (CHECK && (row0 + dr >= g.m || col >= g.n)) continue;
+                cb[dr * ldc] = finish(g, acc[i][j][r], e_add[r], e_old[r]);
+            }
+        }
+}
+
 // EPI: the fused epilogue (alpha, addend, beta, ReLU); without it the
 // accumulators are stored as they are (also the split-K partials).
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool CHECK, bool EPI>
@@ -235,37 +322,7 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
             load_tile<C, BN, BK, !TB, CHECK>(B, g.ldb, g.n, k_end, n0, kn, rb, C::kBLoads,
                                              C::kB4, g.vec);
         }
-        // The fragments of k-pair kk + 2 are read from LDS while the MFMAs of
-        // kk run (two register sets). Tiles of at most 128 x 128 run four or
-        // more waves per SIMD: there the wave issuing its MFMAs also takes
-        // priority over the others' loads and LDS traffic, which keeps the
-        // matrix pipe fed (measured on MI355X: 5-9% on 8192 x 1024 x K;
-        // neither change helps the 256 x 256 tile, nor priority alone).
-        const float* sa = lds_a[cur] + (lane / 32) * C::kLdsA + wm0 + lane % 32;
-        const float* sb = lds_b[cur] + (lane / 32) * C::kLdsB + wn0 + lane % 32;
-        float fa[2][C::kFM], fb[2][C::kFN];
-#pragma unroll
-        for (int i = 0; i < C::kFM; ++i) fa[0][i] = sa[32 * i];
-#pragma unroll
-        for (int j = 0; j < C::kFN; ++j) fb[0][j] = sb[32 * j];
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 2) {
-            const int f = (kk / 2) & 1;
-            if (kk + 2 < BK) {
-#pragma unroll
-                for (int i = 0; i < C::kFM; ++i) fa[f ^ 1][i] = sa[(kk + 2) * C::kLdsA + 32 * i];
-#pragma unroll
-                for (int j = 0; j < C::kFN; ++j) fb[f ^ 1][j] = sb[(kk + 2) * C::kLdsB + 32 * j];
-            }
-            if (C::kPrio) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-            for (int i = 0; i < C::kFM; ++i)
-#pragma unroll
-                for (int j = 0; j < C::kFN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[f][i], fb[f][j], acc[i][j],
-                                                                     0, 0, 0);
-            if (C::kPrio) __builtin_amdgcn_s_setprio(0);
-        }
+        mfma_stage<C, BK>(acc, lds_a[cur], lds_b[cur], wm0, wn0, lane);
         if (colsum_tile && threadIdx.x < BN) {
             // This K step's B rows, in k order, for column n0 + threadIdx.x.
             const float* col = lds_b[cur] + threadIdx.x;
@@ -300,47 +357,8 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
         Cp = g.c + batch_offset(batch, g.inner, g.stride_c, g.stride_c2);
         ldc = g.ldc;
     }
-    if (!EPI) {
-#pragma unroll
-        for (int i = 0; i < C::kFM; ++i)
-#pragma unroll
-            for (int j = 0; j < C::kFN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t row = m0 + wm0 + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-                    const int64_t col = n0 + wn0 + 32 * j + lane % 32;
-                    if (CHECK && (row >= g.m || col >= g.n)) continue;
-                    Cp[row * ldc + col] = acc[i][j][r];
-                }
-        return;
-    }
-    // The fused epilogue, one 32 x 32 block at a time: the block's addend and
-    // old C values are loaded together first (the compiler cannot move a load
-    // above an earlier store to C, which may alias them), then stored.
     const float* addp = g.add ? g.add + (int64_t(batch) % g.add_period) * g.stride_add : nullptr;
-#pragma unroll
-    for (int i = 0; i < C::kFM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::kFN; ++j) {
-            const int64_t row0 = m0 + wm0 + 32 * i + 4 * (lane / 32);
-            const int64_t col = n0 + wn0 + 32 * j + lane % 32;
-            float* cb = Cp + row0 * ldc + col;
-            const float* ab = addp ? addp + row0 * g.ld_add + col : nullptr;
-            float e_add[16], e_old[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int dr = 8 * (r / 4) + (r % 4);
-                const bool in = !CHECK || (row0 + dr < g.m && col < g.n);
-                e_add[r] = (ab && in) ? ab[dr * g.ld_add] : 0.0f;
-                e_old[r] = (g.beta != 0.0f && in) ? cb[dr * ldc] : 0.0f;
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int dr = 8 * (r / 4) + (r % 4);
-                if (CHECK && (row0 + dr >= g.m || col >= g.n)) continue;
-                cb[dr * ldc] = finish(g, acc[i][j][r], e_add[r], e_old[r]);
-            }
-        }
+    store_acc<C, CHECK, EPI>(g, acc, Cp, ldc, addp, m0, n0, wm0, wn0, lane);
 }
 
 // ------------------------------------------------------------ K-sliced tiles
@@ -653,55 +671,11 @@ __global__ __launch_bounds__(64 * W) void gemm_kslice_pair(GemmArgs g0, GemmArgs
         kslice_tile<W, true, false, CHECK, EPI, KU>(g1, int(blockIdx.x) - tiles0, 0, lds, w1);
 }
 
-// C[b] = sum over splits of W[s][b], then the epilogue; with a column sum,
-// the n values after each split's C partials are summed the same way into
-// colsum. A block is RL split lanes x (256 / RL) outputs: lane l adds splits
-// l, l + RL, ... in order, then one thread per output adds the lanes in
-// order. RL grows with the number of splits, so a few outputs with many
-// splits still spread over the block instead of one long serial chain per
-// output; the order depends only on the shape.
-__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w, float* c,
-                                                     GemmArgs g, int64_t batch, int splits,
-                                                     int rl) {
-    const int64_t m = g.m, n = g.n;
-    __shared__ float lanes[256];
-    const int cw = 256 / rl;
-    const int lane = threadIdx.x / cw, cl = threadIdx.x % cw;
-    const int64_t mn = m * n;
-    const int64_t e = int64_t(blockIdx.x) * cw + cl;
-    const int64_t step = g.ws_stride;
-    const int64_t outputs = batch * mn + (g.colsum ? n : 0);
-    float acc = 0.0f;
-    if (e < outputs && lane < splits) {
-        const float* p = w + e + int64_t(lane) * step;
-        const int64_t stride = int64_t(rl) * step;
-        const int count = (splits - lane + rl - 1) / rl;
-        acc = p[0];
-        int s = 1;
-        for (; s + 8 <= count; s += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = p[int64_t(s + u) * stride];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc += v[u];
-        }
-        for (; s < count; ++s) acc += p[int64_t(s) * stride];
-    }
-    lanes[threadIdx.x] = acc;
-    __syncthreads();
-    if (lane == 0 && e < outputs) {
-        float sum = lanes[cl];
-        for (int l = 1; l < rl && l < splits; ++l) sum += lanes[l * cw + cl];
-        if (e >= batch * mn) {
-            g.colsum[e - batch * mn] = sum;
-            return;
-        }
-        const int64_t b = e / mn, rc = e % mn;
-        const int64_t row = rc / n, col = rc % n;
-        float* dst = c + batch_offset(b, g.inner, g.stride_c, g.stride_c2) + row * g.ldc + col;
-        *dst = epilogue(g, b, row, col, sum, dst);
-    }
-}
+// Sums the split-K partials in ws (splits x gr.ws_stride floats: the C
+// partials of `batch` products, then the column sums when gr.colsum is set)
+// into gr's output `out` through its epilogue, in a fixed order (gemm.hip).
+int splitk_finish(const float* ws, float* out, const GemmArgs& gr, int64_t batch, int splits,
+                  hipStream_t s);
 
 }  // namespace gemm_detail
 }  // namespace ehip

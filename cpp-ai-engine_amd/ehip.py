@@ -117,6 +117,8 @@ _SIGS = {
     "ehip_conv2d_forward_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_backward_input_f32": [_vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_backward_weight_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
+    "ehip_conv2d_igemm_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
+    "ehip_conv2d_igemm_backward_f32": [_vp] * 6 + [C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_relu_maxpool_supported": [C.POINTER(Window), _i64, C.POINTER(Window)],
     "ehip_conv2d_relu_maxpool_f32": [_vp, _vp, _vp, _vp, _vp, C.POINTER(Window), _i64,
                                      C.POINTER(Window), _vp],
@@ -434,6 +436,28 @@ class Backend:
             self.p(x), self.p(g), self.p(dw), self.p(db) if bias else None, C.byref(w), co,
             self.stream()), "conv2d_backward_weight")
         return dw, db
+
+    def conv2d_igemm(self, x, weight, bias, stride, pad):
+        co, ci, kh, kw = weight.shape
+        w = window(*x.shape, kh, kw, stride, pad)
+        out = self.f32((w.batch, co, w.out_h, w.out_w))
+        self.ok(self.lib.ehip_conv2d_igemm_f32(
+            self.p(x), self.p(weight), self.p(bias) if bias is not None else None, self.p(out),
+            C.byref(w), co, self.stream()), "conv2d_igemm")
+        return out
+
+    def conv2d_igemm_backward(self, x, weight, g, stride, pad, want=(True, True, True)):
+        """(dx, dweight, dbias); the parts not in `want` are skipped and returned as None."""
+        co, ci, kh, kw = weight.shape
+        w = window(*x.shape, kh, kw, stride, pad)
+        dx = self.f32(tuple(x.shape)) if want[0] else None
+        dw = self.f32(tuple(weight.shape)) if want[1] else None
+        db = self.f32((co,)) if want[2] else None
+        self.ok(self.lib.ehip_conv2d_igemm_backward_f32(
+            self.p(x), self.p(weight), self.p(g), self.p(dx) if want[0] else None,
+            self.p(dw) if want[1] else None, self.p(db) if want[2] else None, C.byref(w), co,
+            self.stream()), "conv2d_igemm_backward")
+        return dx, dw, db
 
     def conv_relu_pool_windows(self, x_shape, weight_shape, stride, pad, pk):
         co, ci, kh, kw = weight_shape

@@ -28,6 +28,15 @@ struct Window2d {
 Tensor im2col(const Tensor& input, const Window2d& window);
 Tensor col2im(const Tensor& cols, const std::vector<size_t>& input_shape, const Window2d& window);
 
+// Wide convolutions (the direct kernels refuse them) run as implicit GEMMs by
+// default: the forward, weight-gradient and input-gradient products on MFMA
+// with the column operand gathered from the tensors, no column matrix in
+// memory. Off, they compose as the reference does (im2col, the product with
+// the transposed weight, the bias add, the permute). The values agree within
+// the products' K-term tolerance. Process-wide; set it between steps.
+void set_conv_implicit_gemm(bool on);
+bool conv_implicit_gemm();
+
 class Conv2d : public Module {
 public:
     Conv2d(size_t in_channels, size_t out_channels, const Window2d& window, bool use_bias = true);

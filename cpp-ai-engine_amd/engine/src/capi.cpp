@@ -429,6 +429,12 @@ int eng_set_fused_nodes(int on) {
     return was ? 1 : 0;
 }
 
+int eng_set_conv_implicit_gemm(int on) {
+    const bool was = nn::conv_implicit_gemm();
+    nn::set_conv_implicit_gemm(on != 0);
+    return was ? 1 : 0;
+}
+
 int eng_set_fused_bias_grad(int on) {
     const bool was = nn::fused_bias_grad();
     nn::set_fused_bias_grad(on != 0);

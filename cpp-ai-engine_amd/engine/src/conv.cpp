@@ -2,6 +2,7 @@
 // one GEMM otherwise), MaxPool2d and Flatten (the reference's src/conv.cpp).
 #include "engine/conv.hpp"
 
+#include <atomic>
 #include <cmath>
 #include <stdexcept>
 
@@ -101,7 +102,52 @@ Tensor conv2d_direct(const Tensor& input, const Tensor& weight, const Tensor& bi
     return out;
 }
 
+std::atomic<bool> g_conv_igemm{true};
+
+// The implicit-GEMM convolution node (wide layers): one forward launch (the
+// bias in its epilogue) and one backward call making the input gradient and
+// the weight and bias gradients that are needed. Same mathematics as the
+// reference's composition (src/conv.cpp:280-338), summed in another order:
+// within the K-term tolerance of its values.
+Tensor conv2d_igemm(const Tensor& input, const Tensor& weight, const Tensor& bias, bool use_bias,
+                    const ehip_window_t& w) {
+    const size_t co = weight.shape()[0];
+    Tensor out({size_t(w.batch), co, size_t(w.out_h), size_t(w.out_w)}, 0.0f, false);
+    hip::check(ehip_conv2d_igemm_f32(dptr(input), dptr(weight), use_bias ? dptr(bias) : nullptr,
+                                     dout(out), &w, int64_t(co), nullptr),
+               "conv2d (implicit GEMM)");
+    const bool need_x = input.requires_grad();
+    const bool need_w = weight.requires_grad();
+    const bool need_b = use_bias && bias.requires_grad();
+    if (!track(need_x || need_w || need_b)) return out;
+    out.set_requires_grad(true);
+    auto& parents = out.get_impl()->parents;
+    if (need_x) parents.push_back(input.get_impl());
+    if (need_w) parents.push_back(weight.get_impl());
+    if (need_b) parents.push_back(bias.get_impl());
+    Tensor x_copy = input, w_copy = weight, b_copy = bias;
+    out.get_impl()->backward_fn = [x_copy, w_copy, b_copy, need_x, need_w, need_b,
+                                   w](const Tensor& g) mutable {
+        Tensor dx, dw, db;
+        if (need_x) dx = Tensor(x_copy.shape(), 0.0f, false);
+        if (need_w) dw = Tensor(w_copy.shape(), 0.0f, false);
+        if (need_b) db = Tensor({w_copy.shape()[0]}, 0.0f, false);
+        hip::check(ehip_conv2d_igemm_backward_f32(
+                       dptr(x_copy), dptr(w_copy), dptr(g), need_x ? dout(dx) : nullptr,
+                       need_w ? dout(dw) : nullptr, need_b ? dout(db) : nullptr, &w,
+                       int64_t(w_copy.shape()[0]), nullptr),
+                   "conv2d backward (implicit GEMM)");
+        if (need_x) x_copy.add_grad(dx);
+        if (need_w) w_copy.add_grad(dw);
+        if (need_b) b_copy.add_grad(db);
+    };
+    return out;
+}
+
 }  // namespace
+
+void set_conv_implicit_gemm(bool on) { g_conv_igemm.store(on); }
+bool conv_implicit_gemm() { return g_conv_igemm.load(); }
 
 size_t Window2d::out_h(size_t in_h) const { return output_size(in_h, kernel_h, stride, padding); }
 size_t Window2d::out_w(size_t in_w) const { return output_size(in_w, kernel_w, stride, padding); }
@@ -154,8 +200,9 @@ Conv2d::Conv2d(size_t in_channels, size_t out_channels, const Window2d& window, 
     bias_ = Tensor({out_channels}, 0.0f, use_bias);
 }
 
-// Narrow layers take the direct kernels. Wider ones compose as the reference
-// does: im2col -> cols (W reshaped to (outC, K))^T -> + bias -> (N, outC, oH, oW)
+// Narrow layers take the direct kernels, wider ones the implicit GEMM. With
+// that switched off, wide layers compose as the reference does: im2col ->
+// cols (W reshaped to (outC, K))^T -> + bias -> (N, outC, oH, oW)
 // (src/conv.cpp:280-338), the product on MFMA reading W in place through the
 // GEMM's transposed mode, so its derivative needs no transpose either.
 Tensor Conv2d::forward(const Tensor& input) {
@@ -172,6 +219,7 @@ Tensor Conv2d::forward(const Tensor& input) {
     const ehip_window_t w = window_of(input.shape(), window_);
     if (ehip_conv2d_direct_supported(&w, int64_t(out_channels_)))
         return conv2d_direct(input, weight_, bias_, use_bias_, w);
+    if (conv_implicit_gemm()) return conv2d_igemm(input, weight_, bias_, use_bias_, w);
     Tensor cols = im2col_node(input, window_);
     Tensor out = ops::matmul_nt(cols, weight_.reshape({out_channels_, K}));
     if (use_bias_) out = out + bias_;

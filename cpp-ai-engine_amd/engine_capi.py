@@ -352,6 +352,11 @@ class Engine:
         returns the previous setting."""
         return bool(self.lib.eng_set_fused_nodes(int(bool(on))))
 
+    def set_conv_implicit_gemm(self, on):
+        """Wide convolutions as implicit GEMMs (default on) or the reference's im2col
+        composition; returns the previous setting."""
+        return bool(self.lib.eng_set_conv_implicit_gemm(int(bool(on))))
+
     def set_fused_bias_grad(self, on):
         """Bias gradients of mid-sized layers from the weight-gradient products' column sums
         (default on) or the separate column sum; returns the previous setting."""

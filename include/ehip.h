@@ -431,6 +431,29 @@ int ehip_conv2d_backward_weight_f32(const float* x, const float* grad_out, float
                                     float* dbias, const ehip_window_t* w, int64_t out_channels,
                                     void* stream);
 
+/* Implicit-GEMM convolution for layers of any width, on the fp32 MFMA tiles:
+ * the products of the reference's wide composition -- im2col, the product with
+ * the transposed weight, the bias add and the permute to (N, C_out, oH, oW)
+ * (src/conv.cpp:280-338, im2col/col2im src/conv.cpp:61-217) -- with the column
+ * operand gathered from x (forward, weight gradient) or from grad_out (input
+ * gradient, col2im's adjoint as a gather), never written to HBM. Layouts as
+ * for the direct kernels above: x (N, C_in, H, W), weight (C_out, C_in, kH, kW),
+ * out and grad_out (N, C_out, oH, oW), dense row-major.
+ *   forward: out = weight . cols + bias[co] (bias may be NULL).
+ *   backward: dx = sum over (co, i, j) of weight . grad_out at the window that
+ *     covers the pixel; dweight = sum over images and pixels of grad_out .
+ *     cols; dbias = sum of grad_out per channel. Each output may be NULL to
+ *     skip it; the ones given are overwritten.
+ * Fixed-order sums (K split into fixed chunks on small grids): deterministic,
+ * within the K-term tolerance of the reference's serial loops. Layers with
+ * more than 2^31 - 1 elements in one image's input, output or weight rows, or
+ * more than 65535 images, are refused with EHIP_EINVAL. */
+int ehip_conv2d_igemm_f32(const float* x, const float* weight, const float* bias, float* out,
+                          const ehip_window_t* w, int64_t out_channels, void* stream);
+int ehip_conv2d_igemm_backward_f32(const float* x, const float* weight, const float* grad_out,
+                                   float* dx, float* dweight, float* dbias,
+                                   const ehip_window_t* w, int64_t out_channels, void* stream);
+
 /* Conv2d -> ReLU -> MaxPool2d fused, for a narrow convolution followed by a
  * max pool with disjoint square windows (kernel == stride, no padding): the
  * Sequential pattern of the reference's CNN (conv, ReLU, pool, twice). `conv`

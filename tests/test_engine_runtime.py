@@ -1,5 +1,5 @@
 """The engine's runtime contract on the GPU: residency, the arena, failure handling, the
-queued convolution weight sums, and the wide-convolution (im2col + GEMM) path.
+queued convolution weight sums, and the wide-convolution paths (implicit GEMM, im2col + GEMM).
 
 Residency follows the reference's transfer-accounting tests
 (tests/test_cuda_parity.cpp:786-818 and 988-1036 of the reference): values computed on the
@@ -192,13 +192,16 @@ def test_orphaned_weight_sums_touch_no_reused_memory(eng):
 
 @pytest.mark.parametrize("n,c,hw,oc,k,stride,pad", [(4, 64, 16, 128, 3, 1, 1),
                                                     (2, 32, 15, 96, 5, 2, 2)])
-def test_wide_conv2d_im2col_gemm_path(eng, n, c, hw, oc, k, stride, pad):
+@pytest.mark.parametrize("igemm", [True, False])
+def test_wide_conv2d_paths(eng, n, c, hw, oc, k, stride, pad, igemm):
     """Convolutions too wide for the direct kernels (out_channels * C_in * kH * kW above
-    8192) go through im2col, the MFMA product, the bias and the permute
-    (src/conv.cpp:280-338 of the reference); forward and all three gradients against the
-    compiled reference with its metric at the K-term bound."""
-    print_case("wide conv", n, c, hw, oc, k, stride, pad)
+    8192) run as implicit GEMMs, or, with that switched off, through im2col, the MFMA
+    product, the bias and the permute (src/conv.cpp:280-338 of the reference); forward
+    and all three gradients against the compiled reference with its metric at the
+    K-term bound."""
+    print_case("wide conv", n, c, hw, oc, k, stride, pad, igemm)
     ref = ref_or_skip()
+    was = eng.set_conv_implicit_gemm(igemm)
     ref.set_threads(8)
     assert oc * c * k * k > 8192
     r = np.random.default_rng(n * 1000 + c + oc)
@@ -207,7 +210,10 @@ def test_wide_conv2d_im2col_gemm_path(eng, n, c, hw, oc, k, stride, pad):
     b = r.standard_normal(oc, dtype=np.float32)
     oh = (hw + 2 * pad - k) // stride + 1
     dy = r.standard_normal((n, oc, oh, oh), dtype=np.float32)
-    y, dx, dw, db = eng.conv2d_fwd_bwd(x, w, b, stride, pad, dy)
+    try:
+        y, dx, dw, db = eng.conv2d_fwd_bwd(x, w, b, stride, pad, dy)
+    finally:
+        eng.set_conv_implicit_gemm(was)
     wy, wdx, wdw, wdb = ref.conv2d_fwd_bwd(x, w, b, stride, pad, dy)
     ref_close(y, wy, k_tol(c * k * k), "y")
     ref_close(dx, wdx, k_tol(oc * k * k), "dx")
