@@ -125,6 +125,9 @@ public:
         const std::string& prefix = "") override;
     void train(bool mode = true) override;
     std::string name() const override { return "Sequential"; }
+    // Prints each layer's name and parameter count and the total to stdout
+    // (src/nn.cpp:303-313 of the reference).
+    void summary() const;
     size_t size() const noexcept { return layers_.size(); }
     Module& at(size_t index);
 

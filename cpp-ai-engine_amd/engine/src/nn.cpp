@@ -5,6 +5,7 @@
 
 #include <atomic>
 #include <cmath>
+#include <cstdio>
 #include <stdexcept>
 
 #include "detail.hpp"
@@ -166,6 +167,19 @@ std::vector<std::pair<std::string, Tensor>> Sequential::named_parameters(const s
 void Sequential::train(bool mode) {
     Module::train(mode);
     for (auto& layer : layers_) layer->train(mode);
+}
+
+// The reference's console format (src/nn.cpp:303-313), wording included, so
+// that programs print the same text.
+void Sequential::summary() const {
+    std::printf("Sequential (%zu layers)\n", layers_.size());
+    size_t total = 0;
+    for (size_t i = 0; i < layers_.size(); ++i) {
+        const size_t n = layers_[i]->num_parameters();
+        total += n;
+        std::printf("  [%zu] %-32s%10zu parametros\n", i, layers_[i]->name().c_str(), n);
+    }
+    std::printf("  Total entrenable: %zu parametros\n", total);
 }
 
 Module& Sequential::at(size_t index) {

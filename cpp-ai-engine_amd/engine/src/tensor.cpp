@@ -266,16 +266,48 @@ std::string Tensor::shape_str() const {
     return os.str();
 }
 
+// The reference's console format (src/tensor_ops.cpp:762-805), so programs
+// that print tensors print the same text: the shape in brackets, then 1-D as
+// one bracketed row, 2-D as bracketed rows, higher ranks as one block broken
+// at the last axis, values in width 8 with 4 decimals; the gradient follows
+// when there is one.
 void Tensor::print(const std::string& name) const {
     if (!name.empty()) std::cout << name << " = ";
-    std::cout << "Tensor(shape=" << shape_str()
-              << ", requires_grad=" << (requires_grad() ? "true" : "false") << ")\n[ ";
+    std::cout << "Tensor(shape=[";
+    const std::vector<size_t>& sh = shape();
+    for (size_t i = 0; i < sh.size(); ++i) std::cout << (i ? ", " : "") << sh[i];
+    std::cout << "], requires_grad=" << (requires_grad() ? "true" : "false") << ")\n";
     const float* v = data();
-    for (size_t i = 0; i < size(); ++i) {
-        std::cout << std::setw(8) << std::fixed << std::setprecision(4) << v[i] << " ";
-        if (!shape().empty() && (i + 1) % shape().back() == 0 && i + 1 < size()) std::cout << "\n  ";
+    const auto value = [&](size_t i) -> std::ostream& {
+        return std::cout << std::setw(8) << std::fixed << std::setprecision(4) << v[i];
+    };
+    if (sh.size() == 1) {
+        std::cout << "[";
+        for (size_t i = 0; i < sh[0]; ++i) value(i) << (i + 1 < sh[0] ? ", " : "");
+        std::cout << "]\n";
+    } else if (sh.size() == 2) {
+        std::cout << "[\n";
+        for (size_t r = 0; r < sh[0]; ++r) {
+            std::cout << "  [";
+            for (size_t c = 0; c < sh[1]; ++c) value(r * sh[1] + c) << (c + 1 < sh[1] ? ", " : "");
+            std::cout << "]\n";
+        }
+        std::cout << "]\n";
+    } else if (size() > 0) {
+        std::cout << "[ ";
+        for (size_t i = 0; i < size(); ++i) {
+            value(i) << " ";
+            if ((i + 1) % sh.back() == 0 && i + 1 < size()) std::cout << "\n  ";
+        }
+        std::cout << "]\n";
+    } else {
+        std::cout << "[]\n";
     }
-    std::cout << "]\n";
+    if (has_grad()) {
+        std::cout << "  grad = \n";
+        grad().print("  gradientes");
+    }
+    std::cout << "\n";
 }
 
 // ------------------------------------------------------------------ reductions

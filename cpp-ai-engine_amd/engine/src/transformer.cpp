@@ -147,6 +147,8 @@ std::string Embedding::name() const {
 
 // Sinusoidal table, float std::pow/sin/cos on the host (src/transformer.cpp:249-267).
 Tensor positional_encoding(size_t seq_len, size_t d_model) {
+    if (seq_len == 0 || d_model == 0)
+        throw std::invalid_argument("positional_encoding needs a positive length and dimension.");
     std::vector<float> pe(seq_len * d_model);
     for (size_t pos = 0; pos < seq_len; ++pos)
         for (size_t i = 0; i < d_model; ++i) {
