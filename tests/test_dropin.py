@@ -17,8 +17,9 @@ against this repository's engine headers and linked with libengine_hip.so
   set, where chance is 16.7 %).
   charlm_demo is built but not run: it reads a corpus from the reference checkout, which
   the GPU box does not have.
-- The reference's autograd and Transformer unit suites (its tests/test_autograd.cpp and
-  tests/test_transformer.cpp), run through tests/dropin/suite_main.cpp: no check may fail.
+- The reference's autograd, convolution and Transformer unit suites (its
+  tests/test_autograd.cpp, test_conv.cpp and test_transformer.cpp), run through
+  tests/dropin/suite_main.cpp: no check may fail.
 
 The binaries are built in this container (they need the reference checkout) and travel
 with the tree; the tests skip where they were not built."""
