@@ -294,9 +294,26 @@ def cpu_matmul_threads(threads_list):
 
 # ------------------------------------------------------------------ cfg 2, cfg 3
 
+def graph_mode(make, timer, steps, warmup, eager_loss):
+    """The same training run with the trainer in graph mode (the second step captured into
+    one HIP graph, every later one a single replay): the same number of steps as the eager
+    leg, so the last loss must be the eager leg's, bit for bit."""
+    tr = make()
+    tr.set_graph(True)
+    tr.step()
+    total, per = timer.time_steps(tr.step, steps, warmup)
+    last = tr.loss()
+    tr.close()
+    sec = total / steps
+    return {"steps_per_s": round(1.0 / sec, 2), "ms_per_step": round(sec * 1e3, 4),
+            "median_ms_per_step": round(float(np.median(per)) * 1e3, 4),
+            "loss_last": round(last, 5), "loss_last_equals_eager": bool(last == eager_loss)}
+
+
 def cnn_leg(engine_mod, eng, timer, steps, warmup):
     x, labels, params = W.cnn_inputs()
-    tr = engine_mod.Trainer.cnn(eng, x, labels, params, lr=1e-3)
+    make = lambda: engine_mod.Trainer.cnn(eng, x, labels, params, lr=1e-3)  # noqa: E731
+    tr = make()
     tr.step()
     first = tr.loss()
     total, per = timer.time_steps(tr.step, steps, max(warmup - 1, 0))
@@ -306,7 +323,8 @@ def cnn_leg(engine_mod, eng, timer, steps, warmup):
     sec = total / steps
     return {"steps_per_s": round(1.0 / sec, 2), "ms_per_step": round(sec * 1e3, 4),
             "median_ms_per_step": round(float(np.median(per)) * 1e3, 4),
-            "loss_first_step": round(first, 5), "loss_last": round(last, 5)}
+            "loss_first_step": round(first, 5), "loss_last": round(last, 5),
+            "graph": graph_mode(make, timer, steps, max(warmup - 1, 0), last)}
 
 
 def cnn_dominant_kernel(eng, hip, timer, torch):
@@ -382,7 +400,9 @@ def charlm_leg(engine_mod, eng, timer, cpu_seconds):
     b, s, vocab, d, h, ff, layers = W.CHARLM_CFG3
     ids, targets = W.lm_inputs(LM_INPUT_SEED, b, s, vocab)
     params = W.lm_init_params(CFG5_PARAM_SEED, vocab, d, ff, layers)
-    tr = engine_mod.Trainer.charlm(eng, ids, targets, vocab, d, h, ff, layers, params, lr=1e-3)
+    make = lambda: engine_mod.Trainer.charlm(eng, ids, targets, vocab, d, h, ff,  # noqa: E731
+                                             layers, params, lr=1e-3)
+    tr = make()
     tr.step()
     first = tr.loss()
     total, per = timer.time_steps(tr.step, 100, 9)
@@ -394,7 +414,12 @@ def charlm_leg(engine_mod, eng, timer, cpu_seconds):
            "achieved_tflops": round(fl / sec / 1e12, 2),
            "frac_of_mfma_peak": round(fl / sec / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
            "loss_first_step": round(first, 5), "loss_last": round(tr.loss(), 5)}
+    eager_last = tr.loss()
     tr.close()
+    g = graph_mode(make, timer, 100, 9, eager_last)
+    g["achieved_tflops"] = round(fl * g["steps_per_s"] / 1e12, 2)
+    g["frac_of_mfma_peak"] = round(fl * g["steps_per_s"] / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)
+    rec["graph"] = g
     if cpu_seconds > 0:
         log("bench: reference CPU baseline, cfg3")
         cpu = cpu_charlm_baseline(ids, targets, (vocab, d, h, ff, layers), params, cpu_seconds)

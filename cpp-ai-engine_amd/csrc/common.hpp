@@ -27,7 +27,15 @@ int ready();
 int before_launch(const char* name);
 int after_launch(const char* name, hipStream_t stream);
 
-inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+// The stream of this thread's graph capture (ehip_graph_begin), or null. While
+// it is set, every call made with a null stream is recorded into the graph
+// instead of being queued on the null stream.
+extern thread_local hipStream_t t_capture;
+
+inline hipStream_t as_stream(void* s) {
+    return s != nullptr ? reinterpret_cast<hipStream_t>(s) : t_capture;
+}
+inline bool capturing() { return t_capture != nullptr; }
 
 // Grow-only device scratch owned by the library (never shrinks; replaced by a
 // larger block when asked for more). Work is ordered on one stream, so a

@@ -469,10 +469,22 @@ __device__ __forceinline__ void adam_chunk(const AdamSlot& s, int64_t b, float l
     for (int64_t i = tail + threadIdx.x; i < end; i += kThreads) op.scalar(i);
 }
 
+// lr, c1 and c2 come from the arguments, or from hyper[0..2] in device memory
+// when hyper is not null (a captured step whose replays change them).
+__device__ __forceinline__ void read_hyper(const float* hyper, float& lr, float& c1, float& c2) {
+    if (hyper != nullptr) {
+        lr = hyper[0];
+        c1 = hyper[1];
+        c2 = hyper[2];
+    }
+}
+
 template <bool NT>
 __global__ __launch_bounds__(kThreads) void adam_multi(const AdamSlot* __restrict__ slots,
                                                        int count, float lr, float b1, float b2,
-                                                       float eps, float wd, float c1, float c2) {
+                                                       float eps, float wd, float c1, float c2,
+                                                       const float* __restrict__ hyper) {
+    read_hyper(hyper, lr, c1, c2);
     const int64_t b = blockIdx.x;
     adam_chunk<NT, kUnroll>(find_slot(slots, count, b), b, lr, b1, b2, eps, wd, c1, c2);
 }
@@ -481,9 +493,20 @@ template <bool NT, int U>
 __global__ __launch_bounds__(kThreads) void adam_multi_inline(AdamInline table, int count,
                                                               float lr, float b1, float b2,
                                                               float eps, float wd, float c1,
-                                                              float c2) {
+                                                              float c2,
+                                                              const float* __restrict__ hyper) {
+    read_hyper(hyper, lr, c1, c2);
     const int64_t b = blockIdx.x;
     adam_chunk<NT, U>(find_slot(table.s, count, b), b, lr, b1, b2, eps, wd, c1, c2);
+}
+
+// Copies one argument-borne piece of a slot table to device memory (one
+// thread per slot): the table upload of a captured step, which can record no
+// host transfer.
+__global__ __launch_bounds__(kInlineSlots) void write_slots(AdamInline piece, int count,
+                                                            AdamSlot* __restrict__ dst) {
+    const int i = int(threadIdx.x);
+    if (i < count) dst[i] = piece.s[i];
 }
 
 // Adam over the multi-tensor table, launched together with the ordered sums
@@ -512,7 +535,9 @@ template <bool NT, int U>
 __global__ __launch_bounds__(kThreads) void adam_multi_reduce(ReduceAdamBatch rb, AdamInline table,
                                                               int count, float lr, float b1,
                                                               float b2, float eps, float wd,
-                                                              float c1, float c2) {
+                                                              float c1, float c2,
+                                                              const float* __restrict__ hyper) {
+    read_hyper(hyper, lr, c1, c2);
     __shared__ float lanes[256];
     if (int(blockIdx.x) < rb.blocks) {
         int j = 0;
@@ -543,6 +568,36 @@ __global__ __launch_bounds__(kThreads) void adam_multi_reduce(ReduceAdamBatch rb
     if (count == 0) return;
     const int64_t b = int64_t(blockIdx.x) - rb.blocks;
     adam_chunk<NT, U>(find_slot(table.s, count, b), b, lr, b1, b2, eps, wd, c1, c2);
+}
+
+// Up to kStoreMax floats carried in the kernel arguments, stored by one thread
+// each: a few values reach the device with one launch and no DMA transfer.
+constexpr int kStoreMax = 16;
+struct StoreValues {
+    float v[kStoreMax];
+};
+__global__ __launch_bounds__(64) void store_values(StoreValues vals, int count,
+                                                   float* __restrict__ dst) {
+    const int i = int(threadIdx.x);
+    if (i < count) dst[i] = vals.v[i];
+}
+
+int launch_write_slots(const AdamInline& piece, int n, AdamSlot* dst, hipStream_t s) {
+    EHIP_LAUNCH("adam_table", write_slots, dim3(1), dim3(kInlineSlots), 0, s, piece, n, dst);
+    return EHIP_OK;
+}
+
+// The table-driven update over `chunks` chunks of kAdamChunk elements.
+int launch_adam_table(const AdamSlot* table, int count, int64_t chunks, bool nt, float lr,
+                      float b1, float b2, float eps, float wd, float c1, float c2,
+                      const float* hyper, hipStream_t s) {
+    if (nt)
+        EHIP_LAUNCH("adam_multi", adam_multi<true>, dim3(unsigned(chunks)), dim3(kThreads), 0, s,
+                    table, count, lr, b1, b2, eps, wd, c1, c2, hyper);
+    else
+        EHIP_LAUNCH("adam_multi", adam_multi<false>, dim3(unsigned(chunks)), dim3(kThreads), 0, s,
+                    table, count, lr, b1, b2, eps, wd, c1, c2, hyper);
+    return EHIP_OK;
 }
 
 template <int OP>
@@ -651,6 +706,18 @@ int ehip_fill_f32(float* x, int64_t n, float value, void* stream) {
     return launch_stream("fill", Fill{x, value}, n, aligned16(x), as_stream(stream));
 }
 
+int ehip_store_f32(float* dst, const float* values, int count, void* stream) {
+    EHIP_READY();
+    if (count < 0 || count > kStoreMax)
+        return fail(EHIP_EINVAL, "store: %d values (at most %d)", count, kStoreMax);
+    if (count == 0) return EHIP_OK;
+    if (!dst || !values) return fail(EHIP_EINVAL, "store: null pointer");
+    StoreValues vals{};
+    std::memcpy(vals.v, values, size_t(count) * sizeof(float));
+    EHIP_LAUNCH("store", store_values, dim3(1), dim3(64), 0, as_stream(stream), vals, count, dst);
+    return EHIP_OK;
+}
+
 int ehip_scale_f32(float* x, int64_t n, float factor, void* stream) {
     EHIP_READY();
     if (!x && n > 0) return fail(EHIP_EINVAL, "scale: null pointer");
@@ -682,9 +749,9 @@ int ehip_adam_f32(float* p, const float* g, float* m, float* v, int64_t n, float
                          n, vec, as_stream(stream));
 }
 
-int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, float beta1,
-                        float beta2, float eps, float weight_decay, float bias_c1,
-                        float bias_c2, void* stream) {
+static int adam_multi_impl(const ehip_adam_tensor_t* tensors, int count, float lr, float beta1,
+                           float beta2, float eps, float weight_decay, float bias_c1,
+                           float bias_c2, const float* hyper, void* stream) {
     EHIP_READY();
     if (count < 0 || (count > 0 && tensors == nullptr))
         return fail(EHIP_EINVAL, "adam_multi: bad tensor list");
@@ -721,16 +788,37 @@ int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, 
         if (small)
             EHIP_LAUNCH("adam_multi", (adam_multi_inline<false, 1>), dim3(unsigned(chunks)),
                         dim3(kThreads), 0, s, inline_table, int(slots.size()), lr, beta1, beta2,
-                        eps, weight_decay, bias_c1, bias_c2);
+                        eps, weight_decay, bias_c1, bias_c2, hyper);
         else if (nt)
             EHIP_LAUNCH("adam_multi", (adam_multi_inline<true, kUnroll>), dim3(unsigned(chunks)),
                         dim3(kThreads), 0, s, inline_table, int(slots.size()), lr, beta1, beta2,
-                        eps, weight_decay, bias_c1, bias_c2);
+                        eps, weight_decay, bias_c1, bias_c2, hyper);
         else
             EHIP_LAUNCH("adam_multi", (adam_multi_inline<false, kUnroll>), dim3(unsigned(chunks)),
                         dim3(kThreads), 0, s, inline_table, int(slots.size()), lr, beta1, beta2,
-                        eps, weight_decay, bias_c1, bias_c2);
+                        eps, weight_decay, bias_c1, bias_c2, hyper);
         return EHIP_OK;
+    }
+    if (capturing() && s == t_capture) {
+        // A captured step: a table block of the graph's own, written by kernels
+        // whose arguments carry the slots; freed at once, the arena holds the
+        // block for the graph until it is destroyed.
+        const size_t bytes = slots.size() * sizeof(AdamSlot);
+        void* p = nullptr;
+        if (int rc = ehip_arena_alloc(bytes, &p)) return rc;
+        AdamSlot* tab = static_cast<AdamSlot*>(p);
+        int rc = EHIP_OK;
+        for (size_t at = 0; at < slots.size() && rc == EHIP_OK; at += kInlineSlots) {
+            const int n = int(std::min(slots.size() - at, size_t(kInlineSlots)));
+            AdamInline piece{};
+            std::memcpy(piece.s, slots.data() + at, size_t(n) * sizeof(AdamSlot));
+            rc = launch_write_slots(piece, n, tab + at, s);
+        }
+        if (rc == EHIP_OK)
+            rc = launch_adam_table(tab, int(slots.size()), chunks, nt, lr, beta1, beta2, eps,
+                                   weight_decay, bias_c1, bias_c2, hyper, s);
+        ehip_arena_free(p);
+        return rc;
     }
     // The slot table lives in a buffer of its own and is uploaded only when it
     // differs from the previous call's: an optimiser stepping the same
@@ -759,21 +847,31 @@ int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, 
         if (int rc = ehip_memcpy_h2d(table, slots.data(), bytes, stream)) return rc;
         last = slots;
     }
-    if (nt)
-        EHIP_LAUNCH("adam_multi", adam_multi<true>, dim3(unsigned(chunks)), dim3(kThreads), 0, s,
-                    table, int(slots.size()), lr, beta1, beta2, eps, weight_decay, bias_c1,
-                    bias_c2);
-    else
-        EHIP_LAUNCH("adam_multi", adam_multi<false>, dim3(unsigned(chunks)), dim3(kThreads), 0, s,
-                    table, int(slots.size()), lr, beta1, beta2, eps, weight_decay, bias_c1,
-                    bias_c2);
-    return EHIP_OK;
+    return launch_adam_table(table, int(slots.size()), chunks, nt, lr, beta1, beta2, eps,
+                             weight_decay, bias_c1, bias_c2, hyper, s);
 }
 
-int ehip_adam_multi_reduce_f32(const ehip_adam_tensor_t* tensors, int count,
-                               const ehip_conv_reduce_t* jobs, int njobs, float lr, float beta1,
-                               float beta2, float eps, float weight_decay, float bias_c1,
-                               float bias_c2, void* stream) {
+int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, float beta1,
+                        float beta2, float eps, float weight_decay, float bias_c1,
+                        float bias_c2, void* stream) {
+    return adam_multi_impl(tensors, count, lr, beta1, beta2, eps, weight_decay, bias_c1, bias_c2,
+                           nullptr, stream);
+}
+
+int ehip_adam_multi_dev_f32(const ehip_adam_tensor_t* tensors, int count, const float* hyper,
+                            float beta1, float beta2, float eps, float weight_decay,
+                            void* stream) {
+    if (hyper == nullptr) return fail(EHIP_EINVAL, "adam_multi_dev: null hyper-parameter array");
+    return adam_multi_impl(tensors, count, 0.0f, beta1, beta2, eps, weight_decay, 0.0f, 0.0f,
+                           hyper, stream);
+}
+
+
+static int adam_multi_reduce_impl(const ehip_adam_tensor_t* tensors, int count,
+                                  const ehip_conv_reduce_t* jobs, int njobs, float lr,
+                                  float beta1, float beta2, float eps, float weight_decay,
+                                  float bias_c1, float bias_c2, const float* hyper,
+                                  void* stream) {
     EHIP_READY();
     if (count < 0 || (count > 0 && tensors == nullptr) || njobs < 0 ||
         (njobs > 0 && jobs == nullptr))
@@ -782,8 +880,8 @@ int ehip_adam_multi_reduce_f32(const ehip_adam_tensor_t* tensors, int count,
     // Beyond one launch's job table: the separate reduction, then the step.
     if (njobs > kMaxReduceAdam) {
         if (int rc = ehip_conv_weight_reduce_f32(jobs, njobs, stream)) return rc;
-        return ehip_adam_multi_f32(tensors, count, lr, beta1, beta2, eps, weight_decay, bias_c1,
-                                   bias_c2, stream);
+        return adam_multi_impl(tensors, count, lr, beta1, beta2, eps, weight_decay, bias_c1,
+                               bias_c2, hyper, stream);
     }
     ReduceAdamBatch rb{};
     std::vector<char> owned(size_t(count), 0);
@@ -835,8 +933,8 @@ int ehip_adam_multi_reduce_f32(const ehip_adam_tensor_t* tensors, int count,
     if (total > (int64_t(1) << 20) || slots.size() > size_t(kInlineSlots)) {
         // A large model: the separate reduction, then the step.
         if (int rc = ehip_conv_weight_reduce_f32(jobs, njobs, stream)) return rc;
-        return ehip_adam_multi_f32(tensors, count, lr, beta1, beta2, eps, weight_decay, bias_c1,
-                                   bias_c2, stream);
+        return adam_multi_impl(tensors, count, lr, beta1, beta2, eps, weight_decay, bias_c1,
+                               bias_c2, hyper, stream);
     }
     AdamInline inline_table{};
     if (!slots.empty()) std::memcpy(inline_table.s, slots.data(), slots.size() * sizeof(AdamSlot));
@@ -844,8 +942,27 @@ int ehip_adam_multi_reduce_f32(const ehip_adam_tensor_t* tensors, int count,
     if (blocks + chunks > 0x7fffffff) return fail(EHIP_EINVAL, "adam_multi_reduce: too many blocks");
     EHIP_LAUNCH("adam_multi_reduce", (adam_multi_reduce<false, 1>), dim3(unsigned(blocks + chunks)),
                 dim3(kThreads), 0, s, rb, inline_table, int(slots.size()), lr, beta1, beta2, eps,
-                weight_decay, bias_c1, bias_c2);
+                weight_decay, bias_c1, bias_c2, hyper);
     return EHIP_OK;
 }
+
+int ehip_adam_multi_reduce_f32(const ehip_adam_tensor_t* tensors, int count,
+                               const ehip_conv_reduce_t* jobs, int njobs, float lr, float beta1,
+                               float beta2, float eps, float weight_decay, float bias_c1,
+                               float bias_c2, void* stream) {
+    return adam_multi_reduce_impl(tensors, count, jobs, njobs, lr, beta1, beta2, eps,
+                                  weight_decay, bias_c1, bias_c2, nullptr, stream);
+}
+
+int ehip_adam_multi_reduce_dev_f32(const ehip_adam_tensor_t* tensors, int count,
+                                   const ehip_conv_reduce_t* jobs, int njobs, const float* hyper,
+                                   float beta1, float beta2, float eps, float weight_decay,
+                                   void* stream) {
+    if (hyper == nullptr)
+        return fail(EHIP_EINVAL, "adam_multi_reduce_dev: null hyper-parameter array");
+    return adam_multi_reduce_impl(tensors, count, jobs, njobs, 0.0f, beta1, beta2, eps,
+                                  weight_decay, 0.0f, 0.0f, hyper, stream);
+}
+
 
 }  // extern "C"

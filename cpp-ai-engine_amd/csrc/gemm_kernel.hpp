@@ -313,10 +313,6 @@ __device__ __forceinline__ void mfma_stage_kc(floatx16 (&acc)[C::kFM][C::kFN], c
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool CHECK, bool EPI>
 __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kernel(GemmArgs g) {
     using C = Cfg<BM, BN, BK, WM, WN>;
-    // The launch uses exactly C::kThreads threads; stated so that the
-    // compiler drops the tile loaders' guards for thread counts that divide a
-    // tile evenly (no exec-mask branches inside the main loop).
-    __builtin_assume(threadIdx.x < unsigned(C::kThreads));
     constexpr bool KC = !TA && TB;  // both operands k-contiguous: [row][k] tiles
     constexpr int kFloatsA = KC ? BM * KcTile<BK>::kPitch : BK * C::kLdsA;
     constexpr int kFloatsB = KC ? BN * KcTile<BK>::kPitch : BK * C::kLdsB;

@@ -16,12 +16,17 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 namespace ehip {
+
+thread_local hipStream_t t_capture = nullptr;
+
 namespace {
 
 thread_local std::string g_error;
+thread_local uint64_t t_capture_graph = 0;  // serial of the graph this thread captures
 
 struct Context {
     bool ok = false;
@@ -104,7 +109,7 @@ int before_launch(const char* name) {
 
 int after_launch(const char* name, hipStream_t stream) {
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && g_sync_each) e = hipStreamSynchronize(stream);
+    if (e == hipSuccess && g_sync_each && !capturing()) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) {
         ++g_failed;
         return fail(EHIP_ELAUNCH, "%s: %s", name, hipGetErrorString(e));
@@ -117,10 +122,21 @@ int after_launch(const char* name, hipStream_t stream) {
 
 namespace {
 
+// The blocks a captured graph may touch: every block live when its capture
+// began and every block handed out while it ran. Such a block, once freed, is
+// held for the graph (replays still write or read it) instead of going back to
+// the cache, until the graph is destroyed; allocations made during the capture
+// itself reuse the graph's held blocks first.
+struct GraphPool {
+    std::unordered_set<void*> touched;
+    std::unordered_map<size_t, std::vector<void*>> held;  // class size -> freed blocks
+};
+
 struct Arena {
     std::mutex mu;
     std::unordered_map<size_t, std::vector<void*>> cache;  // class size -> free blocks
     std::unordered_map<void*, size_t> live;                // block -> class size
+    std::unordered_map<uint64_t, GraphPool> graphs;        // graph serial -> its blocks
     ehip_arena_stats_t stats{};
 };
 
@@ -213,6 +229,7 @@ int ehip_device_info(ehip_device_info_t* out) {
 
 int ehip_synchronize(void) {
     if (int rc = ehip_init()) return rc;
+    if (capturing()) return fail(EHIP_EINVAL, "synchronize: not allowed during a graph capture");
     hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) return fail(EHIP_ELAUNCH, "synchronize: %s", hipGetErrorString(e));
     return EHIP_OK;
@@ -220,6 +237,8 @@ int ehip_synchronize(void) {
 
 int ehip_stream_synchronize(void* stream) {
     if (int rc = ehip_init()) return rc;
+    if (stream == nullptr && capturing())
+        return fail(EHIP_EINVAL, "stream synchronize: not allowed during a graph capture");
     hipError_t e = hipStreamSynchronize(as_stream(stream));
     if (e != hipSuccess) return fail(EHIP_ELAUNCH, "stream synchronize: %s", hipGetErrorString(e));
     return EHIP_OK;
@@ -255,6 +274,24 @@ int ehip_arena_alloc(size_t bytes, void** out) {
     Arena& a = arena();
     std::lock_guard<std::mutex> lock(a.mu);
     ++a.stats.allocations;
+    GraphPool* pool = nullptr;
+    if (t_capture_graph != 0) {
+        auto g = a.graphs.find(t_capture_graph);
+        if (g != a.graphs.end()) pool = &g->second;
+    }
+    if (pool != nullptr) {
+        auto h = pool->held.find(cls);
+        if (h != pool->held.end() && !h->second.empty()) {
+            void* p = h->second.back();
+            h->second.pop_back();
+            a.live[p] = cls;
+            a.stats.bytes_cached -= cls;
+            a.stats.bytes_graph_held -= cls;
+            a.stats.bytes_in_use += cls;
+            *out = p;
+            return EHIP_OK;
+        }
+    }
     auto it = a.cache.find(cls);
     if (it != a.cache.end() && !it->second.empty()) {
         void* p = it->second.back();
@@ -262,6 +299,7 @@ int ehip_arena_alloc(size_t bytes, void** out) {
         a.live[p] = cls;
         a.stats.bytes_cached -= cls;
         a.stats.bytes_in_use += cls;
+        if (pool != nullptr) pool->touched.insert(p);
         *out = p;
         return EHIP_OK;
     }
@@ -280,6 +318,7 @@ int ehip_arena_alloc(size_t bytes, void** out) {
     a.stats.bytes_reserved += cls;
     a.stats.bytes_in_use += cls;
     a.live[p] = cls;
+    if (pool != nullptr) pool->touched.insert(p);
     *out = p;
     return EHIP_OK;
 }
@@ -295,13 +334,27 @@ void ehip_arena_free(void* ptr) {
     }
     const size_t cls = it->second;
     a.live.erase(it);
-    a.cache[cls].push_back(ptr);
     a.stats.bytes_in_use -= cls;
     a.stats.bytes_cached += cls;
+    // Held for the newest graph that may touch the block, if any.
+    GraphPool* keep = nullptr;
+    uint64_t newest = 0;
+    for (auto& g : a.graphs)
+        if (g.first > newest && g.second.touched.count(ptr) != 0) {
+            newest = g.first;
+            keep = &g.second;
+        }
+    if (keep != nullptr) {
+        keep->held[cls].push_back(ptr);
+        a.stats.bytes_graph_held += cls;
+        return;
+    }
+    a.cache[cls].push_back(ptr);
 }
 
 int ehip_arena_trim(void) {
     if (int rc = ehip_init()) return rc;
+    if (capturing()) return fail(EHIP_EINVAL, "ehip_arena_trim: not allowed during a graph capture");
     Arena& a = arena();
     std::lock_guard<std::mutex> lock(a.mu);
     release_cache(a);
@@ -391,6 +444,8 @@ int copy(void* dst, const void* src, size_t bytes, void* stream, hipMemcpyKind k
     if (dst == nullptr || src == nullptr) return fail(EHIP_EINVAL, "memcpy: null pointer");
     const auto t0 = std::chrono::steady_clock::now();
     hipStream_t s = as_stream(stream);
+    if (capturing() && s == t_capture && kind != hipMemcpyDeviceToDevice)
+        return fail(EHIP_EINVAL, "memcpy: a host transfer cannot be recorded into a graph");
     bool staged = false;
     hipError_t e = hipSuccess;
     if (kind == hipMemcpyHostToDevice) e = staged_upload(dst, src, bytes, s, &staged);
@@ -429,6 +484,149 @@ int ehip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
 }
 int ehip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
     return copy(dst, src, bytes, stream, hipMemcpyDeviceToDevice);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ graphs
+
+namespace {
+
+std::atomic<uint64_t> g_graph_serial{0};
+thread_local hipStream_t t_capture_owned = nullptr;  // the stream this thread captures on
+
+struct Graph {
+    hipGraphExec_t exec = nullptr;
+    uint64_t serial = 0;
+};
+
+// Hands a graph's held blocks to the next graph that may touch them, or back
+// to the cache, and forgets the graph. Caller holds no lock.
+void release_pool(uint64_t serial) {
+    Arena& a = arena();
+    std::lock_guard<std::mutex> lock(a.mu);
+    auto it = a.graphs.find(serial);
+    if (it == a.graphs.end()) return;
+    GraphPool pool = std::move(it->second);
+    a.graphs.erase(it);
+    for (auto& kv : pool.held)
+        for (void* p : kv.second) {
+            GraphPool* next = nullptr;
+            uint64_t newest = 0;
+            for (auto& g : a.graphs)
+                if (g.first > newest && g.second.touched.count(p) != 0) {
+                    newest = g.first;
+                    next = &g.second;
+                }
+            if (next != nullptr) {
+                next->held[kv.first].push_back(p);
+            } else {
+                a.cache[kv.first].push_back(p);
+                a.stats.bytes_graph_held -= kv.first;
+            }
+        }
+}
+
+void end_capture_state() {
+    t_capture = nullptr;
+    t_capture_graph = 0;
+    if (t_capture_owned != nullptr) (void)hipStreamDestroy(t_capture_owned);
+    t_capture_owned = nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ehip_graph_begin(void) {
+    EHIP_READY();
+    if (capturing()) return fail(EHIP_EINVAL, "ehip_graph_begin: this thread is already capturing");
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) return fail(EHIP_ELAUNCH, "ehip_graph_begin: %s", hipGetErrorString(e));
+    const uint64_t serial = ++g_graph_serial;
+    {
+        Arena& a = arena();
+        std::lock_guard<std::mutex> lock(a.mu);
+        GraphPool& pool = a.graphs[serial];
+        pool.touched.reserve(a.live.size() * 2 + 64);
+        for (const auto& kv : a.live) pool.touched.insert(kv.first);
+    }
+    e = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(s);
+        release_pool(serial);
+        return fail(EHIP_ELAUNCH, "ehip_graph_begin: %s", hipGetErrorString(e));
+    }
+    t_capture = s;
+    t_capture_owned = s;
+    t_capture_graph = serial;
+    return EHIP_OK;
+}
+
+int ehip_graph_end(void** graph) {
+    if (graph != nullptr) *graph = nullptr;
+    if (!capturing()) return fail(EHIP_EINVAL, "ehip_graph_end: no capture in progress");
+    const uint64_t serial = t_capture_graph;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(t_capture, &g);
+    end_capture_state();
+    hipGraphExec_t exec = nullptr;
+    if (e == hipSuccess && graph == nullptr) e = hipErrorInvalidValue;
+    if (e == hipSuccess) e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    if (g != nullptr) (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        release_pool(serial);
+        return fail(EHIP_ELAUNCH, "ehip_graph_end: %s", hipGetErrorString(e));
+    }
+    *graph = new Graph{exec, serial};
+    return EHIP_OK;
+}
+
+int ehip_graph_abort(void) {
+    if (!capturing()) return EHIP_OK;
+    const uint64_t serial = t_capture_graph;
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(t_capture, &g);
+    (void)hipGetLastError();
+    end_capture_state();
+    if (g != nullptr) (void)hipGraphDestroy(g);
+    release_pool(serial);
+    return EHIP_OK;
+}
+
+int ehip_capturing(void) { return capturing() ? 1 : 0; }
+
+int ehip_graph_launch(void* graph, void* stream) {
+    EHIP_READY();
+    if (graph == nullptr) return fail(EHIP_EINVAL, "ehip_graph_launch: null graph");
+    if (capturing()) return fail(EHIP_EINVAL, "ehip_graph_launch: not allowed during a capture");
+    if (int rc = before_launch("graph")) return rc;
+    hipError_t e = hipGraphLaunch(static_cast<Graph*>(graph)->exec, as_stream(stream));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        ++g_failed;
+        return fail(EHIP_ELAUNCH, "ehip_graph_launch: %s", hipGetErrorString(e));
+    }
+    ++g_launched;
+    if (g_sync_each) {
+        e = hipStreamSynchronize(as_stream(stream));
+        if (e != hipSuccess) return fail(EHIP_ELAUNCH, "graph: %s", hipGetErrorString(e));
+    }
+    return EHIP_OK;
+}
+
+int ehip_graph_destroy(void* graph) {
+    if (graph == nullptr) return EHIP_OK;
+    if (capturing()) return fail(EHIP_EINVAL, "ehip_graph_destroy: not allowed during a capture");
+    Graph* g = static_cast<Graph*>(graph);
+    hipError_t e = hipDeviceSynchronize();  // the last replay has finished with the blocks
+    if (g->exec != nullptr) (void)hipGraphExecDestroy(g->exec);
+    release_pool(g->serial);
+    delete g;
+    if (e != hipSuccess) return fail(EHIP_ELAUNCH, "ehip_graph_destroy: %s", hipGetErrorString(e));
+    return EHIP_OK;
 }
 
 }  // extern "C"

@@ -43,7 +43,8 @@ class DeviceInfo(C.Structure):
 
 class ArenaStats(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in ("bytes_in_use", "bytes_cached", "bytes_reserved",
-                                         "allocations", "driver_allocations")]
+                                         "allocations", "driver_allocations",
+                                         "bytes_graph_held")]
 
 
 class TransferStats(C.Structure):
@@ -98,12 +99,18 @@ _SIGS = {
     "ehip_add_backward_f32": [_vp, _vp, _vp, _i64, _i, _i, _vp],
     "ehip_mul_backward_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _vp],
     "ehip_fill_f32": [_vp, _i64, _f, _vp],
+    "ehip_store_f32": [_vp, _vp, _i, _vp],
     "ehip_scale_f32": [_vp, _i64, _f, _vp],
     "ehip_sgd_f32": [_vp, _vp, _vp, _i64, _f, _f, _f, _vp],
     "ehip_adam_f32": [_vp, _vp, _vp, _vp, _i64] + [_f] * 7 + [_vp],
     "ehip_adam_multi_f32": [C.POINTER(AdamTensor), _i] + [_f] * 7 + [_vp],
     "ehip_adam_multi_reduce_f32": [C.POINTER(AdamTensor), _i, C.POINTER(ConvReduce), _i] +
                                   [_f] * 7 + [_vp],
+    "ehip_adam_multi_dev_f32": [C.POINTER(AdamTensor), _i, _vp] + [_f] * 4 + [_vp],
+    "ehip_adam_multi_reduce_dev_f32": [C.POINTER(AdamTensor), _i, C.POINTER(ConvReduce), _i,
+                                       _vp] + [_f] * 4 + [_vp],
+    "ehip_graph_begin": [], "ehip_graph_end": [C.POINTER(_vp)], "ehip_graph_abort": [],
+    "ehip_capturing": [], "ehip_graph_launch": [_vp, _vp], "ehip_graph_destroy": [_vp],
     "ehip_permute_f32": [_vp, _vp, _i, C.POINTER(_i64), C.POINTER(_i64), _vp],
     "ehip_transpose_f32": [_vp, _vp, _i64, _i64, _i64, _vp],
     "ehip_im2col_f32": [_vp, _vp, C.POINTER(Window), _vp],

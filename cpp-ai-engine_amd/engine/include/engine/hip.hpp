@@ -5,6 +5,7 @@
 #define ENGINE_HIP_HPP
 
 #include <cstddef>
+#include <functional>
 #include <optional>
 #include <string>
 
@@ -41,6 +42,31 @@ void reset_transfer_stats();
 
 // Throws std::runtime_error carrying ehip_last_error() when rc != 0.
 void check(int rc, const char* what);
+
+// A sequence of engine calls captured once and replayed with one launch (the
+// ehip_graph_* calls; no counterpart in the reference, whose steps are host
+// loops of launches). capture() runs `body` with every launch of this thread
+// recorded instead of run; if body throws, the capture is dropped and the
+// exception passed on. Kernel arguments are fixed by the capture: each
+// launch() reads and writes the buffers the capture saw, and the device
+// allocator keeps them reserved until reset() or destruction. Values that
+// change between replays must be read from device memory (Adam's
+// set_device_scalars). Host transfers and synchronisation are refused inside
+// body.
+class Graph {
+public:
+    Graph() = default;
+    ~Graph();
+    Graph(const Graph&) = delete;
+    Graph& operator=(const Graph&) = delete;
+    void capture(const std::function<void()>& body);
+    void launch();
+    void reset();
+    bool ready() const noexcept { return handle_ != nullptr; }
+
+private:
+    void* handle_ = nullptr;
+};
 
 }  // namespace hip
 }  // namespace engine

@@ -50,6 +50,15 @@ public:
     // optimizer's buffers); set_state() copies them back (shapes must match).
     std::vector<Tensor> state_tensors() const;
     void set_state(size_t t, const std::vector<Tensor>& moments);
+    // For a step captured into a hip::Graph (an engine extension): while on,
+    // step() launches an update that reads the step size and both bias
+    // corrections from a device array and leaves the step count alone;
+    // prepare_replay() computes the next step's three values on the host with
+    // step()'s own arithmetic, uploads them and advances the count, before
+    // each launch of the captured step. The moments are device-resident after
+    // it, as after step().
+    void set_device_scalars(bool on);
+    void prepare_replay();
 
 private:
     float beta1_;
@@ -59,6 +68,8 @@ private:
     size_t t_ = 0;
     std::vector<Storage> m_;
     std::vector<Storage> v_;
+    bool device_scalars_ = false;
+    Storage hyper_;  // {lr, bias_c1, bias_c2} on the device
 };
 
 // Scales every gradient by max_norm / total_norm when the global L2 norm

@@ -135,14 +135,61 @@ struct Trainer {
     size_t rows = 0, classes = 0;
     Tensor loss;
 
+    // Graph mode: the second step is captured into a hip::Graph (the first
+    // runs eagerly and creates the optimiser state), later steps refresh
+    // Adam's device scalars and replay it with one launch.
+    bool use_graph = false;
+    size_t steps_run = 0;
+    engine::hip::Graph graph;
+    std::vector<Tensor> graph_params;
+
     std::vector<Tensor> parameters() { return cnn ? cnn->parameters() : lm->parameters(); }
 
-    void step() {
+    void eager_step() {
         opt->zero_grad();
         Tensor logits = cnn ? (*cnn)(x) : lm->forward(x, mask).reshape({rows, classes});
         loss = nn::cross_entropy_loss(logits, device_labels);
         loss.backward();
         opt->step();
+    }
+
+    void step() {
+        if (!use_graph || steps_run == 0) {
+            eager_step();
+            ++steps_run;
+            return;
+        }
+        if (!graph.ready()) {
+            opt->set_device_scalars(true);
+            try {
+                graph.capture([&] { eager_step(); });
+            } catch (...) {
+                opt->set_device_scalars(false);
+                use_graph = false;
+                throw;
+            }
+            graph_params = parameters();
+        }
+        opt->prepare_replay();
+        graph.launch();
+        // The replay rewrote these on the device behind the host's back.
+        for (Tensor& p : graph_params) {
+            (void)p.storage().device_write();
+            if (p.has_grad()) (void)p.get_impl()->grad->storage.device_write();
+        }
+        (void)loss.storage().device_write();
+        ++steps_run;
+    }
+
+    void drop_graph() {
+        graph.reset();
+        graph_params.clear();
+        opt->set_device_scalars(false);
+    }
+
+    void set_graph(bool on) {
+        if (!on && graph.ready()) drop_graph();
+        use_graph = on;
     }
 };
 
@@ -790,6 +837,8 @@ int eng_trainer_save(void* h, const char* params_path, const char* opt_path) {
 int eng_trainer_load(void* h, const char* params_path, const char* opt_path) {
     return guarded([&] {
         Trainer* t = static_cast<Trainer*>(h);
+        // New values may come in new buffers: a captured step is taken again.
+        if (t->graph.ready()) t->drop_graph();
         if (t->cnn) {
             engine::load_parameters(*t->cnn, params_path, true);
         } else {
@@ -802,6 +851,11 @@ int eng_trainer_load(void* h, const char* params_path, const char* opt_path) {
 
 int eng_trainer_step(void* h) {
     return guarded([&] { static_cast<Trainer*>(h)->step(); });
+}
+
+// Graph mode on (1) or off (0): see Trainer::step. Off drops the captured step.
+int eng_trainer_set_graph(void* h, int on) {
+    return guarded([&] { static_cast<Trainer*>(h)->set_graph(on != 0); });
 }
 
 int eng_trainer_loss(void* h, float* loss) {

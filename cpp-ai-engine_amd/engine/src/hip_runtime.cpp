@@ -29,6 +29,31 @@ std::optional<DeviceInfo> device_info() {
 }
 
 void synchronize() { check(ehip_synchronize(), "synchronize"); }
+
+Graph::~Graph() { (void)ehip_graph_destroy(handle_); }
+
+void Graph::capture(const std::function<void()>& body) {
+    reset();
+    check(ehip_graph_begin(), "graph capture");
+    try {
+        body();
+    } catch (...) {
+        (void)ehip_graph_abort();
+        throw;
+    }
+    check(ehip_graph_end(&handle_), "graph capture");
+}
+
+void Graph::launch() {
+    if (handle_ == nullptr) throw std::logic_error("Graph::launch: nothing captured");
+    check(ehip_graph_launch(handle_, nullptr), "graph launch");
+}
+
+void Graph::reset() {
+    void* h = handle_;
+    handle_ = nullptr;
+    check(ehip_graph_destroy(h), "graph destroy");
+}
 size_t kernels_launched() { return size_t(ehip_kernels_launched()); }
 size_t kernels_failed() { return size_t(ehip_kernels_failed()); }
 void reset_kernel_counters() { ehip_reset_counters(); }

@@ -80,15 +80,47 @@ void Adam::step() {
         table.push_back({p.storage().device_mut(), g, m_[i].device_mut(), v_[i].device_mut(),
                          int64_t(p.size())});
     }
-    const int rc =
-        jobs.empty()
-            ? ehip_adam_multi_f32(table.data(), int(table.size()), lr_, beta1_, beta2_, eps_,
-                                  weight_decay_, bias_c1, bias_c2, nullptr)
-            : ehip_adam_multi_reduce_f32(table.data(), int(table.size()), jobs.data(),
-                                         int(jobs.size()), lr_, beta1_, beta2_, eps_,
-                                         weight_decay_, bias_c1, bias_c2, nullptr);
+    int rc;
+    if (device_scalars_) {
+        const float* h = hyper_.device();
+        rc = jobs.empty()
+                 ? ehip_adam_multi_dev_f32(table.data(), int(table.size()), h, beta1_, beta2_,
+                                           eps_, weight_decay_, nullptr)
+                 : ehip_adam_multi_reduce_dev_f32(table.data(), int(table.size()), jobs.data(),
+                                                  int(jobs.size()), h, beta1_, beta2_, eps_,
+                                                  weight_decay_, nullptr);
+    } else {
+        rc = jobs.empty()
+                 ? ehip_adam_multi_f32(table.data(), int(table.size()), lr_, beta1_, beta2_, eps_,
+                                       weight_decay_, bias_c1, bias_c2, nullptr)
+                 : ehip_adam_multi_reduce_f32(table.data(), int(table.size()), jobs.data(),
+                                              int(jobs.size()), lr_, beta1_, beta2_, eps_,
+                                              weight_decay_, bias_c1, bias_c2, nullptr);
+    }
     if (rc != EHIP_OK) keep.reset_outputs();
     hip::check(rc, "adam step");
+    if (!device_scalars_) t_ = t;
+}
+
+void Adam::set_device_scalars(bool on) {
+    if (on && hyper_.size() != 3) {
+        hyper_ = Storage(3, 0.0f);
+        (void)hyper_.device_write();
+    }
+    device_scalars_ = on;
+}
+
+void Adam::prepare_replay() {
+    if (!device_scalars_) throw std::logic_error("Adam::prepare_replay: device scalars are off");
+    const size_t t = t_ + 1;
+    const float vals[3] = {lr_, 1.0f - std::pow(beta1_, static_cast<float>(t)),
+                           1.0f - std::pow(beta2_, static_cast<float>(t))};
+    hip::check(ehip_store_f32(hyper_.device_write(), vals, 3, nullptr), "adam scalars");
+    // The launch that follows rewrites the moments on the device.
+    for (size_t i = 0; i < m_.size(); ++i) {
+        if (m_[i].resident_on_device()) (void)m_[i].device_write();
+        if (v_[i].resident_on_device()) (void)v_[i].device_write();
+    }
     t_ = t;
 }
 

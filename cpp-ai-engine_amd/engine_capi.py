@@ -56,6 +56,7 @@ def load_library(path=LIB_PATH):
                  "eng_trainer_num_params", "eng_trainer_destroy"):
         getattr(lib, name).argtypes = [C.c_void_p] + (
             [_f32p] if name in ("eng_trainer_loss", "eng_trainer_params") else [])
+    lib.eng_trainer_set_graph.argtypes = [C.c_void_p, C.c_int]
     lib.eng_trainer_num_params.restype = _i64
     lib.eng_trainer_destroy.restype = None
     return lib
@@ -467,6 +468,13 @@ class Trainer:
 
     def step(self):
         if self.lib.eng_trainer_step(self.h) != 0:
+            raise RuntimeError(self.lib.eng_last_error().decode())
+
+    def set_graph(self, on=True):
+        """Graph mode: the second step is captured into one HIP graph (the first runs eagerly
+        and creates the Adam state); every later step refreshes Adam's step size and bias
+        corrections in device memory and replays the graph with one launch."""
+        if self.lib.eng_trainer_set_graph(self.h, int(bool(on))) != 0:
             raise RuntimeError(self.lib.eng_last_error().decode())
 
     def loss(self):

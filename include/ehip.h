@@ -130,8 +130,41 @@ typedef struct {
     uint64_t bytes_reserved;   /* everything obtained from the driver */
     uint64_t allocations;      /* ehip_arena_alloc calls              */
     uint64_t driver_allocations; /* misses that reached hipMalloc    */
+    uint64_t bytes_graph_held; /* part of bytes_cached held for graphs */
 } ehip_arena_stats_t;
 void ehip_arena_stats(ehip_arena_stats_t* out);
+
+/* ------------------------------------------------------------ graph capture */
+
+/* Captures a sequence of library calls as one HIP graph and replays it with a
+ * single launch. No counterpart in the reference, whose training step is a
+ * host loop of launches (src/optim.cpp:113-162, src/autograd.cpp): these are
+ * for launch-bound steps (a small model's forward, backward and update).
+ *
+ * ehip_graph_begin() starts recording on a non-blocking stream of the calling
+ * thread: from then on every call of this thread made with a NULL stream is
+ * recorded into the graph instead of being run (calls naming a stream of
+ * their own still go to it). Refused while capturing: host-to-device and
+ * device-to-host copies on the capture, ehip_synchronize, ehip_arena_trim and
+ * nested captures (each returns EHIP_EINVAL and leaves the capture going).
+ * ehip_graph_end() stops recording and instantiates the graph into *graph;
+ * ehip_graph_abort() drops a capture. ehip_graph_launch() replays it on
+ * `stream` (NULL: the null stream, ordered with the library's other work), and
+ * ehip_graph_destroy() waits for the device and frees it.
+ *
+ * Kernel arguments (pointers, sizes, scalars) are fixed at capture time: a
+ * replay reads and writes the same buffers. The arena keeps those buffers
+ * valid: a block live when the capture began, or handed out during it, is
+ * held for the graph once freed (not handed to anyone else) until the graph
+ * is destroyed. Values a replay must see change (Adam's step size and bias
+ * corrections) are read from device memory instead (ehip_adam_multi_dev_f32).
+ */
+int ehip_graph_begin(void);
+int ehip_graph_end(void** graph);
+int ehip_graph_abort(void);
+int ehip_capturing(void);
+int ehip_graph_launch(void* graph, void* stream);
+int ehip_graph_destroy(void* graph);
 
 /* Copies of `bytes` bytes (cuda::detail::copy_to_device/copy_to_host/
  * copy_device_to_device, include/engine/cuda.hpp:231-236). All three are
@@ -316,6 +349,13 @@ int ehip_add_backward_f32(const float* g, float* da, float* db, int64_t n, int a
 /* x[i] = value. A kernel, not a memset, so it is safe inside graph capture. */
 int ehip_fill_f32(float* x, int64_t n, float value, void* stream);
 
+/* dst[i] = values[i] for i < count <= 16, `values` a HOST array whose floats
+ * travel in the kernel's arguments: a handful of values stored with one
+ * launch and no host-to-device transfer, so also recordable into a graph.
+ * No counterpart in the reference; it sets the device scalars of a captured
+ * step (Adam's step size and bias corrections) before each replay. */
+int ehip_store_f32(float* dst, const float* values, int count, void* stream);
+
 /* x *= factor in place. cuda::ops::scale_in_place (cuda_ops.hpp:144). */
 int ehip_scale_f32(float* x, int64_t n, float factor, void* stream);
 
@@ -352,6 +392,18 @@ typedef struct {
 int ehip_adam_multi_f32(const ehip_adam_tensor_t* tensors, int count, float lr, float beta1,
                         float beta2, float eps, float weight_decay, float bias_c1,
                         float bias_c2, void* stream);
+
+/* ehip_adam_multi_f32 with lr, bias_c1 and bias_c2 read by the kernel from the
+ * DEVICE array hyper[3] = {lr, bias_c1, bias_c2} when it runs, so that a
+ * captured graph (ehip_graph_begin) takes each replay's values from memory the
+ * host refreshes before the launch. The same bits as ehip_adam_multi_f32 given
+ * the same three values. No counterpart in the reference (whose Adam::step,
+ * src/optim.cpp:113-162, passes them by value); for captured training steps.
+ * Tables beyond 48 tensors are written by kernels whose arguments carry them,
+ * so a capture records no host transfer. */
+int ehip_adam_multi_dev_f32(const ehip_adam_tensor_t* tensors, int count, const float* hyper,
+                            float beta1, float beta2, float eps, float weight_decay,
+                            void* stream);
 
 /* ------------------------------------------------------ layout and index maps */
 
@@ -530,6 +582,13 @@ int ehip_adam_multi_reduce_f32(const ehip_adam_tensor_t* tensors, int count,
                                const ehip_conv_reduce_t* jobs, int njobs, float lr, float beta1,
                                float beta2, float eps, float weight_decay, float bias_c1,
                                float bias_c2, void* stream);
+/* ehip_adam_multi_reduce_f32 with lr, bias_c1 and bias_c2 read from the
+ * DEVICE array hyper[3], as ehip_adam_multi_dev_f32 (for captured steps; no
+ * counterpart in the reference). */
+int ehip_adam_multi_reduce_dev_f32(const ehip_adam_tensor_t* tensors, int count,
+                                   const ehip_conv_reduce_t* jobs, int njobs, const float* hyper,
+                                   float beta1, float beta2, float eps, float weight_decay,
+                                   void* stream);
 
 /* out[i] = x[idx[i]] row by row (rows of row_size floats); an index outside
  * [0, n_rows) yields a row of NaN instead of a read out of bounds.
