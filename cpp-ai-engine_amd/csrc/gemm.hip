@@ -139,6 +139,9 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s,
     g.k_chunk = ceil_div(ceil_div(g.k, splits), BK) * BK;
     splits = int(ceil_div(g.k, g.k_chunk));
     g.splits = splits;
+    // Unstored tiles would leave their split-K partials unwritten for the
+    // reduction to read: split products store them as mode 1 does.
+    if (splits > 1 && g.causal == 4) g.causal = 1;
     float* out = g.c;
     g.ws_stride = batch * g.m * g.n + (g.colsum ? g.n : 0);
     if (splits > 1) {
@@ -608,7 +611,7 @@ int check_desc(const ehip_gemm_ex_t& d) {
         return fail(EHIP_EINVAL, "gemm: bad addend geometry");
     if (d.colsum_b && (d.batch != 1 || d.trans_b))
         return fail(EHIP_EINVAL, "gemm: column sums need batch 1 and a K x N B");
-    if (d.causal < 0 || d.causal > 3) return fail(EHIP_EINVAL, "gemm: causal mode %d", d.causal);
+    if (d.causal < 0 || d.causal > 4) return fail(EHIP_EINVAL, "gemm: causal mode %d", d.causal);
     if (d.batch > 65535) return fail(EHIP_EINVAL, "gemm: batch %lld > 65535", (long long)d.batch);
     if (d.m > (int64_t(1) << 31) || d.n > (int64_t(1) << 31))
         return fail(EHIP_EINVAL, "gemm: extent beyond 2^31");

@@ -40,7 +40,7 @@ struct GemmArgs {
     int splits;        // K is cut into `splits` chunks of k_chunk (a multiple of BK)
     int64_t k_chunk;
     int vec;           // rows 16-byte aligned: checked loads may use float4 inside the edges
-    int causal;        // ehip_gemm_ex_t::causal: 0, or the skipping mode 1, 2 or 3
+    int causal;        // ehip_gemm_ex_t::causal: 0, or the skipping mode 1 to 4
 };
 
 // The element offset of product z's matrix.
@@ -354,6 +354,7 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
     if (k_end > g.k) k_end = g.k;
     // Causal skipping (modes of ehip_gemm_ex_t::causal); m0 and m0 + BM are
     // multiples of BK, so the K steps stay aligned.
+    if (g.causal == 4 && n0 >= m0 + BM) return;  // wholly above the diagonal: not stored
     if (g.causal == 1 && n0 >= m0 + BM) {
         k_end = k_begin;  // wholly above the diagonal: the epilogue of acc = 0
     } else if (g.causal == 2) {

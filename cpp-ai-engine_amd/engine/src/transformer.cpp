@@ -300,16 +300,16 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
     const int64_t sd = int64_t(S * D), ss = int64_t(S * S), hss = int64_t(H * S * S);
     const auto act = [&](const Tensor& t) { return HeadOperand{dptr(t), int64_t(D), sd, int64_t(hd)}; };
 
-    // With a causal mask: score tiles above the diagonal hold the mask value
-    // (their softmax is 0 either way), the softmax reads each row up to the
-    // diagonal only, and the products with the weights skip the zero blocks
-    // above it.
+    // With a causal mask: score tiles wholly above the diagonal are neither
+    // computed nor stored (the softmax reads each row up to the diagonal only
+    // and stores 0 past it), and the products with the weights skip the zero
+    // blocks above it.
     const bool causal = skippable_causal(mask, S);
     Tensor scores({B, H, S, S}, 0.0f, false);
     ehip_gemm_ex_t d = head_product(false, true, B, H, S, S, hd, act(query), act(key),
                                     dout(scores), int64_t(S), hss, ss);
     d.alpha = scale;
-    d.causal = causal ? 1 : 0;
+    d.causal = causal ? 4 : 0;
     if (mask != nullptr) {
         MaskPlan plan;
         mask_plan(*mask, B, H, S, plan);
@@ -356,9 +356,10 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
         Tensor ds({B, H, S, S}, 0.0f, false);  // dW, then dS in place
         ehip_gemm_ex_t d = head_product(false, true, B, H, S, S, hd, head(g), head(v), dout(ds),
                                         int64_t(S), hss, ss);
-        // Above the diagonal dW only meets W = 0 in the softmax backward:
-        // whole tiles there are stored as 0 instead of computed.
-        d.causal = causal ? 1 : 0;
+        // Above the diagonal dW only meets W = 0 in the softmax backward,
+        // which reads each row up to the diagonal and stores all of dS: whole
+        // tiles there are neither computed nor stored.
+        d.causal = causal ? 4 : 0;
         hip::check(ehip_gemm_ex_f32(&d, nullptr), "attention dW");
         hip::check(causal ? ehip_softmax_backward_scaled_causal_f32(dptr(weights), dptr(ds),
                                                                     dout(ds), int64_t(B * H * S),

@@ -256,7 +256,11 @@ int ehip_gemm_f32_noalloc(int trans_a, int trans_b, int64_t batch, int64_t m, in
  *   2  op(A)(i, k) = 0 whenever k > i: products past a tile's last row are
  *      skipped;
  *   3  op(A)(i, k) = 0 whenever k < i: products before a tile's first row are
- *      skipped.
+ *      skipped;
+ *   4  as 1, but tiles lying wholly above the diagonal are not stored at all
+ *      (their C elements keep whatever they held; where another kernel or a
+ *      split K computes the product they are stored as in mode 1), for a
+ *      consumer that never reads j > i: the causal softmax pair below.
  * Skipped products are exact zeros, so every result keeps its value (its bits,
  * but for the sign of a sum that is exactly zero) as long as the operands are
  * finite; 0 computes everything. Honoured by the staged MFMA tiles; the other

@@ -529,8 +529,26 @@ def test_causal_skipping_modes(hip, S, hd, bt):
     if S == 512:  # the staged tiles did skip: whole tiles above the diagonal hold the epilogue of 0
         assert np.all(s_skip[:, :128, 384:] == np.float32(-1e9))
         assert np.all(dp_skip[:, :128, 384:] == 0)
+    # Mode 4: mode 1's values on and below the diagonal; above it, tiles the staged
+    # kernels skip keep what C held (a sentinel here), the others mode 1's values.
+    sentinel = np.float32(12345.0)
+
+    def run4(a, b, **kw):
+        c = dev(np.full((bt, S, S), sentinel, np.float32))
+        d = desc(hip, False, True, bt, 1, S, S, hd, a, hd, sh, 0, b, hd, sh, 0, c, S, ss, 0, **kw)
+        d.causal = 4
+        hip.gemm_ex(d)
+        return host(c)
+
+    for got, want, what in ((run4(Q, Kd, alpha=scale, addend=M, ld_add=S, stride_add=0,
+                                  period=1), s_skip, "scores"),
+                            (run4(G, V), dp_skip, "dP")):
+        exact(got[:, below], want[:, below], f"{what} (mode 4) on and below the diagonal")
+        assert np.all((got[:, ~below] == want[:, ~below]) | (got[:, ~below] == sentinel)), what
+        if S == 512:
+            assert np.all(got[:, :128, 384:] == sentinel), f"{what}: whole tiles not stored"
     with pytest.raises(RuntimeError, match="causal"):
-        run(False, False, S, hd, S, P, S, ss, V, hd, sh, sh, hd, 4)
+        run(False, False, S, hd, S, P, S, ss, V, hd, sh, sh, hd, 5)
 
 
 @pytest.mark.parametrize("S,mats", [(512, 8), (64, 40), (300, 3), (1, 5), (2048, 2)])
