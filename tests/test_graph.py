@@ -159,6 +159,42 @@ def test_graph_refuses_host_work(hip):
     assert lib.ehip_graph_launch(None, None) != 0
 
 
+def test_graph_noalloc_split_gemm(hip):
+    """The allocation-free GEMM recorded into a graph (a caller it exists for): a split-K
+    product whose partials live in the library's fixed device array replays on new inputs
+    with the bits of the allocating call, also with eager allocation-free products using
+    the same array between the replays."""
+    import torch
+    print_case("graph-noalloc")
+    lib = hip.lib
+    m = n = 256
+    k = 4096  # four 128 x 128 tiles: K split sixteen ways
+    r = np.random.default_rng(9)
+    a = torch.from_numpy(r.standard_normal((k, m), dtype=np.float32)).cuda()
+    b = torch.from_numpy(r.standard_normal((k, n), dtype=np.float32)).cuda()
+    c, other = hip.f32((m, n)), hip.f32((m, n))
+    torch.cuda.synchronize()
+
+    def noalloc(out, x):
+        return lib.ehip_gemm_f32_noalloc(1, 0, 1, m, n, k, hip.p(x), m, 0, hip.p(b), n, 0, 0.0,
+                                         hip.p(out), n, 0, None)
+
+    hip.ok(lib.ehip_graph_begin(), "begin")
+    hip.ok(noalloc(c, a), "noalloc in capture")
+    g = ctypes.c_void_p()
+    hip.ok(lib.ehip_graph_end(ctypes.byref(g)), "end")
+    for rep in range(3):
+        a.copy_(torch.from_numpy(r.standard_normal((k, m), dtype=np.float32)))
+        torch.cuda.synchronize()
+        hip.ok(lib.ehip_graph_launch(g, None), "launch")
+        hip.ok(noalloc(other, b), "eager noalloc between replays")
+        want = hip.gemm(a, b, trans_a=True)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(c.cpu().numpy().view(np.uint32),
+                                      want.cpu().numpy().view(np.uint32), err_msg=f"replay {rep}")
+    hip.ok(lib.ehip_graph_destroy(g), "destroy")
+
+
 def _pair(eng, kind):
     from engine_capi import Trainer
     import workloads as W
