@@ -173,6 +173,122 @@ struct Relu {
     __device__ void scalar(int64_t i) const { y[i] = f(x[i], 0, 0); }
 };
 
+// Sigmoid, tanh and the tanh form of GELU, forward and backward, in the
+// reference's expressions (src/nn.cpp:154-198), evaluated in the same order;
+// expf and tanhf are the device library's, within a few ulp of the host's.
+constexpr float kGeluAlpha = 0.7978845608028654f;  // sqrt(2 / pi)
+constexpr float kGeluBeta = 0.044715f;
+
+template <int KIND>  // 0 sigmoid, 1 tanh, 2 GELU
+__device__ __forceinline__ float act_f(float x) {
+    if (KIND == 0) return (x >= 0.0f) ? 1.0f / (1.0f + expf(-x)) : expf(x) / (1.0f + expf(x));
+    if (KIND == 1) return tanhf(x);
+    return 0.5f * x * (1.0f + tanhf(kGeluAlpha * (x + kGeluBeta * x * x * x)));
+}
+
+// The derivative at x, given y = f(x).
+template <int KIND>
+__device__ __forceinline__ float act_d(float x, float v) {
+    if (KIND == 0) return v * (1.0f - v);
+    if (KIND == 1) return 1.0f - v * v;
+    const float inner = kGeluAlpha * (x + kGeluBeta * x * x * x);
+    const float t = tanhf(inner);
+    const float dinner = kGeluAlpha * (1.0f + 3.0f * kGeluBeta * x * x);
+    return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * dinner;
+}
+
+template <int KIND>
+struct Activation {
+    static constexpr int kIn = 1;
+    const float* x;
+    float* y;
+    static __device__ float f(float v, float, float) { return act_f<KIND>(v); }
+    template <bool NT>
+    __device__ void load(int64_t v, float4* r) const { r[0] = ld4<NT>(x, v); }
+    template <bool NT>
+    __device__ void store(int64_t v, const float4* r) const { st4<NT>(y, v, map4(f, r[0], r[0], r[0])); }
+    __device__ void scalar(int64_t i) const { y[i] = f(x[i], 0, 0); }
+};
+
+// dx = g * f'(x, y)
+template <int KIND>
+struct ActivationBackward {
+    static constexpr int kIn = 3;
+    const float* x;
+    const float* y;
+    const float* g;
+    float* dx;
+    static __device__ float f(float xv, float yv, float gv) { return gv * act_d<KIND>(xv, yv); }
+    template <bool NT>
+    __device__ void load(int64_t v, float4* r) const {
+        r[0] = ld4<NT>(x, v);
+        r[1] = ld4<NT>(y, v);
+        r[2] = ld4<NT>(g, v);
+    }
+    template <bool NT>
+    __device__ void store(int64_t v, const float4* r) const {
+        st4<NT>(dx, v, map4(f, r[0], r[1], r[2]));
+    }
+    __device__ void scalar(int64_t i) const { dx[i] = f(x[i], y[i], g[i]); }
+};
+
+// rows x len floats from src (row pitch sp) to dst (row pitch dp): the moves of
+// slice, concat and stack and of their backward passes. One workgroup per
+// (row, 1024-float chunk); float4 where every address allows.
+__global__ __launch_bounds__(256) void copy_rows(const float* __restrict__ src, int64_t sp,
+                                                 float* __restrict__ dst, int64_t dp, int64_t len,
+                                                 int64_t chunks, int vec) {
+    const int64_t row = int64_t(blockIdx.x) / chunks, c = int64_t(blockIdx.x) % chunks;
+    const float* s = src + row * sp;
+    float* d = dst + row * dp;
+    const int64_t begin = c * 1024, end = min(begin + 1024, len);
+    if (vec) {
+        const int64_t i = begin + 4 * int64_t(threadIdx.x);
+        if (i + 3 < end)
+            *reinterpret_cast<float4*>(d + i) = *reinterpret_cast<const float4*>(s + i);
+        else
+            for (int64_t j = i; j < end; ++j) d[j] = s[j];
+    } else {
+        for (int64_t i = begin + threadIdx.x; i < end; i += 256) d[i] = s[i];
+    }
+}
+
+// Maximum over the middle axis of (outer, axis_len, inner) and the axis index
+// of the first maximum, scanning in axis order with a strict > as the
+// reference does (src/tensor.cpp:383-424): a NaN first element stays the
+// maximum, a later NaN is never taken.
+__global__ __launch_bounds__(256) void max_axis(const float* __restrict__ x, float* __restrict__ y,
+                                                int32_t* __restrict__ arg, int64_t outer,
+                                                int64_t axis_len, int64_t inner) {
+    const int64_t k = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (k >= outer * inner) return;
+    const int64_t o = k / inner, i = k % inner;
+    const float* p = x + o * axis_len * inner + i;
+    float best = p[0];
+    int32_t best_a = 0;
+    for (int64_t a = 1; a < axis_len; ++a) {
+        const float v = p[a * inner];
+        if (v > best) {
+            best = v;
+            best_a = int32_t(a);
+        }
+    }
+    y[k] = best;
+    arg[k] = best_a;
+}
+
+// dx of max_axis: 0 + g at each winning position, 0 elsewhere.
+__global__ __launch_bounds__(256) void max_axis_backward(const float* __restrict__ g,
+                                                         const int32_t* __restrict__ arg,
+                                                         float* __restrict__ dx, int64_t outer,
+                                                         int64_t axis_len, int64_t inner) {
+    const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= outer * axis_len * inner) return;
+    const int64_t i = e % inner, a = (e / inner) % axis_len, o = e / (inner * axis_len);
+    const int64_t k = o * inner + i;
+    dx[e] = (arg[k] == a) ? 0.0f + g[k] : 0.0f;
+}
+
 struct ReluBackward {
     static constexpr int kIn = 2;
     const float* x;
@@ -640,6 +756,78 @@ int ehip_relu_f32(const float* x, float* y, int64_t n, void* stream) {
     EHIP_READY();
     if (!x || !y) return fail(EHIP_EINVAL, "relu: null pointer");
     return launch_stream("relu", Relu{x, y}, n, aligned16(x) && aligned16(y), as_stream(stream));
+}
+
+int ehip_activation_f32(int kind, const float* x, float* y, int64_t n, void* stream) {
+    EHIP_READY();
+    if (!x || !y) return fail(EHIP_EINVAL, "activation: null pointer");
+    const bool vec = aligned16(x) && aligned16(y);
+    hipStream_t s = as_stream(stream);
+    switch (kind) {
+        case EHIP_SIGMOID: return launch_stream("sigmoid", Activation<0>{x, y}, n, vec, s);
+        case EHIP_TANH: return launch_stream("tanh", Activation<1>{x, y}, n, vec, s);
+        case EHIP_GELU: return launch_stream("gelu", Activation<2>{x, y}, n, vec, s);
+        default: return fail(EHIP_EINVAL, "activation: kind %d", kind);
+    }
+}
+
+int ehip_activation_backward_f32(int kind, const float* x, const float* y, const float* g,
+                                 float* dx, int64_t n, void* stream) {
+    EHIP_READY();
+    if (!x || !y || !g || !dx) return fail(EHIP_EINVAL, "activation_backward: null pointer");
+    const bool vec = aligned16(x) && aligned16(y) && aligned16(g) && aligned16(dx);
+    hipStream_t s = as_stream(stream);
+    switch (kind) {
+        case EHIP_SIGMOID:
+            return launch_stream("sigmoid_backward", ActivationBackward<0>{x, y, g, dx}, n, vec, s);
+        case EHIP_TANH:
+            return launch_stream("tanh_backward", ActivationBackward<1>{x, y, g, dx}, n, vec, s);
+        case EHIP_GELU:
+            return launch_stream("gelu_backward", ActivationBackward<2>{x, y, g, dx}, n, vec, s);
+        default: return fail(EHIP_EINVAL, "activation_backward: kind %d", kind);
+    }
+}
+
+int ehip_copy_rows_f32(const float* src, int64_t src_pitch, float* dst, int64_t dst_pitch,
+                       int64_t rows, int64_t len, void* stream) {
+    EHIP_READY();
+    if (rows < 0 || len < 0 || src_pitch < len || dst_pitch < len)
+        return fail(EHIP_EINVAL, "copy_rows: bad geometry");
+    if (rows == 0 || len == 0) return EHIP_OK;
+    if (!src || !dst) return fail(EHIP_EINVAL, "copy_rows: null pointer");
+    const int64_t chunks = ceil_div(len, 1024);
+    if (rows * chunks > 0x7fffffff) return fail(EHIP_EINVAL, "copy_rows: too large");
+    const int vec = aligned16(src) && aligned16(dst) && src_pitch % 4 == 0 && dst_pitch % 4 == 0;
+    EHIP_LAUNCH("copy_rows", copy_rows, dim3(unsigned(rows * chunks)), dim3(256), 0,
+                as_stream(stream), src, src_pitch, dst, dst_pitch, len, chunks, vec);
+    return EHIP_OK;
+}
+
+int ehip_max_axis_f32(const float* x, float* y, int32_t* argmax, int64_t outer, int64_t axis_len,
+                      int64_t inner, void* stream) {
+    EHIP_READY();
+    if (outer < 0 || axis_len < 1 || inner < 0 || axis_len > 0x7fffffff)
+        return fail(EHIP_EINVAL, "max_axis: bad shape");
+    const int64_t n = outer * inner;
+    if (n == 0) return EHIP_OK;
+    if (!x || !y || !argmax) return fail(EHIP_EINVAL, "max_axis: null pointer");
+    if (ceil_div(n, 256) > 0x7fffffff) return fail(EHIP_EINVAL, "max_axis: too large");
+    EHIP_LAUNCH("max_axis", max_axis, dim3(unsigned(ceil_div(n, 256))), dim3(256), 0,
+                as_stream(stream), x, y, argmax, outer, axis_len, inner);
+    return EHIP_OK;
+}
+
+int ehip_max_axis_backward_f32(const float* g, const int32_t* argmax, float* dx, int64_t outer,
+                               int64_t axis_len, int64_t inner, void* stream) {
+    EHIP_READY();
+    if (outer < 0 || axis_len < 1 || inner < 0) return fail(EHIP_EINVAL, "max_axis_backward: bad shape");
+    const int64_t n = outer * axis_len * inner;
+    if (n == 0) return EHIP_OK;
+    if (!g || !argmax || !dx) return fail(EHIP_EINVAL, "max_axis_backward: null pointer");
+    if (ceil_div(n, 256) > 0x7fffffff) return fail(EHIP_EINVAL, "max_axis_backward: too large");
+    EHIP_LAUNCH("max_axis_backward", max_axis_backward, dim3(unsigned(ceil_div(n, 256))), dim3(256),
+                0, as_stream(stream), g, argmax, dx, outer, axis_len, inner);
+    return EHIP_OK;
 }
 
 int ehip_relu_backward_f32(const float* x, const float* g, float* dx, int64_t n, void* stream) {

@@ -100,6 +100,11 @@ _SIGS = {
     "ehip_mul_backward_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _vp],
     "ehip_fill_f32": [_vp, _i64, _f, _vp],
     "ehip_store_f32": [_vp, _vp, _i, _vp],
+    "ehip_activation_f32": [_i, _vp, _vp, _i64, _vp],
+    "ehip_activation_backward_f32": [_i, _vp, _vp, _vp, _vp, _i64, _vp],
+    "ehip_copy_rows_f32": [_vp, _i64, _vp, _i64, _i64, _i64, _vp],
+    "ehip_max_axis_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "ehip_max_axis_backward_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "ehip_scale_f32": [_vp, _i64, _f, _vp],
     "ehip_sgd_f32": [_vp, _vp, _vp, _i64, _f, _f, _f, _vp],
     "ehip_adam_f32": [_vp, _vp, _vp, _vp, _i64] + [_f] * 7 + [_vp],

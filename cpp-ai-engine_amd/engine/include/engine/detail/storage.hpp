@@ -18,6 +18,18 @@
 
 namespace engine {
 
+// Reuse statistics of the device buffer pool (the HBM arena), under the
+// reference's names (include/engine/detail/storage.hpp:36-46): `fresh` counts
+// allocations the pool could not serve from its free lists, `recycled` those
+// it could, `bytes_held` the cached free bytes.
+struct BufferPoolStats {
+    size_t fresh = 0;
+    size_t recycled = 0;
+    size_t bytes_held = 0;
+};
+
+BufferPoolStats buffer_pool_stats();
+
 class Storage {
 public:
     Storage() = default;

@@ -109,6 +109,27 @@ public:
     std::string name() const override { return "Softmax"; }
 };
 
+// The smooth activations (the reference's include/engine/nn.hpp:97-116):
+// element-wise kernels on the device, forward and backward.
+class Sigmoid : public Module {
+public:
+    Tensor forward(const Tensor& input) override;
+    std::string name() const override { return "Sigmoid"; }
+};
+
+class Tanh : public Module {
+public:
+    Tensor forward(const Tensor& input) override;
+    std::string name() const override { return "Tanh"; }
+};
+
+// GELU in its hyperbolic-tangent approximation.
+class GELU : public Module {
+public:
+    Tensor forward(const Tensor& input) override;
+    std::string name() const override { return "GELU"; }
+};
+
 class Sequential : public Module {
 public:
     Sequential() = default;

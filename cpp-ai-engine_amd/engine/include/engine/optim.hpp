@@ -76,6 +76,65 @@ private:
 // exceeds max_norm; returns the norm (the reference's src/optim.cpp:168-208).
 float clip_grad_norm(const std::vector<Tensor>& parameters, float max_norm);
 
+// Learning-rate schedulers (the reference's include/engine/optim.hpp:102-170):
+// step() once per epoch sets the optimiser's learning rate for the new epoch.
+// Host arithmetic only; the next Adam or SGD step takes the new rate.
+class Scheduler {
+public:
+    explicit Scheduler(Optimizer& optimizer);
+    virtual ~Scheduler() = default;
+    void step();
+    size_t epoch() const noexcept { return epoch_; }
+    float base_learning_rate() const noexcept { return base_lr_; }
+
+protected:
+    virtual float compute(size_t epoch) const = 0;  // epoch 0 is the initial rate
+    Optimizer& optimizer_;
+    float base_lr_;
+    size_t epoch_ = 0;
+};
+
+// base_lr * gamma^(epoch / step_size)
+class StepLR : public Scheduler {
+public:
+    StepLR(Optimizer& optimizer, size_t step_size, float gamma = 0.1f);
+
+protected:
+    float compute(size_t epoch) const override;
+
+private:
+    size_t step_size_;
+    float gamma_;
+};
+
+// A cosine from base_lr down to min_lr over total_epochs.
+class CosineAnnealingLR : public Scheduler {
+public:
+    CosineAnnealingLR(Optimizer& optimizer, size_t total_epochs, float min_lr = 0.0f);
+
+protected:
+    float compute(size_t epoch) const override;
+
+private:
+    size_t total_epochs_;
+    float min_lr_;
+};
+
+// A linear ramp over warmup_epochs, then a cosine to min_lr at total_epochs.
+class WarmupCosineLR : public Scheduler {
+public:
+    WarmupCosineLR(Optimizer& optimizer, size_t warmup_epochs, size_t total_epochs,
+                   float min_lr = 0.0f);
+
+protected:
+    float compute(size_t epoch) const override;
+
+private:
+    size_t warmup_epochs_;
+    size_t total_epochs_;
+    float min_lr_;
+};
+
 }  // namespace optim
 }  // namespace engine
 

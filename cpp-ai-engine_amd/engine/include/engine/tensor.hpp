@@ -108,6 +108,14 @@ public:
     [[nodiscard]] Tensor mean() const;
     [[nodiscard]] Tensor sum(size_t axis, bool keepdim = false) const;
     [[nodiscard]] Tensor mean(size_t axis, bool keepdim = false) const;
+    [[nodiscard]] Tensor max(size_t axis, bool keepdim = false) const;
+
+    // Contiguous sub-tensor along an axis: [start, start + count).
+    [[nodiscard]] Tensor slice(size_t axis, size_t start, size_t count) const;
+    // Concatenates along an axis (every other dimension must match); stacks
+    // along a new axis.
+    [[nodiscard]] static Tensor concat(const std::vector<Tensor>& parts, size_t axis);
+    [[nodiscard]] static Tensor stack(const std::vector<Tensor>& parts, size_t axis = 0);
 
     [[nodiscard]] Tensor select_rows(const std::vector<size_t>& indices) const;
     [[nodiscard]] Tensor detach() const;

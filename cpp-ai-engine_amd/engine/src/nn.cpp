@@ -101,6 +101,35 @@ Dropout::Dropout(float p) : p_(p) {
 
 // src/nn.cpp:206-244 with the mask drawn on the device; the backward
 // multiplies by the same mask.
+namespace {
+
+// y = f(x) on the device; backward dx = g * f'(x, y) (the reference's
+// unary_with_grad, src/nn.cpp:27-48, with its derivatives of src/nn.cpp:154-198).
+Tensor activation(const Tensor& input, int kind) {
+    Tensor out(input.shape(), 0.0f, false);
+    hip::check(ehip_activation_f32(kind, dptr(input), dout(out), int64_t(input.size()), nullptr),
+               "activation");
+    if (!track(input.requires_grad())) return out;
+    out.set_requires_grad(true);
+    out.get_impl()->parents = {input.get_impl()};
+    Tensor input_copy = input;
+    Tensor saved = out.detach();
+    out.get_impl()->backward_fn = [input_copy, saved, kind](const Tensor& g) mutable {
+        Tensor dX(input_copy.shape(), 0.0f, false);
+        hip::check(ehip_activation_backward_f32(kind, dptr(input_copy), dptr(saved), dptr(g),
+                                                dout(dX), int64_t(dX.size()), nullptr),
+                   "activation backward");
+        input_copy.add_grad(dX);
+    };
+    return out;
+}
+
+}  // namespace
+
+Tensor Sigmoid::forward(const Tensor& input) { return activation(input, EHIP_SIGMOID); }
+Tensor Tanh::forward(const Tensor& input) { return activation(input, EHIP_TANH); }
+Tensor GELU::forward(const Tensor& input) { return activation(input, EHIP_GELU); }
+
 Tensor Dropout::forward(const Tensor& input) {
     if (!is_training() || p_ == 0.0f) return input;
     Tensor out(input.shape(), 0.0f, false);

@@ -2,6 +2,7 @@
 // clip_grad_norm over the device reductions (the reference's src/optim.cpp).
 #include "engine/optim.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <stdexcept>
 
@@ -186,6 +187,70 @@ float clip_grad_norm(const std::vector<Tensor>& parameters, float max_norm) {
         }
     }
     return norm;
+}
+
+}  // namespace optim
+}  // namespace engine
+
+namespace engine {
+namespace optim {
+
+// ------------------------------------------------------------------ schedulers
+// The reference's src/optim.cpp:214-275; each rate is the same float
+// expression, so a schedule matches it value for value.
+
+Scheduler::Scheduler(Optimizer& optimizer)
+    : optimizer_(optimizer), base_lr_(optimizer.learning_rate()) {}
+
+void Scheduler::step() {
+    ++epoch_;
+    optimizer_.set_learning_rate(compute(epoch_));
+}
+
+StepLR::StepLR(Optimizer& optimizer, size_t step_size, float gamma)
+    : Scheduler(optimizer), step_size_(step_size), gamma_(gamma) {
+    if (step_size == 0) throw std::invalid_argument("StepLR needs a positive step_size.");
+    if (gamma <= 0.0f) throw std::invalid_argument("StepLR needs a positive gamma.");
+}
+
+float StepLR::compute(size_t epoch) const {
+    const size_t drops = epoch / step_size_;  // the rate falls in whole steps
+    return base_lr_ * std::pow(gamma_, static_cast<float>(drops));
+}
+
+CosineAnnealingLR::CosineAnnealingLR(Optimizer& optimizer, size_t total_epochs, float min_lr)
+    : Scheduler(optimizer), total_epochs_(total_epochs), min_lr_(min_lr) {
+    if (total_epochs == 0) throw std::invalid_argument("CosineAnnealingLR needs at least one epoch.");
+    if (min_lr < 0.0f) throw std::invalid_argument("CosineAnnealingLR needs min_lr >= 0.");
+}
+
+namespace {
+constexpr float kPi = 3.14159265358979f;
+float half_cosine(float t) { return 0.5f * (1.0f + std::cos(kPi * t)); }
+}  // namespace
+
+float CosineAnnealingLR::compute(size_t epoch) const {
+    const float t = std::min(static_cast<float>(epoch) / static_cast<float>(total_epochs_), 1.0f);
+    return min_lr_ + (base_lr_ - min_lr_) * half_cosine(t);
+}
+
+WarmupCosineLR::WarmupCosineLR(Optimizer& optimizer, size_t warmup_epochs, size_t total_epochs,
+                               float min_lr)
+    : Scheduler(optimizer),
+      warmup_epochs_(warmup_epochs),
+      total_epochs_(total_epochs),
+      min_lr_(min_lr) {
+    if (total_epochs == 0) throw std::invalid_argument("WarmupCosineLR needs at least one epoch.");
+    if (warmup_epochs >= total_epochs)
+        throw std::invalid_argument("The warm-up must be shorter than the total number of epochs.");
+}
+
+float WarmupCosineLR::compute(size_t epoch) const {
+    if (epoch < warmup_epochs_)
+        return base_lr_ * static_cast<float>(epoch) / static_cast<float>(warmup_epochs_);
+    const float t = static_cast<float>(epoch - warmup_epochs_) /
+                    static_cast<float>(total_epochs_ - warmup_epochs_);
+    return min_lr_ + (base_lr_ - min_lr_) * half_cosine(std::min(t, 1.0f));
 }
 
 }  // namespace optim

@@ -169,6 +169,16 @@ Storage Storage::clone() const {
     return s;
 }
 
+BufferPoolStats buffer_pool_stats() {
+    ehip_arena_stats_t a{};
+    ehip_arena_stats(&a);
+    BufferPoolStats b;
+    b.fresh = size_t(a.driver_allocations);
+    b.recycled = size_t(a.allocations - a.driver_allocations);
+    b.bytes_held = size_t(a.bytes_cached);
+    return b;
+}
+
 // ------------------------------------------------------------------ ints
 
 struct DeviceInts::Block {

@@ -329,6 +329,33 @@ int ehip_scalar_f32(const float* x, float* out, int64_t n, float mul, float add,
 int ehip_relu_f32(const float* x, float* y, int64_t n, void* stream);
 int ehip_relu_backward_f32(const float* x, const float* g, float* dx, int64_t n, void* stream);
 
+/* y = f(x) and dx = g * f'(x, y) for the smooth activations of nn::Sigmoid,
+ * nn::Tanh and nn::GELU (src/nn.cpp:154-198 of the reference, which runs
+ * them on the host only): sigmoid in the reference's two-branch stable form,
+ * tanh, and GELU's tanh approximation 0.5 x (1 + tanh(sqrt(2/pi) (x +
+ * 0.044715 x^3))), each evaluated in the reference's order; exp and tanh are
+ * the device library's (a few ulp from the host's). */
+enum { EHIP_SIGMOID = 0, EHIP_TANH = 1, EHIP_GELU = 2 };
+int ehip_activation_f32(int kind, const float* x, float* y, int64_t n, void* stream);
+int ehip_activation_backward_f32(int kind, const float* x, const float* y, const float* g,
+                                 float* dx, int64_t n, void* stream);
+
+/* For r < rows: dst[r * dst_pitch + j] = src[r * src_pitch + j], j < len. The
+ * moves of Tensor::slice, concat and stack and of their backward passes
+ * (src/tensor.cpp:428-552: per outer index, a run of count x inner floats).
+ * Bit-exact. */
+int ehip_copy_rows_f32(const float* src, int64_t src_pitch, float* dst, int64_t dst_pitch,
+                       int64_t rows, int64_t len, void* stream);
+
+/* Tensor::max(axis) over x viewed as (outer, axis_len, inner)
+ * (src/tensor.cpp:383-424): y[o][i] = the first maximum along the axis
+ * (strict >, in axis order, so a leading NaN stays), argmax[o][i] its axis
+ * index; backward dx = 0 + g at the winning position, 0 elsewhere. Bit-exact. */
+int ehip_max_axis_f32(const float* x, float* y, int32_t* argmax, int64_t outer, int64_t axis_len,
+                      int64_t inner, void* stream);
+int ehip_max_axis_backward_f32(const float* g, const int32_t* argmax, float* dx, int64_t outer,
+                               int64_t axis_len, int64_t inner, void* stream);
+
 /* grad = g (initialize != 0) or grad += g. Bit-exact.
  * cuda::ops::accumulate_grad (cuda_ops.hpp:61). */
 int ehip_accumulate_grad_f32(float* grad, const float* g, int64_t n, int initialize,

@@ -17,9 +17,10 @@ against this repository's engine headers and linked with libengine_hip.so
   set, where chance is 16.7 %).
   charlm_demo is built but not run: it reads a corpus from the reference checkout, which
   the GPU box does not have.
-- The reference's autograd, convolution and Transformer unit suites (its
-  tests/test_autograd.cpp, test_conv.cpp and test_transformer.cpp), run through
-  tests/dropin/suite_main.cpp: no check may fail.
+- The reference's unit suites but its CUDA one (its tests/test_tensor.cpp,
+  test_autograd.cpp, test_nn.cpp, test_conv.cpp, test_transformer.cpp and
+  test_reference.cpp, the last against the committed PyTorch fixtures), run through
+  tests/dropin/suite_main.cpp: no check may fail, and all six suites must have run.
 
 The binaries are built in this container (they need the reference checkout) and travel
 with the tree; the tests skip where they were not built."""
@@ -105,3 +106,6 @@ def test_reference_unit_suites_on_the_engine():
     failed = [ln for ln in run.stdout.splitlines() if "[FAIL]" in ln]
     assert run.returncode == 0 and not failed, "\n".join(failed) or run.stderr[-2000:]
     assert "0 failed" in run.stdout
+    import re
+    checks = int(re.search(r"reference suites: (\d+) checks", run.stdout).group(1))
+    assert checks >= 500, f"only {checks} checks ran"
