@@ -916,11 +916,13 @@ bool rows_vec_ok(int64_t cols, std::initializer_list<const void*> ptrs) {
 }
 
 // Groups of the large-problem form for rows x cols, or 0 when the shape takes
-// the small-problem kernels (fewer than 2^20 elements, or rows beyond 2048
+// the small-problem kernels (fewer than 2^17 elements, or rows beyond 2048
 // columns). About 32 rows per group, at most 256 (one per CU); the group count
-// fixes the order of the dgamma / dbeta sums.
+// fixes the order of the dgamma / dbeta sums. From 2^17 elements up (the char
+// Transformer's 2048 x 96) the engine queues those sums into the step's Adam
+// launch, two launches fewer per LayerNorm than the small form's separate sums.
 int64_t ln_wide_groups(int64_t rows, int64_t cols) {
-    if (rows <= 0 || rows * cols < (int64_t(1) << 20) || cols > 2048) return 0;
+    if (rows <= 0 || rows * cols < (int64_t(1) << 17) || cols > 2048) return 0;
     return std::min<int64_t>(ceil_div(rows, 32), 256);
 }
 

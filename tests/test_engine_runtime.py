@@ -225,7 +225,7 @@ def test_wide_conv2d_paths(eng, n, c, hw, oc, k, stride, pad, igemm):
 
 @pytest.mark.parametrize("rows,d", [(1024, 1024), (2048, 1000)])
 def test_layernorm_queued_sums_match_one_call(eng, hip, rows, d):
-    """A LayerNorm of at least 2^20 elements queues its dgamma / dbeta sums during backward
+    """A LayerNorm of at least 2^17 elements queues its dgamma / dbeta sums during backward
     (only dx and the group partials are computed there); reading the gradients runs the
     queue. The values are the one-call backward's, bit for bit."""
     print_case("engine layernorm queued", rows, d)

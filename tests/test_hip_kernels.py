@@ -994,10 +994,10 @@ def test_layernorm_backward_partials_match_one_call(hip, orc, rows, d):
 
 
 def test_layernorm_backward_partials_small_shapes_refused(hip):
-    """Shapes under 2^20 elements (cfg3's 2048 x 96) or wider than 2048 columns are summed
-    in one call only: the size query returns 0 and the entry point refuses them."""
+    """Shapes under 2^17 elements or wider than 2048 columns are summed in one call only:
+    the size query returns 0 and the entry point refuses them."""
     print_case("layernorm partials small")
-    for rows, d in [(2048, 96), (600, 4096)]:
+    for rows, d in [(1024, 96), (600, 4096)]:
         x = dev(np.ones((rows, d), np.float32))
         g = dev(np.ones(d, np.float32))
         inv = dev(np.ones(rows, np.float32))
