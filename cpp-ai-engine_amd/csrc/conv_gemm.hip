@@ -775,18 +775,21 @@ using DoutByPixelS1 = DoutByPixel<C, BR, BK, true>;
 template <class C, int BR, int BK>
 using DoutByPixelStrided = DoutByPixel<C, BR, BK, false>;
 
+// Indices within an image, and the batch's output pixels (the weight
+// gradient's reduction index), are 32-bit; the batch is a grid dimension.
+bool layer_fits(const ehip_window_t* w, int64_t out_channels) {
+    const int64_t lim = 0x7fffffffLL;
+    return !(w->channels * w->height * w->width > lim || out_channels * w->out_h * w->out_w > lim ||
+             w->channels * w->kernel_h * w->kernel_w > lim ||
+             out_channels * w->kernel_h * w->kernel_w > lim ||
+             w->batch * w->out_h * w->out_w > lim || w->batch > 65535);
+}
+
 int check_layer(const char* name, const ehip_window_t* w, int64_t out_channels) {
     if (int rc = check_window(name, w)) return rc;
     if (out_channels <= 0)
         return fail(EHIP_EINVAL, "%s: out_channels %lld", name, (long long)out_channels);
-    // Indices within an image, and the batch's output pixels (the weight
-    // gradient's reduction index), are 32-bit.
-    const int64_t lim = 0x7fffffffLL;
-    if (w->channels * w->height * w->width > lim || out_channels * w->out_h * w->out_w > lim ||
-        w->channels * w->kernel_h * w->kernel_w > lim ||
-        out_channels * w->kernel_h * w->kernel_w > lim ||
-        w->batch * w->out_h * w->out_w > lim || w->batch > 65535)
-        return fail(EHIP_EINVAL, "%s: layer too large", name);
+    if (!layer_fits(w, out_channels)) return fail(EHIP_EINVAL, "%s: layer too large", name);
     return EHIP_OK;
 }
 
@@ -796,6 +799,13 @@ int check_layer(const char* name, const ehip_window_t* w, int64_t out_channels) 
 using namespace ehip;
 
 extern "C" {
+
+int ehip_conv2d_igemm_supported(const ehip_window_t* w, int64_t out_channels) {
+    if (w == nullptr || out_channels <= 0 || w->batch < 0 || w->channels <= 0 ||
+        w->out_h <= 0 || w->out_w <= 0 || w->kernel_h <= 0 || w->kernel_w <= 0)
+        return 0;
+    return layer_fits(w, out_channels) ? 1 : 0;
+}
 
 int ehip_conv2d_igemm_f32(const float* x, const float* weight, const float* bias, float* out,
                           const ehip_window_t* win, int64_t out_channels, void* stream) {

@@ -226,36 +226,46 @@ __device__ float block_reduce_loop(float v, float* sh, bool is_max) {
     return r;
 }
 
+// Both honour `causal` as the register path does: columns at or past
+// read_cols() are not read, count as -inf (forward) or 0 (backward), and
+// their outputs come from the same expressions on those values.
 __global__ __launch_bounds__(kLoopThreads) void softmax_rows_loop(const float* __restrict__ x,
                                                                   float* __restrict__ y,
-                                                                  int64_t rows, int64_t cols) {
+                                                                  int64_t rows, int64_t cols,
+                                                                  int causal) {
     __shared__ float sh[kLoopThreads / 64];
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const float* xr = x + r * cols;
         float* yr = y + r * cols;
+        const int64_t rc = read_cols(r, cols, causal);
         float mx = -INFINITY;
-        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) mx = fmaxf(mx, xr[c]);
+        for (int64_t c = threadIdx.x; c < rc; c += kLoopThreads) mx = fmaxf(mx, xr[c]);
         mx = block_reduce_loop(mx, sh, true);
         float sum = 0.0f;
-        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) sum += expf(xr[c] - mx);
+        for (int64_t c = threadIdx.x; c < rc; c += kLoopThreads) sum += expf(xr[c] - mx);
         sum = block_reduce_loop(sum, sh, false);
         const float rs = 1.0f / sum;
-        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) yr[c] = expf(xr[c] - mx) * rs;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads)
+            yr[c] = expf((c < rc ? xr[c] : -INFINITY) - mx) * rs;
     }
 }
 
 __global__ __launch_bounds__(kLoopThreads) void softmax_rows_backward_loop(
     const float* __restrict__ y, const float* g, float* dx, int64_t rows, int64_t cols,
-    float scale) {
+    float scale, int causal) {
     __shared__ float sh[kLoopThreads / 64];
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const float* yr = y + r * cols;
         const float* gr = g + r * cols;
+        const int64_t rc = read_cols(r, cols, causal);
         float dot = 0.0f;
-        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) dot += gr[c] * yr[c];
+        for (int64_t c = threadIdx.x; c < rc; c += kLoopThreads) dot += gr[c] * yr[c];
         dot = block_reduce_loop(dot, sh, false);
-        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads)
-            dx[r * cols + c] = (yr[c] * (gr[c] - dot)) * scale;
+        // dx may alias g: each element is read by the thread that stores it.
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) {
+            const float yv = c < rc ? yr[c] : 0.0f, gv = c < rc ? gr[c] : 0.0f;
+            dx[r * cols + c] = (yv * (gv - dot)) * scale;
+        }
     }
 }
 
@@ -985,9 +995,8 @@ int softmax_run(const float* x, float* y, int64_t rows, int64_t cols, int causal
     if (dispatch_row(rows, cols, rows_vec_ok(cols, {x, y}),
                      SoftmaxLaunch{x, y, rows, cols, s, &rc, causal}))
         return rc;
-    // Rows beyond the register path read every column (the same values).
     EHIP_LAUNCH("softmax", softmax_rows_loop, dim3(loop_grid(rows)), dim3(kLoopThreads), 0, s, x, y,
-                rows, cols);
+                rows, cols, causal);
     return EHIP_OK;
 }
 
@@ -1007,7 +1016,7 @@ int softmax_backward_run(const float* y, const float* g, float* dx, int64_t rows
                      SoftmaxBackwardLaunch{y, g, dx, rows, cols, scale, s, &rc, causal}))
         return rc;
     EHIP_LAUNCH("softmax_backward", softmax_rows_backward_loop, dim3(loop_grid(rows)),
-                dim3(kLoopThreads), 0, s, y, g, dx, rows, cols, scale);
+                dim3(kLoopThreads), 0, s, y, g, dx, rows, cols, scale, causal);
     return EHIP_OK;
 }
 

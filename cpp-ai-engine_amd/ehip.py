@@ -129,6 +129,7 @@ _SIGS = {
     "ehip_conv2d_forward_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_backward_input_f32": [_vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_backward_weight_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
+    "ehip_conv2d_igemm_supported": [C.POINTER(Window), _i64],
     "ehip_conv2d_igemm_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_igemm_backward_f32": [_vp] * 6 + [C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_relu_maxpool_supported": [C.POINTER(Window), _i64, C.POINTER(Window)],

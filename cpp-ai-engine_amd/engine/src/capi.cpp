@@ -28,6 +28,11 @@
 #include "engine/tensor.hpp"
 #include "engine/transformer.hpp"
 
+namespace engine::data {
+size_t idx_payload_bytes(const std::string& path, uint32_t magic, size_t max_items,
+                         size_t* count);
+}
+
 using engine::Tensor;
 namespace nn = engine::nn;
 namespace optim = engine::optim;
@@ -200,6 +205,17 @@ extern "C" {
 const char* eng_last_error() { return g_error.c_str(); }
 
 int eng_available() { return engine::hip::available() ? 1 : 0; }
+
+// Host-only: reads an IDX file's header and payload (engine/src/data.cpp)
+// and returns the items kept and the payload size, or the reader's error.
+int eng_idx_probe(const char* path, uint32_t magic, int64_t max_items, int64_t* count,
+                  int64_t* bytes) {
+    return guarded([&] {
+        size_t n = 0;
+        *bytes = int64_t(engine::data::idx_payload_bytes(path, magic, size_t(max_items), &n));
+        *count = int64_t(n);
+    });
+}
 
 int eng_synchronize() {
     return guarded([&] { engine::hip::synchronize(); });

@@ -201,7 +201,8 @@ Conv2d::Conv2d(size_t in_channels, size_t out_channels, const Window2d& window, 
 }
 
 // Narrow layers take the direct kernels, wider ones the implicit GEMM. With
-// that switched off, wide layers compose as the reference does: im2col ->
+// that switched off, or for a layer beyond the implicit GEMM's 32-bit index
+// and batch limits, wide layers compose as the reference does: im2col ->
 // cols (W reshaped to (outC, K))^T -> + bias -> (N, outC, oH, oW)
 // (src/conv.cpp:280-338), the product on MFMA reading W in place through the
 // GEMM's transposed mode, so its derivative needs no transpose either.
@@ -219,7 +220,8 @@ Tensor Conv2d::forward(const Tensor& input) {
     const ehip_window_t w = window_of(input.shape(), window_);
     if (ehip_conv2d_direct_supported(&w, int64_t(out_channels_)))
         return conv2d_direct(input, weight_, bias_, use_bias_, w);
-    if (conv_implicit_gemm()) return conv2d_igemm(input, weight_, bias_, use_bias_, w);
+    if (conv_implicit_gemm() && ehip_conv2d_igemm_supported(&w, int64_t(out_channels_)))
+        return conv2d_igemm(input, weight_, bias_, use_bias_, w);
     Tensor cols = im2col_node(input, window_);
     Tensor out = ops::matmul_nt(cols, weight_.reshape({out_channels_, K}));
     if (use_bias_) out = out + bias_;

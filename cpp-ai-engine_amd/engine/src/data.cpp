@@ -37,25 +37,48 @@ Idx read_idx(const std::string& path, uint32_t magic, size_t max_items) {
                                  ", expected " + std::to_string(magic) + ".");
     Idx idx;
     const size_t ndims = magic & 0xffu;
+    // The header's dimensions are untrusted: the payload size they imply is
+    // checked for overflow and against the bytes the file still holds before
+    // anything is allocated, so a corrupt header reads as a truncated file.
+    const auto truncated = [&] {
+        return std::runtime_error("IDX file '" + path + "' holds fewer than " +
+                                  std::to_string(idx.count) + " items.");
+    };
     size_t item = 1;
+    bool overflow = false;
     for (size_t d = 0; d < ndims; ++d) {
         if (!in.read(reinterpret_cast<char*>(word), 4))
             throw std::runtime_error("IDX file '" + path + "' ends inside its header.");
         idx.dims.push_back(big_endian(word));
-        if (d > 0) item *= idx.dims.back();
+        if (d > 0) overflow |= __builtin_mul_overflow(item, size_t(idx.dims.back()), &item);
     }
     const size_t items = ndims ? idx.dims[0] : 0;
     idx.count = max_items > 0 && max_items < items ? max_items : items;
-    idx.bytes.resize(idx.count * item);
+    size_t payload = 0;
+    overflow |= __builtin_mul_overflow(idx.count, item, &payload);
+    const std::streampos start = in.tellg();
+    in.seekg(0, std::ios::end);
+    const std::streampos end = in.tellg();
+    in.seekg(start);
+    if (overflow || start < 0 || end < start || payload > size_t(end - start)) throw truncated();
+    idx.bytes.resize(payload);
     if (!in.read(reinterpret_cast<char*>(idx.bytes.data()), std::streamsize(idx.bytes.size())))
-        throw std::runtime_error("IDX file '" + path + "' holds fewer than " +
-                                 std::to_string(idx.count) + " items.");
+        throw truncated();
     return idx;
 }
 
 bool readable(const std::string& path) { return std::ifstream(path, std::ios::binary).good(); }
 
 }  // namespace
+
+// The IDX header check on its own, for the C ABI's tests: items kept and
+// payload bytes of a file, or the reader's exception.
+size_t idx_payload_bytes(const std::string& path, uint32_t magic, size_t max_items,
+                         size_t* count) {
+    const Idx idx = read_idx(path, magic, max_items);
+    if (count) *count = idx.count;
+    return idx.bytes.size();
+}
 
 Tensor load_idx_images(const std::string& path, size_t max_samples) {
     const Idx idx = read_idx(path, 0x00000803u, max_samples);

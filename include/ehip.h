@@ -530,7 +530,11 @@ int ehip_conv2d_backward_weight_f32(const float* x, const float* grad_out, float
  * Fixed-order sums (K split into fixed chunks on small grids): deterministic,
  * within the K-term tolerance of the reference's serial loops. Layers with
  * more than 2^31 - 1 elements in one image's input, output or weight rows, or
- * more than 65535 images, are refused with EHIP_EINVAL. */
+ * more than 65535 images, are refused with EHIP_EINVAL;
+ * ehip_conv2d_igemm_supported() says 1 for a layer inside those limits (a
+ * query without side effects: the caller composes im2col + ehip_gemm_f32 for
+ * the others, as Conv2d::forward does in src/conv.cpp:280-338). */
+int ehip_conv2d_igemm_supported(const ehip_window_t* w, int64_t out_channels);
 int ehip_conv2d_igemm_f32(const float* x, const float* weight, const float* bias, float* out,
                           const ehip_window_t* w, int64_t out_channels, void* stream);
 int ehip_conv2d_igemm_backward_f32(const float* x, const float* weight, const float* grad_out,

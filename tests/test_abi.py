@@ -51,3 +51,18 @@ def test_no_device_is_an_error_not_a_crash(lib):
     assert lib.ehip_relu_f32(None, None, 16, None) == 3
     p = ctypes.c_void_p()
     assert lib.ehip_arena_alloc(1024, ctypes.byref(p)) == 3 and not p.value
+
+
+def test_igemm_supported_is_a_pure_query(lib):
+    """ehip_conv2d_igemm_supported needs no device and says 0 beyond the implicit GEMM's
+    limits (65535 images; 2^31 output pixels over the batch), where the engine composes
+    im2col + GEMM instead."""
+    def win(n, c, h, w, k=3, s=1, p=1):
+        oh, ow = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+        return E.Window(n, c, h, w, k, k, s, p, oh, ow)
+    f = lib.ehip_conv2d_igemm_supported
+    assert f(ctypes.byref(win(32, 64, 28, 28)), 128) == 1
+    assert f(ctypes.byref(win(65535, 64, 4, 4)), 128) == 1
+    assert f(ctypes.byref(win(65536, 64, 4, 4)), 128) == 0
+    assert f(ctypes.byref(win(4096, 3, 1024, 1024)), 16) == 0
+    assert f(None, 16) == 0 and f(ctypes.byref(win(1, 1, 4, 4)), 0) == 0

@@ -551,7 +551,7 @@ def test_causal_skipping_modes(hip, S, hd, bt):
         run(False, False, S, hd, S, P, S, ss, V, hd, sh, sh, hd, 5)
 
 
-@pytest.mark.parametrize("S,mats", [(512, 8), (64, 40), (300, 3), (1, 5), (2048, 2)])
+@pytest.mark.parametrize("S,mats", [(512, 8), (64, 40), (300, 3), (1, 5), (2048, 2), (2050, 2)])
 def test_causal_softmax_matches_full(hip, S, mats):
     """The causal softmax pair reads each row only up to the diagonal: on scores whose
     masked entries are -1e9 + q.k (as the score product writes them), the forward equals
@@ -580,7 +580,39 @@ def test_causal_softmax_matches_full(hip, S, mats):
                                                    hip.stream()), "causal")
 
 
-@pytest.mark.parametrize("b,s,d,heads", [(8, 512, 512, 8), (2, 64, 96, 4), (16, 300, 128, 2)])
+@pytest.mark.parametrize("S,mats", [(64, 3), (300, 2), (2050, 2)])
+def test_causal_softmax_reads_only_the_triangle(hip, S, mats):
+    """Masked entries (right of the diagonal) are not read by the causal pair, on the
+    register path (S <= 2048) and on the looped one (2050: more than 2048 columns, not a
+    multiple of 4): with NaN planted there in x and g, both outputs equal those computed
+    from the -1e9 scores, and the masked outputs are zeros."""
+    print_case("causal softmax unread", S, mats)
+    r = np.random.default_rng(S * 3 + mats)
+    upper = np.triu(np.ones((S, S), bool), 1)
+    x = randn(r, mats, S, S) * 3
+    g = randn(r, mats, S, S)
+    rows = mats * S
+
+    def run(xv, gv):
+        X, G = dev(xv), dev(gv)
+        y, dx = hip.f32(X.shape), hip.f32(X.shape)
+        hip.ok(hip.lib.ehip_softmax_causal_f32(hip.p(X), hip.p(y), rows, S, hip.stream()),
+               "causal")
+        hip.ok(hip.lib.ehip_softmax_backward_scaled_causal_f32(
+            hip.p(y), hip.p(G), hip.p(dx), rows, S, 0.25, hip.stream()), "causal bwd")
+        return host(y), host(dx)
+
+    y_mask, dx_mask = run(np.where(upper, x + np.float32(-1e9), x).astype(np.float32), g)
+    y_nan, dx_nan = run(np.where(upper, np.float32(np.nan), x).astype(np.float32),
+                        np.where(upper, np.float32(np.nan), g).astype(np.float32))
+    exact(y_nan, y_mask, "forward with NaN in the masked entries")
+    assert np.array_equal(dx_nan, dx_mask), "backward with NaN in the masked entries"
+    assert np.all(y_nan[:, upper] == 0) and np.all(dx_nan[:, upper] == 0), "masked outputs"
+    assert np.all(np.isfinite(y_nan)) and np.all(np.isfinite(dx_nan))
+
+
+@pytest.mark.parametrize("b,s,d,heads", [(8, 512, 512, 8), (2, 64, 96, 4), (16, 300, 128, 2),
+                                         (1, 2050, 64, 2)])
 def test_mha_causal_mask_skipping_keeps_values(eng, b, s, d, heads):
     """The fused attention node under nn::causal_mask (whose score tiles above the diagonal,
     the products with the weights past it and the matching backward products are skipped)

@@ -223,11 +223,13 @@ def test_wide_conv2d_paths(eng, n, c, hw, oc, k, stride, pad, igemm):
 
 # ------------------------------------------------------------------ queued LayerNorm sums
 
-@pytest.mark.parametrize("rows,d", [(1024, 1024), (2048, 1000)])
+@pytest.mark.parametrize("rows,d", [(1024, 1024), (2048, 1000), (2048, 96), (1024, 128),
+                                    (1366, 96)])
 def test_layernorm_queued_sums_match_one_call(eng, hip, rows, d):
     """A LayerNorm of at least 2^17 elements queues its dgamma / dbeta sums during backward
     (only dx and the group partials are computed there); reading the gradients runs the
-    queue. The values are the one-call backward's, bit for bit."""
+    queue. The values are the one-call backward's, bit for bit: cfg5's and cfg3's shapes
+    (1024 and 96 wide), exactly 2^17 elements and just above it."""
     print_case("engine layernorm queued", rows, d)
     import torch
     r = np.random.default_rng(rows + d)
