@@ -88,7 +88,17 @@ struct Frag {
             for (int q = 0; q < V / 4; ++q) {
                 const int c4 = tid + T * q;
                 nf4 x = {fill, fill, fill, fill};
-                if (4 * c4 < cols) x = NT ? __builtin_nontemporal_load(r4 + c4) : r4[c4];
+                if (4 * c4 < cols) {
+                    x = NT ? __builtin_nontemporal_load(r4 + c4) : r4[c4];
+                    // A limit inside the vector (the causal diagonal): the
+                    // lanes past it are read with the vector but count as
+                    // `fill`, so their memory never reaches the result.
+                    if (4 * c4 + 4 > cols) {
+                        if (4 * c4 + 1 >= cols) x.y = fill;
+                        if (4 * c4 + 2 >= cols) x.z = fill;
+                        if (4 * c4 + 3 >= cols) x.w = fill;
+                    }
+                }
                 v[4 * q] = x.x;
                 v[4 * q + 1] = x.y;
                 v[4 * q + 2] = x.z;

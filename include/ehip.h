@@ -691,7 +691,10 @@ int ehip_softmax_backward_scaled_f32(const float* y, const float* g, float* dx, 
  * rows are stacked cols x cols matrices, and entries right of the diagonal
  * (column j > row i within a matrix) are masked -- in the forward at least
  * 104 below the row's maximum (their exponential is 0), in the backward with
- * y = 0. Masked entries are not read; they are stored as 0. Every other output
+ * y = 0. Masked entries are not used -- any values there, NaN included, leave
+ * the results as they are (the 16-byte vector that straddles the diagonal is
+ * loaded whole, its masked lanes discarded; whole vectors past it are never
+ * loaded) -- and they are stored as 0. Every other output
  * equals ehip_softmax_f32's / ehip_softmax_backward_scaled_f32's bit for bit,
  * and a masked one by value (its sign of zero may differ). rows must be a
  * multiple of cols. (The reference reads and computes the masked entries:
