@@ -114,6 +114,9 @@ struct Workspace {
     size_t cap_bytes = 0;
 };
 
+// The grid's z extent: products beyond it run as further launches.
+constexpr int64_t kGridZ = 65535;
+
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
 int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s,
                const Workspace& wsp) {
@@ -160,20 +163,26 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s,
         }
         g.c = ws;
     }
-    const dim3 grid{unsigned(tiles), unsigned(splits), unsigned(batch)};
     const bool epi = splits == 1 && !plain_epilogue(g);
-    if (check && epi) {
-        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, true, true>), grid,
-                    dim3(C::kThreads), 0, s, g);
-    } else if (check) {
-        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, true, false>), grid,
-                    dim3(C::kThreads), 0, s, g);
-    } else if (epi) {
-        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, false, true>), grid,
-                    dim3(C::kThreads), 0, s, g);
-    } else {
-        EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, false, false>), grid,
-                    dim3(C::kThreads), 0, s, g);
+    // Split K only below ~512 workgroups, so a split product is one launch;
+    // longer batches run in ranges of the grid's z extent.
+    for (int64_t z0 = 0; z0 < batch; z0 += kGridZ) {
+        g.batch0 = z0;
+        const dim3 grid{unsigned(tiles), unsigned(splits),
+                        unsigned(batch - z0 < kGridZ ? batch - z0 : kGridZ)};
+        if (check && epi) {
+            EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, true, true>), grid,
+                        dim3(C::kThreads), 0, s, g);
+        } else if (check) {
+            EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, true, false>), grid,
+                        dim3(C::kThreads), 0, s, g);
+        } else if (epi) {
+            EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, false, true>), grid,
+                        dim3(C::kThreads), 0, s, g);
+        } else {
+            EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, false, false>), grid,
+                        dim3(C::kThreads), 0, s, g);
+        }
     }
     if (splits > 1) {
         GemmArgs gr = g0;  // the caller's output and epilogue, the workspace geometry
@@ -191,17 +200,22 @@ double padding(int64_t m, int64_t n, int bm, int bn) {
 // launch, no workspace. W, the waves per workgroup, doubles while the grid
 // stays within 2048 waves (8 per CU) and each wave keeps at least 32 k.
 template <int W, bool TA, bool TB>
-int launch_kslice_w(const GemmArgs& g, int64_t batch, bool whole, hipStream_t s) {
-    const dim3 grid{unsigned(int64_t(g.tiles_m) * g.tiles_n), 1u, unsigned(batch)};
+int launch_kslice_w(GemmArgs g, int64_t batch, bool whole, hipStream_t s) {
     const bool epi = !plain_epilogue(g);
-    if (whole && !epi)
-        EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, false, false>), grid, dim3(64 * W), 0, s, g);
-    else if (whole)
-        EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, false, true>), grid, dim3(64 * W), 0, s, g);
-    else if (!epi)
-        EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, true, false>), grid, dim3(64 * W), 0, s, g);
-    else
-        EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, true, true>), grid, dim3(64 * W), 0, s, g);
+    for (int64_t z0 = 0; z0 < batch; z0 += kGridZ) {
+        g.batch0 = z0;
+        const dim3 grid{unsigned(int64_t(g.tiles_m) * g.tiles_n), 1u,
+                        unsigned(batch - z0 < kGridZ ? batch - z0 : kGridZ)};
+        if (whole && !epi)
+            EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, false, false>), grid, dim3(64 * W), 0, s,
+                        g);
+        else if (whole)
+            EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, false, true>), grid, dim3(64 * W), 0, s, g);
+        else if (!epi)
+            EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, true, false>), grid, dim3(64 * W), 0, s, g);
+        else
+            EHIP_LAUNCH("gemm", (gemm_kslice<W, TA, TB, true, true>), grid, dim3(64 * W), 0, s, g);
+    }
     return EHIP_OK;
 }
 
@@ -612,7 +626,6 @@ int check_desc(const ehip_gemm_ex_t& d) {
     if (d.colsum_b && (d.batch != 1 || d.trans_b))
         return fail(EHIP_EINVAL, "gemm: column sums need batch 1 and a K x N B");
     if (d.causal < 0 || d.causal > 4) return fail(EHIP_EINVAL, "gemm: causal mode %d", d.causal);
-    if (d.batch > 65535) return fail(EHIP_EINVAL, "gemm: batch %lld > 65535", (long long)d.batch);
     if (d.m > (int64_t(1) << 31) || d.n > (int64_t(1) << 31))
         return fail(EHIP_EINVAL, "gemm: extent beyond 2^31");
     return EHIP_OK;

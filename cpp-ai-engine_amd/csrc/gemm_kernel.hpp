@@ -41,6 +41,9 @@ struct GemmArgs {
     int64_t k_chunk;
     int vec;           // rows 16-byte aligned: checked loads may use float4 inside the edges
     int causal;        // ehip_gemm_ex_t::causal: 0, or the skipping mode 1 to 4
+    // The product index of grid z = 0: batches beyond the grid's 65535 z
+    // extent run as several launches of consecutive product ranges.
+    int64_t batch0;
 };
 
 // The element offset of product z's matrix.
@@ -322,14 +325,14 @@ __global__ __launch_bounds__((Cfg<BM, BN, BK, WM, WN>::kThreads)) void gemm_kern
     // Tile coordinates: XCD-contiguous renumbering, then GROUP_M-row groups.
     const int tiles = g.tiles_m * g.tiles_n;
     int tm, tn;
-    int64_t batch = blockIdx.z;
+    int64_t batch = g.batch0 + blockIdx.z;
     if (g.causal != 0 && gridDim.y == 1) {
         // Causal skipping makes a tile's work depend on its row band. Workgroups
         // reach the XCDs (and their CUs) in turn in launch order, so the order
         // runs over the products first: every XCD and CU then gets tiles of
         // every band instead of, with few tiles per product, one band only.
         const int64_t lin = int64_t(blockIdx.z) * gridDim.x + blockIdx.x;
-        batch = lin % gridDim.z;
+        batch = g.batch0 + lin % gridDim.z;
         const int t = int(lin / gridDim.z);
         tm = t / g.tiles_n;
         tn = t % g.tiles_n;
@@ -742,7 +745,7 @@ __device__ __forceinline__ void kslice_tile(const GemmArgs& g, int bid, int64_t 
 template <int W, bool TA, bool TB, bool CHECK, bool EPI, int KU = 4>
 __global__ __launch_bounds__(64 * W) void gemm_kslice(GemmArgs g) {
     __shared__ __attribute__((aligned(16))) float lds[KsliceLds<W>::kFloats];
-    kslice_tile<W, TA, TB, CHECK, EPI, KU>(g, blockIdx.x, blockIdx.z, lds, W);
+    kslice_tile<W, TA, TB, CHECK, EPI, KU>(g, blockIdx.x, g.batch0 + blockIdx.z, lds, W);
 }
 
 // The two products of a matmul's backward in one launch: g0 is dA = dC B^T

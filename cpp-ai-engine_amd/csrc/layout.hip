@@ -468,11 +468,17 @@ int ehip_transpose_f32(const float* x, float* out, int64_t batch, int64_t rows, 
     if (batch < 0 || rows < 0 || cols < 0) return fail(EHIP_EINVAL, "transpose: bad shape");
     if (!x || !out) return fail(EHIP_EINVAL, "transpose: null pointer");
     if (batch == 0 || rows == 0 || cols == 0) return EHIP_OK;
-    if (batch > 65535) return fail(EHIP_EINVAL, "transpose: batch %lld > 65535", (long long)batch);
     const int64_t tr = ceil_div(rows, kT), tc = ceil_div(cols, kT);
     if (tr * tc > 0x7fffffff) return fail(EHIP_EINVAL, "transpose: too many tiles");
-    EHIP_LAUNCH("transpose", transpose_tiled, dim3(unsigned(tr * tc), unsigned(batch)),
-                dim3(kT, 4), 0, as_stream(stream), x, out, rows, cols, tr, tc);
+    // The batch is the grid's y extent (at most 65535): longer batches run as
+    // several launches over consecutive matrices.
+    const int64_t mat = rows * cols;
+    for (int64_t z0 = 0; z0 < batch; z0 += 65535) {
+        const int64_t nz = batch - z0 < 65535 ? batch - z0 : 65535;
+        EHIP_LAUNCH("transpose", transpose_tiled, dim3(unsigned(tr * tc), unsigned(nz)),
+                    dim3(kT, 4), 0, as_stream(stream), x + z0 * mat, out + z0 * mat, rows, cols,
+                    tr, tc);
+    }
     return EHIP_OK;
 }
 

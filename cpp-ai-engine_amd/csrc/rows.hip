@@ -279,6 +279,72 @@ __global__ __launch_bounds__(kLoopThreads) void softmax_rows_backward_loop(
     }
 }
 
+// LayerNorm rows wider than the register path (more than 8192 columns): one
+// block per row, passes over global memory (the row stays in the caches
+// between them), the expressions of layernorm_rows and
+// layernorm_rows_backward. The backward's dgamma / dbeta partials accumulate
+// per group in partial[group][2][cols]; column c always belongs to thread
+// c mod kLoopThreads of its group's block, so each partial has one writer.
+__global__ __launch_bounds__(kLoopThreads) void layernorm_rows_loop(
+    const float* __restrict__ x, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float* __restrict__ out, float* __restrict__ xhat, float* __restrict__ inv_std, int64_t rows,
+    int64_t cols, float eps) {
+    __shared__ float sh[kLoopThreads / 64];
+    const float inv_d = 1.0f / static_cast<float>(cols);
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* xr = x + r * cols;
+        float sum = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) sum += xr[c];
+        const float mean = block_reduce_loop(sum, sh, false) * inv_d;
+        float q = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) {
+            const float d = xr[c] - mean;
+            q += d * d;
+        }
+        const float var = block_reduce_loop(q, sh, false) * inv_d;
+        const float inv = 1.0f / sqrtf(var + eps);
+        if (threadIdx.x == 0) inv_std[r] = inv;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) {
+            const float h = (xr[c] - mean) * inv;
+            xhat[r * cols + c] = h;
+            out[r * cols + c] = gamma[c] * h + beta[c];
+        }
+    }
+}
+
+__global__ __launch_bounds__(kLoopThreads) void layernorm_rows_backward_loop(
+    const float* __restrict__ dy, const float* __restrict__ xhat, const float* __restrict__ gamma,
+    const float* __restrict__ inv_std, float* __restrict__ dx, float* __restrict__ partial,
+    int64_t rows, int64_t cols) {
+    __shared__ float sh[kLoopThreads / 64];
+    const float inv_d = 1.0f / static_cast<float>(cols);
+    float* pg = partial + int64_t(blockIdx.x) * 2 * cols;
+    for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) {
+        pg[c] = 0.0f;
+        pg[cols + c] = 0.0f;
+    }
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* dr = dy + r * cols;
+        const float* hr = xhat + r * cols;
+        float s1 = 0.0f, s2 = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) {
+            const float dxh = dr[c] * gamma[c];
+            s1 += dxh;
+            s2 += dxh * hr[c];
+        }
+        s1 = block_reduce_loop(s1, sh, false);
+        s2 = block_reduce_loop(s2, sh, false);
+        const float inv = inv_std[r];
+        for (int64_t c = threadIdx.x; c < cols; c += kLoopThreads) {
+            const float d = dr[c], h = hr[c];
+            const float dxh = d * gamma[c];
+            dx[r * cols + c] = inv * (dxh - inv_d * s1 - h * inv_d * s2);
+            pg[c] = pg[c] + d * h;
+            pg[cols + c] = pg[cols + c] + d;
+        }
+    }
+}
+
 // ------------------------------------------------------------ cross-entropy
 
 // probs = softmax(logits); row_loss[r] = -((x[t] - max) - log(sum)), the
@@ -941,6 +1007,9 @@ bool rows_vec_ok(int64_t cols, std::initializer_list<const void*> ptrs) {
 // fixes the order of the dgamma / dbeta sums. From 2^17 elements up (the char
 // Transformer's 2048 x 96) the engine queues those sums into the step's Adam
 // launch, two launches fewer per LayerNorm than the small form's separate sums.
+// Widest LayerNorm row held in registers; wider rows take the looped kernels.
+constexpr int64_t kLnRegisterCols = 8192;
+
 int64_t ln_wide_groups(int64_t rows, int64_t cols) {
     if (rows <= 0 || rows * cols < (int64_t(1) << 17) || cols > 2048) return 0;
     return std::min<int64_t>(ceil_div(rows, 32), 256);
@@ -1144,11 +1213,15 @@ int ehip_layernorm_f32(const float* x, const float* gamma, const float* beta, fl
                        void* stream) {
     EHIP_READY();
     if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "layernorm: bad shape");
-    if (cols > 8192) return fail(EHIP_EINVAL, "layernorm: width %lld > 8192", (long long)cols);
     if (!x || !gamma || !beta || !out || !xhat || !inv_std)
         return fail(EHIP_EINVAL, "layernorm: null pointer");
     if (rows == 0) return EHIP_OK;
     hipStream_t s = as_stream(stream);
+    if (cols > kLnRegisterCols) {
+        EHIP_LAUNCH("layernorm", layernorm_rows_loop, dim3(loop_grid(rows)), dim3(kLoopThreads), 0,
+                    s, x, gamma, beta, out, xhat, inv_std, rows, cols, eps);
+        return EHIP_OK;
+    }
     const bool vec = cols >= 256 && rows_vec_ok(cols, {x, gamma, beta, out, xhat});
     // At most 512 blocks (two per CU): large inputs give each group several rows,
     // so that its loads of the next row overlap the stores of the current one.
@@ -1194,11 +1267,22 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
                                 int64_t rows, int64_t cols, void* stream) {
     EHIP_READY();
     if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "layernorm_backward: bad shape");
-    if (cols > 8192)
-        return fail(EHIP_EINVAL, "layernorm_backward: width %lld > 8192", (long long)cols);
     if (!dy || !xhat || !gamma || !inv_std || !dx || !dgamma || !dbeta)
         return fail(EHIP_EINVAL, "layernorm_backward: null pointer");
     hipStream_t s = as_stream(stream);
+    if (cols > kLnRegisterCols) {
+        // Row groups as for the small problems, fewer for very wide rows so
+        // that the partials stay within 2^24 floats.
+        int64_t groups = std::min<int64_t>(ceil_div(rows, 16), 256);
+        groups = std::min<int64_t>(groups, std::max<int64_t>(1, (int64_t(1) << 23) / cols));
+        if (groups < 1) groups = 1;
+        float* partial =
+            static_cast<float*>(scratch(size_t(groups) * 2 * size_t(cols) * sizeof(float)));
+        if (partial == nullptr) return EHIP_ENOMEM;
+        EHIP_LAUNCH("layernorm_backward", layernorm_rows_backward_loop, dim3(unsigned(groups)),
+                    dim3(kLoopThreads), 0, s, dy, xhat, gamma, inv_std, dx, partial, rows, cols);
+        return column_sums_pair(partial, groups, cols, 2 * cols, cols, dgamma, dbeta, s);
+    }
     // A fixed number of row groups per shape, which fixes the order of the
     // dgamma / dbeta sums.
     const bool vec = cols >= 256 && rows_vec_ok(cols, {dy, xhat, gamma, dx});

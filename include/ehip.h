@@ -706,7 +706,10 @@ int ehip_softmax_backward_scaled_causal_f32(const float* y, const float* g, floa
 
 /* LayerNorm over the last axis (two-pass mean and variance, eps inside the
  * square root) saving xhat and inv_std, and its derivative; dgamma and dbeta
- * are summed over rows in a fixed order (deterministic, no atomics).
+ * are summed over rows in a fixed order (deterministic, no atomics). Rows of
+ * up to 8192 columns are held in registers; wider ones take looped kernels
+ * with the same expressions (up to 4,194,240 columns: 65535 column tiles of
+ * the parameter sums).
  * cuda::ops::layernorm / layernorm_backward (cuda_ops.hpp:193-197). */
 int ehip_layernorm_f32(const float* x, const float* gamma, const float* beta, float* out,
                        float* xhat, float* inv_std, int64_t rows, int64_t cols, float eps,
@@ -720,7 +723,7 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
  * LayerNorm's dgamma / dbeta of a backward in the launch of the conv weight
  * sums, or inside Adam's). ehip_layernorm_backward_partials returns the floats
  * of the partial buffer for rows x cols and the group count through *groups,
- * or 0 when that shape is summed in one call only (fewer than 2^20 elements,
+ * or 0 when that shape is summed in one call only (fewer than 2^17 elements,
  * or more than 2048 columns). ehip_layernorm_backward_partials_f32 writes dx
  * and partials[group][c][2] = (dgamma, dbeta) of each row group; the job
  * {partials, groups, out_channels = cols, k = 1, dweight = dgamma,

@@ -920,7 +920,8 @@ def test_softmax(hip, orc, rows, cols):
                                    (8192, 1024), (300, 260), (64, 4096), (16, 8192),
                                    (2048, 512), (9000, 256), (5000, 257), (700, 2048),
                                    (600, 2000), (20000, 100), (2048, 256), (160, 200),
-                                   (1, 8), (8191, 128)])
+                                   (1, 8), (8191, 128), (64, 8193), (3, 20000),
+                                   (600, 10000)])
 def test_layernorm(hip, orc, rows, d):
     print_case("layernorm", rows, d)
     r = rng(rows + d)
@@ -1069,9 +1070,9 @@ def test_refusals_are_errors(hip):
         import ctypes
         hip.ok(hip.lib.ehip_im2col_f32(hip.p(x), hip.p(x), ctypes.byref(w), hip.stream()),
                "im2col")
-    with pytest.raises(RuntimeError, match="layernorm"):
+    with pytest.raises(RuntimeError, match="layernorm: bad shape"):
         hip.ok(hip.lib.ehip_layernorm_f32(hip.p(x), hip.p(x), hip.p(x), hip.p(x), hip.p(x),
-                                          hip.p(x), 1, 9000, 1e-5, hip.stream()), "layernorm")
+                                          hip.p(x), -1, 16, 1e-5, hip.stream()), "layernorm")
     with pytest.raises(RuntimeError, match="beyond exact indices"):
         import ehip as E
         import ctypes
