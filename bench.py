@@ -14,12 +14,15 @@ The same line carries:
   roofline      the step's dominant kernel, the MFMA weight-gradient products dW = X^T dY
                 (gemm_kernel<128,128,32,64,32,true,false>), timed live at their in-step
                 shapes with HIP events, against the fp32 MFMA peak;
-  cpu_baseline  the reference engine compiled from its own sources (oracle/_ref) running a
-                bounded sample of the same training step on the host cores;
+  cpu_baseline  the reference engine compiled from its own sources (oracle/_ref) running one
+                whole training step of the same model on the host cores (about 40 s);
   extra         the other configurations: cfg 2 CNN and cfg 3 char-Transformer steps (each
                 with its own reference CPU baseline), cfg 1 GEMMs (512^3 and 4096^3), cfg 4
                 bandwidth kernels and the path's other bandwidth kernels, each with its
                 roofline fraction.
+
+The line is compacted (compact()) to about 4 KB so that a log tail keeps all of it;
+--full-out FILE writes the uncompacted record (per-mode GEMM timings, per-shape details).
 
 Only the cpu_baseline legs touch oracle/ (through tests/_oracle.py), as the reference being
 timed; nothing measured on the GPU goes through it.
@@ -233,11 +236,12 @@ def dominant_kernel(eng, timer, torch):
 
 
 def cpu_cfg5_baseline(sample_batch):
-    """A bounded sample of the cfg 5 step on the reference engine (oracle/_ref) on all host
-    cores: the full 12-block model from the same initial parameters, one training step
-    (forward, backward, Adam) over `sample_batch` of the 16 sequences. The step's work is
-    linear in the batch except the Adam update over the 151.7 M parameters, which is timed on
-    its own (the reference's Adam over one flat tensor of that size) and counted once:
+    """The cfg 5 step on the reference engine (oracle/_ref) on all host cores: the full
+    12-block model from the same initial parameters, one training step (forward, backward,
+    Adam). With sample_batch = 16 (the default) that is one whole step, timed as it is (about
+    40 s on 16 threads). A smaller sample_batch times the step over that many of the 16
+    sequences and scales it: the work is linear in the batch except the Adam update over the
+    151.7 M parameters, timed on its own and counted once,
     t(16) = (16 / sample_batch) * (t(sample) - t(adam)) + t(adam)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from _oracle import Ref
@@ -252,22 +256,25 @@ def cpu_cfg5_baseline(sample_batch):
     losses, _ = ref.charlm_train(ids, targets, vocab, d, h, ff, layers, params, 1, 1e-3)
     t_sample = time.perf_counter() - t0
     assert np.all(np.isfinite(losses))
+    info = host_info()
+    cpu = {"cores": threads, "kind": "reference", "cpu_model": info["cpu_model"],
+           "nproc": info["nproc"]}
+    if sample_batch >= b:
+        return {"value": round(1.0 / t_sample, 5), "unit": "steps/s", **cpu,
+                "sample": f"one whole cfg5 step (batch 16 x 512, fwd+bwd+Adam) of the reference "
+                          f"engine (oracle/_ref, its sources, g++ -O3) on {threads} threads from "
+                          f"the GPU run's initial parameters: {t_sample:.1f} s",
+                "seconds_per_step": round(t_sample, 2)}
     g = np.full(params.size, 1e-3, np.float32)
     t0 = time.perf_counter()
     ref.adam_steps(params, g, 1e-3)
     t_adam = time.perf_counter() - t0
     t_full = (b / sample_batch) * (t_sample - t_adam) + t_adam
-    return {"value": round(1.0 / t_full, 5), "unit": "steps/s", "cores": threads,
-            "kind": "reference",
-            "sample": f"cfg5 training step of the reference engine compiled from its own sources "
-                      f"(oracle/_ref, g++ -O3, no -march) on {threads} host threads: the full "
-                      f"12-block model from the GPU run's initial parameters, one step (forward, "
-                      f"backward, Adam) over {sample_batch} of the 16 sequences in "
-                      f"{t_sample:.1f} s, of which Adam over 151.7 M parameters {t_adam:.1f} s; "
-                      f"scaled to 16 sequences as (16/{sample_batch})(t - t_adam) + t_adam = "
-                      f"{t_full:.1f} s per step",
-            "seconds_sample": round(t_sample, 2), "seconds_adam": round(t_adam, 2),
-            "seconds_per_step_scaled": round(t_full, 2), **host_info()}
+    return {"value": round(1.0 / t_full, 5), "unit": "steps/s", **cpu,
+            "sample": f"cfg5 step of the reference engine (oracle/_ref) on {threads} threads over "
+                      f"{sample_batch} of 16 sequences ({t_sample:.1f} s, Adam {t_adam:.1f} s), "
+                      f"scaled to 16: {t_full:.1f} s",
+            "seconds_per_step": round(t_full, 2)}
 
 
 def cpu_matmul_threads(threads_list):
@@ -659,6 +666,65 @@ def kernel_only(eng, hip, timer, torch):
                       "copy_64MiB_us": round(sec * 1e6, 3)}), flush=True)
 
 
+def _r(v, n=3):
+    return None if v is None else round(v, n)
+
+
+def compact_roof(r, keep_kernel=False):
+    out = {"bound": r["bound"], "achieved": r["achieved"], "peak": r["peak"], "unit": r["unit"],
+           "frac": r["frac"], "traffic": r["traffic"]}
+    if keep_kernel:
+        out["kernel"] = r["kernel"]
+    return out
+
+
+def compact(line):
+    """The printed line, compacted so that the whole of it survives a log tail of a few KB:
+    every leg keeps its rate, roofline fraction and CPU baseline; per-mode and per-shape
+    details go to --full-out."""
+    roof = dict(compact_roof(line["roofline"], keep_kernel=True))
+    roof["us_per_launch"] = line["roofline"]["us_per_launch"]
+    roof["flop_per_launch"] = line["roofline"]["flop_per_launch"]
+    roof["shapes_tflops"] = {k: v["tflops"] for k, v in line["roofline"]["shapes"].items()}
+    out = dict(line, roofline=roof)
+    ex = line.get("extra")
+    if not ex:
+        return out
+    c = {}
+    cnn = ex["cnn_cfg2"]
+    c["cnn_cfg2"] = {"steps_per_s": cnn["steps_per_s"], "ms_per_step": cnn["ms_per_step"],
+                     "graph_steps_per_s": cnn["graph"]["steps_per_s"],
+                     "roofline": dict(compact_roof(cnn["roofline"]),
+                                      kernel="conv2 block backward (conv3_pool_backward + "
+                                             "conv_weight_reduce)"),
+                     "cpu_steps_per_s": cnn.get("cpu_baseline", {}).get("value"),
+                     "gpu_over_cpu": cnn.get("gpu_over_cpu")}
+    lm = ex["charlm_cfg3"]
+    c["charlm_cfg3"] = {"steps_per_s": lm["steps_per_s"], "ms_per_step": lm["ms_per_step"],
+                        "achieved_tflops": lm["achieved_tflops"],
+                        "frac_of_mfma_peak": lm["frac_of_mfma_peak"],
+                        "graph_steps_per_s": lm["graph"]["steps_per_s"],
+                        "cpu_steps_per_s": lm.get("cpu_baseline", {}).get("value"),
+                        "gpu_over_cpu": lm.get("gpu_over_cpu")}
+    for n in (512, 4096):
+        g = ex[f"gemm_{n}^3"]
+        pm = g["per_mode"]
+        c[f"gemm_{n}^3"] = {"fwd+bwd_tflops": g["fwd+bwd_tflops"],
+                            "frac": g["fwd+bwd_frac_of_mfma_peak"],
+                            "fwd_us": pm["fwd C=AB"]["us_per_launch"],
+                            "bwd_us": pm["bwd dA and dB (one call)"]["us_per_launch"]}
+    for key in ("bandwidth_cfg4", "bandwidth_transformer_shapes", "bandwidth_2^28"):
+        c[key] = {k: [round(v["achieved"]), v["frac"]] for k, v in ex[key].items()}
+    c["bandwidth_units"] = "[GB/s, fraction of 8000 GB/s]"
+    c["conv_wide_implicit_gemm"] = {
+        k: {"fwd_tflops": v["forward"]["achieved"],
+            "bwd_tflops": v["backward (dx, dW, db)"]["achieved"],
+            "x_composition": v["speedup_over_composition"]}
+        for k, v in ex["conv_wide_implicit_gemm"].items()}
+    out["extra"] = c
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -666,8 +732,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target length of the cfg 2 / cfg 3 reference CPU samples")
-    ap.add_argument("--cpu-sample-batch", type=int, default=4,
-                    help="sequences of the cfg 5 batch in the reference CPU sample")
+    ap.add_argument("--cpu-sample-batch", type=int, default=16,
+                    help="sequences of the cfg 5 batch in the reference CPU sample (16: one "
+                         "whole step, timed as it is)")
+    ap.add_argument("--full-out", default=None,
+                    help="also write the uncompacted record (every leg's details) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
@@ -748,7 +817,10 @@ def main():
                    "compute_units": info.compute_units},
         "extra": extra,
     }
-    print(json.dumps(line), flush=True)
+    if args.full_out:
+        with open(args.full_out, "w") as f:
+            json.dump(line, f)
+    print(json.dumps(compact(line)), flush=True)
 
 
 if __name__ == "__main__":

@@ -80,13 +80,28 @@ def cpu_model():
 VARIANTS = {"": "libref_engine.so", "_fma": "libref_engine_fma.so"}
 
 
+def cache_path(args, suffix):
+    return os.path.join(args.work, f"cfg5_ref{suffix}_{args.steps}.npz")
+
+
 def run_variant(suffix, args, params, ids, targets):
-    """One training run of the compiled reference; cached in args.work by variant and steps."""
+    """One training run of the compiled reference, cached in args.work by variant and steps.
+    Each run happens in a child process: the reference's buffer pool keeps every block it
+    ever allocated (about 30 GB for this model), so two runs in one process would hold
+    both."""
+    cache = cache_path(args, suffix)
+    if not os.path.exists(cache):
+        import subprocess
+        subprocess.run([sys.executable, os.path.abspath(__file__), "--steps", str(args.steps),
+                        "--threads", str(args.threads), "--work", args.work,
+                        "--variant", suffix or "release"], check=True)
+    with np.load(cache, allow_pickle=False) as z:
+        return z["losses"], z["final"], z["g0"], float(z["wall"])
+
+
+def compute_variant(suffix, args, params, ids, targets):
     from _oracle import Ref
-    cache = os.path.join(args.work, f"cfg5_ref{suffix}_{args.steps}.npz")
-    if os.path.exists(cache):
-        with np.load(cache, allow_pickle=False) as z:
-            return z["losses"], z["final"], z["g0"], float(z["wall"])
+    cache = cache_path(args, suffix)
     b, s, vocab, d, heads, ff, layers = W.TRANSFORMER_CFG5
     ref = Ref(os.path.join(ROOT, "oracle", "_ref", VARIANTS[suffix]))
     ref.set_threads(args.threads)
@@ -99,7 +114,6 @@ def run_variant(suffix, args, params, ids, targets):
           f"losses {losses}", flush=True)
     os.makedirs(args.work, exist_ok=True)
     np.savez(cache, losses=losses, final=final, g0=g0, wall=wall)
-    return losses, final, g0, wall
 
 
 def main():
@@ -108,11 +122,15 @@ def main():
     ap.add_argument("--threads", type=int, default=os.cpu_count() or 1)
     ap.add_argument("--out", default=os.path.join(HERE, "cfg5_reference.npz"))
     ap.add_argument("--work", default="/tmp/cfg5_golden")
+    ap.add_argument("--variant", choices=["release", "fma"], help=argparse.SUPPRESS)
     args = ap.parse_args()
 
     b, s, vocab, d, heads, ff, layers = W.TRANSFORMER_CFG5
     params = W.lm_init_params(PARAM_SEED, vocab, d, ff, layers)
     ids, targets = W.lm_inputs(INPUT_SEED, b, s, vocab)
+    if args.variant:  # the child process of run_variant
+        compute_variant("" if args.variant == "release" else "_fma", args, params, ids, targets)
+        return
     layout = W.lm_param_layout(vocab, d, ff, layers)
     out, walls = {}, {}
     names = [name for name, _, _ in layout]
