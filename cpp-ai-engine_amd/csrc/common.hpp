@@ -46,6 +46,20 @@ inline bool capturing() { return t_capture != nullptr; }
 constexpr int kScratchSlots = 2;
 void* scratch(size_t bytes, int slot = 0);
 
+// Kernels reported by ehip_kernel_occupancy: each source file registers its
+// representative instantiations (name, kernel, the block size it launches
+// with) through a file-scope OccupancyEntries object at load time.
+struct OccupancyKernel {
+    const char* name;
+    const void* func;
+    int block_threads;
+};
+void register_occupancy(const OccupancyKernel* kernels, int count);
+struct OccupancyEntries {
+    template <int N>
+    explicit OccupancyEntries(const OccupancyKernel (&k)[N]) { register_occupancy(k, N); }
+};
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Column sums of `slabs` row-major (rows, cols) matrices with row pitch `ld`,

@@ -1941,6 +1941,12 @@ int check_conv(const char* name, const ehip_window_t* w, int64_t cout) {
     return EHIP_OK;
 }
 
+const OccupancyKernel kConvKernels[] = {
+    {"conv_weight_reduce", reinterpret_cast<const void*>(&conv_weight_reduce), 256},
+    {"conv_weight_reduce_batch", reinterpret_cast<const void*>(&conv_weight_reduce_batch), 256},
+};
+const OccupancyEntries kConvKernelsReg(kConvKernels);
+
 }  // namespace
 }  // namespace ehip
 

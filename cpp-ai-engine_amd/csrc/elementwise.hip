@@ -723,6 +723,14 @@ int binary_op(const float* a, const float* b, float* out, int64_t inner, int64_t
     return launch_stream("binary", Binary<OP>{a, b, out, inner}, inner * repeat, vec, s);
 }
 
+const OccupancyKernel kElementwiseKernels[] = {
+    {"stream_vec<ReluBackward>", reinterpret_cast<const void*>(&stream_vec<ReluBackward, true>), kThreads},
+    {"stream_vec<Adam>", reinterpret_cast<const void*>(&stream_vec<Adam, true>), kThreads},
+    {"adam_multi", reinterpret_cast<const void*>(&adam_multi<true>), kThreads},
+    {"adam_multi_reduce", reinterpret_cast<const void*>(&adam_multi_reduce<true, 1>), kThreads},
+};
+const OccupancyEntries kElementwiseKernelsReg(kElementwiseKernels);
+
 }  // namespace
 }  // namespace ehip
 

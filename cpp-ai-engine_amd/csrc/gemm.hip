@@ -631,6 +631,24 @@ int check_desc(const ehip_gemm_ex_t& d) {
     return EHIP_OK;
 }
 
+const OccupancyKernel kGemmKernels[] = {
+    {"gemm_kernel 256x256x16, 8 waves of 128x64 (NN)",
+     reinterpret_cast<const void*>(&gemm_kernel<256, 256, 16, 128, 64, false, false, false, false>), 512},
+    {"gemm_kernel 128x128x32, 8 waves of 64x32 (TN: dW)",
+     reinterpret_cast<const void*>(&gemm_kernel<128, 128, 32, 64, 32, true, false, false, false>), 512},
+    {"gemm_kernel 128x128x32 (NT: dX, [row][k] tiles)",
+     reinterpret_cast<const void*>(&gemm_kernel<128, 128, 32, 64, 32, false, true, false, false>), 512},
+    {"gemm_kernel 128x64x32, 8 waves of 32x32 (NN)",
+     reinterpret_cast<const void*>(&gemm_kernel<128, 64, 32, 32, 32, false, false, false, false>), 512},
+    {"gemm_kernel 64x64x16 checked, 4 waves (NN)",
+     reinterpret_cast<const void*>(&gemm_kernel<64, 64, 16, 32, 32, false, false, true, false>), 256},
+    {"gemm_kslice 32x32, 8 waves (NN)",
+     reinterpret_cast<const void*>(&gemm_kslice<8, false, false, false, false>), 512},
+    {"gemm_small_thread (NN)", reinterpret_cast<const void*>(&gemm_small_thread<false, false>), 256},
+    {"gemm_splitk_reduce", reinterpret_cast<const void*>(&splitk_reduce), 256},
+};
+const OccupancyEntries kGemmKernelsReg(kGemmKernels);
+
 }  // namespace
 }  // namespace ehip
 

@@ -408,6 +408,13 @@ int maxpool_backward(const char* name, const Idx* argmax, const float* g, float*
     return EHIP_OK;
 }
 
+const OccupancyKernel kLayoutKernels[] = {
+    {"transpose_tiled", reinterpret_cast<const void*>(&transpose_tiled), kT * 4},
+    {"maxpool_2x2_kernel", reinterpret_cast<const void*>(&maxpool_2x2_kernel<int32_t>), kThreads},
+    {"im2col_kernel", reinterpret_cast<const void*>(&im2col_kernel), kThreads},
+};
+const OccupancyEntries kLayoutKernelsReg(kLayoutKernels);
+
 }  // namespace
 
 int check_window(const char* name, const ehip_window_t* w) {

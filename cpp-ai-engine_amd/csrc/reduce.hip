@@ -194,6 +194,12 @@ __global__ __launch_bounds__(kThreads) void reduce_stage2(const double* __restri
     }
 }
 
+const OccupancyKernel kReduceKernels[] = {
+    {"sum_cols4 (bias-gradient column sums)", reinterpret_cast<const void*>(&sum_cols4), kThreads},
+    {"reduce_stage1 (double sum)", reinterpret_cast<const void*>(&reduce_stage1<false>), kThreads},
+};
+const OccupancyEntries kReduceKernelsReg(kReduceKernels);
+
 }  // namespace
 
 // Two passes of sum_cols: row blocks into partials, then the partials of each

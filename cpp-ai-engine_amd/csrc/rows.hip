@@ -1015,6 +1015,29 @@ int64_t ln_wide_groups(int64_t rows, int64_t cols) {
     return std::min<int64_t>(ceil_div(rows, 32), 256);
 }
 
+// One width class of the large-problem row kernel: four rows in flight per
+// wave below 2^25 elements for rows of up to 1024 columns (512 without
+// 16-byte rows), one otherwise. Wider rows take one row at a time always
+// (four would need more registers than a lane has: the compiler spills), so
+// those instantiations are never compiled.
+template <int V, bool VEC>
+int launch_ln_wide_v(bool ahead, const float* dy, const float* xhat, const float* gamma,
+                     const float* inv_std, float* dx, float* partial, int64_t groups,
+                     int64_t rows, int64_t cols, hipStream_t s) {
+    if constexpr (V <= (VEC ? 16 : 8)) {
+        if (ahead) {
+            EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 4>),
+                        dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma, inv_std,
+                        dx, partial, rows, cols);
+            return EHIP_OK;
+        }
+    }
+    EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 1>),
+                dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma, inv_std, dx,
+                partial, rows, cols);
+    return EHIP_OK;
+}
+
 // Launches the large-problem row kernel for `groups` groups.
 int launch_ln_wide(const float* dy, const float* xhat, const float* gamma, const float* inv_std,
                    float* dx, float* partial, int64_t groups, int64_t rows, int64_t cols,
@@ -1022,33 +1045,37 @@ int launch_ln_wide(const float* dy, const float* xhat, const float* gamma, const
     const bool vec = cols >= 256 && rows_vec_ok(cols, {dy, xhat, gamma, dx});
     // Four rows ahead below the last-level cache size, one beyond it (2^25 elements).
     const bool ahead = rows * cols < (int64_t(1) << 25);
-#define EHIP_LNW(V, VEC)                                                                           \
-    do {                                                                                           \
-        if (ahead && V <= 16)                                                                      \
-            EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 4>),           \
-                        dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma,        \
-                        inv_std, dx, partial, rows, cols);                                         \
-        else                                                                                       \
-            EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 1>),           \
-                        dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma,        \
-                        inv_std, dx, partial, rows, cols);                                         \
-    } while (0)
+#define EHIP_LNW(V, VEC) \
+    return launch_ln_wide_v<V, VEC>(ahead, dy, xhat, gamma, inv_std, dx, partial, groups, rows, cols, s)
     if (vec) {
         if (cols <= 256) EHIP_LNW(4, true);
-        else if (cols <= 512) EHIP_LNW(8, true);
-        else if (cols <= 1024) EHIP_LNW(16, true);
-        else EHIP_LNW(32, true);
-    } else if (cols <= 64) EHIP_LNW(1, false);
-    else if (cols <= 128) EHIP_LNW(2, false);
-    else if (cols <= 256) EHIP_LNW(4, false);
-    else if (cols <= 512) EHIP_LNW(8, false);
-    else if (cols <= 1024) EHIP_LNW(16, false);
-    else EHIP_LNW(32, false);
+        if (cols <= 512) EHIP_LNW(8, true);
+        if (cols <= 1024) EHIP_LNW(16, true);
+        EHIP_LNW(32, true);
+    }
+    if (cols <= 64) EHIP_LNW(1, false);
+    if (cols <= 128) EHIP_LNW(2, false);
+    if (cols <= 256) EHIP_LNW(4, false);
+    if (cols <= 512) EHIP_LNW(8, false);
+    if (cols <= 1024) EHIP_LNW(16, false);
+    EHIP_LNW(32, false);
 #undef EHIP_LNW
-    return EHIP_OK;
 }
 
 unsigned loop_grid(int64_t rows) { return unsigned(rows < 65536 ? rows : 65536); }
+
+const OccupancyKernel kRowKernels[] = {
+    {"softmax_rows, 64-lane rows of 512", reinterpret_cast<const void*>(&softmax_rows<64, 8, true, false>), 256},
+    {"softmax_rows, 1024-thread rows of 32768",
+     reinterpret_cast<const void*>(&softmax_rows<1024, 32, true, true>), 1024},
+    {"xent_rows_backward_fused, rows of 32000",
+     reinterpret_cast<const void*>(&xent_rows_backward_fused<1024, 32, true, true>), 1024},
+    {"layernorm_rows, rows of 1024", reinterpret_cast<const void*>(&layernorm_rows<64, 16, true, false>), 256},
+    {"layernorm_rows_backward_wide, rows of 1024, 4 ahead",
+     reinterpret_cast<const void*>(&layernorm_rows_backward_wide<16, true, 4>), 64 * kLnWaves},
+    {"softmax_rows_loop", reinterpret_cast<const void*>(&softmax_rows_loop), kLoopThreads},
+};
+const OccupancyEntries kRowKernelsReg(kRowKernels);
 
 }  // namespace
 }  // namespace ehip

@@ -77,7 +77,22 @@ void init_once() {
     g_ctx.status = EHIP_OK;
 }
 
+std::mutex& occupancy_mu() {
+    static std::mutex mu;
+    return mu;
+}
+
+std::vector<OccupancyKernel>& occupancy_kernels() {
+    static std::vector<OccupancyKernel> all;
+    return all;
+}
+
 }  // namespace
+
+void register_occupancy(const OccupancyKernel* kernels, int count) {
+    std::lock_guard<std::mutex> lock(occupancy_mu());
+    occupancy_kernels().insert(occupancy_kernels().end(), kernels, kernels + count);
+}
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -205,6 +220,63 @@ int ehip_enabled(void) { return g_enabled.load(); }
 void ehip_set_enabled(int on) {
     std::call_once(g_init_once, init_once);
     g_enabled = on ? 1 : 0;
+}
+
+int ehip_version_info(int* compiled, int* runtime, int* driver) {
+    if (!compiled || !runtime || !driver) return fail(EHIP_EINVAL, "ehip_version_info: null output");
+    *compiled = HIP_VERSION;
+    *runtime = 0;
+    *driver = 0;
+    hipError_t e = hipRuntimeGetVersion(runtime);
+    if (e != hipSuccess)
+        return fail(EHIP_ENODEV, "hipRuntimeGetVersion: %s", hipGetErrorString(e));
+    e = hipDriverGetVersion(driver);
+    if (e != hipSuccess)
+        return fail(EHIP_ENODEV, "hipDriverGetVersion: %s", hipGetErrorString(e));
+    return EHIP_OK;
+}
+
+int ehip_kernel_occupancy(ehip_kernel_occupancy_t* out, int capacity, int* count) {
+    if (count == nullptr || (capacity > 0 && out == nullptr))
+        return fail(EHIP_EINVAL, "ehip_kernel_occupancy: null output");
+    if (int rc = ehip_init()) return rc;
+    const hipDeviceProp_t& p = g_ctx.prop;
+    const int max_waves = p.maxThreadsPerMultiProcessor / 64;  // per CU
+    const int64_t lds_cu = int64_t(p.maxSharedMemoryPerMultiProcessor);
+    std::lock_guard<std::mutex> lock(occupancy_mu());
+    const std::vector<OccupancyKernel>& all = occupancy_kernels();
+    *count = int(all.size());
+    for (int i = 0; i < int(all.size()) && i < capacity; ++i) {
+        const OccupancyKernel& k = all[i];
+        ehip_kernel_occupancy_t& o = out[i];
+        std::memset(&o, 0, sizeof(o));
+        std::snprintf(o.name, sizeof(o.name), "%s", k.name);
+        o.block_threads = k.block_threads;
+        hipFuncAttributes fa{};
+        hipError_t e = hipFuncGetAttributes(&fa, k.func);
+        if (e != hipSuccess)
+            return fail(EHIP_ENODEV, "hipFuncGetAttributes(%s): %s", k.name, hipGetErrorString(e));
+        int blocks = 0;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, k.func, k.block_threads, 0);
+        if (e != hipSuccess)
+            return fail(EHIP_ENODEV, "hipOccupancyMaxActiveBlocksPerMultiprocessor(%s): %s",
+                        k.name, hipGetErrorString(e));
+        o.registers = fa.numRegs;
+        o.lds_bytes = int64_t(fa.sharedSizeBytes);
+        o.blocks_per_cu = blocks;
+        const int waves = (k.block_threads + 63) / 64;
+        o.occupancy = max_waves > 0 ? double(blocks * waves) / max_waves : 0.0;
+        // What runs out first: LDS when one more block would not fit in it,
+        // waves when one more block's waves would exceed the CU's, registers
+        // otherwise.
+        const char* lim = "registers";
+        if (o.lds_bytes > 0 && (blocks + 1) * o.lds_bytes > lds_cu)
+            lim = "lds";
+        else if ((blocks + 1) * waves > max_waves)
+            lim = "waves";
+        std::snprintf(o.limiter, sizeof(o.limiter), "%s", lim);
+    }
+    return EHIP_OK;
 }
 
 int ehip_device_info(ehip_device_info_t* out) {

@@ -33,6 +33,12 @@ class AdamTensor(C.Structure):
                 ("n", C.c_int64)]
 
 
+class KernelOccupancy(C.Structure):
+    _fields_ = [("name", C.c_char * 96), ("block_threads", C.c_int), ("registers", C.c_int),
+                ("lds_bytes", C.c_int64), ("blocks_per_cu", C.c_int), ("occupancy", C.c_double),
+                ("limiter", C.c_char * 16)]
+
+
 class DeviceInfo(C.Structure):
     _fields_ = [("name", C.c_char * 256), ("arch", C.c_char * 64), ("compute_units", C.c_int),
                 ("clock_khz", C.c_int), ("memory_clock_khz", C.c_int),
@@ -77,6 +83,8 @@ class GemmEx(C.Structure):
 _SIGS = {
     "ehip_init": [], "ehip_available": [], "ehip_enabled": [], "ehip_set_enabled": [_i],
     "ehip_device_info": [C.POINTER(DeviceInfo)], "ehip_synchronize": [],
+    "ehip_version_info": [C.POINTER(C.c_int)] * 3,
+    "ehip_kernel_occupancy": [C.POINTER(KernelOccupancy), C.c_int, C.POINTER(C.c_int)],
     "ehip_stream_synchronize": [_vp], "ehip_kernels_launched": [], "ehip_kernels_failed": [],
     "ehip_reset_counters": [], "ehip_fail_launch_after": [_i64], "ehip_transfer_stats": [C.POINTER(TransferStats)],
     "ehip_reset_transfer_stats": [], "ehip_arena_alloc": [_sz, C.POINTER(_vp)],
@@ -230,6 +238,19 @@ class Backend:
         info = DeviceInfo()
         self.ok(self.lib.ehip_device_info(C.byref(info)), "device_info")
         return info
+
+    def versions(self):
+        v = [C.c_int(0) for _ in range(3)]
+        self.ok(self.lib.ehip_version_info(*[C.byref(x) for x in v]), "version_info")
+        return tuple(x.value for x in v)
+
+    def kernel_occupancy(self):
+        count = C.c_int(0)
+        self.ok(self.lib.ehip_kernel_occupancy(None, 0, C.byref(count)), "kernel_occupancy")
+        arr = (KernelOccupancy * max(count.value, 1))()
+        self.ok(self.lib.ehip_kernel_occupancy(arr, count.value, C.byref(count)),
+                "kernel_occupancy")
+        return [arr[i] for i in range(count.value)]
 
     def launched(self):
         return self.lib.ehip_kernels_launched()

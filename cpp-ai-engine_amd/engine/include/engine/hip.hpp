@@ -8,11 +8,27 @@
 #include <functional>
 #include <optional>
 #include <string>
+#include <vector>
 
 namespace engine {
 namespace hip {
 
 bool available();
+
+// Runtime switch (the reference's cuda::enabled / set_enabled). It starts on,
+// or off with ENGINE_HIP=0 in the environment. This engine computes on the
+// device only: with the backend switched off every operation that would launch
+// a kernel throws (std::runtime_error, "switched off"), where the reference
+// would run its CPU loops.
+bool enabled();
+void set_enabled(bool on);
+
+// The HIP versions in play, in HIP's encoding (major * 10000000 + minor *
+// 100000 + patch): the headers the backend was compiled with, and the runtime
+// and driver it runs on; 0 where the runtime cannot tell.
+int compiled_version();
+int runtime_version();
+int driver_version();
 
 struct DeviceInfo {
     std::string name;
@@ -28,6 +44,23 @@ size_t kernels_failed();
 void reset_kernel_counters();
 double peak_fp32_gflops();
 double peak_bandwidth_gbs();
+
+// What each of the backend's main kernels costs the scheduler on this device:
+// the block size it is launched with, VGPRs per lane, static LDS per block,
+// the blocks that fit on one CU at once, the resident waves that makes as a
+// fraction of the CU's maximum, and what runs out first ("registers", "lds" or
+// "waves"). The static ceiling, not the achieved occupancy. Empty without a
+// device.
+struct KernelOccupancy {
+    std::string name;
+    int block_threads = 0;
+    int registers = 0;
+    size_t shared_bytes = 0;
+    int blocks_per_cu = 0;
+    double occupancy = 0.0;
+    std::string limiter;
+};
+std::vector<KernelOccupancy> kernel_occupancy();
 
 struct TransferStats {
     size_t to_device_bytes = 0;

@@ -10,6 +10,7 @@
 // host transfers: eng_trainer_step() enqueues forward, backward and the Adam
 // update and returns without waiting.
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <exception>
@@ -205,6 +206,32 @@ extern "C" {
 const char* eng_last_error() { return g_error.c_str(); }
 
 int eng_available() { return engine::hip::available() ? 1 : 0; }
+
+// engine::hip's control API (the reference's cuda.hpp:28-29, 67-69, 100-125).
+int eng_enabled() { return engine::hip::enabled() ? 1 : 0; }
+void eng_set_enabled(int on) { engine::hip::set_enabled(on != 0); }
+void eng_versions(int* compiled, int* runtime, int* driver) {
+    *compiled = engine::hip::compiled_version();
+    *runtime = engine::hip::runtime_version();
+    *driver = engine::hip::driver_version();
+}
+// Writes up to `capacity` lines "name|threads|registers|lds|blocks|occupancy|limiter"
+// into out (NUL-separated lines in one buffer of `bytes`); returns the kernel count.
+int eng_kernel_occupancy(char* out, int64_t bytes) {
+    const auto all = engine::hip::kernel_occupancy();
+    std::string text;
+    for (const auto& k : all)
+        text += k.name + "|" + std::to_string(k.block_threads) + "|" +
+                std::to_string(k.registers) + "|" + std::to_string(k.shared_bytes) + "|" +
+                std::to_string(k.blocks_per_cu) + "|" + std::to_string(k.occupancy) + "|" +
+                k.limiter + "\n";
+    if (out != nullptr && bytes > 0) {
+        const size_t n = std::min(text.size(), size_t(bytes - 1));
+        std::memcpy(out, text.data(), n);
+        out[n] = '\0';
+    }
+    return int(all.size());
+}
 
 // Host-only: reads an IDX file's header and payload (engine/src/data.cpp)
 // and returns the items kept and the payload size, or the reader's error.

@@ -17,6 +17,46 @@ void check(int rc, const char* what) {
 
 bool available() { return ehip_available() != 0; }
 
+bool enabled() { return ehip_enabled() != 0; }
+
+void set_enabled(bool on) { ehip_set_enabled(on ? 1 : 0); }
+
+namespace {
+struct Versions {
+    int compiled = 0, runtime = 0, driver = 0;
+};
+Versions versions() {
+    Versions v;
+    (void)ehip_version_info(&v.compiled, &v.runtime, &v.driver);
+    return v;
+}
+}  // namespace
+
+int compiled_version() { return versions().compiled; }
+int runtime_version() { return versions().runtime; }
+int driver_version() { return versions().driver; }
+
+std::vector<KernelOccupancy> kernel_occupancy() {
+    int count = 0;
+    if (ehip_kernel_occupancy(nullptr, 0, &count) != EHIP_OK || count <= 0) return {};
+    std::vector<ehip_kernel_occupancy_t> raw(static_cast<size_t>(count));
+    if (ehip_kernel_occupancy(raw.data(), count, &count) != EHIP_OK) return {};
+    std::vector<KernelOccupancy> out;
+    out.reserve(raw.size());
+    for (const ehip_kernel_occupancy_t& r : raw) {
+        KernelOccupancy k;
+        k.name = r.name;
+        k.block_threads = r.block_threads;
+        k.registers = r.registers;
+        k.shared_bytes = size_t(r.lds_bytes);
+        k.blocks_per_cu = r.blocks_per_cu;
+        k.occupancy = r.occupancy;
+        k.limiter = r.limiter;
+        out.push_back(std::move(k));
+    }
+    return out;
+}
+
 std::optional<DeviceInfo> device_info() {
     ehip_device_info_t info;
     if (ehip_device_info(&info) != EHIP_OK) return std::nullopt;

@@ -81,6 +81,32 @@ typedef struct {
  * (include/engine/cuda.hpp:49, 93-95). */
 int ehip_device_info(ehip_device_info_t* out);
 
+/* The HIP versions in play, in HIP's encoding (major * 10000000 + minor *
+ * 100000 + patch): the headers this library was compiled with, the runtime
+ * and the driver it runs on (cuda::compiled_version / runtime_version /
+ * driver_version, include/engine/cuda.hpp:67-69). A query the runtime cannot
+ * answer leaves 0 there and returns its error. */
+int ehip_version_info(int* compiled, int* runtime, int* driver);
+
+/* The static occupancy of the library's main kernels on this device
+ * (cuda::kernel_occupancy, include/engine/cuda.hpp:100-125): for each, the block
+ * size it is launched with, VGPRs per lane, static LDS per block, the blocks
+ * that fit on one CU at once (hipOccupancyMaxActiveBlocksPerMultiprocessor),
+ * the resident waves that makes as a fraction of the CU's maximum, and the
+ * resource that runs out first ("registers", "lds" or "waves"). The ceiling,
+ * not the achieved occupancy. Writes at most `capacity` entries and the number
+ * available to *count. */
+typedef struct {
+    char name[96];
+    int block_threads;
+    int registers;
+    int64_t lds_bytes;
+    int blocks_per_cu;
+    double occupancy;
+    char limiter[16];
+} ehip_kernel_occupancy_t;
+int ehip_kernel_occupancy(ehip_kernel_occupancy_t* out, int capacity, int* count);
+
 /* Waits for all work on the device (cuda::synchronize, include/engine/cuda.hpp:53). */
 int ehip_synchronize(void);
 /* Waits for one stream. */

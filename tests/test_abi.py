@@ -66,3 +66,16 @@ def test_igemm_supported_is_a_pure_query(lib):
     assert f(ctypes.byref(win(65536, 64, 4, 4)), 128) == 0
     assert f(ctypes.byref(win(4096, 3, 1024, 1024)), 16) == 0
     assert f(None, 16) == 0 and f(ctypes.byref(win(1, 1, 4, 4)), 0) == 0
+
+
+def test_control_queries_without_a_device(lib):
+    """The version and occupancy queries report a missing device as a status, and the
+    compiled-in HIP version is known without one."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    v = [ctypes.c_int(-1) for _ in range(3)]
+    lib.ehip_version_info(*[ctypes.byref(x) for x in v])
+    assert v[0].value >= 60000000, v[0].value  # HIP 6.0 or later in HIP's encoding
+    count = ctypes.c_int(-1)
+    assert lib.ehip_kernel_occupancy(None, 0, ctypes.byref(count)) == 3  # EHIP_ENODEV
