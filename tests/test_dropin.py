@@ -15,8 +15,13 @@ against this repository's engine headers and linked with libengine_hip.so
   differently on every run (an unseeded generator in the tensor-basics demo). Those are
   compared as text; the Transformer demo must still learn its task (over 50 % on the test
   set, where chance is 16.7 %).
-  charlm_demo is built but not run: it reads a corpus from the reference checkout, which
-  the GPU box does not have.
+- The character-level language model demo (charlm_demo.cpp), built with ENGINE_REPO_DIR
+  pointing at a synthetic corpus (tests/dropin/make_corpus.py, written at build time; the
+  demo reads the reference checkout's documentation otherwise), 200 training steps: the
+  corpus and model lines identical to the reference's, the loss at step 1 within 1e-4 and
+  at steps 100 and 200 within max(2 %, 4x the reference's own FMA-rounding spread) of it,
+  and the generated-text section in the reference's shape (its text is sampled from a
+  trained model and differs between any two roundings).
 - The reference's unit suites but its CUDA one (its tests/test_tensor.cpp,
   test_autograd.cpp, test_nn.cpp, test_conv.cpp, test_transformer.cpp and
   test_reference.cpp, the last against the committed PyTorch fixtures), run through
@@ -109,3 +114,35 @@ def test_reference_unit_suites_on_the_engine():
     import re
     checks = int(re.search(r"reference suites: (\d+) checks", run.stdout).group(1))
     assert checks >= 500, f"only {checks} checks ran"
+
+
+LOSS = re.compile(r"step\s+(\d+) \| loss = ([\d.]+)")
+
+
+def test_reference_charlm_demo_on_the_engine():
+    exe = os.path.join(BUILD, "charlm_demo")
+    if not os.path.exists(exe):
+        pytest.skip("drop-in binaries not built (they need the reference checkout)")
+    print_case("drop-in example", "charlm_demo 200")
+    run = subprocess.run([exe, "200"], capture_output=True, text=True, timeout=300)
+    assert run.returncode == 0, run.stderr[-2000:]
+    with open(os.path.join(GOLDEN, "charlm_demo.txt")) as f:
+        ref = f.read()
+    with open(os.path.join(GOLDEN, "charlm_demo.fma.txt")) as f:
+        fma = f.read()
+    out = run.stdout
+    head = ref.split("--- 3. Training")[0]
+    assert out.split("--- 3. Training")[0] == head, "corpus and model lines differ"
+    got = {int(a): float(b) for a, b in LOSS.findall(out)}
+    want = {int(a): float(b) for a, b in LOSS.findall(ref)}
+    spread = {int(a): float(b) for a, b in LOSS.findall(fma)}
+    assert sorted(got) == sorted(want) == [1, 100, 200], (got, want)
+    for step, w in want.items():
+        tol = 1e-4 * w if step == 1 else max(2e-2 * w, 4 * abs(spread[step] - w))
+        print(f"charlm_demo step {step}: loss {got[step]:.4f}, reference {w:.4f} "
+              f"(FMA reference {spread[step]:.4f}), bound {tol:.4f}")
+        assert abs(got[step] - w) <= tol, (step, got[step], w, tol)
+    gen = out.split("--- 4. Generated text ---")[1]
+    assert gen.count("temperature 0.5:") == 1 and gen.count("temperature 0.8:") == 1
+    assert gen.count("    The engine ") == 2
+    assert out.rstrip().splitlines()[-2:] == ref.rstrip().splitlines()[-2:]
