@@ -18,6 +18,11 @@ def hip():
 
 @pytest.fixture(scope="module")
 def eng():
+    # torch's HIP runtime first, as the other GPU fixtures do: initialised after the engine
+    # library in a fresh process, torch reports no device.
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test ran without a visible GPU")
     from engine_capi import Engine
     e = Engine()
     e.lib.eng_set_enabled.argtypes = [C.c_int]
