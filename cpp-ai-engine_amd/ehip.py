@@ -137,6 +137,9 @@ _SIGS = {
     "ehip_conv2d_forward_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_backward_input_f32": [_vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_backward_weight_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
+    "ehip_attention_short_supported": [_i64, _i64],
+    "ehip_attention_short_f32": [_vp] * 5 + [_i64] * 5 + [_f, _i, _vp],
+    "ehip_attention_short_backward_f32": [_vp] * 8 + [_i64] * 5 + [_f, _i, _vp],
     "ehip_conv2d_igemm_supported": [C.POINTER(Window), _i64],
     "ehip_conv2d_igemm_f32": [_vp, _vp, _vp, _vp, C.POINTER(Window), _i64, _vp],
     "ehip_conv2d_igemm_backward_f32": [_vp] * 6 + [C.POINTER(Window), _i64, _vp],
@@ -238,6 +241,27 @@ class Backend:
         info = DeviceInfo()
         self.ok(self.lib.ehip_device_info(C.byref(info)), "device_info")
         return info
+
+    def attention_short(self, q, k, v, heads, scale, causal):
+        """q, k, v: (batch, seq, width) device tensors; returns (weights, out)."""
+        b, s_, w = q.shape
+        hd = w // heads
+        weights, out = self.f32((b, heads, s_, s_)), self.f32((b, s_, w))
+        self.ok(self.lib.ehip_attention_short_f32(self.p(q), self.p(k), self.p(v), self.p(weights),
+                                                  self.p(out), b, s_, w, heads, hd, scale,
+                                                  int(causal), self.stream()), "attention_short")
+        return weights, out
+
+    def attention_short_backward(self, q, k, v, weights, g, heads, scale, causal,
+                                 want=(True, True, True)):
+        b, s_, w = q.shape
+        hd = w // heads
+        outs = [self.f32((b, s_, w)) if x else None for x in want]
+        self.ok(self.lib.ehip_attention_short_backward_f32(
+            self.p(q), self.p(k), self.p(v), self.p(weights), self.p(g), self.p(outs[0]),
+            self.p(outs[1]), self.p(outs[2]), b, s_, w, heads, hd, scale, int(causal),
+            self.stream()), "attention_short_backward")
+        return outs
 
     def versions(self):
         v = [C.c_int(0) for _ in range(3)]

@@ -25,6 +25,16 @@ namespace nn {
 void set_fused_nodes(bool on);
 bool fused_nodes();
 
+// Short attention, on by default: the fused attention node takes one launch
+// per direction (ehip_attention_short_f32 and its backward: a workgroup per
+// batch and head, scores, softmax and products in LDS, each sum in the
+// reference's loop order) for sequences and heads of at most 64 values, with
+// no mask or nn::causal_mask's. Off, those take the batched products and
+// softmax kernels as longer sequences do; the values agree to the reference's
+// tolerance, not bit for bit. Process-wide; set it between steps.
+void set_short_attention(bool on);
+bool short_attention();
+
 // Bias gradients from the weight-gradient product, on by default: Linear and
 // the feed-forward node take db of a mid-sized layer (more than 64 rows, dY of
 // at most 2^21 elements) from the column sums of dY that the dW = X^T dY

@@ -519,6 +519,12 @@ int eng_set_fused_nodes(int on) {
     return was ? 1 : 0;
 }
 
+int eng_set_short_attention(int on) {
+    const bool was = nn::short_attention();
+    nn::set_short_attention(on != 0);
+    return was ? 1 : 0;
+}
+
 int eng_set_conv_implicit_gemm(int on) {
     const bool was = nn::conv_implicit_gemm();
     nn::set_conv_implicit_gemm(on != 0);

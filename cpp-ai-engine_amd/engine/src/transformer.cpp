@@ -267,6 +267,49 @@ ehip_gemm_ex_t head_product(bool ta, bool tb, size_t batch, size_t heads, size_t
 
 }  // namespace
 
+namespace {
+
+// Sequences and heads of at most 64 values: the whole attention of a head in
+// one workgroup (ehip_attention_short_f32 / _backward_f32), two launches per
+// step instead of eight; the weights are kept for the backward as the product
+// path keeps them.
+Tensor attention_short(const Tensor& query, const Tensor& key, const Tensor& value, size_t B,
+                       size_t S, size_t D, size_t H, size_t hd, float scale, bool causal,
+                       Tensor* attention_weights) {
+    Tensor weights({B, H, S, S}, 0.0f, false);
+    Tensor out({B, S, D}, 0.0f, false);
+    hip::check(ehip_attention_short_f32(dptr(query), dptr(key), dptr(value), dout(weights),
+                                        dout(out), int64_t(B), int64_t(S), int64_t(D), int64_t(H),
+                                        int64_t(hd), scale, causal ? 1 : 0, nullptr),
+               "attention");
+    if (attention_weights != nullptr) *attention_weights = weights.detach();
+    if (!track(query.requires_grad() || key.requires_grad() || value.requires_grad())) return out;
+    out.set_requires_grad(true);
+    out.get_impl()->parents = {query.get_impl(), key.get_impl(), value.get_impl()};
+    Tensor q = query, k = key, v = value;
+    out.get_impl()->backward_fn = [q, k, v, weights, B, S, D, H, hd, scale,
+                                   causal](const Tensor& g) mutable {
+        Tensor dq, dk, dv;
+        if (q.requires_grad()) dq = Tensor({B, S, D}, 0.0f, false);
+        if (k.requires_grad()) dk = Tensor({B, S, D}, 0.0f, false);
+        if (v.requires_grad()) dv = Tensor({B, S, D}, 0.0f, false);
+        hip::check(ehip_attention_short_backward_f32(
+                       dptr(q), dptr(k), dptr(v), dptr(weights), dptr(g),
+                       q.requires_grad() ? dout(dq) : nullptr,
+                       k.requires_grad() ? dout(dk) : nullptr,
+                       v.requires_grad() ? dout(dv) : nullptr, int64_t(B), int64_t(S), int64_t(D),
+                       int64_t(H), int64_t(hd), scale, causal ? 1 : 0, nullptr),
+                   "attention backward");
+        // The product path's order of the three hand-overs.
+        if (v.requires_grad()) v.add_grad(dv);
+        if (q.requires_grad()) q.add_grad(dq);
+        if (k.requires_grad()) k.add_grad(dk);
+    };
+    return out;
+}
+
+}  // namespace
+
 bool attention_heads_supported(const Tensor& query, size_t heads, const Tensor* mask) {
     if (query.ndim() != 3 || heads == 0 || query.shape()[2] % heads != 0) return false;
     if (mask == nullptr) return true;
@@ -305,6 +348,10 @@ Tensor attention_heads(const Tensor& query, const Tensor& key, const Tensor& val
     // and stores 0 past it), and the products with the weights skip the zero
     // blocks above it.
     const bool causal = skippable_causal(mask, S);
+    if (nn::short_attention() && (mask == nullptr || causal) &&
+        ehip_attention_short_supported(int64_t(S), int64_t(hd)))
+        return attention_short(query, key, value, B, S, D, H, hd, scale, causal,
+                               attention_weights);
     Tensor scores({B, H, S, S}, 0.0f, false);
     ehip_gemm_ex_t d = head_product(false, true, B, H, S, S, hd, act(query), act(key),
                                     dout(scores), int64_t(S), hss, ss);

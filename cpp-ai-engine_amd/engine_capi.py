@@ -353,6 +353,11 @@ class Engine:
         returns the previous setting."""
         return bool(self.lib.eng_set_fused_nodes(int(bool(on))))
 
+    def set_short_attention(self, on):
+        """Attention of sequences and heads of at most 64 values in one launch per direction
+        (default on) or through the batched products; returns the previous setting."""
+        return bool(self.lib.eng_set_short_attention(int(bool(on))))
+
     def set_conv_implicit_gemm(self, on):
         """Wide convolutions as implicit GEMMs (default on) or the reference's im2col
         composition; returns the previous setting."""

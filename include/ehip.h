@@ -730,6 +730,32 @@ int ehip_softmax_backward_scaled_causal_f32(const float* y, const float* g, floa
                                             int64_t rows, int64_t cols, float scale,
                                             void* stream);
 
+/* Scaled dot-product attention of short sequences in one launch per direction
+ * (one workgroup per batch and head, everything in LDS): the reference's
+ * scaled_dot_product_attention under its multi-head split and merge
+ * (src/transformer.cpp:279-304, 320-349) -- weights = softmax(Q K^T * scale
+ * [+ causal mask]), out = weights V -- and its autograd backward, each sum in
+ * the reference CPU loops' order (ascending index from zero, zero A operands
+ * skipped; the softmax's denominator and the backward's row dot serial), so
+ * that only the device exp separates the values from the reference's. q, k,
+ * v, out, grad, dq, dk, dv are (batch, seq, width) activations holding head h
+ * at columns [h head_dim, (h + 1) head_dim); weights is (batch, heads, seq,
+ * seq). causal = 1 masks entries right of the diagonal, as nn::causal_mask's
+ * -1e9 addend does (those weights are 0; masked entries are not read or
+ * computed). The backward takes the forward's weights and writes (does not
+ * accumulate) each of dq, dk, dv that is not NULL. seq and head_dim at most 64
+ * (ehip_attention_short_supported says 1); others are refused with EHIP_EINVAL
+ * and take the batched products and softmax kernels above. */
+int ehip_attention_short_supported(int64_t seq, int64_t head_dim);
+int ehip_attention_short_f32(const float* q, const float* k, const float* v, float* weights,
+                             float* out, int64_t batch, int64_t seq, int64_t width, int64_t heads,
+                             int64_t head_dim, float scale, int causal, void* stream);
+int ehip_attention_short_backward_f32(const float* q, const float* k, const float* v,
+                                      const float* weights, const float* grad, float* dq,
+                                      float* dk, float* dv, int64_t batch, int64_t seq,
+                                      int64_t width, int64_t heads, int64_t head_dim, float scale,
+                                      int causal, void* stream);
+
 /* LayerNorm over the last axis (two-pass mean and variance, eps inside the
  * square root) saving xhat and inv_std, and its derivative; dgamma and dbeta
  * are summed over rows in a fixed order (deterministic, no atomics). Rows of

@@ -40,6 +40,40 @@ def lm_layout(vocab, d, ff, layers):
     return [(n, s) for n, s, _ in W.lm_param_layout(vocab, d, ff, layers)]
 
 
+def lm_case(dims, seed, xavier, param_shapes):
+    """The seeded inputs of a language-model trajectory: parameters (LayerNorm gamma 1 and
+    beta 0, biases 0, weights Xavier-uniform or normal with std 0.02 for the vocabulary
+    rows and sqrt(2 / fan_in) otherwise), then tokens and targets, all from one generator."""
+    vocab, d, heads, ff, layers, b, s = dims
+    r = np.random.default_rng(seed)
+    params = []
+    for shp in param_shapes:
+        size = int(np.prod(shp))
+        if len(shp) == 1:  # LayerNorm: gamma 1, beta 0, in that order per norm
+            params.append(np.ones(size, np.float32) if len(params) % 2 == 1 else
+                          np.zeros(size, np.float32))
+        elif shp[0] == 1:
+            params.append(np.zeros(size, np.float32))
+        elif xavier:
+            lim = np.sqrt(6.0 / (shp[0] + shp[1]))
+            params.append(r.uniform(-lim, lim, size).astype(np.float32))
+        else:
+            params.append((r.standard_normal(size) * (0.02 if shp[0] == vocab else
+                                                      np.sqrt(2.0 / shp[0]))).astype(np.float32))
+    ids = r.integers(0, vocab, (b, s)).astype(np.float32)
+    targets = r.integers(0, vocab, b * s)
+    return np.concatenate(params), ids, targets
+
+
+def loss_bounds(ref, ref_fma, floor=1e-5, factor=2.0):
+    """Per-step relative bound on a trajectory's losses: the floor, or FACTOR times how far
+    the reference's own FMA-contracted build (another valid fp32 rounding of the same
+    source) moved that step's loss, whichever is larger. Past a few Adam steps a training
+    trajectory amplifies rounding, so two correct engines drift apart by that much."""
+    ref, ref_fma = np.asarray(ref, np.float64), np.asarray(ref_fma, np.float64)
+    return np.maximum(floor, factor * np.abs(ref_fma - ref) / np.abs(ref))
+
+
 def vanishing(name):
     return name.endswith("attn.key.bias")
 

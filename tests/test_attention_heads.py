@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import _compose as K
-from _hip import backend, dev, exact, host, k_tol, print_case, ref_close
+from _hip import backend, dev, exact, host, k_tol, print_case, ref_close, ref_err
 from _oracle import oracle_or_skip
 
 pytestmark = pytest.mark.gpu
@@ -225,13 +225,16 @@ def test_mha_fused_equals_composed(eng, orc, b, s, d, heads, causal):
     x, dy = randn(r, b, s, d), randn(r, b, s, d)
     params = mha_params(r, d)
     mask = np.triu(np.full((s, s), -1e9, np.float32), 1) if causal else None
-    # Bias gradients from the separate column sums on both sides (see both_graphs).
+    # Bias gradients from the separate column sums on both sides (see both_graphs); the
+    # batched-product attention (the short path has its own test below).
     prev_db = eng.set_fused_bias_grad(False)
+    prev_short = eng.set_short_attention(False)
     try:
         fused = eng.mha_fwd_bwd(x, heads, params, dy, mask=mask, fuse=True, weights=True)
         comp = eng.mha_fwd_bwd(x, heads, params, dy, mask=mask, fuse=False, weights=True)
     finally:
         eng.set_fused_bias_grad(prev_db)
+        eng.set_short_attention(prev_short)
     for got, want, what in zip(fused, comp, ("y", "dx", "dparams", "weights")):
         exact(got, want, f"fused {what}")
     # And against the oracle composition (the reference's CPU arithmetic).
@@ -296,6 +299,7 @@ def both_graphs(eng, fn):
     from the dW products, another order, are tested against the separate sums elsewhere."""
     prev = eng.set_fused_nodes(True)
     prev_db = eng.set_fused_bias_grad(False)
+    prev_short = eng.set_short_attention(False)  # its own test: test_short_attention_node
     try:
         fused = fn()
         eng.set_fused_nodes(False)
@@ -303,6 +307,7 @@ def both_graphs(eng, fn):
     finally:
         eng.set_fused_nodes(prev)
         eng.set_fused_bias_grad(prev_db)
+        eng.set_short_attention(prev_short)
     return fused, comp
 
 
@@ -623,7 +628,66 @@ def test_mha_causal_mask_skipping_keeps_values(eng, b, s, d, heads):
     r = np.random.default_rng(b * 7 + s + d + heads)
     x, dy = randn(r, b, s, d), randn(r, b, s, d)
     params = mha_params(r, d)
-    tagged = eng.mha_causal_fwd_bwd(x, heads, params, dy, tagged=True)
-    plain = eng.mha_causal_fwd_bwd(x, heads, params, dy, tagged=False)
+    prev = eng.set_short_attention(False)  # the product path's skipping (short: its own test)
+    try:
+        tagged = eng.mha_causal_fwd_bwd(x, heads, params, dy, tagged=True)
+        plain = eng.mha_causal_fwd_bwd(x, heads, params, dy, tagged=False)
+    finally:
+        eng.set_short_attention(prev)
     for got, want, what in zip(tagged, plain, ("y", "dx", "dparams", "weights")):
         assert np.array_equal(got, want), f"{what}: {np.sum(got != want)} values differ"
+
+
+def unflatten_mha(params, d):
+    names = ("wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo")
+    shapes = [(d, d), (1, d)] * 4
+    p, off = {}, 0
+    for name, shp in zip(names, shapes):
+        n = int(np.prod(shp))
+        p[name] = params[off:off + n].reshape(shp)
+        off += n
+    return p, names, shapes
+
+
+@pytest.mark.parametrize("b,s,d,heads,causal", [(32, 64, 96, 4, True), (2, 64, 96, 4, False),
+                                                (3, 37, 48, 2, True), (4, 64, 256, 4, True)])
+def test_short_attention_node(eng, orc, b, s, d, heads, causal):
+    """The attention node with sequences and heads of at most 64 values takes one launch per
+    direction (nn::set_short_attention, the default; with nn::causal_mask's tagged mask or
+    none); the same node through the batched products is the bit-tested path above. Both
+    against the reference composition run by the oracle: the short path sums in the
+    reference's order, so it meets the reference's metric at 1e-5 where the products are
+    held to 4 k_tol; every parameter gradient too."""
+    print_case("short attention node", b, s, d, heads, causal)
+    r = np.random.default_rng(b * 11 + s + d + heads + causal)
+    x, dy = randn(r, b, s, d), randn(r, b, s, d)
+    params = mha_params(r, d)
+    mask = np.triu(np.full((s, s), -1e9, np.float32), 1) if causal else None
+
+    def run(short):
+        prev = eng.set_short_attention(short)
+        prev_db = eng.set_fused_bias_grad(False)
+        try:
+            if causal:
+                return eng.mha_causal_fwd_bwd(x, heads, params, dy, tagged=True)
+            return eng.mha_fwd_bwd(x, heads, params, dy, mask=None, fuse=True, weights=True)
+        finally:
+            eng.set_short_attention(prev)
+            eng.set_fused_bias_grad(prev_db)
+
+    short, prod = run(True), run(False)
+    p, names, shapes = unflatten_mha(params, d)
+    y, cache = K.mha_fwd(orc, x, p, heads, mask)
+    dx, grads = K.mha_bwd(orc, dy, cache)
+    for name, got_s, got_p, w in (("y", short[0], prod[0], y), ("dx", short[1], prod[1], dx)):
+        es, ep = ref_err(got_s, w), ref_err(got_p, w)
+        print(f"{name}: short {es:.2e}, products {ep:.2e}")
+        assert es <= k_tol(max(s, d)), (name, es)
+    off = 0
+    for name, shp in zip(names, shapes):
+        n = int(np.prod(shp))
+        es = ref_err(short[2][off:off + n].reshape(shp), grads[name])
+        assert es <= k_tol(b * s), (name, es)
+        off += n
+    w_ref = cache[3][3]
+    assert ref_err(short[3], w_ref) <= 1e-5
