@@ -262,9 +262,106 @@ int launch_kslice(GemmArgs g, int64_t batch, hipStream_t s) {
 //   K  32 x 32 per workgroup, K sliced over its waves: outputs too small for
 //      the larger tiles to fill the chip (512^3, the char-Transformer's layers)
 //   T   64 x  64 x 16, 4 waves of  32 x 32   the rest (few tiles; B column sums)
+//   P   16 x 16 per workgroup of 16 waves, each wave a sixteenth of K: A^T B
+//       products of few tiles over a long K (weight gradients of narrow
+//       layers), one load round trip per 128 k of a wave, no workspace
 // A tile size is taken when its grid fills the 256 CUs (with split-K where K
 // is long) and the padding it adds to the output stays small.
-enum class Tile { L, M, S, K, T };
+enum class Tile { L, M, S, K, T, P };
+
+// ------------------------------------------------------------ panel products
+//
+// C (m x n, few 16 x 16 tiles) = A^T B over a long K, A stored K x M and B
+// K x N (a weight gradient X^T dY). One workgroup of kPanelWaves waves per
+// output tile; wave w takes k in [w kw, (w + 1) kw) and issues the loads of
+// kPanelSteps MFMA steps (4 k each) at once: lane l reads A(k0 + l / 16,
+// m0 + l % 16) and B(k0 + l / 16, n0 + l % 16), sixteen consecutive floats
+// of a row per lane group, which are exactly the operands of
+// v_mfma_f32_16x16x4f32 (A: i = lane % 16, k = lane / 16; B: j = lane % 16,
+// k = lane / 16; D: j = lane % 16, i = 4 (lane / 16) + register). The waves'
+// tiles are then added in wave order through LDS, and the epilogue applied.
+// With a column sum (the bias gradient), each lane adds its B values in k
+// order, and the tile row 0 workgroups add lanes and waves in a fixed order.
+// The K-sliced 32 x 32 tiles pull the panels of 32 rows and columns through
+// as few CUs; the 16 x 16 tiles spread them over four times as many.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+constexpr int kPanelWaves = 4;
+constexpr int kPanelSteps = 32;
+
+template <bool CHECK, bool EPI>
+__global__ __launch_bounds__(64 * kPanelWaves) void gemm_tn_panel(GemmArgs g) {
+    constexpr int kSteps = CHECK ? kPanelSteps / 2 : kPanelSteps;
+    __shared__ float red[kPanelWaves][256];
+    __shared__ float cred[kPanelWaves][64];
+    const int tile = int(blockIdx.x);
+    const int64_t m0 = int64_t(tile / g.tiles_n) * 16, n0 = int64_t(tile % g.tiles_n) * 16;
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / 64);
+    const int lane = int(threadIdx.x) % 64;
+    const int li = lane % 16, lk = lane / 16;
+    const int64_t kb = int64_t(wave) * g.k_chunk;
+    const int64_t ke = kb + g.k_chunk < g.k ? kb + g.k_chunk : g.k;
+    const bool col_sums = g.colsum != nullptr && m0 == 0;
+    const bool row_in = !CHECK || m0 + li < g.m, col_in = !CHECK || n0 + li < g.n;
+    // Lane offsets within a step's four rows; the rows' bases are uniform.
+    const int32_t offa = int32_t(lk * g.lda + m0 + li), offb = int32_t(lk * g.ldb + n0 + li);
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float cs = 0.0f;
+    for (int64_t k0 = kb; k0 < ke; k0 += 4 * kSteps) {
+        float a[kSteps], b[kSteps];
+#pragma unroll
+        for (int u = 0; u < kSteps; ++u) {
+            const float* ra = g.a + (k0 + 4 * u) * g.lda;
+            const float* rb = g.b + (k0 + 4 * u) * g.ldb;
+            if (CHECK) {
+                const bool kin = k0 + 4 * u + lk < ke;
+                a[u] = kin && row_in ? ra[offa] : 0.0f;
+                b[u] = kin && col_in ? rb[offb] : 0.0f;
+            } else {
+                a[u] = ra[offa];
+                b[u] = rb[offb];
+            }
+        }
+        // Every load of the chunk issued before the first wait.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < kSteps; ++u)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+        if (col_sums) {
+#pragma unroll
+            for (int u = 0; u < kSteps; ++u) cs = cs + b[u];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][(4 * lk + r) * 16 + li] = acc[r];
+    cred[wave][lane] = cs;
+    __syncthreads();
+    for (int o = int(threadIdx.x); o < 256; o += 64 * kPanelWaves) {
+        const int i = o / 16, j = o % 16;
+        float v = red[0][o];
+#pragma unroll
+        for (int w = 1; w < kPanelWaves; ++w) v = v + red[w][o];
+        const int64_t row = m0 + i, col = n0 + j;
+        if (!CHECK || (row < g.m && col < g.n)) {
+            float* dst = g.c + row * g.ldc + col;
+            *dst = EPI ? epilogue(g, 0, row, col, v, dst) : v;
+        }
+    }
+    if (col_sums && threadIdx.x < 16) {
+        const int j = int(threadIdx.x);
+        float v = 0.0f;
+        for (int w = 0; w < kPanelWaves; ++w)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v = v + cred[w][16 * q + j];
+        if (n0 + j < g.n) g.colsum[n0 + j] = v;
+    }
+}
+
+// The panel product's k per wave: whole chunks of 4 kPanelSteps k (the
+// unchecked kernel loads them without guards), else a multiple of 4.
+int64_t panel_wave_k(int64_t k, bool whole) {
+    const int64_t q = whole ? 4 * kPanelSteps : 4;
+    return ceil_div(ceil_div(k, kPanelWaves), q) * q;
+}
 
 bool operands_aligned(const GemmArgs& g) {
     return aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
@@ -272,7 +369,7 @@ bool operands_aligned(const GemmArgs& g) {
            (g.inner == 1 || (g.stride_a2 % 4 == 0 && g.stride_b2 % 4 == 0));
 }
 
-Tile plan_tile(const GemmArgs& g, int64_t batch) {
+Tile plan_tile(const GemmArgs& g, int64_t batch, bool ta, bool tb) {
     const int64_t tl = ceil_div(g.m, 256) * ceil_div(g.n, 256) * batch;
     const int64_t tm = ceil_div(g.m, 128) * ceil_div(g.n, 128) * batch;
     const int64_t ts = ceil_div(g.m, 128) * ceil_div(g.n, 64) * batch;
@@ -280,9 +377,34 @@ Tile plan_tile(const GemmArgs& g, int64_t batch) {
     if (tl >= 256 && padding(g.m, g.n, 256, 256) < 0.15 && g.k >= 256) return Tile::L;
     if ((tm >= 128 || (tm >= 32 && long_k)) && padding(g.m, g.n, 128, 128) < 0.25) return Tile::M;
     if ((ts >= 128 || (ts >= 32 && long_k)) && padding(g.m, g.n, 128, 64) < 0.25) return Tile::S;
+    // Weight gradients of narrow layers: few output tiles, long K.
+    if (ta && !tb && batch == 1 && g.causal == 0 && g.k >= 1024 &&
+        ceil_div(g.m, 16) * ceil_div(g.n, 16) <= 1024)
+        return Tile::P;
     // A B column sum is computed only by the staged tiles.
     if (g.colsum == nullptr && ceil_div(g.m, 32) * ceil_div(g.n, 32) * batch >= 64) return Tile::K;
     return Tile::T;
+}
+
+int launch_panel(GemmArgs g, hipStream_t s) {
+    g.tiles_m = int(ceil_div(g.m, 16));
+    g.tiles_n = int(ceil_div(g.n, 16));
+    const bool whole = g.m % 16 == 0 && g.n % 16 == 0 && g.k % (4 * kPanelSteps) == 0 &&
+                       g.lda * g.k < (int64_t(1) << 31) && g.ldb * g.k < (int64_t(1) << 31);
+    g.k_chunk = panel_wave_k(g.k, whole);
+    g.splits = 1;
+    const unsigned tiles = unsigned(int64_t(g.tiles_m) * g.tiles_n);
+    const bool epi = !plain_epilogue(g);
+    const dim3 block(64 * kPanelWaves);
+    if (whole && !epi)
+        EHIP_LAUNCH("gemm", (gemm_tn_panel<false, false>), dim3(tiles), block, 0, s, g);
+    else if (whole)
+        EHIP_LAUNCH("gemm", (gemm_tn_panel<false, true>), dim3(tiles), block, 0, s, g);
+    else if (!epi)
+        EHIP_LAUNCH("gemm", (gemm_tn_panel<true, false>), dim3(tiles), block, 0, s, g);
+    else
+        EHIP_LAUNCH("gemm", (gemm_tn_panel<true, true>), dim3(tiles), block, 0, s, g);
+    return EHIP_OK;
 }
 
 template <bool TA, bool TB>
@@ -294,7 +416,7 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s, const Workspace& wsp) {
     const auto whole = [&](int bm, int bn, int bk) {
         return g.vec && g.m % bm == 0 && g.n % bn == 0 && g.k % bk == 0;
     };
-    switch (plan_tile(g, batch)) {
+    switch (plan_tile(g, batch, TA, TB)) {
         case Tile::L:
             return launch_cfg<256, 256, 16, 128, 64, TA, TB>(g, batch, !whole(256, 256, 16), s,
                                                              wsp);
@@ -304,6 +426,8 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s, const Workspace& wsp) {
             return launch_cfg<128, 64, 32, 32, 32, TA, TB>(g, batch, !whole(128, 64, 32), s, wsp);
         case Tile::K:
             return launch_kslice<TA, TB>(g, batch, s);
+        case Tile::P:
+            return launch_panel(g, s);
         default:
             return launch_cfg<64, 64, 16, 32, 32, TA, TB>(g, batch, !whole(64, 64, 16), s, wsp);
     }
@@ -315,7 +439,8 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s, const Workspace& wsp) {
 bool try_kslice_pair(GemmArgs g0, GemmArgs g1, hipStream_t s, int* rc) {
     g0.vec = operands_aligned(g0) ? 1 : 0;
     g1.vec = operands_aligned(g1) ? 1 : 0;
-    if (plan_tile(g0, 1) != Tile::K || plan_tile(g1, 1) != Tile::K) return false;
+    if (plan_tile(g0, 1, false, true) != Tile::K || plan_tile(g1, 1, true, false) != Tile::K)
+        return false;
     // Each product is sliced as its own launch would slice it (same bits).
     const int64_t t0 = ceil_div(g0.m, 32) * ceil_div(g0.n, 32);
     const int64_t t1 = ceil_div(g1.m, 32) * ceil_div(g1.n, 32);
@@ -551,7 +676,7 @@ bool bias_from_dw(int64_t rows, int64_t in, int64_t out) {
     g.m = in;
     g.n = out;
     g.k = rows;
-    return plan_tile(g, 1) != Tile::K;
+    return plan_tile(g, 1, true, false) != Tile::K;
 }
 
 // Validation shared by both entry points, then the kernel choice.
@@ -644,6 +769,8 @@ const OccupancyKernel kGemmKernels[] = {
      reinterpret_cast<const void*>(&gemm_kernel<64, 64, 16, 32, 32, false, false, true, false>), 256},
     {"gemm_kslice 32x32, 8 waves (NN)",
      reinterpret_cast<const void*>(&gemm_kslice<8, false, false, false, false>), 512},
+    {"gemm_tn_panel 16x16 (TN: narrow dW)",
+     reinterpret_cast<const void*>(&gemm_tn_panel<false, false>), 64 * kPanelWaves},
     {"gemm_small_thread (NN)", reinterpret_cast<const void*>(&gemm_small_thread<false, false>), 256},
     {"gemm_splitk_reduce", reinterpret_cast<const void*>(&splitk_reduce), 256},
 };

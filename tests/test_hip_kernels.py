@@ -84,6 +84,11 @@ TILE_CASES = [
     # workgroup, whole and ragged tiles, a batch of attention-sized products.
     ("K-sliced 512^3 W=8", 1, 512, 512, 512), ("K-sliced W=2", 1, 2048, 96, 96),
     ("K-sliced ragged", 1, 1000, 300, 200), ("K-sliced batched K=24", 128, 64, 24, 64),
+    # A^T B over a long K into few 16 x 16 tiles, one workgroup of 16 waves per tile
+    # (gemm_tn_panel; the TA mode takes it, the others the tiles above): whole, ragged
+    # (checked loads, K not a multiple of 128), and a K long enough for 32 chunks a wave.
+    ("P 96x96 K=2048", 1, 96, 2048, 96), ("P 96x384", 1, 96, 2048, 384),
+    ("P ragged", 1, 100, 1500, 37), ("P K=65536", 1, 64, 65536, 64),
 ]
 
 
