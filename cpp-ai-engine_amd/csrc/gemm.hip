@@ -290,6 +290,9 @@ constexpr int kPanelSteps = 32;
 
 template <bool CHECK, bool EPI>
 __global__ __launch_bounds__(64 * kPanelWaves) void gemm_tn_panel(GemmArgs g) {
+    // The checked form takes half the steps per round trip: its rows are often
+    // unaligned (a 121-float row's 64-byte segments straddle cache lines), and
+    // more loads in flight then only add line traffic (17.0 against 14.2 us).
     constexpr int kSteps = CHECK ? kPanelSteps / 2 : kPanelSteps;
     __shared__ float red[kPanelWaves][256];
     __shared__ float cred[kPanelWaves][64];

@@ -325,6 +325,10 @@ __global__ __launch_bounds__(kThreads) void select_rows_kernel(const float* __re
 }
 
 // CSR scatter-add: every destination element sums its sources in list order.
+// kScatterBatch positions are read at a time, then their source rows, then added
+// in order: two load round trips per batch instead of two per source row.
+constexpr int kScatterBatch = 8;
+
 __global__ __launch_bounds__(kThreads) void scatter_add_rows_kernel(
     const float* __restrict__ g, const int32_t* __restrict__ row_ptr,
     const int32_t* __restrict__ pos, float* __restrict__ dx, int64_t row_size, int64_t n_src,
@@ -332,10 +336,21 @@ __global__ __launch_bounds__(kThreads) void scatter_add_rows_kernel(
     const int64_t step = int64_t(gridDim.x) * kThreads;
     for (int64_t e = int64_t(blockIdx.x) * kThreads + threadIdx.x; e < n; e += step) {
         const int64_t r = e / row_size, j = e % row_size;
+        const int32_t p0 = row_ptr[r], p1 = row_ptr[r + 1];
         float acc = 0.0f;
-        for (int32_t p = row_ptr[r]; p < row_ptr[r + 1]; ++p) {
-            const int64_t src = pos[p];
-            acc += (src >= 0 && src < n_src) ? g[src * row_size + j] : NAN;
+        for (int32_t p = p0; p < p1; p += kScatterBatch) {
+            int64_t src[kScatterBatch];
+#pragma unroll
+            for (int u = 0; u < kScatterBatch; ++u) src[u] = p + u < p1 ? pos[p + u] : 0;
+            float v[kScatterBatch];
+#pragma unroll
+            for (int u = 0; u < kScatterBatch; ++u)
+                v[u] = p + u >= p1 ? 0.0f
+                       : (src[u] >= 0 && src[u] < n_src) ? g[src[u] * row_size + j]
+                                                         : NAN;
+#pragma unroll
+            for (int u = 0; u < kScatterBatch; ++u)
+                if (p + u < p1) acc += v[u];
         }
         dx[e] = accumulate ? dx[e] + acc : acc;
     }

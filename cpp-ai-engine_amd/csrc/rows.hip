@@ -793,7 +793,7 @@ template <int V, bool VEC4, int AHEAD>
 __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
     const float* __restrict__ dy, const float* __restrict__ xhat, const float* __restrict__ gamma,
     const float* __restrict__ inv_std, float* __restrict__ dx, float* __restrict__ partial,
-    int64_t rows, int64_t cols) {
+    int64_t rows, int64_t cols, int accumulate) {
     using F = Frag<64, V, VEC4, true>;
     __shared__ float tree[kLnWaves / 2][V][64];
     const float inv_d = 1.0f / static_cast<float>(cols);
@@ -810,7 +810,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
     }
     const int64_t step = groups * kLnWaves;
     for (int64_t r0 = group + groups * wave; r0 < rows; r0 += step * AHEAD) {
-        F fd[AHEAD], fh[AHEAD];
+        F fd[AHEAD], fh[AHEAD], fx[AHEAD];
         float iv[AHEAD];
 #pragma unroll
         for (int a = 0; a < AHEAD; ++a) {
@@ -819,6 +819,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
             if (r < rows) {
                 fd[a].load(dy + r * cols, int(cols), lane, 0.0f);
                 fh[a].load(xhat + r * cols, int(cols), lane, 0.0f);
+                if (accumulate) fx[a].load(dx + r * cols, int(cols), lane, 0.0f);
                 iv[a] = inv_std[r];
             }
         }
@@ -842,6 +843,12 @@ __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
                 fo.v[t] = iv[a] * (dxh - inv_d * s1 - fh[a].v[t] * inv_d * s2);
                 dg[t] = dg[t] + fd[a].v[t] * fh[a].v[t];
                 db[t] = db[t] + fd[a].v[t];
+            }
+            // Accumulating: the gradient already held plus this one, one add
+            // (the bits of a separate accumulate pass).
+            if (accumulate) {
+#pragma unroll
+                for (int t = 0; t < V; ++t) fo.v[t] = fx[a].v[t] + fo.v[t];
             }
             fo.store(dx + r * cols, int(cols), lane);
         }
@@ -1023,30 +1030,32 @@ int64_t ln_wide_groups(int64_t rows, int64_t cols) {
 template <int V, bool VEC>
 int launch_ln_wide_v(bool ahead, const float* dy, const float* xhat, const float* gamma,
                      const float* inv_std, float* dx, float* partial, int64_t groups,
-                     int64_t rows, int64_t cols, hipStream_t s) {
+                     int64_t rows, int64_t cols, int accumulate, hipStream_t s) {
     if constexpr (V <= (VEC ? 16 : 8)) {
         if (ahead) {
             EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 4>),
                         dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma, inv_std,
-                        dx, partial, rows, cols);
+                        dx, partial, rows, cols, accumulate);
             return EHIP_OK;
         }
     }
     EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 1>),
                 dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma, inv_std, dx,
-                partial, rows, cols);
+                partial, rows, cols, accumulate);
     return EHIP_OK;
 }
 
-// Launches the large-problem row kernel for `groups` groups.
+// Launches the large-problem row kernel for `groups` groups (dx = or, with
+// accumulate, dx += the rows' input gradient).
 int launch_ln_wide(const float* dy, const float* xhat, const float* gamma, const float* inv_std,
                    float* dx, float* partial, int64_t groups, int64_t rows, int64_t cols,
-                   hipStream_t s) {
+                   hipStream_t s, int accumulate = 0) {
     const bool vec = cols >= 256 && rows_vec_ok(cols, {dy, xhat, gamma, dx});
     // Four rows ahead below the last-level cache size, one beyond it (2^25 elements).
     const bool ahead = rows * cols < (int64_t(1) << 25);
 #define EHIP_LNW(V, VEC) \
-    return launch_ln_wide_v<V, VEC>(ahead, dy, xhat, gamma, inv_std, dx, partial, groups, rows, cols, s)
+    return launch_ln_wide_v<V, VEC>(ahead, dy, xhat, gamma, inv_std, dx, partial, groups, rows, \
+                                    cols, accumulate, s)
     if (vec) {
         if (cols <= 256) EHIP_LNW(4, true);
         if (cols <= 512) EHIP_LNW(8, true);
@@ -1376,7 +1385,7 @@ int64_t ehip_layernorm_backward_partials(int64_t rows, int64_t cols, int64_t* gr
 int ehip_layernorm_backward_partials_f32(const float* dy, const float* xhat, const float* gamma,
                                          const float* inv_std, float* dx, float* partials,
                                          int64_t groups, int64_t rows, int64_t cols,
-                                         void* stream) {
+                                         int accumulate, void* stream) {
     EHIP_READY();
     if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "layernorm_backward_partials: bad shape");
     if (!dy || !xhat || !gamma || !inv_std || !dx || !partials)
@@ -1387,7 +1396,7 @@ int ehip_layernorm_backward_partials_f32(const float* dy, const float* xhat, con
                     "layernorm_backward_partials: %lld groups for %lld x %lld (expected %lld)",
                     (long long)groups, (long long)rows, (long long)cols, (long long)want);
     return launch_ln_wide(dy, xhat, gamma, inv_std, dx, partials, groups, rows, cols,
-                          as_stream(stream));
+                          as_stream(stream), accumulate ? 1 : 0);
 }
 
 }  // extern "C"

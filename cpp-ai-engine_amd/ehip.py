@@ -166,7 +166,7 @@ _SIGS = {
     "ehip_layernorm_backward_f32": [_vp] * 7 + [_i64, _i64, _vp],
     "ehip_layernorm_backward_partials": [_i64, _i64, C.POINTER(_i64)],
     "ehip_linear_bias_from_dw": [_i],
-    "ehip_layernorm_backward_partials_f32": [_vp] * 6 + [_i64, _i64, _i64, _vp],
+    "ehip_layernorm_backward_partials_f32": [_vp] * 6 + [_i64, _i64, _i64, _i, _vp],
     "ehip_cross_entropy_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _vp],
     "ehip_cross_entropy_backward_f32": [_vp, _vp, _vp, _i64, _i64, _vp, _vp],
     "ehip_cross_entropy_fused_supported": [_i64, _i64],
@@ -662,21 +662,24 @@ class Backend:
                                                      self.stream()), "layernorm_backward")
         return dx, dg, db
 
-    def layernorm_backward_partials(self, dy, xhat, gamma, inv, groups=None):
+    def layernorm_backward_partials(self, dy, xhat, gamma, inv, groups=None, dx=None):
         """dx and the per-group dgamma / dbeta partials ([groups][d][2]) of the deferred
         LayerNorm backward; returns (dx, partials, groups), or None when the shape is summed
-        in one call only. `groups` overrides the count (to test the refusal)."""
+        in one call only. `groups` overrides the count (to test the refusal); a given `dx`
+        receives dx + the input gradient (accumulate)."""
         d = dy.shape[-1]
         rows = dy.numel() // d
         g = _i64(0)
         n = self.lib.ehip_layernorm_backward_partials(rows, d, C.byref(g))
         if n == 0 and groups is None:
             return None
-        dx, part = self.f32(dy.shape), self.f32((max(n, 1),))
+        acc = dx is not None
+        dx = dx if acc else self.f32(dy.shape)
+        part = self.f32((max(n, 1),))
         use = g.value if groups is None else groups
         self.ok(self.lib.ehip_layernorm_backward_partials_f32(
             self.p(dy), self.p(xhat), self.p(gamma), self.p(inv), self.p(dx), self.p(part), use,
-            rows, d, self.stream()), "layernorm_backward_partials")
+            rows, d, int(acc), self.stream()), "layernorm_backward_partials")
         return dx, part, g.value
 
     def cross_entropy(self, logits, targets):

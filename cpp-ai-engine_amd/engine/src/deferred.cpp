@@ -80,5 +80,14 @@ bool grad_adoptable(const Tensor& target) {
     return impl->requires_grad && (!impl->grad || impl->grad->storage.pending_zero());
 }
 
+float* grad_in_place(const Tensor& target) {
+    const auto& impl = target.get_impl();
+    if (!impl->requires_grad || !impl->grad) return nullptr;
+    Storage& acc = impl->grad->storage;
+    if (acc.pending_zero() || !acc.exclusive() || acc.size() != target.size()) return nullptr;
+    if (deferred_pending() && deferred_writes(acc)) flush_deferred();
+    return acc.device_mut();
+}
+
 }  // namespace detail
 }  // namespace engine

@@ -115,6 +115,11 @@ void take_deferred(std::vector<ehip_conv_reduce_t>& jobs, DeferredKeep& keep);
 // True when add_grad of a fresh, unshared gradient buffer into `target` adopts
 // that buffer (no gradient yet, or a pending zero).
 bool grad_adoptable(const Tensor& target);
+// The device buffer of `target`'s gradient when add_grad of a gradient into it
+// would add in place (a gradient is held, not a pending zero, and not shared),
+// after finishing any queued sum that writes it; else nullptr. A kernel that
+// adds its result into this buffer replaces the add_grad call.
+float* grad_in_place(const Tensor& target);
 
 // A tensor viewing `src` with a new shape (no copy).
 inline Tensor view_with_shape(const Storage& src, const std::vector<size_t>& shape, bool req) {

@@ -58,14 +58,19 @@ Tensor LayerNorm::forward(const Tensor& input) {
                 : 0;
         if (nparts > 0) {
             Tensor part({size_t(nparts)}, 0.0f, false);
+            // The input's gradient already held (the residual branch's) takes dx
+            // added in the row kernel itself: the add_grad below, folded in.
+            float* acc_dx =
+                input_copy.requires_grad() ? detail::grad_in_place(input_copy) : nullptr;
             hip::check(ehip_layernorm_backward_partials_f32(
-                           dptr(g), dptr(xhat), dptr(gamma_copy), dptr(inv_std), dout(dX),
-                           dout(part), groups, int64_t(rows), int64_t(D), nullptr),
+                           dptr(g), dptr(xhat), dptr(gamma_copy), dptr(inv_std),
+                           acc_dx ? acc_dx : dout(dX), dout(part), groups, int64_t(rows),
+                           int64_t(D), acc_dx ? 1 : 0, nullptr),
                        "layernorm backward");
             const ehip_conv_reduce_t job{dptr(part), groups, int64_t(D), 1, dout(dgamma),
                                          dout(dbeta)};
             detail::defer_conv_reduce(job, part);
-            if (input_copy.requires_grad()) input_copy.add_grad(dX);
+            if (input_copy.requires_grad() && acc_dx == nullptr) input_copy.add_grad(dX);
             gamma_copy.add_grad(dgamma);
             beta_copy.add_grad(dbeta);
             detail::defer_conv_output(gamma_copy, dgamma);

@@ -80,3 +80,36 @@ def test_attention_short_refusals(hip):
     with pytest.raises(RuntimeError, match="exceed"):
         hip.attention_short(x, x, x, 1, 1.0, True)
     assert hip.launched() == before
+
+
+def test_attention_short_nonfinite_operands(hip, orc):
+    """The reference skips zero A terms (src/tensor_ops.cpp:553-560), which matters only
+    when the other operand is not finite: a key whose score underflows exp (weight exactly
+    0) facing a V row of +inf leaves the output finite in the reference, where a plain
+    multiply-add would make it NaN. The kernels take the exact path when an operand of a
+    product is not finite; the backward, whose dP row meets inf * 0, is NaN where the
+    reference's is and equal elsewhere."""
+    print_case("attention short non-finite")
+    r = np.random.default_rng(77)
+    b, s, heads, hd = 2, 16, 2, 8
+    w = heads * hd
+    q, k, v, g = (r.standard_normal((b, s, w), dtype=np.float32) for _ in range(4))
+    q[:, :, :hd] = 1.0 + np.abs(q[:, :, :hd])   # head 0: every query positive ...
+    k[:, 3, :hd] = -50.0                        # ... so key 3's scores underflow exp
+    v[:, 3, :hd] = np.inf
+    scale = 1.0 / math.sqrt(hd)
+    out_ref, cache = K.attention_fwd(orc, split(q, heads), split(k, heads), split(v, heads), None)
+    dq_ref, dk_ref, dv_ref = K.attention_bwd(orc, split(g, heads), cache)
+    assert np.all(cache[3][:, 0, :, 3] == 0.0) and np.all(np.isfinite(out_ref))
+    Q, Kd, V, G = dev(q), dev(k), dev(v), dev(g)
+    weights, out = hip.attention_short(Q, Kd, V, heads, np.float32(scale), False)
+    dq, dk, dv = hip.attention_short_backward(Q, Kd, V, weights, G, heads, np.float32(scale),
+                                              False)
+    assert ref_err(host(weights), cache[3]) <= 1e-5
+    assert np.all(np.isfinite(host(out))) and ref_err(host(out), merge(out_ref)) <= 1e-5
+    for name, got, want in (("dq", host(dq), merge(dq_ref)), ("dk", host(dk), merge(dk_ref)),
+                            ("dv", host(dv), merge(dv_ref))):
+        assert np.array_equal(np.isnan(got), np.isnan(want)), name
+        assert np.array_equal(np.isinf(got), np.isinf(want)), name
+        fin = np.isfinite(want)
+        assert ref_err(got[fin], want[fin]) <= 1e-5, name
