@@ -94,7 +94,7 @@ def run_variant(suffix, args, params, ids, targets):
         import subprocess
         subprocess.run([sys.executable, os.path.abspath(__file__), "--steps", str(args.steps),
                         "--threads", str(args.threads), "--work", args.work,
-                        "--variant", suffix or "release"], check=True)
+                        "--variant", "fma" if suffix else "release"], check=True)
     with np.load(cache, allow_pickle=False) as z:
         return z["losses"], z["final"], z["g0"], float(z["wall"])
 
