@@ -372,6 +372,15 @@ bool operands_aligned(const GemmArgs& g) {
            (g.inner == 1 || (g.stride_a2 % 4 == 0 && g.stride_b2 % 4 == 0));
 }
 
+// Per operand: bit 0 when A's rows are 16-byte aligned, bit 1 for B's.
+int operand_alignment(const GemmArgs& g) {
+    const bool a = aligned16(g.a) && g.lda % 4 == 0 && g.stride_a % 4 == 0 &&
+                   (g.inner == 1 || g.stride_a2 % 4 == 0);
+    const bool b = aligned16(g.b) && g.ldb % 4 == 0 && g.stride_b % 4 == 0 &&
+                   (g.inner == 1 || g.stride_b2 % 4 == 0);
+    return (a ? 1 : 0) | (b ? 2 : 0);
+}
+
 Tile plan_tile(const GemmArgs& g, int64_t batch, bool ta, bool tb) {
     const int64_t tl = ceil_div(g.m, 256) * ceil_div(g.n, 256) * batch;
     const int64_t tm = ceil_div(g.m, 128) * ceil_div(g.n, 128) * batch;
@@ -416,6 +425,7 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s, const Workspace& wsp) {
     // the checked ones still load whole float4s away from the edges when the
     // rows are aligned.
     g.vec = operands_aligned(g) ? 1 : 0;
+    g.vec_ab = operand_alignment(g);
     const auto whole = [&](int bm, int bn, int bk) {
         return g.vec && g.m % bm == 0 && g.n % bn == 0 && g.k % bk == 0;
     };
@@ -442,6 +452,8 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s, const Workspace& wsp) {
 bool try_kslice_pair(GemmArgs g0, GemmArgs g1, hipStream_t s, int* rc) {
     g0.vec = operands_aligned(g0) ? 1 : 0;
     g1.vec = operands_aligned(g1) ? 1 : 0;
+    g0.vec_ab = operand_alignment(g0);
+    g1.vec_ab = operand_alignment(g1);
     if (plan_tile(g0, 1, false, true) != Tile::K || plan_tile(g1, 1, true, false) != Tile::K)
         return false;
     // Each product is sliced as its own launch would slice it (same bits).

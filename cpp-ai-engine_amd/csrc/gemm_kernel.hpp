@@ -40,6 +40,7 @@ struct GemmArgs {
     int splits;        // K is cut into `splits` chunks of k_chunk (a multiple of BK)
     int64_t k_chunk;
     int vec;           // rows 16-byte aligned: checked loads may use float4 inside the edges
+    int vec_ab;        // the same per operand: bit 0 A's rows, bit 1 B's (K-sliced checked loads)
     int causal;        // ehip_gemm_ex_t::causal: 0, or the skipping mode 1 to 4
     // The product index of grid z = 0: batches beyond the grid's 65535 z
     // extent run as several launches of consecutive product ranges.
@@ -666,8 +667,10 @@ __device__ __forceinline__ void kslice_tile(const GemmArgs& g, int bid, int64_t 
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
                 const int64_t k = kb + 8 * u + 4 * h;
-                fa[u] = load_kblock<!TA, CHECK>(A, g.lda, g.m, k_end, m0 + r, k, g.vec != 0);
-                fb[u] = load_kblock<TB, CHECK>(B, g.ldb, g.n, k_end, n0 + r, k, g.vec != 0);
+                fa[u] = load_kblock<!TA, CHECK>(A, g.lda, g.m, k_end, m0 + r, k,
+                                                (g.vec_ab & 1) != 0);
+                fb[u] = load_kblock<TB, CHECK>(B, g.ldb, g.n, k_end, n0 + r, k,
+                                               (g.vec_ab & 2) != 0);
             }
         };
         // Two register buffers alternate: a stage's loads are issued before the
