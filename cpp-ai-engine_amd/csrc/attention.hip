@@ -262,7 +262,10 @@ __global__ __launch_bounds__(kFwdThreads) void attention_short_forward(
 }
 
 // dv = weights^T g; dP = g v^T; dS = (weights (dP - rowdot(dP, weights))) * scale;
-// dq = dS k; dk = dS^T q (each of dq, dk, dv may be null). One workgroup per (batch, head).
+// dq = dS k; dk = dS^T q (each of dq, dk, dv may be null). Two workgroups per
+// (batch, head): blockIdx.x = 2 (batch * heads + head) + role; role 0 forms dv
+// and dq, role 1 dk, and both form dP and dS (the same values), so the longest
+// chain is three products instead of four over twice the workgroups.
 template <bool VEC>
 __global__ __launch_bounds__(kBwdThreads) void attention_short_backward(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
@@ -271,7 +274,14 @@ __global__ __launch_bounds__(kBwdThreads) void attention_short_backward(
     __shared__ float sq[kAttnMax][kAttnPitch], sk[kAttnMax][kAttnPitch], sv[kAttnMax][kAttnPitch];
     __shared__ float sg[kAttnMax][kAttnPitch], sp[kAttnMax][kAttnPitch], sd[kAttnMax][kAttnPitch];
     __shared__ float sdot[kAttnMax];
-    const int64_t bh = blockIdx.x, b = bh / a.heads, h = bh % a.heads;
+    if (blockIdx.x & 1) {
+        dq = nullptr;
+        dv = nullptr;
+    } else {
+        dk = nullptr;
+    }
+    if (dq == nullptr && dk == nullptr && dv == nullptr) return;
+    const int64_t bh = blockIdx.x / 2, b = bh / a.heads, h = bh % a.heads;
     const int S = int(a.seq), hd = int(a.head_dim);
     const bool causal = a.causal != 0;
     const bool want_qk = dq != nullptr || dk != nullptr;
@@ -422,14 +432,17 @@ int ehip_attention_short_backward_f32(const float* q, const float* k, const floa
     const bool vec = head_dim % 4 == 0 && width % 4 == 0 && (!q || aligned16(q)) &&
                      (!k || aligned16(k)) && (!v || aligned16(v)) && aligned16(grad);
     const AttnShape a{batch, seq, width, heads, head_dim, scale, causal ? 1 : 0};
+    if (2 * batch * heads > 0x7fffffffLL)
+        return fail(EHIP_EINVAL, "attention_short_backward: too many heads");
+    const dim3 grid(unsigned(2 * batch * heads));
     if (vec)
-        EHIP_LAUNCH("attention_short_backward", attention_short_backward<true>,
-                    dim3(unsigned(batch * heads)), dim3(kBwdThreads), 0, as_stream(stream), q, k,
-                    v, weights, grad, dq, dk, dv, a);
+        EHIP_LAUNCH("attention_short_backward", attention_short_backward<true>, grid,
+                    dim3(kBwdThreads), 0, as_stream(stream), q, k, v, weights, grad, dq, dk, dv,
+                    a);
     else
-        EHIP_LAUNCH("attention_short_backward", attention_short_backward<false>,
-                    dim3(unsigned(batch * heads)), dim3(kBwdThreads), 0, as_stream(stream), q, k,
-                    v, weights, grad, dq, dk, dv, a);
+        EHIP_LAUNCH("attention_short_backward", attention_short_backward<false>, grid,
+                    dim3(kBwdThreads), 0, as_stream(stream), q, k, v, weights, grad, dq, dk, dv,
+                    a);
     return EHIP_OK;
 }
 
