@@ -725,6 +725,40 @@ def compact(line):
     return out
 
 
+def step_kernels(db_path, top=40):
+    """Per-step kernel table from a rocprofv3 rocpd database (for the kernel profiles): the
+    trace is cut into steps after each Adam launch (`adam_multi*`), steps that initialise
+    state (ten or more fills) are dropped with five more at each end, and each kernel's
+    launches and execution time are averaged per step."""
+    import collections
+    import re
+    import sqlite3
+    rows = sqlite3.connect(db_path).execute(
+        "select name, duration, grid_x, grid_y, grid_z from kernels order by start").fetchall()
+    steps, cur = [], []
+    for r in rows:
+        cur.append(r)
+        if "adam_multi" in r[0]:
+            steps.append(cur)
+            cur = []
+    sel = [s for s in steps if sum("Fill" in k[0] for k in s) < 10][5:-5]
+    if not sel:
+        print("no steps found")
+        return
+    agg = collections.defaultdict(lambda: [0, 0.0, None])
+    for st in sel:
+        for k in st:
+            n = re.sub(r"ehip::|\(anonymous namespace\)::|gemm_detail::", "", k[0])[:80]
+            agg[n][0] += 1
+            agg[n][1] += k[1]
+            agg[n][2] = k[2:5]
+    ns = len(sel)
+    print(f"steps {ns} launches {sum(v[0] for v in agg.values()) / ns:.1f} "
+          f"kernel {sum(v[1] for v in agg.values()) / ns / 1e3:.1f} us")
+    for n, (c, t, grid) in sorted(agg.items(), key=lambda x: -x[1][1])[:top]:
+        print(f"  {c / ns:5.1f} x {t / c / 1e3:7.2f} us = {t / ns / 1e3:6.1f} us  {grid} {n}")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -745,7 +779,15 @@ def main():
     ap.add_argument("--transformer-only", action="store_true",
                     help="the cfg 5 step and its dominant kernel only (no CPU baseline, no "
                          "other configurations): the kernel profile's command")
+    ap.add_argument("--step-kernels", default=None, metavar="DB",
+                    help="print the per-step kernel table of a rocprofv3 rocpd database (no GPU)")
+    ap.add_argument("--charlm-only", action="store_true",
+                    help="the cfg 3 char-Transformer leg only (no CPU baseline), printed as "
+                         "JSON: the cfg 3 kernel profile's command")
     args = ap.parse_args()
+    if args.step_kernels:
+        step_kernels(args.step_kernels)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -764,6 +806,10 @@ def main():
 
     if args.kernel_only:
         kernel_only(eng, hip, timer, torch)
+        return
+    if args.charlm_only:
+        log("bench: cfg3 char-Transformer training step")
+        print(json.dumps(charlm_leg(engine_capi, eng, timer, 0.0)), flush=True)
         return
 
     log("bench: cfg5 Transformer training step")
