@@ -721,6 +721,8 @@ int gemm_run(const ehip_gemm_ex_t& d, hipStream_t s, const Workspace& wsp = Work
     g.add_period = d.addend ? d.addend_period : 1;
     g.beta = d.beta;
     g.relu = d.relu;
+    g.res = d.residual;
+    g.ld_res = d.ld_residual;
     const int64_t batch = d.batch;
     const bool ta = d.trans_a != 0, tb = d.trans_b != 0;
     // K = 0 (only reached from the extended entry point): acc = 0, then the
@@ -766,6 +768,8 @@ int check_desc(const ehip_gemm_ex_t& d) {
     if (d.colsum_b && (d.batch != 1 || d.trans_b))
         return fail(EHIP_EINVAL, "gemm: column sums need batch 1 and a K x N B");
     if (d.causal < 0 || d.causal > 4) return fail(EHIP_EINVAL, "gemm: causal mode %d", d.causal);
+    if (d.residual && (d.batch != 1 || d.ld_residual < d.n))
+        return fail(EHIP_EINVAL, "gemm: a residual needs batch 1 and ld_residual >= n");
     if (d.m > (int64_t(1) << 31) || d.n > (int64_t(1) << 31))
         return fail(EHIP_EINVAL, "gemm: extent beyond 2^31");
     return EHIP_OK;

@@ -30,6 +30,10 @@ struct GemmArgs {
     int64_t ld_add, stride_add, add_period;
     int add_row;  // the addend is one value per row: add[i] (a convolution's bias)
     float beta;
+    // v += res[i * ld_res + j] (res != null, batch 1): a residual stream added
+    // after the product's own epilogue, as the add node after a Linear does.
+    const float* res;
+    int64_t ld_res;
     int relu;  // then v = max(0, v)
     // colsum[j] = sum over k of op(B)[k][j] (batch 1), made by the first
     // tile-row's workgroups from the B tiles they stage anyway; with split K
@@ -57,10 +61,12 @@ __device__ __forceinline__ int64_t batch_offset(int64_t z, int64_t inner, int64_
 
 // The epilogue's arithmetic on one value: each step rounded on its own, so
 // that a fused scale, mask, bias or ReLU equals the separate nodes bit for bit.
-__device__ __forceinline__ float finish(const GemmArgs& g, float v, float add, float old) {
+__device__ __forceinline__ float finish(const GemmArgs& g, float v, float add, float old,
+                                        float res) {
     if (g.alpha != 1.0f) v = v * g.alpha;
     if (g.add != nullptr) v = v + add;
     if (g.beta != 0.0f) v = v + g.beta * old;
+    if (g.res != nullptr) v = v + res;
     if (g.relu) v = (0.0f < v) ? v : 0.0f;
     return v;
 }
@@ -71,12 +77,13 @@ __device__ __forceinline__ float epilogue(const GemmArgs& g, int64_t z, int64_t 
     const float add = g.add ? g.add[(z % g.add_period) * g.stride_add +
                                     (g.add_row ? row : row * g.ld_add + col)]
                             : 0.0f;
-    return finish(g, v, add, g.beta != 0.0f ? *dst : 0.0f);
+    const float res = g.res ? g.res[row * g.ld_res + col] : 0.0f;
+    return finish(g, v, add, g.beta != 0.0f ? *dst : 0.0f, res);
 }
 
 // True when the stored value is the accumulator itself.
 __host__ __device__ inline bool plain_epilogue(const GemmArgs& g) {
-    return g.alpha == 1.0f && g.add == nullptr && g.beta == 0.0f && !g.relu;
+    return g.alpha == 1.0f && g.add == nullptr && g.beta == 0.0f && !g.relu && g.res == nullptr;
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
@@ -227,19 +234,21 @@ __device__ __forceinline__ void store_acc(const GemmArgs& g, floatx16 (&acc)[C::
             const int64_t col = n0 + wn0 + 32 * j + lane % 32;
             float* cb = Cp + row0 * ldc + col;
             const float* ab = addp ? addp + row0 * ld_add + (g.add_row ? 0 : col) : nullptr;
-            float e_add[16], e_old[16];
+            const float* rb = g.res ? g.res + row0 * g.ld_res + col : nullptr;
+            float e_add[16], e_old[16], e_res[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int dr = 8 * (r / 4) + (r % 4);
                 const bool in = !CHECK || (row0 + dr < g.m && col < g.n);
                 e_add[r] = (ab && in) ? ab[dr * ld_add] : 0.0f;
                 e_old[r] = (g.beta != 0.0f && in) ? cb[dr * ldc] : 0.0f;
+                e_res[r] = (rb && in) ? rb[dr * g.ld_res] : 0.0f;
             }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int dr = 8 * (r / 4) + (r % 4);
                 if (CHECK && (row0 + dr >= g.m || col >= g.n)) continue;
-                cb[dr * ldc] = finish(g, acc[i][j][r], e_add[r], e_old[r]);
+                cb[dr * ldc] = finish(g, acc[i][j][r], e_add[r], e_old[r], e_res[r]);
             }
         }
 }
@@ -725,7 +734,7 @@ __device__ __forceinline__ void kslice_tile(const GemmArgs& g, int bid, int64_t 
     float* Cp = g.c + batch_offset(batch, g.inner, g.stride_c, g.stride_c2);
     const float* addp = g.add ? g.add + (int64_t(batch) % g.add_period) * g.stride_add : nullptr;
     const int64_t col = n0 + r;
-    float e_add[kPer], e_old[kPer];
+    float e_add[kPer], e_old[kPer], e_res[kPer];
     if (EPI) {
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
@@ -734,6 +743,7 @@ __device__ __forceinline__ void kslice_tile(const GemmArgs& g, int bid, int64_t 
             const bool in = !CHECK || (row < g.m && col < g.n);
             e_add[q] = (addp && in) ? addp[row * g.ld_add + col] : 0.0f;
             e_old[q] = (g.beta != 0.0f && in) ? Cp[row * g.ldc + col] : 0.0f;
+            e_res[q] = (g.res && in) ? g.res[row * g.ld_res + col] : 0.0f;
         }
     }
 #pragma unroll
@@ -741,7 +751,7 @@ __device__ __forceinline__ void kslice_tile(const GemmArgs& g, int bid, int64_t 
         const int i = wave * kPer + q;
         const int64_t row = m0 + 8 * (i / 4) + 4 * h + (i % 4);
         if (CHECK && (row >= g.m || col >= g.n)) continue;
-        Cp[row * g.ldc + col] = EPI ? finish(g, out[q], e_add[q], e_old[q]) : out[q];
+        Cp[row * g.ldc + col] = EPI ? finish(g, out[q], e_add[q], e_old[q], e_res[q]) : out[q];
     }
 }
 

@@ -67,7 +67,8 @@ class ConvReduce(C.Structure):
 
 
 class GemmEx(C.Structure):
-    """ehip_gemm_ex_t: two-level batch strides and the alpha / addend / beta epilogue."""
+    """ehip_gemm_ex_t: two-level batch strides and the alpha / addend / beta / residual
+    epilogue."""
     _fields_ = [("trans_a", C.c_int), ("trans_b", C.c_int), ("batch", C.c_int64),
                 ("inner", C.c_int64), ("m", C.c_int64), ("n", C.c_int64), ("k", C.c_int64),
                 ("a", C.c_void_p), ("lda", C.c_int64), ("stride_a", C.c_int64),
@@ -76,7 +77,8 @@ class GemmEx(C.Structure):
                 ("ldc", C.c_int64), ("stride_c", C.c_int64), ("stride_c_inner", C.c_int64),
                 ("alpha", C.c_float), ("addend", C.c_void_p), ("ld_addend", C.c_int64),
                 ("stride_addend", C.c_int64), ("addend_period", C.c_int64), ("beta", C.c_float),
-                ("relu", C.c_int), ("colsum_b", C.c_void_p), ("causal", C.c_int)]
+                ("relu", C.c_int), ("colsum_b", C.c_void_p), ("causal", C.c_int),
+                ("residual", C.c_void_p), ("ld_residual", C.c_int64)]
 
 
 # name -> argtypes (all return int unless listed in _RESTYPES)

@@ -139,15 +139,20 @@ Tensor matmul_nt(const Tensor& a, const Tensor& b);
 // x (rows, in) . w (in, out) + bias as one node: the broadcast bias add runs
 // in the product's epilogue. Equal bit for bit to x.matmul(w) + bias (the
 // reference's Linear::forward, src/nn.cpp:119-122). bias is (out) or
-// (1, out), or null for no bias.
-Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias);
+// (1, out), or null for no bias. With a residual (any shape of rows * out
+// elements), the node is residual + (x w + bias) under the residual's shape,
+// the add in the same epilogue: equal bit for bit to
+// residual + linear(x, w, bias).reshape(residual.shape()).
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias,
+              const Tensor* residual = nullptr);
 
 // relu(x w1 + b1) w2 + b2 as one node (TransformerBlock's feed-forward,
 // src/transformer.cpp:409-414): the biases and the ReLU in the products'
 // epilogues, only the ReLU output kept (its backward reads the mask from
-// it). Equal bit for bit to the composed nodes. x is 2-D.
+// it). Equal bit for bit to the composed nodes. x is 2-D. A residual is
+// added as in linear().
 Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2,
-                         const Tensor& b2);
+                         const Tensor& b2, const Tensor* residual = nullptr);
 
 }  // namespace ops
 

@@ -79,6 +79,9 @@ public:
     MultiHeadAttention(size_t d_model, size_t num_heads);
     Tensor forward(const Tensor& input) override;
     Tensor forward(const Tensor& input, const Tensor* mask);
+    // residual + forward(input, mask), the add folded into the output
+    // projection on the fused path; residual is (batch, seq, d_model).
+    Tensor forward(const Tensor& input, const Tensor* mask, const Tensor* residual);
     std::vector<Tensor> parameters() override;
     std::vector<std::pair<std::string, Tensor>> named_parameters(
         const std::string& prefix = "") override;

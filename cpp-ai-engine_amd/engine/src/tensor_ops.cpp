@@ -315,9 +315,11 @@ Tensor matmul_nt(const Tensor& A, const Tensor& B) {
 
 namespace {
 
-// out (m, n) = op(a) op(b) over plain 2-D operands, then + bias (a row) and ReLU.
+// out (m, n) = op(a) op(b) over plain 2-D operands, then + bias (a row),
+// + residual (an (m, n) array) and ReLU, each rounded on its own.
 void gemm_2d(bool ta, bool tb, size_t m, size_t n, size_t k, const float* a, const float* b,
-             float* c, const float* bias, bool relu, const char* what) {
+             float* c, const float* bias, bool relu, const char* what,
+             const float* residual = nullptr) {
     ehip_gemm_ex_t d{};
     d.trans_a = ta ? 1 : 0;
     d.trans_b = tb ? 1 : 0;
@@ -336,6 +338,8 @@ void gemm_2d(bool ta, bool tb, size_t m, size_t n, size_t k, const float* a, con
     d.addend = bias;
     d.addend_period = 1;  // ld_addend 0: one row over every row
     d.relu = relu ? 1 : 0;
+    d.residual = residual;
+    d.ld_residual = int64_t(n);
     hip::check(ehip_gemm_ex_f32(&d, nullptr), what);
 }
 
@@ -346,6 +350,15 @@ bool row_bias(const Tensor* bias, size_t n) {
 
 Tensor empty_2d(size_t rows, size_t cols) { return Tensor({rows, cols}, 0.0f, false); }
 
+// A residual added in a product's epilogue: any shape holding the (m, n)
+// result's elements in row-major order; the node's output takes its shape.
+void check_residual(const Tensor* residual, size_t m, size_t n, const char* what) {
+    if (residual != nullptr && residual->size() != m * n)
+        throw std::invalid_argument(std::string(what) + ": residual " + residual->shape_str() +
+                                    " does not hold the (" + std::to_string(m) + ", " +
+                                    std::to_string(n) + ") result.");
+}
+
 // Multiply-adds of g w^T above which Linear's backward no longer runs as one
 // launch (csrc/gemm.hip's thread-per-output limit), so that adding dx into
 // x's gradient in place saves a pass instead of splitting a launch in two.
@@ -353,23 +366,31 @@ constexpr double kInPlaceWork = double(1 << 21);
 
 }  // namespace
 
-Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias) {
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias, const Tensor* residual) {
     if (x.ndim() != 2 || w.ndim() != 2 || x.shape()[1] != w.shape()[0] ||
         !row_bias(bias, w.shape()[1])) {
         Tensor out = x.matmul(w);
-        return bias ? out + *bias : out;
+        if (bias) out = out + *bias;
+        return residual ? *residual + out.reshape(residual->shape()) : out;
     }
     const size_t M = x.shape()[0], K = x.shape()[1], N = w.shape()[1];
-    Tensor out = empty_2d(M, N);
+    check_residual(residual, M, N, "linear");
+    Tensor out = residual ? Tensor(residual->shape(), 0.0f, false) : empty_2d(M, N);
     if (M > 0 && N > 0)
         gemm_2d(false, false, M, N, K, dptr(x), dptr(w), dout(out), bias ? dptr(*bias) : nullptr,
-                false, "linear");
+                false, "linear", residual ? dptr(*residual) : nullptr);
     const bool bias_grad = bias != nullptr && bias->requires_grad();
-    if (!track(x.requires_grad() || w.requires_grad() || bias_grad)) return out;
-    Tensor xc = x, wc = w, bc = bias ? *bias : Tensor();
+    const bool res_grad = residual != nullptr && residual->requires_grad();
+    if (!track(x.requires_grad() || w.requires_grad() || bias_grad || res_grad)) return out;
+    Tensor xc = x, wc = w, bc = bias ? *bias : Tensor(), rc = residual ? *residual : Tensor();
     std::vector<std::shared_ptr<TensorImpl>> parents = {x.get_impl(), w.get_impl()};
     if (bias) parents.push_back(bias->get_impl());
-    attach(out, std::move(parents), [xc, wc, bc, M, N, K](const Tensor& g) mutable {
+    if (residual) parents.push_back(residual->get_impl());
+    attach(out, std::move(parents), [xc, wc, bc, rc, M, N, K](const Tensor& g) mutable {
+        // The residual add's node comes last in the composed graph, so its
+        // gradient goes first; the product reads g itself instead of the copy
+        // the add's backward would hand it.
+        if (rc.get_impl() && rc.requires_grad()) rc.add_grad(g);
         const bool want_db = bc.get_impl() && bc.requires_grad();
         if (M > 0 && K > 0 && N > 0) {
             // The same three results as the composed graph's add and product
@@ -419,30 +440,37 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias) {
 }
 
 Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2,
-                         const Tensor& b2) {
+                         const Tensor& b2, const Tensor* residual) {
     const bool plain = x.ndim() == 2 && w1.ndim() == 2 && w2.ndim() == 2 &&
                        x.shape()[1] == w1.shape()[0] && w1.shape()[1] == w2.shape()[0] &&
                        row_bias(&b1, w1.shape()[1]) && row_bias(&b2, w2.shape()[1]);
-    if (!plain) return linear(linear(x, w1, &b1).relu(), w2, &b2);
+    if (!plain) return linear(linear(x, w1, &b1).relu(), w2, &b2, residual);
     const size_t M = x.shape()[0], D = x.shape()[1], F = w1.shape()[1], N = w2.shape()[1];
+    check_residual(residual, M, N, "feed-forward");
     Tensor h = empty_2d(M, F);  // relu(x w1 + b1)
     if (M > 0 && F > 0)
         gemm_2d(false, false, M, F, D, dptr(x), dptr(w1), dout(h), dptr(b1), true,
                 "feed-forward 1");
-    Tensor out = empty_2d(M, N);
+    Tensor out = residual ? Tensor(residual->shape(), 0.0f, false) : empty_2d(M, N);
     if (M > 0 && N > 0)
         gemm_2d(false, false, M, N, F, dptr(h), dptr(w2), dout(out), dptr(b2), false,
-                "feed-forward 2");
+                "feed-forward 2", residual ? dptr(*residual) : nullptr);
+    const bool res_grad = residual != nullptr && residual->requires_grad();
     if (!track(x.requires_grad() || w1.requires_grad() || b1.requires_grad() ||
-               w2.requires_grad() || b2.requires_grad()))
+               w2.requires_grad() || b2.requires_grad() || res_grad))
         return out;
-    Tensor xc = x, w1c = w1, b1c = b1, w2c = w2, b2c = b2;
-    attach(out, {x.get_impl(), w1.get_impl(), b1.get_impl(), w2.get_impl(), b2.get_impl()},
-           [xc, w1c, b1c, w2c, b2c, h, M, D, F, N](const Tensor& g) mutable {
-               // The composed graph's order: second bias, second product (h,
-               // then w2), ReLU, first bias, first product (x, then w1). A bias
-               // and its weight both trained take one ehip_linear_backward_f32
-               // call (db from the dW product where that pays, as in Linear).
+    Tensor xc = x, w1c = w1, b1c = b1, w2c = w2, b2c = b2, rc = residual ? *residual : Tensor();
+    std::vector<std::shared_ptr<TensorImpl>> parents = {x.get_impl(), w1.get_impl(), b1.get_impl(),
+                                                        w2.get_impl(), b2.get_impl()};
+    if (residual) parents.push_back(residual->get_impl());
+    attach(out, std::move(parents),
+           [xc, w1c, b1c, w2c, b2c, rc, h, M, D, F, N](const Tensor& g) mutable {
+               // The composed graph's order: the residual add, second bias,
+               // second product (h, then w2), ReLU, first bias, first product
+               // (x, then w1). A bias and its weight both trained take one
+               // ehip_linear_backward_f32 call (db from the dW product where
+               // that pays, as in Linear).
+               if (rc.get_impl() && rc.requires_grad()) rc.add_grad(g);
                Tensor dw2;
                if (b2c.requires_grad() && w2c.requires_grad() && F > 0 && N > 0) {
                    dw2 = empty_2d(F, N);

@@ -459,6 +459,11 @@ MultiHeadAttention::MultiHeadAttention(size_t d_model, size_t num_heads)
 Tensor MultiHeadAttention::forward(const Tensor& input) { return forward(input, nullptr); }
 
 Tensor MultiHeadAttention::forward(const Tensor& input, const Tensor* mask) {
+    return forward(input, mask, nullptr);
+}
+
+Tensor MultiHeadAttention::forward(const Tensor& input, const Tensor* mask,
+                                   const Tensor* residual) {
     if (input.ndim() != 3 || input.shape()[2] != d_model_)
         throw std::invalid_argument("MultiHeadAttention expects (batch, seq, " +
                                     std::to_string(d_model_) + "), received " + input.shape_str() + ".");
@@ -472,7 +477,11 @@ Tensor MultiHeadAttention::forward(const Tensor& input, const Tensor* mask) {
         Tensor attended = attention_heads(project(w_query_), project(w_key_), project(w_value_),
                                           num_heads_, mask,
                                           keep_attention_ ? &last_attention_ : nullptr);
-        return w_out_(attended);
+        if (residual == nullptr) return w_out_(attended);
+        if (residual->shape() != input.shape()) return *residual + w_out_(attended);
+        // residual + attended w_out + b_out, the add in the product's epilogue.
+        return ops::linear(attended.reshape({batch * seq, d_model_}), w_out_.weight(),
+                           w_out_.has_bias() ? &w_out_.bias() : nullptr, residual);
     }
     auto split_heads = [&](const Tensor& projected) {
         return projected.reshape({batch, seq, num_heads_, head_dim_}).permute({0, 2, 1, 3});
@@ -483,7 +492,7 @@ Tensor MultiHeadAttention::forward(const Tensor& input, const Tensor* mask) {
     Tensor attended =
         scaled_dot_product_attention(q, k, v, mask, keep_attention_ ? &last_attention_ : nullptr);
     Tensor merged = attended.permute({0, 2, 1, 3}).reshape({batch, seq, d_model_});
-    return w_out_(merged);
+    return residual ? *residual + w_out_(merged) : w_out_(merged);
 }
 
 std::vector<Tensor> MultiHeadAttention::parameters() {
@@ -523,17 +532,16 @@ TransformerBlock::TransformerBlock(size_t d_model, size_t num_heads, size_t ff_h
 Tensor TransformerBlock::forward(const Tensor& input) { return forward(input, nullptr); }
 
 // Pre-LN: h = x + MHA(LN1(x)); out = h + FF2(ReLU(FF1(LN2(h)))) (src/transformer.cpp:409-414).
+// With fused nodes both residual adds run in the epilogues of the products
+// that end their branches (the output projection, the second feed-forward
+// layer).
 Tensor TransformerBlock::forward(const Tensor& input, const Tensor* mask) {
-    Tensor h = input + attention_.forward(norm1_(input), mask);
+    Tensor h = attention_.forward(norm1_(input), mask, &input);
     Tensor n2 = norm2_(h);
     if (fused_nodes() && ff1_.has_bias() && ff2_.has_bias()) {
-        const std::vector<size_t> shape = n2.shape();
-        const size_t rows = n2.size() / shape.back();
-        Tensor ff = ops::feed_forward_relu(n2.reshape({rows, shape.back()}), ff1_.weight(),
-                                           ff1_.bias(), ff2_.weight(), ff2_.bias());
-        std::vector<size_t> out_shape = shape;
-        out_shape.back() = ff.shape().back();
-        return h + ff.reshape(out_shape);
+        const size_t cols = n2.shape().back();
+        return ops::feed_forward_relu(n2.reshape({n2.size() / cols, cols}), ff1_.weight(),
+                                      ff1_.bias(), ff2_.weight(), ff2_.bias(), &h);
     }
     return h + ff2_(ff1_(n2).relu());
 }

@@ -261,8 +261,11 @@ int ehip_gemm_f32_noalloc(int trans_a, int trans_b, int64_t batch, int64_t m, in
  * each step rounded to fp32 on its own -- the separate `scores * scale` and
  * `scores + mask` nodes of src/transformer.cpp:285-291, bit for bit; an
  * addend with ld_addend 0 is Linear's broadcast bias add (src/nn.cpp:119-122).
- * Then, when relu != 0, c = (0 < c) ? c : 0, std::max(0.0f, c) of
- * Tensor::relu (src/tensor_ops.cpp:591-600).
+ * Then, with residual != NULL (batch 1), c = c + residual[i * ld_residual + j]:
+ * the residual add that follows a block's output projection or feed-forward
+ * (src/transformer.cpp:409-414; the add commutes, so the same bits). Then,
+ * when relu != 0, c = (0 < c) ? c : 0, std::max(0.0f, c) of Tensor::relu
+ * (src/tensor_ops.cpp:591-600).
  * colsum_b, when not NULL (batch 1, trans_b 0), receives the n column sums
  * of B over its k rows -- for dW = X^T dY the bias gradient sum_rows(dY) of
  * Linear's broadcast add (src/tensor_ops.cpp:81-102 through fold_leading,
@@ -309,6 +312,8 @@ typedef struct {
     int relu;
     float* colsum_b;
     int causal;
+    const float* residual;  /* batch 1: v += residual[i * ld_residual + j], after beta C */
+    int64_t ld_residual;
 } ehip_gemm_ex_t;
 
 int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream);

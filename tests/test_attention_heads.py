@@ -58,12 +58,13 @@ def merged_of(t, b, s, h, hd):
 
 
 def desc(hip, ta, tb, batch, inner, m, n, k, a, lda, sa, sa2, b, ldb, sb, sb2, c, ldc, sc, sc2,
-         alpha=1.0, addend=None, ld_add=0, stride_add=0, period=1, beta=0.0, relu=False):
+         alpha=1.0, addend=None, ld_add=0, stride_add=0, period=1, beta=0.0, relu=False,
+         residual=None, ld_res=0):
     from ehip import GemmEx
     return GemmEx(int(ta), int(tb), batch, inner, m, n, k, hip.p(a), lda, sa, sa2, hip.p(b), ldb,
                   sb, sb2, hip.p(c), ldc, sc, sc2, alpha,
                   None if addend is None else hip.p(addend), ld_add, stride_add, period, beta,
-                  int(relu))
+                  int(relu), None, 0, None if residual is None else hip.p(residual), ld_res)
 
 
 # (batch, seq, heads, head_dim): the char model's heads (cfg3), a head_dim that
@@ -279,6 +280,43 @@ def test_bias_relu_epilogue(hip, m, k, n):
     hip.gemm_ex(desc(hip, False, False, 1, 1, m, n, k, a, k, 0, 0, b, n, 0, 0, y, n, 0, 0,
                      addend=bias, ld_add=0, relu=True))
     exact(host(y), host(hip.relu(pre)), "bias + relu")
+
+
+@pytest.mark.parametrize("m,k,n", [(2048, 384, 96), (2048, 96, 96), (300, 1024, 257),
+                                   (64, 8, 10), (2048, 4096, 1024), (8192, 4096, 1024)])
+def test_residual_epilogue(hip, m, k, n):
+    """The residual add of a Transformer block's branch in the product's epilogue: after
+    the bias and beta C, before ReLU, each rounded on its own, so equal bit for bit to the
+    separate adds; a residual with its own row stride is read through it."""
+    print_case("gemm_ex residual", m, k, n)
+    r = np.random.default_rng(m + k + n + 1)
+    a, b = dev(randn(r, m, k)), dev(randn(r, k, n))
+    bias = dev(randn(r, 1, n))
+    wide = dev(randn(r, m, n + 3))
+    res = wide[:, 1:n + 1].contiguous()
+    c0 = dev(randn(r, m, n))
+    pre = hip.gemm(a, b) + bias
+    y = hip.f32((m, n))
+    hip.gemm_ex(desc(hip, False, False, 1, 1, m, n, k, a, k, 0, 0, b, n, 0, 0, y, n, 0, 0,
+                     addend=bias, ld_add=0, residual=res, ld_res=n))
+    exact(host(y), host(res + pre), "bias + residual")
+    y.copy_(c0)
+    hip.gemm_ex(desc(hip, False, False, 1, 1, m, n, k, a, k, 0, 0, b, n, 0, 0, y, n, 0, 0,
+                     addend=bias, ld_add=0, beta=1.0, relu=True, residual=wide.view(-1)[1:],
+                     ld_res=n + 3))
+    exact(host(y), host(hip.relu(pre + c0 + res)), "bias + beta C + strided residual, ReLU")
+
+
+def test_residual_refusals(hip):
+    """A residual row stride shorter than a row, or a residual on a batched product, is
+    refused before any launch."""
+    print_case("gemm_ex residual refusals")
+    x = dev(np.zeros(64, np.float32))
+    for batch, ld in ((1, 3), (2, 4)):
+        dsc = desc(hip, False, False, batch, 1, 4, 4, 4, x, 4, 0, 0, x, 4, 0, 0, x, 4, 16, 0,
+                   residual=x, ld_res=ld)
+        with pytest.raises(RuntimeError):
+            hip.gemm_ex(dsc)
 
 
 def test_relu_epilogue_signs(hip):
