@@ -466,6 +466,11 @@ def bandwidth_legs(hip, eng, timer, torch, r, rows, d, sum_rows, ff, srows, scol
         sec = med("layernorm_backward_rows", [x, xh, gam, inv, dx, part], (rows, d, groups.value))
         bl[f"layernorm_backward {rows}x{d} (engine: sums deferred)"] = roofline(
             "layernorm_backward_rows", "hbm", 12 * n + 4 * rows + 4 * d, sec)
+        if d <= 1024:  # dx added into the residual stream's gradient (reads it too)
+            sec = med("layernorm_backward_rows_acc", [x, xh, gam, inv, dx, part],
+                      (rows, d, groups.value))
+            bl[f"layernorm_backward {rows}x{d} (engine: accumulating dx)"] = roofline(
+                "layernorm_backward_rows", "hbm", 16 * n + 4 * rows + 4 * d, sec)
         del part
     del x, y, xh, inv, dx
     torch.cuda.empty_cache()

@@ -789,11 +789,14 @@ __device__ __forceinline__ void combine_waves(float (&acc)[V], float (*tree)[V][
 // 8192 x 1024 (cfg5): four rows ahead with nontemporal accesses 16.6 us against
 // 19.0 us for the previous one-row prefetch; at 2^28 elements one row at a time
 // is faster (545 against 564 us).
-template <int V, bool VEC4, int AHEAD>
+//
+// ACC: dx += the rows' gradient (the held gradient read with the row), a
+// template parameter so that the plain form holds no registers for it.
+template <int V, bool VEC4, int AHEAD, bool ACC>
 __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
     const float* __restrict__ dy, const float* __restrict__ xhat, const float* __restrict__ gamma,
     const float* __restrict__ inv_std, float* __restrict__ dx, float* __restrict__ partial,
-    int64_t rows, int64_t cols, int accumulate) {
+    int64_t rows, int64_t cols) {
     using F = Frag<64, V, VEC4, true>;
     __shared__ float tree[kLnWaves / 2][V][64];
     const float inv_d = 1.0f / static_cast<float>(cols);
@@ -810,7 +813,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
     }
     const int64_t step = groups * kLnWaves;
     for (int64_t r0 = group + groups * wave; r0 < rows; r0 += step * AHEAD) {
-        F fd[AHEAD], fh[AHEAD], fx[AHEAD];
+        F fd[AHEAD], fh[AHEAD], fx[ACC ? AHEAD : 1];
         float iv[AHEAD];
 #pragma unroll
         for (int a = 0; a < AHEAD; ++a) {
@@ -819,7 +822,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
             if (r < rows) {
                 fd[a].load(dy + r * cols, int(cols), lane, 0.0f);
                 fh[a].load(xhat + r * cols, int(cols), lane, 0.0f);
-                if (accumulate) fx[a].load(dx + r * cols, int(cols), lane, 0.0f);
+                if constexpr (ACC) fx[a].load(dx + r * cols, int(cols), lane, 0.0f);
                 iv[a] = inv_std[r];
             }
         }
@@ -836,17 +839,18 @@ __global__ __launch_bounds__(64 * kLnWaves) void layernorm_rows_backward_wide(
             }
             s1 = wave_sum(s1);
             s2 = wave_sum(s2);
-            F fo;
+            // dx overwrites dy's registers once dgamma and dbeta have read them.
+            F& fo = fd[a];
 #pragma unroll
             for (int t = 0; t < V; ++t) {
-                const float dxh = fd[a].v[t] * gm[t];
-                fo.v[t] = iv[a] * (dxh - inv_d * s1 - fh[a].v[t] * inv_d * s2);
-                dg[t] = dg[t] + fd[a].v[t] * fh[a].v[t];
-                db[t] = db[t] + fd[a].v[t];
+                const float g = fd[a].v[t];
+                dg[t] = dg[t] + g * fh[a].v[t];
+                db[t] = db[t] + g;
+                fo.v[t] = iv[a] * (g * gm[t] - inv_d * s1 - fh[a].v[t] * inv_d * s2);
             }
             // Accumulating: the gradient already held plus this one, one add
             // (the bits of a separate accumulate pass).
-            if (accumulate) {
+            if constexpr (ACC) {
 #pragma unroll
                 for (int t = 0; t < V; ++t) fo.v[t] = fx[a].v[t] + fo.v[t];
             }
@@ -1031,17 +1035,33 @@ template <int V, bool VEC>
 int launch_ln_wide_v(bool ahead, const float* dy, const float* xhat, const float* gamma,
                      const float* inv_std, float* dx, float* partial, int64_t groups,
                      int64_t rows, int64_t cols, int accumulate, hipStream_t s) {
+#define EHIP_LN_WIDE(AHEAD, ACC)                                                                   \
+    EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, AHEAD, ACC>),          \
+                dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma, inv_std, dx,   \
+                partial, rows, cols)
     if constexpr (V <= (VEC ? 16 : 8)) {
         if (ahead) {
-            EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 4>),
-                        dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma, inv_std,
-                        dx, partial, rows, cols, accumulate);
+            // Accumulating holds a third row per row in flight: two ahead at
+            // 1024 columns, where four would spill.
+            if (!accumulate)
+                EHIP_LN_WIDE(4, false);
+            else if constexpr (V >= 16)
+                EHIP_LN_WIDE(2, true);
+            else
+                EHIP_LN_WIDE(4, true);
             return EHIP_OK;
         }
     }
-    EHIP_LAUNCH("layernorm_backward", (layernorm_rows_backward_wide<V, VEC, 1>),
-                dim3(unsigned(groups)), dim3(64 * kLnWaves), 0, s, dy, xhat, gamma, inv_std, dx,
-                partial, rows, cols, accumulate);
+    // Accumulating rows of 2048 columns would spill even one row at a time:
+    // the entry point refuses them, so that form is never compiled.
+    if constexpr (V < 32) {
+        if (accumulate) {
+            EHIP_LN_WIDE(1, true);
+            return EHIP_OK;
+        }
+    }
+    EHIP_LN_WIDE(1, false);
+#undef EHIP_LN_WIDE
     return EHIP_OK;
 }
 
@@ -1081,7 +1101,7 @@ const OccupancyKernel kRowKernels[] = {
      reinterpret_cast<const void*>(&xent_rows_backward_fused<1024, 32, true, true>), 1024},
     {"layernorm_rows, rows of 1024", reinterpret_cast<const void*>(&layernorm_rows<64, 16, true, false>), 256},
     {"layernorm_rows_backward_wide, rows of 1024, 4 ahead",
-     reinterpret_cast<const void*>(&layernorm_rows_backward_wide<16, true, 4>), 64 * kLnWaves},
+     reinterpret_cast<const void*>(&layernorm_rows_backward_wide<16, true, 4, false>), 64 * kLnWaves},
     {"softmax_rows_loop", reinterpret_cast<const void*>(&softmax_rows_loop), kLoopThreads},
 };
 const OccupancyEntries kRowKernelsReg(kRowKernels);
@@ -1390,6 +1410,10 @@ int ehip_layernorm_backward_partials_f32(const float* dy, const float* xhat, con
     if (rows < 0 || cols <= 0) return fail(EHIP_EINVAL, "layernorm_backward_partials: bad shape");
     if (!dy || !xhat || !gamma || !inv_std || !dx || !partials)
         return fail(EHIP_EINVAL, "layernorm_backward_partials: null pointer");
+    if (accumulate && cols > 1024)
+        return fail(EHIP_EINVAL,
+                    "layernorm_backward_partials: accumulating rows of %lld columns (at most 1024)",
+                    (long long)cols);
     const int64_t want = ln_wide_groups(rows, cols);
     if (want == 0 || groups != want)
         return fail(EHIP_EINVAL,

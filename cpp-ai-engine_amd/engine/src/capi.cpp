@@ -785,9 +785,10 @@ int eng_repeat_bandwidth(int op, void* const* p, const int64_t* n, float f, cons
                         break;
                 case 6: rc = ehip_maxpool_backward_f32(static_cast<const int32_t*>(p[0]), F(1),
                                                        F(2), w, stream); break;
-                case 7: rc = ehip_layernorm_backward_partials_f32(F(0), F(1), F(2), F(3), F(4),
-                                                                  F(5), n[2], n[0], n[1], 0,
-                                                                  stream);
+                case 7:
+                case 8: rc = ehip_layernorm_backward_partials_f32(F(0), F(1), F(2), F(3), F(4),
+                                                                  F(5), n[2], n[0], n[1],
+                                                                  op == 8 ? 1 : 0, stream);
                         break;
                 default: throw std::invalid_argument("repeat_bandwidth: unknown op");
             }

@@ -59,9 +59,11 @@ Tensor LayerNorm::forward(const Tensor& input) {
         if (nparts > 0) {
             Tensor part({size_t(nparts)}, 0.0f, false);
             // The input's gradient already held (the residual branch's) takes dx
-            // added in the row kernel itself: the add_grad below, folded in.
-            float* acc_dx =
-                input_copy.requires_grad() ? detail::grad_in_place(input_copy) : nullptr;
+            // added in the row kernel itself: the add_grad below, folded in (rows
+            // of at most 1024 columns, the kernel's accumulating form).
+            float* acc_dx = input_copy.requires_grad() && D <= 1024
+                                ? detail::grad_in_place(input_copy)
+                                : nullptr;
             hip::check(ehip_layernorm_backward_partials_f32(
                            dptr(g), dptr(xhat), dptr(gamma_copy), dptr(inv_std),
                            acc_dx ? acc_dx : dout(dX), dout(part), groups, int64_t(rows),

@@ -94,7 +94,7 @@ class Engine:
 
     BANDWIDTH_OPS = {"layernorm": 0, "layernorm_backward": 1, "sum_axis": 2, "softmax": 3,
                      "softmax_backward": 4, "maxpool": 5, "maxpool_backward": 6,
-                     "layernorm_backward_rows": 7}
+                     "layernorm_backward_rows": 7, "layernorm_backward_rows_acc": 8}
 
     def repeat_bandwidth(self, reps, op, tensors, extents=(), f=0.0, window=None):
         """Enqueues `reps` calls of a bandwidth-bound ehip entry point from C++ on torch's

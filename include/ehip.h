@@ -787,9 +787,10 @@ int ehip_layernorm_backward_f32(const float* dy, const float* xhat, const float*
  * dbias = dbeta} of ehip_conv_weight_reduce_f32 or ehip_adam_multi_reduce_f32
  * then forms dgamma and dbeta with the same bits as
  * ehip_layernorm_backward_f32. Refuses a group count other than the one
- * returned. With accumulate != 0, dx receives dx + (the input gradient), one
- * add per element: the bits of writing it and then accumulating it into dx
- * with ehip_accumulate_grad_f32, in one pass. The backward of the reference's
+ * returned. With accumulate != 0 (rows of at most 1024 columns; wider ones are
+ * refused), dx receives dx + (the input gradient), one add per element: the
+ * bits of writing it and then accumulating it into dx with
+ * ehip_accumulate_grad_f32, in one pass. The backward of the reference's
  * LayerNorm node (src/transformer.cpp:123-150) with the parameter folds
  * deferred, and its add_grad into the input's gradient (src/tensor.cpp:168-203). */
 int64_t ehip_layernorm_backward_partials(int64_t rows, int64_t cols, int64_t* groups);

@@ -996,12 +996,19 @@ def test_layernorm_backward_partials_match_one_call(hip, orc, rows, d):
     ref_close(host(dg).reshape(d), wdg, k_tol(rows), "dgamma")
     ref_close(host(db), wdb, k_tol(rows), "dbeta")
     # Accumulating into a gradient already held: old + dx in one add per element (the
-    # bits of the separate accumulate pass), and the same partials.
+    # bits of the separate accumulate pass), and the same partials; rows wider than 1024
+    # columns are refused.
     old = randn(r, rows, d)
     acc = dev(old)
-    _, part2, _ = hip.layernorm_backward_partials(dev(dy), dev(xh), dev(gamma), dev(inv), dx=acc)
-    exact(host(acc), old + host(dx), "dx accumulated")
-    exact(host(part2), host(part), "partials while accumulating")
+    if d > 1024:
+        with pytest.raises(RuntimeError, match="at most 1024"):
+            hip.layernorm_backward_partials(dev(dy), dev(xh), dev(gamma), dev(inv), dx=acc)
+        exact(host(acc), old, "refused call leaves dx")
+    else:
+        _, part2, _ = hip.layernorm_backward_partials(dev(dy), dev(xh), dev(gamma), dev(inv),
+                                                      dx=acc)
+        exact(host(acc), old + host(dx), "dx accumulated")
+        exact(host(part2), host(part), "partials while accumulating")
     with pytest.raises(RuntimeError, match="groups"):
         hip.layernorm_backward_partials(dev(dy), dev(xh), dev(gamma), dev(inv), groups=groups + 1)
 
