@@ -172,9 +172,15 @@ def lm_step_flops(batch, seq, d, ff, vocab, layers):
     return 3 * fwd
 
 
-def cfg5_leg(engine_mod, eng, timer, steps, warmup):
+PROBE_STEPS = 3  # training steps after the timed ones with the dominant products probed
+
+
+def cfg5_leg(engine_mod, eng, timer, steps, warmup, hip=None):
     """cfg 5 training steps through the engine: forward + backward + Adam on one resident
-    batch; returns the record."""
+    batch; returns the record. With `hip`, PROBE_STEPS more steps run with the weight-gradient
+    products bracketed by HIP events on their stream (ehip_gemm_probe_arm): the dominant
+    kernel's time measured inside training steps, outside the timed ones so that their
+    event records cannot touch `value`."""
     b, s, vocab, d, h, ff, layers = W.TRANSFORMER_CFG5
     params = W.lm_init_params(CFG5_PARAM_SEED, vocab, d, ff, layers)
     ids, targets = W.lm_inputs(LM_INPUT_SEED, b, s, vocab)
@@ -185,12 +191,20 @@ def cfg5_leg(engine_mod, eng, timer, steps, warmup):
     total, per = timer.time_steps(tr.step, steps, max(warmup - 1, 0))
     last = tr.loss()
     n_params = int(tr.num_params())
+    probe = None
+    if hip is not None:
+        shapes = [(m, n, k) for m, n, k, _ in cfg5_dw_shapes()]
+        hip.gemm_probe_arm(True, False, shapes, 6 * layers * PROBE_STEPS + 16)
+        for _ in range(PROBE_STEPS):
+            tr.step()
+        ms, products, flop = hip.gemm_probe_read()
+        probe = {"ms": ms, "products": products, "flop": flop}
     tr.close()
     fl = lm_step_flops(b, s, d, ff, vocab, layers)
     sec = total / steps
     return {"seconds": sec, "median_s": float(np.median(per)), "params": n_params,
             "step_tflop": fl / 1e12, "loss_first_step": first, "loss_last": last,
-            "per_step_ms": [round(x * 1e3, 3) for x in per]}
+            "per_step_ms": [round(x * 1e3, 3) for x in per], "dw_probe": probe}
 
 
 def cfg5_dw_shapes():
@@ -232,6 +246,23 @@ def dominant_kernel(eng, timer, torch):
                     committed_traffic("cfg5_dw_gemm"))
     roof["flop_per_launch"] = flops / 6
     roof["shapes"] = shapes
+    return roof
+
+
+def in_step_roofline(probe, leg):
+    """The dominant kernel's roofline from the products timed inside training steps (the
+    probe: summed event time of every weight-gradient product of PROBE_STEPS steps, its
+    split-K reduction included), with the back-to-back leg's figures kept under "leg" (and
+    its per-shape rates) for comparison."""
+    if not probe or probe["products"] == 0:
+        return leg
+    roof = roofline(leg["kernel"], "mfma", probe["flop"] / probe["products"],
+                    probe["ms"] * 1e-3 / probe["products"], leg["traffic"])
+    roof["flop_per_launch"] = probe["flop"] / probe["products"]
+    roof["launches"] = probe["products"]
+    roof["shapes"] = leg["shapes"]
+    roof["leg"] = {"achieved": leg["achieved"], "frac": leg["frac"],
+                   "us_per_launch": leg["us_per_launch"]}
     return roof
 
 
@@ -691,6 +722,8 @@ def compact(line):
     roof["us_per_launch"] = line["roofline"]["us_per_launch"]
     roof["flop_per_launch"] = line["roofline"]["flop_per_launch"]
     roof["shapes_tflops"] = {k: v["tflops"] for k, v in line["roofline"]["shapes"].items()}
+    if "leg" in line["roofline"]:
+        roof["leg"] = line["roofline"]["leg"]
     out = dict(line, roofline=roof)
     ex = line.get("extra")
     if not ex:
@@ -818,12 +851,12 @@ def main():
         return
 
     log("bench: cfg5 Transformer training step")
-    rec = cfg5_leg(engine_capi, eng, timer, args.steps, args.warmup)
+    rec = cfg5_leg(engine_capi, eng, timer, args.steps, args.warmup, hip)
     sec = rec["seconds"]
     log(f"bench: {sec * 1e3:.3f} ms/step (median {rec['median_s'] * 1e3:.3f}), "
         f"loss {rec['loss_first_step']:.5f} -> {rec['loss_last']:.5f}")
     log("bench: dominant kernel (cfg5 weight-gradient products)")
-    roof = dominant_kernel(eng, timer, torch)
+    roof = in_step_roofline(rec["dw_probe"], dominant_kernel(eng, timer, torch))
     cpu = None
     if not args.no_cpu:
         log("bench: reference CPU baseline (cfg5 sample)")

@@ -29,6 +29,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <vector>
 
 #include "gemm_kernel.hpp"
 
@@ -748,8 +749,52 @@ bool bias_from_dw(int64_t rows, int64_t in, int64_t out) {
     return plan_tile(g, 1, true, false) != Tile::K;
 }
 
-// Validation shared by both entry points, then the kernel choice.
+// ------------------------------------------------------------ timing probe
+//
+// ehip_gemm_probe_arm / _read: an event pair on the product's stream around
+// every launch of an armed product shape (the tile kernel and its split-K
+// reduction), for measuring chosen products inside a real workload.
+struct GemmProbe {
+    std::mutex mu;
+    std::atomic<bool> armed{false};
+    int trans_a = 0, trans_b = 0;
+    std::vector<int64_t> shapes;  // m, n, k triples
+    std::vector<hipEvent_t> events;  // start, end pairs
+    size_t used = 0;
+    double flop = 0.0;
+};
+GemmProbe g_probe;
+
+int gemm_dispatch(const ehip_gemm_ex_t& d, hipStream_t s, const Workspace& wsp);
+
+// Validation shared by both entry points, then the kernel choice (bracketed
+// by the probe's events when the product is one it is armed for).
 int gemm_run(const ehip_gemm_ex_t& d, hipStream_t s, const Workspace& wsp = Workspace{}) {
+    if (!g_probe.armed.load(std::memory_order_relaxed)) return gemm_dispatch(d, s, wsp);
+    hipEvent_t start = nullptr, end = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_probe.mu);
+        bool match = d.batch == 1 && d.trans_a == g_probe.trans_a && d.trans_b == g_probe.trans_b &&
+                     g_probe.used + 2 <= g_probe.events.size();
+        bool shape = false;
+        for (size_t i = 0; match && !shape && i + 3 <= g_probe.shapes.size(); i += 3)
+            shape = g_probe.shapes[i] == d.m && g_probe.shapes[i + 1] == d.n &&
+                    g_probe.shapes[i + 2] == d.k;
+        if (match && shape) {
+            start = g_probe.events[g_probe.used];
+            end = g_probe.events[g_probe.used + 1];
+            g_probe.used += 2;
+            g_probe.flop += 2.0 * double(d.m) * double(d.n) * double(d.k);
+        }
+    }
+    if (start == nullptr) return gemm_dispatch(d, s, wsp);
+    if (hipEventRecord(start, s) != hipSuccess) return fail(EHIP_ELAUNCH, "gemm probe: event record");
+    const int rc = gemm_dispatch(d, s, wsp);
+    if (hipEventRecord(end, s) != hipSuccess) return fail(EHIP_ELAUNCH, "gemm probe: event record");
+    return rc;
+}
+
+int gemm_dispatch(const ehip_gemm_ex_t& d, hipStream_t s, const Workspace& wsp) {
     GemmArgs g{};
     g.a = d.a;
     g.b = d.b;
@@ -1088,6 +1133,54 @@ int ehip_linear_backward_f32(const float* x, const float* w, const float* dy, fl
 int ehip_linear_bias_from_dw(int on) {
     if (on < 0) return g_bias_from_dw.load() ? 1 : 0;
     return g_bias_from_dw.exchange(on != 0) ? 1 : 0;
+}
+
+int ehip_gemm_probe_arm(int trans_a, int trans_b, const int64_t* shapes, int count,
+                        int max_products) {
+    EHIP_READY();
+    if (count < 1 || !shapes || max_products < 1 || max_products > 65536)
+        return fail(EHIP_EINVAL, "gemm_probe_arm: %d shapes, %d products", count, max_products);
+    std::lock_guard<std::mutex> lock(g_probe.mu);
+    if (g_probe.armed.load()) return fail(EHIP_EINVAL, "gemm_probe_arm: already armed");
+    g_probe.trans_a = trans_a ? 1 : 0;
+    g_probe.trans_b = trans_b ? 1 : 0;
+    g_probe.shapes.assign(shapes, shapes + 3 * size_t(count));
+    g_probe.events.assign(2 * size_t(max_products), nullptr);
+    for (hipEvent_t& e : g_probe.events)
+        if (hipEventCreate(&e) != hipSuccess) {
+            for (hipEvent_t& f : g_probe.events)
+                if (f) (void)hipEventDestroy(f);
+            g_probe.events.clear();
+            return fail(EHIP_ELAUNCH, "gemm_probe_arm: event creation");
+        }
+    g_probe.used = 0;
+    g_probe.flop = 0.0;
+    g_probe.armed.store(true);
+    return EHIP_OK;
+}
+
+int ehip_gemm_probe_read(double* ms, int64_t* products, double* flop) {
+    EHIP_READY();
+    std::lock_guard<std::mutex> lock(g_probe.mu);
+    if (!g_probe.armed.load()) return fail(EHIP_EINVAL, "gemm_probe_read: not armed");
+    g_probe.armed.store(false);
+    double total = 0.0;
+    int rc = EHIP_OK;
+    for (size_t i = 0; i + 1 < g_probe.used; i += 2) {
+        float t = 0.0f;
+        if (hipEventSynchronize(g_probe.events[i + 1]) != hipSuccess ||
+            hipEventElapsedTime(&t, g_probe.events[i], g_probe.events[i + 1]) != hipSuccess) {
+            rc = fail(EHIP_ELAUNCH, "gemm_probe_read: event timing");
+            break;
+        }
+        total += double(t);
+    }
+    for (hipEvent_t& e : g_probe.events) (void)hipEventDestroy(e);
+    g_probe.events.clear();
+    if (ms) *ms = total;
+    if (products) *products = int64_t(g_probe.used / 2);
+    if (flop) *flop = g_probe.flop;
+    return rc;
 }
 
 int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream) {

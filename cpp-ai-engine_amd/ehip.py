@@ -100,6 +100,8 @@ _SIGS = {
     "ehip_gemm_f32_noalloc": [_i, _i, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                               _f, _vp, _i64, _i64, _vp],
     "ehip_gemm_ex_f32": [C.POINTER(GemmEx), _vp],
+    "ehip_gemm_probe_arm": [_i, _i, C.POINTER(C.c_int64), _i, _i],
+    "ehip_gemm_probe_read": [C.POINTER(C.c_double), C.POINTER(C.c_int64), C.POINTER(C.c_double)],
     "ehip_linear_backward_f32": [_vp] * 6 + [_i64, _i64, _i64, _vp],
     "ehip_binary_f32": [_i, _vp, _vp, _vp, _i64, _i64, _vp],
     "ehip_scalar_f32": [_vp, _vp, _i64, _f, _f, _vp],
@@ -264,6 +266,20 @@ class Backend:
             self.p(outs[1]), self.p(outs[2]), b, s_, w, heads, hd, scale, int(causal),
             self.stream()), "attention_short_backward")
         return outs
+
+    def gemm_probe_arm(self, trans_a, trans_b, shapes, max_products):
+        """Arms the timing probe for batch-1 products with these transposes and (m, n, k)
+        in `shapes`."""
+        flat = (C.c_int64 * (3 * len(shapes)))(*[int(v) for s_ in shapes for v in s_])
+        self.ok(self.lib.ehip_gemm_probe_arm(int(bool(trans_a)), int(bool(trans_b)), flat,
+                                             len(shapes), int(max_products)), "gemm_probe_arm")
+
+    def gemm_probe_read(self):
+        """(ms, products, flop) of the probed products since arming; disarms."""
+        ms, n, fl = C.c_double(0), C.c_int64(0), C.c_double(0)
+        self.ok(self.lib.ehip_gemm_probe_read(C.byref(ms), C.byref(n), C.byref(fl)),
+                "gemm_probe_read")
+        return ms.value, n.value, fl.value
 
     def versions(self):
         v = [C.c_int(0) for _ in range(3)]

@@ -318,6 +318,20 @@ typedef struct {
 
 int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream);
 
+/* Timing probe for chosen products inside a real workload (measurement only; no
+ * counterpart in the reference). ehip_gemm_probe_arm: from now on, every product
+ * of batch 1 with these trans_a / trans_b and (m, n, k) among `count` triples of
+ * `shapes` is bracketed by a pair of events recorded on its own stream -- the
+ * tile kernel and its split-K reduction inside -- for up to max_products
+ * products (events created here, on the host; refused while armed).
+ * ehip_gemm_probe_read waits for the last event, returns the summed GPU time in
+ * ms, the number of products and their 2 m n k FLOPs, and disarms. Event
+ * records ride the products' streams, so calls made under stream capture
+ * record them into the graph: arm only around eager work. */
+int ehip_gemm_probe_arm(int trans_a, int trans_b, const int64_t* shapes, int count,
+                        int max_products);
+int ehip_gemm_probe_read(double* ms, int64_t* products, double* flop);
+
 /* The three gradients of Linear, y = x . w + b with x (rows, in), w (in,
  * out), dy (rows, out): dx = dy . w^T, dw = x^T . dy, db = the column sums of
  * dy -- the matmul backward and the broadcast add's backward through

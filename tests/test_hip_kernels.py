@@ -1099,3 +1099,29 @@ def test_refusals_are_errors(hip):
         hip.ok(hip.lib.ehip_maxpool_fidx_f32(hip.p(x), hip.p(x), hip.p(x), ctypes.byref(w),
                                              hip.stream()), "maxpool_fidx")
     assert hip.launched() == before
+
+
+def test_gemm_probe(hip):
+    """ehip_gemm_probe_arm / _read: only batch-1 products of the armed transposes and shapes
+    are timed (the tile kernel and its split-K reduction between two events), their count and
+    2mnk FLOPs are reported, the results are the unprobed products' bits, and reading
+    disarms (a second read and a second arm while armed are refused)."""
+    import torch
+    print_case("gemm probe")
+    g = torch.Generator(device="cuda").manual_seed(3)
+    a = torch.randn(8192, 1024, device="cuda", generator=g)
+    b = torch.randn(8192, 256, device="cuda", generator=g)
+    want = hip.gemm(a, b, trans_a=True)  # 1024 x 256 x 8192: split along K
+    hip.gemm_probe_arm(True, False, [(1024, 256, 8192), (64, 64, 64)], 8)
+    with pytest.raises(RuntimeError, match="already armed"):
+        hip.gemm_probe_arm(True, False, [(1024, 256, 8192)], 8)
+    got = [hip.gemm(a, b, trans_a=True) for _ in range(2)]
+    hip.gemm(a[:, :256].contiguous(), b, trans_a=True)  # another shape: not probed
+    hip.gemm(b, a[:256, :256].contiguous())             # another mode: not probed
+    ms, n, flop = hip.gemm_probe_read()
+    assert n == 2 and flop == 2 * 2.0 * 1024 * 256 * 8192, (n, flop)
+    assert ms > 0.0
+    for x in got:
+        exact(host(x), host(want), "probed product")
+    with pytest.raises(RuntimeError, match="not armed"):
+        hip.gemm_probe_read()
