@@ -172,9 +172,11 @@ struct Workspace {
 // The grid's z extent: products beyond it run as further launches.
 constexpr int64_t kGridZ = 65535;
 
+// pipe: run the tiles as gemm_nt_pipe (whole 128 x 128 tiles of a batch-1
+// A B^T product; the same split and the same sums as the staged kernel).
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB>
 int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s,
-               const Workspace& wsp) {
+               const Workspace& wsp, bool pipe = false) {
     using C = Cfg<BM, BN, BK, WM, WN>;
     GemmArgs g = g0;
     g.tiles_m = int(ceil_div(g.m, BM));
@@ -225,6 +227,15 @@ int launch_cfg(const GemmArgs& g0, int64_t batch, bool check, hipStream_t s,
         g.batch0 = z0;
         const dim3 grid{unsigned(tiles), unsigned(splits),
                         unsigned(batch - z0 < kGridZ ? batch - z0 : kGridZ)};
+        if constexpr (BM == 128 && BN == 128 && BK == kNtBK && !TA && TB) {
+            if (pipe) {
+                if (epi)
+                    EHIP_LAUNCH("gemm", gemm_nt_pipe<true>, grid, dim3(256), 0, s, g);
+                else
+                    EHIP_LAUNCH("gemm", gemm_nt_pipe<false>, grid, dim3(256), 0, s, g);
+                continue;
+            }
+        }
         if (check && epi) {
             EHIP_LAUNCH("gemm", (gemm_kernel<BM, BN, BK, WM, WN, TA, TB, true, true>), grid,
                         dim3(C::kThreads), 0, s, g);
@@ -484,7 +495,15 @@ int gemm_modes(GemmArgs g, int64_t batch, hipStream_t s, const Workspace& wsp) {
     const auto whole = [&](int bm, int bn, int bk) {
         return g.vec && g.m % bm == 0 && g.n % bn == 0 && g.k % bk == 0;
     };
-    switch (plan_tile(g, batch, TA, TB)) {
+    const Tile tile = plan_tile(g, batch, TA, TB);
+    if constexpr (!TA && TB) {
+        // A B^T in whole 128 x 128 tiles: the two-step pipeline (same sums).
+        if ((tile == Tile::M || tile == Tile::L) && batch == 1 && g.causal == 0 && g.vec &&
+            g.m % 128 == 0 && g.n % 128 == 0 && g.k % kNtBK == 0 &&
+            (g.m / 128) * (g.n / 128) <= 0x7fffffff)
+            return launch_cfg<128, 128, 32, 64, 32, false, true>(g, batch, false, s, wsp, true);
+    }
+    switch (tile) {
         case Tile::L:
             return launch_cfg<256, 256, 16, 128, 64, TA, TB>(g, batch, !whole(256, 256, 16), s,
                                                              wsp);

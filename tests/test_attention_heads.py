@@ -307,6 +307,23 @@ def test_residual_epilogue(hip, m, k, n):
     exact(host(y), host(hip.relu(pre + c0 + res)), "bias + beta C + strided residual, ReLU")
 
 
+@pytest.mark.parametrize("ta,m,k,n", [(False, 256, 8192, 256), (True, 96, 2048, 96),
+                                      (True, 384, 2048, 96)])
+def test_residual_epilogue_split_and_panel(hip, ta, m, k, n):
+    """The residual on the other output paths: a product split along K (the reduction
+    applies the epilogue) and the A^T B panel products of narrow weight gradients."""
+    print_case("gemm_ex residual split/panel", ta, m, k, n)
+    r = np.random.default_rng(m + k + n + 7)
+    a = dev(randn(r, k, m)) if ta else dev(randn(r, m, k))
+    b = dev(randn(r, k, n))
+    res = dev(randn(r, m, n))
+    pre = hip.gemm(a, b, trans_a=ta)
+    y = hip.f32((m, n))
+    hip.gemm_ex(desc(hip, ta, False, 1, 1, m, n, k, a, m if ta else k, 0, 0, b, n, 0, 0, y, n, 0,
+                     0, residual=res, ld_res=n))
+    exact(host(y), host(res + pre), "residual")
+
+
 def test_residual_refusals(hip):
     """A residual row stride shorter than a row, or a residual on a batched product, is
     refused before any launch."""
