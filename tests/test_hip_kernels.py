@@ -1125,3 +1125,38 @@ def test_gemm_probe(hip):
         exact(host(x), host(want), "probed product")
     with pytest.raises(RuntimeError, match="not armed"):
         hip.gemm_probe_read()
+
+
+@pytest.mark.parametrize("m,n,k,epi", [(8192, 1024, 1024, "plain"), (4096, 1024, 384, "beta"),
+                                       (4096, 2048, 256, "residual")])
+def test_nt_pipeline_matches_staged_tiles(hip, m, n, k, epi):
+    """A B^T of batch 1 in whole 128 x 128 tiles runs gemm_nt_pipe; the same product as
+    both entries of a batch of two (operand strides 0) runs the staged tiles, which the
+    pipeline's MFMA chain repeats: the outputs agree bit for bit, plain, with beta = 1 and
+    with a residual in the epilogue (shapes that neither batch splits along K)."""
+    import torch
+    from ehip import GemmEx
+    print_case("nt pipeline vs staged", m, n, k, epi)
+    g = torch.Generator(device="cuda").manual_seed(m + n + k)
+    a = torch.randn(m, k, device="cuda", generator=g)
+    b = torch.randn(n, k, device="cuda", generator=g)
+    c0 = torch.randn(m, n, device="cuda", generator=g)
+    res = torch.randn(m, n, device="cuda", generator=g)
+    outs = []
+    for batch in (1, 2):
+        c = c0.repeat(batch, 1).contiguous()
+        d = GemmEx()
+        d.trans_a, d.trans_b, d.batch, d.inner = 0, 1, batch, 1
+        d.m, d.n, d.k = m, n, k
+        d.a, d.lda, d.stride_a = hip.p(a), k, 0
+        d.b, d.ldb, d.stride_b = hip.p(b), k, 0
+        d.c, d.ldc, d.stride_c = hip.p(c), n, m * n
+        d.alpha, d.addend_period = 1.0, 1
+        d.beta = 1.0 if epi == "beta" else 0.0
+        if epi == "residual" and batch == 1:
+            d.residual, d.ld_residual = hip.p(res), n
+        hip.gemm_ex(d)
+        if epi == "residual" and batch == 2:
+            c[:m] += res  # the separate add the epilogue replaces
+        outs.append(host(c[:m]))
+    exact(outs[0], outs[1], f"pipeline vs staged ({epi})")
