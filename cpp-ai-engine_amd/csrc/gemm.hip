@@ -27,6 +27,7 @@
 // shape. It is not bit-equal to the reference's serial i-k-j loop
 // (src/tensor_ops.cpp:539-562); the parity tests bound the difference.
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <vector>
@@ -354,15 +355,15 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kPanelWaves = 4;
 constexpr int kPanelSteps = 32;
 
+// One output tile of a panel product (the workgroup's whole work).
 template <bool CHECK, bool EPI>
-__global__ __launch_bounds__(64 * kPanelWaves) void gemm_tn_panel(GemmArgs g) {
+__device__ __forceinline__ void panel_tile(const GemmArgs& g, int tile) {
     // The checked form takes half the steps per round trip: its rows are often
     // unaligned (a 121-float row's 64-byte segments straddle cache lines), and
     // more loads in flight then only add line traffic (17.0 against 14.2 us).
     constexpr int kSteps = CHECK ? kPanelSteps / 2 : kPanelSteps;
     __shared__ float red[kPanelWaves][256];
     __shared__ float cred[kPanelWaves][64];
-    const int tile = int(blockIdx.x);
     const int64_t m0 = int64_t(tile / g.tiles_n) * 16, n0 = int64_t(tile % g.tiles_n) * 16;
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / 64);
     const int lane = int(threadIdx.x) % 64;
@@ -425,6 +426,30 @@ __global__ __launch_bounds__(64 * kPanelWaves) void gemm_tn_panel(GemmArgs g) {
     }
 }
 
+template <bool CHECK, bool EPI>
+__global__ __launch_bounds__(64 * kPanelWaves) void gemm_tn_panel(GemmArgs g) {
+    panel_tile<CHECK, EPI>(g, int(blockIdx.x));
+}
+
+// Independent panel products of one mode in one launch (ehip_gemm_batch_f32):
+// workgroups first[j] .. first[j + 1] - 1 are product j's tiles, each formed
+// exactly as its own launch would.
+constexpr int kPanelGroupMax = 8;
+struct PanelGroup {
+    GemmArgs g[kPanelGroupMax];
+    int first[kPanelGroupMax + 1];
+    int count;
+};
+
+template <bool CHECK, bool EPI>
+__global__ __launch_bounds__(64 * kPanelWaves) void gemm_tn_panel_group(PanelGroup p) {
+    const int b = int(blockIdx.x);
+    int j = 0;
+    while (j + 1 < p.count && b >= p.first[j + 1]) ++j;
+    j = __builtin_amdgcn_readfirstlane(j);
+    panel_tile<CHECK, EPI>(p.g[j], b - p.first[j]);
+}
+
 // The panel product's k per wave: whole chunks of 4 kPanelSteps k (the
 // unchecked kernel loads them without guards), else a multiple of 4.
 int64_t panel_wave_k(int64_t k, bool whole) {
@@ -464,13 +489,20 @@ Tile plan_tile(const GemmArgs& g, int64_t batch, bool ta, bool tb) {
     return Tile::T;
 }
 
-int launch_panel(GemmArgs g, hipStream_t s) {
+// A panel product's tile grid and k per wave; returns true for the unchecked
+// (whole) form.
+bool panel_geometry(GemmArgs& g) {
     g.tiles_m = int(ceil_div(g.m, 16));
     g.tiles_n = int(ceil_div(g.n, 16));
     const bool whole = g.m % 16 == 0 && g.n % 16 == 0 && g.k % (4 * kPanelSteps) == 0 &&
                        g.lda * g.k < (int64_t(1) << 31) && g.ldb * g.k < (int64_t(1) << 31);
     g.k_chunk = panel_wave_k(g.k, whole);
     g.splits = 1;
+    return whole;
+}
+
+int launch_panel(GemmArgs g, hipStream_t s) {
+    const bool whole = panel_geometry(g);
     const unsigned tiles = unsigned(int64_t(g.tiles_m) * g.tiles_n);
     const bool epi = !plain_epilogue(g);
     const dim3 block(64 * kPanelWaves);
@@ -811,6 +843,47 @@ int gemm_run(const ehip_gemm_ex_t& d, hipStream_t s, const Workspace& wsp = Work
     const int rc = gemm_dispatch(d, s, wsp);
     if (hipEventRecord(end, s) != hipSuccess) return fail(EHIP_ELAUNCH, "gemm probe: event record");
     return rc;
+}
+
+GemmArgs args_of(const ehip_gemm_ex_t& d) {
+    GemmArgs g{};
+    g.a = d.a;
+    g.b = d.b;
+    g.c = d.c;
+    g.m = d.m;
+    g.n = d.n;
+    g.k = d.k;
+    g.lda = d.lda;
+    g.ldb = d.ldb;
+    g.ldc = d.ldc;
+    g.causal = d.causal;
+    g.stride_a = d.stride_a;
+    g.stride_b = d.stride_b;
+    g.stride_c = d.stride_c;
+    g.inner = d.inner;
+    g.stride_a2 = d.stride_a_inner;
+    g.stride_b2 = d.stride_b_inner;
+    g.stride_c2 = d.stride_c_inner;
+    g.alpha = d.alpha;
+    g.add = d.addend;
+    g.ld_add = d.ld_addend;
+    g.stride_add = d.stride_addend;
+    g.add_period = d.addend ? d.addend_period : 1;
+    g.beta = d.beta;
+    g.relu = d.relu;
+    g.res = d.residual;
+    g.ld_res = d.ld_residual;
+    g.colsum = d.colsum_b;
+    return g;
+}
+
+// True when gemm_dispatch would run the descriptor (already checked) as a
+// panel product.
+bool takes_panel(const ehip_gemm_ex_t& d) {
+    if (d.batch != 1 || d.k == 0 || !d.trans_a || d.trans_b || d.m == 0 || d.n == 0 ||
+        small_kind(1, d.m, d.n, d.k) != 0)
+        return false;
+    return plan_tile(args_of(d), 1, true, false) == Tile::P;
 }
 
 int gemm_dispatch(const ehip_gemm_ex_t& d, hipStream_t s, const Workspace& wsp) {
@@ -1200,6 +1273,59 @@ int ehip_gemm_probe_read(double* ms, int64_t* products, double* flop) {
     if (products) *products = int64_t(g_probe.used / 2);
     if (flop) *flop = g_probe.flop;
     return rc;
+}
+
+int ehip_gemm_groupable(const ehip_gemm_ex_t* desc) {
+    if (!desc || check_desc(*desc) != EHIP_OK) return 0;
+    return takes_panel(*desc) ? 1 : 0;
+}
+
+int ehip_gemm_batch_f32(const ehip_gemm_ex_t* descs, int count, void* stream) {
+    EHIP_READY();
+    if (count < 0 || (count > 0 && !descs)) return fail(EHIP_EINVAL, "gemm_batch: bad list");
+    for (int i = 0; i < count; ++i)
+        if (int rc = check_desc(descs[i])) return rc;
+    hipStream_t s = as_stream(stream);
+    // The panel products of each mode (checked or not, epilogue or not) in
+    // launches of up to kPanelGroupMax; everything else one by one.
+    std::vector<GemmArgs> groups[4];
+    for (int i = 0; i < count; ++i) {
+        const ehip_gemm_ex_t& d = descs[i];
+        if (d.batch == 0 || d.m == 0 || d.n == 0) continue;
+        if (!takes_panel(d) || g_probe.armed.load()) {
+            if (int rc = gemm_run(d, s)) return rc;
+            continue;
+        }
+        GemmArgs g = args_of(d);
+        g.vec = operands_aligned(g) ? 1 : 0;
+        const bool whole = panel_geometry(g);
+        groups[(whole ? 0 : 2) + (plain_epilogue(g) ? 0 : 1)].push_back(g);
+    }
+    for (int mode = 0; mode < 4; ++mode) {
+        const std::vector<GemmArgs>& list = groups[mode];
+        for (size_t base = 0; base < list.size(); base += kPanelGroupMax) {
+            PanelGroup p{};
+            p.count = int(std::min<size_t>(kPanelGroupMax, list.size() - base));
+            p.first[0] = 0;
+            for (int j = 0; j < p.count; ++j) {
+                p.g[j] = list[base + j];
+                p.first[j + 1] = p.first[j] + p.g[j].tiles_m * p.g[j].tiles_n;
+            }
+            const dim3 grid(unsigned(p.first[p.count])), block(64 * kPanelWaves);
+            switch (mode) {
+                case 0: EHIP_LAUNCH("gemm_batch", (gemm_tn_panel_group<false, false>), grid, block, 0, s, p); break;
+                case 1: EHIP_LAUNCH("gemm_batch", (gemm_tn_panel_group<false, true>), grid, block, 0, s, p); break;
+                case 2: EHIP_LAUNCH("gemm_batch", (gemm_tn_panel_group<true, false>), grid, block, 0, s, p); break;
+                default: EHIP_LAUNCH("gemm_batch", (gemm_tn_panel_group<true, true>), grid, block, 0, s, p); break;
+            }
+        }
+    }
+    return EHIP_OK;
+}
+
+int ehip_linear_backward_plan(int64_t rows, int64_t in, int64_t out) {
+    if (rows <= 0 || in <= 0 || out <= 0) return 0;
+    return bias_from_dw(rows, in, out) ? 1 : 0;
 }
 
 int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream) {

@@ -100,6 +100,9 @@ _SIGS = {
     "ehip_gemm_f32_noalloc": [_i, _i, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                               _f, _vp, _i64, _i64, _vp],
     "ehip_gemm_ex_f32": [C.POINTER(GemmEx), _vp],
+    "ehip_gemm_groupable": [C.POINTER(GemmEx)],
+    "ehip_gemm_batch_f32": [C.POINTER(GemmEx), _i, _vp],
+    "ehip_linear_backward_plan": [_i64, _i64, _i64],
     "ehip_gemm_probe_arm": [_i, _i, C.POINTER(C.c_int64), _i, _i],
     "ehip_gemm_probe_read": [C.POINTER(C.c_double), C.POINTER(C.c_int64), C.POINTER(C.c_double)],
     "ehip_linear_backward_f32": [_vp] * 6 + [_i64, _i64, _i64, _vp],

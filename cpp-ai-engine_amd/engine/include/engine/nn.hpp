@@ -35,6 +35,15 @@ bool fused_nodes();
 void set_short_attention(bool on);
 bool short_attention();
 
+// Queued weight gradients, on by default: the Linear and feed-forward nodes of
+// narrow layers (whose dW = X^T dY takes the panel kernel with the bias
+// gradient as its column sums) queue that product instead of launching it,
+// and the queue runs them together (ehip_gemm_batch_f32) when a gradient is
+// first read or before Adam's launch: the same bits, fewer launches per
+// backward. Process-wide; set it between steps.
+void set_deferred_weight_grads(bool on);
+bool deferred_weight_grads();
+
 // Bias gradients from the weight-gradient product, on by default: Linear and
 // the feed-forward node take db of a mid-sized layer (more than 64 rows, dY of
 // at most 2^21 elements) from the column sums of dY that the dW = X^T dY

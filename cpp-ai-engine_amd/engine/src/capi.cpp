@@ -525,6 +525,12 @@ int eng_set_short_attention(int on) {
     return was ? 1 : 0;
 }
 
+int eng_set_deferred_weight_grads(int on) {
+    const bool was = nn::deferred_weight_grads();
+    nn::set_deferred_weight_grads(on != 0);
+    return was ? 1 : 0;
+}
+
 int eng_set_conv_implicit_gemm(int on) {
     const bool was = nn::conv_implicit_gemm();
     nn::set_conv_implicit_gemm(on != 0);

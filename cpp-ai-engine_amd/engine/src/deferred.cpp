@@ -1,7 +1,8 @@
 // deferred.cpp -- gradient work queued during backward: the weight-gradient
 // sums of fused convolution blocks and the parameter sums of large LayerNorms,
 // reduced for every queued node in one launch (ehip_conv_weight_reduce_f32)
-// instead of one launch per node.
+// instead of one launch per node; and the weight-gradient products of narrow
+// Linear layers (with their bias sums), run together by ehip_gemm_batch_f32.
 #include <memory>
 #include <utility>
 #include <vector>
@@ -15,6 +16,8 @@ namespace {
 
 struct Pending {
     std::vector<ehip_conv_reduce_t> jobs;
+    std::vector<ehip_gemm_ex_t> products;
+    std::vector<Tensor> product_inputs;  // the operands the products read
     DeferredKeep keep;
 };
 
@@ -39,11 +42,37 @@ void defer_conv_reduce(const ehip_conv_reduce_t& job, const Tensor& partials) {
 void defer_conv_output(const Tensor& param, const Tensor& grad) {
     // An add_grad between the job and this call may have flushed the queue, and
     // with it the job that writes `grad`: then there is nothing left to own.
-    if (g_pending.jobs.empty()) return;
+    if (g_pending.jobs.empty() && g_pending.products.empty()) return;
     g_pending.keep.outputs.emplace_back(param.get_impl(), grad.storage().share());
 }
 
-bool deferred_pending() { return !g_pending.jobs.empty(); }
+void defer_product(const ehip_gemm_ex_t& desc, std::initializer_list<Tensor> inputs) {
+    g_pending.products.push_back(desc);
+    for (const Tensor& t : inputs) g_pending.product_inputs.push_back(t);
+}
+
+bool deferred_pending() { return !g_pending.jobs.empty() || !g_pending.products.empty(); }
+
+namespace {
+
+// Runs the queued products (before anything reads their outputs or the
+// reductions that follow them in the queue's order).
+void run_products() {
+    if (g_pending.products.empty()) return;
+    std::vector<ehip_gemm_ex_t> products;
+    std::vector<Tensor> inputs;
+    std::swap(products, g_pending.products);
+    std::swap(inputs, g_pending.product_inputs);
+    const int rc = ehip_gemm_batch_f32(products.data(), int(products.size()), nullptr);
+    if (rc != EHIP_OK) {
+        g_pending.keep.reset_outputs();
+        g_pending.jobs.clear();
+        g_pending.keep = DeferredKeep{};
+    }
+    hip::check(rc, "queued weight-gradient products");
+}
+
+}  // namespace
 
 bool deferred_writes(const Storage& s) {
     for (const auto& out : g_pending.keep.outputs)
@@ -52,7 +81,11 @@ bool deferred_writes(const Storage& s) {
 }
 
 void flush_deferred() {
-    if (g_pending.jobs.empty()) return;
+    run_products();
+    if (g_pending.jobs.empty()) {
+        g_pending.keep = DeferredKeep{};
+        return;
+    }
     Pending p;
     std::swap(p, g_pending);
     const int rc = ehip_conv_weight_reduce_f32(p.jobs.data(), int(p.jobs.size()), nullptr);
@@ -63,6 +96,7 @@ void flush_deferred() {
 }
 
 void take_deferred(std::vector<ehip_conv_reduce_t>& jobs, DeferredKeep& keep) {
+    run_products();  // their outputs are gradients the caller's launch reads
     jobs = std::move(g_pending.jobs);
     keep = std::move(g_pending.keep);
     g_pending.jobs.clear();
@@ -72,6 +106,8 @@ void take_deferred(std::vector<ehip_conv_reduce_t>& jobs, DeferredKeep& keep) {
 void drop_deferred() {
     g_pending.keep.reset_outputs();
     g_pending.jobs.clear();
+    g_pending.products.clear();
+    g_pending.product_inputs.clear();
     g_pending.keep = DeferredKeep{};
 }
 

@@ -5,6 +5,7 @@
 #define ENGINE_SRC_DETAIL_HPP
 
 #include <cstdint>
+#include <initializer_list>
 #include <memory>
 #include <string>
 #include <utility>
@@ -103,6 +104,12 @@ struct DeferredKeep {
 };
 void defer_conv_reduce(const ehip_conv_reduce_t& job, const Tensor& partials);
 void defer_conv_output(const Tensor& param, const Tensor& grad);
+// Queues a product (a narrow weight gradient and its bias sum: a descriptor
+// ehip_gemm_groupable accepts) whose operands `inputs` hold; its outputs are
+// registered with defer_conv_output like a reduction's. Queued products run
+// before the queued reductions, all in as few launches as ehip_gemm_batch_f32
+// allows.
+void defer_product(const ehip_gemm_ex_t& desc, std::initializer_list<Tensor> inputs);
 bool deferred_pending();
 // True when a queued job writes the buffer of `s` (a registered output).
 bool deferred_writes(const Storage& s);

@@ -16,12 +16,15 @@ namespace nn {
 namespace {
 std::atomic<bool> g_fused_nodes{true};
 std::atomic<bool> g_short_attention{true};
+std::atomic<bool> g_deferred_weight_grads{true};
 }  // namespace
 
 void set_fused_nodes(bool on) { g_fused_nodes.store(on); }
 bool fused_nodes() { return g_fused_nodes.load(); }
 void set_short_attention(bool on) { g_short_attention.store(on); }
 bool short_attention() { return g_short_attention.load(); }
+void set_deferred_weight_grads(bool on) { g_deferred_weight_grads.store(on); }
+bool deferred_weight_grads() { return g_deferred_weight_grads.load(); }
 void set_fused_bias_grad(bool on) { ehip_linear_bias_from_dw(on ? 1 : 0); }
 bool fused_bias_grad() { return ehip_linear_bias_from_dw(-1) != 0; }
 

@@ -7,6 +7,7 @@
 #include <string>
 
 #include "detail.hpp"
+#include "engine/nn.hpp"
 #include "engine/tensor.hpp"
 
 namespace engine {
@@ -359,6 +360,46 @@ void check_residual(const Tensor* residual, size_t m, size_t n, const char* what
                                     std::to_string(n) + ") result.");
 }
 
+// dW = X^T dY (X rows x in, dY rows x out) with db = the column sums of dY,
+// the descriptor ehip_linear_backward_f32 launches for a layer whose bias
+// gradient comes from the product.
+ehip_gemm_ex_t weight_grad_desc(const float* x, const float* dy, float* dw, float* db,
+                                size_t rows, size_t in, size_t out) {
+    ehip_gemm_ex_t d{};
+    d.trans_a = 1;
+    d.batch = 1;
+    d.inner = 1;
+    d.m = int64_t(in);
+    d.n = int64_t(out);
+    d.k = int64_t(rows);
+    d.a = x;
+    d.lda = int64_t(in);
+    d.b = dy;
+    d.ldb = int64_t(out);
+    d.c = dw;
+    d.ldc = int64_t(out);
+    d.alpha = 1.0f;
+    d.addend_period = 1;
+    d.colsum_b = db;
+    return d;
+}
+
+// Queues dW and db of a narrow layer (see nn::set_deferred_weight_grads) when
+// both are fresh gradients and the library would form db from the product
+// and run it as a panel product (what ehip_gemm_batch_f32 groups); returns
+// false, having done nothing, otherwise. x and dy are kept until it runs.
+bool queue_weight_grads(const Tensor& x, const Tensor& dy, const Tensor& w, const Tensor& b,
+                        Tensor& dw, Tensor& db, size_t rows, size_t in, size_t out) {
+    if (!nn::deferred_weight_grads() || !w.requires_grad() || !b.requires_grad() ||
+        !grad_adoptable(w) || !grad_adoptable(b) ||
+        ehip_linear_backward_plan(int64_t(rows), int64_t(in), int64_t(out)) != 1)
+        return false;
+    const ehip_gemm_ex_t d = weight_grad_desc(dptr(x), dptr(dy), dout(dw), dout(db), rows, in, out);
+    if (!ehip_gemm_groupable(&d)) return false;
+    defer_product(d, {x, dy});
+    return true;
+}
+
 // Multiply-adds of g w^T above which Linear's backward no longer runs as one
 // launch (csrc/gemm.hip's thread-per-output limit), so that adding dx into
 // x's gradient in place saves a pass instead of splitting a launch in two.
@@ -386,7 +427,8 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias, const Tensor
     std::vector<std::shared_ptr<TensorImpl>> parents = {x.get_impl(), w.get_impl()};
     if (bias) parents.push_back(bias->get_impl());
     if (residual) parents.push_back(residual->get_impl());
-    attach(out, std::move(parents), [xc, wc, bc, rc, M, N, K](const Tensor& g) mutable {
+    const bool has_res = residual != nullptr;
+    attach(out, std::move(parents), [xc, wc, bc, rc, has_res, M, N, K](const Tensor& g) mutable {
         // The residual add's node comes last in the composed graph, so its
         // gradient goes first; the product reads g itself instead of the copy
         // the add's backward would hand it.
@@ -410,6 +452,22 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias, const Tensor
                                          int64_t(N), 0, dptr(wc), int64_t(N), 0, 1.0f, dx_acc,
                                          int64_t(K), 0, nullptr),
                            "linear backward dx");
+            // dW and db queued (the residual's gradient may hold g's buffer: a
+            // queued read of it would keep the next in-place add from it).
+            if (want_db && !has_res && queue_weight_grads(xc, g, wc, bc, dw, db, M, K, N)) {
+                // dx as ehip_linear_backward_f32 forms it for such a layer.
+                if (want_dx)
+                    hip::check(ehip_gemm_f32(0, 1, 1, int64_t(M), int64_t(K), int64_t(N),
+                                             dptr(g), int64_t(N), 0, dptr(wc), int64_t(N), 0,
+                                             0.0f, dout(dx), int64_t(K), 0, nullptr),
+                               "linear backward dx");
+                bc.add_grad(db);
+                if (want_dx) xc.add_grad(dx);
+                wc.add_grad(dw);
+                defer_conv_output(wc, dw);
+                defer_conv_output(bc, db);
+                return;
+            }
             hip::check(ehip_linear_backward_f32(dptr(xc), dptr(wc), dptr(g),
                                                 want_dx ? dout(dx) : nullptr,
                                                 wc.requires_grad() ? dout(dw) : nullptr,
@@ -510,14 +568,19 @@ Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, co
                               "feed-forward relu backward");
                dh = Tensor();
                Tensor dw1;
+               bool queued1 = false;
                if (b1c.requires_grad() && w1c.requires_grad() && D > 0 && F > 0) {
                    dw1 = empty_2d(D, F);
                    Tensor db1(b1c.shape(), 0.0f, false);
-                   hip::check(ehip_linear_backward_f32(dptr(xc), dptr(w1c), dptr(dpre), nullptr,
-                                                       dout(dw1), dout(db1), int64_t(M),
-                                                       int64_t(D), int64_t(F), nullptr),
-                              "feed-forward dw1 and db1");
+                   queued1 = queue_weight_grads(xc, dpre, w1c, b1c, dw1, db1, M, D, F);
+                   if (!queued1)
+                       hip::check(ehip_linear_backward_f32(dptr(xc), dptr(w1c), dptr(dpre),
+                                                           nullptr, dout(dw1), dout(db1),
+                                                           int64_t(M), int64_t(D), int64_t(F),
+                                                           nullptr),
+                                  "feed-forward dw1 and db1");
                    b1c.add_grad(db1);
+                   if (queued1) defer_conv_output(b1c, db1);
                } else if (b1c.requires_grad()) {
                    b1c.add_grad(reduce_to(dpre, b1c));
                }
@@ -536,6 +599,7 @@ Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, co
                                    false, "feed-forward dw1");
                    }
                    w1c.add_grad(dw1);
+                   if (queued1) defer_conv_output(w1c, dw1);
                }
            });
     return out;

@@ -358,6 +358,11 @@ class Engine:
         (default on) or through the batched products; returns the previous setting."""
         return bool(self.lib.eng_set_short_attention(int(bool(on))))
 
+    def set_deferred_weight_grads(self, on):
+        """Narrow layers' weight-gradient products queued and run together (default on) or
+        launched by each node; returns the previous setting."""
+        return bool(self.lib.eng_set_deferred_weight_grads(int(bool(on))))
+
     def set_conv_implicit_gemm(self, on):
         """Wide convolutions as implicit GEMMs (default on) or the reference's im2col
         composition; returns the previous setting."""

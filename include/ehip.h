@@ -318,6 +318,18 @@ typedef struct {
 
 int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream);
 
+/* Independent products in as few launches as their kernels allow: the narrow
+ * weight-gradient products (the A^T B panel kernel: trans_a, batch 1, few 16 x
+ * 16 output tiles over a long K; ehip_gemm_groupable says 1) of one kind run
+ * together, up to 8 per launch; every other descriptor runs as its own
+ * ehip_gemm_ex_f32 call. Each product's result, column sums included, has the
+ * bits of its own ehip_gemm_ex_f32 call. The products must be independent (no
+ * output read or written by another of the list). For engines that queue the
+ * weight gradients of a backward and run them together (launch-bound small
+ * models); no counterpart in the reference. */
+int ehip_gemm_groupable(const ehip_gemm_ex_t* desc);
+int ehip_gemm_batch_f32(const ehip_gemm_ex_t* descs, int count, void* stream);
+
 /* Timing probe for chosen products inside a real workload (measurement only; no
  * counterpart in the reference). ehip_gemm_probe_arm: from now on, every product
  * of batch 1 with these trans_a / trans_b and (m, n, k) among `count` triples of
@@ -355,6 +367,9 @@ int ehip_linear_backward_f32(const float* x, const float* w, const float* dy, fl
  * Process-wide; no counterpart in the reference (its fold is always separate,
  * src/tensor_detail.hpp:196-204). */
 int ehip_linear_bias_from_dw(int on);
+/* 1 when ehip_linear_backward_f32 of rows x in -> out takes db from the dW
+ * product's column sums (ehip_gemm_ex_t.colsum_b), 0 when it sums dy apart. */
+int ehip_linear_backward_plan(int64_t rows, int64_t in, int64_t out);
 
 /* --------------------------------------------------------- element-wise */
 

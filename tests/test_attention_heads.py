@@ -410,6 +410,33 @@ def test_charlm_training_fused_equals_composed(eng):
     exact(fused[1], comp[1], "weights")
 
 
+def test_deferred_weight_grads_equal_immediate(eng):
+    """The cfg3 character model with its narrow layers' weight-gradient products queued
+    during backward and run in grouped launches before Adam (ehip_gemm_batch_f32): step-1
+    gradients, losses and final weights equal, bit for bit, those of the same training
+    with every product launched by its node."""
+    import _compose as KC
+    from workloads import CHARLM_CFG3
+    b, s, vocab, d, heads, ff, layers = CHARLM_CFG3
+    print_case("charlm deferred weight gradients", CHARLM_CFG3)
+    r = np.random.default_rng(9)
+    ids = r.integers(0, vocab, (b, s)).astype(np.int64)
+    targets = r.integers(0, vocab, (b, s)).astype(np.int64)
+    shapes = KC.charlm_param_shapes(vocab, d, ff, layers)
+    params = np.concatenate([(randn(r, *shp) * np.float32(0.05)).ravel() for shp in shapes])
+    runs = []
+    prev = eng.set_deferred_weight_grads(True)
+    try:
+        for on in (True, False):
+            eng.set_deferred_weight_grads(on)
+            runs.append(eng.charlm_train(ids, targets, vocab, d, heads, ff, layers, params, 4,
+                                         1e-3, grads0=True))
+    finally:
+        eng.set_deferred_weight_grads(prev)
+    for got, want, what in zip(runs[0], runs[1], ("losses", "weights", "step-1 gradients")):
+        exact(got, want, f"deferred {what}")
+
+
 def test_cnn_gradients_fused_vs_composed(eng):
     """cfg2 CNN, one backward: with fused nodes the conv weight sums are queued and run when
     Tensor::grad() reads them. Loss and Linear gradients are the bits of the node-by-node
@@ -506,6 +533,62 @@ def test_panel_epilogue_and_repeat(hip):
             first = outs[0]
         elif (m, k, n) == cases[0]:
             exact(outs[0], first, "panel after products of other shapes")
+
+
+# (m, k, n, kind): narrow weight gradients with column sums (cfg3's layers), a ragged
+# panel (checked tiles), alpha/beta and plain panels, ten of one kind (two launches of at
+# most eight), and products that do not take the panel kernel (staged tiles, the
+# thread-per-output kernel's column sum) mixed in.
+BATCH_CASES = ([(96, 2048, 96, "colsum"), (96, 2048, 384, "colsum"), (384, 2048, 96, "colsum"),
+                (96, 2048, 121, "colsum"), (100, 1500, 37, "plain"), (96, 4096, 96, "beta"),
+                (1024, 1024, 1024, "plain"), (37, 50, 20, "colsum"), (100, 1500, 37, "beta")] +
+               [(64 + 16 * i, 1024, 48, "colsum") for i in range(10)])
+
+
+def test_gemm_batch_matches_single_calls(hip):
+    """ehip_gemm_batch_f32 equals each product run on its own by ehip_gemm_ex_f32 bit for
+    bit, outputs and column sums, whatever launches it groups them into;
+    ehip_gemm_groupable says which descriptors take the panel kernel."""
+    import ctypes as C
+    from ehip import GemmEx
+    import torch
+    print_case("gemm_batch", len(BATCH_CASES), "products")
+    gen = torch.Generator(device="cuda").manual_seed(23)
+    singles, batch, outs = [], [], []
+    for m, k, n, kind in BATCH_CASES:
+        a = torch.randn(k, m, device="cuda", generator=gen)
+        b = torch.randn(k, n, device="cuda", generator=gen)
+        c0 = torch.randn(m, n, device="cuda", generator=gen)
+        pair = []
+        for _ in range(2):
+            c, cs = c0.clone(), torch.full((n,), 7.0, device="cuda")
+            beta = 1.0 if kind == "beta" else 0.0
+            d = desc(hip, True, False, 1, 1, m, n, k, a, m, 0, 0, b, n, 0, 0, c, n, 0, 0,
+                     alpha=0.5 if kind == "beta" else 1.0, beta=beta)
+            if kind == "colsum":
+                d.colsum_b = hip.p(cs)
+            pair.append((d, c, cs))
+        singles.append(pair[0][0])
+        batch.append(pair[1][0])
+        outs.append((pair[0][1:], pair[1][1:], (a, b), kind))
+    groupable = [hip.lib.ehip_gemm_groupable(C.byref(d)) for d in batch]
+    assert groupable == [1, 1, 1, 1, 1, 1, 0, 0, 1] + [1] * 10, groupable
+    for d in singles:
+        hip.gemm_ex(d)
+    arr = (GemmEx * len(batch))(*batch)
+    hip.ok(hip.lib.ehip_gemm_batch_f32(arr, len(batch), hip.stream()), "gemm_batch")
+    for (m, k, n, kind), (one, together, _, _) in zip(BATCH_CASES, outs):
+        exact(host(together[0]), host(one[0]), f"batched product {m}x{k}x{n} {kind}")
+        if kind == "colsum":
+            exact(host(together[1]), host(one[1]), f"batched column sums {m}x{k}x{n}")
+    # Refusals come before anything runs: a bad descriptor anywhere in the list.
+    bad = (GemmEx * 2)(batch[0], batch[1])
+    bad[1].m = -1
+    with pytest.raises(RuntimeError):
+        hip.ok(hip.lib.ehip_gemm_batch_f32(bad, 2, hip.stream()), "gemm_batch")
+    with pytest.raises(RuntimeError):
+        hip.ok(hip.lib.ehip_gemm_batch_f32(arr, -1, hip.stream()), "gemm_batch")
+    hip.ok(hip.lib.ehip_gemm_batch_f32(arr, 0, hip.stream()), "gemm_batch empty")
 
 
 def test_colsum_refusals_and_k_zero(hip):
