@@ -431,23 +431,31 @@ __global__ __launch_bounds__(64 * kPanelWaves) void gemm_tn_panel(GemmArgs g) {
     panel_tile<CHECK, EPI>(g, int(blockIdx.x));
 }
 
-// Independent panel products of one mode in one launch (ehip_gemm_batch_f32):
-// workgroups first[j] .. first[j + 1] - 1 are product j's tiles, each formed
-// exactly as its own launch would.
-constexpr int kPanelGroupMax = 8;
+// Independent panel products in one launch (ehip_gemm_batch_f32): workgroups
+// first[j] .. first[j + 1] - 1 are product j's tiles, each formed exactly as
+// its own launch would, in the form (mode[j]: bit 0 checked tiles, bit 1 the
+// epilogue) its own launch takes; the branch is uniform per workgroup.
+constexpr int kPanelGroupMax = 12;
 struct PanelGroup {
     GemmArgs g[kPanelGroupMax];
     int first[kPanelGroupMax + 1];
+    int mode[kPanelGroupMax];
     int count;
 };
+static_assert(sizeof(PanelGroup) <= 4096, "kernel arguments of at most 4 KB");
 
-template <bool CHECK, bool EPI>
 __global__ __launch_bounds__(64 * kPanelWaves) void gemm_tn_panel_group(PanelGroup p) {
     const int b = int(blockIdx.x);
     int j = 0;
     while (j + 1 < p.count && b >= p.first[j + 1]) ++j;
     j = __builtin_amdgcn_readfirstlane(j);
-    panel_tile<CHECK, EPI>(p.g[j], b - p.first[j]);
+    const int tile = b - p.first[j];
+    switch (__builtin_amdgcn_readfirstlane(p.mode[j])) {
+        case 0: panel_tile<false, false>(p.g[j], tile); break;
+        case 1: panel_tile<true, false>(p.g[j], tile); break;
+        case 2: panel_tile<false, true>(p.g[j], tile); break;
+        default: panel_tile<true, true>(p.g[j], tile); break;
+    }
 }
 
 // The panel product's k per wave: whole chunks of 4 kPanelSteps k (the
@@ -1286,9 +1294,11 @@ int ehip_gemm_batch_f32(const ehip_gemm_ex_t* descs, int count, void* stream) {
     for (int i = 0; i < count; ++i)
         if (int rc = check_desc(descs[i])) return rc;
     hipStream_t s = as_stream(stream);
-    // The panel products of each mode (checked or not, epilogue or not) in
-    // launches of up to kPanelGroupMax; everything else one by one.
-    std::vector<GemmArgs> groups[4];
+    // The panel products in launches of up to kPanelGroupMax, the checked ones
+    // first (their tiles take the longest: started first, they end with the
+    // rest instead of after it); everything else one by one.
+    std::vector<GemmArgs> list;
+    std::vector<int> modes;
     for (int i = 0; i < count; ++i) {
         const ehip_gemm_ex_t& d = descs[i];
         if (d.batch == 0 || d.m == 0 || d.n == 0) continue;
@@ -1299,26 +1309,23 @@ int ehip_gemm_batch_f32(const ehip_gemm_ex_t* descs, int count, void* stream) {
         GemmArgs g = args_of(d);
         g.vec = operands_aligned(g) ? 1 : 0;
         const bool whole = panel_geometry(g);
-        groups[(whole ? 0 : 2) + (plain_epilogue(g) ? 0 : 1)].push_back(g);
+        list.push_back(g);
+        modes.push_back((whole ? 0 : 1) | (plain_epilogue(g) ? 0 : 2));
     }
-    for (int mode = 0; mode < 4; ++mode) {
-        const std::vector<GemmArgs>& list = groups[mode];
-        for (size_t base = 0; base < list.size(); base += kPanelGroupMax) {
-            PanelGroup p{};
-            p.count = int(std::min<size_t>(kPanelGroupMax, list.size() - base));
-            p.first[0] = 0;
-            for (int j = 0; j < p.count; ++j) {
-                p.g[j] = list[base + j];
-                p.first[j + 1] = p.first[j] + p.g[j].tiles_m * p.g[j].tiles_n;
-            }
-            const dim3 grid(unsigned(p.first[p.count])), block(64 * kPanelWaves);
-            switch (mode) {
-                case 0: EHIP_LAUNCH("gemm_batch", (gemm_tn_panel_group<false, false>), grid, block, 0, s, p); break;
-                case 1: EHIP_LAUNCH("gemm_batch", (gemm_tn_panel_group<false, true>), grid, block, 0, s, p); break;
-                case 2: EHIP_LAUNCH("gemm_batch", (gemm_tn_panel_group<true, false>), grid, block, 0, s, p); break;
-                default: EHIP_LAUNCH("gemm_batch", (gemm_tn_panel_group<true, true>), grid, block, 0, s, p); break;
-            }
+    std::vector<size_t> order(list.size());
+    for (size_t i = 0; i < order.size(); ++i) order[i] = i;
+    std::stable_partition(order.begin(), order.end(), [&](size_t i) { return modes[i] & 1; });
+    for (size_t base = 0; base < list.size(); base += kPanelGroupMax) {
+        PanelGroup p{};
+        p.count = int(std::min<size_t>(kPanelGroupMax, list.size() - base));
+        p.first[0] = 0;
+        for (int j = 0; j < p.count; ++j) {
+            p.g[j] = list[order[base + j]];
+            p.mode[j] = modes[order[base + j]];
+            p.first[j + 1] = p.first[j] + p.g[j].tiles_m * p.g[j].tiles_n;
         }
+        EHIP_LAUNCH("gemm_batch", gemm_tn_panel_group, dim3(unsigned(p.first[p.count])),
+                    dim3(64 * kPanelWaves), 0, s, p);
     }
     return EHIP_OK;
 }
