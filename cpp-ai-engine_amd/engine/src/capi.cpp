@@ -730,6 +730,49 @@ int eng_charlm_train_grads(const float* ids, const int64_t* targets, int64_t bat
     });
 }
 
+// The character model's gradients summed over `passes` forward and backward
+// passes of one batch (gradient accumulation: the second pass adds into
+// gradients the first left, some of them still queued).
+int eng_charlm_accumulated_grads(const float* ids, const int64_t* targets, int64_t batch,
+                                 int64_t seq, int64_t vocab, int64_t d, int64_t heads, int64_t ff,
+                                 int64_t layers, const float* params, int64_t passes,
+                                 float* grads_out) {
+    return guarded([&] {
+        CharModel model{size_t(vocab), size_t(seq), size_t(d), size_t(heads), size_t(ff),
+                        size_t(layers)};
+        load_params(model.parameters(), params);
+        const Tensor mask = nn::causal_mask(size_t(seq));
+        Tensor X = make({size_t(batch), size_t(seq)}, ids, false);
+        const std::vector<size_t> y = labels_of(targets, batch * seq);
+        for (int64_t p = 0; p < passes; ++p) {
+            Tensor logits = model.forward(X, mask).reshape({size_t(batch * seq), size_t(vocab)});
+            nn::cross_entropy_loss(logits, y).backward();
+        }
+        size_t off = 0;
+        for (Tensor& p : model.parameters()) {
+            put(p.grad(), grads_out + off);
+            off += p.size();
+        }
+    });
+}
+
+// Forward and backward of a character model that is then destroyed without
+// anything reading its gradients: the queued weight-gradient products (and
+// LayerNorm sums) outlive the model, to be run by the next engine work.
+int eng_charlm_backward_orphan(const float* ids, const int64_t* targets, int64_t batch,
+                               int64_t seq, int64_t vocab, int64_t d, int64_t heads, int64_t ff,
+                               int64_t layers, const float* params) {
+    return guarded([&] {
+        CharModel model{size_t(vocab), size_t(seq), size_t(d), size_t(heads), size_t(ff),
+                        size_t(layers)};
+        load_params(model.parameters(), params);
+        const Tensor mask = nn::causal_mask(size_t(seq));
+        Tensor X = make({size_t(batch), size_t(seq)}, ids, false);
+        Tensor logits = model.forward(X, mask).reshape({size_t(batch * seq), size_t(vocab)});
+        nn::cross_entropy_loss(logits, labels_of(targets, batch * seq)).backward();
+    });
+}
+
 int eng_charlm_train(const float* ids, const int64_t* targets, int64_t batch, int64_t seq,
                      int64_t vocab, int64_t d, int64_t heads, int64_t ff, int64_t layers,
                      const float* params, int64_t steps, float lr, float* losses,

@@ -407,6 +407,28 @@ class Engine:
         f.argtypes = [_f32p, _i64p] + [_i64] * 6 + [_f32p]
         self._ok(f(_fp(x), _ip(labels), b, cin, c1, c2, hw, classes, _fp(params)))
 
+    def charlm_accumulated_grads(self, ids, targets, vocab, d, heads, ff, layers, params,
+                                 passes):
+        """The character model's gradients summed over `passes` forward + backward passes."""
+        ids, params = _f32(ids), _f32(params)
+        targets = np.ascontiguousarray(targets, np.int64)
+        b, s = ids.shape
+        out = np.empty_like(params)
+        f = self.lib.eng_charlm_accumulated_grads
+        f.argtypes = [_f32p, _i64p] + [_i64] * 7 + [_f32p, _i64, _f32p]
+        self._ok(f(_fp(ids), _ip(targets), b, s, vocab, d, heads, ff, layers, _fp(params),
+                   passes, _fp(out)))
+        return out
+
+    def charlm_backward_orphan(self, ids, targets, vocab, d, heads, ff, layers, params):
+        """Forward + backward of a character model destroyed before its queued work ran."""
+        ids, params = _f32(ids), _f32(params)
+        targets = np.ascontiguousarray(targets, np.int64)
+        b, s = ids.shape
+        f = self.lib.eng_charlm_backward_orphan
+        f.argtypes = [_f32p, _i64p] + [_i64] * 7 + [_f32p]
+        self._ok(f(_fp(ids), _ip(targets), b, s, vocab, d, heads, ff, layers, _fp(params)))
+
     def cnn_train(self, x, labels, params, steps, lr, c1=8, c2=16, classes=10):
         x, params = _f32(x), _f32(params)
         labels = np.ascontiguousarray(labels, np.int64)

@@ -437,6 +437,53 @@ def test_deferred_weight_grads_equal_immediate(eng):
         exact(got, want, f"deferred {what}")
 
 
+def _cfg3_case(seed):
+    import _compose as KC
+    from workloads import CHARLM_CFG3
+    b, s, vocab, d, heads, ff, layers = CHARLM_CFG3
+    r = np.random.default_rng(seed)
+    ids = r.integers(0, vocab, (b, s)).astype(np.int64)
+    targets = r.integers(0, vocab, (b, s)).astype(np.int64)
+    shapes = KC.charlm_param_shapes(vocab, d, ff, layers)
+    params = np.concatenate([(randn(r, *shp) * np.float32(0.05)).ravel() for shp in shapes])
+    return ids, targets, (vocab, d, heads, ff, layers), params
+
+
+def test_deferred_weight_grads_accumulate(eng):
+    """Gradient accumulation: a second forward and backward adds into gradients the first
+    left queued (the queue runs before the add reads them); the sums equal, bit for bit,
+    those of the same two passes with every product launched by its node, and twice one
+    pass's gradients within the rounding of one add."""
+    ids, targets, dims, params = _cfg3_case(13)
+    print_case("charlm deferred gradients accumulated over two passes")
+    got = {}
+    prev = eng.set_deferred_weight_grads(True)
+    try:
+        for on in (True, False):
+            eng.set_deferred_weight_grads(on)
+            got[on] = eng.charlm_accumulated_grads(ids, targets, *dims, params, 2)
+        once = eng.charlm_accumulated_grads(ids, targets, *dims, params, 1)
+    finally:
+        eng.set_deferred_weight_grads(prev)
+    exact(got[True], got[False], "accumulated gradients")
+    assert np.all(np.isfinite(got[True]))
+    np.testing.assert_allclose(got[True], 2 * once, rtol=1e-6, atol=1e-12)
+
+
+def test_orphaned_weight_grad_products_touch_no_reused_memory(eng):
+    """A character model whose backward queued its weight-gradient products is destroyed
+    before anything reads its gradients; the queue runs at the next engine work, writing
+    into buffers it owns and reading operands it keeps. Training a second model right after
+    gives the same bits as the same training in a clean state."""
+    ids, targets, dims, params = _cfg3_case(17)
+    print_case("orphaned weight-gradient products")
+    want_losses, want_p = eng.charlm_train(ids, targets, *dims, params, 3, 1e-3)
+    eng.charlm_backward_orphan(ids, targets, *dims, params * np.float32(0.5))
+    losses, out = eng.charlm_train(ids, targets, *dims, params, 3, 1e-3)
+    exact(losses, want_losses, "losses")
+    exact(out, want_p, "parameters")
+
+
 def test_cnn_gradients_fused_vs_composed(eng):
     """cfg2 CNN, one backward: with fused nodes the conv weight sums are queued and run when
     Tensor::grad() reads them. Loss and Linear gradients are the bits of the node-by-node
