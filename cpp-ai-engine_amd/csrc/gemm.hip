@@ -328,7 +328,8 @@ int launch_kslice(GemmArgs g, int64_t batch, hipStream_t s) {
 //   S  128 x  64 x 32, 8 waves of  32 x 32   thin outputs (N = 64 attention products)
 //   K  32 x 32 per workgroup, K sliced over its waves: outputs too small for
 //      the larger tiles to fill the chip (512^3, the char-Transformer's layers)
-//   T   64 x  64 x 16, 4 waves of  32 x 32   the rest (few tiles; B column sums)
+//   T   64 x  64 x 16, 4 waves of  32 x 32   the rest (few tiles; B column sums;
+//      products that skip K causally)
 //   P   16 x 16 per workgroup of 16 waves, each wave a sixteenth of K: A^T B
 //       products of few tiles over a long K (weight gradients of narrow
 //       layers), one load round trip per 128 k of a wave, no workspace
@@ -487,7 +488,15 @@ Tile plan_tile(const GemmArgs& g, int64_t batch, bool ta, bool tb) {
     const bool long_k = g.k >= 2048;
     if (tl >= 256 && padding(g.m, g.n, 256, 256) < 0.15 && g.k >= 256) return Tile::L;
     if ((tm >= 128 || (tm >= 32 && long_k)) && padding(g.m, g.n, 128, 128) < 0.25) return Tile::M;
-    if ((ts >= 128 || (ts >= 32 && long_k)) && padding(g.m, g.n, 128, 64) < 0.25) return Tile::S;
+    // Causal skipping from below (mode 3, the attention backward's dV = W^T dO
+    // and dK = dS^T Q) skips more in 64-row bands: the 64 x 64 tile there
+    // (measured on MI355X in cfg5's step, 256 heads of 512 x 64 x 512: 60.5 ->
+    // 51.3 us; for mode 2 it measured slower in the step, 58.4 -> 61.0 us, and
+    // without skipping the 128 x 64 tile is 3 % ahead). Only where neither tile
+    // splits K (at least 512 of the 128 x 64 tiles), so that the skipping
+    // product keeps the bits of the same product without it.
+    if ((ts >= 128 || (ts >= 32 && long_k)) && padding(g.m, g.n, 128, 64) < 0.25)
+        return g.causal == 3 && ts >= 512 ? Tile::T : Tile::S;
     // Weight gradients of narrow layers: few output tiles, long K.
     if (ta && !tb && batch == 1 && g.causal == 0 && g.k >= 1024 &&
         ceil_div(g.m, 16) * ceil_div(g.n, 16) <= 1024)
