@@ -459,6 +459,21 @@ __global__ __launch_bounds__(64 * kPanelWaves) void gemm_tn_panel_group(PanelGro
     }
 }
 
+// Independent K-sliced products A B (neither operand transposed) of one
+// kernel form in one launch (ehip_gemm_batch_f32; the projections of one
+// input, e.g. attention's query, key and value): workgroups first[j] ..
+// first[j + 1] - 1 are product j's tiles, each formed with the K slicing its
+// own launch would use.
+template <int W, bool CHECK, bool EPI>
+__global__ __launch_bounds__(64 * W) void gemm_kslice_group(PanelGroup p) {
+    __shared__ __attribute__((aligned(16))) float lds[KsliceLds<W>::kFloats];
+    const int b = int(blockIdx.x);
+    int j = 0;
+    while (j + 1 < p.count && b >= p.first[j + 1]) ++j;
+    j = __builtin_amdgcn_readfirstlane(j);
+    kslice_tile<W, false, false, CHECK, EPI, 4>(p.g[j], b - p.first[j], 0, lds, W);
+}
+
 // The panel product's k per wave: whole chunks of 4 kPanelSteps k (the
 // unchecked kernel loads them without guards), else a multiple of 4.
 int64_t panel_wave_k(int64_t k, bool whole) {
@@ -903,6 +918,37 @@ bool takes_panel(const ehip_gemm_ex_t& d) {
     return plan_tile(args_of(d), 1, true, false) == Tile::P;
 }
 
+// True when gemm_dispatch would run the descriptor (already checked) as an
+// unsplit K-sliced A B product that ehip_gemm_batch_f32 can group; g is then
+// its launch arguments (geometry set) and form its kernel: waves index
+// (0..3 for 1..8 waves) * 4 + checked tiles + 2 * epilogue.
+bool takes_kslice_nn(const ehip_gemm_ex_t& d, GemmArgs& g, int& form) {
+    if (d.batch != 1 || d.k == 0 || d.trans_a || d.trans_b || d.causal || d.colsum_b ||
+        small_kind(1, d.m, d.n, d.k) != 0)
+        return false;
+    g = args_of(d);
+    g.vec = operands_aligned(g) ? 1 : 0;
+    g.vec_ab = operand_alignment(g);
+    if (plan_tile(g, 1, false, false) != Tile::K) return false;
+    const int w = kslice_waves(ceil_div(g.m, 32) * ceil_div(g.n, 32), g.k);
+    kslice_geometry(g, w);
+    form = (w == 1 ? 0 : w == 2 ? 1 : w == 4 ? 2 : 3) * 4 + (kslice_whole(g) ? 0 : 1) +
+           (plain_epilogue(g) ? 0 : 2);
+    return true;
+}
+
+template <int W>
+int launch_kslice_group(const PanelGroup& p, int form, hipStream_t s) {
+    const dim3 grid(unsigned(p.first[p.count])), block(64 * W);
+    switch (form % 4) {
+        case 0: EHIP_LAUNCH("gemm_batch", (gemm_kslice_group<W, false, false>), grid, block, 0, s, p); break;
+        case 1: EHIP_LAUNCH("gemm_batch", (gemm_kslice_group<W, true, false>), grid, block, 0, s, p); break;
+        case 2: EHIP_LAUNCH("gemm_batch", (gemm_kslice_group<W, false, true>), grid, block, 0, s, p); break;
+        default: EHIP_LAUNCH("gemm_batch", (gemm_kslice_group<W, true, true>), grid, block, 0, s, p); break;
+    }
+    return EHIP_OK;
+}
+
 int gemm_dispatch(const ehip_gemm_ex_t& d, hipStream_t s, const Workspace& wsp) {
     GemmArgs g{};
     g.a = d.a;
@@ -1308,9 +1354,16 @@ int ehip_gemm_batch_f32(const ehip_gemm_ex_t* descs, int count, void* stream) {
     // rest instead of after it); everything else one by one.
     std::vector<GemmArgs> list;
     std::vector<int> modes;
+    std::vector<GemmArgs> ks[16];  // K-sliced A B products by kernel form
     for (int i = 0; i < count; ++i) {
         const ehip_gemm_ex_t& d = descs[i];
         if (d.batch == 0 || d.m == 0 || d.n == 0) continue;
+        GemmArgs kg;
+        int form = 0;
+        if (!g_probe.armed.load() && takes_kslice_nn(d, kg, form)) {
+            ks[form].push_back(kg);
+            continue;
+        }
         if (!takes_panel(d) || g_probe.armed.load()) {
             if (int rc = gemm_run(d, s)) return rc;
             continue;
@@ -1335,6 +1388,23 @@ int ehip_gemm_batch_f32(const ehip_gemm_ex_t* descs, int count, void* stream) {
         }
         EHIP_LAUNCH("gemm_batch", gemm_tn_panel_group, dim3(unsigned(p.first[p.count])),
                     dim3(64 * kPanelWaves), 0, s, p);
+    }
+    for (int form = 0; form < 16; ++form) {
+        const std::vector<GemmArgs>& kl = ks[form];
+        for (size_t base = 0; base < kl.size(); base += kPanelGroupMax) {
+            PanelGroup p{};
+            p.count = int(std::min<size_t>(kPanelGroupMax, kl.size() - base));
+            for (int j = 0; j < p.count; ++j) {
+                p.g[j] = kl[base + j];
+                p.first[j + 1] = p.first[j] + p.g[j].tiles_m * p.g[j].tiles_n;
+            }
+            const int w = form / 4;
+            const int rc = w == 0   ? launch_kslice_group<1>(p, form, s)
+                           : w == 1 ? launch_kslice_group<2>(p, form, s)
+                           : w == 2 ? launch_kslice_group<4>(p, form, s)
+                                    : launch_kslice_group<8>(p, form, s);
+            if (rc) return rc;
+        }
     }
     return EHIP_OK;
 }

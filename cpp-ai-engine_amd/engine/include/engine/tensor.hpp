@@ -146,6 +146,13 @@ Tensor matmul_nt(const Tensor& a, const Tensor& b);
 Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias,
               const Tensor* residual = nullptr);
 
+// linear(x, w[i], bias[i]) for several layers over one input (attention's
+// query, key and value projections), the products in one launch where the
+// library groups them (ehip_gemm_batch_f32); each output is linear()'s node
+// with linear()'s bits. bias[i] may be null.
+std::vector<Tensor> linear_many(const Tensor& x, const std::vector<const Tensor*>& w,
+                                const std::vector<const Tensor*>& bias);
+
 // relu(x w1 + b1) w2 + b2 as one node (TransformerBlock's feed-forward,
 // src/transformer.cpp:409-414): the biases and the ReLU in the products'
 // epilogues, only the ReLU output kept (its backward reads the mask from

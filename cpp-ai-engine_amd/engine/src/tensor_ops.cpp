@@ -318,9 +318,9 @@ namespace {
 
 // out (m, n) = op(a) op(b) over plain 2-D operands, then + bias (a row),
 // + residual (an (m, n) array) and ReLU, each rounded on its own.
-void gemm_2d(bool ta, bool tb, size_t m, size_t n, size_t k, const float* a, const float* b,
-             float* c, const float* bias, bool relu, const char* what,
-             const float* residual = nullptr) {
+ehip_gemm_ex_t gemm_2d_desc(bool ta, bool tb, size_t m, size_t n, size_t k, const float* a,
+                            const float* b, float* c, const float* bias, bool relu,
+                            const float* residual) {
     ehip_gemm_ex_t d{};
     d.trans_a = ta ? 1 : 0;
     d.trans_b = tb ? 1 : 0;
@@ -341,6 +341,13 @@ void gemm_2d(bool ta, bool tb, size_t m, size_t n, size_t k, const float* a, con
     d.relu = relu ? 1 : 0;
     d.residual = residual;
     d.ld_residual = int64_t(n);
+    return d;
+}
+
+void gemm_2d(bool ta, bool tb, size_t m, size_t n, size_t k, const float* a, const float* b,
+             float* c, const float* bias, bool relu, const char* what,
+             const float* residual = nullptr) {
+    const ehip_gemm_ex_t d = gemm_2d_desc(ta, tb, m, n, k, a, b, c, bias, relu, residual);
     hip::check(ehip_gemm_ex_f32(&d, nullptr), what);
 }
 
@@ -405,21 +412,16 @@ bool queue_weight_grads(const Tensor& x, const Tensor& dy, const Tensor& w, cons
 // x's gradient in place saves a pass instead of splitting a launch in two.
 constexpr double kInPlaceWork = double(1 << 21);
 
-}  // namespace
+bool linear_fusable(const Tensor& x, const Tensor& w, const Tensor* bias) {
+    return x.ndim() == 2 && w.ndim() == 2 && x.shape()[1] == w.shape()[0] &&
+           row_bias(bias, w.shape()[1]);
+}
 
-Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias, const Tensor* residual) {
-    if (x.ndim() != 2 || w.ndim() != 2 || x.shape()[1] != w.shape()[0] ||
-        !row_bias(bias, w.shape()[1])) {
-        Tensor out = x.matmul(w);
-        if (bias) out = out + *bias;
-        return residual ? *residual + out.reshape(residual->shape()) : out;
-    }
+// The node of out = [residual +] x w + bias, already computed: linear()'s
+// backward attached.
+Tensor linear_node(Tensor out, const Tensor& x, const Tensor& w, const Tensor* bias,
+                   const Tensor* residual) {
     const size_t M = x.shape()[0], K = x.shape()[1], N = w.shape()[1];
-    check_residual(residual, M, N, "linear");
-    Tensor out = residual ? Tensor(residual->shape(), 0.0f, false) : empty_2d(M, N);
-    if (M > 0 && N > 0)
-        gemm_2d(false, false, M, N, K, dptr(x), dptr(w), dout(out), bias ? dptr(*bias) : nullptr,
-                false, "linear", residual ? dptr(*residual) : nullptr);
     const bool bias_grad = bias != nullptr && bias->requires_grad();
     const bool res_grad = residual != nullptr && residual->requires_grad();
     if (!track(x.requires_grad() || w.requires_grad() || bias_grad || res_grad)) return out;
@@ -495,6 +497,51 @@ Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias, const Tensor
         }
     });
     return out;
+}
+
+}  // namespace
+
+Tensor linear(const Tensor& x, const Tensor& w, const Tensor* bias, const Tensor* residual) {
+    if (!linear_fusable(x, w, bias)) {
+        Tensor out = x.matmul(w);
+        if (bias) out = out + *bias;
+        return residual ? *residual + out.reshape(residual->shape()) : out;
+    }
+    const size_t M = x.shape()[0], K = x.shape()[1], N = w.shape()[1];
+    check_residual(residual, M, N, "linear");
+    Tensor out = residual ? Tensor(residual->shape(), 0.0f, false) : empty_2d(M, N);
+    if (M > 0 && N > 0)
+        gemm_2d(false, false, M, N, K, dptr(x), dptr(w), dout(out), bias ? dptr(*bias) : nullptr,
+                false, "linear", residual ? dptr(*residual) : nullptr);
+    return linear_node(out, x, w, bias, residual);
+}
+
+std::vector<Tensor> linear_many(const Tensor& x, const std::vector<const Tensor*>& w,
+                                const std::vector<const Tensor*>& bias) {
+    if (w.size() != bias.size())
+        throw std::invalid_argument("linear_many: " + std::to_string(w.size()) + " weights and " +
+                                    std::to_string(bias.size()) + " biases.");
+    bool fusable = true;
+    for (size_t i = 0; i < w.size(); ++i) fusable = fusable && linear_fusable(x, *w[i], bias[i]);
+    std::vector<Tensor> outs;
+    if (!fusable) {
+        for (size_t i = 0; i < w.size(); ++i) outs.push_back(linear(x, *w[i], bias[i]));
+        return outs;
+    }
+    const size_t M = x.shape()[0], K = x.shape()[1];
+    std::vector<ehip_gemm_ex_t> descs;
+    for (size_t i = 0; i < w.size(); ++i) {
+        const size_t N = w[i]->shape()[1];
+        outs.push_back(empty_2d(M, N));
+        if (M > 0 && N > 0)
+            descs.push_back(gemm_2d_desc(false, false, M, N, K, dptr(x), dptr(*w[i]),
+                                         dout(outs.back()), bias[i] ? dptr(*bias[i]) : nullptr,
+                                         false, nullptr));
+    }
+    if (!descs.empty())
+        hip::check(ehip_gemm_batch_f32(descs.data(), int(descs.size()), nullptr), "linear_many");
+    for (size_t i = 0; i < w.size(); ++i) outs[i] = linear_node(outs[i], x, *w[i], bias[i], nullptr);
+    return outs;
 }
 
 Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, const Tensor& w2,

@@ -475,10 +475,13 @@ Tensor MultiHeadAttention::forward(const Tensor& input, const Tensor* mask,
         // input gradients meet in one buffer (the second and third products add
         // into it in place) before a single reshape hands it to `input`.
         const Tensor flat = input.reshape({batch * seq, d_model_});
-        auto project = [&](Linear& layer) { return layer(flat).reshape({batch, seq, d_model_}); };
-        Tensor attended = attention_heads(project(w_query_), project(w_key_), project(w_value_),
-                                          num_heads_, mask,
-                                          keep_attention_ ? &last_attention_ : nullptr);
+        const auto bias = [](Linear& layer) { return layer.has_bias() ? &layer.bias() : nullptr; };
+        const std::vector<Tensor> qkv = ops::linear_many(
+            flat, {&w_query_.weight(), &w_key_.weight(), &w_value_.weight()},
+            {bias(w_query_), bias(w_key_), bias(w_value_)});
+        const auto heads = [&](const Tensor& t) { return t.reshape({batch, seq, d_model_}); };
+        Tensor attended = attention_heads(heads(qkv[0]), heads(qkv[1]), heads(qkv[2]), num_heads_,
+                                          mask, keep_attention_ ? &last_attention_ : nullptr);
         if (residual == nullptr) return w_out_(attended);
         if (residual->shape() != input.shape()) return *residual + w_out_(attended);
         // residual + attended w_out + b_out, the add in the product's epilogue.

@@ -321,7 +321,9 @@ int ehip_gemm_ex_f32(const ehip_gemm_ex_t* desc, void* stream);
 /* Independent products in as few launches as their kernels allow: the narrow
  * weight-gradient products (the A^T B panel kernel: trans_a, batch 1, few 16 x
  * 16 output tiles over a long K; ehip_gemm_groupable says 1) run together,
- * up to 12 per launch; every other descriptor runs as its own
+ * up to 12 per launch, and so do untransposed batch-1 products small enough
+ * for the K-sliced 32 x 32 tiles (several projections of one input), up to
+ * 12 of one kernel form per launch; every other descriptor runs as its own
  * ehip_gemm_ex_f32 call. Each product's result, column sums included, has the
  * bits of its own ehip_gemm_ex_f32 call. The products must be independent (no
  * output read or written by another of the list). For engines that queue the

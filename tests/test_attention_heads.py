@@ -638,6 +638,42 @@ def test_gemm_batch_matches_single_calls(hip):
     hip.ok(hip.lib.ehip_gemm_batch_f32(arr, 0, hip.stream()), "gemm_batch empty")
 
 
+def test_gemm_batch_groups_k_sliced_products(hip):
+    """Untransposed products small enough for the K-sliced tiles (the char model's
+    projections: one input, several weights, a bias addend) run grouped by kernel form in
+    ehip_gemm_batch_f32 with the bits of their own ehip_gemm_ex_f32 calls: whole and
+    checked tiles, with and without the epilogue, slicing K over 1 to 8 waves."""
+    import ctypes as C
+    from ehip import GemmEx
+    import torch
+    print_case("gemm_batch K-sliced")
+    gen = torch.Generator(device="cuda").manual_seed(29)
+    x = torch.randn(2048, 96, device="cuda", generator=gen)
+    x2 = torch.randn(100, 384, device="cuda", generator=gen)
+    cases = [(x, 96, True), (x, 96, True), (x, 96, True), (x, 384, True), (x, 96, False),
+             (x2, 96, True), (x2, 37, False), (x2, 96, True)]
+    keep, singles, batch = [], [], []
+    for a, n, with_bias in cases:
+        m, k = a.shape
+        b = torch.randn(k, n, device="cuda", generator=gen)
+        bias = torch.randn(n, device="cuda", generator=gen) if with_bias else None
+        pair = []
+        for _ in range(2):
+            c = torch.full((m, n), 3.0, device="cuda")
+            pair.append((desc(hip, False, False, 1, 1, m, n, k, a, k, 0, 0, b, n, 0, 0, c, n, 0, 0,
+                              addend=bias, ld_add=0, period=1), c))
+        keep.append((b, bias))
+        singles.append(pair[0])
+        batch.append(pair[1])
+    for d, _ in singles:
+        hip.gemm_ex(d)
+    arr = (GemmEx * len(batch))(*[d for d, _ in batch])
+    hip.ok(hip.lib.ehip_gemm_batch_f32(arr, len(batch), hip.stream()), "gemm_batch")
+    for i, ((_, one), (_, together)) in enumerate(zip(singles, batch)):
+        exact(host(together), host(one), f"K-sliced product {i} {cases[i][0].shape}x{cases[i][1]}")
+    assert [hip.lib.ehip_gemm_groupable(C.byref(d)) for d, _ in batch] == [0] * len(batch)
+
+
 def test_colsum_refusals_and_k_zero(hip):
     print_case("gemm_ex colsum refusals")
     x = dev(np.ones((4, 4), np.float32))
