@@ -39,8 +39,9 @@ bool short_attention();
 // narrow layers (whose dW = X^T dY takes the panel kernel with the bias
 // gradient as its column sums) queue that product instead of launching it,
 // and the queue runs them together (ehip_gemm_batch_f32) when a gradient is
-// first read or before Adam's launch: the same bits, fewer launches per
-// backward. Process-wide; set it between steps.
+// first read, before an in-place add into a buffer they read, or before
+// Adam's launch: the same bits, fewer launches per backward. Process-wide;
+// set it between steps.
 void set_deferred_weight_grads(bool on);
 bool deferred_weight_grads();
 

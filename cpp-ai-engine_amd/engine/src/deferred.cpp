@@ -80,6 +80,19 @@ bool deferred_writes(const Storage& s) {
     return false;
 }
 
+void settle_deferred(const Storage& s) {
+    if (!deferred_pending()) return;
+    if (deferred_writes(s)) {
+        flush_deferred();
+        return;
+    }
+    for (const Tensor& t : g_pending.product_inputs)
+        if (t.storage().same_buffer(s)) {
+            run_products();  // the sums stay queued for Adam's launch
+            return;
+        }
+}
+
 void flush_deferred() {
     run_products();
     if (g_pending.jobs.empty()) {
@@ -120,8 +133,10 @@ float* grad_in_place(const Tensor& target) {
     const auto& impl = target.get_impl();
     if (!impl->requires_grad || !impl->grad) return nullptr;
     Storage& acc = impl->grad->storage;
+    // Queued work that writes or reads the gradient runs first (it holds a
+    // view of the buffer, so the exclusivity test is only meaningful after).
+    settle_deferred(acc);
     if (acc.pending_zero() || !acc.exclusive() || acc.size() != target.size()) return nullptr;
-    if (deferred_pending() && deferred_writes(acc)) flush_deferred();
     return acc.device_mut();
 }
 

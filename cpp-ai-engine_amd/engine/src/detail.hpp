@@ -113,6 +113,9 @@ void defer_product(const ehip_gemm_ex_t& desc, std::initializer_list<Tensor> inp
 bool deferred_pending();
 // True when a queued job writes the buffer of `s` (a registered output).
 bool deferred_writes(const Storage& s);
+// Before an in-place write into the buffer: runs the queue when queued work
+// writes it, or only the queued products when one reads it.
+void settle_deferred(const Storage& s);
 void flush_deferred();
 void drop_deferred();
 // Moves the queued jobs (and the buffers they touch) to the caller, which must

@@ -181,11 +181,10 @@ void detail::add_grad_reshaped(Tensor& target, const Tensor& g) {
         impl_->grad->storage = g.storage().share();
         return;
     }
-    // Accumulating reads the existing gradient and g: finish first any queued sum
-    // that writes either of them.
-    if (deferred_pending() && ((impl_->grad && deferred_writes(impl_->grad->storage)) ||
-                               deferred_writes(g.storage())))
-        flush_deferred();
+    // Accumulating reads the existing gradient and g and writes the gradient:
+    // finish first queued work that writes either, or reads the gradient.
+    if (impl_->grad) settle_deferred(impl_->grad->storage);
+    if (deferred_pending() && deferred_writes(g.storage())) flush_deferred();
     if (!impl_->grad) impl_->grad = std::make_shared<TensorImpl>(shape, 0.0f, false);
     Storage& acc = impl_->grad->storage;
     const float* src = g.storage().device();
@@ -205,10 +204,11 @@ void detail::add_grad_reshaped(Tensor& target, const Tensor& g) {
 float* detail::grad_in_place(Tensor& target) {
     const std::shared_ptr<TensorImpl>& impl_ = target.get_impl();
     if (!impl_ || !impl_->requires_grad || !impl_->grad) return nullptr;
-    // The product reads the existing gradient: finish first a queued sum that
-    // writes it (the queue holds a view of the buffers it writes, so their
-    // exclusivity test below is only meaningful once it has run).
-    if (deferred_pending() && deferred_writes(impl_->grad->storage)) flush_deferred();
+    // The product reads the existing gradient and adds into it: finish first
+    // queued work that writes or reads it (the queue holds a view of those
+    // buffers, so their exclusivity test below is only meaningful once it has
+    // run).
+    settle_deferred(impl_->grad->storage);
     Storage& acc = impl_->grad->storage;
     if (acc.pending_zero() || !acc.exclusive() || acc.size() != target.size()) return nullptr;
     return acc.device_mut();

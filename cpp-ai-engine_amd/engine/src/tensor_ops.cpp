@@ -429,8 +429,7 @@ Tensor linear_node(Tensor out, const Tensor& x, const Tensor& w, const Tensor* b
     std::vector<std::shared_ptr<TensorImpl>> parents = {x.get_impl(), w.get_impl()};
     if (bias) parents.push_back(bias->get_impl());
     if (residual) parents.push_back(residual->get_impl());
-    const bool has_res = residual != nullptr;
-    attach(out, std::move(parents), [xc, wc, bc, rc, has_res, M, N, K](const Tensor& g) mutable {
+    attach(out, std::move(parents), [xc, wc, bc, rc, M, N, K](const Tensor& g) mutable {
         // The residual add's node comes last in the composed graph, so its
         // gradient goes first; the product reads g itself instead of the copy
         // the add's backward would hand it.
@@ -454,9 +453,9 @@ Tensor linear_node(Tensor out, const Tensor& x, const Tensor& w, const Tensor* b
                                          int64_t(N), 0, dptr(wc), int64_t(N), 0, 1.0f, dx_acc,
                                          int64_t(K), 0, nullptr),
                            "linear backward dx");
-            // dW and db queued (the residual's gradient may hold g's buffer: a
-            // queued read of it would keep the next in-place add from it).
-            if (want_db && !has_res && queue_weight_grads(xc, g, wc, bc, dw, db, M, K, N)) {
+            // dW and db queued (g may be the residual's gradient by now: an
+            // in-place add into it first runs the queue).
+            if (want_db && queue_weight_grads(xc, g, wc, bc, dw, db, M, K, N)) {
                 // dx as ehip_linear_backward_f32 forms it for such a layer.
                 if (want_dx)
                     hip::check(ehip_gemm_f32(0, 1, 1, int64_t(M), int64_t(K), int64_t(N),
@@ -577,14 +576,18 @@ Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, co
                // that pays, as in Linear).
                if (rc.get_impl() && rc.requires_grad()) rc.add_grad(g);
                Tensor dw2;
+               bool queued2 = false;
                if (b2c.requires_grad() && w2c.requires_grad() && F > 0 && N > 0) {
                    dw2 = empty_2d(F, N);
                    Tensor db2(b2c.shape(), 0.0f, false);
-                   hip::check(ehip_linear_backward_f32(dptr(h), dptr(w2c), dptr(g), nullptr,
-                                                       dout(dw2), dout(db2), int64_t(M),
-                                                       int64_t(F), int64_t(N), nullptr),
-                              "feed-forward dw2 and db2");
+                   queued2 = queue_weight_grads(h, g, w2c, b2c, dw2, db2, M, F, N);
+                   if (!queued2)
+                       hip::check(ehip_linear_backward_f32(dptr(h), dptr(w2c), dptr(g), nullptr,
+                                                           dout(dw2), dout(db2), int64_t(M),
+                                                           int64_t(F), int64_t(N), nullptr),
+                                  "feed-forward dw2 and db2");
                    b2c.add_grad(db2);
+                   if (queued2) defer_conv_output(b2c, db2);
                } else if (b2c.requires_grad()) {
                    b2c.add_grad(reduce_to(g, b2c));
                }
@@ -604,6 +607,7 @@ Tensor feed_forward_relu(const Tensor& x, const Tensor& w1, const Tensor& b1, co
                                    false, "feed-forward dw2");
                    }
                    w2c.add_grad(dw2);
+                   if (queued2) defer_conv_output(w2c, dw2);
                }
                if (!need_dh) return;
                // ReLU's backward from its output: h > 0 exactly where the
