@@ -26,7 +26,11 @@ namespace {
 constexpr int kAttnMax = 64;       // positions and head values held in LDS
 constexpr int kAttnPitch = 65;     // LDS row pitch (odd: column walks hit distinct banks)
 constexpr int kFwdThreads = 256;
-constexpr int kFwdRows = 16;       // query rows per forward workgroup
+// Query rows per forward workgroup: 8 (1024 workgroups at the char model's 128
+// heads of 64) measured 10.4 us against 12.4 for 16 rows and 14.6 for 4 on
+// MI355X, the same bits (each output's sum is one thread's whatever the
+// split).
+constexpr int kFwdRows = 8;
 constexpr int kBwdThreads = 1024;
 constexpr int kGroup = 4;          // score entries (consecutive keys) per thread and pass
 
