@@ -674,6 +674,22 @@ def test_gemm_batch_groups_k_sliced_products(hip):
     assert [hip.lib.ehip_gemm_groupable(C.byref(d)) for d, _ in batch] == [0] * len(batch)
 
 
+def test_linear_backward_plan(hip):
+    """ehip_linear_backward_plan: 1 for the mid-sized layers whose db the library takes from
+    the dW product (cfg3's, more than 64 rows and dY of at most 2^21 elements), 0 for small,
+    empty and wide ones (cfg5's), and 0 with the switch off."""
+    print_case("linear_backward_plan")
+    plan = hip.lib.ehip_linear_backward_plan
+    assert plan(2048, 96, 96) == 1 and plan(2048, 96, 384) == 1 and plan(2048, 384, 96) == 1
+    assert plan(64, 784, 10) == 0 and plan(0, 96, 96) == 0 and plan(2048, 0, 96) == 0
+    assert plan(8192, 1024, 1024) == 0 and plan(8192, 1024, 4096) == 0
+    prev = hip.lib.ehip_linear_bias_from_dw(0)
+    try:
+        assert plan(2048, 96, 96) == 0
+    finally:
+        hip.lib.ehip_linear_bias_from_dw(prev)
+
+
 def test_colsum_refusals_and_k_zero(hip):
     print_case("gemm_ex colsum refusals")
     x = dev(np.ones((4, 4), np.float32))
@@ -731,6 +747,12 @@ def test_linear_backward_matches_separate_calls(hip, rows, inp, out, want):
                 assert from_dw, "cfg3's feed-forward layer takes db from its dw product"
             if rows <= 64:
                 assert not from_dw, "up to 64 rows db is the serial column sum"
+            # The plan query an engine asks before queueing the product says the same
+            # (where the sums differ; equal sums cannot tell the two paths apart).
+            plan = hip.lib.ehip_linear_backward_plan(rows, inp, out)
+            assert plan in (0, 1)
+            if from_dw:
+                assert plan == 1, "db came from the dw product, the plan said otherwise"
         if on and from_dw:
             cw, cs = hip.f32((inp, out)), hip.f32((out,))
             d = desc(hip, True, False, 1, 1, inp, out, rows, x, inp, 0, 0, dy, out, 0, 0, cw, out,
