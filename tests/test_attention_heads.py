@@ -642,7 +642,7 @@ def test_gemm_batch_groups_k_sliced_products(hip):
     """Untransposed products small enough for the K-sliced tiles (the char model's
     projections: one input, several weights, a bias addend) run grouped by kernel form in
     ehip_gemm_batch_f32 with the bits of their own ehip_gemm_ex_f32 calls: whole and
-    checked tiles, with and without the epilogue, slicing K over 1 to 8 waves."""
+    checked tiles, with and without the epilogue, slicing K over 2, 4 or 8 waves."""
     import ctypes as C
     from ehip import GemmEx
     import torch
@@ -650,8 +650,9 @@ def test_gemm_batch_groups_k_sliced_products(hip):
     gen = torch.Generator(device="cuda").manual_seed(29)
     x = torch.randn(2048, 96, device="cuda", generator=gen)
     x2 = torch.randn(100, 384, device="cuda", generator=gen)
+    x3 = torch.randn(2048, 192, device="cuda", generator=gen)  # four waves per tile
     cases = [(x, 96, True), (x, 96, True), (x, 96, True), (x, 384, True), (x, 96, False),
-             (x2, 96, True), (x2, 37, False), (x2, 96, True)]
+             (x2, 96, True), (x2, 37, False), (x2, 96, True), (x3, 96, True), (x3, 96, False)]
     keep, singles, batch = [], [], []
     for a, n, with_bias in cases:
         m, k = a.shape
